@@ -1,0 +1,236 @@
+// LayerNorm over selected rows, rotate-half RoPE on the active rows, and the fused post-QKV step
+// (RoPE + in-place K/V cache rewrite + packed query write).
+#include "common.hpp"
+
+namespace oudjat {
+
+static constexpr int kNormThreads = 256;
+static constexpr int kNormRowsPerWg = kNormThreads / 64;
+
+// One wave per row; each lane keeps its CH 16-byte chunks (8 bf16 each) in registers, so the row is
+// read from HBM exactly once. Statistics are fp32: mean, then the biased variance around it.
+template <int CH>
+__global__ __launch_bounds__(kNormThreads) void layernorm_kernel(const uint16_t* __restrict__ x, int64_t rows, int C,
+                                                               int64_t xs, const uint16_t* __restrict__ w,
+                                                               const uint16_t* __restrict__ bias, float eps,
+                                                               uint16_t* __restrict__ out, int64_t os) {
+  const int64_t row = (int64_t)blockIdx.x * kNormRowsPerWg + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int chunks = C >> 3;
+  const uint4* xv = reinterpret_cast<const uint4*>(x + row * xs);
+  float v[CH][8];
+  float sum = 0.0f;
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) {
+      unpack8(xv[c], v[j]);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) sum += v[j][e];
+    }
+  }
+  const float mean = wave_sum(sum) / (float)C;
+  float sq = 0.0f;
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) {
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        const float dlt = v[j][e] - mean;
+        sq = fmaf(dlt, dlt, sq);
+      }
+    }
+  }
+  const float var = wave_sum(sq) / (float)C;
+  const float rstd = 1.0f / sqrtf(var + eps);
+  const uint4* wv = reinterpret_cast<const uint4*>(w);
+  const uint4* bv = reinterpret_cast<const uint4*>(bias);
+  uint4* ov = reinterpret_cast<uint4*>(out + row * os);
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) {
+      float fw[8], fb[8], y[8];
+      unpack8(wv[c], fw);
+      unpack8(bv[c], fb);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) y[e] = fmaf(fw[e], (v[j][e] - mean) * rstd, fb[e]);
+      ov[c] = pack8(y);
+    }
+  }
+}
+
+// Rotate-half RoPE on one 8-wide chunk of the left half and its partner chunk of the right half.
+// fp32 math with every product and sum rounded separately, matching an eager
+// (x * cos) + (rotate_half(x) * sin) evaluated in fp32. Contraction is switched off for this scope
+// (plain operators: the __f*_rn helpers are themselves contractable after inlining).
+__device__ __forceinline__ void rope8(float* l, float* r, const float* cl, const float* cr, const float* sl,
+                                      const float* sr) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float nl = l[e] * cl[e] - r[e] * sl[e];
+    const float nr = r[e] * cr[e] + l[e] * sr[e];
+    l[e] = nl;
+    r[e] = nr;
+  }
+}
+
+__device__ __forceinline__ void load8f(const float* p, float* f) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0];
+  const float4 b = reinterpret_cast<const float4*>(p)[1];
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+  f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+
+// Thread = (row, head, chunk of 8 in the left half). Rows with patch_mask == 0 are left untouched.
+__global__ __launch_bounds__(256) void rope_active_inplace_kernel(
+    uint16_t* q, int64_t qst, int64_t qsh, uint16_t* k, int64_t kst, int64_t ksh, const float* __restrict__ sin_t,
+    const float* __restrict__ cos_t, int64_t tst, const uint8_t* __restrict__ pm, const int64_t* __restrict__ ridx,
+    int64_t n, int H, int Dh) {
+  const int half = Dh >> 1;
+  const int cph = half >> 3;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_row = (int64_t)H * cph;
+  const int64_t row = gid / per_row;
+  if (row >= n) return;
+  if (!pm[row]) return;
+  const int rem = (int)(gid - row * per_row);
+  const int h = rem / cph;
+  const int c = rem - h * cph;
+  const int64_t tr = ridx[row];
+  const int d0 = c * 8;
+  float cl[8], cr[8], sl[8], sr[8];
+  load8f(cos_t + tr * tst + d0, cl);
+  load8f(cos_t + tr * tst + d0 + half, cr);
+  load8f(sin_t + tr * tst + d0, sl);
+  load8f(sin_t + tr * tst + d0 + half, sr);
+  uint16_t* ptrs[2] = {q + row * qst + h * qsh, k + row * kst + h * ksh};
+#pragma unroll
+  for (int m = 0; m < 2; ++m) {
+    uint4* lp = reinterpret_cast<uint4*>(ptrs[m] + d0);
+    uint4* rp = reinterpret_cast<uint4*>(ptrs[m] + d0 + half);
+    float l[8], r[8];
+    unpack8(*lp, l);
+    unpack8(*rp, r);
+    rope8(l, r, cl, cr, sl, sr);
+    *lp = pack8(l);
+    *rp = pack8(r);
+  }
+}
+
+// Post-QKV step: qkv [M, 3, H, Dh] -> RoPE(q), RoPE(k) on patch rows; q -> q_out [M, H, Dh];
+// k, v -> kv[b, t, 0 | 1, h, :] (the [2, H, Dh] part of a cache row is contiguous).
+__global__ __launch_bounds__(256) void qkv_rope_kv_scatter_kernel(
+    const uint16_t* __restrict__ qkv, int64_t M, int H, int Dh, const float* __restrict__ sin_t,
+    const float* __restrict__ cos_t, int64_t tst, const uint8_t* __restrict__ pm, const int64_t* __restrict__ ridx,
+    const int64_t* __restrict__ bi, const int64_t* __restrict__ ti, uint16_t* __restrict__ kv, int64_t kvb,
+    int64_t kvn, uint16_t* __restrict__ qo) {
+  const int half = Dh >> 1;
+  const int cph = half >> 3;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t per_row = (int64_t)H * cph;
+  const int64_t row = gid / per_row;
+  if (row >= M) return;
+  const int rem = (int)(gid - row * per_row);
+  const int h = rem / cph;
+  const int c = rem - h * cph;
+  const int d0 = c * 8;
+  const int64_t HD = (int64_t)H * Dh;
+  const uint16_t* src = qkv + row * 3 * HD + (int64_t)h * Dh;
+  uint4 q_l = *reinterpret_cast<const uint4*>(src + d0);
+  uint4 q_r = *reinterpret_cast<const uint4*>(src + d0 + half);
+  uint4 k_l = *reinterpret_cast<const uint4*>(src + HD + d0);
+  uint4 k_r = *reinterpret_cast<const uint4*>(src + HD + d0 + half);
+  const uint4 v_l = *reinterpret_cast<const uint4*>(src + 2 * HD + d0);
+  const uint4 v_r = *reinterpret_cast<const uint4*>(src + 2 * HD + d0 + half);
+  if (pm[row]) {
+    const int64_t tr = ridx[row];
+    float cl[8], cr[8], sl[8], sr[8];
+    load8f(cos_t + tr * tst + d0, cl);
+    load8f(cos_t + tr * tst + d0 + half, cr);
+    load8f(sin_t + tr * tst + d0, sl);
+    load8f(sin_t + tr * tst + d0 + half, sr);
+    float l[8], r[8];
+    unpack8(q_l, l);
+    unpack8(q_r, r);
+    rope8(l, r, cl, cr, sl, sr);
+    q_l = pack8(l);
+    q_r = pack8(r);
+    unpack8(k_l, l);
+    unpack8(k_r, r);
+    rope8(l, r, cl, cr, sl, sr);
+    k_l = pack8(l);
+    k_r = pack8(r);
+  }
+  uint16_t* qd = qo + row * HD + (int64_t)h * Dh;
+  *reinterpret_cast<uint4*>(qd + d0) = q_l;
+  *reinterpret_cast<uint4*>(qd + d0 + half) = q_r;
+  uint16_t* kd = kv + bi[row] * kvb + ti[row] * kvn + (int64_t)h * Dh;
+  *reinterpret_cast<uint4*>(kd + d0) = k_l;
+  *reinterpret_cast<uint4*>(kd + d0 + half) = k_r;
+  *reinterpret_cast<uint4*>(kd + HD + d0) = v_l;
+  *reinterpret_cast<uint4*>(kd + HD + d0 + half) = v_r;
+}
+
+}  // namespace oudjat
+
+using namespace oudjat;
+
+extern "C" int oudjat_layernorm_rows(const uint16_t* x, int64_t rows, int64_t C, int64_t xs, const uint16_t* w,
+                                     const uint16_t* b, float eps, uint16_t* out, int64_t os, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(rows >= 0 && C > 0, OUDJAT_ERR_INVALID_ARGUMENT, "layernorm_rows: bad size");
+  if (rows == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(x && w && b && out, OUDJAT_ERR_INVALID_ARGUMENT, "layernorm_rows: null pointer");
+  OUDJAT_REQUIRE(C % 8 == 0 && xs % 8 == 0 && os % 8 == 0 && aligned(x, 16) && aligned(out, 16) && aligned(w, 16) &&
+                     aligned(b, 16),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "layernorm_rows: 16-byte aligned rows with C %% 8 == 0 required");
+  OUDJAT_REQUIRE(C <= 8192, OUDJAT_ERR_TOO_LARGE, "layernorm_rows: C=%lld > 8192", (long long)C);
+  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg);
+  hipStream_t st = as_stream(stream);
+  if (C <= 512) layernorm_kernel<1><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os);
+  else if (C <= 1024) layernorm_kernel<2><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os);
+  else if (C <= 2048) layernorm_kernel<4><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os);
+  else if (C <= 4096) layernorm_kernel<8><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os);
+  else layernorm_kernel<16><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os);
+  return check_launch("layernorm_rows");
+}
+
+extern "C" int oudjat_rope_active_inplace(uint16_t* q, int64_t qst, int64_t qsh, uint16_t* k, int64_t kst, int64_t ksh,
+                                          const float* sin_t, const float* cos_t, int64_t tst, const uint8_t* pm,
+                                          const int64_t* ridx, int64_t n, int64_t H, int64_t Dh,
+                                          oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(n >= 0 && H >= 0 && Dh >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "rope_active_inplace: negative size");
+  if (n == 0 || H == 0 || Dh == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(q && k && sin_t && cos_t && pm && ridx, OUDJAT_ERR_INVALID_ARGUMENT, "rope_active_inplace: null pointer");
+  OUDJAT_REQUIRE(Dh % 16 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE, "rope_active_inplace: Dh=%lld must be a multiple of 16",
+                 (long long)Dh);
+  OUDJAT_REQUIRE(qst % 8 == 0 && qsh % 8 == 0 && kst % 8 == 0 && ksh % 8 == 0 && tst % 8 == 0 && aligned(q, 16) &&
+                     aligned(k, 16) && aligned(sin_t, 16) && aligned(cos_t, 16),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "rope_active_inplace: 16-byte aligned rows/heads required");
+  const int64_t threads = n * H * (Dh / 16);
+  rope_active_inplace_kernel<<<(unsigned)cdiv(threads, 256), 256, 0, as_stream(stream)>>>(
+      q, qst, qsh, k, kst, ksh, sin_t, cos_t, tst, pm, ridx, n, (int)H, (int)Dh);
+  return check_launch("rope_active_inplace");
+}
+
+extern "C" int oudjat_qkv_rope_kv_scatter(const uint16_t* qkv, int64_t M, int64_t H, int64_t Dh, const float* sin_t,
+                                          const float* cos_t, int64_t tst, const uint8_t* pm, const int64_t* ridx,
+                                          const int64_t* bi, const int64_t* ti, uint16_t* kv, int64_t kvb,
+                                          int64_t kvn, uint16_t* qo, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(M >= 0 && H > 0 && Dh > 0, OUDJAT_ERR_INVALID_ARGUMENT, "qkv_rope_kv_scatter: bad size");
+  if (M == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(qkv && sin_t && cos_t && pm && ridx && bi && ti && kv && qo, OUDJAT_ERR_INVALID_ARGUMENT,
+                 "qkv_rope_kv_scatter: null pointer");
+  OUDJAT_REQUIRE(Dh % 16 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE, "qkv_rope_kv_scatter: Dh=%lld must be a multiple of 16",
+                 (long long)Dh);
+  OUDJAT_REQUIRE(kvb % 8 == 0 && kvn % 8 == 0 && tst % 8 == 0 && aligned(qkv, 16) && aligned(kv, 16) &&
+                     aligned(qo, 16) && aligned(sin_t, 16) && aligned(cos_t, 16),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "qkv_rope_kv_scatter: 16-byte aligned rows required");
+  const int64_t threads = M * H * (Dh / 16);
+  qkv_rope_kv_scatter_kernel<<<(unsigned)cdiv(threads, 256), 256, 0, as_stream(stream)>>>(
+      qkv, M, (int)H, (int)Dh, sin_t, cos_t, tst, pm, ridx, bi, ti, kv, kvb, kvn, qo);
+  return check_launch("qkv_rope_kv_scatter");
+}

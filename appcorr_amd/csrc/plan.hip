@@ -1,0 +1,213 @@
+// Top-k token selection and the sync-free packed query plan.
+//
+// One 1024-thread workgroup per image. The scores of the image are turned into order-preserving
+// uint32 keys in LDS; a 4-round radix select (8-bit digits, LDS histograms) finds the k-th largest
+// key; kept candidates are then compacted in ascending candidate order with two block-wide prefix
+// sums (equal-to-threshold rank, then kept rank). Ties on the threshold key go to the lowest
+// candidate index, which makes the selected set a pure function of the scores.
+//
+// The same workgroup writes the whole PackedQueryState of its image (update_indice, batch/pos/token
+// index, patch mask, RoPE table row) and, if asked, the per-token slot map that the fused
+// reconstruct kernel uses. Nothing here needs the host: k is a launch argument.
+#include "common.hpp"
+
+namespace oudjat {
+
+static constexpr int kPlanThreads = 1024;
+static constexpr int kPlanWaves = kPlanThreads / 64;
+static constexpr int64_t kMaxCandidates = 16384;
+static constexpr int64_t kMaxPlanLds = 144 * 1024;
+
+__device__ __forceinline__ uint32_t order_key(float f) {
+  uint32_t u = __float_as_uint(f);
+  if ((u & 0x7fffffffu) > 0x7f800000u) return 0xffffffffu;  // NaN ranks above +inf
+  if (u == 0x80000000u) u = 0u;                             // -0.0 ties with +0.0
+  return (u & 0x80000000u) ? ~u : (u | 0x80000000u);
+}
+
+__device__ __forceinline__ uint32_t wave_incl_scan(uint32_t v, int lane) {
+#pragma unroll
+  for (int o = 1; o < 64; o <<= 1) {
+    uint32_t t = __shfl_up(v, o, 64);
+    if (lane >= o) v += t;
+  }
+  return v;
+}
+
+// Exclusive prefix sum of one value per thread over the 1024-thread block, in thread order.
+__device__ __forceinline__ uint32_t block_excl_scan(uint32_t v, uint32_t* sh) {
+  const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+  const uint32_t incl = wave_incl_scan(v, lane);
+  if (lane == 63) sh[w] = incl;
+  __syncthreads();
+  if (w == 0) {
+    uint32_t t = lane < kPlanWaves ? sh[lane] : 0u;
+    uint32_t ti = wave_incl_scan(t, lane);
+    if (lane < kPlanWaves) sh[lane] = ti - t;
+  }
+  __syncthreads();
+  const uint32_t r = sh[w] + incl - v;
+  __syncthreads();
+  return r;
+}
+
+__global__ __launch_bounds__(kPlanThreads) void topk_plan_kernel(
+    const float* __restrict__ scores, int P, int64_t ssb, int k, const int64_t* __restrict__ dind, int64_t dsb,
+    int npre, int ntok, int64_t* __restrict__ upd, int64_t* __restrict__ abat, int64_t* __restrict__ apos,
+    int64_t* __restrict__ atok, uint8_t* __restrict__ pmask, int64_t* __restrict__ ridx, uint8_t* __restrict__ keep,
+    int32_t* __restrict__ slot_map) {
+  extern __shared__ uint32_t smem[];
+  uint32_t* keys = smem;
+  int32_t* lmap = reinterpret_cast<int32_t*>(smem + P);
+  __shared__ uint32_t hist[256];
+  __shared__ uint32_t scan_sh[kPlanWaves];
+  __shared__ uint32_t sel_sh[2];
+
+  const int b = blockIdx.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63;
+  const float* s = scores + (int64_t)b * ssb;
+  const int64_t* d = dind + (int64_t)b * dsb;
+  const int T = npre + k;
+  const int64_t row0 = (int64_t)b * T;
+
+  for (int i = tid; i < P; i += kPlanThreads) keys[i] = order_key(s[i]);
+  if (slot_map)
+    for (int i = tid; i < ntok; i += kPlanThreads) lmap[i] = -1;
+  __syncthreads();
+
+  const bool keep_all = k >= P;
+  const bool keep_none = k <= 0;
+  uint32_t thr = 0u;
+  uint32_t remaining = (uint32_t)(k > 0 ? k : 0);
+  if (!keep_all && !keep_none) {
+    uint32_t prefix = 0u, pbits = 0u;
+    for (int shift = 24; shift >= 0; shift -= 8) {
+      if (tid < 256) hist[tid] = 0u;
+      __syncthreads();
+      for (int i = tid; i < P; i += kPlanThreads) {
+        const uint32_t key = keys[i];
+        if ((key & pbits) == prefix) atomicAdd(&hist[(key >> shift) & 255u], 1u);
+      }
+      __syncthreads();
+      if (tid < 64) {
+        // Lane l owns bins 255-4l .. 252-4l, i.e. the histogram read from the top digit down.
+        uint32_t c[4];
+#pragma unroll
+        for (int j = 0; j < 4; ++j) c[j] = hist[255 - 4 * tid - j];
+        const uint32_t local = c[0] + c[1] + c[2] + c[3];
+        uint32_t run = wave_incl_scan(local, lane) - local;  // elements in higher bins
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          if (run < remaining && remaining <= run + c[j]) {
+            sel_sh[0] = (uint32_t)(255 - 4 * tid - j);
+            sel_sh[1] = run;
+          }
+          run += c[j];
+        }
+      }
+      __syncthreads();
+      const uint32_t digit = sel_sh[0];
+      remaining -= sel_sh[1];
+      prefix |= digit << shift;
+      pbits |= 255u << shift;
+      __syncthreads();
+    }
+    thr = prefix;
+  }
+
+  // Each thread owns a contiguous run of candidates, so thread order is candidate order.
+  const int per = (P + kPlanThreads - 1) / kPlanThreads;
+  const int beg = min(tid * per, P);
+  const int end = min(beg + per, P);
+
+  uint32_t n_eq = 0u;
+  if (!keep_all && !keep_none)
+    for (int i = beg; i < end; ++i) n_eq += keys[i] == thr;
+  uint32_t eq_rank = block_excl_scan(n_eq, scan_sh);
+
+  uint32_t kept_bits = 0u;  // bit (i - beg) set if candidate i is kept; per <= 16
+  uint32_t n_kept = 0u;
+  for (int i = beg; i < end; ++i) {
+    bool kept;
+    if (keep_all) kept = true;
+    else if (keep_none) kept = false;
+    else {
+      const uint32_t key = keys[i];
+      kept = key > thr;
+      if (key == thr) {
+        kept = eq_rank < remaining;
+        ++eq_rank;
+      }
+    }
+    if (kept) {
+      kept_bits |= 1u << (i - beg);
+      ++n_kept;
+    }
+  }
+  uint32_t pos = block_excl_scan(n_kept, scan_sh);
+
+  for (int i = beg; i < end; ++i) {
+    const bool kept = (kept_bits >> (i - beg)) & 1u;
+    if (keep) keep[(int64_t)b * P + i] = kept ? 1 : 0;
+    if (!kept) continue;
+    const int slot = npre + (int)pos;
+    ++pos;
+    const int64_t tok = d[npre + i];
+    const int64_t r = row0 + slot;
+    upd[r] = tok;
+    abat[r] = b;
+    apos[r] = slot;
+    atok[r] = tok;
+    pmask[r] = tok >= npre ? 1 : 0;
+    ridx[r] = tok > npre ? tok - npre : 0;
+    if (slot_map && tok >= 0 && tok < ntok) lmap[tok] = (int32_t)r;
+  }
+  for (int j = tid; j < npre; j += kPlanThreads) {
+    const int64_t tok = d[j];
+    const int64_t r = row0 + j;
+    upd[r] = tok;
+    abat[r] = b;
+    apos[r] = j;
+    atok[r] = tok;
+    pmask[r] = tok >= npre ? 1 : 0;
+    ridx[r] = tok > npre ? tok - npre : 0;
+    if (slot_map && tok >= 0 && tok < ntok) lmap[tok] = (int32_t)r;
+  }
+  if (slot_map) {
+    __syncthreads();
+    for (int i = tid; i < ntok; i += kPlanThreads) slot_map[(int64_t)b * ntok + i] = lmap[i];
+  }
+}
+
+}  // namespace oudjat
+
+using namespace oudjat;
+
+extern "C" int oudjat_topk_plan(const float* scores, int64_t B, int64_t P, int64_t ssb, int64_t k,
+                                const int64_t* dindice, int64_t dsb, int64_t npre, int64_t ntok, int64_t* upd,
+                                int64_t* abat, int64_t* apos, int64_t* atok, uint8_t* pmask, int64_t* ridx,
+                                uint8_t* keep, int32_t* slot_map, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(B >= 0 && P >= 0 && npre >= 0 && ntok >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "topk_plan: negative size");
+  OUDJAT_REQUIRE(k >= 0 && k <= P, OUDJAT_ERR_INVALID_ARGUMENT, "topk_plan: k=%lld outside [0, P=%lld]", (long long)k,
+                 (long long)P);
+  if (B == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(dindice && upd && abat && apos && atok && pmask && ridx && (scores || P == 0),
+                 OUDJAT_ERR_INVALID_ARGUMENT, "topk_plan: null pointer");
+  OUDJAT_REQUIRE(P <= kMaxCandidates, OUDJAT_ERR_TOO_LARGE, "topk_plan: P=%lld exceeds %lld", (long long)P,
+                 (long long)kMaxCandidates);
+  OUDJAT_REQUIRE(npre + k < ((int64_t)1 << 30) && B * (npre + k) < ((int64_t)1 << 31), OUDJAT_ERR_TOO_LARGE,
+                 "topk_plan: plan too large for int32 slots");
+  const int64_t lds = (P + (slot_map ? ntok : 0)) * 4;
+  OUDJAT_REQUIRE(lds <= kMaxPlanLds, OUDJAT_ERR_TOO_LARGE, "topk_plan: needs %lld bytes of LDS (max %lld)",
+                 (long long)lds, (long long)kMaxPlanLds);
+  if (lds > 48 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void*)topk_plan_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                                       (int)lds);
+    if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "topk_plan: hipFuncSetAttribute: %s", hipGetErrorString(e));
+  }
+  topk_plan_kernel<<<(unsigned)B, kPlanThreads, (size_t)lds, as_stream(stream)>>>(
+      scores, (int)P, ssb, (int)k, dindice, dsb, (int)npre, (int)ntok, upd, abat, apos, atok, pmask, ridx, keep,
+      slot_map);
+  return check_launch("topk_plan");
+}

@@ -1,0 +1,535 @@
+"""DINOv3 transformer block whose approx / correct passes run on the gfx950 kernels.
+
+Module tree and parameter names are those of the reference (appcorr/models/dinov3/layers/block.py,
+attention.py, ffn_layers.py, layer_scale.py), so a reference state_dict loads unchanged:
+    norm1.{weight,bias}  attn.qkv.{weight,bias,bias_mask}  attn.proj.{weight,bias}  ls1.gamma
+    norm2.{weight,bias}  mlp.fc1/fc2.{weight,bias} | mlp.w1/w2/w3.{weight,bias}     ls2.gamma
+The modules only hold parameters; their forward never runs a torch op on the hot path. Every step of
+`SelfAttentionBlock.correct_partial_token` is a library call (appcorr_amd.kernels):
+
+    topk_plan (once per plan) -> gather_rows -> layer_norm -> linear[qkv] -> qkv_rope_kv_scatter
+    -> sparse_query_attention -> linear[proj, +LayerScale +residual] -> layer_norm
+    -> linear[fc1, +GELU] -> linear[fc2, +LayerScale] -> reconstruct_scatter_persist
+
+Plan-level bookkeeping that the reference does with small torch ops on [B, P] score tensors (score
+resolution and fusion, the plan cache, the pscore statistics) is kept as torch ops: it runs once per
+plan, not per block.
+"""
+
+from __future__ import annotations
+
+import math
+import os
+from dataclasses import dataclass
+from typing import Dict, Tuple
+
+import torch
+from torch import Tensor, nn
+
+from .. import _lib
+from .. import kernels as K
+
+
+# ------------------------------------------------------------------------------------------------
+# Plan types (attention.py:52-74; block.py:33-44)
+# ------------------------------------------------------------------------------------------------
+
+
+@dataclass
+class PackedQueryState:
+    active_batch_idx: Tensor
+    active_pos_idx: Tensor
+    active_token_idx: Tensor
+    query_valid_mask: Tensor
+    active_query_pos_padded: Tensor
+    active_query_mask: Tensor
+    all_valid: bool
+    active_patch_mask: Tensor | None = None
+    active_rope_idx: Tensor | None = None
+    # Token -> packed row map [B, N] int32 (-1 off the plan); consumed by the fused residual kernel.
+    row_slot: Tensor | None = None
+
+
+@dataclass
+class PartialTokenQueryPlan:
+    update_indice: Tensor
+    fixed_query_state: PackedQueryState
+    server_patch_scores: Tensor
+    mobile_patch_scores: Tensor | None
+    combined_patch_scores: Tensor
+    kept_pscore_mass: Tensor
+    full_pscore_mass: Tensor
+    kept_patch_total: Tensor
+    full_patch_total: Tensor
+    sample_total: Tensor
+
+
+# ------------------------------------------------------------------------------------------------
+# Parameter-holding modules
+# ------------------------------------------------------------------------------------------------
+
+
+class LayerScale(nn.Module):
+    """layer_scale.py:12-29 (parameter holder)."""
+
+    def __init__(self, dim: int, init_values: float = 1e-5, device=None):
+        super().__init__()
+        self.gamma = nn.Parameter(torch.empty(dim, device=device))
+        self.init_values = init_values
+
+    def reset_parameters(self):
+        nn.init.constant_(self.gamma, self.init_values)
+
+
+class LinearKMaskedBias(nn.Linear):
+    """attention.py:39-49: the K third of the qkv bias is multiplied by a 0/1 mask."""
+
+    def __init__(self, *args, **kwargs):
+        super().__init__(*args, **kwargs)
+        if self.out_features % 3 != 0:
+            raise ValueError("qkv out_features must be a multiple of 3")
+        if self.bias is not None:
+            self.register_buffer("bias_mask", torch.full_like(self.bias, fill_value=math.nan))
+
+    def masked_bias(self) -> Tensor | None:
+        if self.bias is None:
+            return None
+        return self.bias * self.bias_mask.to(self.bias.dtype)
+
+
+class Mlp(nn.Module):
+    """ffn_layers.py:24-49: fc1 -> exact GELU -> fc2."""
+
+    def __init__(self, in_features: int, hidden_features: int, bias: bool = True, device=None):
+        super().__init__()
+        self.fc1 = nn.Linear(in_features, hidden_features, bias=bias, device=device)
+        self.fc2 = nn.Linear(hidden_features, in_features, bias=bias, device=device)
+
+
+class SwiGLUFFN(nn.Module):
+    """ffn_layers.py:60-115: silu(w1 x) * (w2 x) -> w3; hidden = int(h * 2/3) rounded up to align_to."""
+
+    def __init__(self, in_features: int, hidden_features: int, bias: bool = True, align_to: int = 64, device=None):
+        super().__init__()
+        d = int(hidden_features * 2 / 3)
+        hidden = d + (-d % align_to)
+        self.w1 = nn.Linear(in_features, hidden, bias=bias, device=device)
+        self.w2 = nn.Linear(in_features, hidden, bias=bias, device=device)
+        self.w3 = nn.Linear(hidden, in_features, bias=bias, device=device)
+
+
+class SelfAttention(nn.Module):
+    """attention.py:77-110 (parameters) and the attention half of the correction step (:393-534)."""
+
+    def __init__(self, dim: int, num_heads: int, qkv_bias: bool = False, proj_bias: bool = True,
+                 mask_k_bias: bool = False, device=None):
+        super().__init__()
+        self.num_heads = num_heads
+        self.head_dim = dim // num_heads
+        self.scale = self.head_dim ** -0.5
+        linear_class = LinearKMaskedBias if mask_k_bias else nn.Linear
+        self.qkv = linear_class(dim, dim * 3, bias=qkv_bias, device=device)
+        self.proj = nn.Linear(dim, dim, bias=proj_bias, device=device)
+        self._bias_key = None
+        self._bias_val = None
+
+    def qkv_bias(self) -> Tensor | None:
+        """Masked qkv bias, recomputed only when the bias or its mask changes."""
+        b = self.qkv.bias
+        if b is None:
+            return None
+        mask = getattr(self.qkv, "bias_mask", None)
+        key = (b.data_ptr(), b._version, None if mask is None else (mask.data_ptr(), mask._version))
+        if key != self._bias_key:
+            val = b.detach() if mask is None else (b.detach() * mask.to(b.dtype))
+            self._bias_val = val.to(torch.bfloat16).contiguous()
+            self._bias_key = key
+        return self._bias_val
+
+    def correct_partial_token(self, x_sel: Tensor, dindice: Tensor, rope, cache_feature: Dict, tag: str, *,
+                              fixed_query_state: PackedQueryState, sdpa_query_bucket_size: int = 0,
+                              **_) -> Tuple[Tensor, Dict]:
+        """Attention half of the correction for pre-normalised selected rows x_sel [M, C]:
+        qkv, RoPE, in-place K/V rewrite, sparse-query attention, proj. Returns (proj(attn), cache).
+
+        `sdpa_query_bucket_size` only padded the reference's SDPA query length; the kernel here
+        reads the packed queries directly, so it has no effect on the result.
+        """
+        kv = cache_feature[f"{tag}_kv"]
+        q_packed, attn = self._qkv_attention(x_sel, rope, kv, fixed_query_state)
+        out = K.linear(attn, self.proj.weight, self.proj.bias)
+        return out, cache_feature
+
+    def _qkv_attention(self, xn: Tensor, rope, kv: Tensor, qs: PackedQueryState):
+        M, C = xn.shape
+        H, D = self.num_heads, self.head_dim
+        B = kv.shape[0]
+        if M % B != 0:
+            raise ValueError(f"packed rows {M} do not split evenly over {B} images")
+        T = M // B
+        qkv = K.linear(xn, self.qkv.weight, self.qkv_bias())
+        q = torch.empty((M, H, D), device=xn.device, dtype=torch.bfloat16)
+        K.qkv_rope_kv_scatter(qkv.view(M, 3, H, D), rope, qs.active_patch_mask, qs.active_rope_idx,
+                              qs.active_batch_idx, qs.active_token_idx, kv, q)
+        attn = K.sparse_query_attention(q, kv, T, self.scale)
+        return q, attn
+
+
+# ------------------------------------------------------------------------------------------------
+# The block
+# ------------------------------------------------------------------------------------------------
+
+
+class SelfAttentionBlock(nn.Module):
+    _MOBILE_HINT_PSCORE_ALIASES = frozenset({
+        "residual_rms", "patch_residual_rms", "residual_l2", "residual_l2_energy", "residual_energy",
+        "patch_residual_l2", "patch_residual_energy",
+    })
+    _VALID_SERVER_PSCORES = frozenset({
+        "cls_attn_prob", "patch_attn_prob", "patch_attn_prob_layermean", "patch_pseudo_attn_prob",
+        "patch_pseudo_attn_prob_layermean", "cls_attn_prob_layermean", "random",
+    })
+    _LAYERMEAN_SERVER_PSCORES = frozenset({
+        "patch_attn_prob_layermean", "patch_pseudo_attn_prob_layermean", "cls_attn_prob_layermean",
+    })
+    _PARTIAL_TOKEN_PLAN_CACHE_KEY = "_partial_token_query_plan_cache"
+
+    def __init__(self, dim: int, num_heads: int, ffn_ratio: float = 4.0, qkv_bias: bool = False,
+                 proj_bias: bool = True, ffn_bias: bool = True, init_values: float | None = None,
+                 norm_eps: float = 1e-5, ffn_layer: str = "mlp", mask_k_bias: bool = False, device=None):
+        super().__init__()
+        self.norm1 = nn.LayerNorm(dim, eps=norm_eps, device=device)
+        self.attn = SelfAttention(dim, num_heads, qkv_bias=qkv_bias, proj_bias=proj_bias, mask_k_bias=mask_k_bias,
+                                  device=device)
+        self.ls1 = LayerScale(dim, init_values, device=device) if init_values else nn.Identity()
+        self.norm2 = nn.LayerNorm(dim, eps=norm_eps, device=device)
+        hidden = int(dim * ffn_ratio)
+        if ffn_layer == "mlp":
+            self.mlp = Mlp(dim, hidden, bias=ffn_bias, device=device)
+        elif ffn_layer.startswith("swiglu"):
+            align = int(ffn_layer[len("swiglu"):] or 8)
+            self.mlp = SwiGLUFFN(dim, hidden, bias=ffn_bias, align_to=align, device=device)
+        else:
+            raise ValueError(f"unknown ffn_layer {ffn_layer!r}")
+        self.ls2 = LayerScale(dim, init_values, device=device) if init_values else nn.Identity()
+        self._ones = None
+
+    # -- helpers ---------------------------------------------------------------------------------
+
+    def _gamma(self, ls: nn.Module, like: Tensor) -> Tensor:
+        g = getattr(ls, "gamma", None)
+        if g is not None:
+            return g if g.dtype == torch.bfloat16 else g.to(torch.bfloat16)
+        if self._ones is None or self._ones.device != like.device or self._ones.numel() != like.shape[-1]:
+            self._ones = torch.ones(like.shape[-1], device=like.device, dtype=torch.bfloat16)
+        return self._ones
+
+    def _mlp_scaled(self, xn: Tensor) -> Tensor:
+        """gamma2 * MLP(xn) with GELU / SwiGLU and LayerScale fused into the GEMM epilogues."""
+        g2 = self._gamma(self.ls2, xn)
+        if isinstance(self.mlp, Mlp):
+            h = K.linear(xn, self.mlp.fc1.weight, self.mlp.fc1.bias, epilogue=_lib.EPI_BIAS_GELU)
+            return K.linear(h, self.mlp.fc2.weight, self.mlp.fc2.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g2)
+        x2 = K.linear(xn, self.mlp.w2.weight, self.mlp.w2.bias)
+        h = K.linear(xn, self.mlp.w1.weight, self.mlp.w1.bias, epilogue=_lib.EPI_BIAS_SILU_MUL, resid=x2)
+        return K.linear(h, self.mlp.w3.weight, self.mlp.w3.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g2)
+
+    # -- dispatch (block.py:274-310) --------------------------------------------------------------
+
+    def approx(self, x: Tensor, rope, cache_feature: Dict, tag: str, **kwargs):
+        method = kwargs.get("appcorr_method", "partial_token")
+        if method != "partial_token":
+            raise NotImplementedError(f"appcorr_method {method!r} is not part of this build (partial_token only)")
+        return self.approx_partial_token(x, rope, cache_feature, tag, **kwargs)
+
+    def correct(self, x: Tensor, dindice: Tensor, rope, cache_feature: Dict, tag: str, **kwargs):
+        method = kwargs.get("appcorr_method", "partial_token")
+        if method != "partial_token":
+            raise NotImplementedError(f"appcorr_method {method!r} is not part of this build (partial_token only)")
+        return self.correct_partial_token(x, dindice, rope, cache_feature, tag, **kwargs)
+
+    # -- approximate pass: the cache producer (block.py:312-349; attention.py:215-278) -------------
+
+    def approx_partial_token(self, x: Tensor, rope, cache_feature: Dict, tag: str, **kwargs):
+        """Full forward over all tokens that caches {tag}_kv (K after RoPE) and
+        {tag}_blocks_out_sum, on the same kernels as the correction (identity plan, T = N)."""
+        server_pscore = str(kwargs.get("server_pscore", "cls_attn_prob"))
+        if float(kwargs.get("server_pscore_weight", 1.0)) == 0.0:
+            server_pscore = "none"
+        self._invalidate_partial_token_derived_caches(cache_feature)
+        B, N, C = x.shape
+        H, D = self.attn.num_heads, self.attn.head_dim
+        prefix = N - rope[0].shape[0] if rope is not None else N
+        dev = x.device
+        tok = torch.arange(N, device=dev, dtype=torch.long)
+        qs = PackedQueryState(
+            active_batch_idx=torch.arange(B, device=dev, dtype=torch.long).repeat_interleave(N),
+            active_pos_idx=tok.repeat(B), active_token_idx=tok.repeat(B),
+            query_valid_mask=torch.ones((B, N), device=dev, dtype=torch.bool),
+            active_query_pos_padded=tok.unsqueeze(0).expand(B, -1), active_query_mask=None, all_valid=True,
+            active_patch_mask=(tok >= prefix).repeat(B), active_rope_idx=(tok - prefix).clamp_min(0).repeat(B))
+        x2 = x.reshape(B * N, C)
+        kv = torch.empty((B, N, 2, H, D), device=dev, dtype=torch.bfloat16)
+        cache_feature[f"{tag}_kv"] = kv
+        xn = K.layer_norm(x2, self.norm1.weight, self.norm1.bias, self.norm1.eps)
+        q, attn = self.attn._qkv_attention(xn, rope, kv, qs)
+        g1 = self._gamma(self.ls1, x2)
+        inc = K.linear(attn, self.attn.proj.weight, self.attn.proj.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g1)
+        ones = self._gamma(nn.Identity(), x2)
+        x_attn = K.fused_layerscale_add(x2, inc, ones)                       # x + ls1(attn)
+        mlp = self._mlp_scaled(K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps))
+        cache_feature[f"{tag}_blocks_out_sum"] = K.fused_layerscale_add(inc, mlp, ones).view(B, N, C)
+        out = K.fused_layerscale_add(x_attn, mlp, ones).view(B, N, C)
+        if server_pscore not in ("none", "disabled"):
+            cache_feature[f"{tag}_server_pscore"] = self._server_pscore(q.view(B, N, H, D), kv, server_pscore)
+        return out, cache_feature
+
+    def _server_pscore(self, q: Tensor, kv: Tensor, kind: str) -> Tensor:
+        """cls_attn_prob (attention.py:267-271): softmax of the cls query over all keys, head mean.
+        Evaluated in fp32 on contiguous copies (a [B, H, 1, N] product per layer)."""
+        if kind not in ("cls_attn_prob", "cls_attn_prob_layermean"):
+            raise NotImplementedError(f"server_pscore {kind!r} is not produced by this build's approx pass")
+        qc = q[:, 0].float().unsqueeze(2)                                    # [B, H, 1, D]
+        kk = kv[:, :, 0].float().permute(0, 2, 3, 1).contiguous()            # [B, H, D, N]
+        s = torch.matmul(qc, kk) * self.attn.scale
+        return s.softmax(-1).mean(dim=1).squeeze(1).to(torch.float32)
+
+    # -- plan bookkeeping (block.py:358-940) --------------------------------------------------------
+
+    @staticmethod
+    def _tensor_cache_signature(t: Tensor | None):
+        if t is None:
+            return None
+        try:
+            version = t._version
+        except RuntimeError:
+            version = None
+        return (t.data_ptr(), tuple(t.shape), tuple(t.stride()), t.storage_offset(), str(t.device), str(t.dtype),
+                version)
+
+    @classmethod
+    def _shared_partial_token_plan_key(cls, *, dindice, mobile_pscore_hint, num_pretokens, num_tokens,
+                                       token_keep_ratio, token_keep_thres, server_pscore, server_pscore_weight,
+                                       mobile_pscore, mobile_pscore_weight, pscore_fusion):
+        """Plans are shared across layers only when the score does not depend on the layer
+        (block.py:709-741): server weight 0, or a layer-mean server score."""
+        if server_pscore_weight != 0.0 and server_pscore not in cls._LAYERMEAN_SERVER_PSCORES:
+            return None
+        return ("partial_token", cls._tensor_cache_signature(dindice), cls._tensor_cache_signature(mobile_pscore_hint),
+                num_pretokens, num_tokens, float(token_keep_ratio), token_keep_thres, server_pscore,
+                float(server_pscore_weight), mobile_pscore, float(mobile_pscore_weight), pscore_fusion)
+
+    @classmethod
+    def _get_partial_token_plan_cache(cls, cache_feature: Dict) -> Dict:
+        pc = cache_feature.setdefault(cls._PARTIAL_TOKEN_PLAN_CACHE_KEY, {})
+        if not isinstance(pc, dict):
+            raise RuntimeError(f"{cls._PARTIAL_TOKEN_PLAN_CACHE_KEY} must be a dict")
+        return pc
+
+    @classmethod
+    def _invalidate_partial_token_derived_caches(cls, cache_feature: Dict) -> None:
+        cache_feature.pop(cls._PARTIAL_TOKEN_PLAN_CACHE_KEY, None)
+        for key in [k for k in cache_feature if k.startswith("_shared_")]:
+            cache_feature.pop(key, None)
+
+    def _resolve_mobile_patch_scores(self, mobile_pscore, hint, dindice_patches, *, num_pretokens, num_tokens):
+        """block.py:638-667."""
+        if mobile_pscore not in self._MOBILE_HINT_PSCORE_ALIASES or hint is None:
+            return None
+        if hint.shape[0] != dindice_patches.shape[0]:
+            raise RuntimeError(f"Mobile pscore hint batch mismatch: hint={tuple(hint.shape)} "
+                               f"candidates={tuple(dindice_patches.shape)}")
+        if hint.shape[1] == num_tokens - num_pretokens:
+            return hint.gather(1, dindice_patches - num_pretokens)
+        if hint.shape[1] == num_tokens:
+            return hint.gather(1, dindice_patches)
+        raise RuntimeError(f"Unsupported mobile pscore hint shape {tuple(hint.shape)} for num_tokens={num_tokens}, "
+                           f"num_pretokens={num_pretokens}")
+
+    @staticmethod
+    def _combine_patch_scores(server, server_w, mobile, mobile_w, fusion):
+        """block.py:669-687."""
+        combined = server_w * server
+        if mobile is None or mobile_w == 0.0:
+            return combined
+        term = mobile_w * mobile.to(dtype=combined.dtype)
+        if fusion == "multiply":
+            return combined * term
+        if fusion == "geo_mean":
+            return torch.sqrt(torch.clamp(combined * term, min=0.0))
+        return combined + term
+
+    def _resolve_server_token_scores(self, cache_feature: Dict, tag: str, server_pscore: str) -> Tensor:
+        """block.py:862-940 (layer-mean averaging over this stack, the per-stack random control)."""
+        if server_pscore in self._LAYERMEAN_SERVER_PSCORES:
+            stack = tag.rstrip("0123456789")
+            ck = f"_shared_{server_pscore}_server_pscore_mean_{stack}"
+            cached = cache_feature.get(ck)
+            if cached is not None:
+                return cached
+            keys = tuple(sorted(k for k, v in cache_feature.items()
+                                if k.endswith("_server_pscore") and isinstance(v, Tensor)
+                                and k[: -len("_server_pscore")].rstrip("0123456789") == stack))
+            if not keys:
+                raise KeyError(f"Missing cached *_server_pscore entries for stack '{stack}'. "
+                               "They must be produced during approx.")
+            ts = [cache_feature[k] for k in keys]
+            if any(t.shape != ts[0].shape for t in ts[1:]):
+                raise RuntimeError("Cannot average server pscores across layers with inconsistent shapes")
+            mean = torch.stack(ts, dim=0).mean(dim=0)
+            cache_feature[ck] = mean.detach()
+            cache_feature[f"{ck}_keys"] = keys
+            return mean
+        scores = cache_feature.get(f"{tag}_server_pscore")
+        if scores is None:
+            raise KeyError(f"Missing cached {tag}_server_pscore. It must be produced during approx.")
+        if server_pscore == "random":
+            stack = tag.rstrip("0123456789")
+            key = f"_shared_random_server_pscore_{stack}"
+            cached = cache_feature.get(key)
+            if cached is None:
+                cached = torch.rand_like(scores)
+                cache_feature[key] = cached
+            return cached
+        return scores
+
+    @staticmethod
+    def _accumulate_partial_token_plan_stats(cache_feature: Dict, plan: PartialTokenQueryPlan, scale: float = 1.0):
+        """block.py:790-844: running kept / full score mass and patch counts."""
+        pairs = (("_token_pscore_kept_mass_total", plan.kept_pscore_mass),
+                 ("_token_pscore_full_mass_total", plan.full_pscore_mass),
+                 ("_partial_token_kept_patch_total", plan.kept_patch_total),
+                 ("_partial_token_full_patch_total", plan.full_patch_total),
+                 ("_partial_token_sample_total", plan.sample_total))
+        for key, val in pairs:
+            v = val * scale if scale != 1.0 else val
+            prev = cache_feature.get(key)
+            cache_feature[key] = (val.new_zeros((), dtype=torch.float32) if prev is None else prev) + v
+
+    def _build_query_plan(self, x: Tensor, dindice: Tensor, rope, cache_feature: Dict, tag: str, kw: dict,
+                          num_pretokens: int) -> PartialTokenQueryPlan:
+        B, N, _ = x.shape
+        dindice_patches = dindice[:, num_pretokens:]
+        mobile = None
+        if kw["mobile_pscore"] != "none" and kw["mobile_pscore_weight"] != 0.0:
+            mobile = self._resolve_mobile_patch_scores(kw["mobile_pscore"], kw["mobile_pscore_hint"], dindice_patches,
+                                                       num_pretokens=num_pretokens, num_tokens=N)
+        if kw["server_pscore_weight"] == 0.0:
+            server = x.new_zeros((B, dindice_patches.shape[1]), dtype=torch.float32)
+        else:
+            server = self._resolve_server_token_scores(cache_feature, tag, kw["server_pscore"]).gather(1,
+                                                                                                       dindice_patches)
+        combined = self._combine_patch_scores(server, kw["server_pscore_weight"], mobile, kw["mobile_pscore_weight"],
+                                              kw["pscore_fusion"])
+        cvm = kw.get("candidate_valid_mask")
+        if cvm is not None:
+            combined = combined.masked_fill(~cvm.to(combined.device), float("-inf"))
+        Pn = dindice_patches.shape[1]
+        if kw["token_keep_thres"] is not None:
+            raise NotImplementedError("threshold token selection (token_keep_thres) is not part of this build; "
+                                      "use token_keep_ratio (top-k)")
+        ratio = float(kw["token_keep_ratio"])
+        k = Pn if ratio >= 1.0 else min(int(Pn * ratio), Pn)
+        scores = combined.to(torch.float32).contiguous()
+        tp = K.topk_plan(scores, k, dindice.contiguous(), num_pretokens, N)
+        T = num_pretokens + k
+        qs = PackedQueryState(
+            active_batch_idx=tp.active_batch_idx, active_pos_idx=tp.active_pos_idx,
+            active_token_idx=tp.active_token_idx,
+            query_valid_mask=torch.ones((B, T), device=x.device, dtype=torch.bool),
+            active_query_pos_padded=torch.arange(T, device=x.device, dtype=torch.long).unsqueeze(0).expand(B, -1),
+            active_query_mask=None, all_valid=True, active_patch_mask=tp.active_patch_mask,
+            active_rope_idx=tp.active_rope_idx, row_slot=tp.row_slot)
+        qs.active_query_mask = qs.query_valid_mask
+        keep = tp.keep_mask
+        return PartialTokenQueryPlan(
+            update_indice=tp.update_indice, fixed_query_state=qs, server_patch_scores=server.detach(),
+            mobile_patch_scores=None if mobile is None else mobile.detach(), combined_patch_scores=combined.detach(),
+            kept_pscore_mass=(combined * keep.to(combined.dtype)).sum(dtype=torch.float32),
+            full_pscore_mass=combined.sum(dtype=torch.float32),
+            kept_patch_total=keep.sum(dtype=torch.float32),
+            full_patch_total=keep.new_full((), float(keep.shape[0] * keep.shape[1]), dtype=torch.float32),
+            sample_total=keep.new_full((), float(keep.shape[0]), dtype=torch.float32))
+
+    # -- the correction step (block.py:942-1191) ---------------------------------------------------
+
+    def correct_partial_token(self, x: Tensor, dindice: Tensor, rope, cache_feature: Dict, tag: str, **kwargs):
+        debug = bool(kwargs.get("debug", False))
+        kw = {
+            "token_keep_ratio": kwargs.get("token_keep_ratio", 0.2),
+            "token_keep_thres": None if kwargs.get("token_keep_thres") in (None, "", "null", "None")
+            else float(kwargs["token_keep_thres"]),
+            "server_pscore_weight": float(kwargs.get("server_pscore_weight", 1.0)),
+            "server_pscore": str(kwargs.get("server_pscore", "cls_attn_prob")),
+            "mobile_pscore": str(kwargs.get("mobile_pscore", "none")),
+            "mobile_pscore_weight": float(kwargs.get("mobile_pscore_weight", 0.0)),
+            "mobile_pscore_hint": kwargs.get("mobile_pscore_hint"),
+            "pscore_fusion": str(kwargs.get("pscore_fusion", "add")).lower(),
+            "candidate_valid_mask": kwargs.get("candidate_valid_mask"),
+        }
+        if kw["pscore_fusion"] not in ("add", "multiply", "geo_mean"):
+            kw["pscore_fusion"] = "add"
+        if kw["server_pscore"] not in self._VALID_SERVER_PSCORES:
+            raise ValueError(f"Unknown server_pscore '{kw['server_pscore']}'. "
+                             f"Available values: {sorted(self._VALID_SERVER_PSCORES)}")
+        if x.dtype != torch.bfloat16 or x.dim() != 3:
+            raise ValueError("correct_partial_token expects x [B, N, C] bf16")
+        B, N, C = x.shape
+        num_pretokens = kwargs.get("num_pretokens")
+        if num_pretokens is None:
+            num_pretokens = N - rope[0].shape[0]
+        num_pretokens = int(num_pretokens)
+
+        key = self._shared_partial_token_plan_key(
+            dindice=dindice, mobile_pscore_hint=kw["mobile_pscore_hint"] if kw["mobile_pscore_weight"] != 0.0 else None,
+            num_pretokens=num_pretokens, num_tokens=N, token_keep_ratio=kw["token_keep_ratio"],
+            token_keep_thres=kw["token_keep_thres"], server_pscore=kw["server_pscore"],
+            server_pscore_weight=kw["server_pscore_weight"], mobile_pscore=kw["mobile_pscore"],
+            mobile_pscore_weight=kw["mobile_pscore_weight"], pscore_fusion=kw["pscore_fusion"])
+        plan = None
+        if key is not None:
+            plan = self._get_partial_token_plan_cache(cache_feature).get(key)
+            if plan is not None and not isinstance(plan, PartialTokenQueryPlan):
+                raise RuntimeError("Corrupt partial-token query-plan cache entry")
+        hit = plan is not None
+        if plan is None:
+            plan = self._build_query_plan(x, dindice, rope, cache_feature, tag, kw, num_pretokens)
+            if key is not None:
+                self._get_partial_token_plan_cache(cache_feature)[key] = plan
+        if not hit:
+            scale = float(kwargs.get("partial_token_plan_stat_scale", 1.0)) if key is not None else 1.0
+            self._accumulate_partial_token_plan_stats(cache_feature, plan, scale=scale)
+        if plan.mobile_patch_scores is not None:
+            cache_feature[f"{tag}_mobile_pscore_sel"] = plan.mobile_patch_scores
+        cache_feature[f"{tag}_server_pscore_sel"] = plan.server_patch_scores
+        cache_feature[f"{tag}_combined_pscore"] = plan.combined_patch_scores
+        if debug:
+            cache_feature[f"{tag}_update_indice"] = plan.update_indice
+
+        qs = plan.fixed_query_state
+        kv = cache_feature[f"{tag}_kv"]
+        bos = cache_feature[f"{tag}_blocks_out_sum"]
+        if kv.dtype != torch.bfloat16 or bos.dtype != torch.bfloat16:
+            raise ValueError("the correction cache ({tag}_kv, {tag}_blocks_out_sum) must be bf16")
+        if not bos.is_contiguous():
+            raise ValueError("{tag}_blocks_out_sum must be contiguous")
+        inplace = bool(kwargs.get("inplace_residual_add", False)) and not torch.is_grad_enabled()
+        xc = x if x.is_contiguous() else x.contiguous()
+        out = xc if inplace else torch.empty_like(xc)
+        M = qs.active_token_idx.numel()
+        if M == 0:
+            empty = xc.new_empty((0, C))
+            return K.reconstruct_scatter_persist(xc, bos, qs.row_slot, empty, empty, empty, out=out), cache_feature
+
+        x_act = K.gather_rows(xc, qs.active_batch_idx, qs.active_token_idx)          # block.py:1111
+        xn = K.layer_norm(x_act, self.norm1.weight, self.norm1.bias, self.norm1.eps)   # :1114
+        _, attn = self.attn._qkv_attention(xn, rope, kv, qs)                         # attention.py:415-523
+        x_attn = K.linear(attn, self.attn.proj.weight, self.attn.proj.bias,          # attention.py:532 +
+                          epilogue=_lib.EPI_BIAS_LS_RESID, gamma=self._gamma(self.ls1, x_act),
+                          resid=x_act)                                               # block.py:1129-1134
+        mlp = self._mlp_scaled(K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps))  # :1141
+        out = K.reconstruct_scatter_persist(xc, bos, qs.row_slot, x_act, x_attn, mlp, out=out)  # :1140-1179
+        if os.environ.get("APPCORR_PERSIST_TRACE") and not getattr(SelfAttentionBlock, "_persist_traced", False):
+            SelfAttentionBlock._persist_traced = True
+            print(f"[persist] blocks_out_sum write executed, tag={tag} rows={M}", flush=True)
+        return out, cache_feature

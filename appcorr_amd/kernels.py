@@ -1,0 +1,413 @@
+"""Tensor-level wrappers over the gfx950 C ABI.
+
+The names and argument meaning follow the reference's kernel wrappers so call sites read the same
+(reference: appcorr/models/dinov3/layers/triton_kernels/{token_update,rope,nvfp4_fused}.py). One
+behavioural difference is deliberate: where a reference wrapper returned False/None on an
+unsupported layout (and `note_fallback` raised by default), these raise `OudjatKernelError` /
+`ValueError` directly. There is no eager fallback.
+
+Every launch is enqueued on torch's current stream of the tensors' device and returns without
+synchronising.
+"""
+
+from __future__ import annotations
+
+import ctypes
+from dataclasses import dataclass
+
+import torch
+
+from . import _lib
+from ._lib import call
+
+P = ctypes.c_void_p
+
+# Optional live timing of one launch site: when `_probe["tag"]` names a site, every launch there is
+# bracketed by a pair of timing events on the launch stream (used by bench.py for the roofline).
+_probe: dict = {"tag": None, "events": []}
+
+
+def set_probe(tag: str | None) -> None:
+    _probe["tag"] = tag
+    _probe["events"] = []
+
+
+def probe_events() -> list:
+    return _probe["events"]
+
+
+def _launch(tag: str, t: torch.Tensor, name: str, *args) -> None:
+    if _probe["tag"] != tag:
+        call(name, *args)
+        return
+    s = torch.cuda.current_stream(t.device)
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0.record(s)
+    call(name, *args)
+    e1.record(s)
+    _probe["events"].append((e0, e1))
+
+
+def _ptr(t: torch.Tensor | None) -> P:
+    return P(0 if t is None else t.data_ptr())
+
+
+def _stream(t: torch.Tensor) -> P:
+    return P(_lib.stream_of(t))
+
+
+def _require_cuda(*tensors: torch.Tensor | None) -> None:
+    dev = None
+    for t in tensors:
+        if t is None:
+            continue
+        if not t.is_cuda:
+            raise ValueError("appcorr_amd kernels run on the GPU only; got a CPU tensor (no CPU fallback exists)")
+        if dev is None:
+            dev = t.device
+        elif t.device != dev:
+            raise ValueError(f"tensors on different devices: {dev} vs {t.device}")
+
+
+def _require(cond: bool, msg: str) -> None:
+    if not cond:
+        raise ValueError(msg)
+
+
+def _index(t: torch.Tensor, name: str) -> torch.Tensor:
+    _require(t.dtype == torch.long and t.dim() == 1, f"{name} must be a 1-D int64 tensor")
+    return t.contiguous()
+
+
+def trailing_is_packed(t: torch.Tensor, first_row_dim: int) -> bool:
+    """True when dims >= first_row_dim form one contiguous run (a row), whatever the outer strides.
+
+    Same acceptance rule as the reference's `_trailing_is_packed` (token_update.py:390-404): a view
+    like qkv_new[:, 1:] has row stride 3C but its 2C row elements are contiguous.
+    """
+    expected = 1
+    for d in range(t.dim() - 1, first_row_dim - 1, -1):
+        if t.shape[d] != 1 and t.stride(d) != expected:
+            return False
+        expected *= t.shape[d]
+    return True
+
+
+def _row_elems(t: torch.Tensor, first_row_dim: int) -> int:
+    n = 1
+    for d in range(first_row_dim, t.dim()):
+        n *= t.shape[d]
+    return n
+
+
+# ------------------------------------------------------------------------------------------------
+# Row movement (token_update.py:352-473, 257-347, 10-60)
+# ------------------------------------------------------------------------------------------------
+
+
+def gather_rows(src: torch.Tensor, batch_idx: torch.Tensor, token_idx: torch.Tensor) -> torch.Tensor:
+    """`src[batch_idx, token_idx]` as a new contiguous tensor of shape [n, *src.shape[2:]]."""
+    _require_cuda(src, batch_idx, token_idx)
+    _require(src.dim() >= 2 and trailing_is_packed(src, 2), "gather_rows: src rows (dims 2..) must be packed")
+    bi, ti = _index(batch_idx, "batch_idx"), _index(token_idx, "token_idx")
+    _require(bi.numel() == ti.numel(), "gather_rows: index length mismatch")
+    n = bi.numel()
+    out = torch.empty((n, *src.shape[2:]), device=src.device, dtype=src.dtype)
+    row_bytes = _row_elems(src, 2) * src.element_size()
+    if n == 0 or row_bytes == 0:
+        return out
+    es = src.element_size()
+    _launch("gather_rows", src, "oudjat_gather_rows", _ptr(src), src.stride(0) * es, src.stride(1) * es, row_bytes, _ptr(bi), _ptr(ti), n,
+         _ptr(out), row_bytes, _stream(src))
+    return out
+
+
+def scatter_rows(dst: torch.Tensor, batch_idx: torch.Tensor, token_idx: torch.Tensor, src: torch.Tensor) -> bool:
+    """`dst[batch_idx, token_idx] = src` in place; (batch, token) pairs must be unique. Returns True."""
+    _require_cuda(dst, batch_idx, token_idx, src)
+    _require(dst.dim() >= 2 and trailing_is_packed(dst, 2), "scatter_rows: dst rows (dims 2..) must be packed")
+    _require(src.dim() >= 1 and trailing_is_packed(src, 1), "scatter_rows: src rows (dims 1..) must be packed")
+    _require(src.dtype == dst.dtype, "scatter_rows: dtype mismatch")
+    bi, ti = _index(batch_idx, "batch_idx"), _index(token_idx, "token_idx")
+    n = bi.numel()
+    _require(ti.numel() == n and src.shape[0] == n, "scatter_rows: length mismatch")
+    row = _row_elems(dst, 2)
+    _require(_row_elems(src, 1) == row, f"scatter_rows: row width mismatch ({_row_elems(src, 1)} vs {row})")
+    if n == 0 or row == 0:
+        return True
+    es = dst.element_size()
+    _launch("scatter_rows", dst, "oudjat_scatter_rows", _ptr(dst), dst.stride(0) * es, dst.stride(1) * es, row * es, _ptr(bi), _ptr(ti), n,
+         _ptr(src), src.stride(0) * es, _stream(dst))
+    return True
+
+
+def active_token_update(x_base: torch.Tensor, active_batch_idx: torch.Tensor, active_token_idx: torch.Tensor,
+                        x_attn_active: torch.Tensor, x_delta_active: torch.Tensor, *,
+                        clone_base: bool = True) -> torch.Tensor:
+    """x_out = x_base (cloned unless clone_base=False); x_out[b_i, t_i] = x_attn_i + x_delta_i (bf16)."""
+    _require_cuda(x_base, active_batch_idx, active_token_idx, x_attn_active, x_delta_active)
+    x_out = x_base.clone() if clone_base else x_base
+    n = active_batch_idx.numel()
+    if n == 0:
+        return x_out
+    _require(x_out.dtype == torch.bfloat16 and x_out.dim() == 3 and x_out.stride(2) == 1,
+             "active_token_update: x_base must be [B, N, C] bf16 with contiguous rows")
+    a = x_attn_active.to(torch.bfloat16).contiguous()
+    d = x_delta_active.to(torch.bfloat16).contiguous()
+    C = x_out.shape[2]
+    _require(a.shape == (n, C) and d.shape == (n, C), "active_token_update: [n, C] sources required")
+    call("oudjat_active_token_update", _ptr(x_out), x_out.stride(0), x_out.stride(1),
+         _ptr(_index(active_batch_idx, "batch")), _ptr(_index(active_token_idx, "token")), n, _ptr(a), C, _ptr(d),
+         C, C, _stream(x_out))
+    return x_out
+
+
+def fused_layerscale_add(x: torch.Tensor, x_attn: torch.Tensor, gamma: torch.Tensor) -> torch.Tensor:
+    """out = x + x_attn * gamma (gamma broadcast over the last dim), bf16."""
+    _require_cuda(x, x_attn, gamma)
+    _require(x.dtype == x_attn.dtype == gamma.dtype == torch.bfloat16, "fused_layerscale_add: bf16 only")
+    _require(x.shape == x_attn.shape and x.is_contiguous() and x_attn.is_contiguous(),
+             "fused_layerscale_add: contiguous tensors of one shape required")
+    C = x.shape[-1]
+    g = gamma.contiguous()
+    _require(g.numel() == C, "fused_layerscale_add: gamma must have C entries")
+    out = torch.empty_like(x)
+    rows = x.numel() // C if C else 0
+    call("oudjat_fused_layerscale_add", _ptr(x), _ptr(x_attn), _ptr(g), rows, C, _ptr(out), _stream(x))
+    return out
+
+
+def reconstruct_scatter_persist(x: torch.Tensor, blocks_out_sum: torch.Tensor, row_slot: torch.Tensor,
+                                x_act: torch.Tensor, x_attn: torch.Tensor, mlp: torch.Tensor,
+                                out: torch.Tensor | None = None) -> torch.Tensor:
+    """Fused block.py:1140-1179: x_out = x + blocks_out_sum off the selected rows; on them
+    x_out = x_attn + mlp and blocks_out_sum = (x_attn - x_act) + mlp (in place). `out` may alias x."""
+    _require_cuda(x, blocks_out_sum, row_slot, x_act, x_attn, mlp, out)
+    _require(x.dtype == blocks_out_sum.dtype == torch.bfloat16, "reconstruct_scatter_persist: bf16 only")
+    _require(x.is_contiguous() and blocks_out_sum.is_contiguous() and x.shape == blocks_out_sum.shape,
+             "reconstruct_scatter_persist: contiguous x / blocks_out_sum of one shape required")
+    _require(row_slot.dtype == torch.int32 and row_slot.is_contiguous() and row_slot.numel() * x.shape[-1] == x.numel(),
+             "reconstruct_scatter_persist: row_slot must be int32 with one entry per row")
+    for t, nm in ((x_act, "x_act"), (x_attn, "x_attn"), (mlp, "mlp")):
+        _require(t.dtype == torch.bfloat16 and t.is_contiguous() and t.shape[-1] == x.shape[-1],
+                 f"reconstruct_scatter_persist: {nm} must be contiguous bf16 [M, C]")
+    if out is None:
+        out = torch.empty_like(x)
+    C = x.shape[-1]
+    _launch("reconstruct", x, "oudjat_reconstruct_scatter_persist", _ptr(x), _ptr(blocks_out_sum), _ptr(row_slot), _ptr(x_act),
+         _ptr(x_attn), _ptr(mlp), x.numel() // C, C, _ptr(out), _stream(x))
+    return out
+
+
+# ------------------------------------------------------------------------------------------------
+# Plan (block.py:358-490)
+# ------------------------------------------------------------------------------------------------
+
+
+@dataclass
+class TopkPlan:
+    update_indice: torch.Tensor      # [B, T] int64
+    active_batch_idx: torch.Tensor   # [M] int64
+    active_pos_idx: torch.Tensor     # [M] int64
+    active_token_idx: torch.Tensor   # [M] int64
+    active_patch_mask: torch.Tensor  # [M] bool
+    active_rope_idx: torch.Tensor    # [M] int64
+    keep_mask: torch.Tensor          # [B, P] bool
+    row_slot: torch.Tensor | None    # [B, N] int32 (packed row of each token or -1)
+
+
+def topk_plan(scores: torch.Tensor, k: int, dindice: torch.Tensor, num_pretokens: int,
+              num_tokens: int | None = None) -> TopkPlan:
+    """Select the k highest-scoring candidates per row and build the packed query plan on device.
+
+    scores [B, P] fp32 (combined patch scores), dindice [B, num_pretokens + P] int64. Ties go to the
+    lower candidate index. `num_tokens` (N) additionally requests the token -> packed-row map.
+    """
+    _require_cuda(scores, dindice)
+    _require(scores.dtype == torch.float32 and scores.dim() == 2 and scores.stride(1) == 1,
+             "topk_plan: scores must be [B, P] fp32 with contiguous rows")
+    _require(dindice.dtype == torch.long and dindice.dim() == 2 and dindice.stride(1) == 1,
+             "topk_plan: dindice must be [B, pre + P] int64 with contiguous rows")
+    B, Pn = scores.shape
+    _require(dindice.shape[0] == B and dindice.shape[1] == num_pretokens + Pn, "topk_plan: dindice shape mismatch")
+    k = int(k)
+    _require(0 <= k <= Pn, f"topk_plan: k={k} outside [0, {Pn}]")
+    T = num_pretokens + k
+    dev = scores.device
+    upd = torch.empty((B, T), device=dev, dtype=torch.long)
+    abat = torch.empty((B * T,), device=dev, dtype=torch.long)
+    apos = torch.empty_like(abat)
+    atok = torch.empty_like(abat)
+    pmask = torch.empty((B * T,), device=dev, dtype=torch.bool)
+    ridx = torch.empty_like(abat)
+    keep = torch.empty((B, Pn), device=dev, dtype=torch.bool)
+    slot = None
+    if num_tokens is not None:
+        slot = torch.empty((B, int(num_tokens)), device=dev, dtype=torch.int32)
+    _launch("topk_plan", scores, "oudjat_topk_plan", _ptr(scores), B, Pn, scores.stride(0), k, _ptr(dindice), dindice.stride(0),
+         num_pretokens, 0 if num_tokens is None else int(num_tokens), _ptr(upd), _ptr(abat), _ptr(apos), _ptr(atok),
+         _ptr(pmask), _ptr(ridx), _ptr(keep), _ptr(slot), _stream(scores))
+    return TopkPlan(upd, abat, apos, atok, pmask, ridx, keep, slot)
+
+
+def patch_importance(delta: torch.Tensor, mode: int = _lib.IMPORTANCE_L2) -> torch.Tensor:
+    """Per-row reduction of a residual delta [..., D] fp32: L2 norm, energy or RMS -> [...]."""
+    _require_cuda(delta)
+    _require(delta.dtype == torch.float32 and delta.stride(-1) == 1, "patch_importance: fp32, contiguous rows")
+    d2 = delta.reshape(-1, delta.shape[-1])
+    out = torch.empty(d2.shape[0], device=delta.device, dtype=torch.float32)
+    _launch("importance", delta, "oudjat_patch_importance", _ptr(d2), d2.shape[0], d2.shape[1], d2.stride(0), int(mode), _ptr(out),
+         _stream(delta))
+    return out.view(delta.shape[:-1])
+
+
+# ------------------------------------------------------------------------------------------------
+# LayerNorm, RoPE, QKV post-processing (block.py:1114,1141; rope.py:186-240; attention.py:415-454)
+# ------------------------------------------------------------------------------------------------
+
+
+def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float = 1e-5,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    _require_cuda(x, weight, bias)
+    _require(x.dtype == weight.dtype == bias.dtype == torch.bfloat16, "layer_norm: bf16 only")
+    C = x.shape[-1]
+    x2 = x.reshape(-1, C)
+    _require(x2.stride(1) == 1, "layer_norm: rows must be contiguous")
+    if out is None:
+        out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
+    o2 = out.view(-1, C)
+    _launch("layernorm", x, "oudjat_layernorm_rows", _ptr(x2), x2.shape[0], C, x2.stride(0), _ptr(weight.contiguous()),
+         _ptr(bias.contiguous()), float(eps), _ptr(o2), o2.stride(0), _stream(x))
+    return out
+
+
+def apply_rope_active_inplace(q_active: torch.Tensor, k_active: torch.Tensor, rope, patch_mask: torch.Tensor,
+                              rope_idx: torch.Tensor) -> None:
+    """Rotate-half RoPE on [T, H, Dh] q and k views in place, fp32 math; rows with patch_mask False
+    are untouched. Same contract as apply_rope_active_inplace_triton (rope.py:186-240)."""
+    sin, cos = rope
+    _require_cuda(q_active, k_active, patch_mask, rope_idx, sin, cos)
+    _require(q_active.dim() == 3 and q_active.shape == k_active.shape, "rope: q/k must be [T, H, D] of one shape")
+    _require(q_active.dtype == k_active.dtype == torch.bfloat16, "rope: bf16 q/k only")
+    _require(sin.dtype == cos.dtype == torch.float32 and sin.stride(-1) == 1 and cos.stride(-1) == 1
+             and sin.stride(0) == cos.stride(0), "rope: fp32 sin/cos tables with matching contiguous rows")
+    _require(patch_mask.dim() == 1 and rope_idx.dim() == 1 and patch_mask.is_contiguous() and rope_idx.is_contiguous(),
+             "rope: patch_mask and rope_idx must be contiguous 1-D")
+    n, H, D = q_active.shape
+    _require(patch_mask.shape[0] == n and rope_idx.shape[0] == n, "rope: one mask/idx entry per row")
+    _require(q_active.stride(2) == 1 and k_active.stride(2) == 1, "rope: head dim must be contiguous")
+    if n == 0 or D == 0:
+        return
+    call("oudjat_rope_active_inplace", _ptr(q_active), q_active.stride(0), q_active.stride(1), _ptr(k_active),
+         k_active.stride(0), k_active.stride(1), _ptr(sin), _ptr(cos), sin.stride(0), _ptr(patch_mask.to(torch.bool)),
+         _ptr(rope_idx), n, H, D, _stream(q_active))
+
+
+def qkv_rope_kv_scatter(qkv: torch.Tensor, rope, patch_mask: torch.Tensor, rope_idx: torch.Tensor,
+                        batch_idx: torch.Tensor, token_idx: torch.Tensor, kv_cache: torch.Tensor,
+                        q_out: torch.Tensor) -> None:
+    """qkv [M, 3, H, Dh] -> RoPE on q/k of patch rows; k, v rows written into kv_cache [B, N, 2, H, Dh]
+    in place; q written to q_out [M, H, Dh]."""
+    sin, cos = rope
+    _require_cuda(qkv, patch_mask, rope_idx, batch_idx, token_idx, kv_cache, q_out, sin, cos)
+    M, three, H, Dh = qkv.shape
+    _require(three == 3 and qkv.is_contiguous() and qkv.dtype == torch.bfloat16, "qkv must be contiguous [M,3,H,Dh]")
+    _require(kv_cache.dim() == 5 and kv_cache.shape[2:] == (2, H, Dh) and trailing_is_packed(kv_cache, 2),
+             "kv_cache must be [B, N, 2, H, Dh] with packed rows")
+    _require(q_out.is_contiguous() and q_out.shape == (M, H, Dh), "q_out must be contiguous [M, H, Dh]")
+    _launch("qkv_post", qkv, "oudjat_qkv_rope_kv_scatter", _ptr(qkv), M, H, Dh, _ptr(sin), _ptr(cos), sin.stride(0), _ptr(patch_mask),
+         _ptr(rope_idx), _ptr(batch_idx), _ptr(token_idx), _ptr(kv_cache), kv_cache.stride(0), kv_cache.stride(1),
+         _ptr(q_out), _stream(qkv))
+
+
+# ------------------------------------------------------------------------------------------------
+# GEMM and attention
+# ------------------------------------------------------------------------------------------------
+
+
+def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
+           epilogue: int = _lib.EPI_BIAS, gamma: torch.Tensor | None = None, resid: torch.Tensor | None = None,
+           out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16 x[..., K] . weight[N, K]^T with a fused epilogue (see include/oudjat.h)."""
+    _require_cuda(x, weight, bias, gamma, resid, out)
+    _require(x.dtype == weight.dtype == torch.bfloat16, "linear: bf16 only")
+    K = x.shape[-1]
+    N = weight.shape[0]
+    _require(weight.shape[1] == K and weight.stride(1) == 1, "linear: weight must be [N, K] with contiguous rows")
+    x2 = x.reshape(-1, K)
+    _require(x2.stride(1) == 1, "linear: input rows must be contiguous")
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty((*x.shape[:-1], N), device=x.device, dtype=torch.bfloat16)
+    o2 = out.view(-1, N)
+    r2 = None
+    if resid is not None:
+        r2 = resid.reshape(-1, N)
+        _require(r2.stride(1) == 1 and r2.shape[0] == M, "linear: resid must be [M, N] with contiguous rows")
+    _launch(f"gemm{int(epilogue)}", x, "oudjat_linear_bf16", _ptr(x2), M, K, x2.stride(0), _ptr(weight), N, weight.stride(0),
+         _ptr(None if bias is None else bias.contiguous()), int(epilogue),
+         _ptr(None if gamma is None else gamma.contiguous()), _ptr(r2), 0 if r2 is None else r2.stride(0), _ptr(o2),
+         o2.stride(0), _stream(x))
+    return out
+
+
+def sparse_query_attention(q: torch.Tensor, kv_cache: torch.Tensor, T: int, scale: float,
+                           out: torch.Tensor | None = None) -> torch.Tensor:
+    """softmax(q . K^T * scale) . V per image over all cached keys.
+
+    q [B*T, H, Dh] packed (rows b*T + t), kv_cache [B, N, 2, H, Dh] (K post-RoPE), -> [B*T, H*Dh]."""
+    _require_cuda(q, kv_cache)
+    _require(q.dtype == kv_cache.dtype == torch.bfloat16, "attention: bf16 only")
+    B, N, two, H, Dh = kv_cache.shape
+    _require(two == 2 and kv_cache.stride(4) == 1 and kv_cache.stride(3) == Dh, "attention: kv heads must be packed")
+    _require(q.dim() == 3 and q.shape[1:] == (H, Dh) and q.shape[0] == B * T and q.stride(2) == 1
+             and q.stride(1) == Dh, "attention: q must be [B*T, H, Dh] with packed heads")
+    if out is None:
+        out = torch.empty((B * T, H * Dh), device=q.device, dtype=torch.bfloat16)
+    _launch("attention", q, "oudjat_sparse_query_attention", _ptr(q), q.stride(0), B, T, H, Dh, _ptr(kv_cache), kv_cache.stride(0),
+         kv_cache.stride(1), kv_cache.stride(2), kv_cache.stride(3), N, float(scale), _ptr(out), out.stride(0),
+         _stream(q))
+    return out
+
+
+# ------------------------------------------------------------------------------------------------
+# NVFP4 (nvfp4_fused.py:119-145; fp4_fast_linear.py:221-283)
+# ------------------------------------------------------------------------------------------------
+
+
+def nvfp4_scale_numel(M: int, K: int) -> int:
+    return -(-M // 128) * -(-K // 64) * 512
+
+
+def quantize_nvfp4_swizzled(x: torch.Tensor, tensor_scale: torch.Tensor):
+    """x [M, K] bf16 -> (qdata uint8 [M, K/2], swizzled e4m3 block scales float8_e4m3fn [tiles*512])."""
+    _require_cuda(x, tensor_scale)
+    _require(x.dim() == 2 and x.dtype == torch.bfloat16 and x.stride(1) == 1, "nvfp4: x must be [M, K] bf16 rows")
+    M, K = x.shape
+    _require(K % 16 == 0, f"nvfp4: K must be a multiple of the 16-element block, got {K}")
+    ts = tensor_scale.reshape(1).to(torch.float32)
+    qdata = torch.empty((M, K // 2), device=x.device, dtype=torch.uint8)
+    scale = torch.empty((nvfp4_scale_numel(M, K),), device=x.device, dtype=torch.uint8)
+    _launch("nvfp4_quantize", x, "oudjat_nvfp4_quantize", _ptr(x), M, K, x.stride(0), _ptr(ts), _ptr(qdata), _ptr(scale), _stream(x))
+    return qdata, scale.view(torch.float8_e4m3fn)
+
+
+def dequantize_nvfp4(qdata: torch.Tensor, scale: torch.Tensor, tensor_scale: torch.Tensor) -> torch.Tensor:
+    """Inverse of quantize_nvfp4_swizzled: bf16 [M, K]."""
+    _require_cuda(qdata, scale, tensor_scale)
+    M, K2 = qdata.shape
+    K = 2 * K2
+    _require(qdata.dtype == torch.uint8 and qdata.is_contiguous(), "nvfp4: qdata must be contiguous uint8")
+    s = scale.reshape(-1).view(torch.uint8)
+    _require(s.numel() == nvfp4_scale_numel(M, K), "nvfp4: scale buffer size mismatch")
+    ts = tensor_scale.reshape(1).to(torch.float32)
+    out = torch.empty((M, K), device=qdata.device, dtype=torch.bfloat16)
+    _launch("nvfp4_dequantize", qdata, "oudjat_nvfp4_dequantize", _ptr(qdata), _ptr(s), _ptr(ts), M, K, _ptr(out), out.stride(0), _stream(qdata))
+    return out
+
+
+# Reference spellings, for call sites written against the Triton wrappers.
+gather_rows_triton = gather_rows
+scatter_rows_triton = scatter_rows
+active_token_update_triton = active_token_update
+apply_rope_active_inplace_triton = apply_rope_active_inplace

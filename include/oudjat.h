@@ -1,0 +1,202 @@
+/*
+ * oudjat.h -- C ABI of the gfx950 token-correction library (liboudjat_hip.so).
+ *
+ * The library implements the server-side DINOv3 token-correction pass of AppCorr ("Oudjat"):
+ * top-k token selection, row gather/scatter, the in-place K/V row rewrite, sparse-query attention,
+ * the selected-row GEMMs with their fused epilogues, the residual reconstruct/scatter/persist step
+ * and NVFP4 quantize/dequantize.
+ *
+ * Conventions shared by every entry point:
+ *   - Pointers are device pointers. bf16 tensors are passed as uint16_t bit patterns.
+ *   - Strides and row strides are in ELEMENTS of the tensor's own type unless the name ends in
+ *     `_bytes`. Index tensors are int64 (torch.long), contiguous.
+ *   - `stream` is a hipStream_t (NULL = the legacy default stream). Every call only enqueues work
+ *     on that stream: no host synchronisation, no device-to-host reads, no allocation.
+ *   - The return value is an oudjat status. OUDJAT_OK is 0; anything else means nothing was
+ *     launched (argument/shape/layout errors) or the launch failed. oudjat_last_error() gives a
+ *     message for the calling thread's most recent failure.
+ *   - Scatter entry points assume the (batch, token) pairs of one call are unique.
+ *
+ * Reference interfaces named below are files of ckswjd99-lab/AppCorr, cited as path:line.
+ */
+#ifndef OUDJAT_H
+#define OUDJAT_H
+
+#include <stdint.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef void* oudjat_stream_t; /* hipStream_t */
+
+enum oudjat_status {
+  OUDJAT_OK = 0,
+  OUDJAT_ERR_INVALID_ARGUMENT = 1, /* null pointer, negative size, bad enum */
+  OUDJAT_ERR_UNSUPPORTED_SHAPE = 2, /* a dimension the kernels do not handle (e.g. K % 64 != 0) */
+  OUDJAT_ERR_UNSUPPORTED_LAYOUT = 3, /* strides or alignment the kernels do not handle */
+  OUDJAT_ERR_TOO_LARGE = 4,         /* exceeds a documented maximum (e.g. LDS capacity) */
+  OUDJAT_ERR_LAUNCH = 5,            /* the kernel launch itself failed */
+  OUDJAT_ERR_HIP = 6                /* another HIP runtime call failed */
+};
+
+/* GEMM epilogues for oudjat_linear_bf16. acc = A.W^T in fp32; every bf16() is one RNE rounding. */
+enum oudjat_epilogue {
+  OUDJAT_EPI_BIAS = 0,          /* C = bf16(acc + bias)                                  */
+  OUDJAT_EPI_BIAS_GELU = 1,     /* C = bf16(gelu_erf(bf16(acc + bias)))                  */
+  OUDJAT_EPI_BIAS_LS_RESID = 2, /* C = bf16(resid + bf16(acc + bias) * gamma)            */
+  OUDJAT_EPI_BIAS_LS = 3,       /* C = bf16(bf16(acc + bias) * gamma)                    */
+  OUDJAT_EPI_BIAS_SILU_MUL = 4  /* C = bf16(bf16(silu(bf16(acc + bias))) * resid)        */
+};
+
+/* Importance modes for oudjat_patch_importance. */
+enum oudjat_importance {
+  OUDJAT_IMPORTANCE_L2 = 0,     /* sqrt(sum d^2)   */
+  OUDJAT_IMPORTANCE_ENERGY = 1, /* sum d^2         */
+  OUDJAT_IMPORTANCE_RMS = 2     /* sqrt(mean d^2)  */
+};
+
+/* ABI version of this header (bumped on any signature change). */
+int oudjat_abi_version(void);
+const char* oudjat_status_string(int status);
+const char* oudjat_last_error(void);
+
+/* Runtime self-test: launches y = 2x on 8 floats and checks the result (the one entry point that
+ * synchronises). Replaces verify_triton_runtime
+ * (appcorr/models/dinov3/layers/triton_kernels/_strict.py:74-125). */
+int oudjat_selftest(oudjat_stream_t stream);
+
+/* Row 1 -- per-patch importance from a residual delta [rows, dim] fp32.
+ * Replaces _compute_patch_residual_rms (offload/server/model/dinov3_classifier.py:91-122) and the
+ * mobile residual energy (offload/policies/transmission/progressive.py:19-22). */
+int oudjat_patch_importance(const float* delta, int64_t rows, int64_t dim, int64_t row_stride,
+                            int mode, float* out, oudjat_stream_t stream);
+
+/* Rows 2+3 -- top-k selection and the sync-free packed query plan, one workgroup per image.
+ * Replaces torch.topk in _select_patch_keep_mask (appcorr/models/dinov3/layers/block.py:358-395)
+ * and _build_packed_query_state_fixed_k / _all_keep (block.py:397-490).
+ * scores [B, P] fp32 (row stride score_stride_b); k in [0, P]; dindice [B, num_pre + P] int64.
+ * Keeps the k largest scores per row; among equal scores the lower candidate index wins
+ * (-0.0 == +0.0; NaN ranks above +inf). Kept candidates are emitted in ascending candidate order.
+ * Outputs (T = num_pre + k, M = B * T):
+ *   update_indice [B, T], active_batch_idx [M], active_pos_idx [M], active_token_idx [M],
+ *   active_patch_mask [M] (1 byte: token >= num_pre), active_rope_idx [M] (max(token-num_pre, 0)),
+ *   keep_mask [B, P] (1 byte, may be NULL),
+ *   row_slot [B, num_tokens] int32 (packed row b*T+s of token t of image b, or -1; may be NULL).
+ * Limits: P <= 16384, (P + num_tokens) * 4 bytes <= 144 KiB. */
+int oudjat_topk_plan(const float* scores, int64_t B, int64_t P, int64_t score_stride_b, int64_t k,
+                     const int64_t* dindice, int64_t dindice_stride_b, int64_t num_pre,
+                     int64_t num_tokens, int64_t* update_indice, int64_t* active_batch_idx,
+                     int64_t* active_pos_idx, int64_t* active_token_idx,
+                     uint8_t* active_patch_mask, int64_t* active_rope_idx, uint8_t* keep_mask,
+                     int32_t* row_slot, oudjat_stream_t stream);
+
+/* Rows 4 and 11 -- dst[i, :] = src[batch_idx[i], token_idx[i], :] for row_bytes contiguous bytes.
+ * Replaces gather_rows_triton (appcorr/models/dinov3/layers/triton_kernels/token_update.py:455-473).
+ * Strides are in bytes. */
+int oudjat_gather_rows(const void* src, int64_t src_stride_b_bytes, int64_t src_stride_n_bytes,
+                       int64_t row_bytes, const int64_t* batch_idx, const int64_t* token_idx,
+                       int64_t n, void* dst, int64_t dst_row_stride_bytes, oudjat_stream_t stream);
+
+/* Rows 8 and 9 -- dst[batch_idx[i], token_idx[i], :] = src[i, :] (the in-place K/V rewrite and the
+ * query scatter). Replaces scatter_rows_triton (token_update.py:417-452); src_row_stride_bytes
+ * covers row views such as qkv_new[:, 1:] whose row stride is 3C while the row is 2C. */
+int oudjat_scatter_rows(void* dst, int64_t dst_stride_b_bytes, int64_t dst_stride_n_bytes,
+                        int64_t row_bytes, const int64_t* batch_idx, const int64_t* token_idx,
+                        int64_t n, const void* src, int64_t src_row_stride_bytes,
+                        oudjat_stream_t stream);
+
+/* Row 15 -- x_out[batch_idx[i], token_idx[i], :] = bf16(x_attn[i] + x_delta[i]) (bf16, C columns).
+ * Replaces active_token_update_triton (token_update.py:297-347). */
+int oudjat_active_token_update(uint16_t* x_out, int64_t stride_b, int64_t stride_n,
+                               const int64_t* batch_idx, const int64_t* token_idx, int64_t n,
+                               const uint16_t* x_attn, int64_t attn_row_stride,
+                               const uint16_t* x_delta, int64_t delta_row_stride, int64_t C,
+                               oudjat_stream_t stream);
+
+/* Rows 14+15+16 fused -- for every row r of [rows, C] (rows = B*N, contiguous):
+ *   slot = row_slot[r];
+ *   slot < 0 : x_out[r] = bf16(x[r] + blocks_out_sum[r])
+ *   slot >= 0: x_out[r] = bf16(x_attn[slot] + mlp[slot]);
+ *              blocks_out_sum[r] = bf16(bf16(x_attn[slot] - x_act[slot]) + mlp[slot])
+ * x_out may alias x (inplace_residual_add). Replaces block.py:1140-1179 (x + blocks_out_sum,
+ * active_token_update_triton, and the blocks_out_sum index_put_). */
+int oudjat_reconstruct_scatter_persist(const uint16_t* x, uint16_t* blocks_out_sum,
+                                       const int32_t* row_slot, const uint16_t* x_act,
+                                       const uint16_t* x_attn, const uint16_t* mlp, int64_t rows,
+                                       int64_t C, uint16_t* x_out, oudjat_stream_t stream);
+
+/* Row 12 -- out = bf16(x + attn * gamma[c]) over [rows, C] contiguous.
+ * Replaces fused_layerscale_add (token_update.py:10-60). */
+int oudjat_fused_layerscale_add(const uint16_t* x, const uint16_t* attn, const uint16_t* gamma,
+                                int64_t rows, int64_t C, uint16_t* out, oudjat_stream_t stream);
+
+/* Row 7 -- rotate-half RoPE on q and k rows [n, H, Dh] in place, fp32 math, rows with
+ * patch_mask == 0 untouched; table row rope_idx[i] of sin/cos [*, Dh] fp32.
+ * Replaces apply_rope_active_inplace_triton (appcorr/models/dinov3/layers/triton_kernels/rope.py:186-240). */
+int oudjat_rope_active_inplace(uint16_t* q, int64_t q_stride_t, int64_t q_stride_h, uint16_t* k,
+                               int64_t k_stride_t, int64_t k_stride_h, const float* sin_table,
+                               const float* cos_table, int64_t table_stride,
+                               const uint8_t* patch_mask, const int64_t* rope_idx, int64_t n,
+                               int64_t H, int64_t Dh, oudjat_stream_t stream);
+
+/* Rows 6-9 fused -- post-QKV step of SelfAttention.correct_partial_token
+ * (appcorr/models/dinov3/layers/attention.py:415-454): qkv [M, 3, H, Dh] bf16 contiguous;
+ * RoPE on q and k of patch rows; k, v rows written into kv[b, t, 0|1, H, Dh] (row stride
+ * kv_stride_n, batch stride kv_stride_b, elements); q written packed into q_out [M, H, Dh]. */
+int oudjat_qkv_rope_kv_scatter(const uint16_t* qkv, int64_t M, int64_t H, int64_t Dh,
+                               const float* sin_table, const float* cos_table,
+                               int64_t table_stride, const uint8_t* patch_mask,
+                               const int64_t* rope_idx, const int64_t* batch_idx,
+                               const int64_t* token_idx, uint16_t* kv, int64_t kv_stride_b,
+                               int64_t kv_stride_n, uint16_t* q_out, oudjat_stream_t stream);
+
+/* Row 5 -- LayerNorm over the last dim (fp32 statistics, biased variance, affine), bf16 in/out.
+ * Replaces nn.LayerNorm(eps=1e-5) at block.py:1114,1141. C % 8 == 0, C <= 8192. */
+int oudjat_layernorm_rows(const uint16_t* x, int64_t rows, int64_t C, int64_t x_row_stride,
+                          const uint16_t* weight, const uint16_t* bias, float eps, uint16_t* out,
+                          int64_t out_row_stride, oudjat_stream_t stream);
+
+/* Rows 6, 11, 12, 13 -- C[M, N] = epilogue(A[M, K] . W[N, K]^T) on bf16 MFMA with fp32 accumulate.
+ * Replaces the qkv / proj / fc1 / fc2 nn.Linear calls (attention.py:415,532; ffn_layers.py:43-49)
+ * and the LayerScale / residual ops folded into their epilogues (block.py:1129-1141); the SwiGLU
+ * gate silu(w1 x) * (w2 x) (ffn_layers.py:106-115) is the SILU_MUL epilogue with resid = w2 x.
+ * bias, gamma, resid may be NULL where the epilogue does not use them (bias NULL = 0).
+ * K % 64 == 0, N % 64 == 0, all leading dimensions % 8 == 0 and 16-byte aligned pointers. */
+int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                       int64_t N, int64_t ldw, const uint16_t* bias, int epilogue,
+                       const uint16_t* gamma, const uint16_t* resid, int64_t ldr, uint16_t* C,
+                       int64_t ldc, oudjat_stream_t stream);
+
+/* Row 10 -- sparse-query attention: for each image b, head h and query t < T,
+ *   out[b*T + t, h*Dh:(h+1)*Dh] = softmax(q . K^T * scale) . V over ALL N cached keys, no mask.
+ * q [B*T, H, Dh] packed (row stride q_row_stride); K = kv[b, n, 0, h, :], V = kv[b, n, 1, h, :]
+ * addressed as b*kv_stride_b + n*kv_stride_n + {0|1}*kv_stride_kv + h*kv_stride_h.
+ * Replaces F.scaled_dot_product_attention over the cache (attention.py:456-532). Dh == 64. */
+int oudjat_sparse_query_attention(const uint16_t* q, int64_t q_row_stride, int64_t B, int64_t T,
+                                  int64_t H, int64_t Dh, const uint16_t* kv, int64_t kv_stride_b,
+                                  int64_t kv_stride_n, int64_t kv_stride_kv, int64_t kv_stride_h,
+                                  int64_t N, float scale, uint16_t* out, int64_t out_row_stride,
+                                  oudjat_stream_t stream);
+
+/* Row 17 -- NVFP4 quantize: x [M, K] bf16 (row stride stride_m) with fp32 tensor scale at
+ * *tensor_scale (device) -> qdata [M, K/2] (two e2m1 codes per byte, even element in the low
+ * nibble) and e4m3 block scales in the swizzled layout of 32x16 bytes per 128x64 tile
+ * (ceil(M/128) * ceil(K/64) * 512 bytes; padding scales are 0).
+ * Replaces quantize_nvfp4_swizzled (appcorr/models/dinov3/layers/triton_kernels/nvfp4_fused.py:119-145). K % 16 == 0. */
+int oudjat_nvfp4_quantize(const uint16_t* x, int64_t M, int64_t K, int64_t stride_m,
+                          const float* tensor_scale, uint8_t* qdata, uint8_t* scales,
+                          oudjat_stream_t stream);
+
+/* Row 18 -- NVFP4 dequantize: out[m, k] = bf16(fp32(e2m1(q) * e4m3(s)) * tensor_scale).
+ * Inverse of oudjat_nvfp4_quantize; the dequant side of FastFP4Linear
+ * (offload/server/model/fp4_fast_linear.py:221-283). */
+int oudjat_nvfp4_dequantize(const uint8_t* qdata, const uint8_t* scales, const float* tensor_scale,
+                            int64_t M, int64_t K, uint16_t* out, int64_t out_stride,
+                            oudjat_stream_t stream);
+
+#ifdef __cplusplus
+}
+#endif
+
+#endif /* OUDJAT_H */

@@ -1,0 +1,175 @@
+"""GPU parity of whole correction blocks and passes against the fp64 oracle (oracle/model.py).
+
+Three levels:
+  1. one block, identical inputs: the GPU block is fed the oracle's own cache and x, so only this
+     block's arithmetic differs -> outputs within 2 bf16 ulps, K/V and blocks_out_sum rows likewise,
+     unselected rows bit-exact;
+  2. a full pass at the BASELINE ViT-S config (12 blocks, B=1, 224px, keep 50%) with the reference
+     init: within the north-star tolerance (2e-2 max abs, 1e-3 mean abs);
+  3. the same with stress weights (LayerScale 1, random biases / LayerNorm affine) so every term of
+     the block moves the output: a looser bound that still catches any wrong term.
+Plus size-independent properties at the full ViT-L shape (B=16, N=1029, k=256).
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from appcorr_amd.dinov3 import SelfAttentionBlock, dinov3_backbone
+from oracle import model as OM
+from oracle import plan as OP
+from tests.util import assert_bits_equal, assert_propagated_close, bf16_ulp, close_stats
+
+pytestmark = pytest.mark.gpu
+
+KW = dict(appcorr_method="partial_token", mobile_pscore="residual_energy", mobile_pscore_weight=1.0,
+          server_pscore="cls_attn_prob", server_pscore_weight=0.0, pscore_fusion="add", token_keep_thres=None)
+
+
+def _gpu_blocks(cfg, weights, dev):
+    ffn = "mlp" if cfg.ffn == "mlp" else "swiglu64"
+    blocks = []
+    for w in weights:
+        blk = SelfAttentionBlock(cfg.dim, cfg.heads, ffn_ratio=cfg.ffn_hidden / cfg.dim if cfg.ffn == "mlp" else 3.0,
+                                 qkv_bias=cfg.qkv_bias, init_values=cfg.layerscale_init, ffn_layer=ffn,
+                                 mask_k_bias=True)
+        blk.load_state_dict({k: v for k, v in w.items()}, strict=True)
+        blocks.append(blk.to(device=dev, dtype=torch.bfloat16))
+    return blocks
+
+
+def _setup(cfg, B, depth, dev, *, gamma=None, bias_std=0.0, ln_std=0.0, seed=0):
+    weights = OM.make_block_weights(cfg, seed, gamma=gamma, bias_std=bias_std, ln_std=ln_std, depth=depth)
+    x_base, x_full, delta, imp = OM.make_inputs(cfg, B, seed + 1)
+    rope = OM.rope_tables(cfg)
+    return weights, x_base, x_full, imp, rope
+
+
+def _gpu_cache(cache, dev):
+    return {k: v.to(dev).contiguous() for k, v in cache.items()}
+
+
+@pytest.mark.parametrize("name,B,ratio", [("vits16_224", 1, 0.5), ("vitb16_512", 2, 0.25), ("vitl16_512", 2, 0.25)])
+def test_single_block_identical_inputs(dev, name, B, ratio):
+    cfg = OM.CONFIGS[name]
+    weights, x_base, x_full, imp, rope = _setup(cfg, B, 1, dev, gamma=1.0, bias_std=0.05, ln_std=0.1)
+    _, cache = OM.approx_pass(cfg, weights, x_base, rope)
+    k = OP.keep_count(cfg.num_patches, ratio)
+    dind = OM.full_dindice(cfg, B)
+    plan = OP.build_plan(imp.numpy(), k, dind.numpy(), cfg.num_pretokens, cfg.num_tokens)
+    gcache = _gpu_cache(cache, dev)
+    x_ref, cache_ref = OM.correct_block(cfg, weights[0], x_full, plan, rope, {k_: v.clone() for k_, v in cache.items()},
+                                        "layer0")
+    blk = _gpu_blocks(cfg, weights, dev)[0]
+    with torch.no_grad():
+        x_got, gcache = blk.correct(x_full.to(dev), dind.to(dev), (rope[0].to(dev), rope[1].to(dev)), gcache,
+                                    "layer0", token_keep_ratio=ratio, mobile_pscore_hint=imp.to(dev), **KW)
+    sel = np.zeros((B, cfg.num_tokens), dtype=bool)
+    sel[plan.active_batch_idx, plan.active_token_idx] = True
+    assert_bits_equal(x_got.cpu()[~torch.from_numpy(sel)], x_ref[~torch.from_numpy(sel)], "unselected rows")
+    assert_propagated_close(x_got, x_ref, what="x_out")
+    assert_propagated_close(gcache["layer0_kv"], cache_ref["layer0_kv"], max_ulps=2, mean_rel=2.0 ** -12,
+                            what="kv cache")
+    # blocks_out_sum = (x_attn - x_act) + mlp: a one-ulp flip of x_attn (|x_attn| ~ |x_out|) shows up at
+    # the ulp of x_attn's magnitude, not of the (smaller) increment.
+    bos_ref = cache_ref["layer0_blocks_out_sum"]
+    summand = (x_ref.float().abs() + bos_ref.float().abs()).numpy()
+    assert_propagated_close(gcache["layer0_blocks_out_sum"], bos_ref, floor_abs=2 * bf16_ulp(summand),
+                            what="blocks_out_sum")
+    assert_bits_equal(gcache["_partial_token_query_plan_cache"][next(iter(gcache["_partial_token_query_plan_cache"]))]
+                      .update_indice, plan.update_indice, "update_indice")
+
+
+def _run_pass(cfg, weights, x_base, x_full, imp, rope, ratio, dev, B):
+    _, cache = OM.approx_pass(cfg, weights, x_base, rope)
+    k = OP.keep_count(cfg.num_patches, ratio)
+    dind = OM.full_dindice(cfg, B)
+    plan = OP.build_plan(imp.numpy(), k, dind.numpy(), cfg.num_pretokens, cfg.num_tokens)
+    x_ref, cache_ref = OM.correct_pass(cfg, weights, x_full, plan, rope, {k_: v.clone() for k_, v in cache.items()})
+    blocks = _gpu_blocks(cfg, weights, dev)
+    gcache = _gpu_cache(cache, dev)
+    r = (rope[0].to(dev), rope[1].to(dev))
+    x = x_full.to(dev)
+    dd, hint = dind.to(dev), imp.to(dev)
+    with torch.no_grad():
+        for i, blk in enumerate(blocks):
+            x, gcache = blk.correct(x, dd, r, gcache, f"layer{i}", token_keep_ratio=ratio, mobile_pscore_hint=hint, **KW)
+    return x, x_ref, gcache, cache_ref
+
+
+def test_vits_pass_reference_init_north_star_tolerance(dev):
+    cfg = OM.CONFIGS["vits16_224"]
+    weights, x_base, x_full, imp, rope = _setup(cfg, 1, None, dev)
+    x, x_ref, _, _ = _run_pass(cfg, weights, x_base, x_full, imp, rope, 0.5, dev, 1)
+    mx, mean = close_stats(x, x_ref)
+    assert mx <= 2e-2 and mean <= 1e-3, (mx, mean)
+
+
+def test_vits_pass_stress_weights(dev):
+    cfg = OM.CONFIGS["vits16_224"]
+    weights, x_base, x_full, imp, rope = _setup(cfg, 1, None, dev, gamma=1.0, bias_std=0.05, ln_std=0.1)
+    x, x_ref, gc, cr = _run_pass(cfg, weights, x_base, x_full, imp, rope, 0.5, dev, 1)
+    mx, mean = close_stats(x, x_ref)
+    scale = float(x_ref.float().abs().mean())
+    # 12 blocks of fp32-vs-fp64 accumulation differences compound through the residual stream
+    assert mean <= 5e-3 * scale and mx <= 0.1 * float(x_ref.float().abs().max()), (mx, mean, scale)
+
+
+def test_vitl_two_blocks_stress(dev):
+    cfg = OM.CONFIGS["vitl16_512"]
+    weights, x_base, x_full, imp, rope = _setup(cfg, 2, 2, dev, gamma=1.0, bias_std=0.05, ln_std=0.1)
+    x, x_ref, gc, cr = _run_pass(cfg, weights, x_base, x_full, imp, rope, 0.25, dev, 2)
+    mx, mean = close_stats(x, x_ref)
+    scale = float(x_ref.float().abs().mean())
+    assert mean <= 2e-3 * scale, (mx, mean, scale)
+    for i in range(2):
+        mk, mnk = close_stats(gc[f"layer{i}_kv"], cr[f"layer{i}_kv"])
+        assert mnk <= 2e-3, (i, mk, mnk)
+
+
+def test_vitl_full_shape_properties(dev):
+    """B=16, N=1029, ViT-L width, k=256, 2 blocks: size-independent identities of the path."""
+    cfg = OM.CONFIGS["vitl16_512"]
+    B = 16
+    model = dinov3_backbone("vitl16", depth=2, device=dev, layerscale_init=1.0)
+    g = torch.Generator().manual_seed(3)
+    x0 = torch.randn(B, cfg.num_tokens, cfg.dim, generator=g).to(torch.bfloat16).to(dev)
+    imp = torch.rand(B, cfg.num_patches, generator=g).to(dev)
+    rope = model.rope_embed(H=cfg.grid, W=cfg.grid)
+    dind = OM.full_dindice(cfg, B).to(dev)
+    with torch.no_grad():
+        cache = {}
+        xa = x0
+        for i, blk in enumerate(model.blocks):
+            xa, cache = blk.approx(xa, rope, cache, f"layer{i}", server_pscore_weight=0.0)
+        kv0 = {k: v.clone() for k, v in cache.items() if k.endswith("_kv")}
+        bos0 = {k: v.clone() for k, v in cache.items() if k.endswith("_blocks_out_sum")}
+        # k = 0: only the 5 pretokens (always in the query set, block.py:975-980) are recomputed;
+        # every patch row is x + blocks_out_sum exactly and its K/V row is untouched
+        c0 = {k: v.clone() for k, v in cache.items()}
+        x_k0, c0 = model.blocks[0].correct(x0, dind, rope, c0, "layer0", token_keep_ratio=0.0,
+                                           mobile_pscore_hint=imp, **KW)
+        ref = (x0.float() + cache["layer0_blocks_out_sum"].float()).to(torch.bfloat16)
+        assert_bits_equal(x_k0[:, 5:], ref[:, 5:], "k=0 -> x + blocks_out_sum on patch rows")
+        assert_bits_equal(c0["layer0_kv"][:, 5:], kv0["layer0_kv"][:, 5:], "k=0 leaves patch K/V")
+        # k = 256: unselected rows are x + bos bit-exact; unselected K/V and bos rows untouched
+        c1 = {k: v.clone() for k, v in cache.items()}
+        x_k, c1 = model.blocks[0].correct(x0, dind, rope, c1, "layer0", token_keep_ratio=0.25,
+                                          mobile_pscore_hint=imp, **KW)
+        plan = next(iter(c1["_partial_token_query_plan_cache"].values()))
+        sel = torch.zeros(B, cfg.num_tokens, dtype=torch.bool, device=dev)
+        sel[plan.fixed_query_state.active_batch_idx, plan.fixed_query_state.active_token_idx] = True
+        assert int(sel.sum()) == B * (5 + 256)
+        assert_bits_equal(x_k[~sel], ref[~sel], "unselected rows")
+        assert_bits_equal(c1["layer0_kv"][~sel], kv0["layer0_kv"][~sel], "unselected K/V rows")
+        assert_bits_equal(c1["layer0_blocks_out_sum"][~sel], bos0["layer0_blocks_out_sum"][~sel], "unselected bos")
+        # 100% keep with the approx input reproduces the approx block (same kernels, same plan order)
+        c2 = {k: v.clone() for k, v in cache.items()}
+        x_all, c2 = model.blocks[0].correct(x0, dind, rope, c2, "layer0", token_keep_ratio=1.0,
+                                            mobile_pscore_hint=imp, **KW)
+        c3 = {}
+        x_apx, c3 = model.blocks[0].approx(x0, rope, c3, "layer0", server_pscore_weight=0.0)
+        mx, mean = close_stats(x_all, x_apx)
+        # approx rounds x + bf16(g * proj) twice, the correction once (fused epilogue): ~1 ulp apart
+        assert mean < 5e-3 and mx < 0.1, (mx, mean)
+        assert_bits_equal(c2["layer0_kv"], c3["layer0_kv"], "100% keep K/V == approx K/V")

@@ -1,0 +1,207 @@
+"""GPU numerics of the MFMA GEMM (every epilogue), LayerNorm, RoPE, the fused post-QKV step and the
+sparse-query attention, against float64 references of the same ops rounded to bf16 at the
+reference's points (oracle/model.py primitives).
+
+Tolerance: results may differ from the fp64 oracle only through fp32 accumulation order, so every
+element must be within 1 bf16 ulp of the oracle and only a small fraction may differ at all
+(attention additionally rounds P to bf16 before P.V, as flash attention does: 2 ulps)."""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+
+from appcorr_amd import _lib
+from appcorr_amd import kernels as K
+from oracle import model as OM
+from tests.util import assert_bf16_close, assert_bits_equal, bf16_ulp
+
+pytestmark = pytest.mark.gpu
+
+F64 = OM._F64
+
+
+def _ref_linear(dev, x, w, b):
+    """fp64 oracle linear evaluated on the device (fp64 GEMM), rounded to bf16 via fp32 on the host."""
+    return F64.linear(x.to(dev), w.to(dev), None if b is None else b.to(dev)).cpu()
+
+
+def _rand(shape, seed, std=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * std).to(torch.bfloat16)
+
+
+U32 = 2.0 ** -24
+
+
+def _check_gemm(dev, got, x, w, b, what):
+    """|got - oracle| <= ulp(oracle) + 2 sqrt(K) u (|x| . |w|^T): the final bf16 rounding plus an fp32
+    accumulation-order bound (u = 2^-24); at most 2% of elements may differ at all."""
+    ref = _ref_linear(dev, x, w, b).double()
+    mag = (x.to(dev).float().abs() @ w.to(dev).float().abs().T).double().cpu()
+    bound = torch.from_numpy(bf16_ulp(ref.numpy())) + 2.0 * math.sqrt(x.shape[-1]) * U32 * mag
+    diff = (got.detach().cpu().double() - ref).abs()
+    bad = diff > bound
+    assert not bad.any(), f"{what}: {int(bad.sum())} elements beyond bound, worst excess {float((diff - bound).max())}"
+    frac = float((diff > 0).double().mean())
+    assert frac <= 0.02, f"{what}: {frac:.3%} differ"
+
+
+@pytest.mark.parametrize("M,N,Kd", [(4176, 3072, 1024), (4176, 1024, 1024), (4176, 4096, 1024), (4176, 1024, 4096),
+                                    (103, 1152, 384), (1, 64, 64), (130, 192, 128), (1656, 8192, 4096)])
+def test_linear_bias(dev, M, N, Kd):
+    x, w, b = _rand((M, Kd), 1), _rand((N, Kd), 2, 0.02), _rand((N,), 3, 0.1)
+    got = K.linear(x.to(dev), w.to(dev), b.to(dev))
+    _check_gemm(dev, got, x, w, b, f"linear {M}x{N}x{Kd}")
+
+
+def test_linear_no_bias_and_strided_input(dev):
+    x, w = _rand((300, 256), 4), _rand((128, 192), 5, 0.02)
+    got = K.linear(x.to(dev)[:, 32:224], w.to(dev), None)
+    _check_gemm(dev, got, x[:, 32:224].contiguous(), w, None, "strided")
+
+
+# Epilogues: the plain GEMM (EPI_BIAS) is checked against the fp64 oracle above; each fused epilogue
+# must then equal the oracle's epilogue applied to that same bf16(acc + bias), because it reads the
+# identical fp32 accumulators. LayerScale and residual forms are exact in fp32 -> bit-exact; GELU and
+# SiLU use fp32 transcendentals -> at most 1 ulp on at most 0.1% of elements.
+
+
+def _epi_case(dev, M, N, Kd, seed):
+    x, w, b = _rand((M, Kd), seed), _rand((N, Kd), seed + 1, 0.02), _rand((N,), seed + 2, 0.1)
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    base = K.linear(xd, wd, bd)
+    _check_gemm(dev, base, x, w, b, "epilogue base")
+    return xd, wd, bd, base.cpu()
+
+
+def test_linear_gelu(dev):
+    xd, wd, bd, base = _epi_case(dev, 4176, 4096, 1024, 6)
+    got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_GELU)
+    assert_bf16_close(got, F64.gelu(base), max_ulps=1, max_frac_off=1e-3, what="fc1+gelu")
+
+
+def test_linear_layerscale_residual(dev):
+    xd, wd, bd, base = _epi_case(dev, 4176, 1024, 1024, 9)
+    g, r = _rand((1024,), 12), _rand((4176, 1024), 13)
+    got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_LS_RESID, gamma=g.to(dev), resid=r.to(dev))
+    assert_bits_equal(got, F64.fma_add(r, base, g), "proj+ls+resid")
+
+
+def test_linear_layerscale(dev):
+    xd, wd, bd, base = _epi_case(dev, 4176, 1024, 4096, 14)
+    g = _rand((1024,), 17)
+    got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_LS, gamma=g.to(dev))
+    assert_bits_equal(got, F64.mul(base, g), "fc2+ls")
+
+
+def test_linear_silu_mul(dev):
+    xd, wd, bd, base = _epi_case(dev, 600, 1024, 512, 18)
+    x2 = _rand((600, 1024), 21)
+    got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_SILU_MUL, resid=x2.to(dev))
+    assert_bf16_close(got, F64.silu_mul(base, x2), max_ulps=1, max_frac_off=1e-3, what="swiglu")
+
+
+@pytest.mark.parametrize("rows,C", [(4176, 1024), (103, 384), (1656, 4096), (7, 8192)])
+def test_layer_norm(dev, rows, C):
+    """|got - oracle| <= ulp(oracle) + 64 u rstd |w| max|x_row| (fp32 statistics vs fp64)."""
+    x = (_rand((rows, C), 22).float() * 3 + 1).to(torch.bfloat16)
+    w, b = _rand((C,), 23), _rand((C,), 24)
+    got = K.layer_norm(x.to(dev), w.to(dev), b.to(dev), 1e-5).cpu().double()
+    ref = F64.ln(x, w, b, 1e-5).double()
+    xf = x.double()
+    rstd = 1.0 / torch.sqrt(xf.var(-1, unbiased=False, keepdim=True) + 1e-5)
+    bound = torch.from_numpy(bf16_ulp(ref.numpy())) + 64 * U32 * rstd * w.double().abs() * xf.abs().amax(-1, True)
+    diff = (got - ref).abs()
+    assert (diff <= bound).all(), float((diff - bound).max())
+    assert float((diff > 0).double().mean()) <= 0.01
+
+
+def _rope_inputs(M, H, D, seed):
+    cfg = OM.with_overrides(OM.CONFIGS["vitl16_512"], dim=H * D, heads=H)
+    sin, cos = OM.rope_tables(cfg)
+    rng = np.random.default_rng(seed)
+    tok = torch.from_numpy(rng.integers(0, cfg.num_tokens, M).astype(np.int64))
+    pm = tok >= 5
+    ri = (tok - 5).clamp_min(0)
+    return cfg, sin, cos, tok, pm, ri
+
+
+def test_rope_active_inplace_bit_exact(dev):
+    M, H, D = 4176, 16, 64
+    cfg, sin, cos, tok, pm, ri = _rope_inputs(M, H, D, 0)
+    qkv = _rand((M, 3, H, D), 25)
+    qd = qkv.to(dev)
+    K.apply_rope_active_inplace(qd[:, 0], qd[:, 1], (sin.to(dev), cos.to(dev)), pm.to(dev), ri.to(dev))
+    s_sel, c_sel = sin[ri][:, None], cos[ri][:, None]
+    ref = qkv.clone()
+    ref[:, 0] = torch.where(pm[:, None, None], OM.rope_rotate(qkv[:, 0], s_sel, c_sel), qkv[:, 0])
+    ref[:, 1] = torch.where(pm[:, None, None], OM.rope_rotate(qkv[:, 1], s_sel, c_sel), qkv[:, 1])
+    assert_bits_equal(qd, ref, "rope in place (q, k rotated; v untouched)")
+
+
+@pytest.mark.parametrize("B,T,H,D", [(16, 261, 16, 64), (2, 50, 32, 128)])
+def test_qkv_rope_kv_scatter_bit_exact(dev, B, T, H, D):
+    N = 1029
+    M = B * T
+    cfg, sin, cos, _, _, _ = _rope_inputs(1, H, D, 0)
+    rng = np.random.default_rng(B)
+    toks = np.stack([np.concatenate([np.arange(5), np.sort(rng.choice(np.arange(5, N), T - 5, replace=False))])
+                     for _ in range(B)])
+    tok = torch.from_numpy(toks.reshape(-1).astype(np.int64))
+    bi = torch.arange(B).repeat_interleave(T)
+    pm, ri = tok >= 5, (tok - 5).clamp_min(0)
+    qkv = _rand((M, 3, H, D), 26)
+    kv = _rand((B, N, 2, H, D), 27)
+    kvd, qo = kv.to(dev), torch.empty((M, H, D), dtype=torch.bfloat16, device=dev)
+    K.qkv_rope_kv_scatter(qkv.to(dev), (sin.to(dev), cos.to(dev)), pm.to(dev), ri.to(dev), bi.to(dev), tok.to(dev),
+                          kvd, qo)
+    s_sel, c_sel = sin[ri][:, None], cos[ri][:, None]
+    q_ref = torch.where(pm[:, None, None], OM.rope_rotate(qkv[:, 0], s_sel, c_sel), qkv[:, 0])
+    k_ref = torch.where(pm[:, None, None], OM.rope_rotate(qkv[:, 1], s_sel, c_sel), qkv[:, 1])
+    kv_ref = kv.clone()
+    kv_ref[bi, tok, 0] = k_ref
+    kv_ref[bi, tok, 1] = qkv[:, 2]
+    assert_bits_equal(qo, q_ref, "q packed")
+    assert_bits_equal(kvd, kv_ref, "kv cache")
+
+
+def _check_attention(got, qb, kv, scale, ref, what):
+    """P is rounded to bf16 before P.V (relative error <= 2^-9 per weight), so
+    |got - oracle| <= 2 ulp(oracle) + 2^-8 * sum_j p_j |v_j|   (the second term from the oracle with |V|);
+    and on average the error stays below 2^-10 of that magnitude (half of a bf16 P rounding)."""
+    B, H, T, D = qb.shape
+    mag = F64.sdpa(qb, kv[:, :, 0].transpose(1, 2), kv[:, :, 1].abs().transpose(1, 2), scale)
+    mag = mag.transpose(1, 2).reshape(B * T, H * D).double()
+    r = ref.double()
+    bound = 2 * torch.from_numpy(bf16_ulp(r.numpy())) + 2.0 ** -8 * mag
+    diff = (got.detach().cpu().double() - r).abs()
+    assert (diff <= bound).all(), f"{what}: worst excess {float((diff - bound).max())}"
+    rel = float(diff.mean() / mag.mean())
+    assert rel <= 2.0 ** -10, f"{what}: mean error {rel:.3g} of mean sum p|v|"
+
+
+@pytest.mark.parametrize("B,T,N,H,D", [(16, 261, 1029, 16, 64), (1, 103, 201, 6, 64), (2, 1029, 1029, 16, 64),
+                                       (2, 7, 70, 4, 64), (1, 100, 4101, 32, 128), (3, 64, 64, 2, 64)])
+def test_sparse_query_attention(dev, B, T, N, H, D):
+    q = _rand((B * T, H, D), 28)
+    kv = _rand((B, N, 2, H, D), 29)
+    scale = D ** -0.5
+    got = K.sparse_query_attention(q.to(dev), kv.to(dev), T, scale)
+    qb = q.reshape(B, T, H, D).transpose(1, 2)
+    ref = F64.sdpa(qb, kv[:, :, 0].transpose(1, 2), kv[:, :, 1].transpose(1, 2), scale)
+    ref = ref.transpose(1, 2).reshape(B * T, H * D)
+    _check_attention(got, qb, kv, scale, ref, f"attention {B},{T},{N},{H},{D}")
+
+
+def test_sparse_query_attention_peaked_softmax(dev):
+    # Large logits: the online max rescaling must keep exp() in range.
+    B, T, N, H, D = 2, 40, 300, 2, 64
+    q = (_rand((B * T, H, D), 30).float() * 8).to(torch.bfloat16)
+    kv = (_rand((B, N, 2, H, D), 31).float() * 8).to(torch.bfloat16)
+    got = K.sparse_query_attention(q.to(dev), kv.to(dev), T, D ** -0.5)
+    qb = q.reshape(B, T, H, D).transpose(1, 2)
+    ref = F64.sdpa(qb, kv[:, :, 0].transpose(1, 2), kv[:, :, 1].transpose(1, 2), D ** -0.5)
+    ref = ref.transpose(1, 2).reshape(B * T, H * D)
+    _check_attention(got, qb, kv, D ** -0.5, ref, "peaked attention")

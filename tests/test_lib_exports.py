@@ -1,0 +1,100 @@
+"""CPU checks of the C ABI: the library loads, exports every symbol include/oudjat.h declares, and
+rejects bad arguments with the documented status before any launch (so these run without a GPU)."""
+
+import ctypes
+import re
+from pathlib import Path
+
+import pytest
+
+from appcorr_amd import _lib
+
+HEADER = Path(__file__).resolve().parents[1] / "include" / "oudjat.h"
+
+
+def declared_functions():
+    text = HEADER.read_text()
+    text = re.sub(r"/\*.*?\*/", "", text, flags=re.S)
+    return sorted(set(re.findall(r"\b(oudjat_[a-z0-9_]+)\s*\(", text)))
+
+
+def test_library_loads_and_abi_version():
+    lib = _lib.load()
+    assert lib.oudjat_abi_version() == _lib.ABI_VERSION
+
+
+def test_every_declared_symbol_is_exported_and_bound():
+    lib = _lib.load()
+    decl = declared_functions()
+    assert len(decl) >= 18
+    for name in decl:
+        assert hasattr(lib, name), f"{name} declared in oudjat.h but not exported"
+        assert name in _lib.SIGNATURES, f"{name} has no ctypes signature in appcorr_amd._lib"
+    assert set(_lib.SIGNATURES) == set(decl)
+
+
+def test_status_strings():
+    lib = _lib.load()
+    for code in range(7):
+        assert lib.oudjat_status_string(code)
+    assert lib.oudjat_status_string(0) == b"ok"
+
+
+NULL = ctypes.c_void_p(0)
+
+
+def _expect(status_name, fn, *args):
+    with pytest.raises(_lib.OudjatKernelError) as ei:
+        _lib.call(fn, *args)
+    assert ei.value.status_name == status_name, str(ei.value)
+
+
+def test_linear_rejects_bad_shapes_before_launch():
+    # K not a multiple of 64
+    _expect("OUDJAT_ERR_UNSUPPORTED_SHAPE", "oudjat_linear_bf16", ctypes.c_void_p(16), 4, 100, 100,
+            ctypes.c_void_p(16), 64, 100, NULL, 0, NULL, NULL, 0, ctypes.c_void_p(16), 64, NULL)
+    # bad epilogue id
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_linear_bf16", NULL, 4, 64, 64, NULL, 64, 64, NULL, 9, NULL, NULL, 0,
+            NULL, 64, NULL)
+    # LayerScale epilogue without gamma
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_linear_bf16", ctypes.c_void_p(16), 4, 64, 64, ctypes.c_void_p(16),
+            64, 64, NULL, 3, NULL, NULL, 0, ctypes.c_void_p(16), 64, NULL)
+    # misaligned A
+    _expect("OUDJAT_ERR_UNSUPPORTED_LAYOUT", "oudjat_linear_bf16", ctypes.c_void_p(18), 4, 64, 64,
+            ctypes.c_void_p(16), 64, 64, NULL, 0, NULL, NULL, 0, ctypes.c_void_p(16), 64, NULL)
+
+
+def test_topk_plan_rejects_bad_k_and_too_large():
+    args = [NULL] * 10
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_topk_plan", NULL, 2, 10, 10, 11, NULL, 15, 5, 15, *args[:9])
+    _expect("OUDJAT_ERR_TOO_LARGE", "oudjat_topk_plan", ctypes.c_void_p(16), 1, 20000, 20000, 5,
+            ctypes.c_void_p(16), 20005, 5, 0, *([ctypes.c_void_p(16)] * 6), NULL, NULL, NULL)
+
+
+def test_nvfp4_rejects_k_not_multiple_of_16():
+    _expect("OUDJAT_ERR_UNSUPPORTED_SHAPE", "oudjat_nvfp4_quantize", NULL, 4, 24, 24, NULL, NULL, NULL, NULL)
+    _expect("OUDJAT_ERR_UNSUPPORTED_SHAPE", "oudjat_nvfp4_dequantize", NULL, NULL, NULL, 4, 24, NULL, 24, NULL)
+
+
+def test_attention_rejects_unsupported_head_dim():
+    _expect("OUDJAT_ERR_UNSUPPORTED_SHAPE", "oudjat_sparse_query_attention", ctypes.c_void_p(16), 96, 1, 4, 1, 96,
+            ctypes.c_void_p(16), 0, 0, 0, 0, 8, 0.1, ctypes.c_void_p(16), 96, NULL)
+
+
+def test_zero_sized_calls_are_noops():
+    # Nothing to do -> OK without touching any pointer (and without a GPU).
+    _lib.call("oudjat_gather_rows", NULL, 0, 0, 2048, NULL, NULL, 0, NULL, 2048, NULL)
+    _lib.call("oudjat_scatter_rows", NULL, 0, 0, 2048, NULL, NULL, 0, NULL, 2048, NULL)
+    _lib.call("oudjat_layernorm_rows", NULL, 0, 1024, 1024, NULL, NULL, 1e-5, NULL, 1024, NULL)
+    _lib.call("oudjat_nvfp4_quantize", NULL, 0, 1024, 1024, NULL, NULL, NULL, NULL)
+
+
+def test_wrappers_refuse_cpu_tensors():
+    import torch
+
+    from appcorr_amd import kernels as K
+
+    x = torch.zeros(2, 8, 64, dtype=torch.bfloat16)
+    idx = torch.zeros(3, dtype=torch.long)
+    with pytest.raises(ValueError, match="GPU only"):
+        K.gather_rows(x, idx, idx)
