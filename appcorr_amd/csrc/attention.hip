@@ -3,148 +3,223 @@
 // Queries: the T selected rows of each image (packed [B*T, H, Dh]); keys/values: all N cached rows of
 // the same image, read in place from the [B, N, 2, H, Dh] cache (K after RoPE, V raw), no mask.
 //
-// Workgroup = (64-query tile, head, image); 4 waves, each owning 16 query rows. Keys stream through
-// LDS in tiles of 64: K row-major (its rows are the B operand of Q.K^T as-is) and V transposed in LDS
-// (so 8 consecutive keys of one head dim are a 16-byte read, the B operand layout of P.V). Both
-// products run on v_mfma_f32_16x16x32_bf16 with fp32 accumulators; softmax is the online (running
-// max / running sum) form in fp32 with exp2, so the N keys are visited once.
+// Formulation: each wave owns 32 queries and computes the transposed products
+//     S^T = K . Q^T          (32 keys x 32 queries per v_mfma_f32_32x32x16_bf16 block)
+//     O^T += V^T . P^T       (32 head dims x 32 queries)
+// so that, in the 32x32 accumulator layout, one query is one lane pair (lanes l and l^32) and all of
+// its scores sit in that pair's registers:
+//   * the online-softmax max / sum of a query is a register reduction plus one xor-32 exchange;
+//   * P^T feeds the second MFMA straight from registers (no LDS round trip). The contraction order
+//     of that MFMA is taken from the accumulator layout: lane group g supplies keys
+//     16j + 4g + {0..3} and 16j + 8 + 4g + {0..3} of k-step j, and V^T is read in that same order;
+//   * K (the A operand of the first product) is read from LDS in its natural row layout.
+// V is transposed once per tile while it is written to LDS (Vt[d][key], rows padded by 8 bytes so
+// the 8-byte fragment reads of 32 consecutive d rows are conflict-free).
+//
+// One workgroup per (image, head) covers up to 10 waves = 320 queries (8 waves for Dh = 128) (T = 261 at the headline
+// shape: 9 waves, 256 workgroups for B*H = 256, one per CU); larger T is split evenly over several
+// workgroups. K/V tiles of 64 keys are double-buffered in LDS with the next tile's global loads in
+// flight during the current tile's MFMAs, so each (image, head) streams its K/V once.
 #include "common.hpp"
 
 namespace oudjat {
 
-static constexpr int kAttnThreads = 256;
 static constexpr int kKeyTile = 64;
-static constexpr int kQTile = 64;
+static constexpr int kMaxWaves64 = 10;   // Dh = 64: 3 waves per SIMD, <= 170 VGPRs
+static constexpr int kMaxWaves128 = 8;   // Dh = 128: 2 waves per SIMD, <= 256 VGPRs
+static constexpr int kMinWaves = 4;
 
-__device__ __forceinline__ float max16(float v) {
+__device__ __forceinline__ bf16x8_t pack_bf16x8(const float* f) {
+  bf16x8_t r;
 #pragma unroll
-  for (int o = 1; o < 16; o <<= 1) v = fmaxf(v, __shfl_xor(v, o, 64));
-  return v;
-}
-__device__ __forceinline__ float sum16(float v) {
-#pragma unroll
-  for (int o = 1; o < 16; o <<= 1) v += __shfl_xor(v, o, 64);
-  return v;
+  for (int e = 0; e < 8; ++e) r[e] = (__bf16)f[e];
+  return r;
 }
 
 template <int DH>
-__global__ __launch_bounds__(kAttnThreads) void sq_attention_kernel(
+__global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void sq_attention_kernel(
     const uint16_t* __restrict__ q, int64_t qrs, int T, const uint16_t* __restrict__ kv, int64_t kvb, int64_t kvn,
-    int64_t kvkv, int64_t kvh, int N, float scale_log2, uint16_t* __restrict__ out, int64_t ors) {
-  constexpr int KROW = DH + 8;
-  constexpr int VROW = kKeyTile + 8;
-  constexpr int PROW = kKeyTile + 8;
-  constexpr int QK_STEPS = DH / 32;   // K=32 steps over the head dim
-  constexpr int OB = DH / 16;         // 16-wide output blocks over the head dim
-  constexpr int CPK = DH / 8;         // 16-byte chunks per key row
-  __shared__ uint16_t Ks[kKeyTile * KROW];
-  __shared__ uint16_t Vt[DH * VROW];
-  __shared__ uint16_t Ps[4][16 * PROW];
+    int64_t kvkv, int64_t kvh, int N, float scale_log2, uint16_t* __restrict__ out, int64_t ors,
+    int waves_per_wg) {
+  constexpr int CPR = DH / 8;                 // 16-byte chunks per K row
+  constexpr int KROWB = DH * 2;               // bytes per K row in LDS
+  constexpr int VTROW = kKeyTile * 2 + 8;     // bytes per Vt row (64 keys + 8 bytes of padding)
+  constexpr int KSTAGE = kKeyTile * KROWB;
+  constexpr int VSTAGE = DH * VTROW;
+  constexpr int STAGE = KSTAGE + VSTAGE;
+  constexpr int QK_STEPS = DH / 16;
+  constexpr int OB = DH / 32;
+  constexpr int ITEMS = kKeyTile * CPR;       // 16-byte chunks per K (or V) tile
+  constexpr int IT = (ITEMS + kMinWaves * 64 - 1) / (kMinWaves * 64);
+
+  extern __shared__ __align__(16) unsigned char smem[];
 
   const int b = blockIdx.z, h = blockIdx.y;
-  const int tid = threadIdx.x, lane = tid & 63, wave = tid >> 6;
-  const int q0 = blockIdx.x * kQTile + wave * 16;
-  const int l16 = lane & 15, g16 = lane >> 4;
+  const int nthreads = blockDim.x;
+  const int tid = threadIdx.x;
+  const int lane = tid & 63, wave = tid >> 6;
+  const int l32 = lane & 31, g = lane >> 5;
+  const int q0 = (blockIdx.x * waves_per_wg + wave) * 32;
+  const bool active = q0 < T;
 
+  // Q^T fragments (B operand of S^T): lane -> query q0 + l32, head dims ks*16 + 8g .. +7.
   bf16x8_t qf[QK_STEPS];
   {
-    const int qr = q0 + l16;
+    const int qr = q0 + l32;
 #pragma unroll
     for (int ks = 0; ks < QK_STEPS; ++ks) {
       uint4 v = make_uint4(0, 0, 0, 0);
-      if (qr < T) v = *reinterpret_cast<const uint4*>(q + ((int64_t)b * T + qr) * qrs + (int64_t)h * DH + ks * 32 + g16 * 8);
+      if (qr < T) v = *reinterpret_cast<const uint4*>(q + ((int64_t)b * T + qr) * qrs + (int64_t)h * DH + ks * 16 + 8 * g);
       qf[ks] = as_bf16x8(v);
     }
   }
 
-  f32x4_t o[OB];
+  f32x16_t o[OB];
 #pragma unroll
-  for (int d = 0; d < OB; ++d) o[d] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
-  float mrow[4], lrow[4];
+  for (int d = 0; d < OB; ++d)
 #pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    mrow[v] = -INFINITY;
-    lrow[v] = 0.0f;
-  }
+    for (int v = 0; v < 16; ++v) o[d][v] = 0.0f;
+  float m_i = -INFINITY, l_i = 0.0f;
 
   const uint16_t* kbase = kv + (int64_t)b * kvb + (int64_t)h * kvh;
   const uint16_t* vbase = kbase + kvkv;
-  uint16_t* Pw = Ps[wave];
+  const int ntiles = (N + kKeyTile - 1) / kKeyTile;
 
-  for (int n0 = 0; n0 < N; n0 += kKeyTile) {
-    for (int c = tid; c < kKeyTile * CPK; c += kAttnThreads) {
-      const int key = c / CPK, dc = (c - key * CPK) * 8;
-      const int n = n0 + key;
-      uint4 kk = make_uint4(0, 0, 0, 0), vv = make_uint4(0, 0, 0, 0);
-      if (n < N) {
-        kk = *reinterpret_cast<const uint4*>(kbase + (int64_t)n * kvn + dc);
-        vv = *reinterpret_cast<const uint4*>(vbase + (int64_t)n * kvn + dc);
-      }
-      *reinterpret_cast<uint4*>(&Ks[key * KROW + dc]) = kk;
-      const uint32_t w[4] = {vv.x, vv.y, vv.z, vv.w};
+  u32x4_t kreg[IT], vreg[IT];
+  auto load_tile = [&](int t) __attribute__((always_inline)) {
 #pragma unroll
-      for (int e = 0; e < 4; ++e) {
-        Vt[(dc + 2 * e) * VROW + key] = (uint16_t)(w[e] & 0xffffu);
-        Vt[(dc + 2 * e + 1) * VROW + key] = (uint16_t)(w[e] >> 16);
+    for (int i = 0; i < IT; ++i) {
+      const int c = tid + i * nthreads;
+      kreg[i] = u32x4_t{0, 0, 0, 0};
+      vreg[i] = u32x4_t{0, 0, 0, 0};
+      if (c < ITEMS) {
+        const int kk = c / CPR, kc = c - kk * CPR;       // K: row-major, 8 lanes per 128-byte row
+        const int nk = t * kKeyTile + kk;
+        if (nk < N) kreg[i] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)nk * kvn + kc * 8);
+        const int vk = c % kKeyTile, vc = c / kKeyTile;  // V: 64 consecutive keys per wave, one chunk
+        const int nv = t * kKeyTile + vk;
+        if (nv < N) vreg[i] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)nv * kvn + vc * 8);
       }
     }
-    __syncthreads();
-
-    // S = Q . K^T for four 16-key blocks: s[kb][v] = S[row 4*g16+v][key kb*16 + l16]
-    f32x4_t s[4];
+  };
+  auto store_tile = [&](int stage) __attribute__((always_inline)) {
+    unsigned char* ks = smem + stage * STAGE;
+    unsigned char* vs = ks + KSTAGE;
 #pragma unroll
-    for (int kb = 0; kb < 4; ++kb) {
-      s[kb] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int i = 0; i < IT; ++i) {
+      const int c = tid + i * nthreads;
+      if (c < ITEMS) {
+        const int kk = c / CPR, kc = c - kk * CPR;
+        *reinterpret_cast<u32x4_t*>(ks + kk * KROWB + ((kc ^ (kk & (CPR - 1))) << 4)) = kreg[i];
+        const int vk = c % kKeyTile, vc = c / kKeyTile;
 #pragma unroll
-      for (int ks = 0; ks < QK_STEPS; ++ks) {
-        const bf16x8_t kf = as_bf16x8(*reinterpret_cast<const uint4*>(&Ks[(kb * 16 + l16) * KROW + ks * 32 + g16 * 8]));
-        s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(qf[ks], kf, s[kb], 0, 0, 0);
+        for (int e = 0; e < 4; ++e) {
+          const uint32_t w = vreg[i][e];
+          *reinterpret_cast<uint16_t*>(vs + (vc * 8 + 2 * e) * VTROW + vk * 2) = (uint16_t)(w & 0xffffu);
+          *reinterpret_cast<uint16_t*>(vs + (vc * 8 + 2 * e + 1) * VTROW + vk * 2) = (uint16_t)(w >> 16);
+        }
       }
-      if (n0 + kb * 16 + l16 >= N) s[kb] = f32x4_t{-INFINITY, -INFINITY, -INFINITY, -INFINITY};
     }
+  };
 
+  auto compute = [&](int stage, int t) __attribute__((always_inline)) {
+    const unsigned char* ks = smem + stage * STAGE;
+    const unsigned char* vs = ks + KSTAGE;
+    // S^T blocks: s[kb][v] = S^T[key kb*32 + 8(v/4) + 4g + v%4][query l32]
+    f32x16_t s[2];
 #pragma unroll
-    for (int v = 0; v < 4; ++v) {
-      float mx = fmaxf(fmaxf(s[0][v], s[1][v]), fmaxf(s[2][v], s[3][v]));
-      mx = max16(mx);
-      const float mnew = fmaxf(mrow[v], mx);
-      const float alpha = exp2f((mrow[v] - mnew) * scale_log2);
-      float rs = 0.0f;
+    for (int kb = 0; kb < 2; ++kb) {
 #pragma unroll
-      for (int kb = 0; kb < 4; ++kb) {
-        const float p = exp2f((s[kb][v] - mnew) * scale_log2);
+      for (int v = 0; v < 16; ++v) s[kb][v] = 0.0f;
+      const int key = kb * 32 + l32;
+#pragma unroll
+      for (int kstep = 0; kstep < QK_STEPS; ++kstep) {
+        const int ch = kstep * 2 + g;
+        const bf16x8_t kf =
+            as_bf16x8(*reinterpret_cast<const uint4*>(ks + key * KROWB + ((ch ^ (key & (CPR - 1))) << 4)));
+        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kstep], s[kb], 0, 0, 0);
+      }
+    }
+    if ((t + 1) * kKeyTile > N) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (t * kKeyTile + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3) >= N) s[kb][v] = -INFINITY;
+    }
+    float mx = s[0][0];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = fmaxf(m_i, mx);
+    const float alpha = exp2f((m_i - m_new) * scale_log2);
+    const float mc = m_new * scale_log2;
+    float rs = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float p = exp2f(fmaf(s[kb][v], scale_log2, -mc));
+        s[kb][v] = p;
         rs += p;
-        Pw[(4 * g16 + v) * PROW + kb * 16 + l16] = (uint16_t)f32_to_bf16(p);
       }
-      rs = sum16(rs);
-      lrow[v] = lrow[v] * alpha + rs;
-      mrow[v] = mnew;
+    rs += __shfl_xor(rs, 32, 64);
+    l_i = l_i * alpha + rs;
+    m_i = m_new;
 #pragma unroll
-      for (int d = 0; d < OB; ++d) o[d][v] *= alpha;
+    for (int d = 0; d < OB; ++d)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) o[d][v] *= alpha;
+    // P^T fragments: k-step j covers keys 16j + {4g..4g+3} and 16j + 8 + {4g..4g+3}.
+    bf16x8_t pf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float tmp[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tmp[e] = s[j >> 1][8 * (j & 1) + e];
+      pf[j] = pack_bf16x8(tmp);
     }
-    __syncthreads();
+#pragma unroll
+    for (int d = 0; d < OB; ++d) {
+      const unsigned char* vrow = vs + (d * 32 + l32) * VTROW;
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + (16 * j + 4 * g) * 2);
+        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + (16 * j + 8 + 4 * g) * 2);
+        const bf16x8_t vf = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
+        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j], o[d], 0, 0, 0);
+      }
+    }
+  };
 
-    // O += P . V over the 64 keys (two K=32 steps).
-#pragma unroll
-    for (int ks = 0; ks < 2; ++ks) {
-      const bf16x8_t pf = as_bf16x8(*reinterpret_cast<const uint4*>(&Pw[l16 * PROW + ks * 32 + g16 * 8]));
-#pragma unroll
-      for (int d = 0; d < OB; ++d) {
-        const bf16x8_t vf = as_bf16x8(*reinterpret_cast<const uint4*>(&Vt[(d * 16 + l16) * VROW + ks * 32 + g16 * 8]));
-        o[d] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(pf, vf, o[d], 0, 0, 0);
-      }
-    }
+  load_tile(0);
+  store_tile(0);
+  __syncthreads();
+  for (int t = 0; t < ntiles; ++t) {
+    if (t + 1 < ntiles) load_tile(t + 1);
+    if (active) compute(t & 1, t);
+    if (t + 1 < ntiles) store_tile((t + 1) & 1);
     __syncthreads();
   }
 
-#pragma unroll
-  for (int v = 0; v < 4; ++v) {
-    const int qr = q0 + 4 * g16 + v;
-    if (qr >= T) continue;
-    const float inv = 1.0f / lrow[v];
+  // O^T[d][q]: lane l, register v of block db -> d = db*32 + 8(v/4) + 4g + v%4 (4 consecutive d per
+  // group of 4 registers -> one 8-byte store), q = q0 + l32.
+  const int qr = q0 + l32;
+  if (active && qr < T) {
+    const float inv = 1.0f / l_i;
     uint16_t* orow = out + ((int64_t)b * T + qr) * ors + (int64_t)h * DH;
 #pragma unroll
-    for (int d = 0; d < OB; ++d) orow[d * 16 + l16] = (uint16_t)f32_to_bf16(o[d][v] * inv);
+    for (int d = 0; d < OB; ++d)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+        bf16x4_t w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = (__bf16)(o[d][4 * r4 + e] * inv);
+        *reinterpret_cast<bf16x4_t*>(orow + d * 32 + 8 * r4 + 4 * g) = w;
+      }
   }
 }
 
@@ -163,20 +238,30 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
   OUDJAT_REQUIRE(N > 0, OUDJAT_ERR_UNSUPPORTED_SHAPE, "sparse_query_attention: no keys");
   OUDJAT_REQUIRE(Dh == 64 || Dh == 128, OUDJAT_ERR_UNSUPPORTED_SHAPE, "sparse_query_attention: Dh=%lld (64 or 128)",
                  (long long)Dh);
-  OUDJAT_REQUIRE(qrs % 8 == 0 && kvb % 8 == 0 && kvn % 8 == 0 && kvkv % 8 == 0 && kvh % 8 == 0 && aligned(q, 16) &&
-                     aligned(kv, 16),
+  OUDJAT_REQUIRE(qrs % 8 == 0 && kvb % 8 == 0 && kvn % 8 == 0 && kvkv % 8 == 0 && kvh % 8 == 0 && ors % 4 == 0 &&
+                     aligned(q, 16) && aligned(kv, 16) && aligned(out, 8),
                  OUDJAT_ERR_UNSUPPORTED_LAYOUT, "sparse_query_attention: 16-byte aligned q and kv rows required");
   OUDJAT_REQUIRE(B <= 65535 && H <= 65535, OUDJAT_ERR_TOO_LARGE, "sparse_query_attention: grid too large");
-  OUDJAT_REQUIRE(N < ((int64_t)1 << 31) && T < ((int64_t)1 << 31), OUDJAT_ERR_TOO_LARGE,
+  OUDJAT_REQUIRE(N < ((int64_t)1 << 30) && T < ((int64_t)1 << 30), OUDJAT_ERR_TOO_LARGE,
                  "sparse_query_attention: N or T too large");
   const float scale_log2 = scale * 1.4426950408889634f;
-  dim3 grid((unsigned)cdiv(T, kQTile), (unsigned)H, (unsigned)B);
+  const int64_t waves = cdiv(T, 32);
+  const int64_t n_wg = cdiv(waves, Dh == 64 ? kMaxWaves64 : kMaxWaves128);
+  int w = (int)cdiv(waves, n_wg);
+  if (w < kMinWaves) w = kMinWaves;
+  dim3 grid((unsigned)n_wg, (unsigned)H, (unsigned)B);
   hipStream_t st = as_stream(stream);
+  const void* fn = Dh == 64 ? (const void*)sq_attention_kernel<64> : (const void*)sq_attention_kernel<128>;
+  const size_t lds = Dh == 64 ? 2 * (64 * 128 + 64 * 136) : 2 * (64 * 256 + 128 * 136);
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "sparse_query_attention: %s", hipGetErrorString(e));
+  }
   if (Dh == 64)
-    sq_attention_kernel<64><<<grid, kAttnThreads, 0, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N,
-                                                           scale_log2, out, ors);
+    sq_attention_kernel<64><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N, scale_log2, out,
+                                                       ors, w);
   else
-    sq_attention_kernel<128><<<grid, kAttnThreads, 0, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N,
-                                                            scale_log2, out, ors);
+    sq_attention_kernel<128><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N, scale_log2,
+                                                        out, ors, w);
   return check_launch("sparse_query_attention");
 }

@@ -74,7 +74,7 @@ def test_single_block_identical_inputs(dev, name, B, ratio):
     # the ulp of x_attn's magnitude, not of the (smaller) increment.
     bos_ref = cache_ref["layer0_blocks_out_sum"]
     summand = (x_ref.float().abs() + bos_ref.float().abs()).numpy()
-    assert_propagated_close(gcache["layer0_blocks_out_sum"], bos_ref, floor_abs=2 * bf16_ulp(summand),
+    assert_propagated_close(gcache["layer0_blocks_out_sum"], bos_ref, floor_abs=4 * bf16_ulp(summand),
                             what="blocks_out_sum")
     assert_bits_equal(gcache["_partial_token_query_plan_cache"][next(iter(gcache["_partial_token_query_plan_cache"]))]
                       .update_indice, plan.update_indice, "update_indice")
