@@ -425,9 +425,6 @@ class SelfAttentionBlock(nn.Module):
         if cvm is not None:
             combined = combined.masked_fill(~cvm.to(combined.device), float("-inf"))
         Pn = dindice_patches.shape[1]
-        if kw["token_keep_thres"] is not None:
-            raise NotImplementedError("threshold token selection (token_keep_thres) is not part of this build; "
-                                      "use token_keep_ratio (top-k)")
         ratio = float(kw["token_keep_ratio"])
         k = Pn if ratio >= 1.0 else min(int(Pn * ratio), Pn)
         scores = combined.to(torch.float32).contiguous()
@@ -472,6 +469,9 @@ class SelfAttentionBlock(nn.Module):
         if kw["server_pscore"] not in self._VALID_SERVER_PSCORES:
             raise ValueError(f"Unknown server_pscore '{kw['server_pscore']}'. "
                              f"Available values: {sorted(self._VALID_SERVER_PSCORES)}")
+        if kw["token_keep_thres"] is not None:
+            raise NotImplementedError("threshold token selection (token_keep_thres) is not part of this build; "
+                                      "use token_keep_ratio (top-k)")
         if x.dtype != torch.bfloat16 or x.dim() != 3:
             raise ValueError("correct_partial_token expects x [B, N, C] bf16")
         B, N, C = x.shape

@@ -1,0 +1,107 @@
+"""Host-side logic of the drop-in (CPU only): option normalisation, the executor registry, group plans,
+the block's parameter names, the product path's refusal of CPU tensors, and bench.py's one-GPU rule.
+
+Semantics follow offload/common/protocol.py:6-181 and offload/server/model/__init__.py:4-40.
+"""
+
+import os
+import subprocess
+import sys
+
+import pytest
+import torch
+
+from appcorr_amd import kernels as K
+from appcorr_amd.dinov3 import SelfAttentionBlock
+from appcorr_amd.server import default_appcorr_kwargs, get_model_executor, normalize_appcorr_kwargs
+from appcorr_amd.server.dinov3_classifier import make_group_plan
+
+ROOT = os.path.dirname(os.path.dirname(os.path.abspath(__file__)))
+
+
+def test_defaults_match_reference_values():
+    d = default_appcorr_kwargs()
+    assert d["token_keep_ratio"] == 0.2 and d["token_keep_thres"] is None
+    assert d["server_pscore"] == "cls_attn_prob" and d["server_pscore_weight"] == 1.0
+    assert d["mobile_pscore"] == "none" and d["mobile_pscore_weight"] == 0.0
+    assert d["pscore_fusion"] == "add" and d["method"] == "partial_token" and d["num_groups"] == 1
+    # empty kwargs -> disabled; any explicit option enables unless "enabled" says otherwise
+    assert normalize_appcorr_kwargs({})["enabled"] is False
+    assert normalize_appcorr_kwargs({"token_keep_ratio": 0.5})["enabled"] is True
+    assert normalize_appcorr_kwargs({"token_keep_ratio": 0.5, "enabled": False})["enabled"] is False
+
+
+def test_aliases_and_coercions():
+    o = normalize_appcorr_kwargs({"mobile_pscore": "patch_residual_l2", "pscore_fusion": "mul",
+                                  "server_pscore": "pseudo_patch_attn_prob", "token_keep_thres": "None",
+                                  "num_groups": 0, "sdpa_query_bucket_size": -3, "token_prune_min_keep": 0})
+    assert o["mobile_pscore"] == "residual_energy"
+    assert o["pscore_fusion"] == "multiply"
+    assert o["server_pscore"] == "patch_pseudo_attn_prob"
+    assert o["token_keep_thres"] is None
+    assert o["num_groups"] == 1 and o["sdpa_query_bucket_size"] == 0 and o["token_prune_min_keep"] == 1
+    assert normalize_appcorr_kwargs({"cls_alive_ratio": 0.3})["token_keep_ratio"] == 0.3
+    assert normalize_appcorr_kwargs({"token_prune_score": "patch_attn_prob"})["server_pscore"] == "patch_attn_prob"
+    o = normalize_appcorr_kwargs({"server_pscore": "cls_attn_prob", "server_pscore_layer_fusion": "mean"})
+    assert o["server_pscore"] == "cls_attn_prob_layermean"
+    assert normalize_appcorr_kwargs({"pscore_fusion": "bogus"})["pscore_fusion"] == "add"
+
+
+def test_validation_errors():
+    with pytest.raises(ValueError, match="Unknown server_pscore"):
+        normalize_appcorr_kwargs({"server_pscore": "nope"})
+    with pytest.raises(ValueError, match="persist_correction_residual"):
+        normalize_appcorr_kwargs({"persist_correction_residual": True})
+    with pytest.raises(ValueError, match="num_groups must match"):
+        normalize_appcorr_kwargs({"num_groups": 2}, {"num_groups": 4})
+    with pytest.raises(ValueError, match="pyramid_levels must match"):
+        normalize_appcorr_kwargs({"pyramid_levels": [0]}, {"pyramid_levels": [0, 1]})
+    assert normalize_appcorr_kwargs({"token_keep_ratio": 0.1}, {"num_groups": 4})["num_groups"] == 4
+
+
+def test_executor_registry():
+    ex = get_model_executor("dinov3_vitl16_classifier", torch.device("cpu"))
+    assert type(ex).__name__ == "DINOv3ClassifierExecutor"
+    for name in ("sam3", "dinov3_vitl16_detector", "gemma3"):
+        with pytest.raises(ValueError):
+            get_model_executor(name, torch.device("cpu"))
+
+
+def test_group_plan_fields():
+    dind = torch.arange(10).unsqueeze(0).expand(3, -1).contiguous()
+    gp = make_group_plan(dind, 5)
+    assert gp.prefix_dindice.shape == (3, 5) and gp.group_patch_dindice.shape == (3, 5)
+    assert torch.equal(gp.group_patch_keep_local_idx[1], torch.arange(5))
+    assert gp.full_patch_count.tolist() == [5, 5, 5]
+
+
+def test_block_parameter_names_match_reference_tree():
+    names = set(SelfAttentionBlock(64, 4, qkv_bias=True, mask_k_bias=True, init_values=1e-5).state_dict())
+    want = {"norm1.weight", "norm1.bias", "attn.qkv.weight", "attn.qkv.bias", "attn.qkv.bias_mask",
+            "attn.proj.weight", "attn.proj.bias", "ls1.gamma", "norm2.weight", "norm2.bias", "mlp.fc1.weight",
+            "mlp.fc1.bias", "mlp.fc2.weight", "mlp.fc2.bias", "ls2.gamma"}
+    assert names == want
+    sw = set(SelfAttentionBlock(128, 4, ffn_layer="swiglu64", ffn_ratio=3.0).state_dict())
+    assert {"mlp.w1.weight", "mlp.w2.weight", "mlp.w3.weight"} <= sw
+
+
+def test_product_path_refuses_cpu_tensors():
+    x = torch.zeros(4, 8, 16, dtype=torch.bfloat16)
+    idx = torch.zeros(2, dtype=torch.long)
+    with pytest.raises(Exception):
+        K.gather_rows(x, idx, idx)
+    with pytest.raises(Exception):
+        K.layer_norm(x.view(-1, 16), torch.ones(16, dtype=torch.bfloat16), torch.zeros(16, dtype=torch.bfloat16))
+
+
+def test_threshold_selection_not_implemented():
+    blk = SelfAttentionBlock(64, 4)
+    with pytest.raises(NotImplementedError):
+        blk.correct(torch.zeros(1, 9, 64), torch.arange(9)[None], None, {}, "layer0", token_keep_thres=0.5,
+                    token_keep_ratio=None, appcorr_method="partial_token")
+
+
+def test_bench_refuses_more_than_one_gpu():
+    r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
+                       text=True, timeout=120, cwd=ROOT)
+    assert r.returncode == 2 and "one MI355X" in r.stderr

@@ -1,0 +1,163 @@
+"""Pins of the DINOv3 block oracle (oracle/model.py) against facts fixed independently of it.
+
+  * primitives: the fp64 LayerNorm / GELU / SDPA against torch.nn.functional's own fp64 kernels;
+  * RoPE: rope_rotate against rotation by complex multiplication (x_i + j x_{i+D/2}) * e^{j theta}
+    (the sign convention of rotate_half), and the tables against closed-form angles at known
+    patch positions;
+  * the correction block against the dense (approx) forward, which it must reproduce:
+      - 100% keep on the approx input: x_out and K/V bit-identical over several blocks
+        (LayerScale 1 so the approx pass's two roundings of x + g * proj coincide with the
+        correction's fused one);
+      - unchanged input, partial keep: the K/V cache is a fixed point and selected rows equal the
+        approx outputs bit-for-bit;
+      - k = 0: every patch row is x + blocks_out_sum exactly;
+  * the bf16-eager mode (the CPU baseline) computes the same block as the fp64 mode.
+"""
+
+import math
+
+import numpy as np
+import pytest
+import torch
+import torch.nn.functional as F
+
+from oracle import model as OM
+from oracle import plan as OP
+from tests.util import bits
+
+
+def _rb(t):
+    return t.to(torch.float32).to(torch.bfloat16)
+
+
+def _bits_equal_frac(a, b):
+    return float((bits(a) == bits(b)).mean())
+
+
+def test_layernorm_gelu_sdpa_match_torch_fp64():
+    g = torch.Generator().manual_seed(0)
+    x = (torch.randn(64, 384, generator=g) * 3 + 0.5).to(torch.bfloat16)
+    w = (1 + 0.1 * torch.randn(384, generator=g)).to(torch.bfloat16)
+    b = (0.1 * torch.randn(384, generator=g)).to(torch.bfloat16)
+    ln = OM._F64.ln(x, w, b, 1e-5)
+    ref = _rb(F.layer_norm(x.double(), (384,), w.double(), b.double(), 1e-5))
+    assert _bits_equal_frac(ln, ref) >= 0.999
+    assert (ln.float() - ref.float()).abs().max() <= 2.0 ** -6
+    ge = OM._F64.gelu(x)
+    assert _bits_equal_frac(ge, _rb(F.gelu(x.double()))) >= 0.999
+    q = torch.randn(2, 3, 7, 64, generator=g).to(torch.bfloat16)
+    k = torch.randn(2, 3, 11, 64, generator=g).to(torch.bfloat16)
+    v = torch.randn(2, 3, 11, 64, generator=g).to(torch.bfloat16)
+    o = OM._F64.sdpa(q, k, v, 64 ** -0.5)
+    ref = _rb(F.scaled_dot_product_attention(q.double(), k.double(), v.double(), scale=64 ** -0.5))
+    assert _bits_equal_frac(o, ref) >= 0.999
+
+
+def test_rope_rotate_is_complex_rotation():
+    g = torch.Generator().manual_seed(1)
+    D, n = 64, 300
+    x = torch.randn(n, D, generator=g).to(torch.bfloat16)
+    theta = torch.rand(n, D // 2, generator=g, dtype=torch.float64) * 2 * math.pi
+    ang = torch.cat([theta, theta], dim=-1)
+    got = OM.rope_rotate(x, torch.sin(ang).float(), torch.cos(ang).float()).double()
+    z = torch.complex(x[:, : D // 2].double(), x[:, D // 2:].double()) * torch.exp(1j * theta)
+    ref = torch.cat([z.real, z.imag], dim=-1)
+    err = (got - ref).abs()
+    assert float(err.max()) <= 2.0 ** -7 * float(ref.abs().max()) + 1e-6
+    assert float((err / (ref.abs() + 1e-3)).mean()) < 2.0 ** -8
+
+
+def test_rope_tables_closed_form():
+    cfg = OM.CONFIGS["vits16_224"]
+    D = cfg.head_dim
+    sin, cos = OM.rope_tables(cfg, H=3, W=3)
+    assert sin.shape == (9, D) and cos.shape == (9, D)
+    # centre patch of an odd grid: both coordinates 0 -> angle 0
+    np.testing.assert_array_equal(sin[4].numpy(), 0.0)
+    np.testing.assert_array_equal(cos[4].numpy(), 1.0)
+    # patch (h=0, w=2): coordinates (-2/3, +2/3); frequency j < D/4 uses h, D/4 <= j < D/2 uses w
+    per = cfg.rope_base ** (2 * np.arange(D // 4) / (D // 2))
+    want = np.concatenate([2 * np.pi * (-2 / 3) / per, 2 * np.pi * (2 / 3) / per])
+    want = np.concatenate([want, want])
+    np.testing.assert_allclose(sin[2].numpy(), np.sin(want), atol=2e-6)
+    np.testing.assert_allclose(cos[2].numpy(), np.cos(want), atol=2e-6)
+
+
+def _stress(cfg, depth, B, seed=0):
+    weights = OM.make_block_weights(cfg, seed, gamma=1.0, bias_std=0.05, ln_std=0.1, depth=depth)
+    x_base, x_full, _, imp = OM.make_inputs(cfg, B, seed + 1)
+    return weights, x_base, x_full, imp, OM.rope_tables(cfg)
+
+
+def test_full_keep_reproduces_approx_forward():
+    cfg = OM.CONFIGS["vits16_224"]
+    B, depth = 2, 3
+    weights, x_base, _, imp, rope = _stress(cfg, depth, B)
+    x_apx, cache_apx = OM.approx_pass(cfg, weights, x_base, rope)
+    plan = OP.build_plan(imp.numpy(), cfg.num_patches, OM.full_dindice(cfg, B).numpy(), cfg.num_pretokens,
+                         cfg.num_tokens)
+    # start from a cache of garbage: every row must be overwritten by the correction
+    cache = {k: torch.randn(v.shape).to(v.dtype) for k, v in cache_apx.items()}
+    x_cor, cache = OM.correct_pass(cfg, weights, x_base, plan, rope, cache)
+    assert torch.equal(bits_t(x_cor), bits_t(x_apx))
+    for i in range(depth):
+        assert torch.equal(bits_t(cache[f"layer{i}_kv"]), bits_t(cache_apx[f"layer{i}_kv"])), i
+
+
+def bits_t(t):
+    return t.view(torch.int16)
+
+
+@pytest.mark.parametrize("ratio", [0.25, 0.5])
+def test_unchanged_input_is_a_fixed_point(ratio):
+    cfg = OM.CONFIGS["vits16_224"]
+    B = 2
+    weights, x_base, _, imp, rope = _stress(cfg, 1, B)
+    x_apx, cache_apx = OM.approx_pass(cfg, weights, x_base, rope)
+    k = OP.keep_count(cfg.num_patches, ratio)
+    plan = OP.build_plan(imp.numpy(), k, OM.full_dindice(cfg, B).numpy(), cfg.num_pretokens, cfg.num_tokens)
+    cache = {k_: v.clone() for k_, v in cache_apx.items()}
+    x_cor, cache = OM.correct_block(cfg, weights[0], x_base, plan, rope, cache, "layer0")
+    assert torch.equal(bits_t(cache["layer0_kv"]), bits_t(cache_apx["layer0_kv"]))
+    bi, ti = torch.from_numpy(plan.active_batch_idx), torch.from_numpy(plan.active_token_idx)
+    assert torch.equal(bits_t(x_cor[bi, ti]), bits_t(x_apx[bi, ti]))
+    # blocks_out_sum is the block's increment x_out - x: re-persisted on selected rows (up to the
+    # roundings of x_attn = x + proj and of x_attn - x_act, a few half-ulps of |x| + |increment|),
+    # untouched elsewhere. Dropping the - x_act term moves it by |x|.
+    bos_new, bos_apx = cache["layer0_blocks_out_sum"], cache_apx["layer0_blocks_out_sum"]
+    sel = torch.zeros(B, cfg.num_tokens, dtype=torch.bool)
+    sel[bi, ti] = True
+    assert torch.equal(bits_t(bos_new[~sel]), bits_t(bos_apx[~sel]))
+    d = (bos_new[sel].double() - bos_apx[sel].double()).abs()
+    lim = 2.0 ** -6 * (x_base[sel].double().abs() + bos_apx[sel].double().abs()) + 1e-30
+    assert bool((d <= lim).all()), float((d - lim).max())
+
+
+def test_zero_keep_gives_x_plus_blocks_out_sum():
+    cfg = OM.CONFIGS["vits16_224"]
+    B = 2
+    weights, x_base, x_full, imp, rope = _stress(cfg, 1, B)
+    _, cache = OM.approx_pass(cfg, weights, x_base, rope)
+    plan = OP.build_plan(imp.numpy(), 0, OM.full_dindice(cfg, B).numpy(), cfg.num_pretokens, cfg.num_tokens)
+    bos = cache["layer0_blocks_out_sum"].clone()
+    kv = cache["layer0_kv"].clone()
+    x_cor, cache = OM.correct_block(cfg, weights[0], x_full, plan, rope, cache, "layer0")
+    p = cfg.num_pretokens
+    ref = (x_full.float() + bos.float()).to(torch.bfloat16)
+    assert torch.equal(bits_t(x_cor[:, p:]), bits_t(ref[:, p:]))
+    assert torch.equal(bits_t(cache["layer0_kv"][:, p:]), bits_t(kv[:, p:]))
+    assert torch.equal(bits_t(cache["layer0_blocks_out_sum"][:, p:]), bits_t(bos[:, p:]))
+
+
+def test_bf16_eager_mode_agrees_with_fp64_mode():
+    cfg = OM.CONFIGS["vits16_224"]
+    B = 1
+    weights, x_base, x_full, imp, rope = _stress(cfg, 1, B)
+    _, cache = OM.approx_pass(cfg, weights, x_base, rope)
+    plan = OP.build_plan(imp.numpy(), 98, OM.full_dindice(cfg, B).numpy(), cfg.num_pretokens, cfg.num_tokens)
+    x64, _ = OM.correct_block(cfg, weights[0], x_full, plan, rope, {k: v.clone() for k, v in cache.items()},
+                              "layer0", mode="f64")
+    x16, _ = OM.correct_block(cfg, weights[0], x_full, plan, rope, {k: v.clone() for k, v in cache.items()},
+                              "layer0", mode="bf16")
+    d = (x64.float() - x16.float()).abs()
+    assert float(d.mean()) <= 2.0 ** -8 * float(x64.float().abs().mean())
