@@ -4,13 +4,17 @@
 // natural operand layout of v_mfma_f32_32x32x16_bf16: each lane feeds 8 consecutive K values of one
 // row of A and one row of W, i.e. one 16-byte LDS read per operand per MFMA.
 //
-// Kernel family (template): workgroup tile BM x BN x 64, WGM x WGN waves, each wave owning a
-// (BM/WGM) x (BN/WGN) sub-tile of 32x32 MFMA blocks whose accumulators live in AGPRs.
-//   * LDS holds two K tiles (double buffer). Rows are 128 bytes with the 16-byte chunks
-//     XOR-swizzled by (row & 7), so both the 16-byte stores of a row and the 16-byte fragment reads
-//     of 8 consecutive rows touch disjoint banks without padding.
-//   * Global loads run PF tiles ahead through registers (PF = 1 or 2), so a K step's loads have one
-//     or two K steps of MFMA work to hide their latency.
+// Three kernel families (templates over the workgroup tile BM x BN and the WGM x WGN wave grid):
+//   * gemm_bf16_pipe_kernel: direct-to-LDS loads (global_load_lds, no staging registers), K tiles of
+//     32 in four LDS stages issued three tiles ahead, fragments read one K tile ahead of their
+//     MFMAs. 256 x 256 tiles with 8 waves; used when one round of tiles fills the GPU.
+//   * gemm_bf16_dma_kernel: direct-to-LDS loads, K tiles of 64, two stages. 128 x 128 tiles with 4
+//     waves, two workgroups per CU; used for the other grids.
+//   * gemm_bf16_kernel: register-staged loads with 16-byte-aligned fallbacks (any N % 64 == 0, any
+//     output alignment).
+// Common to all:
+//   * LDS rows of 16-byte chunks XOR-swizzled so that the 16-byte fragment reads of 16 consecutive
+//     rows cover all 64 LDS banks (measured: zero bank-conflict cycles).
 //   * Rows of A beyond M are clamped to M-1 instead of predicated: they only feed output rows that
 //     are never stored.
 //   * Workgroups are renumbered so that consecutive tiles land on the same XCD (dispatch places
@@ -20,8 +24,11 @@
 // The epilogues fold in the elementwise work the reference runs as separate kernels after each
 // Linear: bias, exact-erf GELU (fc1), LayerScale (fc2), LayerScale + residual (proj) and the SwiGLU
 // gate, with a bf16 rounding at every point where the reference materialises a bf16 tensor.
+#include <math.h>
 #include <stdlib.h>
+#include <string.h>
 
+#include <mutex>
 #include <type_traits>
 
 #include "common.hpp"
@@ -38,13 +45,41 @@ struct EpiArgs {
   int64_t ldr;
 };
 
+// Two fp32 -> packed bf16 pair (low half = a) with the hardware round-to-nearest-even convert.
+typedef float f32x2_t __attribute__((ext_vector_type(2)));
+typedef __bf16 bf16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t cvt_pk_bf16(float a, float b) {
+  return __builtin_bit_cast(uint32_t, __builtin_convertvector((f32x2_t){a, b}, bf16x2_t));
+}
+
+// GELU of a bf16 input as a table. The input of the GELU epilogue is already a bf16 value
+// v = bf16(acc + bias), so the result bf16(0.5 v erfc(-v / sqrt 2)) is a function of 16 bits:
+//   * |v| in [2^-16, 16) (magnitude bits 0x3780 .. 0x417f, both signs): 5120-entry table, filled
+//     on the host from the double-precision erfc, rounded to fp32 and then RNE to bf16;
+//   * |v| < 2^-16: 0.5 v exactly (the next term, v^2 / sqrt(2 pi), is below 2^-17 relative and
+//     cannot move the rounding); bf16 subnormals and zeros give a signed zero;
+//   * v >= 16: v;  v <= -16: -0.0 (the product underflows);  NaN: NaN;  -inf: NaN (as -inf * 0).
+static constexpr int kGeluLut = 5120;
+static constexpr uint32_t kGeluLo = 0x3780u, kGeluSpan = 0x0a00u;
+__device__ uint16_t g_gelu_lut[kGeluLut];
+
+__device__ __forceinline__ uint32_t gelu_bf16_bits(uint32_t b, const uint16_t* lut) {
+  const uint32_t a = b & 0x7fffu;
+  const uint32_t d = a - kGeluLo;  // unsigned: wraps for a < kGeluLo
+  const uint32_t t = lut[min(d, kGeluSpan - 1u) + (b >> 15) * kGeluSpan];
+  if (__builtin_expect(d < kGeluSpan, 1)) return t;
+  if (a < kGeluLo) return a >= 0x0100u ? b - 0x80u : (b & 0x8000u);
+  if ((b >> 15) == 0u) return b;
+  return a == 0x7f80u ? 0x7fc0u : (a > 0x7f80u ? b : 0x8000u);
+}
+
 template <int EPI>
 __device__ __forceinline__ float epilogue(float acc, int64_t row, int64_t col, const EpiArgs& ea) {
   float v = acc;
   if (ea.bias) v += bf16_to_f32(ea.bias[col]);
   v = round_bf16(v);
   if (EPI == OUDJAT_EPI_BIAS_GELU) {
-    v = v * 0.5f * (1.0f + erff(v * 0.70710678118654752440f));
+    v = __uint_as_float(gelu_bf16_bits(__float_as_uint(v) >> 16, g_gelu_lut) << 16);
   } else if (EPI == OUDJAT_EPI_BIAS_LS_RESID) {
     v = fmaf(v, bf16_to_f32(ea.gamma[col]), bf16_to_f32(ea.resid[row * ea.ldr + col]));
   } else if (EPI == OUDJAT_EPI_BIAS_LS) {
@@ -59,7 +94,7 @@ __device__ __forceinline__ float epilogue(float acc, int64_t row, int64_t col, c
 template <int EPI>
 __device__ __forceinline__ float epilogue_post(float v, int64_t row, int64_t col, const EpiArgs& ea) {
   if (EPI == OUDJAT_EPI_BIAS_GELU) {
-    v = v * 0.5f * (1.0f + erff(v * 0.70710678118654752440f));
+    v = __uint_as_float(gelu_bf16_bits(__float_as_uint(v) >> 16, g_gelu_lut) << 16);
   } else if (EPI == OUDJAT_EPI_BIAS_LS_RESID) {
     v = fmaf(v, bf16_to_f32(ea.gamma[col]), bf16_to_f32(ea.resid[row * ea.ldr + col]));
   } else if (EPI == OUDJAT_EPI_BIAS_LS) {
@@ -70,8 +105,11 @@ __device__ __forceinline__ float epilogue_post(float v, int64_t row, int64_t col
   return v;
 }
 
-// Byte offset of 16-byte chunk `c` (K elements 8c .. 8c+7) of LDS row `r`.
-__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ (r & 7)) << 4); }
+// Byte offset of 16-byte chunk `c` (K elements 8c .. 8c+7) of 128-byte LDS row `r`. The XOR with
+// (r >> 1) & 7 spreads 16 consecutive rows read at one chunk over all 64 LDS banks (two rows share a
+// 256-byte bank line, so rows r and r + 1 differ in line half and rows 2q apart in slot).
+__device__ __forceinline__ int swz(int r, int c) { return r * 128 + ((c ^ ((r >> 1) & 7)) << 4); }
+
 
 template <int BM, int BN, int WGM, int WGN, int PF, int EPI>
 __global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_kernel(const uint16_t* __restrict__ A, int M, int K,
@@ -230,6 +268,82 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_kernel(const uint16_
   }
 }
 
+// Tile epilogue shared by the direct-to-LDS kernels. The MFMAs take W as their first operand, so
+// block (i, j) holds the transposed product: lane l, register v -> row wm0 + 32 i + l % 32, column
+// wn0 + 32 j + 8 (v / 4) + 4 (l / 32) + v % 4, i.e. every lane owns runs of 4 consecutive columns
+// of one row. Phase 1: bf16(acc + bias) into LDS with 8-byte writes. Phase 2: the rest of the
+// epilogue on 8 consecutive columns per lane, 16-byte global stores. Needs N % BN == 0, 16-byte
+// aligned C / gamma / resid rows and an 8-byte aligned bias; the caller has passed a barrier
+// after the last LDS read of the main loop.
+template <int BM, int BN, int FM, int FN, int NW, int EPI>
+__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FM][FN], unsigned char* smem, const uint16_t* lut,
+                                           int wm0, int wn0, int m0, int n0, int M, const EpiArgs& ea,
+                                           uint16_t* __restrict__ C, int64_t ldc) {
+  const int lane = threadIdx.x & 63;
+  constexpr int LDT = BN + 8;
+  uint16_t* ct = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int cl = wn0 + j * 32 + g * 8 + 4 * (lane >> 5);
+      float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+      if (ea.bias) {
+        const uint2 bw = *reinterpret_cast<const uint2*>(ea.bias + n0 + cl);
+        b0 = lo_bf16(bw.x); b1 = hi_bf16(bw.x); b2 = lo_bf16(bw.y); b3 = hi_bf16(bw.y);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int rl = wm0 + i * 32 + (lane & 31);
+        uint2 w;
+        w.x = cvt_pk_bf16(acc[i][j][4 * g + 0] + b0, acc[i][j][4 * g + 1] + b1);
+        w.y = cvt_pk_bf16(acc[i][j][4 * g + 2] + b2, acc[i][j][4 * g + 3] + b3);
+        *reinterpret_cast<uint2*>(ct + rl * LDT + cl) = w;
+      }
+    }
+  }
+  __syncthreads();
+  constexpr int CPR = BN / 8;
+  for (int c = threadIdx.x; c < BM * CPR; c += NW * 64) {
+    const int rl = c / CPR, cl = (c - rl * CPR) * 8;
+    const int row = m0 + rl, col = n0 + cl;
+    if (row >= M) continue;
+    uint4 o = *reinterpret_cast<const uint4*>(ct + rl * LDT + cl);
+    if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) {
+      uint32_t* w = reinterpret_cast<uint32_t*>(&o);
+#pragma unroll
+      for (int e = 0; e < 4; ++e)
+        w[e] = gelu_bf16_bits(w[e] & 0xffffu, lut) | (gelu_bf16_bits(w[e] >> 16, lut) << 16);
+    } else if constexpr (EPI != OUDJAT_EPI_BIAS) {
+      // 16-byte loads of the per-column gamma and the residual / gate row segment.
+      float v[8], g[8], r[8];
+      unpack8(o, v);
+      if constexpr (EPI == OUDJAT_EPI_BIAS_LS || EPI == OUDJAT_EPI_BIAS_LS_RESID)
+        unpack8(*reinterpret_cast<const uint4*>(ea.gamma + col), g);
+      if constexpr (EPI == OUDJAT_EPI_BIAS_LS_RESID || EPI == OUDJAT_EPI_BIAS_SILU_MUL)
+        unpack8(*reinterpret_cast<const uint4*>(ea.resid + (int64_t)row * ea.ldr + col), r);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        if constexpr (EPI == OUDJAT_EPI_BIAS_LS_RESID) v[e] = fmaf(v[e], g[e], r[e]);
+        else if constexpr (EPI == OUDJAT_EPI_BIAS_LS) v[e] = v[e] * g[e];
+        else v[e] = round_bf16(v[e] / (1.0f + expf(-v[e]))) * r[e];
+      }
+      o.x = cvt_pk_bf16(v[0], v[1]);
+      o.y = cvt_pk_bf16(v[2], v[3]);
+      o.z = cvt_pk_bf16(v[4], v[5]);
+      o.w = cvt_pk_bf16(v[6], v[7]);
+    }
+    *reinterpret_cast<uint4*>(C + (int64_t)row * ldc + col) = o;
+  }
+}
+
+// Copies the GELU table into LDS at `dst` (16-byte aligned).
+template <int NT>
+__device__ __forceinline__ void load_gelu_table(unsigned char* dst) {
+  for (int i = threadIdx.x; i < kGeluLut / 8; i += NT)
+    reinterpret_cast<uint4*>(dst)[i] = reinterpret_cast<const uint4*>(g_gelu_lut)[i];
+}
+
 // ------------------------------------------------------------------------------------------------
 // Direct-to-LDS variant. global_load_lds_dwordx4 writes lane l's 16 bytes to LDS at
 // M0 + 16*l, i.e. one wave instruction fills 8 consecutive 128-byte LDS rows. Lane l therefore
@@ -240,6 +354,11 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_kernel(const uint16_
 // ------------------------------------------------------------------------------------------------
 
 typedef __attribute__((address_space(3))) void* lds_ptr_t;
+
+// LDS bytes of the direct-to-LDS kernel before the GELU table: two K stages or the epilogue tile.
+__host__ __device__ constexpr int dma_lut_offset(int bm, int bn) {
+  return 2 * (bm + bn) * 128 > bm * (bn + 8) * 2 ? 2 * (bm + bn) * 128 : bm * (bn + 8) * 2;
+}
 
 __device__ __forceinline__ void wait_vm_all() { __builtin_amdgcn_s_waitcnt(0); }
 
@@ -258,6 +377,7 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_dma_kernel(const uin
   static_assert(AG * NW * 8 == BM && BG * NW * 8 == BN, "rows must split into 8-row groups per wave");
 
   extern __shared__ __align__(16) unsigned char smem[];
+  if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) load_gelu_table<NW * 64>(smem + dma_lut_offset(BM, BN));
 
   const int tiles_n = (N + BN - 1) / BN;
   const int tiles_m = (M + BM - 1) / BM;
@@ -279,19 +399,19 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_dma_kernel(const uin
   const int wm0 = (wave / WGN) * WM;
   const int wn0 = (wave % WGN) * WN;
   const int lrow = lane >> 3;                 // row within an 8-row group
-  const int lchunk = (lane & 7) ^ lrow;       // global K chunk this lane fetches
 
+  // Lane l fills slot l % 8 of its row, i.e. global K chunk (l % 8) ^ swizzle(row).
   const uint16_t* a_src[AG];
   const uint16_t* b_src[BG];
 #pragma unroll
   for (int i = 0; i < AG; ++i) {
     const int row = (wave * AG + i) * 8 + lrow;
-    a_src[i] = A + (int64_t)min(m0 + row, M - 1) * lda + lchunk * 8;
+    a_src[i] = A + (int64_t)min(m0 + row, M - 1) * lda + ((lane & 7) ^ ((row >> 1) & 7)) * 8;
   }
 #pragma unroll
   for (int i = 0; i < BG; ++i) {
     const int row = (wave * BG + i) * 8 + lrow;
-    b_src[i] = W + (int64_t)min(n0 + row, N - 1) * ldw + lchunk * 8;
+    b_src[i] = W + (int64_t)min(n0 + row, N - 1) * ldw + ((lane & 7) ^ ((row >> 1) & 7)) * 8;
   }
   auto issue = [&](int stage, int kt) __attribute__((always_inline)) {
     unsigned char* base = smem + stage * STAGE;
@@ -337,44 +457,226 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_dma_kernel(const uin
       for (int i = 0; i < FM; ++i)
 #pragma unroll
         for (int j = 0; j < FN; ++j)
-          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fa[i], fb[j], acc[i][j], 0, 0, 0);
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(fb[j], fa[i], acc[i][j], 0, 0, 0);
     }
   }
 
-  // Epilogue, phase 1: bf16(acc + bias) into LDS (the K stages are free once every wave is past the
-  // last MFMA). Output layout of a 32x32 block: lane l, register v -> row 8*(v/4) + 4*(l/32) + v%4,
-  // col l%32. Rows are padded by 16 bytes so lanes 0-31 and 32-63 (rows r, r+4) use different banks.
-  constexpr int LDT = BN + 8;
-  uint16_t* ct = reinterpret_cast<uint16_t*>(smem);
   __syncthreads();
+  store_tile<BM, BN, FM, FN, NW, EPI>(acc, smem, reinterpret_cast<const uint16_t*>(smem + dma_lut_offset(BM, BN)), wm0,
+                                      wn0, m0, n0, M, ea, C, ldc);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Deep-pipelined direct-to-LDS kernel. K tiles of 32 (64-byte LDS rows), 4 LDS stages, operand
+// loads issued three K tiles ahead of the MFMAs that consume them, one workgroup per CU.
+//
+//   * Swizzle: chunk c of row r sits at 16-byte slot c ^ ((r >> 2) & 3). A wave reading one chunk
+//     of 16 consecutive rows (one quarter of a fragment read) then covers all 64 LDS banks once.
+//   * Loads: one global_load_lds_dwordx4 fills 16 consecutive 64-byte rows (lane l -> row l / 4,
+//     slot l % 4, i.e. global chunk (l % 4) ^ ((l / 16) % 4)). The (BM + BN) / 16 instructions of a
+//     K tile are dealt round-robin to the waves.
+//   * Per K tile: wait for this wave's loads of the tile (vmcnt), one s_barrier (every wave's loads
+//     landed, every wave done reading the stage about to be refilled), issue the loads of tile
+//     kt + 3 into that stage, then 2 x FM x FN MFMAs with all fragments read up front.
+// ------------------------------------------------------------------------------------------------
+
+static constexpr int kBK3 = 32;
+static constexpr int kStages = 4;
+
+__device__ __forceinline__ int swz64(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt in bits 3:0 and
+// 15:14, expcnt 6:4 and lgkmcnt 11:8 at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+__device__ __forceinline__ void wait_vmcnt_rt(int n) {
+  switch (n) {
+    case 0: wait_vmcnt<0>(); break;
+    case 1: wait_vmcnt<1>(); break;
+    case 2: wait_vmcnt<2>(); break;
+    case 3: wait_vmcnt<3>(); break;
+    case 4: wait_vmcnt<4>(); break;
+    case 5: wait_vmcnt<5>(); break;
+    case 6: wait_vmcnt<6>(); break;
+    case 7: wait_vmcnt<7>(); break;
+    case 8: wait_vmcnt<8>(); break;
+    case 9: wait_vmcnt<9>(); break;
+    case 10: wait_vmcnt<10>(); break;
+    case 11: wait_vmcnt<11>(); break;
+    default: wait_vmcnt<12>(); break;
+  }
+}
+
+// Workgroup barrier without the vmcnt(0) of __syncthreads() (which would drain the loads in flight
+// for later K tiles): LDS reads are complete (lgkmcnt(0)), then s_barrier. The scheduling barriers
+// keep the compiler from moving memory operations across it.
+__device__ __forceinline__ void block_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0), vmcnt/expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// LDS bytes of the pipelined kernel before the GELU table: K stages or the epilogue tile.
+__host__ __device__ constexpr int pipe_lut_offset(int bm, int bn) {
+  return kStages * (bm + bn) * 64 > bm * (bn + 8) * 2 ? kStages * (bm + bn) * 64 : bm * (bn + 8) * 2;
+}
+
+template <int BM, int BN, int WGM, int WGN, int EPI>
+__global__ __launch_bounds__(WGM * WGN * 64) __attribute__((amdgpu_waves_per_eu(WGM * WGN / 4, WGM * WGN / 4)))
+void gemm_bf16_pipe_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t lda, const uint16_t* __restrict__ W,
+                           int N, int64_t ldw, EpiArgs ea, uint16_t* __restrict__ C, int64_t ldc, int group_m) {
+  constexpr int NW = WGM * WGN;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int FM = WM / 32, FN = WN / 32;
+  constexpr int NI = (BM + BN) / 16;              // load instructions per K tile
+  constexpr int NLM = (NI + NW - 1) / NW;         // per wave, at most
+  constexpr int STAGE = (BM + BN) * 64;
+  static_assert(BM % 16 == 0 && BN % 16 == 0 && FM >= 1 && FN >= 1 && WM % 32 == 0 && WN % 32 == 0, "tile shape");
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  // LDS: K stages (later the epilogue tile), then the GELU table for the GELU epilogue.
+  constexpr int kLutOff = pipe_lut_offset(BM, BN);
+  if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) load_gelu_table<NW * 64>(smem + kLutOff);
+
+  const int tiles_n = (N + BN - 1) / BN;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles = gridDim.x;
+  const int bid = blockIdx.x;
+  const int xcd = bid % kNumXcd;
+  const int q = tiles / kNumXcd, r = tiles % kNumXcd;
+  const int tile = xcd * q + min(xcd, r) + bid / kNumXcd;
+  const int per_group = group_m * tiles_n;
+  const int grp = tile / per_group;
+  const int first_m = grp * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
+  const int in_grp = tile - grp * per_group;
+  const int tm = first_m + in_grp % gsize, tn = in_grp / gsize;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);  // wave-uniform, kept in SGPRs
+  const int wm0 = (wave / WGN) * WM;
+  const int wn0 = (wave % WGN) * WN;
+
+  // This wave's load instructions: i = wave + j * NW.
+  const int nl = (NI % NW == 0) ? NI / NW : (NI - wave + NW - 1) / NW;
+  const uint16_t* src[NLM];
+  int dst[NLM];
+  {
+    const int lrow = lane >> 2;
+    const int lchunk = (lane & 3) ^ ((lane >> 4) & 3);
 #pragma unroll
-  for (int j = 0; j < FN; ++j) {
-    const int cl = wn0 + j * 32 + (lane & 31);
-    const float bias = ea.bias ? bf16_to_f32(ea.bias[min(n0 + cl, N - 1)]) : 0.0f;
-#pragma unroll
-    for (int i = 0; i < FM; ++i) {
-#pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const int rl = wm0 + i * 32 + 8 * (v >> 2) + 4 * (lane >> 5) + (v & 3);
-        ct[rl * LDT + cl] = (uint16_t)f32_to_bf16(acc[i][j][v] + bias);
+    for (int j = 0; j < NLM; ++j) {
+      const int i = min(wave + j * NW, NI - 1);
+      dst[j] = i * 1024;
+      if (i < BM / 16) {
+        src[j] = A + (int64_t)min(m0 + i * 16 + lrow, M - 1) * lda + lchunk * 8;
+      } else {
+        src[j] = W + (int64_t)min(n0 + (i - BM / 16) * 16 + lrow, N - 1) * ldw + lchunk * 8;
       }
     }
   }
-  __syncthreads();
-  // Phase 2: 8 consecutive columns per lane, the rest of the epilogue, 16-byte stores.
-  constexpr int CPR = BN / 8;
-  for (int c = threadIdx.x; c < BM * CPR; c += NW * 64) {
-    const int rl = c / CPR, cl = (c - rl * CPR) * 8;
-    const int row = m0 + rl, col = n0 + cl;
-    if (row >= M || col >= N) continue;
-    float v[8];
-    unpack8(*reinterpret_cast<const uint4*>(ct + rl * LDT + cl), v);
-    if (EPI != OUDJAT_EPI_BIAS) {
+  const int KT = K / kBK3;
+  auto issue = [&](int stage, int kt) __attribute__((always_inline)) {
+    unsigned char* base = smem + stage * STAGE;
+    const int k0 = kt * kBK3;
 #pragma unroll
-      for (int e = 0; e < 8; ++e) v[e] = epilogue_post<EPI>(v[e], row, col + e, ea);
+    for (int j = 0; j < NLM; ++j)
+      if (j < nl)
+        __builtin_amdgcn_global_load_lds((const void*)(src[j] + k0), (lds_ptr_t)(base + dst[j]), 16, 0, 0);
+  };
+
+  f32x16_t acc[FM][FN];
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) acc[i][j][v] = 0.0f;
+
+  // Fragment offsets: lane l reads row (l % 32) of each 32-row block at K chunk 2 * ks + l / 32.
+  const int sw = (lane >> 2) & 3;
+  const int a_lane = (wm0 + (lane & 31)) * 64;
+  const int b_lane = BM * 64 + (wn0 + (lane & 31)) * 64;
+  const int co0 = ((0 + (lane >> 5)) ^ sw) << 4;
+  const int co1 = ((2 + (lane >> 5)) ^ sw) << 4;
+
+  // Fragments of one K tile: [ks][block] for A and B, read one tile ahead of their MFMAs.
+  struct Frags {
+    bf16x8_t a[2][FM], b[2][FN];
+  };
+  auto read_frags = [&](Frags& f, int kt) __attribute__((always_inline)) {
+    const unsigned char* st = smem + (kt & (kStages - 1)) * STAGE;
+#pragma unroll
+    for (int i = 0; i < FM; ++i) f.a[0][i] = *reinterpret_cast<const bf16x8_t*>(st + a_lane + i * 2048 + co0);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) f.b[0][j] = *reinterpret_cast<const bf16x8_t*>(st + b_lane + j * 2048 + co0);
+#pragma unroll
+    for (int i = 0; i < FM; ++i) f.a[1][i] = *reinterpret_cast<const bf16x8_t*>(st + a_lane + i * 2048 + co1);
+#pragma unroll
+    for (int j = 0; j < FN; ++j) f.b[1][j] = *reinterpret_cast<const bf16x8_t*>(st + b_lane + j * 2048 + co1);
+  };
+  // Row blocks entirely below M (the last tile row of a ragged M) skip their MFMAs.
+  const int rows_left = M - m0 - wm0;
+  auto mfmas = [&](const Frags& f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks)
+#pragma unroll
+      for (int i = 0; i < FM; ++i)
+        if (i * 32 < rows_left) {
+#pragma unroll
+          for (int j = 0; j < FN; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[ks][j], f.a[ks][i], acc[i][j], 0, 0, 0);
+        }
+  };
+  // Wait until at most `n_after` K tiles of this wave's loads are still in flight.
+  auto wait_tiles = [&](int n_after) __attribute__((always_inline)) {
+    if constexpr (NI % NW == 0) {
+      if (n_after >= 3) wait_vmcnt<3 * (NI / NW)>();
+      else if (n_after == 2) wait_vmcnt<2 * (NI / NW)>();
+      else if (n_after == 1) wait_vmcnt<NI / NW>();
+      else wait_vmcnt<0>();
+    } else {
+      wait_vmcnt_rt(n_after * nl);
     }
-    *reinterpret_cast<uint4*>(C + (int64_t)row * ldc + col) = pack8(v);
+  };
+
+  // Pipeline: at the top of step kt the stages hold tiles kt+1 .. kt+3 (landed or in flight) and
+  // tile kt's fragments are already in registers, so tile kt's stage is free for tile kt+4.
+  //   wait for tile kt+1; barrier; issue tile kt+4; read tile kt+1's fragments; MFMAs of tile kt.
+#pragma unroll
+  for (int s = 0; s < kStages; ++s)
+    if (s < KT) issue(s, s);
+  wait_tiles(min(KT - 1, kStages - 1));
+  block_barrier();
+  Frags f0, f1;
+  read_frags(f0, 0);
+
+  auto step = [&](int kt, Frags& cur, Frags& nxt) __attribute__((always_inline)) {
+    if (kt + 1 < KT) {
+      wait_tiles(min(KT - 2 - kt, kStages - 2));
+      block_barrier();
+      if (kt + kStages < KT) issue(kt & (kStages - 1), kt + kStages);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(nxt, kt + 1);
+    }
+    mfmas(cur);
+    __builtin_amdgcn_sched_barrier(0);
+  };
+  int kt = 0;
+  for (; kt + 1 < KT; kt += 2) {
+    step(kt, f0, f1);
+    step(kt + 1, f1, f0);
   }
+  if (kt < KT) step(kt, f0, f1);
+
+  block_barrier();
+  store_tile<BM, BN, FM, FN, NW, EPI>(acc, smem, reinterpret_cast<const uint16_t*>(smem + kLutOff), wm0, wn0, m0, n0,
+                                      M, ea, C, ldc);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -385,7 +687,7 @@ typedef void (*gemm_fn)(const uint16_t*, int, int, int64_t, const uint16_t*, int
                         int64_t, int);
 
 struct GemmCfg {
-  int bm, bn, wgm, wgn, pf;
+  int bm, bn, wgm, wgn, pf;  // pf: register prefetch depth; 0 = direct-to-LDS; -1 = pipelined
   gemm_fn fn[5];
 };
 
@@ -400,6 +702,12 @@ struct GemmCfg {
    {gemm_bf16_dma_kernel<BM, BN, WGM, WGN, 0>, gemm_bf16_dma_kernel<BM, BN, WGM, WGN, 1>,                 \
     gemm_bf16_dma_kernel<BM, BN, WGM, WGN, 2>, gemm_bf16_dma_kernel<BM, BN, WGM, WGN, 3>,                 \
     gemm_bf16_dma_kernel<BM, BN, WGM, WGN, 4>}}
+
+#define OUDJAT_GEMM_PIPE_CFG(BM, BN, WGM, WGN)                                                            \
+  {BM, BN, WGM, WGN, -1,                                                                                 \
+   {gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 0>, gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 1>,               \
+    gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 2>, gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 3>,               \
+    gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 4>}}
 
 static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_CFG(128, 128, 2, 2, 1),  // 0
@@ -417,23 +725,67 @@ static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_DMA_CFG(128, 256, 2, 2),  // 12
     OUDJAT_GEMM_DMA_CFG(256, 256, 4, 2),  // 13
     OUDJAT_GEMM_DMA_CFG(256, 256, 2, 4),  // 14
+    OUDJAT_GEMM_PIPE_CFG(256, 256, 2, 4),  // 15
+    OUDJAT_GEMM_PIPE_CFG(256, 256, 2, 2),  // 16
+    OUDJAT_GEMM_PIPE_CFG(288, 256, 3, 4),  // 17
+    OUDJAT_GEMM_PIPE_CFG(256, 128, 2, 2),  // 18
+    OUDJAT_GEMM_PIPE_CFG(128, 128, 2, 2),  // 19
 };
 static constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
+
+// Host side of the GELU table: entry s * kGeluSpan + d holds bf16(gelu(v)) for the bf16 input v
+// with sign s and magnitude bits kGeluLo + d, computed as 0.5 v erfc(-v / sqrt 2) in double,
+// rounded to fp32 and then to bf16 (nearest even). Copied to each device once, before the first
+// GELU launch on it.
+static uint16_t host_f32_to_bf16(float f) {
+  uint32_t u;
+  memcpy(&u, &f, 4);
+  u += 0x7fffu + ((u >> 16) & 1u);
+  return (uint16_t)(u >> 16);
+}
+
+static int ensure_gelu_table() {
+  static std::once_flag flags[64];
+  static int status[64];
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "linear_bf16: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return set_error(OUDJAT_ERR_HIP, "linear_bf16: device index %d out of range", dev);
+  std::call_once(flags[dev], [&] {
+    static uint16_t table[kGeluLut];
+    for (uint32_t sgn = 0; sgn < 2; ++sgn)
+      for (uint32_t d = 0; d < kGeluSpan; ++d) {
+        const uint32_t bits = ((sgn << 15) | (kGeluLo + d)) << 16;
+        float v;
+        memcpy(&v, &bits, 4);
+        const double g = 0.5 * (double)v * erfc(-(double)v / sqrt(2.0));
+        table[sgn * kGeluSpan + d] = host_f32_to_bf16((float)g);
+      }
+    hipError_t ce = hipMemcpyToSymbol(HIP_SYMBOL(g_gelu_lut), table, sizeof(table), 0, hipMemcpyHostToDevice);
+    status[dev] = ce == hipSuccess ? OUDJAT_OK
+                                   : set_error(OUDJAT_ERR_HIP, "linear_bf16: GELU table upload: %s", hipGetErrorString(ce));
+  });
+  return status[dev];
+}
 
 static int env_int(const char* name, int dflt) {
   const char* e = getenv(name);
   return e ? atoi(e) : dflt;
 }
 
-static int choose_cfg(int64_t M, int64_t N, int64_t K) {
+// aligned_io: C, resid 16-byte aligned with ldc, ldr % 8 == 0 and bias 8-byte aligned, which the
+// vector epilogues need; otherwise the register-staged kernel with 2-byte stores runs.
+static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   static const int forced = env_int("OUDJAT_GEMM_CFG", -1);
-  if (forced >= 0 && forced < kNumCfgs && N % kCfgs[forced].bn == 0) return forced;
-  if (N % 128 != 0) return 8;
   (void)K;
-  // 256x256 tiles (8 waves, direct-to-LDS) when their grid nearly fills the 256 CUs in one round;
-  // otherwise 128x128 direct-to-LDS tiles (two workgroups per CU, finer-grained load balance).
+  if (!aligned_io) return 8;
+  if (forced >= 0 && forced < kNumCfgs && N % kCfgs[forced].bn == 0) return forced;
+  // 256 x 256 pipelined tiles when their grid fills between half and all of the CUs in one round;
+  // 128 x 128 direct-to-LDS tiles otherwise (two workgroups per CU balance a ragged second round
+  // better); the register-staged kernel for N % 128 != 0.
+  if (N % 128 != 0) return 8;
   const int64_t tiles256 = cdiv(M, 256) * cdiv(N, 256);
-  if (N % 256 == 0 && tiles256 >= 192 && tiles256 <= 256) return 14;
+  if (N % 256 == 0 && tiles256 >= 128 && tiles256 <= 256) return 15;
   return 11;
 }
 
@@ -462,12 +814,19 @@ extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64
                  OUDJAT_ERR_UNSUPPORTED_LAYOUT, "linear_bf16: operands must be 16-byte aligned, ld %% 8 == 0");
   OUDJAT_REQUIRE(M < ((int64_t)1 << 31) && N < ((int64_t)1 << 31) && K < ((int64_t)1 << 31), OUDJAT_ERR_TOO_LARGE,
                  "linear_bf16: dimensions must fit in int32");
-  const GemmCfg& cfg = kCfgs[choose_cfg(M, N, K)];
+  const bool aligned_io = aligned(C, 16) && ldc % 8 == 0 && (!bias || aligned(bias, 8)) &&
+                          (!gamma || aligned(gamma, 16)) && (!resid || (aligned(resid, 16) && ldr % 8 == 0));
+  const GemmCfg& cfg = kCfgs[choose_cfg(M, N, K, aligned_io)];
   const int64_t tiles = cdiv(M, cfg.bm) * cdiv(N, cfg.bn);
   OUDJAT_REQUIRE(tiles < ((int64_t)1 << 31), OUDJAT_ERR_TOO_LARGE, "linear_bf16: too many tiles");
   // K stages, or (direct-to-LDS kernels) the bf16 output tile of the epilogue if that is larger.
-  size_t lds = (size_t)2 * (cfg.bm + cfg.bn) * 128;
-  if (cfg.pf == 0) lds = lds > (size_t)cfg.bm * (cfg.bn + 8) * 2 ? lds : (size_t)cfg.bm * (cfg.bn + 8) * 2;
+  size_t lds = cfg.pf < 0 ? (size_t)kStages * (cfg.bm + cfg.bn) * 64 : (size_t)2 * (cfg.bm + cfg.bn) * 128;
+  if (cfg.pf <= 0) lds = lds > (size_t)cfg.bm * (cfg.bn + 8) * 2 ? lds : (size_t)cfg.bm * (cfg.bn + 8) * 2;
+  if (cfg.pf <= 0 && epi == OUDJAT_EPI_BIAS_GELU) lds += kGeluLut * sizeof(uint16_t);
+  if (epi == OUDJAT_EPI_BIAS_GELU) {
+    const int st = ensure_gelu_table();
+    if (st != OUDJAT_OK) return st;
+  }
   const gemm_fn fn = cfg.fn[epi];
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);

@@ -139,6 +139,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline sampling (0 = skip)")
     ap.add_argument("--cache", default="approx", choices=("approx", "random"),
                     help="fill the K/V + residual caches with the approximate pass (default) or random values")
+    ap.add_argument("--calib-copy-mib", type=int, default=0,
+                    help="before the timed steps, copy this many MiB device-to-device once (a plain copy of known "
+                         "size that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
     args = ap.parse_args()
 
     if args.gpus != 1 or int(os.environ.get("WORLD_SIZE", "1")) > 1:
@@ -209,6 +212,16 @@ def main():
     with torch.no_grad():
         for _ in range(args.warmup):
             step()
+        if args.calib_copy_mib > 0:
+            # A plain copy of known size through the library's own row-copy kernel (16-byte lanes,
+            # like the GEMM's operand loads): N MiB of 4 KiB rows. A 512 MiB fill in between evicts
+            # the source from L2 and the MALL so every source byte comes from HBM.
+            rows = (args.calib_copy_mib << 20) // 4096
+            src = torch.ones(1, rows, 2048, device=dev, dtype=torch.bfloat16)
+            torch.zeros(128 << 20, device=dev, dtype=torch.float32)
+            K.gather_rows(src, torch.zeros(rows, device=dev, dtype=torch.long), torch.arange(rows, device=dev))
+            torch.cuda.synchronize()
+            del src
         torch.cuda.synchronize()
         roctx = _roctx()
         if roctx is not None:

@@ -220,8 +220,10 @@ class _F64:
 
     @staticmethod
     def gelu(x):
+        """Exact-erf GELU, 0.5 x (1 + erf(x / sqrt 2)), evaluated as 0.5 x erfc(-x / sqrt 2) so the
+        negative tail keeps full relative accuracy (1 + erf cancels there)."""
         xf = _f(x)
-        return _rb(0.5 * xf * (1.0 + torch.erf(xf / math.sqrt(2.0))))
+        return _rb(0.5 * xf * torch.special.erfc(-xf / math.sqrt(2.0)))
 
     @staticmethod
     def silu_mul(x1, x2):

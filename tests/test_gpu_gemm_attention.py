@@ -56,6 +56,18 @@ def test_linear_bias(dev, M, N, Kd):
     _check_gemm(dev, got, x, w, b, f"linear {M}x{N}x{Kd}")
 
 
+def test_linear_split_k_repeatable(dev):
+    """N = 1024 GEMMs run split over K (68 tiles of 256 x 256 on 256 CUs); the partial tiles are
+    summed in split order, so repeated launches are bit-identical and the arrival counters reset."""
+    for Kd in (1024, 4096):
+        x, w, b = _rand((4176, Kd), 30), _rand((1024, Kd), 31, 0.02), _rand((1024,), 32, 0.1)
+        xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+        outs = [K.linear(xd, wd, bd) for _ in range(3)]
+        _check_gemm(dev, outs[0], x, w, b, f"split-K {Kd}")
+        for o in outs[1:]:
+            assert_bits_equal(o, outs[0], "repeat")
+
+
 def test_linear_no_bias_and_strided_input(dev):
     x, w = _rand((300, 256), 4), _rand((128, 192), 5, 0.02)
     got = K.linear(x.to(dev)[:, 32:224], w.to(dev), None)

@@ -43,8 +43,15 @@ def test_layernorm_gelu_sdpa_match_torch_fp64():
     ref = _rb(F.layer_norm(x.double(), (384,), w.double(), b.double(), 1e-5))
     assert _bits_equal_frac(ln, ref) >= 0.999
     assert (ln.float() - ref.float()).abs().max() <= 2.0 ** -6
-    ge = OM._F64.gelu(x)
-    assert _bits_equal_frac(ge, _rb(F.gelu(x.double()))) >= 0.999
+    # torch's fp64 GELU evaluates 1 + erf(x / sqrt 2), which cancels for x < -5; compare above that
+    xm = x[x.float() > -5.0]
+    ge = OM._F64.gelu(xm)
+    assert _bits_equal_frac(ge, _rb(F.gelu(xm.double()))) >= 0.999
+    # deep negative tail: x Phi(x) with Phi from the normal survival function, no cancellation
+    xt = torch.tensor([-6.0, -8.0, -10.0, -12.0], dtype=torch.bfloat16)
+    want = _rb(xt.double() * 0.5 * torch.special.erfc(-xt.double() / math.sqrt(2.0)))
+    assert torch.equal(bits_t(OM._F64.gelu(xt)), bits_t(want))
+    assert float(OM._F64.gelu(torch.tensor([-10.0], dtype=torch.bfloat16)).float()) < 0  # not flushed to -0
     q = torch.randn(2, 3, 7, 64, generator=g).to(torch.bfloat16)
     k = torch.randn(2, 3, 11, 64, generator=g).to(torch.bfloat16)
     v = torch.randn(2, 3, 11, 64, generator=g).to(torch.bfloat16)
