@@ -56,6 +56,29 @@ __device__ __forceinline__ uint4 pack8(const float* f) {
 
 __device__ __forceinline__ bf16x8_t as_bf16x8(const uint4& v) { return __builtin_bit_cast(bf16x8_t, v); }
 
+// Rotate-half RoPE on one 8-wide chunk of the left half and its partner chunk of the right half.
+// fp32 math with every product and sum rounded separately, matching an eager
+// (x * cos) + (rotate_half(x) * sin) evaluated in fp32. Contraction is switched off for this scope
+// (plain operators: the __f*_rn helpers are themselves contractable after inlining).
+__device__ __forceinline__ void rope8(float* l, float* r, const float* cl, const float* cr, const float* sl,
+                                      const float* sr) {
+#pragma clang fp contract(off)
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float nl = l[e] * cl[e] - r[e] * sl[e];
+    const float nr = r[e] * cr[e] + l[e] * sr[e];
+    l[e] = nl;
+    r[e] = nr;
+  }
+}
+
+__device__ __forceinline__ void load8f(const float* p, float* f) {
+  const float4 a = reinterpret_cast<const float4*>(p)[0];
+  const float4 b = reinterpret_cast<const float4*>(p)[1];
+  f[0] = a.x; f[1] = a.y; f[2] = a.z; f[3] = a.w;
+  f[4] = b.x; f[5] = b.y; f[6] = b.z; f[7] = b.w;
+}
+
 // Wavefront (64-lane) reductions.
 __device__ __forceinline__ float wave_sum(float v) {
 #pragma unroll

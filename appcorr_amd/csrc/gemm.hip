@@ -38,11 +38,30 @@ namespace oudjat {
 static constexpr int kBK = 64;
 static constexpr int kNumXcd = 8;
 
+// Epilogue kind beyond the public ones: QKV projection followed by RoPE on q and k of patch rows,
+// q written packed and k, v written into the K/V cache rows (used by oudjat_linear_qkv_rope_kv).
+static constexpr int kEpiQkv = 5;
+
+struct QkvArgs {
+  int H, Dh;
+  const float* sin_t;
+  const float* cos_t;
+  int64_t tst;
+  const uint8_t* pm;
+  const int64_t* ridx;
+  const int64_t* bi;
+  const int64_t* ti;
+  uint16_t* kv;
+  int64_t kvb, kvn;
+  uint16_t* q_out;
+};
+
 struct EpiArgs {
   const uint16_t* bias;
   const uint16_t* gamma;
   const uint16_t* resid;
   int64_t ldr;
+  QkvArgs qkv;
 };
 
 // Two fp32 -> packed bf16 pair (low half = a) with the hardware round-to-nearest-even convert.
@@ -303,6 +322,48 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FM][FN], unsign
     }
   }
   __syncthreads();
+  if constexpr (EPI == kEpiQkv) {
+    // One work item = (row, head, 8-wide chunk of the left half) with its partner chunk Dh/2 to the
+    // right: RoPE on q and k of patch rows, then q packed or k / v into the cache row. A tile covers
+    // whole heads of one of q, k, v (H * Dh % BN == 0, Dh | BN).
+    const QkvArgs& qa = ea.qkv;
+    const int HD = qa.H * qa.Dh, half = qa.Dh >> 1;
+    const int which = n0 / HD;
+    const int hc0 = n0 - which * HD;
+    const int lg_cph = __builtin_ctz((unsigned)(half >> 3));  // chunk pairs per head = Dh / 16
+    constexpr int PPR = BN / 16;                               // chunk pairs per tile row
+    constexpr int ITEMS = BM * PPR / (NW * 64);
+    static_assert(ITEMS * NW * 64 == BM * PPR, "items must split evenly over the threads");
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int p = threadIdx.x + it * NW * 64;
+      const int rl = p / PPR, pr = p - rl * PPR;
+      const int row = m0 + rl;
+      if (row >= M) continue;
+      const int c0 = ((pr >> lg_cph) << (lg_cph + 4)) + ((pr & ((1 << lg_cph) - 1)) << 3);  // head * Dh + 8 c
+      uint4 lo = *reinterpret_cast<const uint4*>(ct + rl * LDT + c0);
+      uint4 hi = *reinterpret_cast<const uint4*>(ct + rl * LDT + c0 + half);
+      if (which < 2 && qa.pm[row]) {
+        float l[8], rr[8], cl8[8], cr8[8], sl8[8], sr8[8];
+        unpack8(lo, l);
+        unpack8(hi, rr);
+        const int64_t tr = qa.ridx[row] * qa.tst + (c0 & (qa.Dh - 1));
+        load8f(qa.cos_t + tr, cl8);
+        load8f(qa.cos_t + tr + half, cr8);
+        load8f(qa.sin_t + tr, sl8);
+        load8f(qa.sin_t + tr + half, sr8);
+        rope8(l, rr, cl8, cr8, sl8, sr8);
+        lo = pack8(l);
+        hi = pack8(rr);
+      }
+      uint16_t* dst = (which == 0 ? qa.q_out + (int64_t)row * HD
+                                  : qa.kv + qa.bi[row] * qa.kvb + qa.ti[row] * qa.kvn + (which - 1) * HD) +
+                      hc0 + c0;
+      *reinterpret_cast<uint4*>(dst) = lo;
+      *reinterpret_cast<uint4*>(dst + half) = hi;
+    }
+    return;
+  }
   constexpr int CPR = BN / 8;
   for (int c = threadIdx.x; c < BM * CPR; c += NW * 64) {
     const int rl = c / CPR, cl = (c - rl * CPR) * 8;
@@ -314,7 +375,7 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FM][FN], unsign
 #pragma unroll
       for (int e = 0; e < 4; ++e)
         w[e] = gelu_bf16_bits(w[e] & 0xffffu, lut) | (gelu_bf16_bits(w[e] >> 16, lut) << 16);
-    } else if constexpr (EPI != OUDJAT_EPI_BIAS) {
+    } else if constexpr (EPI != OUDJAT_EPI_BIAS && EPI != kEpiQkv) {
       // 16-byte loads of the per-column gamma and the residual / gate row segment.
       float v[8], g[8], r[8];
       unpack8(o, v);
@@ -688,7 +749,7 @@ typedef void (*gemm_fn)(const uint16_t*, int, int, int64_t, const uint16_t*, int
 
 struct GemmCfg {
   int bm, bn, wgm, wgn, pf;  // pf: register prefetch depth; 0 = direct-to-LDS; -1 = pipelined
-  gemm_fn fn[5];
+  gemm_fn fn[6];             // by epilogue; fn[kEpiQkv] only for the direct-to-LDS families
 };
 
 #define OUDJAT_GEMM_CFG(BM, BN, WGM, WGN, PF)                                                             \
@@ -701,13 +762,13 @@ struct GemmCfg {
   {BM, BN, WGM, WGN, 0,                                                                                  \
    {gemm_bf16_dma_kernel<BM, BN, WGM, WGN, 0>, gemm_bf16_dma_kernel<BM, BN, WGM, WGN, 1>,                 \
     gemm_bf16_dma_kernel<BM, BN, WGM, WGN, 2>, gemm_bf16_dma_kernel<BM, BN, WGM, WGN, 3>,                 \
-    gemm_bf16_dma_kernel<BM, BN, WGM, WGN, 4>}}
+    gemm_bf16_dma_kernel<BM, BN, WGM, WGN, 4>, gemm_bf16_dma_kernel<BM, BN, WGM, WGN, kEpiQkv>}}
 
 #define OUDJAT_GEMM_PIPE_CFG(BM, BN, WGM, WGN)                                                            \
   {BM, BN, WGM, WGN, -1,                                                                                 \
    {gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 0>, gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 1>,               \
     gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 2>, gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 3>,               \
-    gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 4>}}
+    gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 4>, gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, kEpiQkv>}}
 
 static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_CFG(128, 128, 2, 2, 1),  // 0
@@ -789,6 +850,35 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   return 11;
 }
 
+
+// Launches configuration `ci` with epilogue `epi` (arguments already validated).
+static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W, int64_t N,
+                       int64_t ldw, int epi, const EpiArgs& ea, uint16_t* C, int64_t ldc, hipStream_t stream,
+                       const char* what) {
+  const GemmCfg& cfg = kCfgs[ci];
+  const int64_t tiles = cdiv(M, cfg.bm) * cdiv(N, cfg.bn);
+  OUDJAT_REQUIRE(tiles < ((int64_t)1 << 31), OUDJAT_ERR_TOO_LARGE, "%s: too many tiles", what);
+  // K stages, or (direct-to-LDS kernels) the bf16 output tile of the epilogue if that is larger.
+  size_t lds = cfg.pf < 0 ? (size_t)kStages * (cfg.bm + cfg.bn) * 64 : (size_t)2 * (cfg.bm + cfg.bn) * 128;
+  if (cfg.pf <= 0) lds = lds > (size_t)cfg.bm * (cfg.bn + 8) * 2 ? lds : (size_t)cfg.bm * (cfg.bn + 8) * 2;
+  if (cfg.pf <= 0 && epi == OUDJAT_EPI_BIAS_GELU) lds += kGeluLut * sizeof(uint16_t);
+  if (epi == OUDJAT_EPI_BIAS_GELU) {
+    const int st = ensure_gelu_table();
+    if (st != OUDJAT_OK) return st;
+  }
+  const gemm_fn fn = cfg.fn[epi];
+  OUDJAT_REQUIRE(fn != nullptr, OUDJAT_ERR_UNSUPPORTED_SHAPE, "%s: no kernel for this epilogue", what);
+  if (lds > 64 * 1024) {
+    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "%s: hipFuncSetAttribute: %s", what, hipGetErrorString(e));
+  }
+  const int threads = cfg.wgm * cfg.wgn * 64;
+  static const int group_m = env_int("OUDJAT_GEMM_GROUP_M", 8);
+  hipLaunchKernelGGL(fn, dim3((unsigned)tiles), dim3(threads), lds, stream, A, (int)M, (int)K, lda, W, (int)N, ldw, ea,
+                     C, ldc, group_m > 0 ? group_m : 1);
+  return check_launch(what);
+}
+
 }  // namespace oudjat
 
 using namespace oudjat;
@@ -816,26 +906,45 @@ extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64
                  "linear_bf16: dimensions must fit in int32");
   const bool aligned_io = aligned(C, 16) && ldc % 8 == 0 && (!bias || aligned(bias, 8)) &&
                           (!gamma || aligned(gamma, 16)) && (!resid || (aligned(resid, 16) && ldr % 8 == 0));
-  const GemmCfg& cfg = kCfgs[choose_cfg(M, N, K, aligned_io)];
-  const int64_t tiles = cdiv(M, cfg.bm) * cdiv(N, cfg.bn);
-  OUDJAT_REQUIRE(tiles < ((int64_t)1 << 31), OUDJAT_ERR_TOO_LARGE, "linear_bf16: too many tiles");
-  // K stages, or (direct-to-LDS kernels) the bf16 output tile of the epilogue if that is larger.
-  size_t lds = cfg.pf < 0 ? (size_t)kStages * (cfg.bm + cfg.bn) * 64 : (size_t)2 * (cfg.bm + cfg.bn) * 128;
-  if (cfg.pf <= 0) lds = lds > (size_t)cfg.bm * (cfg.bn + 8) * 2 ? lds : (size_t)cfg.bm * (cfg.bn + 8) * 2;
-  if (cfg.pf <= 0 && epi == OUDJAT_EPI_BIAS_GELU) lds += kGeluLut * sizeof(uint16_t);
-  if (epi == OUDJAT_EPI_BIAS_GELU) {
-    const int st = ensure_gelu_table();
-    if (st != OUDJAT_OK) return st;
-  }
-  const gemm_fn fn = cfg.fn[epi];
-  if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "linear_bf16: hipFuncSetAttribute: %s", hipGetErrorString(e));
-  }
-  EpiArgs ea{bias, gamma, resid, ldr};
-  const int threads = cfg.wgm * cfg.wgn * 64;
-  static const int group_m = env_int("OUDJAT_GEMM_GROUP_M", 8);
-  hipLaunchKernelGGL(fn, dim3((unsigned)tiles), dim3(threads), lds, as_stream(stream), A, (int)M, (int)K, lda, W,
-                     (int)N, ldw, ea, C, ldc, group_m > 0 ? group_m : 1);
-  return check_launch("linear_bf16");
+  EpiArgs ea{};
+  ea.bias = bias;
+  ea.gamma = gamma;
+  ea.resid = resid;
+  ea.ldr = ldr;
+  return launch_gemm(choose_cfg(M, N, K, aligned_io), A, M, K, lda, W, N, ldw, epi, ea, C, ldc, as_stream(stream),
+                     "linear_bf16");
+}
+
+extern "C" int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                                         int64_t ldw, const uint16_t* bias, int64_t H, int64_t Dh,
+                                         const float* sin_table, const float* cos_table, int64_t table_stride,
+                                         const uint8_t* patch_mask, const int64_t* rope_idx,
+                                         const int64_t* batch_idx, const int64_t* token_idx, uint16_t* kv,
+                                         int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
+                                         oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(M >= 0 && K >= 0 && H > 0 && Dh > 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_qkv_rope_kv: bad size");
+  if (M == 0) return OUDJAT_OK;
+  const int64_t N = 3 * H * Dh;
+  OUDJAT_REQUIRE(A && W && kv && q_out && sin_table && cos_table && patch_mask && rope_idx && batch_idx && token_idx,
+                 OUDJAT_ERR_INVALID_ARGUMENT, "linear_qkv_rope_kv: null pointer");
+  OUDJAT_REQUIRE(K > 0 && K % kBK == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE,
+                 "linear_qkv_rope_kv: K=%lld must be a multiple of %d", (long long)K, kBK);
+  OUDJAT_REQUIRE(Dh % 16 == 0 && 128 % Dh == 0 && (H * Dh) % 128 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE,
+                 "linear_qkv_rope_kv: need Dh in {16, 32, 64, 128} and H*Dh %% 128 == 0 (H=%lld, Dh=%lld)",
+                 (long long)H, (long long)Dh);
+  OUDJAT_REQUIRE(lda % 8 == 0 && ldw % 8 == 0 && lda >= K && ldw >= K && aligned(A, 16) && aligned(W, 16) &&
+                     (!bias || aligned(bias, 8)) && aligned(kv, 16) && aligned(q_out, 16) && kv_stride_b % 8 == 0 &&
+                     kv_stride_n % 8 == 0 && table_stride % 4 == 0 && aligned(sin_table, 16) && aligned(cos_table, 16),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT,
+                 "linear_qkv_rope_kv: 16-byte aligned operands and rows, strides %% 8 == 0, tables 16-byte rows");
+  OUDJAT_REQUIRE(M < ((int64_t)1 << 31) && N < ((int64_t)1 << 31) && K < ((int64_t)1 << 31), OUDJAT_ERR_TOO_LARGE,
+                 "linear_qkv_rope_kv: dimensions must fit in int32");
+  EpiArgs ea{};
+  ea.bias = bias;
+  ea.qkv = QkvArgs{(int)H, (int)Dh, sin_table, cos_table, table_stride, patch_mask, rope_idx, batch_idx, token_idx,
+                   kv, kv_stride_b, kv_stride_n, q_out};
+  // Tiles must cover whole heads of one of q, k, v: Dh | BN and BN | H * Dh.
+  int ci = choose_cfg(M, N, K, true);
+  if (kCfgs[ci].pf > 0 || kCfgs[ci].bn % Dh != 0 || (H * Dh) % kCfgs[ci].bn != 0) ci = 11;  // 128 x 128 direct-to-LDS
+  return launch_gemm(ci, A, M, K, lda, W, N, ldw, kEpiQkv, ea, nullptr, 0, as_stream(stream), "linear_qkv_rope_kv");
 }

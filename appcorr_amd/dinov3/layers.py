@@ -167,10 +167,14 @@ class SelfAttention(nn.Module):
         if M % B != 0:
             raise ValueError(f"packed rows {M} do not split evenly over {B} images")
         T = M // B
-        qkv = K.linear(xn, self.qkv.weight, self.qkv_bias())
         q = torch.empty((M, H, D), device=xn.device, dtype=torch.bfloat16)
-        K.qkv_rope_kv_scatter(qkv.view(M, 3, H, D), rope, qs.active_patch_mask, qs.active_rope_idx,
-                              qs.active_batch_idx, qs.active_token_idx, kv, q)
+        if K.qkv_fusable(H, D):
+            K.linear_qkv_rope_kv(xn, self.qkv.weight, self.qkv_bias(), rope, qs.active_patch_mask, qs.active_rope_idx,
+                                 qs.active_batch_idx, qs.active_token_idx, kv, q)
+        else:
+            qkv = K.linear(xn, self.qkv.weight, self.qkv_bias())
+            K.qkv_rope_kv_scatter(qkv.view(M, 3, H, D), rope, qs.active_patch_mask, qs.active_rope_idx,
+                                  qs.active_batch_idx, qs.active_token_idx, kv, q)
         attn = K.sparse_query_attention(q, kv, T, self.scale)
         return q, attn
 

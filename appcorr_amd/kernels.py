@@ -320,6 +320,36 @@ def qkv_rope_kv_scatter(qkv: torch.Tensor, rope, patch_mask: torch.Tensor, rope_
          _ptr(q_out), _stream(qkv))
 
 
+def qkv_fusable(H: int, Dh: int) -> bool:
+    """Shapes the fused QKV + RoPE + K/V-write GEMM supports (otherwise: linear, then qkv_rope_kv_scatter)."""
+    return Dh % 16 == 0 and 128 % Dh == 0 and (H * Dh) % 128 == 0
+
+
+def linear_qkv_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, rope,
+                       patch_mask: torch.Tensor, rope_idx: torch.Tensor, batch_idx: torch.Tensor,
+                       token_idx: torch.Tensor, kv_cache: torch.Tensor, q_out: torch.Tensor) -> None:
+    """One kernel for attention.py:415-454: qkv = x . weight^T + bias, RoPE on q and k of patch rows,
+    k and v written into kv_cache [B, N, 2, H, Dh] rows (b, t) in place, q written to q_out [M, H, Dh].
+    The qkv tensor itself is never materialised."""
+    sin, cos = rope
+    _require_cuda(x, weight, bias, patch_mask, rope_idx, batch_idx, token_idx, kv_cache, q_out, sin, cos)
+    M, Kd = x.shape
+    _require(x.dtype == weight.dtype == torch.bfloat16 and x.stride(1) == 1 and weight.stride(1) == 1,
+             "linear_qkv_rope_kv: bf16 operands with contiguous rows")
+    _require(kv_cache.dim() == 5 and kv_cache.shape[2] == 2 and trailing_is_packed(kv_cache, 2),
+             "linear_qkv_rope_kv: kv_cache must be [B, N, 2, H, Dh] with packed rows")
+    H, Dh = kv_cache.shape[3], kv_cache.shape[4]
+    _require(weight.shape == (3 * H * Dh, Kd), "linear_qkv_rope_kv: weight must be [3 H Dh, K]")
+    _require(q_out.is_contiguous() and q_out.shape == (M, H, Dh), "linear_qkv_rope_kv: q_out must be contiguous [M, H, Dh]")
+    _require(sin.dtype == cos.dtype == torch.float32 and sin.stride(1) == 1 and cos.stride() == sin.stride(),
+             "linear_qkv_rope_kv: fp32 RoPE tables with contiguous rows")
+    _launch("gemm0", x, "oudjat_linear_qkv_rope_kv", _ptr(x), M, Kd, x.stride(0), _ptr(weight), weight.stride(0),
+            _ptr(None if bias is None else bias.contiguous()), H, Dh, _ptr(sin), _ptr(cos), sin.stride(0),
+            _ptr(patch_mask), _ptr(_index(rope_idx, "rope_idx")), _ptr(_index(batch_idx, "batch_idx")),
+            _ptr(_index(token_idx, "token_idx")), _ptr(kv_cache), kv_cache.stride(0), kv_cache.stride(1), _ptr(q_out),
+            _stream(x))
+
+
 # ------------------------------------------------------------------------------------------------
 # GEMM and attention
 # ------------------------------------------------------------------------------------------------

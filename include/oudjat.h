@@ -168,6 +168,21 @@ int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64_t lda, con
                        const uint16_t* gamma, const uint16_t* resid, int64_t ldr, uint16_t* C,
                        int64_t ldc, oudjat_stream_t stream);
 
+/* Rows 6-9 fused into the QKV GEMM -- SelfAttention.correct_partial_token up to the attention call
+ * (appcorr/models/dinov3/layers/attention.py:415-454): qkv = A . W^T + bias for A [M, K] and
+ * W [3*H*Dh, K] (never materialised), then RoPE on q and k of patch rows (rotate-half, fp32, tables
+ * [*, Dh] fp32 with row stride table_stride), q written packed into q_out [M, H, Dh] and k, v into
+ * kv[b, t, 0|1, H, Dh] at b = batch_idx[m], t = token_idx[m] (strides in elements).
+ * Same arithmetic as oudjat_linear_bf16 (OUDJAT_EPI_BIAS) followed by oudjat_qkv_rope_kv_scatter.
+ * K % 64 == 0, Dh in {16, 32, 64, 128}, H*Dh % 128 == 0; 16-byte aligned operands and rows. */
+int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                              int64_t ldw, const uint16_t* bias, int64_t H, int64_t Dh,
+                              const float* sin_table, const float* cos_table, int64_t table_stride,
+                              const uint8_t* patch_mask, const int64_t* rope_idx,
+                              const int64_t* batch_idx, const int64_t* token_idx, uint16_t* kv,
+                              int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
+                              oudjat_stream_t stream);
+
 /* Row 10 -- sparse-query attention: for each image b, head h and query t < T,
  *   out[b*T + t, h*Dh:(h+1)*Dh] = softmax(q . K^T * scale) . V over ALL N cached keys, no mask.
  * q [B*T, H, Dh] packed (row stride q_row_stride); K = kv[b, n, 0, h, :], V = kv[b, n, 1, h, :]

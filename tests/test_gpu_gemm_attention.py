@@ -179,6 +179,34 @@ def test_qkv_rope_kv_scatter_bit_exact(dev, B, T, H, D):
     assert_bits_equal(kvd, kv_ref, "kv cache")
 
 
+@pytest.mark.parametrize("B,T,H,D,Kd", [(16, 261, 16, 64, 1024), (1, 103, 6, 64, 384), (2, 50, 32, 128, 512)])
+def test_linear_qkv_rope_kv_fused_equals_unfused(dev, B, T, H, D, Kd):
+    """The fused QKV GEMM (qkv never materialised) equals linear + qkv_rope_kv_scatter bit-for-bit:
+    the same GEMM kernel produces bf16(acc + bias), then the same fp32 RoPE. The unfused pair is
+    itself pinned to the oracle above."""
+    N = 1029
+    M = B * T
+    _, sin, cos, _, _, _ = _rope_inputs(1, H, D, 0)
+    rng = np.random.default_rng(B + H)
+    toks = np.stack([np.concatenate([np.arange(5), np.sort(rng.choice(np.arange(5, N), T - 5, replace=False))])
+                     for _ in range(B)])
+    tok = torch.from_numpy(toks.reshape(-1).astype(np.int64)).to(dev)
+    bi = torch.arange(B).repeat_interleave(T).to(dev)
+    pm, ri = tok >= 5, (tok - 5).clamp_min(0)
+    x = _rand((M, Kd), 40).to(dev)
+    w = _rand((3 * H * D, Kd), 41, 0.02).to(dev)
+    b = _rand((3 * H * D,), 42, 0.1).to(dev)
+    kv0 = _rand((B, N, 2, H, D), 43).to(dev)
+    rope = (sin.to(dev), cos.to(dev))
+    assert K.qkv_fusable(H, D)
+    kv_f, q_f = kv0.clone(), torch.empty((M, H, D), dtype=torch.bfloat16, device=dev)
+    K.linear_qkv_rope_kv(x, w, b, rope, pm, ri, bi, tok, kv_f, q_f)
+    kv_u, q_u = kv0.clone(), torch.empty((M, H, D), dtype=torch.bfloat16, device=dev)
+    K.qkv_rope_kv_scatter(K.linear(x, w, b).view(M, 3, H, D), rope, pm, ri, bi, tok, kv_u, q_u)
+    assert_bits_equal(q_f, q_u, "q packed")
+    assert_bits_equal(kv_f, kv_u, "kv cache")
+
+
 def _check_attention(got, qb, kv, scale, ref, what):
     """P is rounded to bf16 before P.V (relative error <= 2^-9 per weight), so
     |got - oracle| <= 2 ulp(oracle) + 2^-8 * sum_j p_j |v_j|   (the second term from the oracle with |V|);
