@@ -29,11 +29,12 @@ static constexpr int kMaxWaves64 = 10;   // Dh = 64: 3 waves per SIMD, <= 170 VG
 static constexpr int kMaxWaves128 = 8;   // Dh = 128: 2 waves per SIMD, <= 256 VGPRs
 static constexpr int kMinWaves = 4;
 
+typedef float f32x8_t __attribute__((ext_vector_type(8)));
+
+// Eight fp32 -> bf16 (RNE) as four packed converts.
 __device__ __forceinline__ bf16x8_t pack_bf16x8(const float* f) {
-  bf16x8_t r;
-#pragma unroll
-  for (int e = 0; e < 8; ++e) r[e] = (__bf16)f[e];
-  return r;
+  const f32x8_t v = {f[0], f[1], f[2], f[3], f[4], f[5], f[6], f[7]};
+  return __builtin_convertvector(v, bf16x8_t);
 }
 
 template <int DH>
@@ -126,18 +127,30 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
     const unsigned char* ks = smem + stage * STAGE;
     const unsigned char* vs = ks + KSTAGE;
     // S^T blocks: s[kb][v] = S^T[key kb*32 + 8(v/4) + 4g + v%4][query l32]
+    // The K fragments of a 32-key block (both blocks for Dh = 64) are read before its MFMAs so the
+    // reads overlap.
+    constexpr int KB_BATCH = DH == 64 ? 2 : 1;
     f32x16_t s[2];
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
+    for (int kb0 = 0; kb0 < 2; kb0 += KB_BATCH) {
+      bf16x8_t kf[KB_BATCH][QK_STEPS];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) s[kb][v] = 0.0f;
-      const int key = kb * 32 + l32;
+      for (int kb = 0; kb < KB_BATCH; ++kb) {
+        const int key = (kb0 + kb) * 32 + l32;
 #pragma unroll
-      for (int kstep = 0; kstep < QK_STEPS; ++kstep) {
-        const int ch = kstep * 2 + g;
-        const bf16x8_t kf =
-            as_bf16x8(*reinterpret_cast<const uint4*>(ks + key * KROWB + ((ch ^ (key & (CPR - 1))) << 4)));
-        s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf, qf[kstep], s[kb], 0, 0, 0);
+        for (int kstep = 0; kstep < QK_STEPS; ++kstep) {
+          const int ch = kstep * 2 + g;
+          kf[kb][kstep] =
+              as_bf16x8(*reinterpret_cast<const uint4*>(ks + key * KROWB + ((ch ^ (key & (CPR - 1))) << 4)));
+        }
+      }
+#pragma unroll
+      for (int kb = 0; kb < KB_BATCH; ++kb) {
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s[kb0 + kb][v] = 0.0f;
+#pragma unroll
+        for (int kstep = 0; kstep < QK_STEPS; ++kstep)
+          s[kb0 + kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kb][kstep], qf[kstep], s[kb0 + kb], 0, 0, 0);
       }
     }
     if ((t + 1) * kKeyTile > N) {
@@ -153,25 +166,31 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
 #pragma unroll
       for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    // exp2 is the bare v_exp_f32 (no subnormal range reduction: a probability below 2^-126 adds
+    // nothing to a sum that contains 1).
     const float m_new = fmaxf(m_i, mx);
-    const float alpha = exp2f((m_i - m_new) * scale_log2);
+    const float alpha = __builtin_amdgcn_exp2f((m_i - m_new) * scale_log2);
     const float mc = m_new * scale_log2;
     float rs = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
       for (int v = 0; v < 16; ++v) {
-        const float p = exp2f(fmaf(s[kb][v], scale_log2, -mc));
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][v], scale_log2, -mc));
         s[kb][v] = p;
         rs += p;
       }
     rs += __shfl_xor(rs, 32, 64);
     l_i = l_i * alpha + rs;
     m_i = m_new;
+    // Rescale the output only when some query's running max moved (alpha != 1 somewhere in the
+    // wave); once the maxima settle, later tiles skip it.
+    if (DH == 128 || __builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
-    for (int d = 0; d < OB; ++d)
+      for (int d = 0; d < OB; ++d)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) o[d][v] *= alpha;
+        for (int v = 0; v < 16; ++v) o[d][v] *= alpha;
+    }
     // P^T fragments: k-step j covers keys 16j + {4g..4g+3} and 16j + 8 + {4g..4g+3}.
     bf16x8_t pf[4];
 #pragma unroll
