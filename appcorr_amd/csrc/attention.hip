@@ -37,7 +37,10 @@ __device__ __forceinline__ bf16x8_t pack_bf16x8(const float* f) {
   return __builtin_convertvector(v, bf16x8_t);
 }
 
-template <int DH>
+// MINW: fewest waves a launch of this instance uses (sizes the per-thread share of a K/V tile);
+// DOUBLE_SET: prefetch K/V two tiles ahead through two register sets (needs the registers that only
+// the Dh = 64, >= 8-wave instance has to spare).
+template <int DH, int MINW, bool DOUBLE_SET>
 __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void sq_attention_kernel(
     const uint16_t* __restrict__ q, int64_t qrs, int T, const uint16_t* __restrict__ kv, int64_t kvb, int64_t kvn,
     int64_t kvkv, int64_t kvh, int N, float scale_log2, uint16_t* __restrict__ out, int64_t ors,
@@ -51,7 +54,7 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
   constexpr int QK_STEPS = DH / 16;
   constexpr int OB = DH / 32;
   constexpr int ITEMS = kKeyTile * CPR;       // 16-byte chunks per K (or V) tile
-  constexpr int IT = (ITEMS + kMinWaves * 64 - 1) / (kMinWaves * 64);
+  constexpr int IT = (ITEMS + MINW * 64 - 1) / (MINW * 64);
 
   extern __shared__ __align__(16) unsigned char smem[];
 
@@ -86,24 +89,28 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
   const uint16_t* vbase = kbase + kvkv;
   const int ntiles = (N + kKeyTile - 1) / kKeyTile;
 
-  u32x4_t kreg[IT], vreg[IT];
-  auto load_tile = [&](int t) __attribute__((always_inline)) {
+  // K/V tiles travel global -> registers -> LDS. Two register sets let the global loads of tile
+  // t + 2 be in flight while tile t is computed and tile t + 1 is written to LDS.
+  struct TileRegs {
+    u32x4_t k[IT], v[IT];
+  };
+  auto load_tile = [&](TileRegs& r, int t) __attribute__((always_inline)) {
 #pragma unroll
     for (int i = 0; i < IT; ++i) {
       const int c = tid + i * nthreads;
-      kreg[i] = u32x4_t{0, 0, 0, 0};
-      vreg[i] = u32x4_t{0, 0, 0, 0};
+      r.k[i] = u32x4_t{0, 0, 0, 0};
+      r.v[i] = u32x4_t{0, 0, 0, 0};
       if (c < ITEMS) {
         const int kk = c / CPR, kc = c - kk * CPR;       // K: row-major, 8 lanes per 128-byte row
         const int nk = t * kKeyTile + kk;
-        if (nk < N) kreg[i] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)nk * kvn + kc * 8);
+        if (nk < N) r.k[i] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)nk * kvn + kc * 8);
         const int vk = c % kKeyTile, vc = c / kKeyTile;  // V: 64 consecutive keys per wave, one chunk
         const int nv = t * kKeyTile + vk;
-        if (nv < N) vreg[i] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)nv * kvn + vc * 8);
+        if (nv < N) r.v[i] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)nv * kvn + vc * 8);
       }
     }
   };
-  auto store_tile = [&](int stage) __attribute__((always_inline)) {
+  auto store_tile = [&](const TileRegs& r, int stage) __attribute__((always_inline)) {
     unsigned char* ks = smem + stage * STAGE;
     unsigned char* vs = ks + KSTAGE;
 #pragma unroll
@@ -111,11 +118,11 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
       const int c = tid + i * nthreads;
       if (c < ITEMS) {
         const int kk = c / CPR, kc = c - kk * CPR;
-        *reinterpret_cast<u32x4_t*>(ks + kk * KROWB + ((kc ^ (kk & (CPR - 1))) << 4)) = kreg[i];
+        *reinterpret_cast<u32x4_t*>(ks + kk * KROWB + ((kc ^ (kk & (CPR - 1))) << 4)) = r.k[i];
         const int vk = c % kKeyTile, vc = c / kKeyTile;
 #pragma unroll
         for (int e = 0; e < 4; ++e) {
-          const uint32_t w = vreg[i][e];
+          const uint32_t w = r.v[i][e];
           *reinterpret_cast<uint16_t*>(vs + (vc * 8 + 2 * e) * VTROW + vk * 2) = (uint16_t)(w & 0xffffu);
           *reinterpret_cast<uint16_t*>(vs + (vc * 8 + 2 * e + 1) * VTROW + vk * 2) = (uint16_t)(w >> 16);
         }
@@ -213,14 +220,37 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
     }
   };
 
-  load_tile(0);
-  store_tile(0);
-  __syncthreads();
-  for (int t = 0; t < ntiles; ++t) {
-    if (t + 1 < ntiles) load_tile(t + 1);
-    if (active) compute(t & 1, t);
-    if (t + 1 < ntiles) store_tile((t + 1) & 1);
+  if constexpr (DOUBLE_SET) {
+    TileRegs ra, rb;
+    load_tile(ra, 0);
+    if (ntiles > 1) load_tile(rb, 1);
+    store_tile(ra, 0);
     __syncthreads();
+    // Iteration t: loads of tile t + 2 into the set that held tile t, compute tile t, store tile
+    // t + 1 (loaded one iteration earlier) into the other LDS stage.
+    auto step = [&](int t, TileRegs& cur_next, TileRegs& other) __attribute__((always_inline)) {
+      if (t + 2 < ntiles) load_tile(cur_next, t + 2);
+      if (active) compute(t & 1, t);
+      if (t + 1 < ntiles) store_tile(other, (t + 1) & 1);
+      __syncthreads();
+    };
+    int t = 0;
+    for (; t + 1 < ntiles; t += 2) {
+      step(t, ra, rb);
+      step(t + 1, rb, ra);
+    }
+    if (t < ntiles) step(t, ra, rb);
+  } else {
+    TileRegs r;
+    load_tile(r, 0);
+    store_tile(r, 0);
+    __syncthreads();
+    for (int t = 0; t < ntiles; ++t) {
+      if (t + 1 < ntiles) load_tile(r, t + 1);
+      if (active) compute(t & 1, t);
+      if (t + 1 < ntiles) store_tile(r, (t + 1) & 1);
+      __syncthreads();
+    }
   }
 
   // O^T[d][q]: lane l, register v of block db -> d = db*32 + 8(v/4) + 4g + v%4 (4 consecutive d per
@@ -270,17 +300,22 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
   if (w < kMinWaves) w = kMinWaves;
   dim3 grid((unsigned)n_wg, (unsigned)H, (unsigned)B);
   hipStream_t st = as_stream(stream);
-  const void* fn = Dh == 64 ? (const void*)sq_attention_kernel<64> : (const void*)sq_attention_kernel<128>;
+  const void* fn = Dh == 128 ? (const void*)sq_attention_kernel<128, kMinWaves, false>
+                  : w >= 8  ? (const void*)sq_attention_kernel<64, 8, true>
+                            : (const void*)sq_attention_kernel<64, kMinWaves, false>;
   const size_t lds = Dh == 64 ? 2 * (64 * 128 + 64 * 136) : 2 * (64 * 256 + 128 * 136);
   if (lds > 64 * 1024) {
     hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "sparse_query_attention: %s", hipGetErrorString(e));
   }
-  if (Dh == 64)
-    sq_attention_kernel<64><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N, scale_log2, out,
-                                                       ors, w);
+  if (Dh == 128)
+    sq_attention_kernel<128, kMinWaves, false><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,
+                                                                          (int)N, scale_log2, out, ors, w);
+  else if (w >= 8)
+    sq_attention_kernel<64, 8, true><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N,
+                                                                scale_log2, out, ors, w);
   else
-    sq_attention_kernel<128><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N, scale_log2,
-                                                        out, ors, w);
+    sq_attention_kernel<64, kMinWaves, false><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,
+                                                                         (int)N, scale_log2, out, ors, w);
   return check_launch("sparse_query_attention");
 }
