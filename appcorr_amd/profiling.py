@@ -1,0 +1,119 @@
+"""Summaries of rocprofv3 output for the correction pass (text in, text out; nothing here touches a GPU).
+
+    python -m appcorr_amd.profiling kernel-stats <run_kernel_stats.csv> <passes> <title> <command>
+        Markdown table of per-pass kernel time from a `rocprofv3 --kernel-trace --stats -f csv` run of
+        bench.py (kernels whose call count is a multiple of the pass count belong to the pass).
+
+    python -m appcorr_amd.profiling traffic <fetch_counter_collection.csv> <write_counter_collection.csv>
+            <kernel substring> <calibration kernel substring> <calibration bytes> <json out> <key> <command>
+        HBM traffic per launch of one kernel from two `rocprofv3 --pmc FETCH_SIZE` / `--pmc WRITE_SIZE`
+        runs. FETCH_SIZE counts 128-byte read requests as 64 bytes on this part, so both counters are
+        scaled by what they read for a plain copy of known size in the same run (bench.py
+        --calib-copy-mib: the library's row-copy kernel, 16-byte lanes like the GEMM operand loads).
+        Prints a markdown summary and merges {key: {...}} into the JSON file that bench.py reads.
+"""
+
+from __future__ import annotations
+
+import csv
+import json
+import os
+import re
+import sys
+from collections import defaultdict
+
+
+def _short(name: str) -> str:
+    n = re.sub(r"\(.*", "", name).replace("void ", "")
+    return n if len(n) < 90 else n[:87] + "..."
+
+
+def kernel_stats(path: str, passes: int, title: str, cmd: str) -> str:
+    rows = list(csv.DictReader(open(path)))
+    per = [r for r in rows if int(r["Calls"]) % passes == 0]
+    setup = [r for r in rows if int(r["Calls"]) % passes != 0]
+    ptot = sum(float(r["TotalDurationNs"]) for r in per)
+    out = [f"# {title}", "", "Command (run from the repository root on one MI355X):", "", "```", cmd, "```", "",
+           f"`rocprofv3 --kernel-trace --stats` kernel_stats.csv, {passes} correction passes in the trace "
+           "(warm-up + timed); per-pass time = total / passes.", "",
+           "| kernel | calls | avg us | per-pass us | share |", "|---|---:|---:|---:|---:|"]
+    for r in sorted(per, key=lambda r: -float(r["TotalDurationNs"])):
+        t = float(r["TotalDurationNs"])
+        if t / ptot < 0.001:
+            continue
+        out.append(f"| `{_short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
+                   f"{t / passes / 1e3:.1f} | {100 * t / ptot:.1f}% |")
+    out.append(f"| **correction pass, all kernels** | | | **{ptot / passes / 1e3:.1f}** | 100% |")
+    out += ["", "One-time setup kernels in the same trace (synthetic data and cache generation, not part of a pass):",
+            ""]
+    out += [f"- `{_short(r['Name'])}`: {r['Calls']} calls, {float(r['TotalDurationNs']) / 1e3:.0f} us total"
+            for r in setup if float(r["TotalDurationNs"]) > 20000]
+    return "\n".join(out)
+
+
+def _per_kernel(path: str):
+    acc = defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        acc[r["Kernel_Name"]].append(float(r["Counter_Value"]))
+    return acc
+
+
+def traffic(fetch_csv: str, write_csv: str, kernel: str, calib: str, calib_bytes: float, json_out: str, key: str,
+            cmd: str) -> str:
+    f, w = _per_kernel(fetch_csv), _per_kernel(write_csv)
+
+    def pick(d, sub):
+        names = [n for n in d if sub in n]
+        if not names:
+            raise SystemExit(f"no kernel matching {sub!r}")
+        vals = [v for n in names for v in d[n]]
+        return names[0], sum(vals) / len(vals), len(vals)
+
+    def largest(d, sub):  # the calibration copy is the largest dispatch of its kernel in the run
+        vals = [v for n in d if sub in n for v in d[n]]
+        if not vals:
+            raise SystemExit(f"no kernel matching {sub!r}")
+        return max(vals)
+
+    kname, kf, nk = pick(f, kernel)
+    _, kw, _ = pick(w, kernel)
+    cf, cw = largest(f, calib), largest(w, calib)
+    # The calibration copy reads its rows plus 16 bytes of row indices per 4 KiB row.
+    f_scale = calib_bytes * (1.0 + 16.0 / 4096.0) / (cf * 1024.0)
+    w_scale = calib_bytes / (cw * 1024.0)
+    fetch_b = kf * 1024.0 * f_scale
+    write_b = kw * 1024.0 * w_scale
+    rec = {"kernel": _short(kname), "fetch_bytes": round(fetch_b), "write_bytes": round(write_b),
+           "traffic_bytes": round(fetch_b + write_b), "fetch_kib_raw": round(kf, 1), "write_kib_raw": round(kw, 1),
+           "fetch_scale": round(f_scale, 4), "write_scale": round(w_scale, 4), "dispatches": nk}
+    data = {}
+    if os.path.exists(json_out):
+        data = json.load(open(json_out))
+    data[key] = rec
+    with open(json_out, "w") as fh:
+        json.dump(data, fh, indent=1, sort_keys=True)
+        fh.write("\n")
+    lines = [f"# HBM traffic per launch: {key}", "", "Commands (run from the repository root on one MI355X):", "",
+             "```", cmd, "```", "",
+             f"- kernel: `{rec['kernel']}` ({nk} dispatches averaged)",
+             f"- FETCH_SIZE {kf:.1f} KiB/dispatch x {f_scale:.4f} = {fetch_b / 1e6:.2f} MB",
+             f"- WRITE_SIZE {kw:.1f} KiB/dispatch x {w_scale:.4f} = {write_b / 1e6:.2f} MB",
+             f"- traffic per launch: {(fetch_b + write_b) / 1e6:.2f} MB",
+             f"- scale factors: the same counters over a {calib_bytes / 2**20:.0f} MiB row copy "
+             f"(`{calib}`) read {cf:.0f} / {cw:.0f} KiB for {calib_bytes / 1024:.0f} KiB moved each way"]
+    return "\n".join(lines)
+
+
+def main(argv):
+    if len(argv) >= 5 and argv[0] == "kernel-stats":
+        print(kernel_stats(argv[1], int(argv[2]), argv[3], argv[4]))
+    elif len(argv) >= 9 and argv[0] == "traffic":
+        print(traffic(argv[1], argv[2], argv[3], argv[4], float(argv[5]), argv[6], argv[7], argv[8]))
+    else:
+        print(__doc__)
+        return 2
+    return 0
+
+
+if __name__ == "__main__":
+    sys.exit(main(sys.argv[1:]))

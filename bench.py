@@ -254,6 +254,15 @@ def main():
         roof = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
                 "frac": round(achieved / peak, 4), "traffic": None, "kernel": args.probe,
                 "launches": len(durs), "avg_us": round(avg_ms * 1e3, 2)}
+        # HBM bytes per launch of this kernel at this workload, from the committed rocprofv3
+        # FETCH_SIZE / WRITE_SIZE summary (appcorr_amd.profiling traffic), when one exists.
+        tkey = f"{args.probe}@{args.config}/b{B}/k{k}"
+        tpath = os.path.join(ROOT, "profiles", "traffic.json")
+        if os.path.exists(tpath):
+            rec = json.load(open(tpath)).get(tkey)
+            if rec:
+                roof["traffic"] = rec["traffic_bytes"]
+                roof["traffic_source"] = f"profiles/traffic.json[{tkey}] ({rec['kernel']})"
 
     cpu = None
     if args.cpu_budget > 0:
