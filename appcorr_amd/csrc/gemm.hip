@@ -294,34 +294,14 @@ __global__ __launch_bounds__(WGM * WGN * 64) void gemm_bf16_kernel(const uint16_
 // epilogue on 8 consecutive columns per lane, 16-byte global stores. Needs N % BN == 0, 16-byte
 // aligned C / gamma / resid rows and an 8-byte aligned bias; the caller has passed a barrier
 // after the last LDS read of the main loop.
-template <int BM, int BN, int FM, int FN, int NW, int EPI>
-__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FM][FN], unsigned char* smem, const uint16_t* lut,
-                                           int wm0, int wn0, int m0, int n0, int M, const EpiArgs& ea,
-                                           uint16_t* __restrict__ C, int64_t ldc) {
-  const int lane = threadIdx.x & 63;
+// Phase 2 of the tile epilogue, shared by every kernel family: the bf16(acc + bias) tile sits in LDS
+// (row pitch BN + 8 elements) and all NT threads finish the epilogue on 8 consecutive columns each.
+template <int BM, int BN, int NT, int EPI>
+__device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uint16_t* lut, int m0, int n0, int M,
+                                                  const EpiArgs& ea, uint16_t* __restrict__ C, int64_t ldc) {
   constexpr int LDT = BN + 8;
-  uint16_t* ct = reinterpret_cast<uint16_t*>(smem);
-#pragma unroll
-  for (int j = 0; j < FN; ++j) {
-#pragma unroll
-    for (int g = 0; g < 4; ++g) {
-      const int cl = wn0 + j * 32 + g * 8 + 4 * (lane >> 5);
-      float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
-      if (ea.bias) {
-        const uint2 bw = *reinterpret_cast<const uint2*>(ea.bias + n0 + cl);
-        b0 = lo_bf16(bw.x); b1 = hi_bf16(bw.x); b2 = lo_bf16(bw.y); b3 = hi_bf16(bw.y);
-      }
-#pragma unroll
-      for (int i = 0; i < FM; ++i) {
-        const int rl = wm0 + i * 32 + (lane & 31);
-        uint2 w;
-        w.x = cvt_pk_bf16(acc[i][j][4 * g + 0] + b0, acc[i][j][4 * g + 1] + b1);
-        w.y = cvt_pk_bf16(acc[i][j][4 * g + 2] + b2, acc[i][j][4 * g + 3] + b3);
-        *reinterpret_cast<uint2*>(ct + rl * LDT + cl) = w;
-      }
-    }
-  }
-  __syncthreads();
+  constexpr int NW = NT / 64;
+  const uint16_t* ct = reinterpret_cast<const uint16_t*>(smem);
   if constexpr (EPI == kEpiQkv) {
     // One work item = (row, head, 8-wide chunk of the left half) with its partner chunk Dh/2 to the
     // right: RoPE on q and k of patch rows, then q packed or k / v into the cache row. A tile covers
@@ -332,11 +312,11 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FM][FN], unsign
     const int hc0 = n0 - which * HD;
     const int lg_cph = __builtin_ctz((unsigned)(half >> 3));  // chunk pairs per head = Dh / 16
     constexpr int PPR = BN / 16;                               // chunk pairs per tile row
-    constexpr int ITEMS = BM * PPR / (NW * 64);
-    static_assert(ITEMS * NW * 64 == BM * PPR, "items must split evenly over the threads");
+    constexpr int ITEMS = (BM * PPR + NW * 64 - 1) / (NW * 64);
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
       const int p = threadIdx.x + it * NW * 64;
+      if (p >= BM * PPR) break;
       const int rl = p / PPR, pr = p - rl * PPR;
       const int row = m0 + rl;
       if (row >= M) continue;
@@ -396,6 +376,37 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FM][FN], unsign
     }
     *reinterpret_cast<uint4*>(C + (int64_t)row * ldc + col) = o;
   }
+}
+
+template <int BM, int BN, int FM, int FN, int NW, int EPI>
+__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FM][FN], unsigned char* smem, const uint16_t* lut,
+                                           int wm0, int wn0, int m0, int n0, int M, const EpiArgs& ea,
+                                           uint16_t* __restrict__ C, int64_t ldc) {
+  const int lane = threadIdx.x & 63;
+  constexpr int LDT = BN + 8;
+  uint16_t* ct = reinterpret_cast<uint16_t*>(smem);
+#pragma unroll
+  for (int j = 0; j < FN; ++j) {
+#pragma unroll
+    for (int g = 0; g < 4; ++g) {
+      const int cl = wn0 + j * 32 + g * 8 + 4 * (lane >> 5);
+      float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+      if (ea.bias) {
+        const uint2 bw = *reinterpret_cast<const uint2*>(ea.bias + n0 + cl);
+        b0 = lo_bf16(bw.x); b1 = hi_bf16(bw.x); b2 = lo_bf16(bw.y); b3 = hi_bf16(bw.y);
+      }
+#pragma unroll
+      for (int i = 0; i < FM; ++i) {
+        const int rl = wm0 + i * 32 + (lane & 31);
+        uint2 w;
+        w.x = cvt_pk_bf16(acc[i][j][4 * g + 0] + b0, acc[i][j][4 * g + 1] + b1);
+        w.y = cvt_pk_bf16(acc[i][j][4 * g + 2] + b2, acc[i][j][4 * g + 3] + b3);
+        *reinterpret_cast<uint2*>(ct + rl * LDT + cl) = w;
+      }
+    }
+  }
+  __syncthreads();
+  store_tile_phase2<BM, BN, NW * 64, EPI>(smem, lut, m0, n0, M, ea, C, ldc);
 }
 
 // Copies the GELU table into LDS at `dst` (16-byte aligned).
@@ -567,7 +578,19 @@ __device__ __forceinline__ void wait_vmcnt_rt(int n) {
     case 9: wait_vmcnt<9>(); break;
     case 10: wait_vmcnt<10>(); break;
     case 11: wait_vmcnt<11>(); break;
-    default: wait_vmcnt<12>(); break;
+    case 12: wait_vmcnt<12>(); break;
+    case 13: wait_vmcnt<13>(); break;
+    case 14: wait_vmcnt<14>(); break;
+    case 15: wait_vmcnt<15>(); break;
+    case 16: wait_vmcnt<16>(); break;
+    case 17: wait_vmcnt<17>(); break;
+    case 18: wait_vmcnt<18>(); break;
+    case 19: wait_vmcnt<19>(); break;
+    case 20: wait_vmcnt<20>(); break;
+    case 21: wait_vmcnt<21>(); break;
+    case 22: wait_vmcnt<22>(); break;
+    case 23: wait_vmcnt<23>(); break;
+    default: wait_vmcnt<24>(); break;
   }
 }
 
@@ -741,6 +764,243 @@ void gemm_bf16_pipe_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t
 }
 
 // ------------------------------------------------------------------------------------------------
+// 16-row-block kernel for M = 144 k-multiples. The correction pass's GEMMs have M = B * (5 + k)
+// rows (4176 = 29 x 144 at the headline shape), which 256-row tiles cover badly (17 tile rows, the
+// last one 31 % full). Tiles of 144 rows (9 blocks of 16) on v_mfma_f32_16x16x32_bf16 cover it
+// exactly: fc1 as 29 x 8 tiles of 144 x 512, the N = C GEMMs as 29 x 8 tiles of 144 x 128 -- 232
+// workgroups, one round on 256 CUs.
+//   * Every wave owns all BM rows and a BN / WGN column strip; with KSPLIT = 2 two wave groups take
+//     alternate 32-deep halves of each K tile (doubling the waves per CU for the narrow N = C tiles)
+//     and are summed through LDS at the end.
+//   * K tiles of BK (32 or 64) in NST LDS stages, direct-to-LDS loads issued NST - 1 tiles ahead,
+//     fragments read one K tile ahead of their MFMAs, one barrier per K tile.
+//   * Rows are 2 * BK bytes; chunk c of row r sits at 16-byte slot c ^ ((r / L) % CPRW) with
+//     L = rows per 256-byte bank line and CPRW = chunks per row, so a fragment read (16 rows at one
+//     chunk per 16 lanes) covers all 64 banks.
+// ------------------------------------------------------------------------------------------------
+
+template <int BK>
+struct R16Layout {
+  static constexpr int kRowBytes = 2 * BK;
+  static constexpr int kChunks = BK / 8;             // 16-byte chunks per row
+  static constexpr int kRowsPerLine = 256 / kRowBytes;
+  static constexpr int kRowsPerLoad = 1024 / kRowBytes;  // rows one global_load_lds instruction fills
+  __device__ static __forceinline__ int swz(int r, int c) {
+    return r * kRowBytes + ((c ^ ((r / kRowsPerLine) % kChunks)) << 4);
+  }
+};
+
+// LDS bytes before the GELU table: K stages, the KSPLIT reduction buffer plus the bf16 tile, or the
+// bf16 tile alone.
+__host__ __device__ constexpr int r16_lut_offset(int bm, int bn, int bk, int nst, int ksplit, int nw) {
+  const int stages = nst * (bm + bn) * 2 * bk;
+  const int tile = bm * (bn + 8) * 2;
+  const int red = ksplit > 1 ? (nw / ksplit) * 64 * (bm * (bn / (nw / ksplit)) / 64) * 4 : 0;  // fp32 partials
+  const int epi = red + tile;
+  return stages > epi ? stages : epi;
+}
+
+// FB: fragments read one K tile ahead (double-buffered registers); without it they are read right
+// after the barrier of their own K tile (for wave tiles whose accumulators leave no room).
+template <int BM, int BN, int WGN, int KSPLIT, int BK, int NST, bool FB, int EPI>
+__global__ __launch_bounds__(WGN * KSPLIT * 64) __attribute__((amdgpu_waves_per_eu((WGN * KSPLIT + 3) / 4,
+                                                                                    (WGN * KSPLIT + 3) / 4)))
+void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t lda, const uint16_t* __restrict__ W,
+                          int N, int64_t ldw, EpiArgs ea, uint16_t* __restrict__ C, int64_t ldc, int group_m) {
+  using L = R16Layout<BK>;
+  constexpr int NW = WGN * KSPLIT;
+  constexpr int NT = NW * 64;
+  constexpr int WN = BN / WGN;
+  constexpr int FMB = BM / 16, FNB = WN / 16;     // 16 x 16 blocks per wave
+  constexpr int SUB = BK / 32;                    // 32-deep MFMA steps per K tile
+  constexpr int SUBW = SUB / KSPLIT;              // ... per wave
+  constexpr int NI = (BM + BN) / L::kRowsPerLoad; // load instructions per K tile
+  constexpr int NLM = (NI + NW - 1) / NW;
+  constexpr int STAGE = (BM + BN) * L::kRowBytes;
+  static_assert(BM % L::kRowsPerLoad == 0 && BN % L::kRowsPerLoad == 0, "rows must fill whole load instructions");
+  static_assert(SUB % KSPLIT == 0 && SUBW >= 1 && WN % 16 == 0 && NST >= 2, "tile shape");
+  typedef float f32x4v __attribute__((ext_vector_type(4)));
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int kLutOff = r16_lut_offset(BM, BN, BK, NST, KSPLIT, NW);
+  if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) load_gelu_table<NT>(smem + kLutOff);
+
+  const int tiles_n = (N + BN - 1) / BN;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles = gridDim.x;
+  const int bid = blockIdx.x;
+  const int xcd = bid % kNumXcd;
+  const int q = tiles / kNumXcd, r = tiles % kNumXcd;
+  const int tile = xcd * q + min(xcd, r) + bid / kNumXcd;
+  const int per_group = group_m * tiles_n;
+  const int grp = tile / per_group;
+  const int first_m = grp * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
+  const int in_grp = tile - grp * per_group;
+  const int tm = first_m + in_grp % gsize, tn = in_grp / gsize;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int kg = wave / WGN;                // K group
+  const int wn0 = (wave % WGN) * WN;        // column strip
+
+  // Loads: instruction i = wave + j * NW fills rows [i * RPL, (i + 1) * RPL) of the stage.
+  const int nl = (NI - wave + NW - 1) / NW;
+  const uint16_t* src[NLM];
+  int dst[NLM];
+  {
+    const int lrow = lane / L::kChunks, lslot = lane % L::kChunks;
+#pragma unroll
+    for (int j = 0; j < NLM; ++j) {
+      const int i = min(wave + j * NW, NI - 1);
+      const int row = i * L::kRowsPerLoad + lrow;  // stage row (A rows first, then B rows)
+      const int chunk = lslot ^ ((row / L::kRowsPerLine) % L::kChunks);
+      dst[j] = i * 1024;
+      if (row < BM) src[j] = A + (int64_t)min(m0 + row, M - 1) * lda + chunk * 8;
+      else src[j] = W + (int64_t)min(n0 + row - BM, N - 1) * ldw + chunk * 8;
+    }
+  }
+  auto issue = [&](int stage, int kt) __attribute__((always_inline)) {
+    unsigned char* base = smem + stage * STAGE;
+    const int k0 = kt * BK;
+#pragma unroll
+    for (int j = 0; j < NLM; ++j)
+      if (j < nl) __builtin_amdgcn_global_load_lds((const void*)(src[j] + k0), (lds_ptr_t)(base + dst[j]), 16, 0, 0);
+  };
+  auto wait_tiles = [&](int n_after) __attribute__((always_inline)) { wait_vmcnt_rt(n_after * nl); };
+
+  f32x4v acc[FMB][FNB];
+#pragma unroll
+  for (int i = 0; i < FMB; ++i)
+#pragma unroll
+    for (int j = 0; j < FNB; ++j) acc[i][j] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // Fragments (16x16x32): lane l reads row l % 16 of a 16-row block at K chunk 4 * sub + l / 16.
+  struct Frags {
+    bf16x8_t a[SUBW][FMB], b[SUBW][FNB];
+  };
+  auto read_frags = [&](Frags& f, int kt) __attribute__((always_inline)) {
+    const unsigned char* st = smem + (kt % NST) * STAGE;
+#pragma unroll
+    for (int s = 0; s < SUBW; ++s) {
+      const int ch = 4 * (s * KSPLIT + kg) + (lane >> 4);
+#pragma unroll
+      for (int i = 0; i < FMB; ++i)
+        f.a[s][i] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(i * 16 + (lane & 15), ch));
+#pragma unroll
+      for (int j = 0; j < FNB; ++j)
+        f.b[s][j] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(BM + wn0 + j * 16 + (lane & 15), ch));
+    }
+  };
+  const int rows_left = M - m0;
+  auto mfmas = [&](const Frags& f) __attribute__((always_inline)) {
+#pragma unroll
+    for (int s = 0; s < SUBW; ++s)
+#pragma unroll
+      for (int i = 0; i < FMB; ++i)
+        if (i * 16 < rows_left) {
+#pragma unroll
+          for (int j = 0; j < FNB; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.b[s][j], f.a[s][i], acc[i][j], 0, 0, 0);
+        }
+  };
+
+  const int KT = K / BK;
+#pragma unroll
+  for (int s = 0; s < NST; ++s)
+    if (s < KT) issue(s, s);
+  if constexpr (FB) {
+    wait_tiles(min(KT - 1, NST - 1));
+    block_barrier();
+    Frags f0, f1;
+    read_frags(f0, 0);
+    // Step kt: wait for tile kt + 1, barrier, refill tile kt's stage with tile kt + NST, read tile
+    // kt + 1's fragments, MFMAs of tile kt.
+    auto step = [&](int kt, Frags& cur, Frags& nxt) __attribute__((always_inline)) {
+      if (kt + 1 < KT) {
+        wait_tiles(min(KT - 2 - kt, NST - 2));
+        block_barrier();
+        if (kt + NST < KT) issue(kt % NST, kt + NST);
+        __builtin_amdgcn_sched_barrier(0);
+        read_frags(nxt, kt + 1);
+      }
+      mfmas(cur);
+      __builtin_amdgcn_sched_barrier(0);
+    };
+    int kt = 0;
+    for (; kt + 1 < KT; kt += 2) {
+      step(kt, f0, f1);
+      step(kt + 1, f1, f0);
+    }
+    if (kt < KT) step(kt, f0, f1);
+  } else {
+    // Step kt: wait for tile kt, barrier (also: every wave is done with tile kt - 1's stage), refill
+    // that stage with tile kt - 1 + NST, read tile kt's fragments, MFMAs of tile kt.
+    Frags f;
+    for (int kt = 0; kt < KT; ++kt) {
+      wait_tiles(min(KT - 1 - kt, NST - 1));
+      block_barrier();
+      if (kt >= 1 && kt - 1 + NST < KT) issue((kt - 1) % NST, kt - 1 + NST);
+      __builtin_amdgcn_sched_barrier(0);
+      read_frags(f, kt);
+      mfmas(f);
+      __builtin_amdgcn_sched_barrier(0);
+    }
+  }
+
+  // Epilogue. Block (i, j) holds the transposed product: lane l, register v -> row i * 16 + l % 16,
+  // column wn0 + j * 16 + 4 (l / 16) + v.
+  constexpr int LDT = BN + 8;
+  constexpr int RED = KSPLIT > 1 ? (NW / KSPLIT) * 64 * FMB * FNB * 4 * 4 : 0;  // fp32 partial bytes
+  uint16_t* ct = reinterpret_cast<uint16_t*>(smem + RED);
+  block_barrier();
+  if constexpr (KSPLIT > 1) {
+    // Group 1 parks its accumulators in LDS ([block][register][thread] fp32), group 0 adds them.
+    float* red = reinterpret_cast<float*>(smem);
+    const int t0 = (wave % WGN) * 64 + lane;
+    if (kg == 1) {
+#pragma unroll
+      for (int i = 0; i < FMB; ++i)
+#pragma unroll
+        for (int j = 0; j < FNB; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) red[((i * FNB + j) * 4 + v) * (WGN * 64) + t0] = acc[i][j][v];
+    }
+    __syncthreads();
+    if (kg == 0) {
+#pragma unroll
+      for (int i = 0; i < FMB; ++i)
+#pragma unroll
+        for (int j = 0; j < FNB; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[i][j][v] += red[((i * FNB + j) * 4 + v) * (WGN * 64) + t0];
+    }
+  }
+  if (kg == 0) {
+#pragma unroll
+    for (int j = 0; j < FNB; ++j) {
+      const int cl = wn0 + j * 16 + 4 * (lane >> 4);
+      float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+      if (ea.bias) {
+        const uint2 bw = *reinterpret_cast<const uint2*>(ea.bias + n0 + cl);
+        b0 = lo_bf16(bw.x); b1 = hi_bf16(bw.x); b2 = lo_bf16(bw.y); b3 = hi_bf16(bw.y);
+      }
+#pragma unroll
+      for (int i = 0; i < FMB; ++i) {
+        uint2 w;
+        w.x = cvt_pk_bf16(acc[i][j][0] + b0, acc[i][j][1] + b1);
+        w.y = cvt_pk_bf16(acc[i][j][2] + b2, acc[i][j][3] + b3);
+        *reinterpret_cast<uint2*>(ct + (i * 16 + (lane & 15)) * LDT + cl) = w;
+      }
+    }
+  }
+  __syncthreads();
+  store_tile_phase2<BM, BN, NT, EPI>(reinterpret_cast<unsigned char*>(ct),
+                                     reinterpret_cast<const uint16_t*>(smem + kLutOff), m0, n0, M, ea, C, ldc);
+}
+
+// ------------------------------------------------------------------------------------------------
 // Configurations and dispatch
 // ------------------------------------------------------------------------------------------------
 
@@ -748,8 +1008,9 @@ typedef void (*gemm_fn)(const uint16_t*, int, int, int64_t, const uint16_t*, int
                         int64_t, int);
 
 struct GemmCfg {
-  int bm, bn, wgm, wgn, pf;  // pf: register prefetch depth; 0 = direct-to-LDS; -1 = pipelined
+  int bm, bn, wgm, wgn, pf;  // pf: register prefetch depth; 0 = direct-to-LDS; -1 = pipelined; -2 = 16-row
   gemm_fn fn[6];             // by epilogue; fn[kEpiQkv] only for the direct-to-LDS families
+  int bk, nst;               // 16-row kernel: K tile depth and LDS stages
 };
 
 #define OUDJAT_GEMM_CFG(BM, BN, WGM, WGN, PF)                                                             \
@@ -769,6 +1030,15 @@ struct GemmCfg {
    {gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 0>, gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 1>,               \
     gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 2>, gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 3>,               \
     gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 4>, gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, kEpiQkv>}}
+
+// pf = -2: 16-row-block kernel; wgm = K groups, wgn = column strips.
+#define OUDJAT_GEMM_R16_CFG(BM, BN, WGN, KS, BK, NST, FB)                                                 \
+  {BM, BN, KS, WGN, -2,                                                                                  \
+   {gemm_bf16_r16_kernel<BM, BN, WGN, KS, BK, NST, FB, 0>, gemm_bf16_r16_kernel<BM, BN, WGN, KS, BK, NST, FB, 1>, \
+    gemm_bf16_r16_kernel<BM, BN, WGN, KS, BK, NST, FB, 2>, gemm_bf16_r16_kernel<BM, BN, WGN, KS, BK, NST, FB, 3>, \
+    gemm_bf16_r16_kernel<BM, BN, WGN, KS, BK, NST, FB, 4>,                                               \
+    gemm_bf16_r16_kernel<BM, BN, WGN, KS, BK, NST, FB, kEpiQkv>},                                        \
+   BK, NST}
 
 static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_CFG(128, 128, 2, 2, 1),  // 0
@@ -791,6 +1061,11 @@ static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_PIPE_CFG(288, 256, 3, 4),  // 17
     OUDJAT_GEMM_PIPE_CFG(256, 128, 2, 2),  // 18
     OUDJAT_GEMM_PIPE_CFG(128, 128, 2, 2),  // 19
+    OUDJAT_GEMM_R16_CFG(144, 512, 4, 1, 32, 3, true),   // 20
+    OUDJAT_GEMM_R16_CFG(144, 128, 2, 2, 64, 4, true),   // 21
+    OUDJAT_GEMM_R16_CFG(144, 512, 8, 1, 32, 3, false),  // 22: fc1-like (N % 512 == 0)
+    OUDJAT_GEMM_R16_CFG(144, 128, 4, 2, 64, 4, true),   // 23: N = C GEMMs
+    OUDJAT_GEMM_R16_CFG(144, 128, 4, 2, 64, 3, true),   // 24
 };
 static constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -847,6 +1122,10 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   if (N % 128 != 0) return 8;
   const int64_t tiles256 = cdiv(M, 256) * cdiv(N, 256);
   if (N % 256 == 0 && tiles256 >= 128 && tiles256 <= 256) return 15;
+  // 144-row tiles (one round of 128..256 workgroups) when 256 x 256 tiles do not fit one round.
+  const int64_t tm144 = cdiv(M, 144);
+  if (N % 512 == 0 && tm144 * (N / 512) >= 128 && tm144 * (N / 512) <= 256) return 22;
+  if (tm144 * (N / 128) >= 128 && tm144 * (N / 128) <= 256) return 23;
   return 11;
 }
 
@@ -861,6 +1140,7 @@ static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t 
   // K stages, or (direct-to-LDS kernels) the bf16 output tile of the epilogue if that is larger.
   size_t lds = cfg.pf < 0 ? (size_t)kStages * (cfg.bm + cfg.bn) * 64 : (size_t)2 * (cfg.bm + cfg.bn) * 128;
   if (cfg.pf <= 0) lds = lds > (size_t)cfg.bm * (cfg.bn + 8) * 2 ? lds : (size_t)cfg.bm * (cfg.bn + 8) * 2;
+  if (cfg.pf == -2) lds = r16_lut_offset(cfg.bm, cfg.bn, cfg.bk, cfg.nst, cfg.wgm, cfg.wgm * cfg.wgn);
   if (cfg.pf <= 0 && epi == OUDJAT_EPI_BIAS_GELU) lds += kGeluLut * sizeof(uint16_t);
   if (epi == OUDJAT_EPI_BIAS_GELU) {
     const int st = ensure_gelu_table();
