@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be loaded before the HIP library, see module docstring
 
 LIB_PATH = Path(__file__).resolve().parent / "liboudjat_hip.so"
-ABI_VERSION = 2
+ABI_VERSION = 3
 
 OK = 0
 STATUS_NAMES = {
@@ -77,6 +77,8 @@ SIGNATURES: dict[str, list] = {
     "oudjat_qkv_rope_kv_scatter": [_p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _p, _p],
     "oudjat_layernorm_rows": [_p, _i64, _i64, _i64, _p, _p, _f32, _p, _i64, _p],
     "oudjat_linear_bf16": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i32, _p, _p, _i64, _p, _i64, _p],
+    "oudjat_packed_residual_persist": [_p, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p],
+    "oudjat_fold_residual_rows": [_p, _i64, _i64, _p, _p, _p, _i64, _p, _p],
     "oudjat_linear_qkv_rope_kv": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p, _p,
                                   _i64, _i64, _p, _p],
     "oudjat_sparse_query_attention": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32, _p,

@@ -22,7 +22,9 @@ BUILD_DIR = PKG_DIR / "_build"
 LIB_PATH = PKG_DIR / "liboudjat_hip.so"
 ARCH = "gfx950"
 
-# Packed-fp32 instruction selection is disabled for all device code ("Build").
+# Packed-fp32 instruction selection is disabled for all device code: the compiler still emits
+# scalar or float2 fp32 arithmetic, but no v_pk_* fp32 instructions, whose results have been unreliable
+# on this hardware.
 HIP_FLAGS = [
     f"--offload-arch={ARCH}",
     "-O3",

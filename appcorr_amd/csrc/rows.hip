@@ -152,6 +152,81 @@ __global__ __launch_bounds__(kRowThreads) void reconstruct_scatter_persist_kerne
   }
 }
 
+// Selected-row half of the residual step when the selected rows stay packed between blocks:
+// x_new[i] = bf16(x_attn + mlp) and blocks_out_sum[b_i, t_i] = bf16(bf16(x_attn - x_act) + mlp).
+// One wave per packed row.
+__global__ __launch_bounds__(kRowThreads) void packed_residual_persist_kernel(
+    const uint16_t* __restrict__ xa, const uint16_t* __restrict__ xt, const uint16_t* __restrict__ mlp, int64_t rows,
+    int64_t C, const int64_t* __restrict__ bi, const int64_t* __restrict__ ti, uint16_t* __restrict__ bos,
+    int64_t bsb, int64_t bsn, uint16_t* xn) {
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerWg + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int chunks = (int)(C >> 3);
+  const uint4* av = reinterpret_cast<const uint4*>(xa + row * C);
+  const uint4* tv = reinterpret_cast<const uint4*>(xt + row * C);
+  const uint4* mv = reinterpret_cast<const uint4*>(mlp + row * C);
+  uint4* ov = reinterpret_cast<uint4*>(xn + row * C);
+  uint4* bv = reinterpret_cast<uint4*>(bos + bi[row] * bsb + ti[row] * bsn);
+  for (int c = lane; c < chunks; c += 64) {
+    float fa[8], ft[8], fm[8], fo[8], fb[8];
+    unpack8(av[c], fa);
+    unpack8(tv[c], ft);
+    unpack8(mv[c], fm);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) {
+      fo[e] = ft[e] + fm[e];
+      fb[e] = round_bf16(ft[e] - fa[e]) + fm[e];
+    }
+    ov[c] = pack8(fo);
+    bv[c] = pack8(fb);
+  }
+}
+
+// Rows of [rows, C] after a run of L correction blocks whose selected rows stayed packed: a selected
+// row (row_slot >= 0) takes its packed row; an unselected row takes x + bos_0 + ... + bos_{L-1}
+// with a bf16 rounding after every addition, i.e. the per-block x + blocks_out_sum sequence. One
+// thread per 8 columns, the L row loads issued four at a time.
+__global__ __launch_bounds__(256) void fold_residual_rows_kernel(const uint16_t* x, int64_t rows, int64_t C,
+                                                                 const int32_t* __restrict__ row_slot,
+                                                                 const uint16_t* __restrict__ xp,
+                                                                 const uint16_t* const* __restrict__ bos, int L,
+                                                                 uint16_t* xo) {
+  const int64_t chunks = C >> 3;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  const int64_t row = gid / chunks;
+  if (row >= rows) return;
+  const int64_t off = row * C + (gid - row * chunks) * 8;
+  const int32_t slot = row_slot[row];
+  if (slot >= 0) {
+    *reinterpret_cast<uint4*>(xo + off) =
+        *reinterpret_cast<const uint4*>(xp + (int64_t)slot * C + (gid - row * chunks) * 8);
+    return;
+  }
+  float v[8];
+  unpack8(*reinterpret_cast<const uint4*>(x + off), v);
+  int l = 0;
+  for (; l + 4 <= L; l += 4) {
+    uint4 b[4];
+#pragma unroll
+    for (int u = 0; u < 4; ++u) b[u] = *reinterpret_cast<const uint4*>(bos[l + u] + off);
+#pragma unroll
+    for (int u = 0; u < 4; ++u) {
+      float f[8];
+      unpack8(b[u], f);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) v[e] = round_bf16(v[e] + f[e]);
+    }
+  }
+  for (; l < L; ++l) {
+    float f[8];
+    unpack8(*reinterpret_cast<const uint4*>(bos[l] + off), f);
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[e] = round_bf16(v[e] + f[e]);
+  }
+  *reinterpret_cast<uint4*>(xo + off) = pack8(v);
+}
+
 __global__ __launch_bounds__(kRowThreads) void layerscale_add_kernel(
     const uint16_t* __restrict__ x, const uint16_t* __restrict__ a, const uint16_t* __restrict__ g, int64_t rows,
     int64_t C, uint16_t* __restrict__ o) {
@@ -245,6 +320,39 @@ extern "C" int oudjat_reconstruct_scatter_persist(const uint16_t* x, uint16_t* b
   reconstruct_scatter_persist_kernel<<<(unsigned)cdiv(rows, kRowsPerWg), kRowThreads, 0, as_stream(stream)>>>(
       x, bos, row_slot, xa, xt, mlp, rows, C, xo);
   return check_launch("reconstruct_scatter_persist");
+}
+
+extern "C" int oudjat_packed_residual_persist(const uint16_t* x_act, const uint16_t* x_attn, const uint16_t* mlp,
+                                              int64_t rows, int64_t C, const int64_t* batch_idx,
+                                              const int64_t* token_idx, uint16_t* bos, int64_t bos_stride_b,
+                                              int64_t bos_stride_n, uint16_t* x_new, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(rows >= 0 && C >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "packed_residual_persist: negative size");
+  if (rows == 0 || C == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(x_act && x_attn && mlp && batch_idx && token_idx && bos && x_new, OUDJAT_ERR_INVALID_ARGUMENT,
+                 "packed_residual_persist: null pointer");
+  OUDJAT_REQUIRE(C % 8 == 0 && aligned(x_act, 16) && aligned(x_attn, 16) && aligned(mlp, 16) && aligned(bos, 16) &&
+                     aligned(x_new, 16) && bos_stride_b % 8 == 0 && bos_stride_n % 8 == 0,
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "packed_residual_persist: 16-byte aligned rows, C %% 8 == 0");
+  packed_residual_persist_kernel<<<(unsigned)cdiv(rows, kRowsPerWg), kRowThreads, 0, as_stream(stream)>>>(
+      x_act, x_attn, mlp, rows, C, batch_idx, token_idx, bos, bos_stride_b, bos_stride_n, x_new);
+  return check_launch("packed_residual_persist");
+}
+
+extern "C" int oudjat_fold_residual_rows(const uint16_t* x, int64_t rows, int64_t C, const int32_t* row_slot,
+                                         const uint16_t* x_packed, const uint16_t* const* bos_rows, int64_t n_blocks,
+                                         uint16_t* out, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(rows >= 0 && C >= 0 && n_blocks >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "fold_residual_rows: negative size");
+  if (rows == 0 || C == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(x && row_slot && out && (n_blocks == 0 || bos_rows), OUDJAT_ERR_INVALID_ARGUMENT,
+                 "fold_residual_rows: null pointer");
+  OUDJAT_REQUIRE(C % 8 == 0 && aligned(x, 16) && aligned(out, 16) && (!x_packed || aligned(x_packed, 16)),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "fold_residual_rows: 16-byte aligned rows, C %% 8 == 0");
+  OUDJAT_REQUIRE(n_blocks < 4096 && rows * (C / 8) < ((int64_t)1 << 40), OUDJAT_ERR_TOO_LARGE,
+                 "fold_residual_rows: too large");
+  const int64_t threads = rows * (C / 8);
+  fold_residual_rows_kernel<<<(unsigned)cdiv(threads, 256), 256, 0, as_stream(stream)>>>(
+      x, rows, C, row_slot, x_packed, bos_rows, (int)n_blocks, out);
+  return check_launch("fold_residual_rows");
 }
 
 extern "C" int oudjat_fused_layerscale_add(const uint16_t* x, const uint16_t* a, const uint16_t* g, int64_t rows,

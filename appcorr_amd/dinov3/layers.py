@@ -454,7 +454,9 @@ class SelfAttentionBlock(nn.Module):
 
     # -- the correction step (block.py:942-1191) ---------------------------------------------------
 
-    def correct_partial_token(self, x: Tensor, dindice: Tensor, rope, cache_feature: Dict, tag: str, **kwargs):
+    def _prepare_correction(self, x: Tensor, dindice: Tensor, rope, cache_feature: Dict, tag: str, kwargs: Dict):
+        """Options, the (cached) query plan and its statistics, the per-tag score keys and the cache
+        tensors of one correction block (block.py:942-1110). Returns (plan, plan_key, kv, bos)."""
         debug = bool(kwargs.get("debug", False))
         kw = {
             "token_keep_ratio": kwargs.get("token_keep_ratio", 0.2),
@@ -510,30 +512,87 @@ class SelfAttentionBlock(nn.Module):
         if debug:
             cache_feature[f"{tag}_update_indice"] = plan.update_indice
 
-        qs = plan.fixed_query_state
         kv = cache_feature[f"{tag}_kv"]
         bos = cache_feature[f"{tag}_blocks_out_sum"]
         if kv.dtype != torch.bfloat16 or bos.dtype != torch.bfloat16:
             raise ValueError("the correction cache ({tag}_kv, {tag}_blocks_out_sum) must be bf16")
         if not bos.is_contiguous():
             raise ValueError("{tag}_blocks_out_sum must be contiguous")
-        inplace = bool(kwargs.get("inplace_residual_add", False)) and not torch.is_grad_enabled()
-        xc = x if x.is_contiguous() else x.contiguous()
-        out = xc if inplace else torch.empty_like(xc)
-        M = qs.active_token_idx.numel()
-        if M == 0:
-            empty = xc.new_empty((0, C))
-            return K.reconstruct_scatter_persist(xc, bos, qs.row_slot, empty, empty, empty, out=out), cache_feature
+        return plan, key, kv, bos
 
-        x_act = K.gather_rows(xc, qs.active_batch_idx, qs.active_token_idx)          # block.py:1111
-        xn = K.layer_norm(x_act, self.norm1.weight, self.norm1.bias, self.norm1.eps)   # :1114
+    def _correct_rows(self, x_act: Tensor, rope, kv: Tensor, qs: PackedQueryState):
+        """The block's arithmetic on the packed selected rows (block.py:1111-1141): returns
+        (x_attn, mlp); the K/V cache rows of the selected tokens are rewritten in place."""
+        xn = K.layer_norm(x_act, self.norm1.weight, self.norm1.bias, self.norm1.eps)   # block.py:1114
         _, attn = self.attn._qkv_attention(xn, rope, kv, qs)                         # attention.py:415-523
         x_attn = K.linear(attn, self.attn.proj.weight, self.attn.proj.bias,          # attention.py:532 +
                           epilogue=_lib.EPI_BIAS_LS_RESID, gamma=self._gamma(self.ls1, x_act),
                           resid=x_act)                                               # block.py:1129-1134
         mlp = self._mlp_scaled(K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps))  # :1141
+        return x_attn, mlp
+
+    def correct_partial_token(self, x: Tensor, dindice: Tensor, rope, cache_feature: Dict, tag: str, **kwargs):
+        plan, _, kv, bos = self._prepare_correction(x, dindice, rope, cache_feature, tag, kwargs)
+        qs = plan.fixed_query_state
+        inplace = bool(kwargs.get("inplace_residual_add", False)) and not torch.is_grad_enabled()
+        xc = x if x.is_contiguous() else x.contiguous()
+        out = xc if inplace else torch.empty_like(xc)
+        M = qs.active_token_idx.numel()
+        if M == 0:
+            empty = xc.new_empty((0, xc.shape[-1]))
+            return K.reconstruct_scatter_persist(xc, bos, qs.row_slot, empty, empty, empty, out=out), cache_feature
+
+        x_act = K.gather_rows(xc, qs.active_batch_idx, qs.active_token_idx)          # block.py:1111
+        x_attn, mlp = self._correct_rows(x_act, rope, kv, qs)
         out = K.reconstruct_scatter_persist(xc, bos, qs.row_slot, x_act, x_attn, mlp, out=out)  # :1140-1179
         if os.environ.get("APPCORR_PERSIST_TRACE") and not getattr(SelfAttentionBlock, "_persist_traced", False):
             SelfAttentionBlock._persist_traced = True
             print(f"[persist] blocks_out_sum write executed, tag={tag} rows={M}", flush=True)
         return out, cache_feature
+
+
+def correct_blocks_packed(blocks, x: Tensor, dindice: Tensor, rope, cache_feature: Dict, tags, **kwargs):
+    """A run of correction blocks with one query plan, the selected rows kept packed between blocks.
+
+    Same results, bit for bit, as calling blocks[i].correct(...) in turn (block.py:942-1191 per
+    block, the executor loop of dinov3_classifier.py:591-663): every block recomputes exactly the
+    selected rows, and an unselected row only ever receives x + blocks_out_sum of each block, which
+    does not depend on the correction. So the selected rows are gathered once, carried packed through
+    the blocks (each block persists its blocks_out_sum rows and K/V rows as usual), and the full
+    tensor is written once at the end: packed rows scattered back, every other row folded through
+    the blocks' blocks_out_sum with the per-block bf16 rounding. Saves a gather and a full-tensor
+    pass per block.
+
+    Returns (x_out, cache_feature), or None when the blocks would not share one plan (the plan
+    depends on per-layer server scores), in which case the caller runs the blocks one by one.
+    """
+    if not blocks:
+        return x, cache_feature
+    # Decided before anything is computed or cached: the plan is shared across blocks exactly when
+    # _shared_partial_token_plan_key returns a key (server weight 0, or a layer-mean server score).
+    server_w = float(kwargs.get("server_pscore_weight", 1.0))
+    if server_w != 0.0 and str(kwargs.get("server_pscore", "cls_attn_prob")) not in \
+            SelfAttentionBlock._LAYERMEAN_SERVER_PSCORES:
+        return None
+    plan0, key, _, _ = blocks[0]._prepare_correction(x, dindice, rope, cache_feature, tags[0], kwargs)
+    if key is None:
+        raise RuntimeError("packed correction run: the query plan is not shared across blocks")
+    qs = plan0.fixed_query_state
+    inplace = bool(kwargs.get("inplace_residual_add", False)) and not torch.is_grad_enabled()
+    xc = x if x.is_contiguous() else x.contiguous()
+    M = qs.active_token_idx.numel()
+    x_p = K.gather_rows(xc, qs.active_batch_idx, qs.active_token_idx) if M else xc.new_empty((0, xc.shape[-1]))
+    bos_list = []
+    for i, (blk, tag) in enumerate(zip(blocks, tags)):
+        if i == 0:
+            plan, kv, bos = plan0, cache_feature[f"{tag}_kv"], cache_feature[f"{tag}_blocks_out_sum"]
+        else:
+            plan, _, kv, bos = blk._prepare_correction(xc, dindice, rope, cache_feature, tag, kwargs)
+        if plan is not plan0:
+            raise RuntimeError("blocks of one packed run resolved different query plans")
+        if x_p.shape[0] > 0:
+            x_attn, mlp = blk._correct_rows(x_p, rope, kv, qs)
+            x_p = K.packed_residual_persist(x_p, x_attn, mlp, qs.active_batch_idx, qs.active_token_idx, bos)
+        bos_list.append(bos)
+    out = K.fold_residual_rows(xc, qs.row_slot, x_p, bos_list, out=xc if inplace else None)
+    return out, cache_feature

@@ -199,6 +199,47 @@ def reconstruct_scatter_persist(x: torch.Tensor, blocks_out_sum: torch.Tensor, r
     return out
 
 
+def packed_residual_persist(x_act: torch.Tensor, x_attn: torch.Tensor, mlp: torch.Tensor, batch_idx: torch.Tensor,
+                            token_idx: torch.Tensor, blocks_out_sum: torch.Tensor) -> torch.Tensor:
+    """Selected rows kept packed: returns x_new = x_attn + mlp (bf16) and writes
+    blocks_out_sum[b_i, t_i] = (x_attn - x_act) + mlp in place (block.py:1140-1179, selected rows)."""
+    _require_cuda(x_act, x_attn, mlp, batch_idx, token_idx, blocks_out_sum)
+    for t, nm in ((x_act, "x_act"), (x_attn, "x_attn"), (mlp, "mlp")):
+        _require(t.dtype == torch.bfloat16 and t.dim() == 2 and t.is_contiguous() and t.shape == x_act.shape,
+                 f"packed_residual_persist: {nm} must be contiguous bf16 [M, C]")
+    M, C = x_act.shape
+    _require(blocks_out_sum.dim() == 3 and blocks_out_sum.shape[2] == C and blocks_out_sum.stride(2) == 1,
+             "packed_residual_persist: blocks_out_sum must be [B, N, C] with contiguous rows")
+    x_new = torch.empty_like(x_act)
+    _launch("reconstruct", x_act, "oudjat_packed_residual_persist", _ptr(x_act), _ptr(x_attn), _ptr(mlp), M, C,
+            _ptr(_index(batch_idx, "batch_idx")), _ptr(_index(token_idx, "token_idx")), _ptr(blocks_out_sum),
+            blocks_out_sum.stride(0), blocks_out_sum.stride(1), _ptr(x_new), _stream(x_act))
+    return x_new
+
+
+def fold_residual_rows(x: torch.Tensor, row_slot: torch.Tensor, x_packed: torch.Tensor, blocks_out_sums,
+                       out: torch.Tensor | None = None) -> torch.Tensor:
+    """x [B, N, C] after a run of correction blocks whose selected rows stayed packed: selected rows from
+    x_packed [M, C] (row_slot [B, N] int32 maps a token to its packed row), the other rows
+    x + bos_0 + ... + bos_{L-1} with a bf16 rounding after each addition. `out` may alias x."""
+    _require_cuda(x, row_slot, x_packed, out, *blocks_out_sums)
+    _require(x.dtype == torch.bfloat16 and x.is_contiguous() and x.dim() == 3, "fold_residual_rows: x [B, N, C] bf16")
+    for b in blocks_out_sums:
+        _require(b.dtype == torch.bfloat16 and b.is_contiguous() and b.shape == x.shape,
+                 "fold_residual_rows: blocks_out_sum tensors must be contiguous and shaped like x")
+    _require(row_slot.dtype == torch.int32 and row_slot.is_contiguous() and row_slot.numel() * x.shape[2] == x.numel(),
+             "fold_residual_rows: row_slot must be int32 [B, N]")
+    _require(x_packed.dtype == torch.bfloat16 and x_packed.is_contiguous() and x_packed.shape[-1] == x.shape[2],
+             "fold_residual_rows: x_packed must be contiguous bf16 [M, C]")
+    if out is None:
+        out = torch.empty_like(x)
+    ptrs = torch.tensor([b.data_ptr() for b in blocks_out_sums] or [0], dtype=torch.int64).to(x.device)
+    C = x.shape[2]
+    _launch("fold", x, "oudjat_fold_residual_rows", _ptr(x), x.numel() // C, C, _ptr(row_slot), _ptr(x_packed),
+            _ptr(ptrs), len(blocks_out_sums), _ptr(out), _stream(x))
+    return out
+
+
 # ------------------------------------------------------------------------------------------------
 # Plan (block.py:358-490)
 # ------------------------------------------------------------------------------------------------

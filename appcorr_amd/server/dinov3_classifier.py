@@ -69,6 +69,8 @@ class DINOv3ClassifierExecutor(ModelExecutor):
         self.norm_mean = torch.tensor([0.485, 0.456, 0.406], device=device).view(1, 3, 1, 1)
         self.norm_std = torch.tensor([0.229, 0.224, 0.225], device=device).view(1, 3, 1, 1)
         self.head = None
+        # Keep the selected rows packed across a correction run when the plan is shared by all layers.
+        self.packed_correction = True
 
     @staticmethod
     def _get_group_plans(context: Dict[str, Any]) -> Dict[int, GroupCorrectionPlan]:
@@ -175,16 +177,26 @@ class DINOv3ClassifierExecutor(ModelExecutor):
         cache["_token_prune_full_patch_total"] = cache.get("_token_prune_full_patch_total", zero) + \
             plan.full_patch_count.sum(dtype=torch.float32)
         self.begin_dinov3_correct_event()
-        for lidx in range(start, end):
-            x, cache = self.run_dinov3_correct_block(
-                lidx, x, dindice, rope, cache, f"layer{lidx}", source_key=f"layer{lidx}",
-                appcorr_method=opts["method"], token_keep_ratio=opts["token_keep_ratio"],
-                token_keep_thres=opts["token_keep_thres"], mobile_pscore=opts["mobile_pscore"],
-                mobile_pscore_weight=opts["mobile_pscore_weight"], mobile_pscore_hint=hint,
-                server_pscore=opts["server_pscore"], server_pscore_weight=opts["server_pscore_weight"],
-                pscore_fusion=opts["pscore_fusion"], sdpa_query_bucket_size=opts["sdpa_query_bucket_size"],
-                attn_col_alive_ratio=opts["attn_col_alive_ratio"], fixed_query_state=plan.query_state,
-                group_plan=plan, attn_cache_key=group_id, debug=False)
+        block_kwargs = dict(
+            appcorr_method=opts["method"], token_keep_ratio=opts["token_keep_ratio"],
+            token_keep_thres=opts["token_keep_thres"], mobile_pscore=opts["mobile_pscore"],
+            mobile_pscore_weight=opts["mobile_pscore_weight"], mobile_pscore_hint=hint,
+            server_pscore=opts["server_pscore"], server_pscore_weight=opts["server_pscore_weight"],
+            pscore_fusion=opts["pscore_fusion"], sdpa_query_bucket_size=opts["sdpa_query_bucket_size"],
+            attn_col_alive_ratio=opts["attn_col_alive_ratio"], fixed_query_state=plan.query_state,
+            group_plan=plan, attn_cache_key=group_id, debug=False)
+        # With a query plan shared by every layer the selected rows stay packed across the whole run
+        # (bit-identical to the per-block loop below, one gather and one full-tensor write in total).
+        res = None
+        if self.packed_correction and self._dinov3_correct_precision is not None and end > start:
+            res = self._dinov3_correct_precision.run_blocks_packed(range(start, end), x, dindice, rope, cache,
+                                                                   **block_kwargs)
+        if res is not None:
+            x, cache = res
+        else:
+            for lidx in range(start, end):
+                x, cache = self.run_dinov3_correct_block(lidx, x, dindice, rope, cache, f"layer{lidx}",
+                                                         source_key=f"layer{lidx}", **block_kwargs)
         context["current_feature"] = x
         context["cache_feature"] = cache
         return self.dinov3_correct_event_metadata()

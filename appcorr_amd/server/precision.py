@@ -66,6 +66,26 @@ class DINOv3CorrectPrecisionController:
                 cache[key] = value.to(torch.bfloat16)
         return out, cache
 
+    def run_blocks_packed(self, layer_range: range, x: torch.Tensor, dindice: torch.Tensor, rope: Any,
+                          cache: Dict[str, Any], **kwargs: Any):
+        """The blocks of layer_range in one packed correction run (the selected rows stay packed between
+        blocks; bit-identical to run_block over the same layers). Records the same per-layer routes as
+        run_block. Returns None, with nothing run or recorded, when the query plan is per-layer."""
+        from appcorr_amd.dinov3.layers import correct_blocks_packed
+
+        if kwargs.get("appcorr_method", "partial_token") != "partial_token":
+            return None
+        blocks = [self.blocks[i] for i in layer_range]
+        tags = [f"layer{i}" for i in layer_range]
+        with torch.no_grad():
+            res = correct_blocks_packed(blocks, x, dindice, rope, cache, tags, **kwargs)
+        if res is None:
+            return None
+        rows = int(x.shape[0] * x.shape[1]) if x.dim() == 3 else int(x.shape[0])
+        for i in layer_range:
+            self._event_routes[f"layer{i}"] = (self._effective_precision(), rows)
+        return res
+
     def event_metadata(self) -> Dict[str, Any]:
         eff = {p for p, _ in self._event_routes.values()}
         effective = "none" if not eff else (next(iter(eff)) if len(eff) == 1 else "mixed")

@@ -126,6 +126,23 @@ int oudjat_reconstruct_scatter_persist(const uint16_t* x, uint16_t* blocks_out_s
                                        const uint16_t* x_attn, const uint16_t* mlp, int64_t rows,
                                        int64_t C, uint16_t* x_out, oudjat_stream_t stream);
 
+/* Rows 14-16, selected half, for selected rows kept packed across blocks (the executor's multi-block
+ * correction, dinov3_classifier.py:591-663 over block.py:1140-1179): for packed row i
+ *   x_new[i] = bf16(x_attn[i] + mlp[i]);  bos[b_i, t_i] = bf16(bf16(x_attn[i] - x_act[i]) + mlp[i])
+ * with b_i = batch_idx[i], t_i = token_idx[i]; bos addressed with element strides (b, n). */
+int oudjat_packed_residual_persist(const uint16_t* x_act, const uint16_t* x_attn, const uint16_t* mlp,
+                                   int64_t rows, int64_t C, const int64_t* batch_idx,
+                                   const int64_t* token_idx, uint16_t* bos, int64_t bos_stride_b,
+                                   int64_t bos_stride_n, uint16_t* x_new, oudjat_stream_t stream);
+
+/* Row 14 over a run of n_blocks correction blocks (block.py:1143-1149 applied block after block):
+ * x, out [rows, C] (rows = B*N, contiguous; out may alias x); row r with row_slot[r] >= 0 takes
+ * x_packed[row_slot[r]]; every other row takes x + bos_0 + ... + bos_{n-1} rounded to bf16 after
+ * each addition, bos_rows = device array of n_blocks pointers to [rows, C] blocks_out_sum tensors. */
+int oudjat_fold_residual_rows(const uint16_t* x, int64_t rows, int64_t C, const int32_t* row_slot,
+                              const uint16_t* x_packed, const uint16_t* const* bos_rows,
+                              int64_t n_blocks, uint16_t* out, oudjat_stream_t stream);
+
 /* Row 12 -- out = bf16(x + attn * gamma[c]) over [rows, C] contiguous.
  * Replaces fused_layerscale_add (token_update.py:10-60). */
 int oudjat_fused_layerscale_add(const uint16_t* x, const uint16_t* attn, const uint16_t* gamma,

@@ -1,0 +1,162 @@
+"""Selected rows kept packed across a run of correction blocks: bit-identical to the block-by-block path.
+
+The per-block path (gather -> block -> reconstruct_scatter_persist, block.py:1111-1179, for each layer
+of the executor loop dinov3_classifier.py:591-663) is itself checked against the oracle elsewhere;
+here the packed run (packed_residual_persist per block, one fold_residual_rows at the end) must give
+the same bits for the output tokens, every layer's K/V cache and every layer's blocks_out_sum.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from appcorr_amd import kernels as K
+from appcorr_amd.dinov3.layers import SelfAttentionBlock, correct_blocks_packed
+from appcorr_amd.server.dinov3_classifier import DINOv3ClassifierExecutor, make_group_plan
+from appcorr_amd.server.protocol import ExperimentConfig
+from tests.util import assert_bits_equal
+
+pytestmark = pytest.mark.gpu
+
+
+def _rand_bf16(shape, seed, scale=1.0):
+    g = torch.Generator().manual_seed(seed)
+    return (torch.randn(shape, generator=g) * scale).to(torch.bfloat16)
+
+
+@pytest.mark.parametrize("B,N,C,M,L", [(16, 261, 1024, 1104, 24), (2, 9, 8, 5, 0), (3, 7, 16, 7, 1),
+                                       (2, 33, 24, 20, 5), (1, 201, 384, 0, 3)])
+def test_fold_equals_blockwise_reconstruct(dev, B, N, C, M, L):
+    """L blocks of random corrections: per block reconstruct_scatter_persist over the full tensor vs
+    packed_residual_persist on the packed rows and one fold at the end (bit-exact, both the
+    outputs and every blocks_out_sum)."""
+    rng = np.random.default_rng(B * 1000 + N + L)
+    flat = np.sort(rng.choice(B * N, M, replace=False))
+    bi = torch.from_numpy(flat // N).to(dev)
+    ti = torch.from_numpy(flat % N).to(dev)
+    row_slot = torch.full((B * N,), -1, dtype=torch.int32)
+    row_slot[torch.from_numpy(flat)] = torch.arange(M, dtype=torch.int32)
+    row_slot = row_slot.view(B, N).to(dev)
+    x = _rand_bf16((B, N, C), 1).to(dev)
+    bos0 = [_rand_bf16((B, N, C), 10 + i, 0.1).to(dev) for i in range(L)]
+    upd = [(_rand_bf16((M, C), 100 + i, 0.5).to(dev), _rand_bf16((M, C), 200 + i, 0.2).to(dev)) for i in range(L)]
+
+    # block by block over the full tensor
+    xr, bos_r = x.clone(), [b.clone() for b in bos0]
+    for i in range(L):
+        x_act = K.gather_rows(xr, bi, ti) if M else xr.new_empty((0, C))
+        x_attn = (x_act.float() + upd[i][0].float()).to(torch.bfloat16)
+        xr = K.reconstruct_scatter_persist(xr, bos_r[i], row_slot, x_act, x_attn, upd[i][1])
+
+    # packed
+    bos_p = [b.clone() for b in bos0]
+    xp = K.gather_rows(x, bi, ti) if M else x.new_empty((0, C))
+    for i in range(L):
+        x_attn = (xp.float() + upd[i][0].float()).to(torch.bfloat16)
+        if M:
+            xp = K.packed_residual_persist(xp, x_attn, upd[i][1], bi, ti, bos_p[i])
+    out = K.fold_residual_rows(x, row_slot, xp, bos_p)
+    assert_bits_equal(out, xr.cpu(), "x_out")
+    for i in range(L):
+        assert_bits_equal(bos_p[i], bos_r[i].cpu(), f"blocks_out_sum[{i}]")
+    # in place (out aliases x)
+    x2 = x.clone()
+    assert K.fold_residual_rows(x2, row_slot, xp, bos_p, out=x2).data_ptr() == x2.data_ptr()
+    assert_bits_equal(x2, xr.cpu(), "x_out in place")
+
+
+def _executor(dev, bb, B, keep, server_w, layers):
+    img = 256
+    grid = img // 16
+    P = grid * grid
+    N = 5 + P
+    config = ExperimentConfig(model_name=f"dinov3_classifier_{bb}", batch_size=B, image_shape=(img, img, 3),
+                              backbone=bb, appcorr_kwargs={
+                                  "method": "partial_token", "token_keep_ratio": keep,
+                                  "mobile_pscore": "residual_energy", "mobile_pscore_weight": 1.0,
+                                  "server_pscore_weight": server_w, "pscore_fusion": "add"})
+    torch.manual_seed(0)
+    ex = DINOv3ClassifierExecutor(dev)
+    ex.load_model(config.model_name, config)
+    C = ex.model.embed_dim
+    g = torch.Generator(device=dev).manual_seed(3)
+    x_base = torch.randn(B, N, C, generator=g, device=dev)
+    delta = torch.randn(B, P, C, generator=g, device=dev)
+    x_full = x_base.clone()
+    x_full[:, 5:] += delta
+    context = {"input_tokens": x_base.to(torch.bfloat16).contiguous(), "rope_sincos": ex.model.rope_embed(H=grid, W=grid)}
+    dind = torch.arange(N, device=dev).unsqueeze(0).expand(B, -1).contiguous()
+    context["group_plans"] = {1: make_group_plan(dind, 5)}
+    with torch.no_grad():
+        ex.approx_forward({"layers": layers}, context, config)
+    context["input_tokens"] = x_full.to(torch.bfloat16).contiguous()
+    context["mobile_pscore_hint_map"] = K.patch_importance(delta)
+    return ex, config, context
+
+
+def _clone_context(ctx):
+    out = dict(ctx)
+    out["cache_feature"] = {k: (v.clone() if torch.is_tensor(v) else v) for k, v in ctx["cache_feature"].items()}
+    SelfAttentionBlock._invalidate_partial_token_derived_caches(out["cache_feature"])
+    return out
+
+
+@pytest.mark.parametrize("bb,B,keep,layers", [("vitl16", 16, 0.25, (0, 4)), ("vits16", 3, 0.1, (0, 12)),
+                                              ("vitb16", 2, 0.0, (2, 5))])
+def test_executor_packed_run_bit_identical(dev, bb, B, keep, layers):
+    ex, config, ctx = _executor(dev, bb, B, keep, 0.0, layers)
+    params = {"layers": layers, "group_id": 1}
+    ca, cb = _clone_context(ctx), _clone_context(ctx)
+    print(f"case {bb} B={B} keep={keep} layers={layers}", flush=True)
+    with torch.no_grad():
+        ex.packed_correction = True
+        meta_a = ex.correct_forward(params, ca, config)
+        ex.packed_correction = False
+        meta_b = ex.correct_forward(params, cb, config)
+    assert meta_a == meta_b
+    assert_bits_equal(ca["current_feature"], cb["current_feature"].cpu(), "x_out")
+    for i in range(*layers):
+        for key in (f"layer{i}_kv", f"layer{i}_blocks_out_sum", f"layer{i}_combined_pscore"):
+            assert_bits_equal(ca["cache_feature"][key], cb["cache_feature"][key].cpu(), key)
+    sa = {k: float(v) for k, v in ca["cache_feature"].items() if k.startswith("_token_prune")}
+    sb = {k: float(v) for k, v in cb["cache_feature"].items() if k.startswith("_token_prune")}
+    assert sa == sb
+
+
+def test_packed_run_declines_per_layer_plans(dev):
+    """A layer-dependent server score (cls_attn_prob, weight 1) gives each block its own plan: the
+    packed run declines before computing or caching anything, and the executor runs block by block."""
+    ex, config, ctx = _executor(dev, "vits16", 2, 0.25, 1.0, (0, 3))
+    c = _clone_context(ctx)
+    before = dict(c["cache_feature"])
+    res = correct_blocks_packed(list(ex.model.blocks[:3]), c["input_tokens"], ctx["group_plans"][1].pruned_dindice,
+                                c["rope_sincos"], c["cache_feature"], ["layer0", "layer1", "layer2"],
+                                server_pscore_weight=1.0, server_pscore="cls_attn_prob", token_keep_ratio=0.25)
+    assert res is None
+    assert c["cache_feature"].keys() == before.keys()
+    assert all(c["cache_feature"][k] is before[k] for k in before)
+    ca, cb = _clone_context(ctx), _clone_context(ctx)
+    with torch.no_grad():
+        ex.packed_correction = True
+        ex.correct_forward({"layers": (0, 3), "group_id": 1}, ca, config)
+        ex.packed_correction = False
+        ex.correct_forward({"layers": (0, 3), "group_id": 1}, cb, config)
+    assert_bits_equal(ca["current_feature"], cb["current_feature"].cpu(), "x_out")
+
+
+def test_packed_run_in_place(dev):
+    ex, config, ctx = _executor(dev, "vits16", 2, 0.25, 0.0, (0, 2))
+    ca, cb = _clone_context(ctx), _clone_context(ctx)
+    blocks = list(ex.model.blocks[:2])
+    dind = ctx["group_plans"][1].pruned_dindice
+    kw = dict(token_keep_ratio=0.25, mobile_pscore="residual_energy", mobile_pscore_weight=1.0,
+              mobile_pscore_hint=ctx["mobile_pscore_hint_map"], server_pscore_weight=0.0)
+    xa = ca["input_tokens"].clone()
+    with torch.no_grad():
+        out_a, _ = correct_blocks_packed(blocks, xa, dind, ca["rope_sincos"], ca["cache_feature"],
+                                         ["layer0", "layer1"], inplace_residual_add=True, **kw)
+        xb = cb["input_tokens"].clone()
+        for i, blk in enumerate(blocks):
+            xb, _ = blk.correct(xb, dind, cb["rope_sincos"], cb["cache_feature"], f"layer{i}", **kw)
+    assert out_a.data_ptr() == xa.data_ptr()
+    assert_bits_equal(out_a, xb.cpu(), "x_out")
