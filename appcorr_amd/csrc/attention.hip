@@ -20,6 +20,10 @@
 // shape: 9 waves, 256 workgroups for B*H = 256, one per CU); larger T is split evenly over several
 // workgroups. K/V tiles of 64 keys are double-buffered in LDS with the next tile's global loads in
 // flight during the current tile's MFMAs, so each (image, head) streams its K/V once.
+#include <stdlib.h>
+
+#include <type_traits>
+
 #include "common.hpp"
 
 namespace oudjat {
@@ -35,6 +39,14 @@ typedef float f32x8_t __attribute__((ext_vector_type(8)));
 __device__ __forceinline__ bf16x8_t pack_bf16x8(const float* f) {
   const f32x8_t v = {f[0], f[1], f[2], f[3], f[4], f[5], f[6], f[7]};
   return __builtin_convertvector(v, bf16x8_t);
+}
+
+// Reference maximum of the online softmax: it moves to the running maximum only when that exceeds it
+// by more than 8 in the exp2 domain (and always from -inf), so most tiles keep the same reference and
+// skip rescaling the output; probabilities stay below 2^8 and the final O / l is unchanged.
+__device__ __forceinline__ float softmax_ref_max(float m_ref, float tile_max, float scale_log2) {
+  const float m_run = fmaxf(m_ref, tile_max);
+  return (m_run - m_ref) * scale_log2 > 8.0f ? m_run : m_ref;
 }
 
 // MINW: fewest waves a launch of this instance uses (sizes the per-thread share of a K/V tile);
@@ -174,8 +186,8 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
       for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
     mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
     // exp2 is the bare v_exp_f32 (no subnormal range reduction: a probability below 2^-126 adds
-    // nothing to a sum that contains 1).
-    const float m_new = fmaxf(m_i, mx);
+    // nothing to a sum that contains a term >= 1).
+    const float m_new = softmax_ref_max(m_i, mx, scale_log2);
     const float alpha = __builtin_amdgcn_exp2f((m_i - m_new) * scale_log2);
     const float mc = m_new * scale_log2;
     float rs = 0.0f;
@@ -272,6 +284,238 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
   }
 }
 
+
+// ------------------------------------------------------------------------------------------------
+// Dh = 64, >= 8 waves: K and V tiles reach LDS by buffer loads straight from the cache (no register
+// staging), both in their natural [key][dim] rows, NST stages deep. Waves 0..7 each load 8 rows of K
+// and 8 rows of V per tile (one 1 KB instruction each); keys past N fall outside the per-(image,
+// head) descriptors and load as zeros (their scores are masked). The A operand of O^T += V^T . P^T
+// comes from V's rows through the LDS transpose read: in each 16-lane group, source lane s addresses
+// 4 dims (8 bytes) of key k0 + s / 4 at dim c0 + 4 (s % 4), and lane j receives dim c0 + j for keys
+// k0 .. k0 + 3. Rows are 128 bytes; 16-byte chunk c of key row r sits in slot c ^ ((r >> 1) & 7) so
+// the K fragment reads (32 consecutive keys at one chunk) cover all 64 banks.
+// The arithmetic (MFMA order, softmax, P rounding) is that of sq_attention_kernel, so both give
+// bit-identical outputs.
+// ------------------------------------------------------------------------------------------------
+
+__device__ __forceinline__ int kv_slot(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
+
+template <int NST>
+__global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
+    const uint16_t* __restrict__ q, int64_t qrs, int T, const uint16_t* __restrict__ kv, int64_t kvb, int64_t kvn,
+    int64_t kvkv, int64_t kvh, int N, float scale_log2, uint16_t* __restrict__ out, int64_t ors,
+    int waves_per_wg) {
+  constexpr int DH = 64, QK_STEPS = 4, OB = 2;
+  constexpr int TILEB = kKeyTile * 128;  // one K (or V) tile: 64 rows of 128 bytes
+  constexpr int STAGE = 2 * TILEB;
+  static_assert(NST >= 2, "stages");
+  typedef short i16x4_t __attribute__((ext_vector_type(4)));
+
+  extern __shared__ __align__(16) unsigned char smem[];
+
+  const int b = blockIdx.z, h = blockIdx.y;
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int l32 = lane & 31, g = lane >> 5;
+  const int q0 = (blockIdx.x * waves_per_wg + wave) * 32;
+  const bool active = q0 < T;
+
+  bf16x8_t qf[QK_STEPS];
+  {
+    const int qr = q0 + l32;
+#pragma unroll
+    for (int ks = 0; ks < QK_STEPS; ++ks) {
+      uint4 v = make_uint4(0, 0, 0, 0);
+      if (qr < T) v = *reinterpret_cast<const uint4*>(q + ((int64_t)b * T + qr) * qrs + (int64_t)h * DH + ks * 16 + 8 * g);
+      qf[ks] = as_bf16x8(v);
+    }
+  }
+  f32x16_t o[OB];
+#pragma unroll
+  for (int d = 0; d < OB; ++d)
+#pragma unroll
+    for (int v = 0; v < 16; ++v) o[d][v] = 0.0f;
+  float m_i = -INFINITY, l_i = 0.0f;
+
+  const uint16_t* kbase = kv + (int64_t)b * kvb + (int64_t)h * kvh;
+  const uint32_t bytes = (uint32_t)((int64_t)N * kvn * 2);
+  const i32x4_t rsrc_k = make_buffer_rsrc(kbase, bytes);
+  const i32x4_t rsrc_v = make_buffer_rsrc(kbase + kvkv, bytes);
+  const bool loader = wave < 8;
+  const int lrow = 8 * wave + (lane >> 3);                  // tile row this lane loads
+  const uint32_t off0 = (uint32_t)lrow * (uint32_t)kvn * 2u + (uint32_t)((((lane & 7) ^ ((lrow >> 1) & 7))) << 4);
+  const uint32_t tstep = (uint32_t)kKeyTile * (uint32_t)kvn * 2u;
+  const int ntiles = (N + kKeyTile - 1) / kKeyTile;
+  auto issue = [&](int stage, int t) __attribute__((always_inline)) {
+    if (loader) {
+      unsigned char* base = smem + stage * STAGE + wave * 1024;
+      buffer_load_lds16(rsrc_k, base, off0 + (uint32_t)t * tstep);
+      buffer_load_lds16(rsrc_v, base + TILEB, off0 + (uint32_t)t * tstep);
+    }
+  };
+  // At most n tiles after the one needed may still be in flight (two loads per tile per loader).
+  static_assert(NST <= 5, "wait_tiles covers up to three tiles in flight");
+  auto wait_tiles = [&](int n) __attribute__((always_inline)) {
+    if (n <= 0) wait_vmcnt<0>();
+    else if (n == 1) wait_vmcnt<2>();
+    else if (n == 2) wait_vmcnt<4>();
+    else wait_vmcnt<6>();
+  };
+
+  // Per-lane LDS offsets, fixed for the whole loop: the swizzle of a key row depends only on
+  // (key >> 1) & 7, which is the same for key and key + 16 j (and key + 32 kb), so the k-step / key
+  // block / stage parts of every fragment address are compile-time offsets.
+  int koff[QK_STEPS];
+#pragma unroll
+  for (int kstep = 0; kstep < QK_STEPS; ++kstep) koff[kstep] = kv_slot(l32, kstep * 2 + g);
+  int voff[OB][2];
+  {
+    const int sl = lane & 15, hh = (lane >> 4) & 1;
+#pragma unroll
+    for (int db = 0; db < OB; ++db) {
+      const int dcol = 32 * db + 16 * hh + 4 * (sl & 3);  // first of the 4 dims this lane addresses
+      const int k1 = 4 * g + (sl >> 2);                   // key of k-step 0 (first run)
+      voff[db][0] = TILEB + kv_slot(k1, dcol >> 3) + ((dcol >> 2) & 1) * 8;
+      voff[db][1] = TILEB + kv_slot(k1 + 8, dcol >> 3) + ((dcol >> 2) & 1) * 8;
+    }
+  }
+
+  // S^T of one tile: s[kb][v] = S^T[key kb*32 + 8(v/4) + 4g + v%4][query l32].
+  struct Scores {
+    f32x16_t s[2];
+  };
+  auto scores = [&](Scores& sc, const unsigned char* st) __attribute__((always_inline)) {
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb) {
+      bf16x8_t kf[QK_STEPS];
+#pragma unroll
+      for (int kstep = 0; kstep < QK_STEPS; ++kstep)
+        kf[kstep] = as_bf16x8(*reinterpret_cast<const uint4*>(st + koff[kstep] + kb * 32 * 128));
+      const f32x16_t zero = {};
+      sc.s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0], zero, 0, 0, 0);
+#pragma unroll
+      for (int kstep = 1; kstep < QK_STEPS; ++kstep)
+        sc.s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kstep], qf[kstep], sc.s[kb], 0, 0, 0);
+    }
+  };
+  // Online softmax of tile t and O^T += V^T . P^T with V from stage `st`.
+  auto finish = [&](Scores& sc, const unsigned char* st, int t) __attribute__((always_inline)) {
+    f32x16_t (&s)[2] = sc.s;
+    if ((t + 1) * kKeyTile > N) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v)
+          if (t * kKeyTile + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3) >= N) s[kb][v] = -INFINITY;
+    }
+    float mx = s[0][0];
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
+    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+    const float m_new = softmax_ref_max(m_i, mx, scale_log2);
+    const float alpha = __builtin_amdgcn_exp2f((m_i - m_new) * scale_log2);
+    const float mc = m_new * scale_log2;
+    float rs = 0.0f;
+#pragma unroll
+    for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+      for (int v = 0; v < 16; ++v) {
+        const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][v], scale_log2, -mc));
+        s[kb][v] = p;
+        rs += p;
+      }
+    rs += __shfl_xor(rs, 32, 64);
+    l_i = l_i * alpha + rs;
+    m_i = m_new;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+      for (int d = 0; d < OB; ++d)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[d][v] *= alpha;
+    }
+    bf16x8_t pf[4];
+#pragma unroll
+    for (int j = 0; j < 4; ++j) {
+      float tmp[8];
+#pragma unroll
+      for (int e = 0; e < 8; ++e) tmp[e] = s[j >> 1][8 * (j & 1) + e];
+      pf[j] = pack_bf16x8(tmp);
+    }
+    // V^T fragment of d-block db, k-step j: elements 0..3 = keys 16j + 4g + {0..3}, elements 4..7 =
+    // keys 16j + 8 + 4g + {0..3}, at dim 32 db + l32 (the P^T order above).
+#pragma unroll
+    for (int db = 0; db < OB; ++db) {
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4_t*)(st + voff[db][0] + j * 16 * 128));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4_t*)(st + voff[db][1] + j * 16 * 128));
+        typedef short i16x8_t __attribute__((ext_vector_type(8)));
+        const i16x8_t both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, both), pf[j], o[db], 0, 0, 0);
+      }
+    }
+  };
+
+  // Iteration t: wait for tile t + 1 (tiles issued so far: 0 .. t + NST - 2), barrier (tile t + 1
+  // visible to every wave; every wave done with tile t - 1's stage), refill that stage with tile
+  // t + NST - 1, issue the S^T MFMAs of tile t + 1, then tile t's softmax (VALU, overlapping those
+  // MFMAs) and its O^T MFMAs. Unrolled by NST so every stage base is a constant.
+  static_assert(NST == 4, "the unrolled loop below is written for four stages");
+#pragma unroll
+  for (int st = 0; st < NST - 1; ++st)
+    if (st < ntiles) issue(st, st);
+  wait_tiles(min(NST - 2, ntiles - 1));
+  block_barrier();
+  Scores sa, sb;
+  if (active) scores(sa, smem);
+  auto step = [&](auto stage_c, int t, Scores& cur, Scores& nxt) __attribute__((always_inline)) {
+    constexpr int SG = decltype(stage_c)::value;  // stage of tile t
+    if (t + 1 < ntiles) {
+      wait_tiles(min(NST - 3, ntiles - 2 - t));
+      block_barrier();
+      if (t + NST - 1 < ntiles) issue((SG + NST - 1) % NST, t + NST - 1);
+      if (active) scores(nxt, smem + ((SG + 1) % NST) * STAGE);
+    }
+    if (active) finish(cur, smem + SG * STAGE, t);
+  };
+  using I0 = std::integral_constant<int, 0>;
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I3 = std::integral_constant<int, 3>;
+  int t = 0;
+  for (; t + NST <= ntiles; t += NST) {
+    step(I0{}, t, sa, sb);
+    step(I1{}, t + 1, sb, sa);
+    step(I2{}, t + 2, sa, sb);
+    step(I3{}, t + 3, sb, sa);
+  }
+  if (t < ntiles) step(I0{}, t, sa, sb);
+  if (t + 1 < ntiles) step(I1{}, t + 1, sb, sa);
+  if (t + 2 < ntiles) step(I2{}, t + 2, sa, sb);
+
+  const int qr = q0 + l32;
+  if (active && qr < T) {
+    const float inv = 1.0f / l_i;
+    uint16_t* orow = out + ((int64_t)b * T + qr) * ors + (int64_t)h * DH;
+#pragma unroll
+    for (int d = 0; d < OB; ++d)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+        bf16x4_t w;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w[e] = (__bf16)(o[d][4 * r4 + e] * inv);
+        *reinterpret_cast<bf16x4_t*>(orow + d * 32 + 8 * r4 + 4 * g) = w;
+      }
+  }
+}
+
+static constexpr int kAttnStages = 4;
+
 }  // namespace oudjat
 
 using namespace oudjat;
@@ -300,6 +544,21 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
   if (w < kMinWaves) w = kMinWaves;
   dim3 grid((unsigned)n_wg, (unsigned)H, (unsigned)B);
   hipStream_t st = as_stream(stream);
+  // Buffer-load kernel for Dh = 64 with >= 8 waves (its byte offsets must fit 31 bits); the
+  // register-staged kernel otherwise (or when OUDJAT_ATTN_STAGED is set, for comparisons).
+  const bool staged_forced = getenv("OUDJAT_ATTN_STAGED") != nullptr;
+  const bool dma = Dh == 64 && w >= 8 && !staged_forced && N * kvn * 2 < ((int64_t)1 << 31);
+  if (dma) {
+    const size_t lds_dma = (size_t)kAttnStages * 2 * kKeyTile * 128;
+    const void* fd = (const void*)sq_attention_dma_kernel<kAttnStages>;
+    if (lds_dma > 64 * 1024) {
+      hipError_t e = hipFuncSetAttribute(fd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_dma);
+      if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "sparse_query_attention: %s", hipGetErrorString(e));
+    }
+    sq_attention_dma_kernel<kAttnStages><<<grid, w * 64, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,
+                                                                         (int)N, scale_log2, out, ors, w);
+    return check_launch("sparse_query_attention");
+  }
   const void* fn = Dh == 128 ? (const void*)sq_attention_kernel<128, kMinWaves, false>
                   : w >= 8  ? (const void*)sq_attention_kernel<64, 8, true>
                             : (const void*)sq_attention_kernel<64, kMinWaves, false>;

@@ -104,6 +104,45 @@ inline bool aligned(const void* p, int64_t a) { return (reinterpret_cast<uintptr
 
 inline int64_t cdiv(int64_t a, int64_t b) { return (a + b - 1) / b; }
 
+// ---- direct-to-LDS loads and their waits (shared by the GEMM and attention kernels) ----------------
+
+// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt in bits 3:0 and
+// 15:14, expcnt 6:4 and lgkmcnt 11:8 at their maxima).
+template <int N>
+__device__ __forceinline__ void wait_vmcnt() {
+  static_assert(N >= 0 && N < 64, "vmcnt range");
+  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
+}
+
+// Workgroup barrier without the vmcnt(0) of __syncthreads() (which would drain the loads in flight
+// for later tiles): LDS reads are complete (lgkmcnt(0)), then s_barrier. The scheduling barriers
+// keep the compiler from moving memory operations across it.
+__device__ __forceinline__ void block_barrier() {
+  __builtin_amdgcn_sched_barrier(0);
+  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0), vmcnt/expcnt unconstrained
+  __builtin_amdgcn_s_barrier();
+  __builtin_amdgcn_sched_barrier(0);
+}
+
+// Buffer descriptor of a raw byte range (stride 0, bounds-checked against `bytes`: loads past it
+// return zeros) and the 16-byte-per-lane buffer load into LDS (lane l's bytes land at lds + 16 l).
+typedef int i32x4_t __attribute__((ext_vector_type(4)));
+__device__ void llvm_raw_buffer_load_lds(i32x4_t rsrc, __attribute__((address_space(3))) void* lds, int size,
+                                         int voffset, int soffset, int offset,
+                                         int aux) __asm("llvm.amdgcn.raw.buffer.load.lds");
+__device__ __forceinline__ i32x4_t make_buffer_rsrc(const void* base, uint32_t bytes) {
+  const uint64_t a = reinterpret_cast<uint64_t>(base);
+  i32x4_t r;
+  r[0] = (int)(uint32_t)a;
+  r[1] = (int)((uint32_t)(a >> 32) & 0xffffu);  // base[47:32], stride 0
+  r[2] = (int)bytes;
+  r[3] = 0x00020000;                            // 32-bit data format, no swizzle
+  return r;
+}
+__device__ __forceinline__ void buffer_load_lds16(i32x4_t rsrc, unsigned char* lds, uint32_t voffset) {
+  llvm_raw_buffer_load_lds(rsrc, (__attribute__((address_space(3))) void*)lds, 16, (int)voffset, 0, 0, 0);
+}
+
 }  // namespace oudjat
 
 #define OUDJAT_REQUIRE(cond, status, ...)                 \

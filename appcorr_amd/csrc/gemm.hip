@@ -25,6 +25,7 @@
 // Linear: bias, exact-erf GELU (fc1), LayerScale (fc2), LayerScale + residual (proj) and the SwiGLU
 // gate, with a bf16 rounding at every point where the reference materialises a bf16 tensor.
 #include <math.h>
+#include <stdio.h>
 #include <stdlib.h>
 #include <string.h>
 
@@ -90,6 +91,22 @@ __device__ __forceinline__ uint32_t gelu_bf16_bits(uint32_t b, const uint16_t* l
   if (a < kGeluLo) return a >= 0x0100u ? b - 0x80u : (b & 0x8000u);
   if ((b >> 15) == 0u) return b;
   return a == 0x7f80u ? 0x7fc0u : (a > 0x7f80u ? b : 0x8000u);
+}
+
+// Two bf16 GELUs per 32-bit word through the table, without branches in the common case: the
+// packed 16-bit index (sign * span + clamped magnitude offset) is computed for both halves at once
+// and both table entries are read unconditionally; `ok` is false when either half lies outside the
+// table range, and the caller then redoes that word with gelu_bf16_bits.
+typedef unsigned short u16x2_t __attribute__((ext_vector_type(2)));
+__device__ __forceinline__ uint32_t gelu_pair_bits(uint32_t w, const uint16_t* lut, bool& ok) {
+  const u16x2_t v = __builtin_bit_cast(u16x2_t, w);
+  const u16x2_t mag = v & (u16x2_t)(0x7fff);
+  const u16x2_t d = mag - (u16x2_t)(kGeluLo);                           // wraps below the range
+  const u16x2_t dc = __builtin_elementwise_min(d, (u16x2_t)(kGeluSpan - 1));
+  const u16x2_t idx = (v >> (u16x2_t)(15)) * (u16x2_t)(kGeluSpan) + dc;  // < 2 * kGeluSpan
+  ok = __builtin_bit_cast(uint32_t, dc) == __builtin_bit_cast(uint32_t, d);
+  const uint32_t lo = lut[idx.x], hi = lut[idx.y];
+  return lo | (hi << 16);
 }
 
 template <int EPI>
@@ -345,17 +362,52 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
     return;
   }
   constexpr int CPR = BN / 8;
+  if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) {
+    // Fully unrolled: all LDS reads of a thread's chunks first, then the table lookups, then the
+    // stores, so the LDS latencies overlap.
+    constexpr int ITERS = (BM * CPR + NT - 1) / NT;
+    uint4 o[ITERS];
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      const int c = threadIdx.x + it * NT;
+      const int cc = c < BM * CPR ? c : BM * CPR - 1;
+      const int rl = cc / CPR, cl = (cc - rl * CPR) * 8;
+      o[it] = *reinterpret_cast<const uint4*>(ct + rl * LDT + cl);
+    }
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      uint32_t* w = reinterpret_cast<uint32_t*>(&o[it]);
+      bool ok0, ok1, ok2, ok3;
+      const uint32_t g0 = gelu_pair_bits(w[0], lut, ok0), g1 = gelu_pair_bits(w[1], lut, ok1);
+      const uint32_t g2 = gelu_pair_bits(w[2], lut, ok2), g3 = gelu_pair_bits(w[3], lut, ok3);
+      const bool ok = ok0 && ok1 && ok2 && ok3;
+      if (__builtin_expect(__builtin_amdgcn_ballot_w64(!ok) != 0, 0)) {
+        if (!ok) {
+#pragma unroll
+          for (int e = 0; e < 4; ++e)
+            w[e] = gelu_bf16_bits(w[e] & 0xffffu, lut) | (gelu_bf16_bits(w[e] >> 16, lut) << 16);
+        } else {
+          w[0] = g0; w[1] = g1; w[2] = g2; w[3] = g3;
+        }
+      } else {
+        w[0] = g0; w[1] = g1; w[2] = g2; w[3] = g3;
+      }
+    }
+#pragma unroll
+    for (int it = 0; it < ITERS; ++it) {
+      const int c = threadIdx.x + it * NT;
+      const int rl = c / CPR, cl = (c - rl * CPR) * 8;
+      const int row = m0 + rl;
+      if (c < BM * CPR && row < M) *reinterpret_cast<uint4*>(C + (int64_t)row * ldc + n0 + cl) = o[it];
+    }
+    return;
+  }
   for (int c = threadIdx.x; c < BM * CPR; c += NW * 64) {
     const int rl = c / CPR, cl = (c - rl * CPR) * 8;
     const int row = m0 + rl, col = n0 + cl;
     if (row >= M) continue;
     uint4 o = *reinterpret_cast<const uint4*>(ct + rl * LDT + cl);
-    if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) {
-      uint32_t* w = reinterpret_cast<uint32_t*>(&o);
-#pragma unroll
-      for (int e = 0; e < 4; ++e)
-        w[e] = gelu_bf16_bits(w[e] & 0xffffu, lut) | (gelu_bf16_bits(w[e] >> 16, lut) << 16);
-    } else if constexpr (EPI != OUDJAT_EPI_BIAS && EPI != kEpiQkv) {
+    if constexpr (EPI != OUDJAT_EPI_BIAS && EPI != kEpiQkv) {
       // 16-byte loads of the per-column gamma and the residual / gate row segment.
       float v[8], g[8], r[8];
       unpack8(o, v);
@@ -557,13 +609,6 @@ static constexpr int kStages = 4;
 
 __device__ __forceinline__ int swz64(int r, int c) { return r * 64 + ((c ^ ((r >> 2) & 3)) << 4); }
 
-// s_waitcnt with only the vector-memory counter constrained (gfx9 encoding: vmcnt in bits 3:0 and
-// 15:14, expcnt 6:4 and lgkmcnt 11:8 at their maxima).
-template <int N>
-__device__ __forceinline__ void wait_vmcnt() {
-  static_assert(N >= 0 && N < 64, "vmcnt range");
-  __builtin_amdgcn_s_waitcnt((N & 15) | (7 << 4) | (15 << 8) | ((N >> 4) << 14));
-}
 __device__ __forceinline__ void wait_vmcnt_rt(int n) {
   switch (n) {
     case 0: wait_vmcnt<0>(); break;
@@ -592,16 +637,6 @@ __device__ __forceinline__ void wait_vmcnt_rt(int n) {
     case 23: wait_vmcnt<23>(); break;
     default: wait_vmcnt<24>(); break;
   }
-}
-
-// Workgroup barrier without the vmcnt(0) of __syncthreads() (which would drain the loads in flight
-// for later K tiles): LDS reads are complete (lgkmcnt(0)), then s_barrier. The scheduling barriers
-// keep the compiler from moving memory operations across it.
-__device__ __forceinline__ void block_barrier() {
-  __builtin_amdgcn_sched_barrier(0);
-  __builtin_amdgcn_s_waitcnt(15 | (7 << 4) | (0 << 8) | (3 << 14));  // lgkmcnt(0), vmcnt/expcnt unconstrained
-  __builtin_amdgcn_s_barrier();
-  __builtin_amdgcn_sched_barrier(0);
 }
 
 // LDS bytes of the pipelined kernel before the GELU table: K stages or the epilogue tile.
@@ -704,18 +739,16 @@ void gemm_bf16_pipe_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t
 #pragma unroll
     for (int j = 0; j < FN; ++j) f.b[1][j] = *reinterpret_cast<const bf16x8_t*>(st + b_lane + j * 2048 + co1);
   };
-  // Row blocks entirely below M (the last tile row of a ragged M) skip their MFMAs.
-  const int rows_left = M - m0 - wm0;
+  // Row blocks at or past M (ragged last tile row) compute on clamped A rows and are never stored;
+  // a branch per row block would drain the prefetched fragments at every block boundary.
   auto mfmas = [&](const Frags& f) __attribute__((always_inline)) {
 #pragma unroll
     for (int ks = 0; ks < 2; ++ks)
 #pragma unroll
       for (int i = 0; i < FM; ++i)
-        if (i * 32 < rows_left) {
 #pragma unroll
-          for (int j = 0; j < FN; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[ks][j], f.a[ks][i], acc[i][j], 0, 0, 0);
-        }
+        for (int j = 0; j < FN; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(f.b[ks][j], f.a[ks][i], acc[i][j], 0, 0, 0);
   };
   // Wait until at most `n_after` K tiles of this wave's loads are still in flight.
   auto wait_tiles = [&](int n_after) __attribute__((always_inline)) {
@@ -769,9 +802,10 @@ void gemm_bf16_pipe_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t
 // last one 31 % full). Tiles of 144 rows (9 blocks of 16) on v_mfma_f32_16x16x32_bf16 cover it
 // exactly: fc1 as 29 x 8 tiles of 144 x 512, the N = C GEMMs as 29 x 8 tiles of 144 x 128 -- 232
 // workgroups, one round on 256 CUs.
-//   * Every wave owns all BM rows and a BN / WGN column strip; with KSPLIT = 2 two wave groups take
-//     alternate 32-deep halves of each K tile (doubling the waves per CU for the narrow N = C tiles)
-//     and are summed through LDS at the end.
+//   * Waves form a WGM x WGN grid of BM / WGM-row, BN / WGN-column wave tiles; with KSPLIT = 2 two
+//     such grids take alternate 32-deep halves of each K tile (doubling the waves per CU for the
+//     narrow N = C tiles) and are summed through LDS at the end. With WGM = 2 (288-row tiles of two
+//     144-row halves) the epilogue stages one half at a time through LDS.
 //   * K tiles of BK (32 or 64) in NST LDS stages, direct-to-LDS loads issued NST - 1 tiles ahead,
 //     fragments read one K tile ahead of their MFMAs, one barrier per K tile.
 //   * Rows are 2 * BK bytes; chunk c of row r sits at 16-byte slot c ^ ((r / L) % CPRW) with
@@ -790,39 +824,40 @@ struct R16Layout {
   }
 };
 
-// LDS bytes before the GELU table: K stages, the KSPLIT reduction buffer plus the bf16 tile, or the
-// bf16 tile alone.
-__host__ __device__ constexpr int r16_lut_offset(int bm, int bn, int bk, int nst, int ksplit, int nw) {
+// LDS bytes before the GELU table: K stages, or the KSPLIT reduction buffer plus the bf16 tile of one
+// wave row (BM / WGM rows), whichever is larger.
+__host__ __device__ constexpr int r16_lut_offset(int bm, int bn, int wgm, int wgn, int ksplit, int bk, int nst) {
   const int stages = nst * (bm + bn) * 2 * bk;
-  const int tile = bm * (bn + 8) * 2;
-  const int red = ksplit > 1 ? (nw / ksplit) * 64 * (bm * (bn / (nw / ksplit)) / 64) * 4 : 0;  // fp32 partials
+  const int tile = (bm / wgm) * (bn + 8) * 2;
+  const int red = ksplit > 1 ? wgm * wgn * 64 * (bm / wgm / 16) * (bn / wgn / 16) * 4 * 4 : 0;  // fp32 partials
   const int epi = red + tile;
   return stages > epi ? stages : epi;
 }
 
 // FB: fragments read one K tile ahead (double-buffered registers); without it they are read right
 // after the barrier of their own K tile (for wave tiles whose accumulators leave no room).
-template <int BM, int BN, int WGN, int KSPLIT, int BK, int NST, bool FB, int EPI>
-__global__ __launch_bounds__(WGN * KSPLIT * 64) __attribute__((amdgpu_waves_per_eu((WGN * KSPLIT + 3) / 4,
-                                                                                    (WGN * KSPLIT + 3) / 4)))
+template <int BM, int BN, int WGM, int WGN, int KSPLIT, int BK, int NST, bool FB, int EPI>
+__global__ __launch_bounds__(WGM * WGN * KSPLIT * 64) __attribute__((amdgpu_waves_per_eu(
+    (WGM * WGN * KSPLIT + 3) / 4, (WGM * WGN * KSPLIT + 3) / 4)))
 void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t lda, const uint16_t* __restrict__ W,
                           int N, int64_t ldw, EpiArgs ea, uint16_t* __restrict__ C, int64_t ldc, int group_m) {
   using L = R16Layout<BK>;
-  constexpr int NW = WGN * KSPLIT;
+  constexpr int NWG = WGM * WGN;                  // waves of one K group
+  constexpr int NW = NWG * KSPLIT;
   constexpr int NT = NW * 64;
-  constexpr int WN = BN / WGN;
-  constexpr int FMB = BM / 16, FNB = WN / 16;     // 16 x 16 blocks per wave
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int FMB = WM / 16, FNB = WN / 16;     // 16 x 16 blocks per wave
   constexpr int SUB = BK / 32;                    // 32-deep MFMA steps per K tile
   constexpr int SUBW = SUB / KSPLIT;              // ... per wave
   constexpr int NI = (BM + BN) / L::kRowsPerLoad; // load instructions per K tile
   constexpr int NLM = (NI + NW - 1) / NW;
   constexpr int STAGE = (BM + BN) * L::kRowBytes;
   static_assert(BM % L::kRowsPerLoad == 0 && BN % L::kRowsPerLoad == 0, "rows must fill whole load instructions");
-  static_assert(SUB % KSPLIT == 0 && SUBW >= 1 && WN % 16 == 0 && NST >= 2, "tile shape");
+  static_assert(SUB % KSPLIT == 0 && SUBW >= 1 && WM % 16 == 0 && WN % 16 == 0 && NST >= 2, "tile shape");
   typedef float f32x4v __attribute__((ext_vector_type(4)));
 
   extern __shared__ __align__(16) unsigned char smem[];
-  constexpr int kLutOff = r16_lut_offset(BM, BN, BK, NST, KSPLIT, NW);
+  constexpr int kLutOff = r16_lut_offset(BM, BN, WGM, WGN, KSPLIT, BK, NST);
   if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) load_gelu_table<NT>(smem + kLutOff);
 
   const int tiles_n = (N + BN - 1) / BN;
@@ -842,33 +877,61 @@ void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t 
 
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
-  const int kg = wave / WGN;                // K group
-  const int wn0 = (wave % WGN) * WN;        // column strip
+  const int kg = wave / NWG;                // K group
+  const int wr = wave - kg * NWG;           // wave within its K group
+  const int wm = wr / WGN;                  // wave row
+  const int wm0 = wm * WM;                  // first tile row of the wave
+  const int wn0 = (wr % WGN) * WN;          // column strip
 
-  // Loads: instruction i = wave + j * NW fills rows [i * RPL, (i + 1) * RPL) of the stage.
+  // Loads: instruction i = wave + j * NW fills rows [i * RPL, (i + 1) * RPL) of the stage, A rows
+  // first, then W rows, through buffer descriptors: a lane keeps one 32-bit byte offset per operand
+  // (its row within instruction j = 0 plus its swizzled chunk) and instruction j adds j * NW * RPL
+  // rows, so no per-instruction address registers are live across the K loop. A rows at or past M
+  // fall outside the A descriptor and load as zeros.
+  static_assert(NW % 2 == 0, "the chunk swizzle of a lane must not depend on j");
   const int nl = (NI - wave + NW - 1) / NW;
-  const uint16_t* src[NLM];
-  int dst[NLM];
+  const i32x4_t rsrc_a = make_buffer_rsrc(A, (uint32_t)((int64_t)M * lda * 2));
+  const i32x4_t rsrc_w = make_buffer_rsrc(W, (uint32_t)((int64_t)N * ldw * 2));
+  uint32_t voff_a, voff_w;
   {
     const int lrow = lane / L::kChunks, lslot = lane % L::kChunks;
-#pragma unroll
-    for (int j = 0; j < NLM; ++j) {
-      const int i = min(wave + j * NW, NI - 1);
-      const int row = i * L::kRowsPerLoad + lrow;  // stage row (A rows first, then B rows)
-      const int chunk = lslot ^ ((row / L::kRowsPerLine) % L::kChunks);
-      dst[j] = i * 1024;
-      if (row < BM) src[j] = A + (int64_t)min(m0 + row, M - 1) * lda + chunk * 8;
-      else src[j] = W + (int64_t)min(n0 + row - BM, N - 1) * ldw + chunk * 8;
-    }
+    const int row0 = wave * L::kRowsPerLoad + lrow;  // stage row of instruction j = 0
+    const int chunk = lslot ^ ((row0 / L::kRowsPerLine) % L::kChunks);
+    voff_a = (uint32_t)((m0 + row0) * (uint32_t)lda * 2u + chunk * 16);
+    voff_w = (uint32_t)((n0 + row0 - BM) * (uint32_t)ldw * 2u + chunk * 16);
   }
+  const uint32_t step_a = (uint32_t)(NW * L::kRowsPerLoad) * (uint32_t)lda * 2u;
+  const uint32_t step_w = (uint32_t)(NW * L::kRowsPerLoad) * (uint32_t)ldw * 2u;
   auto issue = [&](int stage, int kt) __attribute__((always_inline)) {
     unsigned char* base = smem + stage * STAGE;
-    const int k0 = kt * BK;
+    const uint32_t koff = (uint32_t)(kt * BK * 2);
 #pragma unroll
-    for (int j = 0; j < NLM; ++j)
-      if (j < nl) __builtin_amdgcn_global_load_lds((const void*)(src[j] + k0), (lds_ptr_t)(base + dst[j]), 16, 0, 0);
+    for (int j = 0; j < NLM; ++j) {
+      if (j < NLM - 1 || j < nl) {
+        const int i = wave + j * NW;
+        if (i < BM / L::kRowsPerLoad)
+          buffer_load_lds16(rsrc_a, base + i * 1024, voff_a + (uint32_t)j * step_a + koff);
+        else
+          buffer_load_lds16(rsrc_w, base + i * 1024, voff_w + (uint32_t)j * step_w + koff);
+      }
+    }
   };
-  auto wait_tiles = [&](int n_after) __attribute__((always_inline)) { wait_vmcnt_rt(n_after * nl); };
+  // Waves 0 .. NI % NW - 1 issue NLM loads per tile, the others NLM - 1 (all NLM if NW | NI); the
+  // vmcnt immediates are compile-time per class, so the wait is a uniform branch, not a switch.
+  auto wait_tiles = [&](int n_after) __attribute__((always_inline)) {
+    constexpr int NRED = (NI % NW == 0) ? NLM : NLM - 1;
+    const bool full = (NI % NW == 0) || wave < NI % NW;
+    if (n_after <= 0) {
+      wait_vmcnt<0>();
+    } else if (n_after == 1) {
+      if (full) wait_vmcnt<NLM>(); else wait_vmcnt<NRED>();
+    } else if (n_after == 2) {
+      if (full) wait_vmcnt<2 * NLM>(); else wait_vmcnt<2 * NRED>();
+    } else {
+      static_assert(NST <= 4 && 3 * NLM < 64, "vmcnt range");
+      if (full) wait_vmcnt<3 * NLM>(); else wait_vmcnt<3 * NRED>();
+    }
+  };
 
   f32x4v acc[FMB][FNB];
 #pragma unroll
@@ -887,23 +950,23 @@ void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t 
       const int ch = 4 * (s * KSPLIT + kg) + (lane >> 4);
 #pragma unroll
       for (int i = 0; i < FMB; ++i)
-        f.a[s][i] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(i * 16 + (lane & 15), ch));
+        f.a[s][i] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(wm0 + i * 16 + (lane & 15), ch));
 #pragma unroll
       for (int j = 0; j < FNB; ++j)
         f.b[s][j] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(BM + wn0 + j * 16 + (lane & 15), ch));
     }
   };
-  const int rows_left = M - m0;
+  // Row blocks at or past M (the last tile row of a ragged M) run their MFMAs on clamped A rows and
+  // are never stored: skipping them would not shorten the single round of tiles, and a branch per
+  // row block would make the compiler drain the prefetched fragments at every block boundary.
   auto mfmas = [&](const Frags& f) __attribute__((always_inline)) {
 #pragma unroll
     for (int s = 0; s < SUBW; ++s)
 #pragma unroll
       for (int i = 0; i < FMB; ++i)
-        if (i * 16 < rows_left) {
 #pragma unroll
-          for (int j = 0; j < FNB; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.b[s][j], f.a[s][i], acc[i][j], 0, 0, 0);
-        }
+        for (int j = 0; j < FNB; ++j)
+          acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(f.b[s][j], f.a[s][i], acc[i][j], 0, 0, 0);
   };
 
   const int KT = K / BK;
@@ -936,36 +999,57 @@ void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t 
     if (kt < KT) step(kt, f0, f1);
   } else {
     // Step kt: wait for tile kt, barrier (also: every wave is done with tile kt - 1's stage), refill
-    // that stage with tile kt - 1 + NST, read tile kt's fragments, MFMAs of tile kt.
-    Frags f;
+    // that stage with tile kt - 1 + NST, then per 32-deep sub-step: the FNB B fragments, and the A
+    // fragments streamed two row blocks ahead of their MFMAs (a ring of three), so only one
+    // sub-step's B fragments and three A fragments are live next to the accumulators.
+    // Tiles issued before step kt: 0 .. NST - 1 (kt = 0), 0 .. kt - 2 + NST (kt >= 1), so at most
+    // NST - 1, resp. NST - 2, tiles after tile kt may still be in flight.
     for (int kt = 0; kt < KT; ++kt) {
-      wait_tiles(min(KT - 1 - kt, NST - 1));
+      wait_tiles(min(KT - 1 - kt, kt == 0 ? NST - 1 : NST - 2));
       block_barrier();
       if (kt >= 1 && kt - 1 + NST < KT) issue((kt - 1) % NST, kt - 1 + NST);
       __builtin_amdgcn_sched_barrier(0);
-      read_frags(f, kt);
-      mfmas(f);
+      const unsigned char* st = smem + (kt % NST) * STAGE;
+#pragma unroll
+      for (int s = 0; s < SUBW; ++s) {
+        const int ch = 4 * (s * KSPLIT + kg) + (lane >> 4);
+        bf16x8_t b[FNB], a[3];
+#pragma unroll
+        for (int j = 0; j < FNB; ++j)
+          b[j] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(BM + wn0 + j * 16 + (lane & 15), ch));
+#pragma unroll
+        for (int i = 0; i < 2 && i < FMB; ++i)
+          a[i] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(wm0 + i * 16 + (lane & 15), ch));
+#pragma unroll
+        for (int i = 0; i < FMB; ++i) {
+          if (i + 2 < FMB)
+            a[(i + 2) % 3] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(wm0 + (i + 2) * 16 + (lane & 15), ch));
+#pragma unroll
+          for (int j = 0; j < FNB; ++j)
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], a[i % 3], acc[i][j], 0, 0, 0);
+        }
+      }
       __builtin_amdgcn_sched_barrier(0);
     }
   }
 
-  // Epilogue. Block (i, j) holds the transposed product: lane l, register v -> row i * 16 + l % 16,
+  // Epilogue. Block (i, j) holds the transposed product: lane l, register v -> row wm0 + i * 16 + l % 16,
   // column wn0 + j * 16 + 4 (l / 16) + v.
   constexpr int LDT = BN + 8;
-  constexpr int RED = KSPLIT > 1 ? (NW / KSPLIT) * 64 * FMB * FNB * 4 * 4 : 0;  // fp32 partial bytes
+  constexpr int RED = KSPLIT > 1 ? NWG * 64 * FMB * FNB * 4 * 4 : 0;  // fp32 partial bytes
   uint16_t* ct = reinterpret_cast<uint16_t*>(smem + RED);
   block_barrier();
   if constexpr (KSPLIT > 1) {
     // Group 1 parks its accumulators in LDS ([block][register][thread] fp32), group 0 adds them.
     float* red = reinterpret_cast<float*>(smem);
-    const int t0 = (wave % WGN) * 64 + lane;
+    const int t0 = wr * 64 + lane;
     if (kg == 1) {
 #pragma unroll
       for (int i = 0; i < FMB; ++i)
 #pragma unroll
         for (int j = 0; j < FNB; ++j)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) red[((i * FNB + j) * 4 + v) * (WGN * 64) + t0] = acc[i][j][v];
+          for (int v = 0; v < 4; ++v) red[((i * FNB + j) * 4 + v) * (NWG * 64) + t0] = acc[i][j][v];
     }
     __syncthreads();
     if (kg == 0) {
@@ -974,30 +1058,37 @@ void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t 
 #pragma unroll
         for (int j = 0; j < FNB; ++j)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[i][j][v] += red[((i * FNB + j) * 4 + v) * (WGN * 64) + t0];
+          for (int v = 0; v < 4; ++v) acc[i][j][v] += red[((i * FNB + j) * 4 + v) * (NWG * 64) + t0];
     }
   }
-  if (kg == 0) {
+  // One wave row at a time: its waves write bf16(acc + bias) into the LDS tile, then every thread
+  // finishes the epilogue of those WM rows.
 #pragma unroll
-    for (int j = 0; j < FNB; ++j) {
-      const int cl = wn0 + j * 16 + 4 * (lane >> 4);
-      float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
-      if (ea.bias) {
-        const uint2 bw = *reinterpret_cast<const uint2*>(ea.bias + n0 + cl);
-        b0 = lo_bf16(bw.x); b1 = hi_bf16(bw.x); b2 = lo_bf16(bw.y); b3 = hi_bf16(bw.y);
-      }
+  for (int h = 0; h < WGM; ++h) {
+    if (h > 0) __syncthreads();
+    if (kg == 0 && wm == h) {
 #pragma unroll
-      for (int i = 0; i < FMB; ++i) {
-        uint2 w;
-        w.x = cvt_pk_bf16(acc[i][j][0] + b0, acc[i][j][1] + b1);
-        w.y = cvt_pk_bf16(acc[i][j][2] + b2, acc[i][j][3] + b3);
-        *reinterpret_cast<uint2*>(ct + (i * 16 + (lane & 15)) * LDT + cl) = w;
+      for (int j = 0; j < FNB; ++j) {
+        const int cl = wn0 + j * 16 + 4 * (lane >> 4);
+        float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+        if (ea.bias) {
+          const uint2 bw = *reinterpret_cast<const uint2*>(ea.bias + n0 + cl);
+          b0 = lo_bf16(bw.x); b1 = hi_bf16(bw.x); b2 = lo_bf16(bw.y); b3 = hi_bf16(bw.y);
+        }
+#pragma unroll
+        for (int i = 0; i < FMB; ++i) {
+          uint2 w;
+          w.x = cvt_pk_bf16(acc[i][j][0] + b0, acc[i][j][1] + b1);
+          w.y = cvt_pk_bf16(acc[i][j][2] + b2, acc[i][j][3] + b3);
+          *reinterpret_cast<uint2*>(ct + (i * 16 + (lane & 15)) * LDT + cl) = w;
+        }
       }
     }
+    __syncthreads();
+    store_tile_phase2<WM, BN, NT, EPI>(reinterpret_cast<unsigned char*>(ct),
+                                       reinterpret_cast<const uint16_t*>(smem + kLutOff), m0 + h * WM, n0, M, ea, C,
+                                       ldc);
   }
-  __syncthreads();
-  store_tile_phase2<BM, BN, NT, EPI>(reinterpret_cast<unsigned char*>(ct),
-                                     reinterpret_cast<const uint16_t*>(smem + kLutOff), m0, n0, M, ea, C, ldc);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1010,7 +1101,8 @@ typedef void (*gemm_fn)(const uint16_t*, int, int, int64_t, const uint16_t*, int
 struct GemmCfg {
   int bm, bn, wgm, wgn, pf;  // pf: register prefetch depth; 0 = direct-to-LDS; -1 = pipelined; -2 = 16-row
   gemm_fn fn[6];             // by epilogue; fn[kEpiQkv] only for the direct-to-LDS families
-  int bk, nst;               // 16-row kernel: K tile depth and LDS stages
+  int bk, nst, ks;           // 16-row kernel: K tile depth, LDS stages, K groups
+  int fb;                    // 16-row kernel: fragments read one K tile ahead
 };
 
 #define OUDJAT_GEMM_CFG(BM, BN, WGM, WGN, PF)                                                             \
@@ -1031,14 +1123,16 @@ struct GemmCfg {
     gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 2>, gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 3>,               \
     gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, 4>, gemm_bf16_pipe_kernel<BM, BN, WGM, WGN, kEpiQkv>}}
 
-// pf = -2: 16-row-block kernel; wgm = K groups, wgn = column strips.
-#define OUDJAT_GEMM_R16_CFG(BM, BN, WGN, KS, BK, NST, FB)                                                 \
-  {BM, BN, KS, WGN, -2,                                                                                  \
-   {gemm_bf16_r16_kernel<BM, BN, WGN, KS, BK, NST, FB, 0>, gemm_bf16_r16_kernel<BM, BN, WGN, KS, BK, NST, FB, 1>, \
-    gemm_bf16_r16_kernel<BM, BN, WGN, KS, BK, NST, FB, 2>, gemm_bf16_r16_kernel<BM, BN, WGN, KS, BK, NST, FB, 3>, \
-    gemm_bf16_r16_kernel<BM, BN, WGN, KS, BK, NST, FB, 4>,                                               \
-    gemm_bf16_r16_kernel<BM, BN, WGN, KS, BK, NST, FB, kEpiQkv>},                                        \
-   BK, NST}
+// pf = -2: 16-row-block kernel; wgm x wgn waves per K group, ks K groups.
+#define OUDJAT_GEMM_R16_CFG(BM, BN, WGM, WGN, KS, BK, NST, FB)                                            \
+  {BM, BN, WGM, WGN, -2,                                                                                 \
+   {gemm_bf16_r16_kernel<BM, BN, WGM, WGN, KS, BK, NST, FB, 0>,                                          \
+    gemm_bf16_r16_kernel<BM, BN, WGM, WGN, KS, BK, NST, FB, 1>,                                          \
+    gemm_bf16_r16_kernel<BM, BN, WGM, WGN, KS, BK, NST, FB, 2>,                                          \
+    gemm_bf16_r16_kernel<BM, BN, WGM, WGN, KS, BK, NST, FB, 3>,                                          \
+    gemm_bf16_r16_kernel<BM, BN, WGM, WGN, KS, BK, NST, FB, 4>,                                          \
+    gemm_bf16_r16_kernel<BM, BN, WGM, WGN, KS, BK, NST, FB, kEpiQkv>},                                   \
+   BK, NST, KS, FB}
 
 static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_CFG(128, 128, 2, 2, 1),  // 0
@@ -1061,11 +1155,12 @@ static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_PIPE_CFG(288, 256, 3, 4),  // 17
     OUDJAT_GEMM_PIPE_CFG(256, 128, 2, 2),  // 18
     OUDJAT_GEMM_PIPE_CFG(128, 128, 2, 2),  // 19
-    OUDJAT_GEMM_R16_CFG(144, 512, 4, 1, 32, 3, true),   // 20
-    OUDJAT_GEMM_R16_CFG(144, 128, 2, 2, 64, 4, true),   // 21
-    OUDJAT_GEMM_R16_CFG(144, 512, 8, 1, 32, 3, false),  // 22: fc1-like (N % 512 == 0)
-    OUDJAT_GEMM_R16_CFG(144, 128, 4, 2, 64, 4, true),   // 23: N = C GEMMs
-    OUDJAT_GEMM_R16_CFG(144, 128, 4, 2, 64, 3, true),   // 24
+    OUDJAT_GEMM_R16_CFG(144, 512, 1, 4, 1, 32, 3, true),   // 20
+    OUDJAT_GEMM_R16_CFG(144, 128, 1, 2, 2, 64, 4, true),   // 21
+    OUDJAT_GEMM_R16_CFG(144, 512, 1, 8, 1, 32, 3, false),  // 22: fc1-like (N % 512 == 0)
+    OUDJAT_GEMM_R16_CFG(144, 128, 1, 4, 2, 64, 4, true),   // 23: N = C GEMMs
+    OUDJAT_GEMM_R16_CFG(144, 128, 1, 4, 2, 64, 3, true),   // 24
+    OUDJAT_GEMM_R16_CFG(288, 256, 2, 4, 1, 64, 2, false),  // 25: 288 x 256, 128-byte operand rows
 };
 static constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -1122,6 +1217,9 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   if (N % 128 != 0) return 8;
   const int64_t tiles256 = cdiv(M, 256) * cdiv(N, 256);
   if (N % 256 == 0 && tiles256 >= 128 && tiles256 <= 256) return 15;
+  // 288 x 256 tiles with 128-byte operand rows when they fill three quarters or more of the CUs.
+  const int64_t tiles288 = cdiv(M, 288) * (N / 256);
+  if (N % 256 == 0 && tiles288 >= 192 && tiles288 <= 256) return 25;
   // 144-row tiles (one round of 128..256 workgroups) when 256 x 256 tiles do not fit one round.
   const int64_t tm144 = cdiv(M, 144);
   if (N % 512 == 0 && tm144 * (N / 512) >= 128 && tm144 * (N / 512) <= 256) return 22;
@@ -1140,7 +1238,7 @@ static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t 
   // K stages, or (direct-to-LDS kernels) the bf16 output tile of the epilogue if that is larger.
   size_t lds = cfg.pf < 0 ? (size_t)kStages * (cfg.bm + cfg.bn) * 64 : (size_t)2 * (cfg.bm + cfg.bn) * 128;
   if (cfg.pf <= 0) lds = lds > (size_t)cfg.bm * (cfg.bn + 8) * 2 ? lds : (size_t)cfg.bm * (cfg.bn + 8) * 2;
-  if (cfg.pf == -2) lds = r16_lut_offset(cfg.bm, cfg.bn, cfg.bk, cfg.nst, cfg.wgm, cfg.wgm * cfg.wgn);
+  if (cfg.pf == -2) lds = r16_lut_offset(cfg.bm, cfg.bn, cfg.wgm, cfg.wgn, cfg.ks, cfg.bk, cfg.nst);
   if (cfg.pf <= 0 && epi == OUDJAT_EPI_BIAS_GELU) lds += kGeluLut * sizeof(uint16_t);
   if (epi == OUDJAT_EPI_BIAS_GELU) {
     const int st = ensure_gelu_table();
@@ -1152,7 +1250,7 @@ static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t 
     hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
     if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "%s: hipFuncSetAttribute: %s", what, hipGetErrorString(e));
   }
-  const int threads = cfg.wgm * cfg.wgn * 64;
+  const int threads = cfg.wgm * cfg.wgn * (cfg.pf == -2 ? cfg.ks : 1) * 64;
   static const int group_m = env_int("OUDJAT_GEMM_GROUP_M", 8);
   hipLaunchKernelGGL(fn, dim3((unsigned)tiles), dim3(threads), lds, stream, A, (int)M, (int)K, lda, W, (int)N, ldw, ea,
                      C, ldc, group_m > 0 ? group_m : 1);
@@ -1227,4 +1325,26 @@ extern "C" int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K
   int ci = choose_cfg(M, N, K, true);
   if (kCfgs[ci].pf > 0 || kCfgs[ci].bn % Dh != 0 || (H * Dh) % kCfgs[ci].bn != 0) ci = 11;  // 128 x 128 direct-to-LDS
   return launch_gemm(ci, A, M, K, lda, W, N, ldw, kEpiQkv, ea, nullptr, 0, as_stream(stream), "linear_qkv_rope_kv");
+}
+
+// Kernel a linear_bf16 call of this shape would launch, as the demangled name profilers print
+// (aligned operands assumed). For matching profile summaries to the running build.
+extern "C" int oudjat_linear_kernel_name(int64_t M, int64_t N, int64_t K, int epi, char* buf, int64_t buflen) {
+  OUDJAT_REQUIRE(buf && buflen > 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_kernel_name: no buffer");
+  OUDJAT_REQUIRE(M > 0 && N > 0 && K > 0 && epi >= 0 && epi <= kEpiQkv, OUDJAT_ERR_INVALID_ARGUMENT,
+                 "linear_kernel_name: bad arguments");
+  const GemmCfg& c = kCfgs[choose_cfg(M, N, K, true)];
+  int n;
+  if (c.pf == -2)
+    n = snprintf(buf, (size_t)buflen, "oudjat::gemm_bf16_r16_kernel<%d, %d, %d, %d, %d, %d, %d, %s, %d>", c.bm, c.bn,
+                 c.wgm, c.wgn, c.ks, c.bk, c.nst, c.fb ? "true" : "false", epi);
+  else if (c.pf == -1)
+    n = snprintf(buf, (size_t)buflen, "oudjat::gemm_bf16_pipe_kernel<%d, %d, %d, %d, %d>", c.bm, c.bn, c.wgm, c.wgn, epi);
+  else if (c.pf == 0)
+    n = snprintf(buf, (size_t)buflen, "oudjat::gemm_bf16_dma_kernel<%d, %d, %d, %d, %d>", c.bm, c.bn, c.wgm, c.wgn, epi);
+  else
+    n = snprintf(buf, (size_t)buflen, "oudjat::gemm_bf16_kernel<%d, %d, %d, %d, %d, %d>", c.bm, c.bn, c.wgm, c.wgn, c.pf,
+                 epi);
+  OUDJAT_REQUIRE(n >= 0 && n < buflen, OUDJAT_ERR_INVALID_ARGUMENT, "linear_kernel_name: buffer too small");
+  return OUDJAT_OK;
 }

@@ -211,7 +211,7 @@ def packed_residual_persist(x_act: torch.Tensor, x_attn: torch.Tensor, mlp: torc
     _require(blocks_out_sum.dim() == 3 and blocks_out_sum.shape[2] == C and blocks_out_sum.stride(2) == 1,
              "packed_residual_persist: blocks_out_sum must be [B, N, C] with contiguous rows")
     x_new = torch.empty_like(x_act)
-    _launch("reconstruct", x_act, "oudjat_packed_residual_persist", _ptr(x_act), _ptr(x_attn), _ptr(mlp), M, C,
+    _launch("packed_residual", x_act, "oudjat_packed_residual_persist", _ptr(x_act), _ptr(x_attn), _ptr(mlp), M, C,
             _ptr(_index(batch_idx, "batch_idx")), _ptr(_index(token_idx, "token_idx")), _ptr(blocks_out_sum),
             blocks_out_sum.stride(0), blocks_out_sum.stride(1), _ptr(x_new), _stream(x_act))
     return x_new
@@ -394,6 +394,13 @@ def linear_qkv_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor
 # ------------------------------------------------------------------------------------------------
 # GEMM and attention
 # ------------------------------------------------------------------------------------------------
+
+
+def linear_kernel_name(M: int, N: int, K: int, epilogue: int = _lib.EPI_BIAS) -> str:
+    """Demangled name (as profilers print it) of the kernel `linear` launches for an M x N x K product."""
+    buf = ctypes.create_string_buffer(256)
+    call("oudjat_linear_kernel_name", M, N, K, epilogue, buf, len(buf))
+    return buf.value.decode()
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, *,

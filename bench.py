@@ -72,6 +72,8 @@ def kernel_work(tag: str, B: int, T: int, N: int, C: int, H: int, mlp: int):
         return 4.0 * B * H * T * N * (C // H) / 1e12, "TFLOP/s", "mfma"
     if tag == "reconstruct":  # fused minimum: 3 B N C + 2 M C bf16 elements + row map
         return (3.0 * B * N * C * 2 + 2.0 * M * C * 2 + 4.0 * B * N) / 1e9, "GB/s", "hbm"
+    if tag == "packed_residual":  # read x_act, x_attn, mlp; write x_new, blocks_out_sum rows; row ids
+        return (5.0 * M * C * 2 + 16.0 * M) / 1e9, "GB/s", "hbm"
     if tag == "gather_rows":
         return (2.0 * M * C * 2 + 16.0 * M) / 1e9, "GB/s", "hbm"
     if tag == "qkv_post":  # read qkv rows, write q packed + k,v cache rows
@@ -79,6 +81,19 @@ def kernel_work(tag: str, B: int, T: int, N: int, C: int, H: int, mlp: int):
     if tag == "layernorm":
         return (2.0 * M * C * 2) / 1e9, "GB/s", "hbm"
     raise ValueError(tag)
+
+
+def probe_kernel_name(tag: str, B: int, T: int, C: int, mlp: int):
+    """Kernel a GEMM launch site runs in this build (None for other sites)."""
+    from appcorr_amd import _lib
+    from appcorr_amd import kernels as K
+
+    M = B * T
+    shapes = {"gemm0": (M, 3 * C, C, 5), "gemm1": (M, mlp, C, _lib.EPI_BIAS_GELU),
+              "gemm2": (M, C, C, _lib.EPI_BIAS_LS_RESID), "gemm3": (M, C, mlp, _lib.EPI_BIAS_LS)}
+    if tag not in shapes:
+        return None
+    return K.linear_kernel_name(*shapes[tag])
 
 
 def cpu_baseline(name: str, B: int, keep: float, budget_s: float):
@@ -260,9 +275,13 @@ def main():
         tpath = os.path.join(ROOT, "profiles", "traffic.json")
         if os.path.exists(tpath):
             rec = json.load(open(tpath)).get(tkey)
-            if rec:
+            running = probe_kernel_name(args.probe, B, T, C, mlp)
+            if rec and (running is None or rec["kernel"] == running):
                 roof["traffic"] = rec["traffic_bytes"]
                 roof["traffic_source"] = f"profiles/traffic.json[{tkey}] ({rec['kernel']})"
+            elif rec:
+                roof["traffic_source"] = (f"profiles/traffic.json[{tkey}] was measured on {rec['kernel']}, "
+                                          f"this build runs {running}: not used")
 
     cpu = None
     if args.cpu_budget > 0:

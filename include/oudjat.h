@@ -211,6 +211,12 @@ int oudjat_sparse_query_attention(const uint16_t* q, int64_t q_row_stride, int64
                                   int64_t N, float scale, uint16_t* out, int64_t out_row_stride,
                                   oudjat_stream_t stream);
 
+/* Introspection, no counterpart in the reference: writes to buf (NUL-terminated) the demangled name,
+ * as rocprofv3 prints it, of the kernel oudjat_linear_bf16 launches for an M x N x K product with
+ * epilogue epi (16-byte aligned operands). Lets benchmark and profile tooling check that a stored
+ * per-kernel measurement belongs to the kernel the build runs. */
+int oudjat_linear_kernel_name(int64_t M, int64_t N, int64_t K, int epi, char* buf, int64_t buflen);
+
 /* Row 17 -- NVFP4 quantize: x [M, K] bf16 (row stride stride_m) with fp32 tensor scale at
  * *tensor_scale (device) -> qdata [M, K/2] (two e2m1 codes per byte, even element in the low
  * nibble) and e4m3 block scales in the swizzled layout of 32x16 bytes per 128x64 tile

@@ -235,6 +235,22 @@ def test_sparse_query_attention(dev, B, T, N, H, D):
     _check_attention(got, qb, kv, scale, ref, f"attention {B},{T},{N},{H},{D}")
 
 
+@pytest.mark.parametrize("B,T,N,H,scale_up", [(16, 261, 1029, 16, 1.0), (2, 300, 777, 4, 1.0), (1, 256, 64, 3, 1.0),
+                                               (2, 260, 65, 2, 1.0), (2, 261, 300, 2, 8.0)])
+def test_attention_buffer_load_kernel_equals_staged(dev, B, T, N, H, scale_up, monkeypatch):
+    """Dh = 64 with >= 8 waves runs the kernel that loads K/V tiles straight into LDS and reads V^T
+    through LDS transpose reads; its arithmetic is the register-staged kernel's, so the outputs must be
+    bit-identical (one key tile, a ragged last tile of one key, 10 waves, large logits)."""
+    D = 64
+    q = (_rand((B * T, H, D), 40).float() * scale_up).to(torch.bfloat16).to(dev)
+    kv = (_rand((B, N, 2, H, D), 41).float() * scale_up).to(torch.bfloat16).to(dev)
+    monkeypatch.delenv("OUDJAT_ATTN_STAGED", raising=False)
+    got = K.sparse_query_attention(q, kv, T, D ** -0.5)
+    monkeypatch.setenv("OUDJAT_ATTN_STAGED", "1")
+    ref = K.sparse_query_attention(q, kv, T, D ** -0.5)
+    assert_bits_equal(got, ref.cpu(), f"attention {B},{T},{N},{H} x{scale_up}")
+
+
 def test_sparse_query_attention_peaked_softmax(dev):
     # Large logits: the online max rescaling must keep exp() in range.
     B, T, N, H, D = 2, 40, 300, 2, 64

@@ -98,3 +98,13 @@ def test_wrappers_refuse_cpu_tensors():
     idx = torch.zeros(3, dtype=torch.long)
     with pytest.raises(ValueError, match="GPU only"):
         K.gather_rows(x, idx, idx)
+
+
+def test_linear_kernel_name_reports_a_gemm_kernel():
+    """Host-only introspection (no GPU work): the name of the kernel a linear launch would use."""
+    from appcorr_amd import _lib
+    from appcorr_amd import kernels as K
+
+    name = K.linear_kernel_name(4176, 4096, 1024, _lib.EPI_BIAS_GELU)
+    assert name.startswith("oudjat::gemm_bf16_") and name.endswith(", 1>"), name
+    assert K.linear_kernel_name(64, 64, 64).startswith("oudjat::gemm_bf16_")
