@@ -322,11 +322,9 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
   if constexpr (EPI == kEpiQkv) {
     // One work item = (row, head, 8-wide chunk of the left half) with its partner chunk Dh/2 to the
     // right: RoPE on q and k of patch rows, then q packed or k / v into the cache row. A tile covers
-    // whole heads of one of q, k, v (H * Dh % BN == 0, Dh | BN).
+    // whole heads (Dh | BN); each item finds whether its head is one of q, k or v.
     const QkvArgs& qa = ea.qkv;
     const int HD = qa.H * qa.Dh, half = qa.Dh >> 1;
-    const int which = n0 / HD;
-    const int hc0 = n0 - which * HD;
     const int lg_cph = __builtin_ctz((unsigned)(half >> 3));  // chunk pairs per head = Dh / 16
     constexpr int PPR = BN / 16;                               // chunk pairs per tile row
     constexpr int ITEMS = (BM * PPR + NW * 64 - 1) / (NW * 64);
@@ -338,6 +336,9 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
       const int row = m0 + rl;
       if (row >= M) continue;
       const int c0 = ((pr >> lg_cph) << (lg_cph + 4)) + ((pr & ((1 << lg_cph) - 1)) << 3);  // head * Dh + 8 c
+      const int colg = n0 + c0;
+      const int which = colg >= 2 * HD ? 2 : (colg >= HD ? 1 : 0);
+      const int hcol = colg - which * HD;  // column within q, k or v
       uint4 lo = *reinterpret_cast<const uint4*>(ct + rl * LDT + c0);
       uint4 hi = *reinterpret_cast<const uint4*>(ct + rl * LDT + c0 + half);
       if (which < 2 && qa.pm[row]) {
@@ -355,7 +356,7 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
       }
       uint16_t* dst = (which == 0 ? qa.q_out + (int64_t)row * HD
                                   : qa.kv + qa.bi[row] * qa.kvb + qa.ti[row] * qa.kvn + (which - 1) * HD) +
-                      hc0 + c0;
+                      hcol;
       *reinterpret_cast<uint4*>(dst) = lo;
       *reinterpret_cast<uint4*>(dst + half) = hi;
     }
@@ -1161,6 +1162,7 @@ static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_R16_CFG(144, 128, 1, 4, 2, 64, 4, true),   // 23: N = C GEMMs
     OUDJAT_GEMM_R16_CFG(144, 128, 1, 4, 2, 64, 3, true),   // 24
     OUDJAT_GEMM_R16_CFG(288, 256, 2, 4, 1, 64, 2, false),  // 25: 288 x 256, 128-byte operand rows
+    OUDJAT_GEMM_R16_CFG(288, 192, 2, 4, 1, 64, 2, false),  // 26: 288 x 192 (N = 3 C: 240 tiles)
 };
 static constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -1220,6 +1222,8 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   // 288 x 256 tiles with 128-byte operand rows when they fill three quarters or more of the CUs.
   const int64_t tiles288 = cdiv(M, 288) * (N / 256);
   if (N % 256 == 0 && tiles288 >= 192 && tiles288 <= 256) return 25;
+  const int64_t tiles288n = cdiv(M, 288) * (N / 192);
+  if (N % 192 == 0 && tiles288n >= 192 && tiles288n <= 256) return 26;
   // 144-row tiles (one round of 128..256 workgroups) when 256 x 256 tiles do not fit one round.
   const int64_t tm144 = cdiv(M, 144);
   if (N % 512 == 0 && tm144 * (N / 512) >= 128 && tm144 * (N / 512) <= 256) return 22;
@@ -1227,6 +1231,18 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   return 11;
 }
 
+
+// Fused QKV: tiles must cover whole heads (Dh | BN; a tile may span the q / k / v boundaries).
+// 288 x 192 tiles when the plain choice would leave more CUs idle in its single round.
+static int choose_qkv_cfg(int64_t M, int64_t N, int64_t K, int64_t Dh) {
+  int ci = choose_cfg(M, N, K, true);
+  const int64_t tiles288n = cdiv(M, 288) * (N / 192);
+  if (env_int("OUDJAT_GEMM_CFG", -1) < 0 && N % 192 == 0 && tiles288n >= 192 && tiles288n <= 256 &&
+      cdiv(M, kCfgs[ci].bm) * cdiv(N, kCfgs[ci].bn) < tiles288n)
+    ci = 26;
+  if (kCfgs[ci].pf > 0 || kCfgs[ci].bn % Dh != 0 || N % kCfgs[ci].bn != 0) ci = 11;  // 128 x 128 direct-to-LDS
+  return ci;
+}
 
 // Launches configuration `ci` with epilogue `epi` (arguments already validated).
 static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W, int64_t N,
@@ -1321,10 +1337,8 @@ extern "C" int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K
   ea.bias = bias;
   ea.qkv = QkvArgs{(int)H, (int)Dh, sin_table, cos_table, table_stride, patch_mask, rope_idx, batch_idx, token_idx,
                    kv, kv_stride_b, kv_stride_n, q_out};
-  // Tiles must cover whole heads of one of q, k, v: Dh | BN and BN | H * Dh.
-  int ci = choose_cfg(M, N, K, true);
-  if (kCfgs[ci].pf > 0 || kCfgs[ci].bn % Dh != 0 || (H * Dh) % kCfgs[ci].bn != 0) ci = 11;  // 128 x 128 direct-to-LDS
-  return launch_gemm(ci, A, M, K, lda, W, N, ldw, kEpiQkv, ea, nullptr, 0, as_stream(stream), "linear_qkv_rope_kv");
+  return launch_gemm(choose_qkv_cfg(M, N, K, Dh), A, M, K, lda, W, N, ldw, kEpiQkv, ea, nullptr, 0, as_stream(stream),
+                     "linear_qkv_rope_kv");
 }
 
 // Kernel a linear_bf16 call of this shape would launch, as the demangled name profilers print
@@ -1333,7 +1347,7 @@ extern "C" int oudjat_linear_kernel_name(int64_t M, int64_t N, int64_t K, int ep
   OUDJAT_REQUIRE(buf && buflen > 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_kernel_name: no buffer");
   OUDJAT_REQUIRE(M > 0 && N > 0 && K > 0 && epi >= 0 && epi <= kEpiQkv, OUDJAT_ERR_INVALID_ARGUMENT,
                  "linear_kernel_name: bad arguments");
-  const GemmCfg& c = kCfgs[choose_cfg(M, N, K, true)];
+  const GemmCfg& c = kCfgs[epi == kEpiQkv ? choose_qkv_cfg(M, N, K, 64) : choose_cfg(M, N, K, true)];
   int n;
   if (c.pf == -2)
     n = snprintf(buf, (size_t)buflen, "oudjat::gemm_bf16_r16_kernel<%d, %d, %d, %d, %d, %d, %d, %s, %d>", c.bm, c.bn,

@@ -213,7 +213,8 @@ int oudjat_sparse_query_attention(const uint16_t* q, int64_t q_row_stride, int64
 
 /* Introspection, no counterpart in the reference: writes to buf (NUL-terminated) the demangled name,
  * as rocprofv3 prints it, of the kernel oudjat_linear_bf16 launches for an M x N x K product with
- * epilogue epi (16-byte aligned operands). Lets benchmark and profile tooling check that a stored
+ * epilogue epi (16-byte aligned operands); epi = 5 names the oudjat_linear_qkv_rope_kv kernel
+ * (N = 3 H Dh, Dh = 64). Lets benchmark and profile tooling check that a stored
  * per-kernel measurement belongs to the kernel the build runs. */
 int oudjat_linear_kernel_name(int64_t M, int64_t N, int64_t K, int epi, char* buf, int64_t buflen);
 
