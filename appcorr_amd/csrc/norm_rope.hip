@@ -7,25 +7,18 @@ namespace oudjat {
 static constexpr int kNormThreads = 256;
 static constexpr int kNormRowsPerWg = kNormThreads / 64;
 
-// One wave per row; each lane keeps its CH 16-byte chunks (8 bf16 each) in registers, so the row is
-// read from HBM exactly once. Statistics are fp32: mean, then the biased variance around it.
+// LayerNorm of one row held by one wave: lane l holds chunks l + 64 j (j < CH, 8 values each, as
+// fp32 from bf16). Statistics are fp32: mean, then the biased variance around it. Shared by the
+// standalone kernel and the fused residual kernel so both give the same bits.
 template <int CH>
-__global__ __launch_bounds__(kNormThreads) void layernorm_kernel(const uint16_t* __restrict__ x, int64_t rows, int C,
-                                                               int64_t xs, const uint16_t* __restrict__ w,
-                                                               const uint16_t* __restrict__ bias, float eps,
-                                                               uint16_t* __restrict__ out, int64_t os) {
-  const int64_t row = (int64_t)blockIdx.x * kNormRowsPerWg + (threadIdx.x >> 6);
-  if (row >= rows) return;
-  const int lane = threadIdx.x & 63;
-  const int chunks = C >> 3;
-  const uint4* xv = reinterpret_cast<const uint4*>(x + row * xs);
-  float v[CH][8];
+__device__ __forceinline__ void layernorm_row(const float (&v)[CH][8], int lane, int chunks, int C,
+                                              const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
+                                              float eps, uint16_t* __restrict__ out_row) {
   float sum = 0.0f;
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
     const int c = lane + 64 * j;
     if (c < chunks) {
-      unpack8(xv[c], v[j]);
 #pragma unroll
       for (int e = 0; e < 8; ++e) sum += v[j][e];
     }
@@ -47,7 +40,7 @@ __global__ __launch_bounds__(kNormThreads) void layernorm_kernel(const uint16_t*
   const float rstd = 1.0f / sqrtf(var + eps);
   const uint4* wv = reinterpret_cast<const uint4*>(w);
   const uint4* bv = reinterpret_cast<const uint4*>(bias);
-  uint4* ov = reinterpret_cast<uint4*>(out + row * os);
+  uint4* ov = reinterpret_cast<uint4*>(out_row);
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
     const int c = lane + 64 * j;
@@ -60,6 +53,68 @@ __global__ __launch_bounds__(kNormThreads) void layernorm_kernel(const uint16_t*
       ov[c] = pack8(y);
     }
   }
+}
+
+// One wave per row; each lane keeps its CH 16-byte chunks (8 bf16 each) in registers, so the row is
+// read from HBM exactly once.
+template <int CH>
+__global__ __launch_bounds__(kNormThreads) void layernorm_kernel(const uint16_t* __restrict__ x, int64_t rows, int C,
+                                                               int64_t xs, const uint16_t* __restrict__ w,
+                                                               const uint16_t* __restrict__ bias, float eps,
+                                                               uint16_t* __restrict__ out, int64_t os) {
+  const int64_t row = (int64_t)blockIdx.x * kNormRowsPerWg + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int chunks = C >> 3;
+  const uint4* xv = reinterpret_cast<const uint4*>(x + row * xs);
+  float v[CH][8];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) unpack8(xv[c], v[j]);
+  }
+  layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, out + row * os);
+}
+
+// The residual step of a correction block on packed selected rows fused with the next block's
+// LayerNorm: x_new = bf16(x_attn + mlp), blocks_out_sum[b_i, t_i] = bf16(bf16(x_attn - x_act) + mlp)
+// and ln_out = LayerNorm(x_new) (of the bf16 x_new, exactly as the standalone kernel computes it).
+template <int CH>
+__global__ __launch_bounds__(kNormThreads) void packed_residual_ln_kernel(
+    const uint16_t* __restrict__ xa, const uint16_t* __restrict__ xt, const uint16_t* __restrict__ mlp, int64_t rows,
+    int C, const int64_t* __restrict__ bi, const int64_t* __restrict__ ti, uint16_t* __restrict__ bos, int64_t bsb,
+    int64_t bsn, uint16_t* __restrict__ xn, const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
+    float eps, uint16_t* __restrict__ ln_out) {
+  const int64_t row = (int64_t)blockIdx.x * kNormRowsPerWg + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int chunks = C >> 3;
+  const uint4* av = reinterpret_cast<const uint4*>(xa + row * C);
+  const uint4* tv = reinterpret_cast<const uint4*>(xt + row * C);
+  const uint4* mv = reinterpret_cast<const uint4*>(mlp + row * C);
+  uint4* ov = reinterpret_cast<uint4*>(xn + row * C);
+  uint4* bv = reinterpret_cast<uint4*>(bos + bi[row] * bsb + ti[row] * bsn);
+  float v[CH][8];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) {
+      float fa[8], ft[8], fm[8], fo[8], fb[8];
+      unpack8(av[c], fa);
+      unpack8(tv[c], ft);
+      unpack8(mv[c], fm);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        fo[e] = ft[e] + fm[e];
+        fb[e] = round_bf16(ft[e] - fa[e]) + fm[e];
+      }
+      const uint4 o = pack8(fo);
+      ov[c] = o;
+      bv[c] = pack8(fb);
+      unpack8(o, v[j]);
+    }
+  }
+  layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, ln_out + row * C);
 }
 
 // Thread = (row, head, chunk of 8 in the left half). Rows with patch_mask == 0 are left untouched.
@@ -210,4 +265,34 @@ extern "C" int oudjat_qkv_rope_kv_scatter(const uint16_t* qkv, int64_t M, int64_
   qkv_rope_kv_scatter_kernel<<<(unsigned)cdiv(threads, 256), 256, 0, as_stream(stream)>>>(
       qkv, M, (int)H, (int)Dh, sin_t, cos_t, tst, pm, ridx, bi, ti, kv, kvb, kvn, qo);
   return check_launch("qkv_rope_kv_scatter");
+}
+
+extern "C" int oudjat_packed_residual_persist_ln(const uint16_t* x_act, const uint16_t* x_attn, const uint16_t* mlp,
+                                                 int64_t rows, int64_t C, const int64_t* batch_idx,
+                                                 const int64_t* token_idx, uint16_t* bos, int64_t bos_stride_b,
+                                                 int64_t bos_stride_n, uint16_t* x_new, const uint16_t* ln_w,
+                                                 const uint16_t* ln_b, float eps, uint16_t* ln_out,
+                                                 oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(rows >= 0 && C > 0, OUDJAT_ERR_INVALID_ARGUMENT, "packed_residual_persist_ln: bad size");
+  if (rows == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(x_act && x_attn && mlp && batch_idx && token_idx && bos && x_new && ln_w && ln_b && ln_out,
+                 OUDJAT_ERR_INVALID_ARGUMENT, "packed_residual_persist_ln: null pointer");
+  OUDJAT_REQUIRE(C % 8 == 0 && aligned(x_act, 16) && aligned(x_attn, 16) && aligned(mlp, 16) && aligned(bos, 16) &&
+                     aligned(x_new, 16) && aligned(ln_w, 16) && aligned(ln_b, 16) && aligned(ln_out, 16) &&
+                     bos_stride_b % 8 == 0 && bos_stride_n % 8 == 0,
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "packed_residual_persist_ln: 16-byte aligned rows, C %% 8 == 0");
+  OUDJAT_REQUIRE(C <= 8192, OUDJAT_ERR_TOO_LARGE, "packed_residual_persist_ln: C=%lld > 8192", (long long)C);
+  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg);
+  hipStream_t st = as_stream(stream);
+#define OUDJAT_PRLN(CHV)                                                                                        \
+  packed_residual_ln_kernel<CHV><<<grid, kNormThreads, 0, st>>>(x_act, x_attn, mlp, rows, (int)C, batch_idx,     \
+                                                                token_idx, bos, bos_stride_b, bos_stride_n, x_new, \
+                                                                ln_w, ln_b, eps, ln_out)
+  if (C <= 512) OUDJAT_PRLN(1);
+  else if (C <= 1024) OUDJAT_PRLN(2);
+  else if (C <= 2048) OUDJAT_PRLN(4);
+  else if (C <= 4096) OUDJAT_PRLN(8);
+  else OUDJAT_PRLN(16);
+#undef OUDJAT_PRLN
+  return check_launch("packed_residual_persist_ln");
 }

@@ -7,9 +7,15 @@ attention.py, ffn_layers.py, layer_scale.py), so a reference state_dict loads un
 The modules only hold parameters; their forward never runs a torch op on the hot path. Every step of
 `SelfAttentionBlock.correct_partial_token` is a library call (appcorr_amd.kernels):
 
-    topk_plan (once per plan) -> gather_rows -> layer_norm -> linear[qkv] -> qkv_rope_kv_scatter
+    topk_plan (once per plan) -> gather_rows -> layer_norm
+    -> linear_qkv_rope_kv [qkv GEMM + bias + RoPE + K/V cache rows + packed q, one kernel]
     -> sparse_query_attention -> linear[proj, +LayerScale +residual] -> layer_norm
     -> linear[fc1, +GELU] -> linear[fc2, +LayerScale] -> reconstruct_scatter_persist
+
+A run of blocks sharing one query plan (`correct_blocks_packed`, what the executor uses when the
+plan does not depend on the layer) keeps the selected rows packed: gather_rows once, per block the
+same kernels with packed_residual_persist_ln (residual + persist + the next block's layer_norm)
+in place of reconstruct_scatter_persist, and one fold_residual_rows at the end.
 
 Plan-level bookkeeping that the reference does with small torch ops on [B, P] score tensors (score
 resolution and fusion, the plan cache, the pscore statistics) is kept as torch ops: it runs once per
@@ -520,10 +526,12 @@ class SelfAttentionBlock(nn.Module):
             raise ValueError("{tag}_blocks_out_sum must be contiguous")
         return plan, key, kv, bos
 
-    def _correct_rows(self, x_act: Tensor, rope, kv: Tensor, qs: PackedQueryState):
+    def _correct_rows(self, x_act: Tensor, rope, kv: Tensor, qs: PackedQueryState, xn: Tensor | None = None):
         """The block's arithmetic on the packed selected rows (block.py:1111-1141): returns
-        (x_attn, mlp); the K/V cache rows of the selected tokens are rewritten in place."""
-        xn = K.layer_norm(x_act, self.norm1.weight, self.norm1.bias, self.norm1.eps)   # block.py:1114
+        (x_attn, mlp); the K/V cache rows of the selected tokens are rewritten in place. `xn`, when
+        given, is norm1(x_act) already computed (by the previous block's fused residual step)."""
+        if xn is None:
+            xn = K.layer_norm(x_act, self.norm1.weight, self.norm1.bias, self.norm1.eps)   # block.py:1114
         _, attn = self.attn._qkv_attention(xn, rope, kv, qs)                         # attention.py:415-523
         x_attn = K.linear(attn, self.attn.proj.weight, self.attn.proj.bias,          # attention.py:532 +
                           epilogue=_lib.EPI_BIAS_LS_RESID, gamma=self._gamma(self.ls1, x_act),
@@ -583,6 +591,7 @@ def correct_blocks_packed(blocks, x: Tensor, dindice: Tensor, rope, cache_featur
     M = qs.active_token_idx.numel()
     x_p = K.gather_rows(xc, qs.active_batch_idx, qs.active_token_idx) if M else xc.new_empty((0, xc.shape[-1]))
     bos_list = []
+    xn = None  # norm1 of the next block on x_p, from the fused residual + LayerNorm step
     for i, (blk, tag) in enumerate(zip(blocks, tags)):
         if i == 0:
             plan, kv, bos = plan0, cache_feature[f"{tag}_kv"], cache_feature[f"{tag}_blocks_out_sum"]
@@ -591,8 +600,13 @@ def correct_blocks_packed(blocks, x: Tensor, dindice: Tensor, rope, cache_featur
         if plan is not plan0:
             raise RuntimeError("blocks of one packed run resolved different query plans")
         if x_p.shape[0] > 0:
-            x_attn, mlp = blk._correct_rows(x_p, rope, kv, qs)
-            x_p = K.packed_residual_persist(x_p, x_attn, mlp, qs.active_batch_idx, qs.active_token_idx, bos)
+            x_attn, mlp = blk._correct_rows(x_p, rope, kv, qs, xn=xn)
+            if i + 1 < len(blocks):
+                n1 = blocks[i + 1].norm1
+                x_p, xn = K.packed_residual_persist_ln(x_p, x_attn, mlp, qs.active_batch_idx, qs.active_token_idx,
+                                                       bos, n1.weight, n1.bias, n1.eps)
+            else:
+                x_p = K.packed_residual_persist(x_p, x_attn, mlp, qs.active_batch_idx, qs.active_token_idx, bos)
         bos_list.append(bos)
     out = K.fold_residual_rows(xc, qs.row_slot, x_p, bos_list, out=xc if inplace else None)
     return out, cache_feature

@@ -217,6 +217,29 @@ def packed_residual_persist(x_act: torch.Tensor, x_attn: torch.Tensor, mlp: torc
     return x_new
 
 
+def packed_residual_persist_ln(x_act: torch.Tensor, x_attn: torch.Tensor, mlp: torch.Tensor, batch_idx: torch.Tensor,
+                               token_idx: torch.Tensor, blocks_out_sum: torch.Tensor, ln_weight: torch.Tensor,
+                               ln_bias: torch.Tensor, eps: float):
+    """packed_residual_persist fused with the next block's first LayerNorm: returns (x_new, LN(x_new)),
+    the LayerNorm bit-identical to layer_norm(x_new) (block.py:1140-1179, then :1114 of the next block)."""
+    _require_cuda(x_act, x_attn, mlp, batch_idx, token_idx, blocks_out_sum, ln_weight, ln_bias)
+    for t, nm in ((x_act, "x_act"), (x_attn, "x_attn"), (mlp, "mlp")):
+        _require(t.dtype == torch.bfloat16 and t.dim() == 2 and t.is_contiguous() and t.shape == x_act.shape,
+                 f"packed_residual_persist_ln: {nm} must be contiguous bf16 [M, C]")
+    M, C = x_act.shape
+    _require(blocks_out_sum.dim() == 3 and blocks_out_sum.shape[2] == C and blocks_out_sum.stride(2) == 1,
+             "packed_residual_persist_ln: blocks_out_sum must be [B, N, C] with contiguous rows")
+    _require(ln_weight.dtype == ln_bias.dtype == torch.bfloat16 and ln_weight.numel() == C == ln_bias.numel(),
+             "packed_residual_persist_ln: bf16 LayerNorm parameters of size C")
+    x_new = torch.empty_like(x_act)
+    ln_out = torch.empty_like(x_act)
+    _launch("packed_residual", x_act, "oudjat_packed_residual_persist_ln", _ptr(x_act), _ptr(x_attn), _ptr(mlp), M, C,
+            _ptr(_index(batch_idx, "batch_idx")), _ptr(_index(token_idx, "token_idx")), _ptr(blocks_out_sum),
+            blocks_out_sum.stride(0), blocks_out_sum.stride(1), _ptr(x_new), _ptr(ln_weight.contiguous()),
+            _ptr(ln_bias.contiguous()), float(eps), _ptr(ln_out), _stream(x_act))
+    return x_new, ln_out
+
+
 def fold_residual_rows(x: torch.Tensor, row_slot: torch.Tensor, x_packed: torch.Tensor, blocks_out_sums,
                        out: torch.Tensor | None = None) -> torch.Tensor:
     """x [B, N, C] after a run of correction blocks whose selected rows stayed packed: selected rows from

@@ -135,6 +135,17 @@ int oudjat_packed_residual_persist(const uint16_t* x_act, const uint16_t* x_attn
                                    const int64_t* token_idx, uint16_t* bos, int64_t bos_stride_b,
                                    int64_t bos_stride_n, uint16_t* x_new, oudjat_stream_t stream);
 
+/* oudjat_packed_residual_persist fused with the next block's first LayerNorm (block.py:1114 of
+ * block l + 1 after block.py:1140-1179 of block l): additionally ln_out[i] = LayerNorm(x_new[i]) with
+ * weight ln_w, bias ln_b, eps, computed on the bf16 x_new exactly as oudjat_layernorm_rows does.
+ * x_act, x_attn, mlp, x_new, ln_out: [rows, C] contiguous. */
+int oudjat_packed_residual_persist_ln(const uint16_t* x_act, const uint16_t* x_attn, const uint16_t* mlp,
+                                      int64_t rows, int64_t C, const int64_t* batch_idx,
+                                      const int64_t* token_idx, uint16_t* bos, int64_t bos_stride_b,
+                                      int64_t bos_stride_n, uint16_t* x_new, const uint16_t* ln_w,
+                                      const uint16_t* ln_b, float eps, uint16_t* ln_out,
+                                      oudjat_stream_t stream);
+
 /* Row 14 over a run of n_blocks correction blocks (block.py:1143-1149 applied block after block):
  * x, out [rows, C] (rows = B*N, contiguous; out may alias x); row r with row_slot[r] >= 0 takes
  * x_packed[row_slot[r]]; every other row takes x + bos_0 + ... + bos_{n-1} rounded to bf16 after

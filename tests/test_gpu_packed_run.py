@@ -160,3 +160,26 @@ def test_packed_run_in_place(dev):
             xb, _ = blk.correct(xb, dind, cb["rope_sincos"], cb["cache_feature"], f"layer{i}", **kw)
     assert out_a.data_ptr() == xa.data_ptr()
     assert_bits_equal(out_a, xb.cpu(), "x_out")
+
+
+@pytest.mark.parametrize("B,N,C,M", [(16, 261, 1024, 4176), (2, 40, 384, 30), (1, 9, 8, 3), (3, 20, 1536, 17)])
+def test_packed_residual_ln_equals_unfused(dev, B, N, C, M):
+    """The residual step fused with the next block's LayerNorm equals packed_residual_persist followed by
+    layer_norm, bit for bit (x_new, blocks_out_sum rows and the LayerNorm output)."""
+    rng = np.random.default_rng(C + M)
+    flat = np.sort(rng.choice(B * N, M, replace=False))
+    bi = torch.from_numpy(flat // N).to(dev)
+    ti = torch.from_numpy(flat % N).to(dev)
+    x_act = _rand_bf16((M, C), 1).to(dev)
+    x_attn = (x_act.float() + _rand_bf16((M, C), 2, 0.5).float().to(dev)).to(torch.bfloat16)
+    mlp = _rand_bf16((M, C), 3, 0.3).to(dev)
+    bos0 = _rand_bf16((B, N, C), 4, 0.1).to(dev)
+    w = (1.0 + _rand_bf16((C,), 5, 0.2).float()).to(torch.bfloat16).to(dev)
+    b = _rand_bf16((C,), 6, 0.1).to(dev)
+    bos_u, bos_f = bos0.clone(), bos0.clone()
+    x_u = K.packed_residual_persist(x_act, x_attn, mlp, bi, ti, bos_u)
+    ln_u = K.layer_norm(x_u, w, b, 1e-6)
+    x_f, ln_f = K.packed_residual_persist_ln(x_act, x_attn, mlp, bi, ti, bos_f, w, b, 1e-6)
+    assert_bits_equal(x_f, x_u.cpu(), "x_new")
+    assert_bits_equal(bos_f, bos_u.cpu(), "blocks_out_sum")
+    assert_bits_equal(ln_f, ln_u.cpu(), "LayerNorm(x_new)")
