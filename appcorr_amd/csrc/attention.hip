@@ -49,6 +49,34 @@ __device__ __forceinline__ float softmax_ref_max(float m_ref, float tile_max, fl
   return (m_run - m_ref) * scale_log2 > 8.0f ? m_run : m_ref;
 }
 
+// Sum of one query's probabilities over a key tile, taken from the bf16 values the O^T MFMAs
+// multiply (so numerator and normaliser use the same weights): packed dot products against (1, 1),
+// then the partner lane's half (lanes l and l ^ 32 hold the two halves of a query's keys).
+// Lane exchange with lane l ^ 32 through v_permlane32_swap (a VALU op, no LDS round trip): swapping
+// the halves of two copies of x leaves x_l and x_{l^32} in the two results of every lane.
+__device__ __forceinline__ float xor32_max(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor32_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
+
+__device__ __forceinline__ float prob_row_sum(const bf16x8_t (&pf)[4]) {
+  typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+  const bf16x2v_t ones = {(__bf16)1.0f, (__bf16)1.0f};
+  float r[4];  // one short chain per k-step, combined as a tree
+#pragma unroll
+  for (int j = 0; j < 4; ++j) {
+    r[j] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf[j], pf[j], 0, 1), ones, 0.0f, false);
+    r[j] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf[j], pf[j], 2, 3), ones, r[j], false);
+    r[j] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf[j], pf[j], 4, 5), ones, r[j], false);
+    r[j] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf[j], pf[j], 6, 7), ones, r[j], false);
+  }
+  return xor32_sum((r[0] + r[1]) + (r[2] + r[3]));
+}
+
 // MINW: fewest waves a launch of this instance uses (sizes the per-thread share of a K/V tile);
 // DOUBLE_SET: prefetch K/V two tiles ahead through two register sets (needs the registers that only
 // the Dh = 64, >= 8-wave instance has to spare).
@@ -190,26 +218,10 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
     const float m_new = softmax_ref_max(m_i, mx, scale_log2);
     const float alpha = __builtin_amdgcn_exp2f((m_i - m_new) * scale_log2);
     const float mc = m_new * scale_log2;
-    float rs = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][v], scale_log2, -mc));
-        s[kb][v] = p;
-        rs += p;
-      }
-    rs += __shfl_xor(rs, 32, 64);
-    l_i = l_i * alpha + rs;
-    m_i = m_new;
-    // Rescale the output only when some query's running max moved (alpha != 1 somewhere in the
-    // wave); once the maxima settle, later tiles skip it.
-    if (DH == 128 || __builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
-#pragma unroll
-      for (int d = 0; d < OB; ++d)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[d][v] *= alpha;
-    }
+      for (int v = 0; v < 16; ++v) s[kb][v] = __builtin_amdgcn_exp2f(fmaf(s[kb][v], scale_log2, -mc));
     // P^T fragments: k-step j covers keys 16j + {4g..4g+3} and 16j + 8 + {4g..4g+3}.
     bf16x8_t pf[4];
 #pragma unroll
@@ -218,6 +230,17 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
 #pragma unroll
       for (int e = 0; e < 8; ++e) tmp[e] = s[j >> 1][8 * (j & 1) + e];
       pf[j] = pack_bf16x8(tmp);
+    }
+    const float rs = prob_row_sum(pf);
+    l_i = l_i * alpha + rs;
+    m_i = m_new;
+    // Rescale the output only when some query's reference max moved (alpha != 1 somewhere in the
+    // wave).
+    if (DH == 128 || __builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+      for (int d = 0; d < OB; ++d)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[d][v] *= alpha;
     }
 #pragma unroll
     for (int d = 0; d < OB; ++d) {
@@ -292,13 +315,20 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
 // head) descriptors and load as zeros (their scores are masked). The A operand of O^T += V^T . P^T
 // comes from V's rows through the LDS transpose read: in each 16-lane group, source lane s addresses
 // 4 dims (8 bytes) of key k0 + s / 4 at dim c0 + 4 (s % 4), and lane j receives dim c0 + j for keys
-// k0 .. k0 + 3. Rows are 128 bytes; 16-byte chunk c of key row r sits in slot c ^ ((r >> 1) & 7) so
-// the K fragment reads (32 consecutive keys at one chunk) cover all 64 banks.
+// k0 .. k0 + 3. Rows are 128 bytes; 16-byte chunk c of key row r sits in slot c ^ kv_swz(r) (below).
 // The arithmetic (MFMA order, softmax, P rounding) is that of sq_attention_kernel, so both give
 // bit-identical outputs.
 // ------------------------------------------------------------------------------------------------
 
-__device__ __forceinline__ int kv_slot(int row, int chunk) { return row * 128 + ((chunk ^ ((row >> 1) & 7)) << 4); }
+// Slot of 16-byte chunk `chunk` in 128-byte key row `row`: chunk ^ sw(row), sw a permutation of the
+// row pair m = (row >> 1) & 7 (so 16 consecutive keys at one chunk cover all 64 banks) that also
+// flips bit 2 on odd pairs (so keys k and k + 2 -- one 4x16 transpose read -- use opposite halves
+// of the row). sw(row + 16 j) = sw(row).
+__device__ __forceinline__ int kv_swz(int row) {
+  const int m = (row >> 1) & 7;
+  return m ^ ((m & 1) << 2);
+}
+__device__ __forceinline__ int kv_slot(int row, int chunk) { return row * 128 + ((chunk ^ kv_swz(row)) << 4); }
 
 template <int NST>
 __global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
@@ -343,7 +373,7 @@ __global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
   const i32x4_t rsrc_v = make_buffer_rsrc(kbase + kvkv, bytes);
   const bool loader = wave < 8;
   const int lrow = 8 * wave + (lane >> 3);                  // tile row this lane loads
-  const uint32_t off0 = (uint32_t)lrow * (uint32_t)kvn * 2u + (uint32_t)((((lane & 7) ^ ((lrow >> 1) & 7))) << 4);
+  const uint32_t off0 = (uint32_t)lrow * (uint32_t)kvn * 2u + (uint32_t)(((lane & 7) ^ kv_swz(lrow)) << 4);
   const uint32_t tstep = (uint32_t)kKeyTile * (uint32_t)kvn * 2u;
   const int ntiles = (N + kKeyTile - 1) / kKeyTile;
   auto issue = [&](int stage, int t) __attribute__((always_inline)) {
@@ -362,9 +392,9 @@ __global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
     else wait_vmcnt<6>();
   };
 
-  // Per-lane LDS offsets, fixed for the whole loop: the swizzle of a key row depends only on
-  // (key >> 1) & 7, which is the same for key and key + 16 j (and key + 32 kb), so the k-step / key
-  // block / stage parts of every fragment address are compile-time offsets.
+  // Per-lane LDS offsets, fixed for the whole loop: the swizzle of a key row is the same for key and
+  // key + 16 j (and key + 32 kb), so the k-step / key block / stage parts of every fragment address
+  // are compile-time offsets.
   int koff[QK_STEPS];
 #pragma unroll
   for (int kstep = 0; kstep < QK_STEPS; ++kstep) koff[kstep] = kv_slot(l32, kstep * 2 + g);
@@ -408,33 +438,21 @@ __global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
         for (int v = 0; v < 16; ++v)
           if (t * kKeyTile + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3) >= N) s[kb][v] = -INFINITY;
     }
-    float mx = s[0][0];
+    float mq[4];  // four short chains, combined as a tree
 #pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
+    for (int q4 = 0; q4 < 4; ++q4) {
+      mq[q4] = s[q4 >> 1][8 * (q4 & 1)];
 #pragma unroll
-      for (int v = 0; v < 16; ++v) mx = fmaxf(mx, s[kb][v]);
-    mx = fmaxf(mx, __shfl_xor(mx, 32, 64));
+      for (int v = 1; v < 8; ++v) mq[q4] = fmaxf(mq[q4], s[q4 >> 1][8 * (q4 & 1) + v]);
+    }
+    const float mx = xor32_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
     const float m_new = softmax_ref_max(m_i, mx, scale_log2);
     const float alpha = __builtin_amdgcn_exp2f((m_i - m_new) * scale_log2);
     const float mc = m_new * scale_log2;
-    float rs = 0.0f;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) {
-        const float p = __builtin_amdgcn_exp2f(fmaf(s[kb][v], scale_log2, -mc));
-        s[kb][v] = p;
-        rs += p;
-      }
-    rs += __shfl_xor(rs, 32, 64);
-    l_i = l_i * alpha + rs;
-    m_i = m_new;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
-#pragma unroll
-      for (int d = 0; d < OB; ++d)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[d][v] *= alpha;
-    }
+      for (int v = 0; v < 16; ++v) s[kb][v] = __builtin_amdgcn_exp2f(fmaf(s[kb][v], scale_log2, -mc));
     bf16x8_t pf[4];
 #pragma unroll
     for (int j = 0; j < 4; ++j) {
@@ -442,6 +460,15 @@ __global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
 #pragma unroll
       for (int e = 0; e < 8; ++e) tmp[e] = s[j >> 1][8 * (j & 1) + e];
       pf[j] = pack_bf16x8(tmp);
+    }
+    const float rs = prob_row_sum(pf);
+    l_i = l_i * alpha + rs;
+    m_i = m_new;
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+      for (int d = 0; d < OB; ++d)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) o[d][v] *= alpha;
     }
     // V^T fragment of d-block db, k-step j: elements 0..3 = keys 16j + 4g + {0..3}, elements 4..7 =
     // keys 16j + 8 + 4g + {0..3}, at dim 32 db + l32 (the P^T order above).
