@@ -22,6 +22,8 @@
 // flight during the current tile's MFMAs, so each (image, head) streams its K/V once.
 #include <stdlib.h>
 
+#include <atomic>
+
 #include <type_traits>
 
 #include "common.hpp"
@@ -577,11 +579,7 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
   const bool dma = Dh == 64 && w >= 8 && !staged_forced && N * kvn * 2 < ((int64_t)1 << 31);
   if (dma) {
     const size_t lds_dma = (size_t)kAttnStages * 2 * kKeyTile * 128;
-    const void* fd = (const void*)sq_attention_dma_kernel<kAttnStages>;
-    if (lds_dma > 64 * 1024) {
-      hipError_t e = hipFuncSetAttribute(fd, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_dma);
-      if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "sparse_query_attention: %s", hipGetErrorString(e));
-    }
+    static_assert((size_t)kAttnStages * 2 * kKeyTile * 128 <= 64 * 1024, "needs no larger-LDS attribute");
     sq_attention_dma_kernel<kAttnStages><<<grid, w * 64, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,
                                                                          (int)N, scale_log2, out, ors, w);
     return check_launch("sparse_query_attention");
@@ -591,8 +589,17 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
                             : (const void*)sq_attention_kernel<64, kMinWaves, false>;
   const size_t lds = Dh == 64 ? 2 * (64 * 128 + 64 * 136) : 2 * (64 * 256 + 128 * 136);
   if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+    // Once per kernel instance and device.
+    static std::atomic<uint8_t> attr_set[64][3];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "sparse_query_attention: %s", hipGetErrorString(e));
+    const int which = Dh == 128 ? 0 : (w >= 8 ? 1 : 2);
+    if (!attr_set[dev & 63][which].load(std::memory_order_acquire)) {
+      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "sparse_query_attention: %s", hipGetErrorString(e));
+      attr_set[dev & 63][which].store(1, std::memory_order_release);
+    }
   }
   if (Dh == 128)
     sq_attention_kernel<128, kMinWaves, false><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,

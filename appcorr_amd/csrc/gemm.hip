@@ -29,6 +29,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <atomic>
 #include <mutex>
 #include <type_traits>
 
@@ -1263,8 +1264,17 @@ static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t 
   const gemm_fn fn = cfg.fn[epi];
   OUDJAT_REQUIRE(fn != nullptr, OUDJAT_ERR_UNSUPPORTED_SHAPE, "%s: no kernel for this epilogue", what);
   if (lds > 64 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-    if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "%s: hipFuncSetAttribute: %s", what, hipGetErrorString(e));
+    // Once per kernel and device (also keeps the call out of captured launch sequences).
+    static std::atomic<uint8_t> attr_set[64][kNumCfgs][6];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
+    std::atomic<uint8_t>& flag = attr_set[dev & 63][ci][epi];
+    if (!flag.load(std::memory_order_acquire)) {
+      e = hipFuncSetAttribute((const void*)fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
+      if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "%s: hipFuncSetAttribute: %s", what, hipGetErrorString(e));
+      flag.store(1, std::memory_order_release);
+    }
   }
   const int threads = cfg.wgm * cfg.wgn * (cfg.pf == -2 ? cfg.ks : 1) * 64;
   static const int group_m = env_int("OUDJAT_GEMM_GROUP_M", 8);

@@ -9,6 +9,8 @@
 // The same workgroup writes the whole PackedQueryState of its image (update_indice, batch/pos/token
 // index, patch mask, RoPE table row) and, if asked, the per-token slot map that the fused
 // reconstruct kernel uses. Nothing here needs the host: k is a launch argument.
+#include <atomic>
+
 #include "common.hpp"
 
 namespace oudjat {
@@ -202,9 +204,17 @@ extern "C" int oudjat_topk_plan(const float* scores, int64_t B, int64_t P, int64
   OUDJAT_REQUIRE(lds <= kMaxPlanLds, OUDJAT_ERR_TOO_LARGE, "topk_plan: needs %lld bytes of LDS (max %lld)",
                  (long long)lds, (long long)kMaxPlanLds);
   if (lds > 48 * 1024) {
-    hipError_t e = hipFuncSetAttribute((const void*)topk_plan_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
-                                       (int)lds);
-    if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "topk_plan: hipFuncSetAttribute: %s", hipGetErrorString(e));
+    // Raised to the maximum once per device (also keeps the call out of captured launch sequences).
+    static std::atomic<uint8_t> attr_set[64];
+    int dev = 0;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "topk_plan: hipGetDevice: %s", hipGetErrorString(e));
+    if (!attr_set[dev & 63].load(std::memory_order_acquire)) {
+      e = hipFuncSetAttribute((const void*)topk_plan_kernel, hipFuncAttributeMaxDynamicSharedMemorySize,
+                              (int)kMaxPlanLds);
+      if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "topk_plan: hipFuncSetAttribute: %s", hipGetErrorString(e));
+      attr_set[dev & 63].store(1, std::memory_order_release);
+    }
   }
   topk_plan_kernel<<<(unsigned)B, kPlanThreads, (size_t)lds, as_stream(stream)>>>(
       scores, (int)P, ssb, (int)k, dindice, dsb, (int)npre, (int)ntok, upd, abat, apos, atok, pmask, ridx, keep,

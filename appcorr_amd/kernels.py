@@ -240,6 +240,23 @@ def packed_residual_persist_ln(x_act: torch.Tensor, x_attn: torch.Tensor, mlp: t
     return x_new, ln_out
 
 
+_PTR_ARRAYS: dict = {}
+
+
+def _device_pointer_array(ptrs, device) -> torch.Tensor:
+    """Device int64 array of the given addresses, built once per distinct list (the per-layer cache
+    tensors of a session keep their addresses), so repeated calls copy nothing from the host and can
+    run inside a captured HIP graph."""
+    key = (str(device), tuple(ptrs))
+    t = _PTR_ARRAYS.get(key)
+    if t is None:
+        if len(_PTR_ARRAYS) > 256:
+            _PTR_ARRAYS.clear()
+        t = torch.tensor(list(ptrs), dtype=torch.int64).to(device)
+        _PTR_ARRAYS[key] = t
+    return t
+
+
 def fold_residual_rows(x: torch.Tensor, row_slot: torch.Tensor, x_packed: torch.Tensor, blocks_out_sums,
                        out: torch.Tensor | None = None) -> torch.Tensor:
     """x [B, N, C] after a run of correction blocks whose selected rows stayed packed: selected rows from
@@ -256,7 +273,7 @@ def fold_residual_rows(x: torch.Tensor, row_slot: torch.Tensor, x_packed: torch.
              "fold_residual_rows: x_packed must be contiguous bf16 [M, C]")
     if out is None:
         out = torch.empty_like(x)
-    ptrs = torch.tensor([b.data_ptr() for b in blocks_out_sums] or [0], dtype=torch.int64).to(x.device)
+    ptrs = _device_pointer_array([b.data_ptr() for b in blocks_out_sums] or [0], x.device)
     C = x.shape[2]
     _launch("fold", x, "oudjat_fold_residual_rows", _ptr(x), x.numel() // C, C, _ptr(row_slot), _ptr(x_packed),
             _ptr(ptrs), len(blocks_out_sums), _ptr(out), _stream(x))

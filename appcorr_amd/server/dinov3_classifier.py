@@ -201,6 +201,35 @@ class DINOv3ClassifierExecutor(ModelExecutor):
         context["cache_feature"] = cache
         return self.dinov3_correct_event_metadata()
 
+    def capture_correct_forward(self, params: Dict[str, Any], context: Dict[str, Any], config: Any,
+                                warmup: int = 2):
+        """Record one correction pass into a HIP graph and return its replay function.
+
+        The query-plan cache is cleared before recording, so the recorded work includes building the
+        plan: every replay rebuilds it from the current scores and runs every block, on the tensors
+        the recording used (context["input_tokens"], context["mobile_pscore_hint_map"], the cache
+        dict's K/V and blocks_out_sum tensors, the group plan); refresh their contents in place
+        between replays.
+        context["current_feature"] after a replay holds that replay's output. Outputs equal an eager
+        correct_forward bit for bit; the running statistics in the cache hold one pass's values.
+        """
+        from appcorr_amd.dinov3.layers import SelfAttentionBlock
+        from appcorr_amd.graphs import capture
+
+        stat_keys = ("_token_pscore_kept_mass_total", "_token_pscore_full_mass_total", "_partial_token_kept_patch_total",
+                     "_partial_token_full_patch_total", "_partial_token_sample_total",
+                     "_token_prune_kept_patch_total", "_token_prune_full_patch_total")
+
+        def run():
+            cache = context.setdefault("cache_feature", {})
+            SelfAttentionBlock._invalidate_partial_token_derived_caches(cache)
+            for k in stat_keys:  # recorded from zero: each replay leaves one pass's statistics
+                cache.pop(k, None)
+            self.correct_forward(params, context, config)
+
+        with torch.no_grad():
+            return capture(run, self.device, warmup)
+
     def head_inference(self, task: Task, context: Dict[str, Any], config: Any) -> Dict[str, Any]:
         feat = context.get("current_feature")
         xn = self.model.final_norm(feat)

@@ -9,9 +9,12 @@ the importance reduction, the top-k plan (recomputed every pass) and all 24 corr
 blocks_out_sum caches come from an untimed approximate pass over the base tokens.
 
 Output: one JSON line on stdout. `value` = corrected tokens/s = B*k / pass time; `ms_per_step` =
-ms per correction pass. `roofline` is for the dominant kernel, timed live with HIP events around
-each of its launches inside the timed steps; `cpu_baseline` times the CPU oracle (the reference's
-eager op sequence on bf16 CPU tensors) on a bounded sample of the same workload.
+ms per correction pass. By default the step is recorded once into a HIP graph and the timed steps
+are replays (every kernel of the pass runs each step; `config.eager_ms_per_step` is the same K steps
+launched one kernel at a time, `--graph 0` reports that instead). `roofline` is for the dominant
+kernel, timed live with HIP events around each of its launches in the eager steps; `cpu_baseline`
+times the CPU oracle (the reference's eager op sequence on bf16 CPU tensors) on a bounded sample of
+the same workload.
 
 Only one GPU is used: `--gpus N` with N > 1 exits with an explanation.
 """
@@ -154,6 +157,9 @@ def main():
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline sampling (0 = skip)")
     ap.add_argument("--cache", default="approx", choices=("approx", "random"),
                     help="fill the K/V + residual caches with the approximate pass (default) or random values")
+    ap.add_argument("--graph", type=int, default=1,
+                    help="1: record the step into a HIP graph and time its replays (the eager time is reported "
+                         "alongside); 0: time eager launches only")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="before the timed steps, copy this many MiB device-to-device once (a plain copy of known "
                          "size that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -241,22 +247,32 @@ def main():
         roctx = _roctx()
         if roctx is not None:
             roctx.roctxProfilerResume(0)
-        K.set_probe(args.probe)
         s = torch.cuda.current_stream()
-        t0, t1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
-        torch.cuda.synchronize()
-        wall0 = time.perf_counter()
-        t0.record(s)
-        for _ in range(args.steps):
-            step()
-        t1.record(s)
-        torch.cuda.synchronize()
-        wall = time.perf_counter() - wall0
-        if roctx is not None:
-            roctx.roctxProfilerPause(0)
+
+        def timed(fn):
+            a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+            torch.cuda.synchronize()
+            w0 = time.perf_counter()
+            a.record(s)
+            for _ in range(args.steps):
+                fn()
+            b.record(s)
+            torch.cuda.synchronize()
+            return a.elapsed_time(b) / args.steps, time.perf_counter() - w0
+
+        # Eager launches, with the probe on the roofline launch site.
+        K.set_probe(args.probe)
+        ms_eager, wall_eager = timed(step)
         events = K.probe_events()
         K.set_probe(None)
-    ms = t0.elapsed_time(t1) / args.steps
+        ms, wall = ms_eager, wall_eager
+        if args.graph:
+            from appcorr_amd.graphs import capture
+
+            replay = capture(step, dev, warmup=1)
+            ms, wall = timed(replay)
+        if roctx is not None:
+            roctx.roctxProfilerPause(0)
     value = B * k / (ms / 1e3)
 
     roof = None
@@ -294,7 +310,9 @@ def main():
         "config": {"workload": f"dinov3_{args.config}_correction", "batch": B, "tokens_per_image": N,
                    "keep_ratio": args.keep, "k": k, "selected_rows": B * T, "blocks": depth,
                    "pass_tflop": round(flops / 1e12, 4), "pass_tflops_achieved": round(flops / (ms / 1e3) / 1e12, 1),
-                   "wall_ms_per_step": round(wall * 1e3 / args.steps, 4)},
+                   "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
+                   "launch": "hip_graph" if args.graph else "eager",
+                   "eager_ms_per_step": round(ms_eager, 4)},
         "roofline": roof, "cpu_baseline": cpu,
     }
     print(json.dumps(line), flush=True)
