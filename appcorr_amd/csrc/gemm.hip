@@ -4,7 +4,12 @@
 // natural operand layout of v_mfma_f32_32x32x16_bf16: each lane feeds 8 consecutive K values of one
 // row of A and one row of W, i.e. one 16-byte LDS read per operand per MFMA.
 //
-// Three kernel families (templates over the workgroup tile BM x BN and the WGM x WGN wave grid):
+// Kernel families (templates over the workgroup tile BM x BN and the WGM x WGN wave grid):
+//   * gemm_bf16_pp_kernel: 288-row tiles (M = B (5 + k) = 4176 = 14.5 x 288 at the headline shape)
+//     with 8 waves in two groups that alternate between MFMA-only and LDS-read phases; fc1 and the
+//     fused QKV projection.
+//   * gemm_bf16_r16_kernel: 144- and 288-row tiles on 16x16x32 MFMAs with optional split K inside
+//     the workgroup; the N = C projections.
 //   * gemm_bf16_pipe_kernel: direct-to-LDS loads (global_load_lds, no staging registers), K tiles of
 //     32 in four LDS stages issued three tiles ahead, fragments read one K tile ahead of their
 //     MFMAs. 256 x 256 tiles with 8 waves; used when one round of tiles fills the GPU.
@@ -329,37 +334,55 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
     const int lg_cph = __builtin_ctz((unsigned)(half >> 3));  // chunk pairs per head = Dh / 16
     constexpr int PPR = BN / 16;                               // chunk pairs per tile row
     constexpr int ITEMS = (BM * PPR + NW * 64 - 1) / (NW * 64);
+    // The row metadata of all of a thread's items is loaded first (one round trip), and every item
+    // loads its RoPE table rows unconditionally (row 0 of the table for rows without RoPE, whose
+    // values are then not used), so the unrolled items overlap their memory latencies instead of
+    // running one dependent load chain after another.
+    bool rope[ITEMS];
+    int64_t trow[ITEMS], dst[ITEMS];
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
       const int p = threadIdx.x + it * NW * 64;
-      if (p >= BM * PPR) break;
-      const int rl = p / PPR, pr = p - rl * PPR;
-      const int row = m0 + rl;
-      if (row >= M) continue;
+      const int pc = p < BM * PPR ? p : BM * PPR - 1;
+      const int rl = pc / PPR, pr = pc - rl * PPR;
+      const int row = min(m0 + rl, M - 1);
       const int c0 = ((pr >> lg_cph) << (lg_cph + 4)) + ((pr & ((1 << lg_cph) - 1)) << 3);  // head * Dh + 8 c
       const int colg = n0 + c0;
       const int which = colg >= 2 * HD ? 2 : (colg >= HD ? 1 : 0);
       const int hcol = colg - which * HD;  // column within q, k or v
+      const bool pm = qa.pm[row];
+      const int64_t ri = qa.ridx[row], bi = qa.bi[row], ti = qa.ti[row];
+      rope[it] = which < 2 && pm;
+      trow[it] = (rope[it] ? ri * qa.tst : 0) + (c0 & (qa.Dh - 1));
+      dst[it] = (which == 0 ? (int64_t)row * HD : bi * qa.kvb + ti * qa.kvn + (which - 1) * HD) + hcol;
+    }
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      const int p = threadIdx.x + it * NW * 64;
+      const int pc = p < BM * PPR ? p : BM * PPR - 1;
+      const int rl = pc / PPR, pr = pc - rl * PPR;
+      const int c0 = ((pr >> lg_cph) << (lg_cph + 4)) + ((pr & ((1 << lg_cph) - 1)) << 3);
+      const int colg = n0 + c0;
       uint4 lo = *reinterpret_cast<const uint4*>(ct + rl * LDT + c0);
       uint4 hi = *reinterpret_cast<const uint4*>(ct + rl * LDT + c0 + half);
-      if (which < 2 && qa.pm[row]) {
-        float l[8], rr[8], cl8[8], cr8[8], sl8[8], sr8[8];
+      float cl8[8], cr8[8], sl8[8], sr8[8];
+      load8f(qa.cos_t + trow[it], cl8);
+      load8f(qa.cos_t + trow[it] + half, cr8);
+      load8f(qa.sin_t + trow[it], sl8);
+      load8f(qa.sin_t + trow[it] + half, sr8);
+      if (rope[it]) {
+        float l[8], rr[8];
         unpack8(lo, l);
         unpack8(hi, rr);
-        const int64_t tr = qa.ridx[row] * qa.tst + (c0 & (qa.Dh - 1));
-        load8f(qa.cos_t + tr, cl8);
-        load8f(qa.cos_t + tr + half, cr8);
-        load8f(qa.sin_t + tr, sl8);
-        load8f(qa.sin_t + tr + half, sr8);
         rope8(l, rr, cl8, cr8, sl8, sr8);
         lo = pack8(l);
         hi = pack8(rr);
       }
-      uint16_t* dst = (which == 0 ? qa.q_out + (int64_t)row * HD
-                                  : qa.kv + qa.bi[row] * qa.kvb + qa.ti[row] * qa.kvn + (which - 1) * HD) +
-                      hcol;
-      *reinterpret_cast<uint4*>(dst) = lo;
-      *reinterpret_cast<uint4*>(dst + half) = hi;
+      if (p < BM * PPR && m0 + rl < M) {
+        uint16_t* d = (colg < HD ? qa.q_out : qa.kv) + dst[it];
+        *reinterpret_cast<uint4*>(d) = lo;
+        *reinterpret_cast<uint4*>(d + half) = hi;
+      }
     }
     return;
   }
@@ -367,6 +390,9 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
   if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) {
     // Fully unrolled: all LDS reads of a thread's chunks first, then the table lookups, then the
     // stores, so the LDS latencies overlap.
+    // Chunks of rows at or past M are never stored: they are set to bf16 1.0 (inside the table
+    // range) instead of read, so that their values (bf16(bias) on the zero-loaded rows, exactly zero
+    // with zero biases, below the table range) cannot send the wave to the per-element path.
     constexpr int ITERS = (BM * CPR + NT - 1) / NT;
     uint4 o[ITERS];
 #pragma unroll
@@ -374,7 +400,8 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
       const int c = threadIdx.x + it * NT;
       const int cc = c < BM * CPR ? c : BM * CPR - 1;
       const int rl = cc / CPR, cl = (cc - rl * CPR) * 8;
-      o[it] = *reinterpret_cast<const uint4*>(ct + rl * LDT + cl);
+      o[it] = (c < BM * CPR && m0 + rl < M) ? *reinterpret_cast<const uint4*>(ct + rl * LDT + cl)
+                                             : make_uint4(0x3f803f80u, 0x3f803f80u, 0x3f803f80u, 0x3f803f80u);
     }
 #pragma unroll
     for (int it = 0; it < ITERS; ++it) {
@@ -836,6 +863,77 @@ __host__ __device__ constexpr int r16_lut_offset(int bm, int bn, int wgm, int wg
   return stages > epi ? stages : epi;
 }
 
+// Epilogue of the 16-row-block kernels. Block (i, j) of a wave holds the transposed product: lane l,
+// register v -> row wm0 + i * 16 + l % 16, column wn0 + j * 16 + 4 (l / 16) + v. With two K groups,
+// group 1's partial sums are added into group 0's through LDS first. Then one wave row at a time
+// writes bf16(acc + bias) into an LDS tile and every thread finishes the epilogue of those rows.
+// The caller's LDS stages must be free (no wave still reads them); this function begins with a barrier.
+template <int BM, int BN, int WGM, int WGN, int KSPLIT, int FMB, int FNB, int EPI>
+__device__ __forceinline__ void r16_epilogue(f32x4_t (&acc)[FMB][FNB], unsigned char* smem, int kLutOff, int kg, int wr,
+                                             int wm, int wn0, int lane, int m0, int n0, int M, const EpiArgs& ea,
+                                             uint16_t* __restrict__ C, int64_t ldc) {
+  constexpr int NWG = WGM * WGN;
+  constexpr int NT = NWG * KSPLIT * 64;
+  constexpr int WM = BM / WGM;
+  constexpr int LDT = BN + 8;
+  constexpr int RED = KSPLIT > 1 ? NWG * 64 * FMB * FNB * 4 * 4 : 0;  // fp32 partial bytes
+  uint16_t* ct = reinterpret_cast<uint16_t*>(smem + RED);
+  block_barrier();
+  if constexpr (KSPLIT > 1) {
+    // Group 1 parks its accumulators in LDS ([block][register][thread] fp32), group 0 adds them.
+    float* red = reinterpret_cast<float*>(smem);
+    const int t0 = wr * 64 + lane;
+    if (kg == 1) {
+#pragma unroll
+      for (int i = 0; i < FMB; ++i)
+#pragma unroll
+        for (int j = 0; j < FNB; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) red[((i * FNB + j) * 4 + v) * (NWG * 64) + t0] = acc[i][j][v];
+    }
+    __syncthreads();
+    if (kg == 0) {
+#pragma unroll
+      for (int i = 0; i < FMB; ++i)
+#pragma unroll
+        for (int j = 0; j < FNB; ++j)
+#pragma unroll
+          for (int v = 0; v < 4; ++v) acc[i][j][v] += red[((i * FNB + j) * 4 + v) * (NWG * 64) + t0];
+    }
+  }
+  // One wave row at a time: its waves write bf16(acc + bias) into the LDS tile, then every thread
+  // finishes the epilogue of those WM rows.
+#pragma unroll
+  for (int h = 0; h < WGM; ++h) {
+    // Wave rows that start at or past M hold only rows that are never stored (the second half of
+    // the last 288-row tile at M = 14.5 x 288): skip them (block-uniform, so the barriers still pair).
+    if (m0 + h * WM >= M) break;
+    if (h > 0) __syncthreads();
+    if (kg == 0 && wm == h) {
+#pragma unroll
+      for (int j = 0; j < FNB; ++j) {
+        const int cl = wn0 + j * 16 + 4 * (lane >> 4);
+        float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+        if (ea.bias) {
+          const uint2 bw = *reinterpret_cast<const uint2*>(ea.bias + n0 + cl);
+          b0 = lo_bf16(bw.x); b1 = hi_bf16(bw.x); b2 = lo_bf16(bw.y); b3 = hi_bf16(bw.y);
+        }
+#pragma unroll
+        for (int i = 0; i < FMB; ++i) {
+          uint2 w;
+          w.x = cvt_pk_bf16(acc[i][j][0] + b0, acc[i][j][1] + b1);
+          w.y = cvt_pk_bf16(acc[i][j][2] + b2, acc[i][j][3] + b3);
+          *reinterpret_cast<uint2*>(ct + (i * 16 + (lane & 15)) * LDT + cl) = w;
+        }
+      }
+    }
+    __syncthreads();
+    store_tile_phase2<WM, BN, NT, EPI>(reinterpret_cast<unsigned char*>(ct),
+                                       reinterpret_cast<const uint16_t*>(smem + kLutOff), m0 + h * WM, n0, M, ea, C,
+                                       ldc);
+  }
+}
+
 // FB: fragments read one K tile ahead (double-buffered registers); without it they are read right
 // after the barrier of their own K tile (for wave tiles whose accumulators leave no room).
 template <int BM, int BN, int WGM, int WGN, int KSPLIT, int BK, int NST, bool FB, int EPI>
@@ -856,7 +954,6 @@ void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t 
   constexpr int STAGE = (BM + BN) * L::kRowBytes;
   static_assert(BM % L::kRowsPerLoad == 0 && BN % L::kRowsPerLoad == 0, "rows must fill whole load instructions");
   static_assert(SUB % KSPLIT == 0 && SUBW >= 1 && WM % 16 == 0 && WN % 16 == 0 && NST >= 2, "tile shape");
-  typedef float f32x4v __attribute__((ext_vector_type(4)));
 
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int kLutOff = r16_lut_offset(BM, BN, WGM, WGN, KSPLIT, BK, NST);
@@ -935,11 +1032,11 @@ void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t 
     }
   };
 
-  f32x4v acc[FMB][FNB];
+  f32x4_t acc[FMB][FNB];
 #pragma unroll
   for (int i = 0; i < FMB; ++i)
 #pragma unroll
-    for (int j = 0; j < FNB; ++j) acc[i][j] = f32x4v{0.0f, 0.0f, 0.0f, 0.0f};
+    for (int j = 0; j < FNB; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
   // Fragments (16x16x32): lane l reads row l % 16 of a 16-row block at K chunk 4 * sub + l / 16.
   struct Frags {
@@ -1035,62 +1132,190 @@ void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t 
     }
   }
 
-  // Epilogue. Block (i, j) holds the transposed product: lane l, register v -> row wm0 + i * 16 + l % 16,
-  // column wn0 + j * 16 + 4 (l / 16) + v.
-  constexpr int LDT = BN + 8;
-  constexpr int RED = KSPLIT > 1 ? NWG * 64 * FMB * FNB * 4 * 4 : 0;  // fp32 partial bytes
-  uint16_t* ct = reinterpret_cast<uint16_t*>(smem + RED);
+  r16_epilogue<BM, BN, WGM, WGN, KSPLIT, FMB, FNB, EPI>(acc, smem, kLutOff, kg, wr, wm, wn0, lane, m0, n0, M, ea, C,
+                                                      ldc);
+}
+
+// ------------------------------------------------------------------------------------------------
+// Ping-pong kernel: BM x BN tiles, 8 waves in two groups of 4, group g owning rows
+// [g BM / 2, (g + 1) BM / 2) and waves w, w + 4 sharing SIMD w % 4 (wave tile BM / 2 x BN / 4).
+// Between workgroup barriers each group runs one of two kinds of phase, and the groups alternate:
+//   * compute phase: only the MFMAs of one 32-deep K step, on fragments already in registers;
+//   * memory phase: the LDS fragment reads of the wave's next K step, and the group's share of the
+//     direct-to-LDS loads of a later K tile.
+//   group 0: mem(0)  comp(0)  mem(1)   comp(1)  ...  mem(S-1)  comp(S-1)  -
+//   group 1: -       mem(0)   comp(0)  mem(1)   ...  comp(S-2) mem(S-1)   comp(S-1)
+// While one wave of a SIMD issues MFMAs back to back, the other's LDS reads are in flight. (The
+// 8-wave kernel above runs both waves of a SIMD in the same order: the older one takes the MFMA
+// issue slots first and then waits a third of the K loop at the barrier for the younger one, which
+// meanwhile runs alone with its LDS latencies exposed. Measured same-process on MI355X, this
+// schedule is 2-3 % faster on the 288-row tiles; a one-barrier-per-step variant, each group reading
+// and computing in opposite order within the interval, was not faster.)
+// Loads: two 64-deep stages (a K tile is two steps); a load instruction moves 1 KB and the CU's
+// vector memory path takes ~16 clocks for it, so a tile's loads (~1100 clocks at 288 x 256) are
+// split between the groups, each issuing its half in its first memory phase of the previous tile
+// (the stage it reuses was last read in the interval before): group g loads half g of the W rows,
+// W first (both groups read them from group 0's next memory phase on), then its own A rows. Group
+// 0 waits for all of its loads of tile u + 1 at the end of compute(2u + 1); group 1 for its W rows
+// at the end of mem(2u + 1) and for its A rows at the end of compute(2u + 1).
+// ------------------------------------------------------------------------------------------------
+template <int BM, int BN, int EPI>
+__global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
+void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t lda, const uint16_t* __restrict__ W,
+                         int N, int64_t ldw, EpiArgs ea, uint16_t* __restrict__ C, int64_t ldc, int group_m) {
+  constexpr int BK = 64, NST = 2, WGM = 2, WGN = 4;
+  using L = R16Layout<BK>;
+  constexpr int WM = BM / WGM, WN = BN / WGN;
+  constexpr int FMB = WM / 16, FNB = WN / 16;
+  constexpr int RPL = L::kRowsPerLoad;
+  constexpr int NIA = BM / RPL, NIW = BN / RPL;  // load instructions per K tile
+  constexpr int STAGE = (BM + BN) * L::kRowBytes;
+  static_assert(BM % (2 * RPL) == 0 && BN % (2 * RPL) == 0, "rows must split into whole load halves");
+  static_assert(WM % 16 == 0 && WN % 16 == 0, "tile shape");
+
+  extern __shared__ __align__(16) unsigned char smem[];
+  constexpr int kLutOff = r16_lut_offset(BM, BN, WGM, WGN, 1, BK, NST);
+  if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) load_gelu_table<512>(smem + kLutOff);
+
+  const int tiles_n = (N + BN - 1) / BN;
+  const int tiles_m = (M + BM - 1) / BM;
+  const int tiles = gridDim.x;
+  const int bid = blockIdx.x;
+  const int xcd = bid % kNumXcd;
+  const int q = tiles / kNumXcd, r = tiles % kNumXcd;
+  const int tile = xcd * q + min(xcd, r) + bid / kNumXcd;
+  const int per_group = group_m * tiles_n;
+  const int grp = tile / per_group;
+  const int first_m = grp * group_m;
+  const int gsize = min(tiles_m - first_m, group_m);
+  const int in_grp = tile - grp * per_group;
+  const int tm = first_m + in_grp % gsize, tn = in_grp / gsize;
+  const int m0 = tm * BM, n0 = tn * BN;
+
+  const int lane = threadIdx.x & 63;
+  const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
+  const int g = wave >> 2;  // group = wave row
+  const int lw = wave & 3;  // wave within its group = wave column
+  const int wm0 = g * WM;
+  const int wn0 = lw * WN;
+
+  // Loads: a range of the stage's load instructions [ib, ib + CNT) is spread over the group's 4
+  // waves, instruction ib + lw + 4 j to wave lw; instruction i fills stage rows [i RPL, (i + 1) RPL)
+  // (A rows first, then W rows). Each lane keeps one 32-bit byte offset for its first instruction
+  // (its row plus its swizzled chunk); instruction j adds j * 4 * RPL rows. The range starts are
+  // even, so a lane's chunk swizzle is the same for all of its instructions. Rows at or past M / N
+  // fall outside the buffer descriptors and load as zeros.
+  const i32x4_t rsrc_a = make_buffer_rsrc(A, (uint32_t)((int64_t)M * lda * 2));
+  const i32x4_t rsrc_w = make_buffer_rsrc(W, (uint32_t)((int64_t)N * ldw * 2));
+  const uint32_t step_a = (uint32_t)(4 * RPL) * (uint32_t)lda * 2u;
+  const uint32_t step_w = (uint32_t)(4 * RPL) * (uint32_t)ldw * 2u;
+  auto lane_offset = [&](int ib, bool w_rows) __attribute__((always_inline)) {
+    const int lrow = lane / L::kChunks, lslot = lane % L::kChunks;
+    const int row0 = (ib + lw) * RPL + lrow;
+    const int chunk = lslot ^ ((row0 / L::kRowsPerLine) % L::kChunks);
+    return w_rows ? (uint32_t)((n0 + row0 - BM) * (uint32_t)ldw * 2u + chunk * 16)
+                  : (uint32_t)((m0 + row0) * (uint32_t)lda * 2u + chunk * 16);
+  };
+  const int ib_w = NIA + g * (NIW / 2), ib_a = g * (NIA / 2);
+  const uint32_t vw = lane_offset(ib_w, true), va = lane_offset(ib_a, false);
+  auto issue_tile = [&](int kt) __attribute__((always_inline)) {
+    unsigned char* base = smem + (kt % NST) * STAGE;
+    const uint32_t koff = (uint32_t)(kt * BK * 2);
+    constexpr int CW = NIW / 2, CA = NIA / 2;
+#pragma unroll
+    for (int j = 0; j < (CW + 3) / 4; ++j)
+      if (j < CW / 4 || lw < CW % 4)
+        buffer_load_lds16(rsrc_w, base + (ib_w + lw + 4 * j) * 1024, vw + (uint32_t)j * step_w + koff);
+#pragma unroll
+    for (int j = 0; j < (CA + 3) / 4; ++j)
+      if (j < CA / 4 || lw < CA % 4)
+        buffer_load_lds16(rsrc_a, base + (ib_a + lw + 4 * j) * 1024, va + (uint32_t)j * step_a + koff);
+  };
+  constexpr int QMAX = (NIW / 2 + 3) / 4 + (NIA / 2 + 3) / 4;  // loads per wave and tile, at most
+  static_assert(QMAX < 32, "vmcnt range");
+  const int n_tile = (NIW / 2) / 4 + (lw < (NIW / 2) % 4 ? 1 : 0) + (NIA / 2) / 4 + (lw < (NIA / 2) % 4 ? 1 : 0);
+
+  f32x4_t acc[FMB][FNB];
+#pragma unroll
+  for (int i = 0; i < FMB; ++i)
+#pragma unroll
+    for (int j = 0; j < FNB; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+
+  // Fragments of one 32-deep step (16x16x32): lane l reads row l % 16 of a 16-row block at K chunk
+  // 4 * (j % 2) + l / 16 of tile j / 2's stage.
+  bf16x8_t fa[FMB], fb[FNB];
+  const int KT = K / BK;
+  const int S = 2 * KT;
+  auto read_frags = [&](int j) __attribute__((always_inline)) {
+    const unsigned char* st = smem + ((j >> 1) % NST) * STAGE;
+    const int ch = 4 * (j & 1) + (lane >> 4);
+#pragma unroll
+    for (int i = 0; i < FMB; ++i)
+      fa[i] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(wm0 + i * 16 + (lane & 15), ch));
+#pragma unroll
+    for (int jj = 0; jj < FNB; ++jj)
+      fb[jj] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(BM + wn0 + jj * 16 + (lane & 15), ch));
+  };
+  // Row blocks at or past M compute on zero rows and are never stored (see gemm_bf16_r16_kernel).
+  auto mfmas = [&]() __attribute__((always_inline)) {
+#pragma unroll
+    for (int i = 0; i < FMB; ++i)
+#pragma unroll
+      for (int jj = 0; jj < FNB; ++jj)
+        acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[jj], fa[i], acc[i][jj], 0, 0, 0);
+  };
+  // n_arows: this wave's A-row loads of a tile (issued after its W rows).
+  const int n_arows = (NIA / 2) / 4 + (lw < (NIA / 2) % 4 ? 1 : 0);
+  auto wait_n = [&](int n) __attribute__((always_inline)) {
+    switch (n) {
+#define OUDJAT_PP_WAIT(v) case v: wait_vmcnt<v>(); break;
+      OUDJAT_PP_WAIT(1) OUDJAT_PP_WAIT(2) OUDJAT_PP_WAIT(3) OUDJAT_PP_WAIT(4) OUDJAT_PP_WAIT(5) OUDJAT_PP_WAIT(6)
+      OUDJAT_PP_WAIT(7) OUDJAT_PP_WAIT(8) OUDJAT_PP_WAIT(9) OUDJAT_PP_WAIT(10) OUDJAT_PP_WAIT(11)
+      OUDJAT_PP_WAIT(12) OUDJAT_PP_WAIT(13) OUDJAT_PP_WAIT(14) OUDJAT_PP_WAIT(15)
+#undef OUDJAT_PP_WAIT
+      default: wait_vmcnt<0>(); break;
+    }
+  };
+  // Memory phase of step j (tile u = j / 2): fragments, then tile u + 1's loads at the tile's first
+  // step (u >= 1), then (group 1, the tile's last step) its W rows of tile u + 1.
+  auto mem_phase = [&](int j) __attribute__((always_inline)) {
+    read_frags(j);
+    const int u = j >> 1;
+    if ((j & 1) == 0 && u >= 1 && u + 1 < KT) issue_tile(u + 1);
+    if (g == 1 && (j & 1) == 1 && u + 1 < KT) wait_n(n_arows);
+  };
+  auto compute_phase = [&](int j) __attribute__((always_inline)) {
+    mfmas();
+    if ((j & 1) == 1 && (j >> 1) + 1 < KT) wait_vmcnt<0>();  // group 0: all of tile u + 1; group 1: its A rows
+  };
+
+  issue_tile(0);
+  if (KT > 1) {
+    issue_tile(1);
+    wait_n(n_tile);  // tile 0 landed, tile 1 may be in flight
+  } else {
+    wait_vmcnt<0>();
+  }
   block_barrier();
-  if constexpr (KSPLIT > 1) {
-    // Group 1 parks its accumulators in LDS ([block][register][thread] fp32), group 0 adds them.
-    float* red = reinterpret_cast<float*>(smem);
-    const int t0 = wr * 64 + lane;
-    if (kg == 1) {
-#pragma unroll
-      for (int i = 0; i < FMB; ++i)
-#pragma unroll
-        for (int j = 0; j < FNB; ++j)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) red[((i * FNB + j) * 4 + v) * (NWG * 64) + t0] = acc[i][j][v];
+  if (g == 0) {
+    for (int j = 0; j < S; ++j) {
+      mem_phase(j);
+      block_barrier();
+      compute_phase(j);
+      block_barrier();
     }
-    __syncthreads();
-    if (kg == 0) {
-#pragma unroll
-      for (int i = 0; i < FMB; ++i)
-#pragma unroll
-        for (int j = 0; j < FNB; ++j)
-#pragma unroll
-          for (int v = 0; v < 4; ++v) acc[i][j][v] += red[((i * FNB + j) * 4 + v) * (NWG * 64) + t0];
+    block_barrier();
+  } else {
+    block_barrier();
+    for (int j = 0; j < S; ++j) {
+      mem_phase(j);
+      block_barrier();
+      compute_phase(j);
+      block_barrier();
     }
   }
-  // One wave row at a time: its waves write bf16(acc + bias) into the LDS tile, then every thread
-  // finishes the epilogue of those WM rows.
-#pragma unroll
-  for (int h = 0; h < WGM; ++h) {
-    if (h > 0) __syncthreads();
-    if (kg == 0 && wm == h) {
-#pragma unroll
-      for (int j = 0; j < FNB; ++j) {
-        const int cl = wn0 + j * 16 + 4 * (lane >> 4);
-        float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
-        if (ea.bias) {
-          const uint2 bw = *reinterpret_cast<const uint2*>(ea.bias + n0 + cl);
-          b0 = lo_bf16(bw.x); b1 = hi_bf16(bw.x); b2 = lo_bf16(bw.y); b3 = hi_bf16(bw.y);
-        }
-#pragma unroll
-        for (int i = 0; i < FMB; ++i) {
-          uint2 w;
-          w.x = cvt_pk_bf16(acc[i][j][0] + b0, acc[i][j][1] + b1);
-          w.y = cvt_pk_bf16(acc[i][j][2] + b2, acc[i][j][3] + b3);
-          *reinterpret_cast<uint2*>(ct + (i * 16 + (lane & 15)) * LDT + cl) = w;
-        }
-      }
-    }
-    __syncthreads();
-    store_tile_phase2<WM, BN, NT, EPI>(reinterpret_cast<unsigned char*>(ct),
-                                       reinterpret_cast<const uint16_t*>(smem + kLutOff), m0 + h * WM, n0, M, ea, C,
-                                       ldc);
-  }
+
+  r16_epilogue<BM, BN, WGM, WGN, 1, FMB, FNB, EPI>(acc, smem, kLutOff, 0, wave, g, wn0, lane, m0, n0, M, ea, C, ldc);
 }
 
 // ------------------------------------------------------------------------------------------------
@@ -1136,6 +1361,13 @@ struct GemmCfg {
     gemm_bf16_r16_kernel<BM, BN, WGM, WGN, KS, BK, NST, FB, kEpiQkv>},                                   \
    BK, NST, KS, FB}
 
+// pf = -3: ping-pong kernel (8 waves: a 2 x 4 wave grid, 64-deep K tiles in two stages).
+#define OUDJAT_GEMM_PP_CFG(BM, BN)                                                                        \
+  {BM, BN, 2, 4, -3,                                                                                     \
+   {gemm_bf16_pp_kernel<BM, BN, 0>, gemm_bf16_pp_kernel<BM, BN, 1>, gemm_bf16_pp_kernel<BM, BN, 2>,      \
+    gemm_bf16_pp_kernel<BM, BN, 3>, gemm_bf16_pp_kernel<BM, BN, 4>, gemm_bf16_pp_kernel<BM, BN, kEpiQkv>}, \
+   64, 2, 1, 0}
+
 static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_CFG(128, 128, 2, 2, 1),  // 0
     OUDJAT_GEMM_CFG(128, 128, 2, 2, 2),  // 1
@@ -1164,6 +1396,8 @@ static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_R16_CFG(144, 128, 1, 4, 2, 64, 3, true),   // 24
     OUDJAT_GEMM_R16_CFG(288, 256, 2, 4, 1, 64, 2, false),  // 25: 288 x 256, 128-byte operand rows
     OUDJAT_GEMM_R16_CFG(288, 192, 2, 4, 1, 64, 2, false),  // 26: 288 x 192 (N = 3 C: 240 tiles)
+    OUDJAT_GEMM_PP_CFG(288, 256),  // 27: ping-pong 288 x 256
+    OUDJAT_GEMM_PP_CFG(288, 192),  // 28: ping-pong 288 x 192
 };
 static constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -1220,11 +1454,12 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   if (N % 128 != 0) return 8;
   const int64_t tiles256 = cdiv(M, 256) * cdiv(N, 256);
   if (N % 256 == 0 && tiles256 >= 128 && tiles256 <= 256) return 15;
-  // 288 x 256 tiles with 128-byte operand rows when they fill three quarters or more of the CUs.
+  // 288 x 256 (ping-pong) tiles with 128-byte operand rows when they fill three quarters or more of
+  // the CUs.
   const int64_t tiles288 = cdiv(M, 288) * (N / 256);
-  if (N % 256 == 0 && tiles288 >= 192 && tiles288 <= 256) return 25;
+  if (N % 256 == 0 && tiles288 >= 192 && tiles288 <= 256) return 27;
   const int64_t tiles288n = cdiv(M, 288) * (N / 192);
-  if (N % 192 == 0 && tiles288n >= 192 && tiles288n <= 256) return 26;
+  if (N % 192 == 0 && tiles288n >= 192 && tiles288n <= 256) return 28;
   // 144-row tiles (one round of 128..256 workgroups) when 256 x 256 tiles do not fit one round.
   const int64_t tm144 = cdiv(M, 144);
   if (N % 512 == 0 && tm144 * (N / 512) >= 128 && tm144 * (N / 512) <= 256) return 22;
@@ -1234,13 +1469,13 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
 
 
 // Fused QKV: tiles must cover whole heads (Dh | BN; a tile may span the q / k / v boundaries).
-// 288 x 192 tiles when the plain choice would leave more CUs idle in its single round.
+// 288 x 192 (ping-pong) tiles when the plain choice would leave more CUs idle in its single round.
 static int choose_qkv_cfg(int64_t M, int64_t N, int64_t K, int64_t Dh) {
   int ci = choose_cfg(M, N, K, true);
   const int64_t tiles288n = cdiv(M, 288) * (N / 192);
   if (env_int("OUDJAT_GEMM_CFG", -1) < 0 && N % 192 == 0 && tiles288n >= 192 && tiles288n <= 256 &&
       cdiv(M, kCfgs[ci].bm) * cdiv(N, kCfgs[ci].bn) < tiles288n)
-    ci = 26;
+    ci = 28;
   if (kCfgs[ci].pf > 0 || kCfgs[ci].bn % Dh != 0 || N % kCfgs[ci].bn != 0) ci = 11;  // 128 x 128 direct-to-LDS
   return ci;
 }
@@ -1255,7 +1490,7 @@ static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t 
   // K stages, or (direct-to-LDS kernels) the bf16 output tile of the epilogue if that is larger.
   size_t lds = cfg.pf < 0 ? (size_t)kStages * (cfg.bm + cfg.bn) * 64 : (size_t)2 * (cfg.bm + cfg.bn) * 128;
   if (cfg.pf <= 0) lds = lds > (size_t)cfg.bm * (cfg.bn + 8) * 2 ? lds : (size_t)cfg.bm * (cfg.bn + 8) * 2;
-  if (cfg.pf == -2) lds = r16_lut_offset(cfg.bm, cfg.bn, cfg.wgm, cfg.wgn, cfg.ks, cfg.bk, cfg.nst);
+  if (cfg.pf == -2 || cfg.pf == -3) lds = r16_lut_offset(cfg.bm, cfg.bn, cfg.wgm, cfg.wgn, cfg.ks, cfg.bk, cfg.nst);
   if (cfg.pf <= 0 && epi == OUDJAT_EPI_BIAS_GELU) lds += kGeluLut * sizeof(uint16_t);
   if (epi == OUDJAT_EPI_BIAS_GELU) {
     const int st = ensure_gelu_table();
@@ -1276,7 +1511,7 @@ static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t 
       flag.store(1, std::memory_order_release);
     }
   }
-  const int threads = cfg.wgm * cfg.wgn * (cfg.pf == -2 ? cfg.ks : 1) * 64;
+  const int threads = cfg.wgm * cfg.wgn * (cfg.pf <= -2 ? cfg.ks : 1) * 64;
   static const int group_m = env_int("OUDJAT_GEMM_GROUP_M", 8);
   hipLaunchKernelGGL(fn, dim3((unsigned)tiles), dim3(threads), lds, stream, A, (int)M, (int)K, lda, W, (int)N, ldw, ea,
                      C, ldc, group_m > 0 ? group_m : 1);
@@ -1359,7 +1594,9 @@ extern "C" int oudjat_linear_kernel_name(int64_t M, int64_t N, int64_t K, int ep
                  "linear_kernel_name: bad arguments");
   const GemmCfg& c = kCfgs[epi == kEpiQkv ? choose_qkv_cfg(M, N, K, 64) : choose_cfg(M, N, K, true)];
   int n;
-  if (c.pf == -2)
+  if (c.pf == -3)
+    n = snprintf(buf, (size_t)buflen, "oudjat::gemm_bf16_pp_kernel<%d, %d, %d>", c.bm, c.bn, epi);
+  else if (c.pf == -2)
     n = snprintf(buf, (size_t)buflen, "oudjat::gemm_bf16_r16_kernel<%d, %d, %d, %d, %d, %d, %d, %s, %d>", c.bm, c.bn,
                  c.wgm, c.wgn, c.ks, c.bk, c.nst, c.fb ? "true" : "false", epi);
   else if (c.pf == -1)
