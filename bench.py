@@ -201,8 +201,14 @@ def main():
     # Synthetic tokens: base ~ N(0,1); full-res = base + delta on patch rows, delta ~ Laplace(0,1).
     g = torch.Generator(device=dev).manual_seed(1)
     x_base = torch.randn(B, N, C, generator=g, device=dev)
-    u = torch.rand(B, P, C, generator=g, device=dev) - 0.5
-    delta = -torch.sign(u) * torch.log1p(-2.0 * u.abs())
+    # u uniform on the open interval (-1, 1) as torch.distributions.Laplace samples it: u = rand - 0.5
+    # with log1p(-2|u|) gives -inf whenever rand returns exactly 0 (about once per 2^24 draws, i.e.
+    # about once in this 16.7M-element tensor), which turns a whole image into NaN downstream.
+    eps = torch.finfo(torch.float32).eps
+    u = torch.rand(B, P, C, generator=g, device=dev) * (2.0 - eps) + (eps - 1.0)
+    delta = -torch.sign(u) * torch.log1p(-u.abs())
+    if not bool(torch.isfinite(delta).all()):
+        raise RuntimeError("bench: non-finite synthetic residual")
     x_full = x_base.clone()
     x_full[:, 5:] += delta
     context = {"input_tokens": x_base.to(torch.bfloat16).contiguous(),
@@ -273,6 +279,10 @@ def main():
             ms, wall = timed(replay)
         if roctx is not None:
             roctx.roctxProfilerPause(0)
+        # The corrected tokens of the last timed pass must be finite (outside the timed region).
+        out = context["current_feature"]
+        if not bool(torch.isfinite(out.float()).all()):
+            raise RuntimeError("bench: the correction pass produced non-finite tokens")
     value = B * k / (ms / 1e3)
 
     roof = None
