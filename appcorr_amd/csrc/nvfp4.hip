@@ -64,27 +64,78 @@ __device__ __forceinline__ float e2m1_decode(uint32_t c) {
   return (c & 8u) ? -mag : mag;
 }
 
-// One workgroup per 128x64 tile; thread t owns row t/2 and blocks 2*(t%2), 2*(t%2)+1 (32 elements).
+// Per-block scale of a 16-element block with maximum magnitude amax: the e4m3 code and the divisor
+// ts * e4m3(code) of its elements.
+__device__ __forceinline__ void nvfp4_block_scale(float amax, float ts, uint32_t& code, float& tot) {
+  const float bs = amax / kE2m1Max;
+  const float scaled = fminf(fmaxf(bs / ts, kE4m3Eps), kE4m3Max);
+  code = e4m3_encode_pos(scaled);
+  tot = ts * e4m3_decode(code);
+}
+
+// e2m1 codes of x_e / tot (IEEE quotient, e = 0..7) as one 32-bit word, element e in nibble e.
+// Quotient: Markstein's correction step. With y = RN(1 / tot) (one IEEE division per block),
+// q0 = RN(x y) is within one ulp of x / tot, the remainder r = x - q0 tot is exact under an FMA,
+// and RN(q0 + r y) is the correctly rounded quotient (Markstein's theorem for round-to-nearest;
+// checked bitwise against IEEE division on 2.7e8 random pairs on gfx950, all-ones significands
+// included). The quotient takes the sign of x, as x / tot does for tot > 0 (the chain alone turns
+// x = -0 into +0). Below the normal range the quotient may differ, but only values far below 0.25
+// are there and their code is 0 with the sign of x either way. A divisor that is not finite and
+// positive (tot == 0 for a block whose scale rounds to e4m3 zero, or a non-positive or non-finite
+// tensor scale) takes IEEE division and the integer encoder.
+// Codes: v_cvt_scalef32_pk_fp4_f32 with scale 1.0, which was checked on gfx950 to give exactly
+// e2m1_encode (round to nearest even, saturation to +-6, -0 -> 0x8) on the neighbourhoods of every
+// rounding boundary, ties, zeros, subnormals and huge values; element 2i goes to the low nibble.
+__device__ __forceinline__ uint32_t nvfp4_codes8(const float* f, float tot, float y) {
+  if (__builtin_expect(!(tot > 0.0f && tot <= 3.40282347e38f), 0)) {
+    uint32_t word = 0;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) word |= e2m1_encode(f[e] / tot) << (4 * e);
+    return word;
+  }
+  float q[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float q0 = f[e] * y;
+    const float r = __builtin_fmaf(-q0, tot, f[e]);
+    q[e] = __builtin_copysignf(__builtin_fmaf(r, y, q0), f[e]);
+  }
+  uint32_t word = 0;
+  word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, q[0], q[1], 1.0f, 0);
+  word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, q[2], q[3], 1.0f, 1);
+  word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, q[4], q[5], 1.0f, 2);
+  word = __builtin_amdgcn_cvt_scalef32_pk_fp4_f32(word, q[6], q[7], 1.0f, 3);
+  return word;
+}
+
+// One workgroup (256 threads) per 128-row x 64 CT-column region (CT scale tiles side by side),
+// 64 / CT rows per pass: lane t of a pass owns row t / (4 CT) and 16-element block t % (4 CT) of the
+// region, so 4 CT consecutive lanes read 128 CT contiguous bytes of one row (two 16-byte loads each)
+// and write its 32 CT bytes of codes (8 each). The block scale is computed once per block; the 4
+// scale bytes of a row within a scale tile are contiguous in the swizzled layout and leave as one
+// 4-byte store from the tile's first lane of the row.
+template <int CT>
 __global__ __launch_bounds__(256) void nvfp4_quantize_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t K,
                                                              int64_t sm, const float* __restrict__ tsp,
                                                              uint8_t* __restrict__ qd, uint8_t* __restrict__ sc) {
-  const int pn = blockIdx.x, pm = blockIdx.y;
+  constexpr int LPR = 4 * CT;        // lanes per row
+  constexpr int RPP = 256 / LPR;     // rows per pass
+  const int pm = blockIdx.y;
   const int t = threadIdx.x;
-  const int r = t >> 1;
-  const int jb = (t & 1) * 2;
-  const int64_t row = (int64_t)pm * 128 + r;
-  const int64_t col0 = (int64_t)pn * 64 + jb * 16;
+  const int j = t % LPR;
+  const int64_t col = ((int64_t)blockIdx.x * CT) * 64 + j * 16;
+  const bool col_ok = col < K;  // K % 16 == 0: a block is wholly in or out
   const float ts = *tsp;
-  const bool row_ok = row < M;
-  uint32_t s8[2];
-  uint32_t packed[4];
+  const int64_t tiles_n = (K + 63) >> 6;
+  const int64_t tile = (int64_t)pm * tiles_n + (int64_t)blockIdx.x * CT + j / 4;
 #pragma unroll
-  for (int bb = 0; bb < 2; ++bb) {
-    const int64_t c0 = col0 + bb * 16;
-    const bool ok = row_ok && c0 < K;
+  for (int pass = 0; pass < 128 / RPP; ++pass) {
+    const int r = pass * RPP + t / LPR;  // row within the tile
+    const int64_t row = (int64_t)pm * 128 + r;
+    const bool ok = col_ok && row < M;
     float f[16];
     if (ok) {
-      const uint4* p = reinterpret_cast<const uint4*>(x + row * sm + c0);
+      const uint4* p = reinterpret_cast<const uint4*>(x + row * sm + col);
       unpack8(p[0], f);
       unpack8(p[1], f + 8);
     } else {
@@ -94,56 +145,66 @@ __global__ __launch_bounds__(256) void nvfp4_quantize_kernel(const uint16_t* __r
     float amax = 0.0f;
 #pragma unroll
     for (int e = 0; e < 16; ++e) amax = fmaxf(amax, fabsf(f[e]));
-    const float bs = amax / kE2m1Max;
-    const float scaled = fminf(fmaxf(bs / ts, kE4m3Eps), kE4m3Max);
-    const uint32_t code = e4m3_encode_pos(scaled);
-    const float tot = ts * e4m3_decode(code);
-    s8[bb] = ok ? code : 0u;
-#pragma unroll
-    for (int w = 0; w < 2; ++w) {
-      uint32_t word = 0;
-#pragma unroll
-      for (int e = 0; e < 8; ++e) word |= e2m1_encode(f[w * 8 + e] / tot) << (4 * e);
-      packed[bb * 2 + w] = word;
-    }
+    uint32_t code;
+    float tot;
+    nvfp4_block_scale(amax, ts, code, tot);
+    const float y = 1.0f / tot;
+    const uint32_t w0 = nvfp4_codes8(f, tot, y), w1 = nvfp4_codes8(f + 8, tot, y);
+    if (ok) *reinterpret_cast<uint2*>(qd + row * (K >> 1) + (col >> 1)) = make_uint2(w0, w1);
+    // Scale bytes of the row's 4 blocks of this tile (zero for blocks past K or rows past M).
+    const uint32_t b = ok ? code : 0u;
+    const uint32_t b1 = __shfl_down(b, 1, 64), b2 = __shfl_down(b, 2, 64), b3 = __shfl_down(b, 3, 64);
+    if ((j & 3) == 0 && ((int64_t)blockIdx.x * CT + j / 4) < tiles_n)
+      *reinterpret_cast<uint32_t*>(sc + tile * 512 + (r & 31) * 16 + (r >> 5) * 4) = b | (b1 << 8) | (b2 << 16) | (b3 << 24);
   }
-  if (row_ok) {
-    uint8_t* qrow = qd + row * (K >> 1);
-    const int64_t qc = (int64_t)pn * 32 + jb * 8;
-    // 8-byte stores: rows of K/2 bytes are only guaranteed 8-byte aligned (K % 16 == 0).
-    if (qc < (K >> 1)) *reinterpret_cast<uint2*>(qrow + qc) = make_uint2(packed[0], packed[1]);
-    if (qc + 8 < (K >> 1)) *reinterpret_cast<uint2*>(qrow + qc + 8) = make_uint2(packed[2], packed[3]);
-  }
-  const int64_t tile = (int64_t)pm * gridDim.x + pn;
-  uint16_t pair = (uint16_t)(s8[0] | (s8[1] << 8));
-  *reinterpret_cast<uint16_t*>(sc + tile * 512 + (r & 31) * 16 + (r >> 5) * 4 + jb) = pair;
 }
 
-// One thread per 16-element block.
+// Dequantize: one workgroup per 128-row x 64 CT-column region, lane t of a pass decoding the 8
+// codes (4 bytes) of 8-element chunk t % (8 CT) of row t / (8 CT), so every 16-byte store of a wave
+// writes 1 KB of consecutive row segments (whole cache lines). e2m1 values by
+// v_cvt_scalef32_pk_f32_fp4 with scale 1.0 (checked on gfx950 against the e2m1 table for all 256
+// code bytes); x = (e2m1 * s) * ts in fp32 (the first product is exact), then bf16.
+template <int CT>
 __global__ __launch_bounds__(256) void nvfp4_dequantize_kernel(const uint8_t* __restrict__ qd,
                                                                const uint8_t* __restrict__ sc,
                                                                const float* __restrict__ tsp, int64_t M, int64_t K,
                                                                uint16_t* __restrict__ out, int64_t os) {
-  const int64_t nb = K >> 4;
-  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-  if (gid >= M * nb) return;
-  const int64_t row = gid / nb;
-  const int64_t jg = gid - row * nb;
+  constexpr int LPR = 8 * CT;
+  constexpr int RPP = 256 / LPR;
+  const int pm = blockIdx.y;
+  const int t = threadIdx.x;
+  const int c = t % LPR;  // 8-element chunk within the region row
+  const int64_t col = ((int64_t)blockIdx.x * CT) * 64 + c * 8;
+  if (col >= K) return;
   const float ts = *tsp;
-  const int64_t grid_n = (K + 63) >> 6;
-  const int64_t pm = row >> 7, pn = jg >> 2;
-  const int r = (int)(row & 127), j = (int)(jg & 3);
-  const float s = e4m3_decode(sc[(pm * grid_n + pn) * 512 + (r & 31) * 16 + (r >> 5) * 4 + j]);
-  const uint2 w = *reinterpret_cast<const uint2*>(qd + row * (K >> 1) + jg * 8);
-  float f[16];
+  const int64_t tiles_n = (K + 63) >> 6;
+  const int64_t tile = (int64_t)pm * tiles_n + (int64_t)blockIdx.x * CT + c / 8;
+  const int jb = (c >> 1) & 3;  // block within the scale tile
 #pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    f[e] = (e2m1_decode((w.x >> (4 * e)) & 15u) * s) * ts;
-    f[8 + e] = (e2m1_decode((w.y >> (4 * e)) & 15u) * s) * ts;
+  for (int pass = 0; pass < 128 / RPP; ++pass) {
+    const int r = pass * RPP + t / LPR;
+    const int64_t row = (int64_t)pm * 128 + r;
+    if (row >= M) break;
+    const float s = e4m3_decode(sc[tile * 512 + (r & 31) * 16 + (r >> 5) * 4 + jb]);
+    const uint32_t w = *reinterpret_cast<const uint32_t*>(qd + row * (K >> 1) + (col >> 1));
+    const auto v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
+    const auto v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
+    const auto v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
+    const auto v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+    const float e2[8] = {v0[0], v0[1], v1[0], v1[1], v2[0], v2[1], v3[0], v3[1]};
+    float f[8];
+#pragma unroll
+    for (int e = 0; e < 8; ++e) f[e] = (e2[e] * s) * ts;
+    *reinterpret_cast<uint4*>(out + row * os + col) = pack8(f);
   }
-  uint4* o = reinterpret_cast<uint4*>(out + row * os + jg * 16);
-  o[0] = pack8(f);
-  o[1] = pack8(f + 8);
+}
+
+// Scale tiles per workgroup: the widest of 4, 2, 1 that still leaves >= 1024 workgroups.
+static int nvfp4_tiles_per_wg(int64_t M, int64_t K) {
+  for (int ct : {4, 2}) {
+    if (cdiv(K, 64 * ct) * cdiv(M, 128) >= 1024) return ct;
+  }
+  return 1;
 }
 
 }  // namespace oudjat
@@ -157,10 +218,15 @@ extern "C" int oudjat_nvfp4_quantize(const uint16_t* x, int64_t M, int64_t K, in
                  (long long)K);
   if (M == 0 || K == 0) return OUDJAT_OK;
   OUDJAT_REQUIRE(x && ts && qdata && scales, OUDJAT_ERR_INVALID_ARGUMENT, "nvfp4_quantize: null pointer");
-  OUDJAT_REQUIRE(sm % 8 == 0 && sm >= K && aligned(x, 16) && aligned(qdata, 8) && aligned(scales, 2),
+  OUDJAT_REQUIRE(sm % 8 == 0 && sm >= K && aligned(x, 16) && aligned(qdata, 8) && aligned(scales, 4),
                  OUDJAT_ERR_UNSUPPORTED_LAYOUT, "nvfp4_quantize: 16-byte aligned rows required");
-  dim3 grid((unsigned)cdiv(K, 64), (unsigned)cdiv(M, 128));
-  nvfp4_quantize_kernel<<<grid, 256, 0, as_stream(stream)>>>(x, M, K, sm, ts, qdata, scales);
+  OUDJAT_REQUIRE(cdiv(M, 128) < 65536, OUDJAT_ERR_TOO_LARGE, "nvfp4_quantize: M too large");
+  const int ct = nvfp4_tiles_per_wg(M, K);
+  dim3 grid((unsigned)cdiv(K, 64 * ct), (unsigned)cdiv(M, 128));
+  hipStream_t st = as_stream(stream);
+  if (ct == 4) nvfp4_quantize_kernel<4><<<grid, 256, 0, st>>>(x, M, K, sm, ts, qdata, scales);
+  else if (ct == 2) nvfp4_quantize_kernel<2><<<grid, 256, 0, st>>>(x, M, K, sm, ts, qdata, scales);
+  else nvfp4_quantize_kernel<1><<<grid, 256, 0, st>>>(x, M, K, sm, ts, qdata, scales);
   return check_launch("nvfp4_quantize");
 }
 
@@ -173,7 +239,12 @@ extern "C" int oudjat_nvfp4_dequantize(const uint8_t* qdata, const uint8_t* scal
   OUDJAT_REQUIRE(qdata && scales && ts && out, OUDJAT_ERR_INVALID_ARGUMENT, "nvfp4_dequantize: null pointer");
   OUDJAT_REQUIRE(os % 8 == 0 && os >= K && aligned(out, 16) && aligned(qdata, 8), OUDJAT_ERR_UNSUPPORTED_LAYOUT,
                  "nvfp4_dequantize: 16-byte aligned rows required");
-  const int64_t n = M * (K / 16);
-  nvfp4_dequantize_kernel<<<(unsigned)cdiv(n, 256), 256, 0, as_stream(stream)>>>(qdata, scales, ts, M, K, out, os);
+  OUDJAT_REQUIRE(cdiv(M, 128) < 65536, OUDJAT_ERR_TOO_LARGE, "nvfp4_dequantize: M too large");
+  const int ct = nvfp4_tiles_per_wg(M, K);
+  dim3 grid((unsigned)cdiv(K, 64 * ct), (unsigned)cdiv(M, 128));
+  hipStream_t st = as_stream(stream);
+  if (ct == 4) nvfp4_dequantize_kernel<4><<<grid, 256, 0, st>>>(qdata, scales, ts, M, K, out, os);
+  else if (ct == 2) nvfp4_dequantize_kernel<2><<<grid, 256, 0, st>>>(qdata, scales, ts, M, K, out, os);
+  else nvfp4_dequantize_kernel<1><<<grid, 256, 0, st>>>(qdata, scales, ts, M, K, out, os);
   return check_launch("nvfp4_dequantize");
 }

@@ -11,6 +11,13 @@
         scaled by what they read for a plain copy of known size in the same run (bench.py
         --calib-copy-mib: the library's row-copy kernel, 16-byte lanes like the GEMM operand loads).
         Prints a markdown summary and merges {key: {...}} into the JSON file that bench.py reads.
+
+    python -m appcorr_amd.profiling kernels <kernel_trace.csv> <fetch_counter_collection.csv>
+            <write_counter_collection.csv> <calibration kernel substring> <calibration bytes>
+            <kernel substrings, comma-separated> <title> <command>
+        Markdown table per (kernel, grid size): median duration from a `--kernel-trace` run and HBM
+        read / write bytes per dispatch from the two counter runs, scaled as in `traffic`. For the
+        standalone kernels of `python -m appcorr_amd.kernel_bench --calib-copy-mib 1024`.
 """
 
 from __future__ import annotations
@@ -104,11 +111,61 @@ def traffic(fetch_csv: str, write_csv: str, kernel: str, calib: str, calib_bytes
     return "\n".join(lines)
 
 
+def _groups(path: str, value_col: str):
+    """{(kernel name, grid threads): [values]} of a rocprofv3 CSV (per-dispatch rows)."""
+    acc = defaultdict(list)
+    for r in csv.DictReader(open(path)):
+        if "Grid_Size" in r:
+            thr = int(r["Grid_Size"])
+        else:
+            thr = int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        v = (float(r["End_Timestamp"]) - float(r["Start_Timestamp"])) if value_col == "duration" else \
+            float(r[value_col])
+        acc[(r["Kernel_Name"], thr)].append(v)
+    return acc
+
+
+def kernels(trace_csv: str, fetch_csv: str, write_csv: str, calib: str, calib_bytes: float, subs, title: str,
+            cmd: str) -> str:
+    """Per (kernel, grid) of every kernel whose name contains one of `subs`: dispatches, average
+    duration (kernel trace) and HBM bytes per dispatch (FETCH_SIZE / WRITE_SIZE runs, scaled by what
+    the same counters read for the calibration copy, as in `traffic`)."""
+    dur = _groups(trace_csv, "duration")
+    f = _groups(fetch_csv, "Counter_Value")
+    w = _groups(write_csv, "Counter_Value")
+    cf = max(v for (n, _), vals in f.items() if calib in n for v in vals)
+    cw = max(v for (n, _), vals in w.items() if calib in n for v in vals)
+    f_scale = calib_bytes * (1.0 + 16.0 / 4096.0) / (cf * 1024.0)
+    w_scale = calib_bytes / (cw * 1024.0)
+    lines = [f"# {title}", "", "Commands (run from the repository root on one MI355X):", "", "```", cmd, "```", "",
+             f"Scale factors from the calibration copy (`{calib}`, {calib_bytes / 2**20:.0f} MiB of 4 KiB rows, "
+             f"the largest dispatch of that kernel in each run): FETCH_SIZE x {f_scale:.4f}, WRITE_SIZE x "
+             f"{w_scale:.4f}.", "",
+             "| kernel | grid threads | dispatches | avg us (trace) | HBM read MB | HBM write MB | HBM GB/s |",
+             "|---|---:|---:|---:|---:|---:|---:|"]
+    for key in sorted(dur, key=lambda k: (_short(k[0]), k[1])):
+        name, thr = key
+        if not any(sub in name for sub in subs) or key not in f or key not in w:
+            continue
+        d = sorted(dur[key])
+        # the calibration copy is not a timed launch of its kernel: leave out the largest dispatch
+        if calib in name and len(d) > 1:
+            d = d[:-1]
+        us = d[len(d) // 2] / 1e3
+        fb = sum(f[key]) / len(f[key]) * 1024.0 * f_scale
+        wb = sum(w[key]) / len(w[key]) * 1024.0 * w_scale
+        lines.append(f"| `{_short(name)}` | {thr} | {len(d)} | {us:.2f} | {fb / 1e6:.2f} | {wb / 1e6:.2f} | "
+                     f"{(fb + wb) / (us * 1e3):.0f} |")
+    return "\n".join(lines)
+
+
 def main(argv):
     if len(argv) >= 5 and argv[0] == "kernel-stats":
         print(kernel_stats(argv[1], int(argv[2]), argv[3], argv[4]))
     elif len(argv) >= 9 and argv[0] == "traffic":
         print(traffic(argv[1], argv[2], argv[3], argv[4], float(argv[5]), argv[6], argv[7], argv[8]))
+    elif len(argv) >= 9 and argv[0] == "kernels":
+        print(kernels(argv[1], argv[2], argv[3], argv[4], float(argv[5]), argv[6].split(","), argv[7], argv[8]))
     else:
         print(__doc__)
         return 2

@@ -233,14 +233,16 @@ int oudjat_linear_kernel_name(int64_t M, int64_t N, int64_t K, int epi, char* bu
  * *tensor_scale (device) -> qdata [M, K/2] (two e2m1 codes per byte, even element in the low
  * nibble) and e4m3 block scales in the swizzled layout of 32x16 bytes per 128x64 tile
  * (ceil(M/128) * ceil(K/64) * 512 bytes; padding scales are 0).
- * Replaces quantize_nvfp4_swizzled (appcorr/models/dinov3/layers/triton_kernels/nvfp4_fused.py:119-145). K % 16 == 0. */
+ * Replaces quantize_nvfp4_swizzled (appcorr/models/dinov3/layers/triton_kernels/nvfp4_fused.py:119-145). K % 16 == 0;
+ * x 16-byte aligned with stride_m % 8 == 0, qdata 8-byte and scales 4-byte aligned. */
 int oudjat_nvfp4_quantize(const uint16_t* x, int64_t M, int64_t K, int64_t stride_m,
                           const float* tensor_scale, uint8_t* qdata, uint8_t* scales,
                           oudjat_stream_t stream);
 
 /* Row 18 -- NVFP4 dequantize: out[m, k] = bf16(fp32(e2m1(q) * e4m3(s)) * tensor_scale).
  * Inverse of oudjat_nvfp4_quantize; the dequant side of FastFP4Linear
- * (offload/server/model/fp4_fast_linear.py:221-283). */
+ * (offload/server/model/fp4_fast_linear.py:221-283). K % 16 == 0; qdata 8-byte aligned, out
+ * 16-byte aligned with out_stride % 8 == 0. */
 int oudjat_nvfp4_dequantize(const uint8_t* qdata, const uint8_t* scales, const float* tensor_scale,
                             int64_t M, int64_t K, uint16_t* out, int64_t out_stride,
                             oudjat_stream_t stream);

@@ -66,3 +66,41 @@ def test_strided_rows(dev):
     rq, rs = Q.quantize(xf, ts)
     assert_bits_equal(qd, rq, "qdata strided")
     assert_bits_equal(sc.view(torch.uint8), rs, "scales strided")
+
+
+def test_signed_zeros_tiny_values_and_rounding_boundaries(dev):
+    """-0.0 must encode as 0x8 (x / tot keeps the sign of x), tiny values as signed zero codes, and
+    quotients that land exactly on or one ulp around an e2m1 rounding boundary (0.25, 0.75, 1.25,
+    1.75, 2.5, 3.5, 5.0) must round as IEEE division does. Each 16-element block holds its maximum
+    6 * tot at element 0, so the block's divisor is known, and boundary quotients are built by
+    scaling that divisor."""
+    M, K_ = 128, 256
+    rng = np.random.default_rng(11)
+    xf = rng.standard_normal((M, K_)).astype(np.float32)
+    xb = f32_to_bf16_bits(xf)
+    xf = bf16_bits_to_f32(xb)
+    blocks = xf.reshape(M, K_ // 16, 16)
+    blocks[:, :, 1] = -0.0
+    blocks[:, :, 2] = 0.0
+    blocks[:, ::3, 3] = -1e-30
+    bounds = np.array([0.25, 0.75, 1.25, 1.75, 2.5, 3.5, 5.0], np.float32)
+    amax = np.abs(blocks).max(axis=2, keepdims=True)
+    for e in range(4, 16):
+        t = bounds[(e - 4) % 7] * (1.0 if e % 2 else -1.0)
+        # a multiple of the block maximum, nudged by -1/0/+1 bf16 ulp; its quotient by the block's
+        # divisor lands on or next to the boundary t (exactly on it when the scale is exact)
+        v = bf16_bits_to_f32(f32_to_bf16_bits((amax[..., 0] * np.float32(t / 6.0)).astype(np.float32)))
+        vb = f32_to_bf16_bits(v).astype(np.int32) + ((e % 3) - 1)
+        blocks[:, :, e] = bf16_bits_to_f32(vb.astype(np.uint16))
+    xb = f32_to_bf16_bits(blocks.reshape(M, K_))  # -1e-30 rounds to a bf16 value; the rest is bf16 already
+    xf = bf16_bits_to_f32(xb)
+    assert (np.signbit(xf.reshape(M, K_ // 16, 16)[:, :, 1]) & (xf.reshape(M, K_ // 16, 16)[:, :, 1] == 0)).all()
+    ts = Q.per_tensor_amax_to_scale(np.abs(xf).max())
+    x = bits_to_torch_bf16(xb).to(dev)
+    tsd = torch.tensor([ts], dtype=torch.float32, device=dev)
+    qd, sc = K.quantize_nvfp4_swizzled(x, tsd)
+    rq, rs = Q.quantize(xf, ts)
+    assert_bits_equal(qd, rq, "qdata signed zeros / boundaries")
+    assert_bits_equal(sc.view(torch.uint8), rs, "scales signed zeros / boundaries")
+    codes = np.stack([rq & 15, rq >> 4], axis=-1).reshape(M, K_)
+    assert (codes.reshape(M, K_ // 16, 16)[:, :, 1] == 8).all()  # -0.0 -> 0x8 in the oracle too
