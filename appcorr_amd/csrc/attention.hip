@@ -64,6 +64,15 @@ __device__ __forceinline__ float xor32_sum(float x) {
   const auto r = __builtin_amdgcn_permlane32_swap(__float_as_uint(x), __float_as_uint(x), false, false);
   return __uint_as_float(r[0]) + __uint_as_float(r[1]);
 }
+// The same with lane l ^ 16 through v_permlane16_swap (rows of 16 lanes swapped pairwise).
+__device__ __forceinline__ float xor16_max(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return fmaxf(__uint_as_float(r[0]), __uint_as_float(r[1]));
+}
+__device__ __forceinline__ float xor16_sum(float x) {
+  const auto r = __builtin_amdgcn_permlane16_swap(__float_as_uint(x), __float_as_uint(x), false, false);
+  return __uint_as_float(r[0]) + __uint_as_float(r[1]);
+}
 
 __device__ __forceinline__ float prob_row_sum(const bf16x8_t (&pf)[4]) {
   typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
@@ -352,23 +361,6 @@ __global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
   const int q0 = (blockIdx.x * waves_per_wg + wave) * 32;
   const bool active = q0 < T;
 
-  bf16x8_t qf[QK_STEPS];
-  {
-    const int qr = q0 + l32;
-#pragma unroll
-    for (int ks = 0; ks < QK_STEPS; ++ks) {
-      uint4 v = make_uint4(0, 0, 0, 0);
-      if (qr < T) v = *reinterpret_cast<const uint4*>(q + ((int64_t)b * T + qr) * qrs + (int64_t)h * DH + ks * 16 + 8 * g);
-      qf[ks] = as_bf16x8(v);
-    }
-  }
-  f32x16_t o[OB];
-#pragma unroll
-  for (int d = 0; d < OB; ++d)
-#pragma unroll
-    for (int v = 0; v < 16; ++v) o[d][v] = 0.0f;
-  float m_i = -INFINITY, l_i = 0.0f;
-
   const uint16_t* kbase = kv + (int64_t)b * kvb + (int64_t)h * kvh;
   const uint32_t bytes = (uint32_t)((int64_t)N * kvn * 2);
   const i32x4_t rsrc_k = make_buffer_rsrc(kbase, bytes);
@@ -394,152 +386,304 @@ __global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
     else wait_vmcnt<6>();
   };
 
-  // Per-lane LDS offsets, fixed for the whole loop: the swizzle of a key row is the same for key and
-  // key + 16 j (and key + 32 kb), so the k-step / key block / stage parts of every fragment address
-  // are compile-time offsets.
-  int koff[QK_STEPS];
-#pragma unroll
-  for (int kstep = 0; kstep < QK_STEPS; ++kstep) koff[kstep] = kv_slot(l32, kstep * 2 + g);
-  int voff[OB][2];
-  {
-    const int sl = lane & 15, hh = (lane >> 4) & 1;
-#pragma unroll
-    for (int db = 0; db < OB; ++db) {
-      const int dcol = 32 * db + 16 * hh + 4 * (sl & 3);  // first of the 4 dims this lane addresses
-      const int k1 = 4 * g + (sl >> 2);                   // key of k-step 0 (first run)
-      voff[db][0] = TILEB + kv_slot(k1, dcol >> 3) + ((dcol >> 2) & 1) * 8;
-      voff[db][1] = TILEB + kv_slot(k1 + 8, dcol >> 3) + ((dcol >> 2) & 1) * 8;
-    }
-  }
-
-  // S^T of one tile: s[kb][v] = S^T[key kb*32 + 8(v/4) + 4g + v%4][query l32].
-  struct Scores {
-    f32x16_t s[2];
-  };
-  auto scores = [&](Scores& sc, const unsigned char* st) __attribute__((always_inline)) {
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb) {
-      bf16x8_t kf[QK_STEPS];
-#pragma unroll
-      for (int kstep = 0; kstep < QK_STEPS; ++kstep)
-        kf[kstep] = as_bf16x8(*reinterpret_cast<const uint4*>(st + koff[kstep] + kb * 32 * 128));
-      const f32x16_t zero = {};
-      sc.s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0], zero, 0, 0, 0);
-#pragma unroll
-      for (int kstep = 1; kstep < QK_STEPS; ++kstep)
-        sc.s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kstep], qf[kstep], sc.s[kb], 0, 0, 0);
-    }
-  };
-  // Online softmax of tile t and O^T += V^T . P^T with V from stage `st`.
-  auto finish = [&](Scores& sc, const unsigned char* st, int t) __attribute__((always_inline)) {
-    f32x16_t (&s)[2] = sc.s;
-    if ((t + 1) * kKeyTile > N) {
-#pragma unroll
-      for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-        for (int v = 0; v < 16; ++v)
-          if (t * kKeyTile + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3) >= N) s[kb][v] = -INFINITY;
-    }
-    float mq[4];  // four short chains, combined as a tree
-#pragma unroll
-    for (int q4 = 0; q4 < 4; ++q4) {
-      mq[q4] = s[q4 >> 1][8 * (q4 & 1)];
-#pragma unroll
-      for (int v = 1; v < 8; ++v) mq[q4] = fmaxf(mq[q4], s[q4 >> 1][8 * (q4 & 1) + v]);
-    }
-    const float mx = xor32_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
-    const float m_new = softmax_ref_max(m_i, mx, scale_log2);
-    const float alpha = __builtin_amdgcn_exp2f((m_i - m_new) * scale_log2);
-    const float mc = m_new * scale_log2;
-#pragma unroll
-    for (int kb = 0; kb < 2; ++kb)
-#pragma unroll
-      for (int v = 0; v < 16; ++v) s[kb][v] = __builtin_amdgcn_exp2f(fmaf(s[kb][v], scale_log2, -mc));
-    bf16x8_t pf[4];
-#pragma unroll
-    for (int j = 0; j < 4; ++j) {
-      float tmp[8];
-#pragma unroll
-      for (int e = 0; e < 8; ++e) tmp[e] = s[j >> 1][8 * (j & 1) + e];
-      pf[j] = pack_bf16x8(tmp);
-    }
-    const float rs = prob_row_sum(pf);
-    l_i = l_i * alpha + rs;
-    m_i = m_new;
-    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
-#pragma unroll
-      for (int d = 0; d < OB; ++d)
-#pragma unroll
-        for (int v = 0; v < 16; ++v) o[d][v] *= alpha;
-    }
-    // V^T fragment of d-block db, k-step j: elements 0..3 = keys 16j + 4g + {0..3}, elements 4..7 =
-    // keys 16j + 8 + 4g + {0..3}, at dim 32 db + l32 (the P^T order above).
-#pragma unroll
-    for (int db = 0; db < OB; ++db) {
-#pragma unroll
-      for (int j = 0; j < 4; ++j) {
-        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4_t*)(st + voff[db][0] + j * 16 * 128));
-        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-            (__attribute__((address_space(3))) i16x4_t*)(st + voff[db][1] + j * 16 * 128));
-        typedef short i16x8_t __attribute__((ext_vector_type(8)));
-        const i16x8_t both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
-        o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, both), pf[j], o[db], 0, 0, 0);
-      }
-    }
-  };
-
-  // Iteration t: wait for tile t + 1 (tiles issued so far: 0 .. t + NST - 2), barrier (tile t + 1
-  // visible to every wave; every wave done with tile t - 1's stage), refill that stage with tile
-  // t + NST - 1, issue the S^T MFMAs of tile t + 1, then tile t's softmax (VALU, overlapping those
-  // MFMAs) and its O^T MFMAs. Unrolled by NST so every stage base is a constant.
-  static_assert(NST == 4, "the unrolled loop below is written for four stages");
+  // The prologue of the K/V pipeline is common to both wave kinds below.
+  static_assert(NST == 4, "the unrolled loops below are written for four stages");
 #pragma unroll
   for (int st = 0; st < NST - 1; ++st)
     if (st < ntiles) issue(st, st);
   wait_tiles(min(NST - 2, ntiles - 1));
   block_barrier();
-  Scores sa, sb;
-  if (active) scores(sa, smem);
-  auto step = [&](auto stage_c, int t, Scores& cur, Scores& nxt) __attribute__((always_inline)) {
-    constexpr int SG = decltype(stage_c)::value;  // stage of tile t
-    if (t + 1 < ntiles) {
-      wait_tiles(min(NST - 3, ntiles - 2 - t));
-      block_barrier();
-      if (t + NST - 1 < ntiles) issue((SG + NST - 1) % NST, t + NST - 1);
-      if (active) scores(nxt, smem + ((SG + 1) % NST) * STAGE);
-    }
-    if (active) finish(cur, smem + SG * STAGE, t);
-  };
+
+  // Iteration t of either loop: wait for tile t + 1 (tiles issued so far: 0 .. t + NST - 2),
+  // barrier (tile t + 1 visible to every wave; every wave done with tile t - 1's stage), refill that
+  // stage with tile t + NST - 1, issue the S^T MFMAs of tile t + 1, then tile t's softmax (VALU,
+  // overlapping those MFMAs) and its O^T MFMAs. Unrolled by NST so every stage base is a constant.
+  // Both loops pass the same barriers in the same order.
   using I0 = std::integral_constant<int, 0>;
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
-  int t = 0;
-  for (; t + NST <= ntiles; t += NST) {
-    step(I0{}, t, sa, sb);
-    step(I1{}, t + 1, sb, sa);
-    step(I2{}, t + 2, sa, sb);
-    step(I3{}, t + 3, sb, sa);
-  }
-  if (t < ntiles) step(I0{}, t, sa, sb);
-  if (t + 1 < ntiles) step(I1{}, t + 1, sb, sa);
-  if (t + 2 < ntiles) step(I2{}, t + 2, sa, sb);
+  auto pipeline = [&](auto& sa, auto& sb, auto&& scores, auto&& finish) __attribute__((always_inline)) {
+    if (active) scores(sa, smem);
+    auto step = [&](auto stage_c, int t, auto& cur, auto& nxt) __attribute__((always_inline)) {
+      constexpr int SG = decltype(stage_c)::value;  // stage of tile t
+      if (t + 1 < ntiles) {
+        wait_tiles(min(NST - 3, ntiles - 2 - t));
+        block_barrier();
+        if (t + NST - 1 < ntiles) issue((SG + NST - 1) % NST, t + NST - 1);
+        if (active) scores(nxt, smem + ((SG + 1) % NST) * STAGE);
+      }
+      if (active) finish(cur, smem + SG * STAGE, t);
+    };
+    int t = 0;
+    for (; t + NST <= ntiles; t += NST) {
+      step(I0{}, t, sa, sb);
+      step(I1{}, t + 1, sb, sa);
+      step(I2{}, t + 2, sa, sb);
+      step(I3{}, t + 3, sb, sa);
+    }
+    if (t < ntiles) step(I0{}, t, sa, sb);
+    if (t + 1 < ntiles) step(I1{}, t + 1, sb, sa);
+    if (t + 2 < ntiles) step(I2{}, t + 2, sa, sb);
+  };
 
-  const int qr = q0 + l32;
-  if (active && qr < T) {
-    const float inv = 1.0f / l_i;
-    uint16_t* orow = out + ((int64_t)b * T + qr) * ors + (int64_t)h * DH;
+  if (T - q0 > 16) {
+    // ---- Full wave: 32 queries on v_mfma_f32_32x32x16_bf16 (layout in the file comment). ----
+    bf16x8_t qf[QK_STEPS];
+    {
+      const int qr = q0 + l32;
+#pragma unroll
+      for (int ks = 0; ks < QK_STEPS; ++ks) {
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (qr < T) v = *reinterpret_cast<const uint4*>(q + ((int64_t)b * T + qr) * qrs + (int64_t)h * DH + ks * 16 + 8 * g);
+        qf[ks] = as_bf16x8(v);
+      }
+    }
+    f32x16_t o[OB];
 #pragma unroll
     for (int d = 0; d < OB; ++d)
 #pragma unroll
-      for (int r4 = 0; r4 < 4; ++r4) {
+      for (int v = 0; v < 16; ++v) o[d][v] = 0.0f;
+    float m_i = -INFINITY, l_i = 0.0f;
+
+    // Per-lane LDS offsets, fixed for the whole loop: the swizzle of a key row is the same for key
+    // and key + 16 j (and key + 32 kb), so the k-step / key block / stage parts of every fragment
+    // address are compile-time offsets.
+    int koff[QK_STEPS];
+#pragma unroll
+    for (int kstep = 0; kstep < QK_STEPS; ++kstep) koff[kstep] = kv_slot(l32, kstep * 2 + g);
+    int voff[OB][2];
+    {
+      const int sl = lane & 15, hh = (lane >> 4) & 1;
+#pragma unroll
+      for (int db = 0; db < OB; ++db) {
+        const int dcol = 32 * db + 16 * hh + 4 * (sl & 3);  // first of the 4 dims this lane addresses
+        const int k1 = 4 * g + (sl >> 2);                   // key of k-step 0 (first run)
+        voff[db][0] = TILEB + kv_slot(k1, dcol >> 3) + ((dcol >> 2) & 1) * 8;
+        voff[db][1] = TILEB + kv_slot(k1 + 8, dcol >> 3) + ((dcol >> 2) & 1) * 8;
+      }
+    }
+
+    // S^T of one tile: s[kb][v] = S^T[key kb*32 + 8(v/4) + 4g + v%4][query l32].
+    struct Scores {
+      f32x16_t s[2];
+    };
+    auto scores = [&](Scores& sc, const unsigned char* st) __attribute__((always_inline)) {
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb) {
+        bf16x8_t kf[QK_STEPS];
+#pragma unroll
+        for (int kstep = 0; kstep < QK_STEPS; ++kstep)
+          kf[kstep] = as_bf16x8(*reinterpret_cast<const uint4*>(st + koff[kstep] + kb * 32 * 128));
+        const f32x16_t zero = {};
+        sc.s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0], zero, 0, 0, 0);
+#pragma unroll
+        for (int kstep = 1; kstep < QK_STEPS; ++kstep)
+          sc.s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[kstep], qf[kstep], sc.s[kb], 0, 0, 0);
+      }
+    };
+    // Online softmax of tile t and O^T += V^T . P^T with V from stage `st`.
+    auto finish = [&](Scores& sc, const unsigned char* st, int t) __attribute__((always_inline)) {
+      f32x16_t (&s)[2] = sc.s;
+      if ((t + 1) * kKeyTile > N) {
+#pragma unroll
+        for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+          for (int v = 0; v < 16; ++v)
+            if (t * kKeyTile + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3) >= N) s[kb][v] = -INFINITY;
+      }
+      float mq[4];  // four short chains, combined as a tree
+#pragma unroll
+      for (int q4 = 0; q4 < 4; ++q4) {
+        mq[q4] = s[q4 >> 1][8 * (q4 & 1)];
+#pragma unroll
+        for (int v = 1; v < 8; ++v) mq[q4] = fmaxf(mq[q4], s[q4 >> 1][8 * (q4 & 1) + v]);
+      }
+      const float mx = xor32_max(fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3])));
+      const float m_new = softmax_ref_max(m_i, mx, scale_log2);
+      const float alpha = __builtin_amdgcn_exp2f((m_i - m_new) * scale_log2);
+      const float mc = m_new * scale_log2;
+#pragma unroll
+      for (int kb = 0; kb < 2; ++kb)
+#pragma unroll
+        for (int v = 0; v < 16; ++v) s[kb][v] = __builtin_amdgcn_exp2f(fmaf(s[kb][v], scale_log2, -mc));
+      bf16x8_t pf[4];
+#pragma unroll
+      for (int j = 0; j < 4; ++j) {
+        float tmp[8];
+#pragma unroll
+        for (int e = 0; e < 8; ++e) tmp[e] = s[j >> 1][8 * (j & 1) + e];
+        pf[j] = pack_bf16x8(tmp);
+      }
+      const float rs = prob_row_sum(pf);
+      l_i = l_i * alpha + rs;
+      m_i = m_new;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+        for (int d = 0; d < OB; ++d)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) o[d][v] *= alpha;
+      }
+      // V^T fragment of d-block db, k-step j: elements 0..3 = keys 16j + 4g + {0..3}, elements 4..7 =
+      // keys 16j + 8 + 4g + {0..3}, at dim 32 db + l32 (the P^T order above).
+#pragma unroll
+      for (int db = 0; db < OB; ++db) {
+#pragma unroll
+        for (int j = 0; j < 4; ++j) {
+          const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4_t*)(st + voff[db][0] + j * 16 * 128));
+          const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4_t*)(st + voff[db][1] + j * 16 * 128));
+          typedef short i16x8_t __attribute__((ext_vector_type(8)));
+          const i16x8_t both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, both), pf[j], o[db], 0, 0, 0);
+        }
+      }
+    };
+    Scores sa, sb;
+    pipeline(sa, sb, scores, finish);
+
+    const int qr = q0 + l32;
+    if (active && qr < T) {
+      const float inv = 1.0f / l_i;
+      uint16_t* orow = out + ((int64_t)b * T + qr) * ors + (int64_t)h * DH;
+#pragma unroll
+      for (int d = 0; d < OB; ++d)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4) {
+          typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+          bf16x4_t w;
+#pragma unroll
+          for (int e = 0; e < 4; ++e) w[e] = (__bf16)(o[d][4 * r4 + e] * inv);
+          *reinterpret_cast<bf16x4_t*>(orow + d * 32 + 8 * r4 + 4 * g) = w;
+        }
+    }
+  } else {
+    // ---- Light wave (<= 16 queries left, e.g. the 5 of T = 261 after 8 full waves): 16 queries on
+    // v_mfma_f32_16x16x32_bf16, half the MFMA and softmax work of a full wave. With 9 waves on 4
+    // SIMDs one SIMD carries three waves; this one is the third.
+    // Layout: lane l, 16-lane group G = l / 16. S^T = K . Q^T per 16-key block kb (A = K rows
+    // 16 kb + l % 16, dims 32 ks + 8 G; B = Q^T, query l % 16): s16[kb][v] = S^T[key 16 kb + 4 G + v]
+    // [query l % 16], so a query's 64 keys lie in the four groups (max / sum over xor 16, xor 32).
+    // O^T = V^T . P^T per 16-dim block db and 32-key k-step j: group G supplies keys 32 j + 4 G +
+    // {0..3} and 32 j + 16 + 4 G + {0..3} (P from s16[2j], s16[2j + 1]), and V^T is read in the same
+    // order with the LDS transpose read (in each 16-lane group, lane i receives dim 16 db + i of 4
+    // consecutive keys).
+    const int l16 = lane & 15, G = lane >> 4;
+    bf16x8_t qf[2];
+    {
+      const int qr = q0 + l16;
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) {
+        uint4 v = make_uint4(0, 0, 0, 0);
+        if (qr < T) v = *reinterpret_cast<const uint4*>(q + ((int64_t)b * T + qr) * qrs + (int64_t)h * DH + ks * 32 + 8 * G);
+        qf[ks] = as_bf16x8(v);
+      }
+    }
+    f32x4_t o[4];
+#pragma unroll
+    for (int d = 0; d < 4; ++d) o[d] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
+    float m_i = -INFINITY, l_i = 0.0f;
+    int koff[2];
+#pragma unroll
+    for (int ks = 0; ks < 2; ++ks) koff[ks] = kv_slot(l16, 4 * ks + G);
+    int voff[4][2];
+#pragma unroll
+    for (int db = 0; db < 4; ++db) {
+      const int dcol = 16 * db + 4 * (l16 & 3);  // first of the 4 dims this lane addresses
+      const int k1 = 4 * G + (l16 >> 2);         // key of k-step 0 (first run)
+      voff[db][0] = TILEB + kv_slot(k1, dcol >> 3) + ((dcol >> 2) & 1) * 8;
+      voff[db][1] = TILEB + kv_slot(k1 + 16, dcol >> 3) + ((dcol >> 2) & 1) * 8;
+    }
+    struct Scores16 {
+      f32x4_t s[4];
+    };
+    auto scores = [&](Scores16& sc, const unsigned char* st) __attribute__((always_inline)) {
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) {
+        const bf16x8_t k0 = as_bf16x8(*reinterpret_cast<const uint4*>(st + koff[0] + kb * 16 * 128));
+        const bf16x8_t k1 = as_bf16x8(*reinterpret_cast<const uint4*>(st + koff[1] + kb * 16 * 128));
+        const f32x4_t zero = {};
+        sc.s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qf[0], zero, 0, 0, 0);
+        sc.s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qf[1], sc.s[kb], 0, 0, 0);
+      }
+    };
+    auto finish = [&](Scores16& sc, const unsigned char* st, int t) __attribute__((always_inline)) {
+      f32x4_t (&s)[4] = sc.s;
+      if ((t + 1) * kKeyTile > N) {
+#pragma unroll
+        for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (t * kKeyTile + 16 * kb + 4 * G + v >= N) s[kb][v] = -INFINITY;
+      }
+      float mq[4];
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb) mq[kb] = fmaxf(fmaxf(s[kb][0], s[kb][1]), fmaxf(s[kb][2], s[kb][3]));
+      float mx = fmaxf(fmaxf(mq[0], mq[1]), fmaxf(mq[2], mq[3]));
+      mx = xor32_max(xor16_max(mx));
+      const float m_new = softmax_ref_max(m_i, mx, scale_log2);
+      const float alpha = __builtin_amdgcn_exp2f((m_i - m_new) * scale_log2);
+      const float mc = m_new * scale_log2;
+#pragma unroll
+      for (int kb = 0; kb < 4; ++kb)
+#pragma unroll
+        for (int v = 0; v < 4; ++v) s[kb][v] = __builtin_amdgcn_exp2f(fmaf(s[kb][v], scale_log2, -mc));
+      bf16x8_t pf[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        const float tmp[8] = {s[2 * j][0], s[2 * j][1], s[2 * j][2], s[2 * j][3],
+                              s[2 * j + 1][0], s[2 * j + 1][1], s[2 * j + 1][2], s[2 * j + 1][3]};
+        pf[j] = pack_bf16x8(tmp);
+      }
+      typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+      const bf16x2v_t ones = {(__bf16)1.0f, (__bf16)1.0f};
+      float r[2];
+#pragma unroll
+      for (int j = 0; j < 2; ++j) {
+        r[j] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf[j], pf[j], 0, 1), ones, 0.0f, false);
+        r[j] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf[j], pf[j], 2, 3), ones, r[j], false);
+        r[j] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf[j], pf[j], 4, 5), ones, r[j], false);
+        r[j] = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pf[j], pf[j], 6, 7), ones, r[j], false);
+      }
+      const float rs = xor32_sum(xor16_sum(r[0] + r[1]));
+      l_i = l_i * alpha + rs;
+      m_i = m_new;
+      if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+        for (int d = 0; d < 4; ++d) o[d] *= alpha;
+      }
+#pragma unroll
+      for (int db = 0; db < 4; ++db) {
+#pragma unroll
+        for (int j = 0; j < 2; ++j) {
+          const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4_t*)(st + voff[db][0] + j * 32 * 128));
+          const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4_t*)(st + voff[db][1] + j * 32 * 128));
+          typedef short i16x8_t __attribute__((ext_vector_type(8)));
+          const i16x8_t both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+          o[db] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(__builtin_bit_cast(bf16x8_t, both), pf[j], o[db], 0, 0, 0);
+        }
+      }
+    };
+    Scores16 sa, sb;
+    pipeline(sa, sb, scores, finish);
+
+    // O^T[16 db + 4 G + v][query l16]: 4 consecutive dims per lane and block.
+    const int qr = q0 + l16;
+    if (active && qr < T) {
+      const float inv = 1.0f / l_i;
+      uint16_t* orow = out + ((int64_t)b * T + qr) * ors + (int64_t)h * DH;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) {
         typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
         bf16x4_t w;
 #pragma unroll
-        for (int e = 0; e < 4; ++e) w[e] = (__bf16)(o[d][4 * r4 + e] * inv);
-        *reinterpret_cast<bf16x4_t*>(orow + d * 32 + 8 * r4 + 4 * g) = w;
+        for (int e = 0; e < 4; ++e) w[e] = (__bf16)(o[d][e] * inv);
+        *reinterpret_cast<bf16x4_t*>(orow + 16 * d + 4 * G) = w;
       }
+    }
   }
 }
 
