@@ -1398,6 +1398,7 @@ static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_R16_CFG(288, 192, 2, 4, 1, 64, 2, false),  // 26: 288 x 192 (N = 3 C: 240 tiles)
     OUDJAT_GEMM_PP_CFG(288, 256),  // 27: ping-pong 288 x 256
     OUDJAT_GEMM_PP_CFG(288, 192),  // 28: ping-pong 288 x 192
+    OUDJAT_GEMM_R16_CFG(144, 128, 1, 4, 2, 128, 2, false),  // 29: N = C GEMMs with K % 128 == 0
 };
 static constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -1445,9 +1446,9 @@ static int env_int(const char* name, int dflt) {
 // vector epilogues need; otherwise the register-staged kernel with 2-byte stores runs.
 static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   static const int forced = env_int("OUDJAT_GEMM_CFG", -1);
-  (void)K;
   if (!aligned_io) return 8;
-  if (forced >= 0 && forced < kNumCfgs && N % kCfgs[forced].bn == 0) return forced;
+  if (forced >= 0 && forced < kNumCfgs && N % kCfgs[forced].bn == 0 && (kCfgs[forced].pf > -2 || K % kCfgs[forced].bk == 0))
+    return forced;
   // 256 x 256 pipelined tiles when their grid fills between half and all of the CUs in one round;
   // 128 x 128 direct-to-LDS tiles otherwise (two workgroups per CU balance a ragged second round
   // better); the register-staged kernel for N % 128 != 0.
@@ -1463,7 +1464,9 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   // 144-row tiles (one round of 128..256 workgroups) when 256 x 256 tiles do not fit one round.
   const int64_t tm144 = cdiv(M, 144);
   if (N % 512 == 0 && tm144 * (N / 512) >= 128 && tm144 * (N / 512) <= 256) return 22;
-  if (tm144 * (N / 128) >= 128 && tm144 * (N / 128) <= 256) return 23;
+  // 128-deep K tiles (half the barriers and load batches of the 64-deep ones; the two K groups still
+  // take alternate 32-deep steps, so the result is the same bit for bit) when K allows.
+  if (tm144 * (N / 128) >= 128 && tm144 * (N / 128) <= 256) return K % 128 == 0 ? 29 : 23;
   return 11;
 }
 
