@@ -16,9 +16,10 @@
 // V is transposed once per tile while it is written to LDS (Vt[d][key], rows padded by 8 bytes so
 // the 8-byte fragment reads of 32 consecutive d rows are conflict-free).
 //
-// One workgroup per (image, head) covers up to 10 waves = 320 queries (8 waves for Dh = 128) (T = 261 at the headline
-// shape: 9 waves, 256 workgroups for B*H = 256, one per CU); larger T is split evenly over several
-// workgroups. K/V tiles of 64 keys are double-buffered in LDS with the next tile's global loads in
+// One workgroup per (image, head) covers up to 10 query waves = 320 queries (8 for Dh = 128); larger T
+// is split evenly over several workgroups. At the headline shape (T = 261: 8 full waves and a last
+// wave of 5 queries, 256 workgroups for B*H = 256, one per CU) the buffer-load kernel shares the
+// last wave's key tiles among 4 waves, so each workgroup runs 12. K/V tiles of 64 keys are double-buffered in LDS with the next tile's global loads in
 // flight during the current tile's MFMAs, so each (image, head) streams its K/V once.
 #include <stdlib.h>
 
@@ -32,6 +33,8 @@ namespace oudjat {
 
 static constexpr int kKeyTile = 64;
 static constexpr int kMaxWaves64 = 10;   // Dh = 64: 3 waves per SIMD, <= 170 VGPRs
+static constexpr int kLightParts = 4;     // waves that share a light (<= 16-query) last wave, one per SIMD
+static constexpr int kDmaMaxWaves = 12;   // buffer-load kernel: up to 8 full waves + kLightParts
 static constexpr int kMaxWaves128 = 8;   // Dh = 128: 2 waves per SIMD, <= 256 VGPRs
 static constexpr int kMinWaves = 4;
 
@@ -341,11 +344,14 @@ __device__ __forceinline__ int kv_swz(int row) {
 }
 __device__ __forceinline__ int kv_slot(int row, int chunk) { return row * 128 + ((chunk ^ kv_swz(row)) << 4); }
 
+// light_split: 0, or kLightParts when the launch has one workgroup per (image, head) whose last
+// query wave is light; that wave's work is then done by kLightParts waves (the last ones), part p
+// taking the key tiles t with t % NST == p, and merged at the end (see the light path below).
 template <int NST>
-__global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
+__global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     const uint16_t* __restrict__ q, int64_t qrs, int T, const uint16_t* __restrict__ kv, int64_t kvb, int64_t kvn,
     int64_t kvkv, int64_t kvh, int N, float scale_log2, uint16_t* __restrict__ out, int64_t ors,
-    int waves_per_wg) {
+    int waves_per_wg, int light_split) {
   constexpr int DH = 64, QK_STEPS = 4, OB = 2;
   constexpr int TILEB = kKeyTile * 128;  // one K (or V) tile: 64 rows of 128 bytes
   constexpr int STAGE = 2 * TILEB;
@@ -358,7 +364,9 @@ __global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, g = lane >> 5;
-  const int q0 = (blockIdx.x * waves_per_wg + wave) * 32;
+  // Query wave of this wave, and its part of a split light wave (-1: not split).
+  const int lpart = (light_split && wave >= waves_per_wg - 1) ? wave - (waves_per_wg - 1) : -1;
+  const int q0 = (blockIdx.x * waves_per_wg + (lpart >= 0 ? waves_per_wg - 1 : wave)) * 32;
   const bool active = q0 < T;
 
   const uint16_t* kbase = kv + (int64_t)b * kvb + (int64_t)h * kvh;
@@ -403,17 +411,19 @@ __global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
   using I1 = std::integral_constant<int, 1>;
   using I2 = std::integral_constant<int, 2>;
   using I3 = std::integral_constant<int, 3>;
-  auto pipeline = [&](auto& sa, auto& sb, auto&& scores, auto&& finish) __attribute__((always_inline)) {
-    if (active) scores(sa, smem);
+  // `stages`: bit s set when this wave computes the tiles held in stage s (all of them, except for
+  // the parts of a split light wave).
+  auto pipeline = [&](auto& sa, auto& sb, auto&& scores, auto&& finish, auto stages) __attribute__((always_inline)) {
+    if (active && (stages & 1)) scores(sa, smem);
     auto step = [&](auto stage_c, int t, auto& cur, auto& nxt) __attribute__((always_inline)) {
       constexpr int SG = decltype(stage_c)::value;  // stage of tile t
       if (t + 1 < ntiles) {
         wait_tiles(min(NST - 3, ntiles - 2 - t));
         block_barrier();
         if (t + NST - 1 < ntiles) issue((SG + NST - 1) % NST, t + NST - 1);
-        if (active) scores(nxt, smem + ((SG + 1) % NST) * STAGE);
+        if (active && ((stages >> ((SG + 1) % NST)) & 1)) scores(nxt, smem + ((SG + 1) % NST) * STAGE);
       }
-      if (active) finish(cur, smem + SG * STAGE, t);
+      if (active && ((stages >> SG) & 1)) finish(cur, smem + SG * STAGE, t);
     };
     int t = 0;
     for (; t + NST <= ntiles; t += NST) {
@@ -541,7 +551,7 @@ __global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
       }
     };
     Scores sa, sb;
-    pipeline(sa, sb, scores, finish);
+    pipeline(sa, sb, scores, finish, std::integral_constant<int, (1 << NST) - 1>{});
 
     const int qr = q0 + l32;
     if (active && qr < T) {
@@ -558,10 +568,18 @@ __global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
           *reinterpret_cast<bf16x4_t*>(orow + d * 32 + 8 * r4 + 4 * g) = w;
         }
     }
+    if (light_split) {  // the two barriers of the light parts' merge below
+      block_barrier();
+      block_barrier();
+    }
   } else {
     // ---- Light wave (<= 16 queries left, e.g. the 5 of T = 261 after 8 full waves): 16 queries on
-    // v_mfma_f32_16x16x32_bf16, half the MFMA and softmax work of a full wave. With 9 waves on 4
-    // SIMDs one SIMD carries three waves; this one is the third.
+    // v_mfma_f32_16x16x32_bf16, half the MFMA and softmax work of a full wave. 8 full waves and one
+    // light wave would put three waves on one SIMD, which every other SIMD then waits for at each
+    // tile's barrier; so, split (light_split), the light wave's tiles are shared by kLightParts
+    // waves, one per SIMD, part p taking the tiles of stage p (t % NST == p). Each part keeps its
+    // own running max, sum and output; parts 1.. park them in LDS after the loop and part 0 merges
+    // them (rescaled to the largest reference max, summed in part order) and stores the rows.
     // Layout: lane l, 16-lane group G = l / 16. S^T = K . Q^T per 16-key block kb (A = K rows
     // 16 kb + l % 16, dims 32 ks + 8 G; B = Q^T, query l % 16): s16[kb][v] = S^T[key 16 kb + 4 G + v]
     // [query l % 16], so a query's 64 keys lie in the four groups (max / sum over xor 16, xor 32).
@@ -668,11 +686,58 @@ __global__ __launch_bounds__(kMaxWaves64 * 64) void sq_attention_dma_kernel(
       }
     };
     Scores16 sa, sb;
-    pipeline(sa, sb, scores, finish);
+    static_assert(kLightParts == NST, "one light part per stage");
+    pipeline(sa, sb, scores, finish, lpart >= 0 ? 1 << lpart : (1 << NST) - 1);
+
+    if (light_split) {
+      // Every wave has passed its last tile's reads after the first barrier, so the stages are free.
+      constexpr int PSTRIDE = 18 * 64;  // floats per part: m, l, o[4][4] for 64 lanes
+      float* park = reinterpret_cast<float*>(smem);
+      block_barrier();
+      if (lpart > 0) {
+        float* pp = park + (lpart - 1) * PSTRIDE;
+        pp[lane] = m_i;
+        pp[64 + lane] = l_i;
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) pp[(2 + 4 * d + e) * 64 + lane] = o[d][e];
+      }
+      block_barrier();
+      if (lpart == 0) {
+        float mp[kLightParts], lp[kLightParts];
+        mp[0] = m_i;
+        lp[0] = l_i;
+#pragma unroll
+        for (int p = 1; p < kLightParts; ++p) {
+          mp[p] = park[(p - 1) * PSTRIDE + lane];
+          lp[p] = park[(p - 1) * PSTRIDE + 64 + lane];
+        }
+        float m = mp[0];
+#pragma unroll
+        for (int p = 1; p < kLightParts; ++p) m = fmaxf(m, mp[p]);
+        // Part 0 holds tile 0, so m is finite; a part without tiles has m = -inf, l = 0, o = 0.
+        float a[kLightParts];
+#pragma unroll
+        for (int p = 0; p < kLightParts; ++p) a[p] = __builtin_amdgcn_exp2f((mp[p] - m) * scale_log2);
+        l_i = lp[0] * a[0];
+#pragma unroll
+        for (int p = 1; p < kLightParts; ++p) l_i = fmaf(lp[p], a[p], l_i);
+#pragma unroll
+        for (int d = 0; d < 4; ++d)
+#pragma unroll
+          for (int e = 0; e < 4; ++e) {
+            float v = o[d][e] * a[0];
+#pragma unroll
+            for (int p = 1; p < kLightParts; ++p) v = fmaf(park[(p - 1) * PSTRIDE + (2 + 4 * d + e) * 64 + lane], a[p], v);
+            o[d][e] = v;
+          }
+      }
+    }
 
     // O^T[16 db + 4 G + v][query l16]: 4 consecutive dims per lane and block.
     const int qr = q0 + l16;
-    if (active && qr < T) {
+    if (active && qr < T && lpart <= 0) {
       const float inv = 1.0f / l_i;
       uint16_t* orow = out + ((int64_t)b * T + qr) * ors + (int64_t)h * DH;
 #pragma unroll
@@ -724,8 +789,15 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
   if (dma) {
     const size_t lds_dma = (size_t)kAttnStages * 2 * kKeyTile * 128;
     static_assert((size_t)kAttnStages * 2 * kKeyTile * 128 <= 64 * 1024, "needs no larger-LDS attribute");
-    sq_attention_dma_kernel<kAttnStages><<<grid, w * 64, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,
-                                                                         (int)N, scale_log2, out, ors, w);
+    // One workgroup per (image, head) whose last query wave is light (1..16 queries): that wave is
+    // split over kLightParts waves (its merge area, 3 parts of 18 x 64 floats, fits the stages).
+    const int64_t last = T - (w - 1) * 32;
+    const int split = (n_wg == 1 && last >= 1 && last <= 16 && w - 1 + kLightParts <= kDmaMaxWaves &&
+                       getenv("OUDJAT_ATTN_NO_SPLIT") == nullptr) ? kLightParts : 0;
+    static_assert((kLightParts - 1) * 18 * 64 * 4 <= kAttnStages * 2 * kKeyTile * 128, "merge area");
+    const int threads = (split ? w - 1 + kLightParts : w) * 64;
+    sq_attention_dma_kernel<kAttnStages><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,
+                                                                          (int)N, scale_log2, out, ors, w, split);
     return check_launch("sparse_query_attention");
   }
   const void* fn = Dh == 128 ? (const void*)sq_attention_kernel<128, kMinWaves, false>

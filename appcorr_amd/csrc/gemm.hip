@@ -388,8 +388,8 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
   }
   constexpr int CPR = BN / 8;
   if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) {
-    // Fully unrolled: all LDS reads of a thread's chunks first, then the table lookups, then the
-    // stores, so the LDS latencies overlap.
+    // Fully unrolled: all LDS reads of a thread's chunks first (their latencies overlap), then
+    // per chunk the table lookups and its store.
     // Chunks of rows at or past M are never stored: they are set to bf16 1.0 (inside the table
     // range) instead of read, so that their values (bf16(bias) on the zero-loaded rows, exactly zero
     // with zero biases, below the table range) cannot send the wave to the per-element path.
@@ -421,9 +421,7 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
       } else {
         w[0] = g0; w[1] = g1; w[2] = g2; w[3] = g3;
       }
-    }
-#pragma unroll
-    for (int it = 0; it < ITERS; ++it) {
+      // Stored as soon as it is ready: the stores drain while the next chunks' lookups run.
       const int c = threadIdx.x + it * NT;
       const int rl = c / CPR, cl = (c - rl * CPR) * 8;
       const int row = m0 + rl;
