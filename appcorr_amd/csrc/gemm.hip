@@ -1216,18 +1216,27 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
   };
   const int ib_w = NIA + g * (NIW / 2), ib_a = g * (NIA / 2);
   const uint32_t vw = lane_offset(ib_w, true), va = lane_offset(ib_a, false);
-  auto issue_tile = [&](int kt) __attribute__((always_inline)) {
+  auto issue_w = [&](int kt) __attribute__((always_inline)) {
     unsigned char* base = smem + (kt % NST) * STAGE;
     const uint32_t koff = (uint32_t)(kt * BK * 2);
-    constexpr int CW = NIW / 2, CA = NIA / 2;
+    constexpr int CW = NIW / 2;
 #pragma unroll
     for (int j = 0; j < (CW + 3) / 4; ++j)
       if (j < CW / 4 || lw < CW % 4)
         buffer_load_lds16(rsrc_w, base + (ib_w + lw + 4 * j) * 1024, vw + (uint32_t)j * step_w + koff);
+  };
+  auto issue_a = [&](int kt) __attribute__((always_inline)) {
+    unsigned char* base = smem + (kt % NST) * STAGE;
+    const uint32_t koff = (uint32_t)(kt * BK * 2);
+    constexpr int CA = NIA / 2;
 #pragma unroll
     for (int j = 0; j < (CA + 3) / 4; ++j)
       if (j < CA / 4 || lw < CA % 4)
         buffer_load_lds16(rsrc_a, base + (ib_a + lw + 4 * j) * 1024, va + (uint32_t)j * step_a + koff);
+  };
+  auto issue_tile = [&](int kt) __attribute__((always_inline)) {
+    issue_w(kt);
+    issue_a(kt);
   };
   constexpr int QMAX = (NIW / 2 + 3) / 4 + (NIA / 2 + 3) / 4;  // loads per wave and tile, at most
   static_assert(QMAX < 32, "vmcnt range");
@@ -1274,12 +1283,18 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
       default: wait_vmcnt<0>(); break;
     }
   };
-  // Memory phase of step j (tile u = j / 2): fragments, then tile u + 1's loads at the tile's first
-  // step (u >= 1), then (group 1, the tile's last step) its W rows of tile u + 1.
+  // Memory phase of step j (tile u = j / 2): fragments, then (u >= 1) the group's share of tile
+  // u + 1's loads, its W rows at the tile's first step and its A rows at the second (so that every
+  // memory phase issues about the same number of loads: with all of them at the first step, those
+  // phases outlasted the other group's MFMAs), then (group 1, the tile's last step) a wait for its
+  // W rows of tile u + 1, which group 0 reads after the next barrier.
   auto mem_phase = [&](int j) __attribute__((always_inline)) {
     read_frags(j);
     const int u = j >> 1;
-    if ((j & 1) == 0 && u >= 1 && u + 1 < KT) issue_tile(u + 1);
+    if (u >= 1 && u + 1 < KT) {
+      if ((j & 1) == 0) issue_w(u + 1);
+      else issue_a(u + 1);
+    }
     if (g == 1 && (j & 1) == 1 && u + 1 < KT) wait_n(n_arows);
   };
   auto compute_phase = [&](int j) __attribute__((always_inline)) {
