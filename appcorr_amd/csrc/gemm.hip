@@ -1096,9 +1096,10 @@ void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t 
     if (kt < KT) step(kt, f0, f1);
   } else {
     // Step kt: wait for tile kt, barrier (also: every wave is done with tile kt - 1's stage), refill
-    // that stage with tile kt - 1 + NST, then per 32-deep sub-step: the FNB B fragments, and the A
-    // fragments streamed two row blocks ahead of their MFMAs (a ring of three), so only one
-    // sub-step's B fragments and three A fragments are live next to the accumulators.
+    // that stage with tile kt - 1 + NST, then the MFMAs of the tile's 32-deep sub-steps with the A
+    // fragments streamed four row blocks ahead (a ring of five) and two sub-steps' B fragments, so
+    // few fragments are live next to the accumulators. (Two row blocks ahead, re-started at every
+    // sub-step, left LDS latency exposed: 44.0 -> 43.2 us on fc2.)
     // Tiles issued before step kt: 0 .. NST - 1 (kt = 0), 0 .. kt - 2 + NST (kt >= 1), so at most
     // NST - 1, resp. NST - 2, tiles after tile kt may still be in flight.
     for (int kt = 0; kt < KT; ++kt) {
@@ -1107,23 +1108,34 @@ void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t 
       if (kt >= 1 && kt - 1 + NST < KT) issue((kt - 1) % NST, kt - 1 + NST);
       __builtin_amdgcn_sched_barrier(0);
       const unsigned char* st = smem + (kt % NST) * STAGE;
-#pragma unroll
-      for (int s = 0; s < SUBW; ++s) {
+      // A fragments streamed RD row blocks ahead through a ring of RD + 1 across the tile's
+      // sub-steps, and the next sub-step's B fragments read at the start of the current one.
+      constexpr int RD = 4, NB = SUBW * FMB;
+      bf16x8_t b[2][FNB], a[RD + 1];
+      auto rd_a = [&](int idx) __attribute__((always_inline)) {
+        const int s = idx / FMB, i = idx % FMB;
         const int ch = 4 * (s * KSPLIT + kg) + (lane >> 4);
-        bf16x8_t b[FNB], a[3];
+        return *reinterpret_cast<const bf16x8_t*>(st + L::swz(wm0 + i * 16 + (lane & 15), ch));
+      };
+      auto rd_b = [&](int s, bf16x8_t (&bb)[FNB]) __attribute__((always_inline)) {
+        const int ch = 4 * (s * KSPLIT + kg) + (lane >> 4);
 #pragma unroll
         for (int j = 0; j < FNB; ++j)
-          b[j] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(BM + wn0 + j * 16 + (lane & 15), ch));
+          bb[j] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(BM + wn0 + j * 16 + (lane & 15), ch));
+      };
+      rd_b(0, b[0]);
 #pragma unroll
-        for (int i = 0; i < 2 && i < FMB; ++i)
-          a[i] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(wm0 + i * 16 + (lane & 15), ch));
+      for (int x = 0; x < RD && x < NB; ++x) a[x] = rd_a(x);
+#pragma unroll
+      for (int s = 0; s < SUBW; ++s) {
+        if (s + 1 < SUBW) rd_b(s + 1, b[(s + 1) & 1]);
 #pragma unroll
         for (int i = 0; i < FMB; ++i) {
-          if (i + 2 < FMB)
-            a[(i + 2) % 3] = *reinterpret_cast<const bf16x8_t*>(st + L::swz(wm0 + (i + 2) * 16 + (lane & 15), ch));
+          const int x = s * FMB + i;
+          if (x + RD < NB) a[(x + RD) % (RD + 1)] = rd_a(x + RD);
 #pragma unroll
           for (int j = 0; j < FNB; ++j)
-            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[j], a[i % 3], acc[i][j], 0, 0, 0);
+            acc[i][j] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(b[s & 1][j], a[x % (RD + 1)], acc[i][j], 0, 0, 0);
         }
       }
       __builtin_amdgcn_sched_barrier(0);
