@@ -182,9 +182,75 @@ __global__ __launch_bounds__(kPlanThreads) void topk_plan_kernel(
   }
 }
 
+// Running statistics of one plan (one 1024-thread workgroup, a fixed summation order, so the values
+// do not depend on timing): out = {sum(scores * keep), sum(scores), sum(keep), B * P, B}. The
+// product takes keep as 0.0 / 1.0 exactly like (scores * keep.float()).sum(), so a -inf score that
+// is not kept makes the first sum NaN, as it does there.
+__global__ __launch_bounds__(kPlanThreads) void plan_stats_kernel(const float* __restrict__ scores, int B, int P,
+                                                                  int64_t ssb, const uint8_t* __restrict__ keep,
+                                                                  float* __restrict__ out) {
+  __shared__ float part[3][kPlanWaves];
+  const int tid = threadIdx.x, lane = tid & 63, w = tid >> 6;
+  float kept_mass = 0.0f, full_mass = 0.0f, kept = 0.0f;
+  // Thread t takes columns t, t + 1024, ... of every row, rows in order; four loads in flight.
+  for (int b = 0; b < B; ++b) {
+    const float* srow = scores + (int64_t)b * ssb;
+    const uint8_t* krow = keep + (int64_t)b * P;
+    for (int p0 = tid; p0 < P; p0 += 4 * kPlanThreads) {
+      float v[4], kf[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        const int p = p0 + u * kPlanThreads;
+        v[u] = p < P ? srow[p] : 0.0f;
+        kf[u] = (p < P && krow[p]) ? 1.0f : 0.0f;
+      }
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        if (p0 + u * kPlanThreads < P) {
+          kept_mass += v[u] * kf[u];
+          full_mass += v[u];
+          kept += kf[u];
+        }
+      }
+    }
+  }
+#pragma unroll
+  for (int o = 32; o >= 1; o >>= 1) {
+    kept_mass += __shfl_xor(kept_mass, o, 64);
+    full_mass += __shfl_xor(full_mass, o, 64);
+    kept += __shfl_xor(kept, o, 64);
+  }
+  if (lane == 0) {
+    part[0][w] = kept_mass;
+    part[1][w] = full_mass;
+    part[2][w] = kept;
+  }
+  __syncthreads();
+  if (tid < 3) {
+    float t = part[tid][0];
+    for (int j = 1; j < kPlanWaves; ++j) t += part[tid][j];
+    out[tid] = 0.0f + t;  // as the running total 0 + sum after the first plan (-0 becomes +0)
+  } else if (tid == 3) {
+    out[3] = (float)B * (float)P;
+  } else if (tid == 4) {
+    out[4] = (float)B;
+  }
+}
+
 }  // namespace oudjat
 
 using namespace oudjat;
+
+extern "C" int oudjat_plan_stats(const float* scores, int64_t B, int64_t P, int64_t ssb, const uint8_t* keep,
+                                 float* out, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(B >= 0 && P >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "plan_stats: negative size");
+  OUDJAT_REQUIRE(out && (B * P == 0 || (scores && keep)), OUDJAT_ERR_INVALID_ARGUMENT, "plan_stats: null pointer");
+  OUDJAT_REQUIRE(ssb >= P, OUDJAT_ERR_UNSUPPORTED_LAYOUT, "plan_stats: score row stride %lld < P=%lld",
+                 (long long)ssb, (long long)P);
+  OUDJAT_REQUIRE(B < ((int64_t)1 << 24) && B * P < ((int64_t)1 << 40), OUDJAT_ERR_TOO_LARGE, "plan_stats: too large");
+  plan_stats_kernel<<<1, kPlanThreads, 0, as_stream(stream)>>>(scores, (int)B, (int)P, ssb, keep, out);
+  return check_launch("plan_stats");
+}
 
 extern "C" int oudjat_topk_plan(const float* scores, int64_t B, int64_t P, int64_t ssb, int64_t k,
                                 const int64_t* dindice, int64_t dsb, int64_t npre, int64_t ntok, int64_t* upd,

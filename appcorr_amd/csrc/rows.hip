@@ -249,16 +249,43 @@ __global__ __launch_bounds__(kRowThreads) void layerscale_add_kernel(
   }
 }
 
+// vec: rows are 16-byte aligned with dim % 4 == 0, so a lane reads 16-byte vectors, four in flight
+// (a 1024-wide row is one round of four loads per lane).
 __global__ __launch_bounds__(kRowThreads) void patch_importance_kernel(
-    const float* __restrict__ d, int64_t rows, int64_t dim, int64_t rs, int mode, float* __restrict__ out) {
+    const float* __restrict__ d, int64_t rows, int64_t dim, int64_t rs, int mode, bool vec, float* __restrict__ out) {
   const int64_t row = (int64_t)blockIdx.x * kRowsPerWg + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
   const float* p = d + row * rs;
   float acc = 0.0f;
-  for (int64_t c = lane; c < dim; c += 64) {
-    float v = p[c];
-    acc = fmaf(v, v, acc);
+  if (vec) {
+    const float4* p4 = reinterpret_cast<const float4*>(p);
+    const int64_t n4 = dim >> 2;
+    int64_t c = lane;
+    for (; c + 192 < n4; c += 256) {
+      float4 v[4];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) v[u] = p4[c + 64 * u];
+#pragma unroll
+      for (int u = 0; u < 4; ++u) {
+        acc = fmaf(v[u].x, v[u].x, acc);
+        acc = fmaf(v[u].y, v[u].y, acc);
+        acc = fmaf(v[u].z, v[u].z, acc);
+        acc = fmaf(v[u].w, v[u].w, acc);
+      }
+    }
+    for (; c < n4; c += 64) {
+      const float4 v = p4[c];
+      acc = fmaf(v.x, v.x, acc);
+      acc = fmaf(v.y, v.y, acc);
+      acc = fmaf(v.z, v.z, acc);
+      acc = fmaf(v.w, v.w, acc);
+    }
+  } else {
+    for (int64_t c = lane; c < dim; c += 64) {
+      float v = p[c];
+      acc = fmaf(v, v, acc);
+    }
   }
   acc = wave_sum(acc);
   if (lane == 0) {
@@ -372,7 +399,8 @@ extern "C" int oudjat_patch_importance(const float* d, int64_t rows, int64_t dim
   OUDJAT_REQUIRE(mode >= 0 && mode <= 2, OUDJAT_ERR_INVALID_ARGUMENT, "patch_importance: bad mode %d", mode);
   if (rows == 0) return OUDJAT_OK;
   OUDJAT_REQUIRE(out && (d || dim == 0), OUDJAT_ERR_INVALID_ARGUMENT, "patch_importance: null pointer");
+  const bool vec = dim % 4 == 0 && rs % 4 == 0 && aligned(d, 16);
   patch_importance_kernel<<<(unsigned)cdiv(rows, kRowsPerWg), kRowThreads, 0, as_stream(stream)>>>(d, rows, dim, rs,
-                                                                                                    mode, out);
+                                                                                                    mode, vec, out);
   return check_launch("patch_importance");
 }

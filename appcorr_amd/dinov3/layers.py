@@ -403,18 +403,29 @@ class SelfAttentionBlock(nn.Module):
             return cached
         return scores
 
+    _PLAN_STAT_KEYS = ("_token_pscore_kept_mass_total", "_token_pscore_full_mass_total",
+                       "_partial_token_kept_patch_total", "_partial_token_full_patch_total",
+                       "_partial_token_sample_total")
+
     @staticmethod
     def _accumulate_partial_token_plan_stats(cache_feature: Dict, plan: PartialTokenQueryPlan, scale: float = 1.0):
-        """block.py:790-844: running kept / full score mass and patch counts."""
-        pairs = (("_token_pscore_kept_mass_total", plan.kept_pscore_mass),
-                 ("_token_pscore_full_mass_total", plan.full_pscore_mass),
-                 ("_partial_token_kept_patch_total", plan.kept_patch_total),
-                 ("_partial_token_full_patch_total", plan.full_patch_total),
-                 ("_partial_token_sample_total", plan.sample_total))
-        for key, val in pairs:
-            v = val * scale if scale != 1.0 else val
-            prev = cache_feature.get(key)
-            cache_feature[key] = (val.new_zeros((), dtype=torch.float32) if prev is None else prev) + v
+        """block.py:790-844: running kept / full score mass and patch counts, total = total + value
+        (value * scale when scale != 1) for the five statistics, as fresh tensors; all five in one
+        multi-tensor launch. A missing total starts from the value itself, which equals 0 + value
+        here: the plan's statistics already carry the + 0 (plan_stats)."""
+        keys = SelfAttentionBlock._PLAN_STAT_KEYS
+        vals = [plan.kept_pscore_mass, plan.full_pscore_mass, plan.kept_patch_total, plan.full_patch_total,
+                plan.sample_total]
+        if scale != 1.0:
+            vals = list(torch._foreach_mul(vals, scale))
+        prev = [cache_feature.get(k) for k in keys]
+        if all(p is None for p in prev) and scale == 1.0:
+            for k, v in zip(keys, vals):
+                cache_feature[k] = v
+            return
+        prev = [v.new_zeros((), dtype=torch.float32) if p is None else p for p, v in zip(prev, vals)]
+        for k, t in zip(keys, torch._foreach_add(prev, vals)):
+            cache_feature[k] = t
 
     def _build_query_plan(self, x: Tensor, dindice: Tensor, rope, cache_feature: Dict, tag: str, kw: dict,
                           num_pretokens: int) -> PartialTokenQueryPlan:
@@ -429,8 +440,14 @@ class SelfAttentionBlock(nn.Module):
         else:
             server = self._resolve_server_token_scores(cache_feature, tag, kw["server_pscore"]).gather(1,
                                                                                                        dindice_patches)
-        combined = self._combine_patch_scores(server, kw["server_pscore_weight"], mobile, kw["mobile_pscore_weight"],
-                                              kw["pscore_fusion"])
+        if (kw["server_pscore_weight"] == 0.0 and kw["mobile_pscore_weight"] == 1.0 and mobile is not None
+                and mobile.dtype == torch.float32 and kw["pscore_fusion"] not in ("multiply", "geo_mean")):
+            # 0 * 0 + 1 * mobile is mobile itself (up to the sign of a zero score, which ranks and
+            # sums the same): no launches for the combine.
+            combined = mobile
+        else:
+            combined = self._combine_patch_scores(server, kw["server_pscore_weight"], mobile,
+                                                  kw["mobile_pscore_weight"], kw["pscore_fusion"])
         cvm = kw.get("candidate_valid_mask")
         if cvm is not None:
             combined = combined.masked_fill(~cvm.to(combined.device), float("-inf"))
@@ -449,14 +466,12 @@ class SelfAttentionBlock(nn.Module):
             active_rope_idx=tp.active_rope_idx, row_slot=tp.row_slot)
         qs.active_query_mask = qs.query_valid_mask
         keep = tp.keep_mask
+        stats = K.plan_stats(scores, keep)  # block.py:762-788 in one launch
         return PartialTokenQueryPlan(
             update_indice=tp.update_indice, fixed_query_state=qs, server_patch_scores=server.detach(),
             mobile_patch_scores=None if mobile is None else mobile.detach(), combined_patch_scores=combined.detach(),
-            kept_pscore_mass=(combined * keep.to(combined.dtype)).sum(dtype=torch.float32),
-            full_pscore_mass=combined.sum(dtype=torch.float32),
-            kept_patch_total=keep.sum(dtype=torch.float32),
-            full_patch_total=keep.new_full((), float(keep.shape[0] * keep.shape[1]), dtype=torch.float32),
-            sample_total=keep.new_full((), float(keep.shape[0]), dtype=torch.float32))
+            kept_pscore_mass=stats[0], full_pscore_mass=stats[1], kept_patch_total=stats[2],
+            full_patch_total=stats[3], sample_total=stats[4])
 
     # -- the correction step (block.py:942-1191) ---------------------------------------------------
 

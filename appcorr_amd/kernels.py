@@ -331,6 +331,21 @@ def topk_plan(scores: torch.Tensor, k: int, dindice: torch.Tensor, num_pretokens
     return TopkPlan(upd, abat, apos, atok, pmask, ridx, keep, slot)
 
 
+def plan_stats(scores: torch.Tensor, keep: torch.Tensor) -> torch.Tensor:
+    """The plan's statistics in one launch (block.py:762-788): fp32 [5] = (sum(scores * keep),
+    sum(scores), sum(keep), B * P, B) for scores [B, P] fp32 and the bool keep mask [B, P]."""
+    _require_cuda(scores, keep)
+    _require(scores.dtype == torch.float32 and scores.dim() == 2 and (scores.numel() == 0 or scores.stride(1) == 1),
+             "plan_stats: scores must be [B, P] fp32 with contiguous rows")
+    _require(keep.dtype == torch.bool and keep.shape == scores.shape and keep.is_contiguous(),
+             "plan_stats: keep must be a contiguous bool mask shaped like scores")
+    B, Pn = scores.shape
+    out = torch.empty((5,), device=scores.device, dtype=torch.float32)
+    _launch("plan_stats", scores, "oudjat_plan_stats", _ptr(scores), B, Pn, max(scores.stride(0), Pn), _ptr(keep),
+            _ptr(out), _stream(scores))
+    return out
+
+
 def patch_importance(delta: torch.Tensor, mode: int = _lib.IMPORTANCE_L2) -> torch.Tensor:
     """Per-row reduction of a residual delta [..., D] fp32: L2 norm, energy or RMS -> [...]."""
     _require_cuda(delta)

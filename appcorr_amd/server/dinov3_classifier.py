@@ -63,6 +63,18 @@ def make_group_plan(dindice: torch.Tensor, num_pretokens: int) -> GroupCorrectio
         full_patch_count=count.clone(), kept_residual_mass=zeros, full_residual_mass=zeros.clone())
 
 
+def _patch_count_sums(plan: GroupCorrectionPlan) -> torch.Tensor:
+    """fp32 [2] = (0 + kept_patch_count.sum(), 0 + full_patch_count.sum()), computed once per pair
+    of count tensors (a plan whose count tensors are replaced gets new sums)."""
+    cached = getattr(plan, "_count_sums", None)
+    if cached is None or cached[0] is not plan.kept_patch_count or cached[1] is not plan.full_patch_count:
+        sums = torch.stack([plan.kept_patch_count.sum(dtype=torch.float32),
+                            plan.full_patch_count.sum(dtype=torch.float32)]) + 0.0
+        cached = (plan.kept_patch_count, plan.full_patch_count, sums)
+        plan._count_sums = cached
+    return cached[2]
+
+
 class DINOv3ClassifierExecutor(ModelExecutor):
     def __init__(self, device: torch.device):
         super().__init__(device)
@@ -171,11 +183,17 @@ class DINOv3ClassifierExecutor(ModelExecutor):
         x = context.get("input_tokens")
         opts = normalize_appcorr_kwargs(config.appcorr_kwargs, config.transmission_kwargs)
         hint = context.get("mobile_pscore_hint_map")
-        zero = x.new_zeros((), dtype=torch.float32)
-        cache["_token_prune_kept_patch_total"] = cache.get("_token_prune_kept_patch_total", zero) + \
-            plan.kept_patch_count.sum(dtype=torch.float32)
-        cache["_token_prune_full_patch_total"] = cache.get("_token_prune_full_patch_total", zero) + \
-            plan.full_patch_count.sum(dtype=torch.float32)
+        # total = total + count.sum() for the two counters (dinov3_classifier.py:618-634), with the
+        # group plan's sums computed once and both additions in one launch.
+        keys = ("_token_prune_kept_patch_total", "_token_prune_full_patch_total")
+        sums = _patch_count_sums(plan)
+        prev = [cache.get(k) for k in keys]
+        if prev[0] is None and prev[1] is None:
+            cache[keys[0]], cache[keys[1]] = sums[0], sums[1]
+        else:
+            prev = [x.new_zeros((), dtype=torch.float32) if p is None else p for p in prev]
+            for k, t in zip(keys, torch._foreach_add(prev, [sums[0], sums[1]])):
+                cache[k] = t
         self.begin_dinov3_correct_event()
         block_kwargs = dict(
             appcorr_method=opts["method"], token_keep_ratio=opts["token_keep_ratio"],

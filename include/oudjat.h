@@ -84,6 +84,14 @@ int oudjat_patch_importance(const float* delta, int64_t rows, int64_t dim, int64
  *   keep_mask [B, P] (1 byte, may be NULL),
  *   row_slot [B, num_tokens] int32 (packed row b*T+s of token t of image b, or -1; may be NULL).
  * Limits: P <= 16384, (P + num_tokens) * 4 bytes <= 144 KiB. */
+/* Rows 2+3 -- the plan's running statistics, _compute_partial_token_plan_stats
+ * (appcorr/models/dinov3/layers/block.py:762-788): out[5] fp32 = {sum(scores * keep),
+ * sum(scores), sum(keep), B * P, B} for scores [B, P] fp32 (row stride score_stride_b) and the
+ * keep_mask [B, P] of oudjat_topk_plan. One workgroup, fixed summation order (deterministic);
+ * an unkept -inf score makes the first sum NaN, as (scores * keep.float()).sum() does. */
+int oudjat_plan_stats(const float* scores, int64_t B, int64_t P, int64_t score_stride_b,
+                      const uint8_t* keep_mask, float* out, oudjat_stream_t stream);
+
 int oudjat_topk_plan(const float* scores, int64_t B, int64_t P, int64_t score_stride_b, int64_t k,
                      const int64_t* dindice, int64_t dindice_stride_b, int64_t num_pre,
                      int64_t num_tokens, int64_t* update_indice, int64_t* active_batch_idx,

@@ -4,6 +4,7 @@ Follows appcorr/models/dinov3/layers/block.py:
   _select_patch_keep_mask           :358-395  (k = min(int(P * ratio), P); k == 0 -> none; k == P -> all)
   _build_packed_query_state_fixed_k :397-442  (kept indices sorted ascending; pretokens first)
   _build_packed_query_state_all_keep:444-490
+  _compute_partial_token_plan_stats :762-788  (plan_stats)
 and the PackedQueryState fields of attention.py:64-74.
 
 torch.topk leaves the order of equal scores unspecified (block.py:385-390); the selection here
@@ -82,3 +83,15 @@ def build_plan(scores: np.ndarray, k: int, dindice: np.ndarray, num_pretokens: i
         keep_mask=keep_mask,
         row_slot=row_slot,
     )
+
+
+def plan_stats(scores: np.ndarray, keep: np.ndarray) -> np.ndarray:
+    """block.py:762-788, in float64: (sum(scores * keep), sum(scores), sum(keep), B * P, B).
+    keep enters the product as 0.0 / 1.0, so an unkept -inf (or any NaN) score makes the first sum
+    NaN, as (scores * keep.to(scores.dtype)).sum() does."""
+    s = np.asarray(scores, dtype=np.float64)
+    kf = np.asarray(keep, dtype=bool).astype(np.float64)
+    B, P = s.shape
+    with np.errstate(invalid="ignore"):
+        kept_mass = float((s * kf).sum())
+    return np.array([kept_mass, float(s.sum()), float(kf.sum()), float(B * P), float(B)], dtype=np.float64)

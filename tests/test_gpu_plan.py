@@ -75,3 +75,40 @@ def test_topk_candidate_subset_dindice(dev):
     scores = rng.standard_normal((B, grp.size)).astype(np.float32)
     _check(dev, scores, 64, npre, ntok=N, dindice=dind)
 
+
+
+def _check_stats(dev, scores: np.ndarray, keep: np.ndarray):
+    got = K.plan_stats(torch.from_numpy(scores).to(dev), torch.from_numpy(keep).to(dev)).cpu().numpy().astype(np.float64)
+    ref = OP.plan_stats(scores, keep)
+    # fp32 sums in a fixed order against the float64 oracle: |error| <= n * 2^-24 * sum|s|.
+    bound = scores.size * 2.0 ** -24 * float(np.abs(scores[np.isfinite(scores)]).sum()) + 1e-30
+    for i in range(2):
+        if np.isnan(ref[i]) or np.isinf(ref[i]):
+            assert (np.isnan(got[i]) and np.isnan(ref[i])) or got[i] == ref[i], (i, got[i], ref[i])
+        else:
+            assert abs(got[i] - ref[i]) <= bound, (i, got[i], ref[i], bound)
+    np.testing.assert_array_equal(got[2:], ref[2:])
+
+
+@pytest.mark.parametrize("B,P,ratio", [(16, 1024, 0.25), (1, 196, 0.5), (3, 100, 0.33), (2, 16384, 0.05)])
+def test_plan_stats_against_oracle(dev, B, P, ratio):
+    rng = np.random.default_rng(B * 7 + P)
+    scores = np.abs(rng.laplace(size=(B, P))).astype(np.float32)
+    k = OP.keep_count(P, ratio)
+    got = K.topk_plan(torch.from_numpy(scores).to(dev), k,
+                      torch.from_numpy(np.broadcast_to(np.arange(5 + P, dtype=np.int64), (B, 5 + P)).copy()).to(dev), 5)
+    _check_stats(dev, scores, got.keep_mask.cpu().numpy().astype(bool))
+
+
+def test_plan_stats_masked_and_special_values(dev):
+    rng = np.random.default_rng(11)
+    scores = rng.standard_normal((3, 300)).astype(np.float32)
+    keep = rng.random((3, 300)) < 0.3
+    _check_stats(dev, scores, keep)
+    s2 = scores.copy()
+    s2[0, ~keep[0]] = -np.inf           # masked candidates (candidate_valid_mask): NaN kept mass
+    _check_stats(dev, s2, keep)
+    s3 = scores.copy()
+    s3[1, np.flatnonzero(keep[1])[:2]] = -np.inf  # only kept -inf: kept mass -inf
+    _check_stats(dev, s3, keep)
+    _check_stats(dev, np.zeros((2, 0), dtype=np.float32), np.zeros((2, 0), dtype=bool))

@@ -145,3 +145,34 @@ def test_reconstruct_matches_torch_eager_sequence():
     np.testing.assert_array_equal(xo, torch_bf16_to_bits(x_out))
     np.testing.assert_array_equal(nb, torch_bf16_to_bits(bos_ref))
     assert bits_to_torch_bf16(xo).shape == x.shape
+
+
+def test_plan_stats_known_answers():
+    # Hand-derived: masses are sums of the kept / all scores, counts are plain counts.
+    s = np.array([[1.0, 2.0, 3.0, 4.0], [0.5, -1.5, 2.5, 0.0]], dtype=np.float32)
+    keep = np.array([[0, 1, 0, 1], [1, 0, 1, 0]], dtype=bool)
+    got = OP.plan_stats(s, keep)
+    np.testing.assert_array_equal(got, [2.0 + 4.0 + 0.5 + 2.5, 1 + 2 + 3 + 4 + 0.5 - 1.5 + 2.5 + 0.0, 4.0, 8.0, 2.0])
+    # An unkept -inf score: -inf * 0 is NaN in the kept mass; the full mass is -inf.
+    s2 = s.copy()
+    s2[0, 0] = -np.inf
+    got = OP.plan_stats(s2, keep)
+    assert np.isnan(got[0]) and got[1] == -np.inf and got[2] == 4.0
+    # Kept -inf alone: the kept mass is -inf, not NaN.
+    keep2 = keep.copy()
+    keep2[0, 0] = True
+    got = OP.plan_stats(s2, keep2)
+    assert got[0] == -np.inf and got[2] == 5.0
+
+
+def test_plan_stats_matches_torch_formula():
+    import torch
+    rng = np.random.default_rng(3)
+    s = rng.standard_normal((16, 1024)).astype(np.float32)
+    keep = rng.random((16, 1024)) < 0.25
+    st, kt = torch.from_numpy(s), torch.from_numpy(keep)
+    ref = [float((st * kt.to(st.dtype)).sum(dtype=torch.float32)), float(st.sum(dtype=torch.float32)),
+           float(kt.sum(dtype=torch.float32))]
+    got = OP.plan_stats(s, keep)
+    np.testing.assert_allclose(got[:3], ref, rtol=1e-5, atol=1e-3)
+    assert got[3] == 16 * 1024 and got[4] == 16
