@@ -180,13 +180,28 @@ __global__ __launch_bounds__(256) void nvfp4_dequantize_kernel(const uint8_t* __
   const int64_t tiles_n = (K + 63) >> 6;
   const int64_t tile = (int64_t)pm * tiles_n + (int64_t)blockIdx.x * CT + c / 8;
   const int jb = (c >> 1) & 3;  // block within the scale tile
+  // Every pass's scale byte and code word are loaded first (all loads of the lane in flight at
+  // once), then decoded and stored.
+  constexpr int NP = 128 / RPP;
+  uint32_t wq[NP], sq[NP];
 #pragma unroll
-  for (int pass = 0; pass < 128 / RPP; ++pass) {
+  for (int pass = 0; pass < NP; ++pass) {
+    const int r = pass * RPP + t / LPR;
+    const int64_t row = (int64_t)pm * 128 + r;
+    wq[pass] = 0u;
+    sq[pass] = 0u;
+    if (row < M) {
+      sq[pass] = sc[tile * 512 + (r & 31) * 16 + (r >> 5) * 4 + jb];
+      wq[pass] = *reinterpret_cast<const uint32_t*>(qd + row * (K >> 1) + (col >> 1));
+    }
+  }
+#pragma unroll
+  for (int pass = 0; pass < NP; ++pass) {
     const int r = pass * RPP + t / LPR;
     const int64_t row = (int64_t)pm * 128 + r;
     if (row >= M) break;
-    const float s = e4m3_decode(sc[tile * 512 + (r & 31) * 16 + (r >> 5) * 4 + jb]);
-    const uint32_t w = *reinterpret_cast<const uint32_t*>(qd + row * (K >> 1) + (col >> 1));
+    const float s = e4m3_decode((uint8_t)sq[pass]);
+    const uint32_t w = wq[pass];
     const auto v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
     const auto v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
     const auto v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
