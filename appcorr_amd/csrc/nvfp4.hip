@@ -112,8 +112,8 @@ __device__ __forceinline__ uint32_t nvfp4_codes8(const float* f, float tot, floa
 // 64 / CT rows per pass: lane t of a pass owns row t / (4 CT) and 16-element block t % (4 CT) of the
 // region, so 4 CT consecutive lanes read 128 CT contiguous bytes of one row (two 16-byte loads each)
 // and write its 32 CT bytes of codes (8 each). The block scale is computed once per block; the 4
-// scale bytes of a row within a scale tile are contiguous in the swizzled layout and leave as one
-// 4-byte store from the tile's first lane of the row.
+// scale bytes of a row within a scale tile are contiguous in the swizzled layout and go to LDS as one
+// word from the tile's first lane of the row; the CT finished tiles are stored at the end.
 template <int CT>
 __global__ __launch_bounds__(256) void nvfp4_quantize_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t K,
                                                              int64_t sm, const float* __restrict__ tsp,
@@ -127,7 +127,7 @@ __global__ __launch_bounds__(256) void nvfp4_quantize_kernel(const uint16_t* __r
   const bool col_ok = col < K;  // K % 16 == 0: a block is wholly in or out
   const float ts = *tsp;
   const int64_t tiles_n = (K + 63) >> 6;
-  const int64_t tile = (int64_t)pm * tiles_n + (int64_t)blockIdx.x * CT + j / 4;
+  __shared__ __align__(16) uint32_t sscale[CT * 128];  // the CT scale tiles, in their global byte order
 #pragma unroll
   for (int pass = 0; pass < 128 / RPP; ++pass) {
     const int r = pass * RPP + t / LPR;  // row within the tile
@@ -154,9 +154,14 @@ __global__ __launch_bounds__(256) void nvfp4_quantize_kernel(const uint16_t* __r
     // Scale bytes of the row's 4 blocks of this tile (zero for blocks past K or rows past M).
     const uint32_t b = ok ? code : 0u;
     const uint32_t b1 = __shfl_down(b, 1, 64), b2 = __shfl_down(b, 2, 64), b3 = __shfl_down(b, 3, 64);
-    if ((j & 3) == 0 && ((int64_t)blockIdx.x * CT + j / 4) < tiles_n)
-      *reinterpret_cast<uint32_t*>(sc + tile * 512 + (r & 31) * 16 + (r >> 5) * 4) = b | (b1 << 8) | (b2 << 16) | (b3 << 24);
+    if ((j & 3) == 0) sscale[(j / 4) * 128 + (r & 31) * 4 + (r >> 5)] = b | (b1 << 8) | (b2 << 16) | (b3 << 24);
   }
+  // The workgroup's CT scale tiles (512 bytes each, consecutive in the swizzled layout) leave as
+  // whole 16-byte stores instead of 4-byte pieces spread over the passes.
+  __syncthreads();
+  const int64_t tile0 = (int64_t)pm * tiles_n + (int64_t)blockIdx.x * CT;
+  if (t < CT * 32 && (int64_t)blockIdx.x * CT + t / 32 < tiles_n)
+    reinterpret_cast<uint4*>(sc + tile0 * 512)[t] = reinterpret_cast<const uint4*>(sscale)[t];
 }
 
 // Dequantize: one workgroup per 128-row x 64 CT-column region, lane t of a pass decoding the 8
