@@ -326,60 +326,67 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
   constexpr int NW = NT / 64;
   const uint16_t* ct = reinterpret_cast<const uint16_t*>(smem);
   if constexpr (EPI == kEpiQkv) {
-    // One work item = (row, head, 8-wide chunk of the left half) with its partner chunk Dh/2 to the
-    // right: RoPE on q and k of patch rows, then q packed or k / v into the cache row. A tile covers
-    // whole heads (Dh | BN); each item finds whether its head is one of q, k or v.
+    // One work item = (row, 8-wide chunk c of a head's left half); the item handles that chunk and
+    // its partner c + Dh/2 in every head of the tile (Dh | BN), so the row's metadata and its four
+    // RoPE table chunks (cos / sin at c and c + Dh/2) are loaded once for all of them: RoPE on q and
+    // k of patch rows, then q packed or k / v into the cache row. Metadata of all of a thread's items
+    // first, then their table chunks (one round trip each), then the heads.
     const QkvArgs& qa = ea.qkv;
-    const int HD = qa.H * qa.Dh, half = qa.Dh >> 1;
-    const int lg_cph = __builtin_ctz((unsigned)(half >> 3));  // chunk pairs per head = Dh / 16
-    constexpr int PPR = BN / 16;                               // chunk pairs per tile row
-    constexpr int ITEMS = (BM * PPR + NW * 64 - 1) / (NW * 64);
-    // The row metadata of all of a thread's items is loaded first (one round trip), and every item
-    // loads its RoPE table rows unconditionally (row 0 of the table for rows without RoPE, whose
-    // values are then not used), so the unrolled items overlap their memory latencies instead of
-    // running one dependent load chain after another.
+    const int Dh = qa.Dh, HD = qa.H * Dh, half = Dh >> 1;
+    const int cph = half >> 3;                               // chunks per half head (4 at Dh = 64)
+    const int lg_cph = __builtin_ctz((unsigned)cph);
+    const int nh = BN / Dh;                                  // heads in the tile
+    const int n_items = BM * cph;
+    constexpr int ITEMS = (BM * 8 + NW * 64 - 1) / (NW * 64);  // cph <= 8 (Dh <= 128)
+    const bool tile_qk = n0 < 2 * HD;                        // some head of the tile is q or k
     bool rope[ITEMS];
-    int64_t trow[ITEMS], dst[ITEMS];
+    int64_t trow[ITEMS], rowq[ITEMS], kvrow[ITEMS];
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
       const int p = threadIdx.x + it * NW * 64;
-      const int pc = p < BM * PPR ? p : BM * PPR - 1;
-      const int rl = pc / PPR, pr = pc - rl * PPR;
+      const int pc = p < n_items ? p : n_items - 1;
+      const int rl = pc >> lg_cph, cc = pc & (cph - 1);
       const int row = min(m0 + rl, M - 1);
-      const int c0 = ((pr >> lg_cph) << (lg_cph + 4)) + ((pr & ((1 << lg_cph) - 1)) << 3);  // head * Dh + 8 c
-      const int colg = n0 + c0;
-      const int which = colg >= 2 * HD ? 2 : (colg >= HD ? 1 : 0);
-      const int hcol = colg - which * HD;  // column within q, k or v
       const bool pm = qa.pm[row];
       const int64_t ri = qa.ridx[row], bi = qa.bi[row], ti = qa.ti[row];
-      rope[it] = which < 2 && pm;
-      trow[it] = (rope[it] ? ri * qa.tst : 0) + (c0 & (qa.Dh - 1));
-      dst[it] = (which == 0 ? (int64_t)row * HD : bi * qa.kvb + ti * qa.kvn + (which - 1) * HD) + hcol;
+      rope[it] = pm && tile_qk;
+      trow[it] = (rope[it] ? ri * qa.tst : 0) + cc * 8;
+      rowq[it] = (int64_t)row * HD;
+      kvrow[it] = bi * qa.kvb + ti * qa.kvn;
+    }
+    float cl8[ITEMS][8], cr8[ITEMS][8], sl8[ITEMS][8], sr8[ITEMS][8];
+#pragma unroll
+    for (int it = 0; it < ITEMS; ++it) {
+      if (tile_qk && threadIdx.x + it * NW * 64 < n_items) {
+        load8f(qa.cos_t + trow[it], cl8[it]);
+        load8f(qa.cos_t + trow[it] + half, cr8[it]);
+        load8f(qa.sin_t + trow[it], sl8[it]);
+        load8f(qa.sin_t + trow[it] + half, sr8[it]);
+      }
     }
 #pragma unroll
     for (int it = 0; it < ITEMS; ++it) {
       const int p = threadIdx.x + it * NW * 64;
-      const int pc = p < BM * PPR ? p : BM * PPR - 1;
-      const int rl = pc / PPR, pr = pc - rl * PPR;
-      const int c0 = ((pr >> lg_cph) << (lg_cph + 4)) + ((pr & ((1 << lg_cph) - 1)) << 3);
-      const int colg = n0 + c0;
-      uint4 lo = *reinterpret_cast<const uint4*>(ct + rl * LDT + c0);
-      uint4 hi = *reinterpret_cast<const uint4*>(ct + rl * LDT + c0 + half);
-      float cl8[8], cr8[8], sl8[8], sr8[8];
-      load8f(qa.cos_t + trow[it], cl8);
-      load8f(qa.cos_t + trow[it] + half, cr8);
-      load8f(qa.sin_t + trow[it], sl8);
-      load8f(qa.sin_t + trow[it] + half, sr8);
-      if (rope[it]) {
-        float l[8], rr[8];
-        unpack8(lo, l);
-        unpack8(hi, rr);
-        rope8(l, rr, cl8, cr8, sl8, sr8);
-        lo = pack8(l);
-        hi = pack8(rr);
-      }
-      if (p < BM * PPR && m0 + rl < M) {
-        uint16_t* d = (colg < HD ? qa.q_out : qa.kv) + dst[it];
+      const int rl = p >> lg_cph, cc = p & (cph - 1);
+      if (p >= n_items || m0 + rl >= M) continue;
+#pragma unroll
+      for (int j = 0; j < BN / 16; ++j) {  // Dh >= 16
+        if (j >= nh) break;
+        const int c0 = j * Dh + cc * 8;
+        const int colg = n0 + c0;
+        const int which = colg >= 2 * HD ? 2 : (colg >= HD ? 1 : 0);
+        const int hcol = colg - which * HD;  // column within q, k or v
+        uint4 lo = *reinterpret_cast<const uint4*>(ct + rl * LDT + c0);
+        uint4 hi = *reinterpret_cast<const uint4*>(ct + rl * LDT + c0 + half);
+        if (which < 2 && rope[it]) {
+          float l[8], rr[8];
+          unpack8(lo, l);
+          unpack8(hi, rr);
+          rope8(l, rr, cl8[it], cr8[it], sl8[it], sr8[it]);
+          lo = pack8(l);
+          hi = pack8(rr);
+        }
+        uint16_t* d = which == 0 ? qa.q_out + rowq[it] + hcol : qa.kv + kvrow[it] + (which - 1) * HD + hcol;
         *reinterpret_cast<uint4*>(d) = lo;
         *reinterpret_cast<uint4*>(d + half) = hi;
       }
@@ -855,7 +862,10 @@ struct R16Layout {
 // wave row (BM / WGM rows), whichever is larger.
 __host__ __device__ constexpr int r16_lut_offset(int bm, int bn, int wgm, int wgn, int ksplit, int bk, int nst) {
   const int stages = nst * (bm + bn) * 2 * bk;
-  const int tile = (bm / wgm) * (bn + 8) * 2;
+  // The whole bf16 tile when it fits next to the GELU table in the 160 KB of LDS (the epilogue then
+  // runs in one pass), else one wave row's share.
+  const int full = bm * (bn + 8) * 2;
+  const int tile = (ksplit == 1 && wgm > 1 && full + 2 * kGeluLut <= 160 * 1024) ? full : (bm / wgm) * (bn + 8) * 2;
   const int red = ksplit > 1 ? wgm * wgn * 64 * (bm / wgm / 16) * (bn / wgn / 16) * 4 * 4 : 0;  // fp32 partials
   const int epi = red + tile;
   return stages > epi ? stages : epi;
@@ -866,7 +876,10 @@ __host__ __device__ constexpr int r16_lut_offset(int bm, int bn, int wgm, int wg
 // group 1's partial sums are added into group 0's through LDS first. Then one wave row at a time
 // writes bf16(acc + bias) into an LDS tile and every thread finishes the epilogue of those rows.
 // The caller's LDS stages must be free (no wave still reads them); this function begins with a barrier.
-template <int BM, int BN, int WGM, int WGN, int KSPLIT, int FMB, int FNB, int EPI>
+// TILE_BYTES: LDS the caller can give the bf16 tile (0: unknown). When the whole BM-row tile fits,
+// all wave rows write it at once and phase 2 runs once over all rows (one latency chain of its
+// loads instead of one per wave row).
+template <int BM, int BN, int WGM, int WGN, int KSPLIT, int FMB, int FNB, int EPI, int TILE_BYTES = 0>
 __device__ __forceinline__ void r16_epilogue(f32x4_t (&acc)[FMB][FNB], unsigned char* smem, int kLutOff, int kg, int wr,
                                              int wm, int wn0, int lane, int m0, int n0, int M, const EpiArgs& ea,
                                              uint16_t* __restrict__ C, int64_t ldc) {
@@ -898,6 +911,28 @@ __device__ __forceinline__ void r16_epilogue(f32x4_t (&acc)[FMB][FNB], unsigned 
 #pragma unroll
           for (int v = 0; v < 4; ++v) acc[i][j][v] += red[((i * FNB + j) * 4 + v) * (NWG * 64) + t0];
     }
+  }
+  if constexpr (WGM > 1 && KSPLIT == 1 && RED == 0 && BM * LDT * 2 <= TILE_BYTES) {
+#pragma unroll
+    for (int j = 0; j < FNB; ++j) {
+      const int cl = wn0 + j * 16 + 4 * (lane >> 4);
+      float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+      if (ea.bias) {
+        const uint2 bw = *reinterpret_cast<const uint2*>(ea.bias + n0 + cl);
+        b0 = lo_bf16(bw.x); b1 = hi_bf16(bw.x); b2 = lo_bf16(bw.y); b3 = hi_bf16(bw.y);
+      }
+#pragma unroll
+      for (int i = 0; i < FMB; ++i) {
+        uint2 w;
+        w.x = cvt_pk_bf16(acc[i][j][0] + b0, acc[i][j][1] + b1);
+        w.y = cvt_pk_bf16(acc[i][j][2] + b2, acc[i][j][3] + b3);
+        *reinterpret_cast<uint2*>(ct + (wm * WM + i * 16 + (lane & 15)) * LDT + cl) = w;
+      }
+    }
+    __syncthreads();
+    store_tile_phase2<BM, BN, NT, EPI>(reinterpret_cast<unsigned char*>(ct),
+                                       reinterpret_cast<const uint16_t*>(smem + kLutOff), m0, n0, M, ea, C, ldc);
+    return;
   }
   // One wave row at a time: its waves write bf16(acc + bias) into the LDS tile, then every thread
   // finishes the epilogue of those WM rows.
@@ -1340,7 +1375,8 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
     }
   }
 
-  r16_epilogue<BM, BN, WGM, WGN, 1, FMB, FNB, EPI>(acc, smem, kLutOff, 0, wave, g, wn0, lane, m0, n0, M, ea, C, ldc);
+  r16_epilogue<BM, BN, WGM, WGN, 1, FMB, FNB, EPI, kLutOff>(acc, smem, kLutOff, 0, wave, g, wn0, lane, m0, n0, M, ea, C,
+                                                           ldc);
 }
 
 // ------------------------------------------------------------------------------------------------
