@@ -1220,7 +1220,17 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
 
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int kLutOff = r16_lut_offset(BM, BN, WGM, WGN, 1, BK, NST);
-  if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) load_gelu_table<512>(smem + kLutOff);
+  // The GELU table (10 KB) is only needed by the epilogue: its loads are issued here, ahead of the
+  // first K tiles (so they retire first and no wait holds the tiles back), and the registers are
+  // written to LDS after the K loop.
+  constexpr int kLutChunks = kGeluLut / 8;  // 16-byte pieces
+  static_assert(kLutChunks <= 2 * 512, "two pieces per thread");
+  uint4 lut_lo = make_uint4(0u, 0u, 0u, 0u), lut_hi = lut_lo;
+  if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) {
+    const uint4* src = reinterpret_cast<const uint4*>(g_gelu_lut);
+    lut_lo = src[threadIdx.x];
+    if (threadIdx.x + 512 < kLutChunks) lut_hi = src[threadIdx.x + 512];
+  }
 
   const int tiles_n = (N + BN - 1) / BN;
   const int tiles_m = (M + BM - 1) / BM;
@@ -1375,6 +1385,11 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
     }
   }
 
+  if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) {  // visible after the epilogue's first barrier
+    uint4* dst = reinterpret_cast<uint4*>(smem + kLutOff);
+    dst[threadIdx.x] = lut_lo;
+    if (threadIdx.x + 512 < kLutChunks) dst[threadIdx.x + 512] = lut_hi;
+  }
   r16_epilogue<BM, BN, WGM, WGN, 1, FMB, FNB, EPI, kLutOff>(acc, smem, kLutOff, 0, wave, g, wn0, lane, m0, n0, M, ea, C,
                                                            ldc);
 }
