@@ -890,26 +890,39 @@ __device__ __forceinline__ void r16_epilogue(f32x4_t (&acc)[FMB][FNB], unsigned 
   constexpr int RED = KSPLIT > 1 ? NWG * 64 * FMB * FNB * 4 * 4 : 0;  // fp32 partial bytes
   uint16_t* ct = reinterpret_cast<uint16_t*>(smem + RED);
   block_barrier();
-  if constexpr (KSPLIT > 1) {
-    // Group 1 parks its accumulators in LDS ([block][register][thread] fp32), group 0 adds them.
+  // With two K groups, group 0 finishes row blocks [0, HB) and group 1 row blocks [HB, FMB): each
+  // parks the other's blocks in LDS ([block][register][thread] fp32),
+  // adds the blocks parked for it (a + b is the same float in either order) and moves them to
+  // acc[0, HB) (selects on the group with static indices, so the accumulators stay in registers).
+  // Both groups then write their blocks of the bf16 tile below, at row block i + kg * HB.
+  static_assert(KSPLIT <= 2, "two K groups at most");
+  constexpr int HB = KSPLIT == 2 ? (FMB + 1) / 2 : FMB;
+  if constexpr (KSPLIT == 2) {
     float* red = reinterpret_cast<float*>(smem);
     const int t0 = wr * 64 + lane;
-    if (kg == 1) {
+    const bool g0 = kg == 0;
 #pragma unroll
-      for (int i = 0; i < FMB; ++i)
+    for (int i = 0; i < HB; ++i) {
+      if (i + HB >= FMB && g0) continue;
+      const int blk = g0 ? i + HB : i;  // block parked: one the other group finishes
 #pragma unroll
-        for (int j = 0; j < FNB; ++j)
+      for (int j = 0; j < FNB; ++j)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) red[((i * FNB + j) * 4 + v) * (NWG * 64) + t0] = acc[i][j][v];
+        for (int v = 0; v < 4; ++v)
+          red[((blk * FNB + j) * 4 + v) * (NWG * 64) + t0] = (i + HB < FMB && g0) ? acc[i + HB < FMB ? i + HB : i][j][v] : acc[i][j][v];
     }
     __syncthreads();
-    if (kg == 0) {
 #pragma unroll
-      for (int i = 0; i < FMB; ++i)
+    for (int i = 0; i < HB; ++i) {
+      if (i + HB >= FMB && !g0) continue;
+      const int blk = g0 ? i : i + HB;  // block this group finishes
 #pragma unroll
-        for (int j = 0; j < FNB; ++j)
+      for (int j = 0; j < FNB; ++j)
 #pragma unroll
-          for (int v = 0; v < 4; ++v) acc[i][j][v] += red[((i * FNB + j) * 4 + v) * (NWG * 64) + t0];
+        for (int v = 0; v < 4; ++v) {
+          const float mine = (i + HB < FMB && !g0) ? acc[i + HB < FMB ? i + HB : i][j][v] : acc[i][j][v];
+          acc[i][j][v] = mine + red[((blk * FNB + j) * 4 + v) * (NWG * 64) + t0];
+        }
     }
   }
   if constexpr (WGM > 1 && KSPLIT == 1 && RED == 0 && BM * LDT * 2 <= TILE_BYTES) {
@@ -942,7 +955,8 @@ __device__ __forceinline__ void r16_epilogue(f32x4_t (&acc)[FMB][FNB], unsigned 
     // the last 288-row tile at M = 14.5 x 288): skip them (block-uniform, so the barriers still pair).
     if (m0 + h * WM >= M) break;
     if (h > 0) __syncthreads();
-    if (kg == 0 && wm == h) {
+    if (wm == h) {
+      const int rb0 = KSPLIT == 2 ? kg * HB : 0;  // row block of acc[0]
 #pragma unroll
       for (int j = 0; j < FNB; ++j) {
         const int cl = wn0 + j * 16 + 4 * (lane >> 4);
@@ -952,11 +966,12 @@ __device__ __forceinline__ void r16_epilogue(f32x4_t (&acc)[FMB][FNB], unsigned 
           b0 = lo_bf16(bw.x); b1 = hi_bf16(bw.x); b2 = lo_bf16(bw.y); b3 = hi_bf16(bw.y);
         }
 #pragma unroll
-        for (int i = 0; i < FMB; ++i) {
+        for (int i = 0; i < HB; ++i) {
+          if (rb0 + i >= FMB) continue;
           uint2 w;
           w.x = cvt_pk_bf16(acc[i][j][0] + b0, acc[i][j][1] + b1);
           w.y = cvt_pk_bf16(acc[i][j][2] + b2, acc[i][j][3] + b3);
-          *reinterpret_cast<uint2*>(ct + (i * 16 + (lane & 15)) * LDT + cl) = w;
+          *reinterpret_cast<uint2*>(ct + ((rb0 + i) * 16 + (lane & 15)) * LDT + cl) = w;
         }
       }
     }
