@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be loaded before the HIP library, see module docstring
 
 LIB_PATH = Path(__file__).resolve().parent / "liboudjat_hip.so"
-ABI_VERSION = 4
+ABI_VERSION = 5
 
 OK = 0
 STATUS_NAMES = {
@@ -88,6 +88,9 @@ SIGNATURES: dict[str, list] = {
                                       _i64, _p],
     "oudjat_nvfp4_quantize": [_p, _i64, _i64, _i64, _p, _p, _p, _p],
     "oudjat_nvfp4_dequantize": [_p, _p, _p, _i64, _i64, _p, _i64, _p],
+    "oudjat_query_attention_prob": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p, _p, _i64,
+                                    _i32, _p],
+    "oudjat_pseudo_query": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
 }
 _RESTYPES = {"oudjat_status_string": ctypes.c_char_p, "oudjat_last_error": ctypes.c_char_p}
 

@@ -783,17 +783,15 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
   dim3 grid((unsigned)n_wg, (unsigned)H, (unsigned)B);
   hipStream_t st = as_stream(stream);
   // Buffer-load kernel for Dh = 64 with >= 8 waves (its byte offsets must fit 31 bits); the
-  // register-staged kernel otherwise (or when OUDJAT_ATTN_STAGED is set, for comparisons).
-  const bool staged_forced = getenv("OUDJAT_ATTN_STAGED") != nullptr;
-  const bool dma = Dh == 64 && w >= 8 && !staged_forced && N * kvn * 2 < ((int64_t)1 << 31);
+  // register-staged kernel otherwise.
+  const bool dma = Dh == 64 && w >= 8 && N * kvn * 2 < ((int64_t)1 << 31);
   if (dma) {
     const size_t lds_dma = (size_t)kAttnStages * 2 * kKeyTile * 128;
     static_assert((size_t)kAttnStages * 2 * kKeyTile * 128 <= 64 * 1024, "needs no larger-LDS attribute");
     // One workgroup per (image, head) whose last query wave is light (1..16 queries): that wave is
     // split over kLightParts waves (its merge area, 3 parts of 18 x 64 floats, fits the stages).
     const int64_t last = T - (w - 1) * 32;
-    const int split = (n_wg == 1 && last >= 1 && last <= 16 && w - 1 + kLightParts <= kDmaMaxWaves &&
-                       getenv("OUDJAT_ATTN_NO_SPLIT") == nullptr) ? kLightParts : 0;
+    const int split = (n_wg == 1 && last >= 1 && last <= 16 && w - 1 + kLightParts <= kDmaMaxWaves) ? kLightParts : 0;
     static_assert((kLightParts - 1) * 18 * 64 * 4 <= kAttnStages * 2 * kKeyTile * 128, "merge area");
     const int threads = (split ? w - 1 + kLightParts : w) * 64;
     sq_attention_dma_kernel<kAttnStages><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,

@@ -1528,18 +1528,13 @@ static int ensure_gelu_table() {
   return status[dev];
 }
 
-static int env_int(const char* name, int dflt) {
-  const char* e = getenv(name);
-  return e ? atoi(e) : dflt;
-}
+// Rows of output tiles each XCD sweeps before moving to the next tile column (L2 reuse of the W panel).
+constexpr int kGroupM = 8;
 
 // aligned_io: C, resid 16-byte aligned with ldc, ldr % 8 == 0 and bias 8-byte aligned, which the
 // vector epilogues need; otherwise the register-staged kernel with 2-byte stores runs.
 static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
-  static const int forced = env_int("OUDJAT_GEMM_CFG", -1);
   if (!aligned_io) return 8;
-  if (forced >= 0 && forced < kNumCfgs && N % kCfgs[forced].bn == 0 && (kCfgs[forced].pf > -2 || K % kCfgs[forced].bk == 0))
-    return forced;
   // 256 x 256 pipelined tiles when their grid fills between half and all of the CUs in one round;
   // 128 x 128 direct-to-LDS tiles otherwise (two workgroups per CU balance a ragged second round
   // better); the register-staged kernel for N % 128 != 0.
@@ -1567,7 +1562,7 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
 static int choose_qkv_cfg(int64_t M, int64_t N, int64_t K, int64_t Dh) {
   int ci = choose_cfg(M, N, K, true);
   const int64_t tiles288n = cdiv(M, 288) * (N / 192);
-  if (env_int("OUDJAT_GEMM_CFG", -1) < 0 && N % 192 == 0 && tiles288n >= 192 && tiles288n <= 256 &&
+  if (N % 192 == 0 && tiles288n >= 192 && tiles288n <= 256 &&
       cdiv(M, kCfgs[ci].bm) * cdiv(N, kCfgs[ci].bn) < tiles288n)
     ci = 28;
   if (kCfgs[ci].pf > 0 || kCfgs[ci].bn % Dh != 0 || N % kCfgs[ci].bn != 0) ci = 11;  // 128 x 128 direct-to-LDS
@@ -1606,9 +1601,8 @@ static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t 
     }
   }
   const int threads = cfg.wgm * cfg.wgn * (cfg.pf <= -2 ? cfg.ks : 1) * 64;
-  static const int group_m = env_int("OUDJAT_GEMM_GROUP_M", 8);
   hipLaunchKernelGGL(fn, dim3((unsigned)tiles), dim3(threads), lds, stream, A, (int)M, (int)K, lda, W, (int)N, ldw, ea,
-                     C, ldc, group_m > 0 ? group_m : 1);
+                     C, ldc, kGroupM);
   return check_launch(what);
 }
 

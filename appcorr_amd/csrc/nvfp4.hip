@@ -11,8 +11,12 @@
 // rows x 4 blocks) are stored as 32x16 bytes: scale (r, j) of the tile goes to byte
 // (r % 32) * 16 + (r / 32) * 4 + j, tiles in row-major tile order. Scales of rows >= M are 0.
 //
-// Both conversions are integer/compare code written from the OCP 8-bit / MX e2m1 definitions, not
-// hardware converts, so the rounding is exactly the one stated above.
+// The e4m3 scale is encoded by integer code written from the OCP 8-bit definition. The e2m1 codes
+// come from gfx950's v_cvt_scalef32_pk_fp4_f32 (scale operand 1.0), whose rounding (nearest even,
+// saturating, -0 -> 0x8) was checked against an integer encoder written from the OCP MX definition
+// on the neighbourhood of every rounding boundary; blocks whose divisor is not a positive finite
+// value keep the integer encoder. Dequantize decodes with v_cvt_scalef32_pk_f32_fp4 (checked against
+// the e2m1 table for all 256 code bytes).
 #include "common.hpp"
 
 namespace oudjat {

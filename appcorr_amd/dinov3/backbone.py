@@ -101,11 +101,15 @@ def dinov3_backbone(name: str, *, depth: int | None = None, layerscale_init: flo
                      qkv_bias=qkv_bias, ffn_layer=ffn, layerscale_init=layerscale_init)
     if seed is not None:
         m.init_weights(torch.Generator().manual_seed(seed))
-    # Buffers such as RoPE periods stay fp32; parameters move to the serving dtype.
+    # Every floating parameter and buffer moves to the serving dtype, as the reference's
+    # `model.to(dtype=torch.bfloat16)` does (offload/server/model/dinov3_classifier.py:304;
+    # analysis/experiments/dinov3_correct_profile.py:60). That includes the RoPE `periods` buffer
+    # (rope_position_encoding.py:50-53): the tables are then computed in fp32 from bf16-rounded
+    # periods (rope_position_encoding.py:100), which is what the reference serves.
     for p in m.parameters():
         p.data = p.data.to(dtype)
-    for name_, buf in m.named_buffers():
-        if name_.endswith("bias_mask"):
+    for buf in m.buffers():
+        if buf.is_floating_point():
             buf.data = buf.data.to(dtype)
     return m.to(device) if device is not None else m
 

@@ -291,18 +291,25 @@ class SelfAttentionBlock(nn.Module):
         cache_feature[f"{tag}_blocks_out_sum"] = K.fused_layerscale_add(inc, mlp, ones).view(B, N, C)
         out = K.fused_layerscale_add(x_attn, mlp, ones).view(B, N, C)
         if server_pscore not in ("none", "disabled"):
-            cache_feature[f"{tag}_server_pscore"] = self._server_pscore(q.view(B, N, H, D), kv, server_pscore)
+            cache_feature[f"{tag}_server_pscore"] = self._server_pscore(q.view(B, N, H, D), kv, server_pscore,
+                                                                        N - prefix)
         return out, cache_feature
 
-    def _server_pscore(self, q: Tensor, kv: Tensor, kind: str) -> Tensor:
-        """cls_attn_prob (attention.py:267-271): softmax of the cls query over all keys, head mean.
-        Evaluated in fp32 on contiguous copies (a [B, H, 1, N] product per layer)."""
-        if kind not in ("cls_attn_prob", "cls_attn_prob_layermean"):
+    _PATCH_ATTN_PSCORES = frozenset({"patch_attn_prob", "patch_attn_prob_layermean"})
+    _PSEUDO_ATTN_PSCORES = frozenset({"patch_pseudo_attn_prob", "patch_pseudo_attn_prob_layermean"})
+
+    def _server_pscore(self, q: Tensor, kv: Tensor, kind: str, num_patches: int) -> Tensor:
+        """The approx pass's server score (attention.py:241-273) from the queries q [B, N, H, Dh] and the
+        cache kv [B, N, 2, H, Dh] (both after RoPE), with the reference's bf16 rounding points:
+          patch_pseudo_attn_prob(_layermean): softmax of the pseudo query (:254-261), bf16 [B, N];
+          any other kind (cls_attn_prob, cls_attn_prob_layermean, random: the reference's else branch,
+          :266-271): softmax of the cls query over all keys, mean over heads, fp32 [B, N]."""
+        if kind in self._PATCH_ATTN_PSCORES:
             raise NotImplementedError(f"server_pscore {kind!r} is not produced by this build's approx pass")
-        qc = q[:, 0].float().unsqueeze(2)                                    # [B, H, 1, D]
-        kk = kv[:, :, 0].float().permute(0, 2, 3, 1).contiguous()            # [B, H, D, N]
-        s = torch.matmul(qc, kk) * self.attn.scale
-        return s.softmax(-1).mean(dim=1).squeeze(1).to(torch.float32)
+        if kind in self._PSEUDO_ATTN_PSCORES:
+            qp = K.pseudo_query(q[:, q.shape[1] - num_patches:])
+            return K.query_attention_prob(qp, kv, self.attn.scale, out_dtype=torch.bfloat16)
+        return K.query_attention_prob(q[:, 0], kv, self.attn.scale)
 
     # -- plan bookkeeping (block.py:358-940) --------------------------------------------------------
 
@@ -623,5 +630,5 @@ def correct_blocks_packed(blocks, x: Tensor, dindice: Tensor, rope, cache_featur
             else:
                 x_p = K.packed_residual_persist(x_p, x_attn, mlp, qs.active_batch_idx, qs.active_token_idx, bos)
         bos_list.append(bos)
-    out = K.fold_residual_rows(xc, qs.row_slot, x_p, bos_list, out=xc if inplace else None)
+    out = K.fold_residual_rows(xc, qs.row_slot, x_p, bos_list, out=xc if inplace else None, ptr_holder=cache_feature)
     return out, cache_feature

@@ -5,6 +5,11 @@ Same parametrisation as the reference's RopePositionEmbedding in eval mode
 i < D/4, coordinates at patch centres normalised per axis ("separate") to [-1, 1], angles tiled to
 the full head dim. Tables are built once per (H, W) with torch on the target device (setup work,
 not part of the per-block path) and handed to every block as (sin, cos), each [H*W, Dh] fp32.
+
+`self.dtype` (fp32, the hub factories' `pos_embed_rope_dtype`) sets the dtype of the coordinates
+and of the tables; the `periods` buffer follows the module's dtype casts like any buffer, so a
+backbone served in bf16 divides by bf16-rounded periods, as the reference does
+(rope_position_encoding.py:47-53, 100).
 """
 
 from __future__ import annotations

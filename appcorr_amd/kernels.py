@@ -240,28 +240,38 @@ def packed_residual_persist_ln(x_act: torch.Tensor, x_attn: torch.Tensor, mlp: t
     return x_new, ln_out
 
 
-_PTR_ARRAYS: dict = {}
+POINTER_ARRAYS_KEY = "_oudjat_device_pointer_arrays"
 
 
-def _device_pointer_array(ptrs, device) -> torch.Tensor:
-    """Device int64 array of the given addresses, built once per distinct list (the per-layer cache
-    tensors of a session keep their addresses), so repeated calls copy nothing from the host and can
-    run inside a captured HIP graph."""
-    key = (str(device), tuple(ptrs))
-    t = _PTR_ARRAYS.get(key)
+def device_pointer_array(ptrs, device, holder: dict | None = None) -> torch.Tensor:
+    """Device int64 array of the given addresses.
+
+    With a `holder` (the session's cache dict, which owns the tensors the addresses point at) the
+    array is built once per distinct address list and kept in holder[POINTER_ARRAYS_KEY], so repeated
+    calls copy nothing from the host and can run inside a captured HIP graph: the array lives exactly
+    as long as the dict that keeps its tensors alive. An array is dropped only when the holder no
+    longer holds every tensor it points at (a graph recorded over those tensors could not be replayed
+    anyway). Without a holder a fresh array is copied from the host on every call."""
+    if holder is None:
+        return torch.tensor(list(ptrs), dtype=torch.int64).to(device)
+    store = holder.setdefault(POINTER_ARRAYS_KEY, {})
+    key = (str(device), tuple(int(p) for p in ptrs))
+    t = store.get(key)
     if t is None:
-        if len(_PTR_ARRAYS) > 256:
-            _PTR_ARRAYS.clear()
-        t = torch.tensor(list(ptrs), dtype=torch.int64).to(device)
-        _PTR_ARRAYS[key] = t
+        live = {v.data_ptr() for v in holder.values() if isinstance(v, torch.Tensor)}
+        for stale in [k for k in store if not set(k[1]) <= live]:
+            del store[stale]
+        t = torch.tensor(list(key[1]), dtype=torch.int64).to(device)
+        store[key] = t
     return t
 
 
 def fold_residual_rows(x: torch.Tensor, row_slot: torch.Tensor, x_packed: torch.Tensor, blocks_out_sums,
-                       out: torch.Tensor | None = None) -> torch.Tensor:
+                       out: torch.Tensor | None = None, ptr_holder: dict | None = None) -> torch.Tensor:
     """x [B, N, C] after a run of correction blocks whose selected rows stayed packed: selected rows from
     x_packed [M, C] (row_slot [B, N] int32 maps a token to its packed row), the other rows
-    x + bos_0 + ... + bos_{L-1} with a bf16 rounding after each addition. `out` may alias x."""
+    x + bos_0 + ... + bos_{L-1} with a bf16 rounding after each addition. `out` may alias x.
+    `ptr_holder`: the dict owning the blocks_out_sum tensors (see device_pointer_array)."""
     _require_cuda(x, row_slot, x_packed, out, *blocks_out_sums)
     _require(x.dtype == torch.bfloat16 and x.is_contiguous() and x.dim() == 3, "fold_residual_rows: x [B, N, C] bf16")
     for b in blocks_out_sums:
@@ -273,7 +283,7 @@ def fold_residual_rows(x: torch.Tensor, row_slot: torch.Tensor, x_packed: torch.
              "fold_residual_rows: x_packed must be contiguous bf16 [M, C]")
     if out is None:
         out = torch.empty_like(x)
-    ptrs = _device_pointer_array([b.data_ptr() for b in blocks_out_sums] or [0], x.device)
+    ptrs = device_pointer_array([b.data_ptr() for b in blocks_out_sums] or [0], x.device, ptr_holder)
     C = x.shape[2]
     _launch("fold", x, "oudjat_fold_residual_rows", _ptr(x), x.numel() // C, C, _ptr(row_slot), _ptr(x_packed),
             _ptr(ptrs), len(blocks_out_sums), _ptr(out), _stream(x))
@@ -500,6 +510,54 @@ def sparse_query_attention(q: torch.Tensor, kv_cache: torch.Tensor, T: int, scal
     _launch("attention", q, "oudjat_sparse_query_attention", _ptr(q), q.stride(0), B, T, H, Dh, _ptr(kv_cache), kv_cache.stride(0),
          kv_cache.stride(1), kv_cache.stride(2), kv_cache.stride(3), N, float(scale), _ptr(out), out.stride(0),
          _stream(q))
+    return out
+
+
+# ------------------------------------------------------------------------------------------------
+# Server scores of the approximate pass (attention.py:246-273)
+# ------------------------------------------------------------------------------------------------
+
+
+def _kv_k_view_ok(kv_cache: torch.Tensor) -> None:
+    _require(kv_cache.dim() == 5 and kv_cache.shape[2] == 2 and kv_cache.stride(4) == 1
+             and kv_cache.dtype == torch.bfloat16, "pscore: kv_cache must be [B, N, 2, H, Dh] bf16 with packed heads")
+
+
+def query_attention_prob(q: torch.Tensor, kv_cache: torch.Tensor, scale: float, *, out_dtype=torch.float32,
+                         workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """mean_h softmax_n(bf16(bf16(q[b, h] . K[b, n, h]) * scale)) with torch's bf16 rounding points ->
+    [B, N] (attention.py:267-271 with q = the cls query; :260-261 with the pseudo query).
+
+    q [B, H, Dh] (any strides with a contiguous head dim), kv_cache [B, N, 2, H, Dh] (K after RoPE).
+    out_dtype float32 (cls_attn_prob) or bfloat16 (the pseudo score); the values are bf16 either way.
+    `workspace` (fp32, >= B*H*N elements) is scratch; one is allocated when not given."""
+    _require_cuda(q, kv_cache, workspace)
+    _kv_k_view_ok(kv_cache)
+    B, N, _, H, Dh = kv_cache.shape
+    _require(q.dim() == 3 and q.shape == (B, H, Dh) and q.stride(2) == 1 and q.dtype == torch.bfloat16,
+             "query_attention_prob: q must be [B, H, Dh] bf16 with a contiguous head dim")
+    _require(out_dtype in (torch.float32, torch.bfloat16), "query_attention_prob: out_dtype fp32 or bf16")
+    if workspace is None:
+        workspace = torch.empty((B * H * N,), device=q.device, dtype=torch.float32)
+    _require(workspace.dtype == torch.float32 and workspace.is_contiguous() and workspace.numel() >= B * H * N,
+             "query_attention_prob: workspace must be contiguous fp32 with B*H*N elements")
+    out = torch.empty((B, N), device=q.device, dtype=out_dtype)
+    _launch("pscore", q, "oudjat_query_attention_prob", _ptr(q), q.stride(0), q.stride(1), B, H, Dh, _ptr(kv_cache),
+            kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(3), N, float(scale), _ptr(workspace), _ptr(out),
+            N, int(out_dtype == torch.bfloat16), _stream(q))
+    return out
+
+
+def pseudo_query(q_patch: torch.Tensor) -> torch.Tensor:
+    """The pseudo query of patch_pseudo_attn_prob (attention.py:254-259): q_patch [B, P, H, Dh] (patch
+    queries after RoPE, any strides with a contiguous head dim) -> [B, H, Dh] bf16."""
+    _require_cuda(q_patch)
+    _require(q_patch.dim() == 4 and q_patch.dtype == torch.bfloat16 and q_patch.stride(3) == 1,
+             "pseudo_query: q_patch must be [B, P, H, Dh] bf16 with a contiguous head dim")
+    B, P, H, Dh = q_patch.shape
+    out = torch.empty((B, H, Dh), device=q_patch.device, dtype=torch.bfloat16)
+    _launch("pscore", q_patch, "oudjat_pseudo_query", _ptr(q_patch), q_patch.stride(0), q_patch.stride(1),
+            q_patch.stride(2), B, P, H, Dh, _ptr(out), _stream(q_patch))
     return out
 
 

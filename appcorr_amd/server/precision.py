@@ -5,10 +5,10 @@ Mirrors DINOv3CorrectPrecisionController / DINOv3ApproxPrecisionController
 calls its `correct` / `approx` without autograd, and keeps the public contract that activations and
 the K/V cache leave the block as bf16 (:972-985); `event_metadata` reports the route taken.
 
-Precision: the correction GEMMs run in bf16 on MFMA. fp8 / fp4 requests are accepted and, as in the
-reference when its low-precision linears are unavailable (:724-732, 906-910), fall back to bf16 with
-the reason recorded in the route metadata: this build has no NVFP4 / FP8 scaled GEMM consumer on
-gfx950 (only the NVFP4 activation quantize / dequantize kernels).
+Precision: the correction GEMMs run in bf16 on MFMA. An explicit `correct_precision` of "fp8" or
+"fp4" whose low-precision path is unavailable raises RuntimeError at construction, as the
+reference's `_handle_fp8_unavailable` / `_handle_fp4_unavailable` do (:723-731); "bf16" and "auto"
+run bf16.
 """
 
 from __future__ import annotations
@@ -33,10 +33,16 @@ class DINOv3CorrectPrecisionController:
         self.fp4_proj_precision = str(fp4_proj_precision)
         self.bucket_rows = max(0, int(bucket_rows))
         self.unavailable_reason = None
-        if precision in ("fp8", "fp4"):
-            self.unavailable_reason = (f"{precision} correction GEMMs are not part of this build "
-                                       "(no block-scaled FP4/FP8 MFMA consumer); running bf16")
         self._event_routes: Dict[str, tuple[str, int]] = {}
+        if precision in ("fp8", "fp4"):
+            self._handle_unavailable(precision, f"{precision} correction linears are not part of this build")
+
+    def _handle_unavailable(self, precision: str, reason: str) -> None:
+        """Record why a low-precision path is unavailable; an explicit request for it is an error
+        (dinov3_precision.py:723-731)."""
+        self.unavailable_reason = reason
+        if self.precision == precision:
+            raise RuntimeError(f"correct_precision={precision!r} is unavailable: {reason}")
 
     @classmethod
     def from_config(cls, blocks: nn.ModuleList, config: Any, device: torch.device):

@@ -223,12 +223,42 @@ int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K, int64_t l
  *   out[b*T + t, h*Dh:(h+1)*Dh] = softmax(q . K^T * scale) . V over ALL N cached keys, no mask.
  * q [B*T, H, Dh] packed (row stride q_row_stride); K = kv[b, n, 0, h, :], V = kv[b, n, 1, h, :]
  * addressed as b*kv_stride_b + n*kv_stride_n + {0|1}*kv_stride_kv + h*kv_stride_h.
- * Replaces F.scaled_dot_product_attention over the cache (attention.py:456-532). Dh == 64. */
+ * Replaces F.scaled_dot_product_attention over the cache (attention.py:456-532). Dh in {64, 128};
+ * 16-byte aligned q and kv rows. */
 int oudjat_sparse_query_attention(const uint16_t* q, int64_t q_row_stride, int64_t B, int64_t T,
                                   int64_t H, int64_t Dh, const uint16_t* kv, int64_t kv_stride_b,
                                   int64_t kv_stride_n, int64_t kv_stride_kv, int64_t kv_stride_h,
                                   int64_t N, float scale, uint16_t* out, int64_t out_row_stride,
                                   oudjat_stream_t stream);
+
+/* Approximate-pass server score with one query per (image, head) -- cls_attn_prob and, with the
+ * pseudo query of oudjat_pseudo_query, patch_pseudo_attn_prob (the cache producer,
+ * appcorr/models/dinov3/layers/attention.py:254-273):
+ *   s[b,h,n] = bf16(bf16(q[b,h] . K[b,n,h]) * scale); p = bf16(softmax_n(s)) (fp32 max, exp, sum and
+ *   division); out[b, n] = bf16(fl(sum_h p[b,h,n]) * fl(1/H))
+ * -- the rounding points of torch's bf16 matmul, scalar multiply, softmax and mean. Each fp32
+ * accumulation and exponential is evaluated exactly (float64, one rounding), so the result is
+ * deterministic. q[b, h, :] at q + b*q_stride_b + h*q_stride_h; K[b, n, h, :] at
+ * k + b*k_stride_b + n*k_stride_n + h*k_stride_h (the K half of the {tag}_kv cache, K after RoPE).
+ * workspace: B*H*N fp32 (the per-head probabilities; its contents are not used after the call).
+ * out: [B, N] at row stride out_stride_b, fp32 (out_bf16 = 0, cls_attn_prob's .to(float32)) or bf16
+ * bits (out_bf16 = 1, the pseudo score's bf16 tensor). Dh in {64, 128}; N <= 8192; 16-byte aligned
+ * q and K rows. */
+int oudjat_query_attention_prob(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, int64_t B,
+                                int64_t H, int64_t Dh, const uint16_t* k, int64_t k_stride_b,
+                                int64_t k_stride_n, int64_t k_stride_h, int64_t N, float scale,
+                                float* workspace, void* out, int64_t out_stride_b, int out_bf16,
+                                oudjat_stream_t stream);
+
+/* The pseudo query of patch_pseudo_attn_prob (attention.py:254-259) for every (image b, head h)
+ * from the P patch queries q[b, t, h, :] at q + b*q_stride_b + t*q_stride_t + h*q_stride_h (after
+ * RoPE), with torch's bf16 rounding points (mean, vector norm, clamp_min(bf16 eps), division,
+ * product; accumulations exact):
+ *   q_mean = bf16(mean_t q_t); qmn = max(bf16(|q_mean|), 2^-7); target = bf16(mean_t bf16(|q_t|))
+ *   out[b, h, :] = bf16(q_mean * bf16(target / qmn))          out: [B, H, Dh] bf16 contiguous.
+ * Dh in {64, 128}; 16-byte aligned rows. */
+int oudjat_pseudo_query(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_t, int64_t q_stride_h,
+                        int64_t B, int64_t P, int64_t H, int64_t Dh, uint16_t* out, oudjat_stream_t stream);
 
 /* Introspection, no counterpart in the reference: writes to buf (NUL-terminated) the demangled name,
  * as rocprofv3 prints it, of the kernel oudjat_linear_bf16 launches for an M x N x K product with

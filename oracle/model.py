@@ -166,12 +166,26 @@ def full_dindice(cfg: ViTConfig, B: int) -> torch.Tensor:
 # ------------------------------------------------------------------------------------------------
 
 
-def rope_tables(cfg: ViTConfig, H: int | None = None, W: int | None = None):
+def rope_periods(cfg: ViTConfig, periods_dtype: torch.dtype = torch.bfloat16) -> torch.Tensor:
+    """base^(2i / (D/2)) for i < D/4, computed in fp32 (rope_position_encoding.py:110-113) and then
+    held in the serving dtype: the reference casts the whole model, this persistent buffer
+    included, with `model.to(dtype=torch.bfloat16)` (offload/server/model/dinov3_classifier.py:304;
+    analysis/experiments/dinov3_correct_profile.py:60) after init_weights. fp32 `periods_dtype`
+    gives the uncast module's periods."""
+    D = cfg.head_dim
+    p = cfg.rope_base ** (2 * torch.arange(D // 4, dtype=torch.float32) / (D // 2))
+    return p.to(periods_dtype)
+
+
+def rope_tables(cfg: ViTConfig, H: int | None = None, W: int | None = None,
+                periods_dtype: torch.dtype = torch.bfloat16):
+    """(sin, cos) [H*W, Dh] fp32 (rope_position_encoding.py:57-106): coordinates and angles in fp32,
+    divided by the periods held in `periods_dtype` (bf16 for a bf16-served model), which fp32
+    division promotes exactly to fp32 (:100)."""
     H = cfg.grid if H is None else H
     W = cfg.grid if W is None else W
-    D = cfg.head_dim
     dt = torch.float32
-    periods = cfg.rope_base ** (2 * torch.arange(D // 4, dtype=dt) / (D // 2))
+    periods = rope_periods(cfg, periods_dtype)
     coords_h = torch.arange(0.5, H, dtype=dt) / H
     coords_w = torch.arange(0.5, W, dtype=dt) / W
     coords = torch.stack(torch.meshgrid(coords_h, coords_w, indexing="ij"), dim=-1).flatten(0, 1)
@@ -310,7 +324,33 @@ def _mlp(ops, cfg: ViTConfig, blk: dict, x):
 # ------------------------------------------------------------------------------------------------
 
 
-def approx_block(cfg: ViTConfig, blk: dict, x: torch.Tensor, rope, cache: dict, tag: str, mode: str = "f64"):
+def server_score(kind: str, q: torch.Tensor, k: torch.Tensor, num_patches: int, scale: float) -> torch.Tensor:
+    """The approx pass's {tag}_server_pscore (attention.py:241-273) from q, k [B, N, H, D] bf16 (after
+    RoPE), with the reference's dispatch: patch_attn_prob(_layermean) -> dense mean over heads and
+    queries (bf16 [B, N]; the layer-mean kind takes the fused fp32 key-side kernel's value for 32 heads
+    of 128, attention.py:241-250 and attention_pscore.py:104-120); patch_pseudo_attn_prob(_layermean)
+    -> the pseudo query's probabilities (bf16 [B, N]); every other kind -> cls_attn_prob (fp32 [B, N])."""
+    from . import pscore as PS
+
+    qn = q.float().numpy()
+    kn = k.float().numpy()
+    B, N, H, D = q.shape
+    if kind in ("patch_attn_prob", "patch_attn_prob_layermean"):
+        qh = np.ascontiguousarray(qn.transpose(0, 2, 1, 3))
+        if kind == "patch_attn_prob_layermean" and H == 32 and D == 128 and 0 < N <= 4096:
+            return torch.from_numpy(PS.patch_attn_prob_fused(qh, kn, scale)).to(torch.bfloat16)
+        return torch.from_numpy(PS.patch_attn_prob(qh, kn, scale)).to(torch.bfloat16)
+    if kind in ("patch_pseudo_attn_prob", "patch_pseudo_attn_prob_layermean"):
+        qp = PS.pseudo_query(np.ascontiguousarray(qn[:, N - num_patches:].transpose(0, 2, 1, 3)))
+        return torch.from_numpy(PS.query_attention_prob(qp, kn, scale)).to(torch.bfloat16)
+    return torch.from_numpy(PS.query_attention_prob(np.ascontiguousarray(qn[:, 0]), kn, scale))
+
+
+def approx_block(cfg: ViTConfig, blk: dict, x: torch.Tensor, rope, cache: dict, tag: str, mode: str = "f64",
+                 server_pscore: str = "none"):
+    """One approximate-pass block (the cache producer): {tag}_kv, {tag}_blocks_out_sum and, unless
+    server_pscore is "none"/"disabled" (block.py:317-319 maps a zero server weight to "none"), the
+    server score {tag}_server_pscore (attention.py:241-273)."""
     ops = _MODES[mode]
     B, N, C = x.shape
     H, D = cfg.heads, cfg.head_dim
@@ -324,6 +364,8 @@ def approx_block(cfg: ViTConfig, blk: dict, x: torch.Tensor, rope, cache: dict, 
     k = torch.cat([k[:, :prefix], rope_rotate(k[:, prefix:], sin[None, :, None], cos[None, :, None])], dim=1)
     kv[:, :, 0] = k
     cache[f"{tag}_kv"] = kv
+    if server_pscore not in ("none", "disabled"):
+        cache[f"{tag}_server_pscore"] = server_score(server_pscore, q, k, sin.shape[0], D ** -0.5)
     attn = ops.sdpa(q.transpose(1, 2), k.transpose(1, 2), v.transpose(1, 2), D ** -0.5)
     attn = attn.transpose(1, 2).reshape(B, N, C)
     inc = ops.mul(ops.linear(attn, blk["attn.proj.weight"], blk["attn.proj.bias"]), blk["ls1.gamma"])
@@ -334,10 +376,10 @@ def approx_block(cfg: ViTConfig, blk: dict, x: torch.Tensor, rope, cache: dict, 
     return ops.add(x_attn, mlp), cache
 
 
-def approx_pass(cfg: ViTConfig, blocks: list, x: torch.Tensor, rope, mode: str = "f64"):
+def approx_pass(cfg: ViTConfig, blocks: list, x: torch.Tensor, rope, mode: str = "f64", server_pscore: str = "none"):
     cache: dict = {}
     for i, blk in enumerate(blocks):
-        x, cache = approx_block(cfg, blk, x, rope, cache, f"layer{i}", mode)
+        x, cache = approx_block(cfg, blk, x, rope, cache, f"layer{i}", mode, server_pscore)
     return x, cache
 
 
@@ -396,7 +438,9 @@ def correct_block(cfg: ViTConfig, blk: dict, x: torch.Tensor, plan, rope, cache:
 
 def correct_pass(cfg: ViTConfig, blocks: list, x: torch.Tensor, plan, rope, cache: dict, mode: str = "f64"):
     """All blocks with one plan (the plan is cached across layers whenever the score does not depend
-    on the layer, block.py:709-727; true for the mobile-hint score with server weight 0)."""
+    on the layer, block.py:709-727; true for the mobile-hint score with server weight 0), or with one
+    plan per block when `plan` is a list (a per-layer server score such as cls_attn_prob)."""
+    plans = list(plan) if isinstance(plan, (list, tuple)) else [plan] * len(blocks)
     for i, blk in enumerate(blocks):
-        x, cache = correct_block(cfg, blk, x, plan, rope, cache, f"layer{i}", mode)
+        x, cache = correct_block(cfg, blk, x, plans[i], rope, cache, f"layer{i}", mode)
     return x, cache

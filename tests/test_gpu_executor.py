@@ -1,0 +1,165 @@
+"""Executor-level parity: the worker's call sequence on DINOv3ClassifierExecutor against the oracle.
+
+preprocess -> prepare_tokens -> approx_forward (base images) -> preprocess -> prepare_tokens ->
+correct_forward (full-resolution images), as offload/server/model/dinov3_classifier.py:330-663 runs
+them. The oracle gets the executor's own layer-0 tokens (patch embedding is plumbing, not the path),
+builds its own RoPE tables from bf16 periods, runs its approx pass and its correction pass, and the
+results are compared:
+
+  * RoPE tables: the executor's (torch on the GPU from the bf16 periods buffer) equal the oracle's
+    within fp32 sin/cos rounding;
+  * mobile-hint plan (server weight 0; the packed run): top-k indices bit-exact, corrected tokens
+    within the north-star tolerance (2e-2 max abs, 1e-3 mean abs) at the reference init, and within a
+    relative bound with LayerScale 1 (every block's increment at full size);
+  * default per-layer plan (cls_attn_prob, weight 1): each layer's server score agrees with the
+    oracle's to bf16 rounding (the two approx passes drift apart only by accumulation order), the plan
+    is the bit-exact top-k of the executor's own score, and the corrected tokens match an oracle pass
+    run with those plans.
+"""
+
+import numpy as np
+import pytest
+import torch
+
+from appcorr_amd.server.dinov3_classifier import DINOv3ClassifierExecutor, make_group_plan
+from appcorr_amd.server.protocol import ExperimentConfig
+from oracle import model as OM
+from oracle import plan as OP
+from tests.util import assert_bits_equal, close_stats
+
+pytestmark = pytest.mark.gpu
+
+BACKBONE = {"vits16_224": "vits16", "vitl16_512": "vitl16"}
+
+
+def _executor(key, B, weights, dev, appcorr_kwargs):
+    cfg = OM.CONFIGS[key]
+    name = BACKBONE[key]
+    config = ExperimentConfig(model_name=f"dinov3_classifier_{name}", batch_size=B,
+                              image_shape=(cfg.img_size, cfg.img_size, 3), backbone=name,
+                              appcorr_kwargs=appcorr_kwargs)
+    ex = DINOv3ClassifierExecutor(dev)
+    ex.load_model(config.model_name, config)
+    for blk, w in zip(ex.model.blocks, weights):
+        blk.load_state_dict(w, strict=True)
+    return ex, config
+
+
+def _images(cfg, B, seed):
+    g = torch.Generator().manual_seed(seed)
+    base = torch.rand(B, 3, cfg.img_size, cfg.img_size, generator=g)
+    full = (base + 0.05 * torch.randn(base.shape, generator=g)).clamp(0, 1)
+    return base, full
+
+
+def _run(key, B, depth, ratio, dev, appcorr_kwargs, gamma, hint_seed=5):
+    cfg = OM.CONFIGS[key]
+    weights = OM.make_block_weights(cfg, 0, gamma=gamma, bias_std=0.05 if gamma == 1.0 else 0.0,
+                                    ln_std=0.1 if gamma == 1.0 else 0.0, depth=depth)
+    ex, config = _executor(key, B, weights, dev, appcorr_kwargs)
+    base, full = _images(cfg, B, 1)
+    ctx = {}
+    with torch.no_grad():
+        ex.preprocess(base, None, ctx, config)
+        ex.prepare_tokens(None, ctx, config)
+        tok_base = ctx["input_tokens"].clone()
+        ex.approx_forward({"layers": (0, depth)}, ctx, config)
+        approx_cache = {k: v.clone() for k, v in ctx["cache_feature"].items() if torch.is_tensor(v)}
+        ex.preprocess(full, None, ctx, config)
+        ex.prepare_tokens(None, ctx, config)
+        tok_full = ctx["input_tokens"].clone()
+        dind = torch.arange(cfg.num_tokens, device=dev).unsqueeze(0).expand(B, -1).contiguous()
+        ctx["group_plans"] = {1: make_group_plan(dind, cfg.num_pretokens)}
+        hint = torch.rand(B, cfg.num_patches, generator=torch.Generator().manual_seed(hint_seed)).to(dev)
+        ctx["mobile_pscore_hint_map"] = hint
+        ex.correct_forward({"layers": (0, depth), "group_id": 1}, ctx, config)
+    torch.cuda.synchronize()
+    return cfg, weights, ctx, tok_base.cpu(), tok_full.cpu(), approx_cache, hint.cpu(), dind.cpu()
+
+
+def _check_rope(cfg, ctx):
+    s, c = ctx["rope_sincos"]
+    s_ref, c_ref = OM.rope_tables(cfg)
+    assert float((s.cpu() - s_ref).abs().max()) <= 1e-6 and float((c.cpu() - c_ref).abs().max()) <= 1e-6
+
+
+@pytest.mark.parametrize("key,B,depth,ratio,gamma", [
+    ("vits16_224", 1, 12, 0.5, None),
+    ("vits16_224", 1, 12, 0.5, 1.0),
+    ("vitl16_512", 2, 2, 0.25, 1.0),
+])
+def test_executor_mobile_hint_plan(dev, key, B, depth, ratio, gamma):
+    print(f"executor mobile-hint {key} B={B} depth={depth} keep={ratio} gamma={gamma}", flush=True)
+    kw = {"method": "partial_token", "token_keep_ratio": ratio, "mobile_pscore": "residual_energy",
+          "mobile_pscore_weight": 1.0, "server_pscore_weight": 0.0, "pscore_fusion": "add"}
+    cfg, weights, ctx, tok_base, tok_full, _, hint, dind = _run(key, B, depth, ratio, dev, kw, gamma)
+    _check_rope(cfg, ctx)
+    rope = OM.rope_tables(cfg)
+    _, cache = OM.approx_pass(cfg, weights, tok_base, rope)
+    k = OP.keep_count(cfg.num_patches, ratio)
+    plan = OP.build_plan(hint.numpy(), k, dind.numpy(), cfg.num_pretokens, cfg.num_tokens)
+    x_ref, cache_ref = OM.correct_pass(cfg, weights, tok_full, plan, rope, cache)
+    gplan = next(iter(ctx["cache_feature"]["_partial_token_query_plan_cache"].values()))
+    assert_bits_equal(gplan.update_indice, plan.update_indice, "top-k indices")
+    x = ctx["current_feature"]
+    mx, mean = close_stats(x, x_ref)
+    print(f"  gpu vs fp64 oracle: max {mx:.4g} mean {mean:.4g}", flush=True)
+    if gamma is None:   # reference init
+        assert mx <= 2e-2 and mean <= 1e-3, (mx, mean)
+        return
+    # LayerScale 1: every block's increment enters at full size and rounding differences compound over
+    # the blocks. The yardstick is the reference's own op sequence in bf16 (torch's CPU kernels, the
+    # oracle's "bf16" mode) on the same inputs: the GPU may drift from the fp64 oracle at most twice as
+    # far as that does (and never beyond 2 % of the mean magnitude), for the tokens and every layer's
+    # rewritten K/V cache.
+    _, cache16 = OM.approx_pass(cfg, weights, tok_base, rope, mode="bf16")
+    x16, cache16 = OM.correct_pass(cfg, weights, tok_full, plan, rope, cache16, mode="bf16")
+    mx16, mean16 = close_stats(x16, x_ref)
+    scale = float(x_ref.float().abs().mean())
+    print(f"  bf16 eager vs fp64 oracle: max {mx16:.4g} mean {mean16:.4g}; mean|x| {scale:.4g}", flush=True)
+    assert mean <= 2.0 * mean16 and mean <= 0.02 * scale, f"x_out mean {mean:.4g} vs eager {mean16:.4g}"
+    assert mx <= 2.0 * mx16 + 2.0 ** -6 * float(x_ref.float().abs().max()), f"x_out max {mx:.4g} vs eager {mx16:.4g}"
+    for i in range(depth):
+        kv_ref = cache_ref[f"layer{i}_kv"]
+        mk, mnk = close_stats(ctx["cache_feature"][f"layer{i}_kv"], kv_ref)
+        mk16, mnk16 = close_stats(cache16[f"layer{i}_kv"], kv_ref)
+        kscale = float(kv_ref.float().abs().mean())
+        assert mnk <= 2.0 * mnk16 + 2.0 ** -10 * kscale, f"layer {i} K/V mean {mnk:.4g} vs eager {mnk16:.4g}"
+        assert mk <= 2.0 * mk16 + 2.0 ** -6 * float(kv_ref.float().abs().max()), f"layer {i} K/V max {mk:.4g}"
+
+
+@pytest.mark.parametrize("key,B,depth,ratio", [("vits16_224", 1, 12, 0.5), ("vitl16_512", 2, 2, 0.25)])
+def test_executor_default_per_layer_plan(dev, key, B, depth, ratio):
+    print(f"executor cls_attn_prob {key} B={B} depth={depth} keep={ratio}", flush=True)
+    kw = {"method": "partial_token", "token_keep_ratio": ratio, "server_pscore": "cls_attn_prob",
+          "server_pscore_weight": 1.0}
+    cfg, weights, ctx, tok_base, tok_full, approx_cache, _, dind = _run(key, B, depth, ratio, dev, kw, 1.0)
+    rope = OM.rope_tables(cfg)
+    _, cache = OM.approx_pass(cfg, weights, tok_base, rope, server_pscore="cls_attn_prob")
+    k = OP.keep_count(cfg.num_patches, ratio)
+    plans, overlap = [], []
+    for i in range(depth):
+        g = approx_cache[f"layer{i}_server_pscore"].cpu()
+        r = cache[f"layer{i}_server_pscore"]
+        assert g.dtype == r.dtype == torch.float32
+        d = (g - r).abs()
+        assert float(d.max()) <= 2.0 ** -6 * float(r.abs().max()) and float(d.mean()) <= 2.0 ** -9 * float(r.abs().mean())
+        gp = OP.build_plan(g[:, 5:].numpy(), k, dind.numpy(), cfg.num_pretokens, cfg.num_tokens)
+        rp = OP.build_plan(r[:, 5:].numpy(), k, dind.numpy(), cfg.num_pretokens, cfg.num_tokens)
+        overlap.append(float((gp.keep_mask & rp.keep_mask).sum()) / max(1, int(rp.keep_mask.sum())))
+        plans.append(gp)
+    assert min(overlap) >= 0.9, overlap
+    # the executor's plans are the exact top-k of its own scores: rerun the oracle with them
+    cache_in = {kk: v for kk, v in cache.items() if not kk.endswith("_server_pscore")}
+    x_ref, _ = OM.correct_pass(cfg, weights, tok_full, plans, rope, cache_in)
+    x = ctx["current_feature"]
+    mx, mean = close_stats(x, x_ref)
+    # yardstick: the reference's own bf16 op sequence (torch CPU kernels) with the same plans
+    _, cache16 = OM.approx_pass(cfg, weights, tok_base, rope, mode="bf16")
+    x16, _ = OM.correct_pass(cfg, weights, tok_full, plans, rope, cache16, mode="bf16")
+    mx16, mean16 = close_stats(x16, x_ref)
+    scale = float(x_ref.float().abs().mean())
+    print(f"  gpu vs fp64: max {mx:.4g} mean {mean:.4g}; bf16 eager vs fp64: max {mx16:.4g} mean {mean16:.4g}; "
+          f"mean|x| {scale:.4g}; kept-set overlap {min(overlap):.4f}", flush=True)
+    assert mean <= 2.0 * mean16 and mean <= 0.02 * scale, (mean, mean16, scale)
+    assert mx <= 2.0 * mx16 + 2.0 ** -6 * float(x_ref.float().abs().max()), (mx, mx16)

@@ -49,21 +49,25 @@ def _check_gemm(dev, got, x, w, b, what):
 
 
 @pytest.mark.parametrize("M,N,Kd", [(4176, 3072, 1024), (4176, 1024, 1024), (4176, 4096, 1024), (4176, 1024, 4096),
-                                    (103, 1152, 384), (1, 64, 64), (130, 192, 128), (1656, 8192, 4096)])
+                                    (103, 1152, 384), (1, 64, 64), (130, 192, 128), (1656, 8192, 4096),
+                                    (1712, 3072, 1024), (1712, 4096, 1024), (8272, 3072, 1024), (8272, 4096, 1024),
+                                    (1656, 12288, 4096), (1656, 4096, 4096), (1656, 4096, 8192)])
 def test_linear_bias(dev, M, N, Kd):
     x, w, b = _rand((M, Kd), 1), _rand((N, Kd), 2, 0.02), _rand((N,), 3, 0.1)
     got = K.linear(x.to(dev), w.to(dev), b.to(dev))
     _check_gemm(dev, got, x, w, b, f"linear {M}x{N}x{Kd}")
 
 
-def test_linear_split_k_repeatable(dev):
-    """N = 1024 GEMMs run split over K (68 tiles of 256 x 256 on 256 CUs); the partial tiles are
-    summed in split order, so repeated launches are bit-identical and the arrival counters reset."""
+@pytest.mark.parametrize("M", [1712, 4176, 8272])
+def test_linear_repeatable_at_keep_ratios(dev, M):
+    """The N = C projections (proj K = C, fc2 K = 4C) at the ViT-L row counts of keep 10 / 25 / 50 %
+    (M = 16 (5 + k)): within the accumulation bound of the fp64 oracle, and repeated launches are
+    bit-identical (fixed summation order, no atomics)."""
     for Kd in (1024, 4096):
-        x, w, b = _rand((4176, Kd), 30), _rand((1024, Kd), 31, 0.02), _rand((1024,), 32, 0.1)
+        x, w, b = _rand((M, Kd), 30), _rand((1024, Kd), 31, 0.02), _rand((1024,), 32, 0.1)
         xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
         outs = [K.linear(xd, wd, bd) for _ in range(3)]
-        _check_gemm(dev, outs[0], x, w, b, f"split-K {Kd}")
+        _check_gemm(dev, outs[0], x, w, b, f"N=C GEMM {M}x1024x{Kd}")
         for o in outs[1:]:
             assert_bits_equal(o, outs[0], "repeat")
 
@@ -179,7 +183,8 @@ def test_qkv_rope_kv_scatter_bit_exact(dev, B, T, H, D):
     assert_bits_equal(kvd, kv_ref, "kv cache")
 
 
-@pytest.mark.parametrize("B,T,H,D,Kd", [(16, 261, 16, 64, 1024), (1, 103, 6, 64, 384), (2, 50, 32, 128, 512)])
+@pytest.mark.parametrize("B,T,H,D,Kd", [(16, 261, 16, 64, 1024), (1, 103, 6, 64, 384), (2, 50, 32, 128, 512),
+                                        (16, 107, 16, 64, 1024), (16, 517, 16, 64, 1024), (4, 414, 32, 128, 4096)])
 def test_linear_qkv_rope_kv_fused_equals_unfused(dev, B, T, H, D, Kd):
     """The fused QKV GEMM (qkv never materialised). Its raw bf16(acc + bias) values, taken from a run
     with no patch rows (no RoPE), are checked against the fp64 oracle like every GEMM; the pinned
@@ -243,33 +248,23 @@ def test_sparse_query_attention(dev, B, T, N, H, D):
 
 
 @pytest.mark.parametrize("B,T,N,H,scale_up", [(16, 261, 1029, 16, 1.0), (2, 300, 777, 4, 1.0), (1, 256, 64, 3, 1.0),
-                                               (2, 260, 65, 2, 1.0), (2, 261, 300, 2, 8.0)])
-def test_attention_buffer_load_kernel_equals_staged(dev, B, T, N, H, scale_up, monkeypatch):
+                                               (2, 260, 65, 2, 1.0), (2, 261, 300, 2, 8.0), (16, 107, 1029, 16, 1.0),
+                                               (16, 517, 1029, 16, 1.0)])
+def test_attention_buffer_load_kernel_shapes(dev, B, T, N, H, scale_up):
     """Dh = 64 with >= 8 waves runs the kernel that loads K/V tiles straight into LDS and reads V^T
-    through LDS transpose reads; for its 32-query waves the arithmetic is the register-staged
-    kernel's, so those rows must be bit-identical (one key tile, a ragged last tile of one key, 10
-    waves, large logits). A last wave with at most 16 queries (T % 32 in 1..16: T = 261, 260, 300)
-    runs on 16x16x32 MFMAs, which sum the products in another order: its rows are checked against
-    the float64 reference within the attention bound instead."""
+    through LDS transpose reads, with the light last wave (T % 32 in 1..16: T = 261, 260, 300, 517)
+    split over four waves: one key tile, a ragged last tile of one key, 10 waves, large logits, and
+    the ViT-L keep-10 % / 50 % query counts (T = 107, 517), all against the float64 reference."""
     D = 64
     q = (_rand((B * T, H, D), 40).float() * scale_up).to(torch.bfloat16)
     kv = (_rand((B, N, 2, H, D), 41).float() * scale_up).to(torch.bfloat16)
-    monkeypatch.delenv("OUDJAT_ATTN_STAGED", raising=False)
     got = K.sparse_query_attention(q.to(dev), kv.to(dev), T, D ** -0.5).cpu()
-    monkeypatch.setenv("OUDJAT_ATTN_STAGED", "1")
-    ref = K.sparse_query_attention(q.to(dev), kv.to(dev), T, D ** -0.5).cpu()
-    q_last = 32 * ((T - 1) // 32)
-    light = T - q_last <= 16
-    full_rows = torch.arange(T) < (q_last if light else T)
-    fr = full_rows.repeat(B)
-    assert_bits_equal(got[fr], ref[fr], f"attention {B},{T},{N},{H} x{scale_up} (32-query waves)")
-    if light:
-        lr = ~fr
-        qb = q.reshape(B, T, H, D)[:, q_last:].transpose(1, 2)
-        o64 = F64.sdpa(qb, kv[:, :, 0].transpose(1, 2), kv[:, :, 1].transpose(1, 2), D ** -0.5)
-        o64 = o64.transpose(1, 2).reshape(-1, H * D)
-        _check_attention(got.reshape(B * T, H * D)[lr], qb, kv, D ** -0.5, o64,
-                         f"attention {B},{T},{N},{H} x{scale_up} (16-query wave)")
+    qb = q.reshape(B, T, H, D).transpose(1, 2)
+    o64 = F64.sdpa(qb, kv[:, :, 0].transpose(1, 2), kv[:, :, 1].transpose(1, 2), D ** -0.5)
+    o64 = o64.transpose(1, 2).reshape(B * T, H * D)
+    _check_attention(got, qb, kv, D ** -0.5, o64, f"attention {B},{T},{N},{H} x{scale_up}")
+    again = K.sparse_query_attention(q.to(dev), kv.to(dev), T, D ** -0.5).cpu()
+    assert_bits_equal(again, got, "repeat launch")
 
 
 def test_sparse_query_attention_peaked_softmax(dev):

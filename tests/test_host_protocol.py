@@ -105,3 +105,41 @@ def test_bench_refuses_more_than_one_gpu():
     r = subprocess.run([sys.executable, os.path.join(ROOT, "bench.py"), "--gpus", "2"], capture_output=True,
                        text=True, timeout=120, cwd=ROOT)
     assert r.returncode == 2 and "one MI355X" in r.stderr
+
+
+def test_explicit_low_precision_request_raises_when_unavailable():
+    """dinov3_precision.py:723-731: an explicit fp8 request the build cannot serve is an error, not a
+    silent bf16 run; bf16 and auto construct normally."""
+    from torch import nn
+
+    from appcorr_amd.server.precision import DINOv3CorrectPrecisionController
+
+    blocks = nn.ModuleList()
+    for p in ("bf16", "auto"):
+        c = DINOv3CorrectPrecisionController(blocks, precision=p)
+        assert c.event_metadata()["correct_precision_requested"] == p
+    with pytest.raises(RuntimeError, match="fp8"):
+        DINOv3CorrectPrecisionController(blocks, precision="fp8")
+    with pytest.raises(ValueError):
+        DINOv3CorrectPrecisionController(blocks, precision="int3")
+
+
+def test_device_pointer_array_lives_with_its_holder():
+    """The fold kernel's pointer array is cached in the dict that owns the pointed-to tensors and is
+    dropped only once that dict no longer holds all of them (a graph over them could not replay)."""
+    holder = {"layer0_blocks_out_sum": torch.zeros(4), "layer1_blocks_out_sum": torch.zeros(4)}
+    ptrs = [holder["layer0_blocks_out_sum"].data_ptr(), holder["layer1_blocks_out_sum"].data_ptr()]
+    a = K.device_pointer_array(ptrs, "cpu", holder)
+    assert a.tolist() == ptrs
+    assert K.device_pointer_array(ptrs, "cpu", holder) is a          # cached: no new host copy
+    one = K.device_pointer_array(ptrs[:1], "cpu", holder)             # another list over live tensors
+    store = holder[K.POINTER_ARRAYS_KEY]
+    assert len(store) == 2
+    holder["layer1_blocks_out_sum"] = torch.ones(4)                   # a new approx pass replaces a tensor
+    new_ptrs = [ptrs[0], holder["layer1_blocks_out_sum"].data_ptr()]
+    b = K.device_pointer_array(new_ptrs, "cpu", holder)
+    assert b.tolist() == new_ptrs
+    keys = {k[1] for k in store}
+    assert tuple(ptrs) not in keys, "array over a tensor the holder dropped must be evicted"
+    assert tuple(ptrs[:1]) in keys and store[("cpu", tuple(ptrs[:1]))] is one
+    assert K.device_pointer_array(ptrs, "cpu", None) is not a         # no holder: a fresh array each call

@@ -82,12 +82,47 @@ def test_rope_tables_closed_form():
     # centre patch of an odd grid: both coordinates 0 -> angle 0
     np.testing.assert_array_equal(sin[4].numpy(), 0.0)
     np.testing.assert_array_equal(cos[4].numpy(), 1.0)
-    # patch (h=0, w=2): coordinates (-2/3, +2/3); frequency j < D/4 uses h, D/4 <= j < D/2 uses w
-    per = cfg.rope_base ** (2 * np.arange(D // 4) / (D // 2))
+    # patch (h=0, w=2): coordinates (-2/3, +2/3); frequency j < D/4 uses h, D/4 <= j < D/2 uses w.
+    # Periods: base^(2i/(D/2)) rounded to bf16 -- the model is served after model.to(bfloat16)
+    # (offload/server/model/dinov3_classifier.py:304), which casts the periods buffer.
+    per = torch.tensor([cfg.rope_base ** (2 * i / (D // 2)) for i in range(D // 4)], dtype=torch.float64)
+    per = per.to(torch.bfloat16).double().numpy()
     want = np.concatenate([2 * np.pi * (-2 / 3) / per, 2 * np.pi * (2 / 3) / per])
     want = np.concatenate([want, want])
     np.testing.assert_allclose(sin[2].numpy(), np.sin(want), atol=2e-6)
     np.testing.assert_allclose(cos[2].numpy(), np.cos(want), atol=2e-6)
+
+
+@pytest.mark.parametrize("name", ["vits16_224", "vit7b16_1024"])
+def test_rope_periods_are_bf16_rounded(name):
+    """The served periods are bf16(base^(2i/(D/2))) (model.to(bfloat16) casts the persistent buffer,
+    rope_position_encoding.py:50-53); for these head dims most of them are not fp32 values of bf16
+    precision, so the tables differ from the uncast module's."""
+    cfg = OM.CONFIGS[name]
+    D = cfg.head_dim
+    closed = torch.tensor([cfg.rope_base ** (2 * i / (D // 2)) for i in range(D // 4)], dtype=torch.float64)
+    got = OM.rope_periods(cfg)
+    assert got.dtype == torch.bfloat16
+    assert torch.equal(got, closed.to(torch.bfloat16))
+    p32 = OM.rope_periods(cfg, torch.float32)
+    assert int((p32 != got.float()).sum()) >= D // 8
+    s16, _ = OM.rope_tables(cfg)
+    s32, _ = OM.rope_tables(cfg, periods_dtype=torch.float32)
+    assert float((s16 - s32).abs().max()) > 1e-3
+
+
+def test_backbone_rope_tables_match_oracle():
+    """The product backbone's tables (built with torch from its bf16 periods buffer) equal the
+    oracle's, bit for bit, on the CPU."""
+    from appcorr_amd.dinov3.backbone import dinov3_backbone
+
+    for name, key in (("vits16", "vits16_224"), ("vitl16", "vitl16_512")):
+        cfg = OM.CONFIGS[key]
+        m = dinov3_backbone(name, depth=1, seed=None)
+        assert m.rope_embed.periods.dtype == torch.bfloat16
+        s, c = m.rope_embed(H=cfg.grid, W=cfg.grid)
+        s_ref, c_ref = OM.rope_tables(cfg)
+        assert s.dtype == torch.float32 and torch.equal(s, s_ref) and torch.equal(c, c_ref)
 
 
 def _stress(cfg, depth, B, seed=0):
