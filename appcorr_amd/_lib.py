@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be loaded before the HIP library, see module docstring
 
 LIB_PATH = Path(__file__).resolve().parent / "liboudjat_hip.so"
-ABI_VERSION = 5
+ABI_VERSION = 6
 
 OK = 0
 STATUS_NAMES = {
@@ -35,6 +35,8 @@ EPI_BIAS_GELU = 1
 EPI_BIAS_LS_RESID = 2
 EPI_BIAS_LS = 3
 EPI_BIAS_SILU_MUL = 4
+
+QUERY_PROB_NOALLOC_MAX = 1 << 20  # OUDJAT_QUERY_PROB_NOALLOC_MAX: fp32 elements of the no-alloc scratch array
 
 IMPORTANCE_L2 = 0
 IMPORTANCE_ENERGY = 1
@@ -91,6 +93,8 @@ SIGNATURES: dict[str, list] = {
     "oudjat_query_attention_prob": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p, _p, _i64,
                                     _i32, _p],
     "oudjat_pseudo_query": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
+    "oudjat_query_attention_prob_noalloc": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p,
+                                            _i64, _i32, _p],
 }
 _RESTYPES = {"oudjat_status_string": ctypes.c_char_p, "oudjat_last_error": ctypes.c_char_p}
 

@@ -1,7 +1,7 @@
 // Status plumbing, ABI version and the runtime self-test.
 #include "common.hpp"
 
-#define OUDJAT_ABI_VERSION 5
+#define OUDJAT_ABI_VERSION 6
 
 namespace oudjat {
 
@@ -71,5 +71,6 @@ extern "C" int oudjat_selftest(oudjat_stream_t stream) {
   if (status != OUDJAT_OK) return status;
   for (int i = 0; i < n; ++i)
     if (hy[i] != 2.0f * hx[i]) return set_error(OUDJAT_ERR_HIP, "selftest: wrong result at %d: %f", i, hy[i]);
-  return OUDJAT_OK;
+  // Library set-up on this device: the address of the no-alloc entry point's scratch array.
+  return noalloc_scratch(nullptr);
 }

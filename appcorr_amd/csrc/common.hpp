@@ -98,6 +98,10 @@ __device__ __forceinline__ float wave_max(float v) {
 int set_error(int status, const char* fmt, ...);
 int check_launch(const char* what);
 
+// Device address of the no-alloc entry point's scratch array on the current device (pscore.hip),
+// looked up once per device; `out` may be NULL to only perform the lookup.
+int noalloc_scratch(float** out);
+
 inline hipStream_t as_stream(oudjat_stream_t s) { return reinterpret_cast<hipStream_t>(s); }
 
 inline bool aligned(const void* p, int64_t a) { return (reinterpret_cast<uintptr_t>(p) % (uintptr_t)a) == 0; }

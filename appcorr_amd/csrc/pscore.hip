@@ -8,6 +8,8 @@
 // each fp32 accumulation exactly (float64 partial sums of exact fp32 products, one rounding to fp32)
 // and each exponential in float64 (one rounding to fp32): the correctly rounded value of every step,
 // independent of the reduction order, hence deterministic and equal bit for bit to the CPU restatement.
+#include <mutex>
+
 #include "common.hpp"
 
 namespace oudjat {
@@ -184,6 +186,35 @@ __global__ void __launch_bounds__(kPsThreads) pseudo_query_kernel(const uint16_t
 }
 
 }  // namespace
+
+// Workspace of oudjat_query_attention_prob_noalloc: the per-head probabilities of one call, B*H*N fp32.
+// Each GPU the library runs on holds its own copy until the process ends; host code must use the
+// address hipGetSymbolAddress returns for the current device, never the array's name.
+constexpr int64_t kNoAllocMaxElems = OUDJAT_QUERY_PROB_NOALLOC_MAX;  // 4 MiB of fp32
+static __device__ __align__(256) float scratch[kNoAllocMaxElems];
+
+static std::once_flag g_scratch_once[64];
+static float* g_scratch_ptr[64];
+static hipError_t g_scratch_err[64];
+
+// The current device's address of `scratch`, looked up once per device (at library init by
+// oudjat_selftest, else at the first no-alloc call on that device).
+int noalloc_scratch(float** out) {
+  int dev = 0;
+  hipError_t e = hipGetDevice(&dev);
+  if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "noalloc scratch: hipGetDevice: %s", hipGetErrorString(e));
+  if (dev < 0 || dev >= 64) return set_error(OUDJAT_ERR_HIP, "noalloc scratch: device index %d out of range", dev);
+  std::call_once(g_scratch_once[dev], [dev] {
+    void* p = nullptr;
+    g_scratch_err[dev] = hipGetSymbolAddress(&p, HIP_SYMBOL(scratch));
+    g_scratch_ptr[dev] = static_cast<float*>(p);
+  });
+  if (g_scratch_err[dev] != hipSuccess || g_scratch_ptr[dev] == nullptr)
+    return set_error(OUDJAT_ERR_HIP, "noalloc scratch: hipGetSymbolAddress: %s", hipGetErrorString(g_scratch_err[dev]));
+  if (out) *out = g_scratch_ptr[dev];
+  return OUDJAT_OK;
+}
+
 }  // namespace oudjat
 
 using namespace oudjat;
@@ -240,4 +271,24 @@ extern "C" int oudjat_pseudo_query(const uint16_t* q, int64_t q_stride_b, int64_
   else
     pseudo_query_kernel<16><<<grid, kPsThreads, 0, s>>>(q, q_stride_b, q_stride_t, q_stride_h, (int)P, inv_p, out);
   return check_launch("pseudo_query");
+}
+
+// oudjat_query_attention_prob with the library's own device array as the workspace (no allocation;
+// calls on one GPU share the array, so calls that overlap in time on one GPU race). The array needs
+// no clearing: the first kernel writes every one of the B*H*N entries the second reads.
+extern "C" int oudjat_query_attention_prob_noalloc(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h,
+                                                   int64_t B, int64_t H, int64_t Dh, const uint16_t* k,
+                                                   int64_t k_stride_b, int64_t k_stride_n, int64_t k_stride_h,
+                                                   int64_t N, float scale, void* out, int64_t out_stride_b,
+                                                   int out_bf16, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(B >= 0 && H > 0 && N > 0 && B <= 65535 && H <= 65535 && N <= kPsMaxKeys,
+                 OUDJAT_ERR_INVALID_ARGUMENT, "query_attention_prob_noalloc: bad sizes");
+  OUDJAT_REQUIRE(B * H * N <= kNoAllocMaxElems, OUDJAT_ERR_TOO_LARGE,
+                 "query_attention_prob_noalloc: B*H*N = %lld exceeds the %lld-element scratch array",
+                 (long long)(B * H * N), (long long)kNoAllocMaxElems);
+  float* ws = nullptr;
+  const int st = noalloc_scratch(&ws);
+  if (st != OUDJAT_OK) return st;
+  return oudjat_query_attention_prob(q, q_stride_b, q_stride_h, B, H, Dh, k, k_stride_b, k_stride_n, k_stride_h, N,
+                                     scale, ws, out, out_stride_b, out_bf16, stream);
 }

@@ -250,6 +250,18 @@ int oudjat_query_attention_prob(const uint16_t* q, int64_t q_stride_b, int64_t q
                                 float* workspace, void* out, int64_t out_stride_b, int out_bf16,
                                 oudjat_stream_t stream);
 
+/* No counterpart in the reference: oudjat_query_attention_prob for callers that cannot allocate
+ * (code under HIP graph capture, tight serving loops, harnesses that forbid hipMalloc). Same
+ * arguments and results without `workspace`: the per-head probabilities go to a library-owned device
+ * array of OUDJAT_QUERY_PROB_NOALLOC_MAX fp32 (4 MiB), which each GPU the library runs on holds until
+ * the process ends. B*H*N above that returns OUDJAT_ERR_TOO_LARGE. Nothing is allocated. All calls on
+ * one GPU share the array: calls that overlap in time on one GPU (unordered streams) race. */
+#define OUDJAT_QUERY_PROB_NOALLOC_MAX (1 << 20)
+int oudjat_query_attention_prob_noalloc(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_h, int64_t B,
+                                        int64_t H, int64_t Dh, const uint16_t* k, int64_t k_stride_b,
+                                        int64_t k_stride_n, int64_t k_stride_h, int64_t N, float scale,
+                                        void* out, int64_t out_stride_b, int out_bf16, oudjat_stream_t stream);
+
 /* The pseudo query of patch_pseudo_attn_prob (attention.py:254-259) for every (image b, head h)
  * from the P patch queries q[b, t, h, :] at q + b*q_stride_b + t*q_stride_t + h*q_stride_h (after
  * RoPE), with torch's bf16 rounding points (mean, vector norm, clamp_min(bf16 eps), division,
