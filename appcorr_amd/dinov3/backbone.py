@@ -47,10 +47,13 @@ class DinoBackbone(nn.Module):
 
     @torch.no_grad()
     def init_weights(self, generator: torch.Generator | None = None) -> "DinoBackbone":
-        """Linear ~ trunc_normal(0.02) (drawn on the CPU from `generator`), biases 0, K-bias mask,
-        LayerNorm (1, 0), LayerScale = init value, cls/storage ~ N(0, 0.02)."""
+        """Linear ~ trunc_normal(0.02) (drawn from `generator`, on the generator's device), biases 0,
+        K-bias mask, LayerNorm (1, 0), LayerScale = init value, cls/storage ~ N(0, 0.02)."""
+        gdev = generator.device if generator is not None else None
+
         def normal_(p, std):
-            p.copy_((torch.randn(p.shape, generator=generator) * std).clamp_(-2.0, 2.0).to(p.dtype))
+            r = torch.randn(p.shape, generator=generator, device=gdev)
+            p.copy_((r * std).clamp_(-2.0, 2.0).to(p.dtype))
 
         normal_(self.cls_token, 0.02)
         normal_(self.storage_tokens, 0.02)
@@ -97,10 +100,12 @@ def dinov3_backbone(name: str, *, depth: int | None = None, layerscale_init: flo
     if key not in _FACTORY:
         raise ValueError(f"unknown DINOv3 backbone {name!r}; choose from {sorted(_FACTORY)}")
     dim, d, heads, ratio, qkv_bias, ffn = _FACTORY[key]
+    # Built on the target device and drawn from a generator there (the ViT-7B stack holds 6.7e9
+    # weights); on the CPU when no device is given.
     m = DinoBackbone(embed_dim=dim, depth=d if depth is None else depth, num_heads=heads, ffn_ratio=ratio,
-                     qkv_bias=qkv_bias, ffn_layer=ffn, layerscale_init=layerscale_init)
+                     qkv_bias=qkv_bias, ffn_layer=ffn, layerscale_init=layerscale_init, device=device)
     if seed is not None:
-        m.init_weights(torch.Generator().manual_seed(seed))
+        m.init_weights(torch.Generator(device=device if device is not None else "cpu").manual_seed(seed))
     # Every floating parameter and buffer moves to the serving dtype, as the reference's
     # `model.to(dtype=torch.bfloat16)` does (offload/server/model/dinov3_classifier.py:304;
     # analysis/experiments/dinov3_correct_profile.py:60). That includes the RoPE `periods` buffer

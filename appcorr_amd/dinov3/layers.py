@@ -163,7 +163,7 @@ class SelfAttention(nn.Module):
         """
         kv = cache_feature[f"{tag}_kv"]
         q_packed, attn = self._qkv_attention(x_sel, rope, kv, fixed_query_state)
-        out = K.linear(attn, self.proj.weight, self.proj.bias)
+        out = K.linear(attn, self.proj.weight, self.proj.bias, site="proj")
         return out, cache_feature
 
     def _qkv_attention(self, xn: Tensor, rope, kv: Tensor, qs: PackedQueryState):
@@ -178,7 +178,7 @@ class SelfAttention(nn.Module):
             K.linear_qkv_rope_kv(xn, self.qkv.weight, self.qkv_bias(), rope, qs.active_patch_mask, qs.active_rope_idx,
                                  qs.active_batch_idx, qs.active_token_idx, kv, q)
         else:
-            qkv = K.linear(xn, self.qkv.weight, self.qkv_bias())
+            qkv = K.linear(xn, self.qkv.weight, self.qkv_bias(), site="qkv")
             K.qkv_rope_kv_scatter(qkv.view(M, 3, H, D), rope, qs.active_patch_mask, qs.active_rope_idx,
                                   qs.active_batch_idx, qs.active_token_idx, kv, q)
         attn = K.sparse_query_attention(q, kv, T, self.scale)
@@ -238,11 +238,11 @@ class SelfAttentionBlock(nn.Module):
         """gamma2 * MLP(xn) with GELU / SwiGLU and LayerScale fused into the GEMM epilogues."""
         g2 = self._gamma(self.ls2, xn)
         if isinstance(self.mlp, Mlp):
-            h = K.linear(xn, self.mlp.fc1.weight, self.mlp.fc1.bias, epilogue=_lib.EPI_BIAS_GELU)
-            return K.linear(h, self.mlp.fc2.weight, self.mlp.fc2.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g2)
-        x2 = K.linear(xn, self.mlp.w2.weight, self.mlp.w2.bias)
-        h = K.linear(xn, self.mlp.w1.weight, self.mlp.w1.bias, epilogue=_lib.EPI_BIAS_SILU_MUL, resid=x2)
-        return K.linear(h, self.mlp.w3.weight, self.mlp.w3.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g2)
+            h = K.linear(xn, self.mlp.fc1.weight, self.mlp.fc1.bias, epilogue=_lib.EPI_BIAS_GELU, site="fc1")
+            return K.linear(h, self.mlp.fc2.weight, self.mlp.fc2.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g2, site="fc2")
+        x2 = K.linear(xn, self.mlp.w2.weight, self.mlp.w2.bias, site="w2")
+        h = K.linear(xn, self.mlp.w1.weight, self.mlp.w1.bias, epilogue=_lib.EPI_BIAS_SILU_MUL, resid=x2, site="w1")
+        return K.linear(h, self.mlp.w3.weight, self.mlp.w3.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g2, site="w3")
 
     # -- dispatch (block.py:274-310) --------------------------------------------------------------
 
@@ -284,7 +284,8 @@ class SelfAttentionBlock(nn.Module):
         xn = K.layer_norm(x2, self.norm1.weight, self.norm1.bias, self.norm1.eps)
         q, attn = self.attn._qkv_attention(xn, rope, kv, qs)
         g1 = self._gamma(self.ls1, x2)
-        inc = K.linear(attn, self.attn.proj.weight, self.attn.proj.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g1)
+        inc = K.linear(attn, self.attn.proj.weight, self.attn.proj.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g1,
+                       site="proj")
         ones = self._gamma(nn.Identity(), x2)
         x_attn = K.fused_layerscale_add(x2, inc, ones)                       # x + ls1(attn)
         mlp = self._mlp_scaled(K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps))
@@ -557,7 +558,7 @@ class SelfAttentionBlock(nn.Module):
         _, attn = self.attn._qkv_attention(xn, rope, kv, qs)                         # attention.py:415-523
         x_attn = K.linear(attn, self.attn.proj.weight, self.attn.proj.bias,          # attention.py:532 +
                           epilogue=_lib.EPI_BIAS_LS_RESID, gamma=self._gamma(self.ls1, x_act),
-                          resid=x_act)                                               # block.py:1129-1134
+                          resid=x_act, site="proj")                                  # block.py:1129-1134
         mlp = self._mlp_scaled(K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps))  # :1141
         return x_attn, mlp
 

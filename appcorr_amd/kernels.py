@@ -22,22 +22,29 @@ from ._lib import call
 
 P = ctypes.c_void_p
 
-# Optional live timing of one launch site: when `_probe["tag"]` names a site, every launch there is
-# bracketed by a pair of timing events on the launch stream (used by bench.py for the roofline).
-_probe: dict = {"tag": None, "events": []}
+# Optional live timing of launch sites: every launch at a site named in `_probe["tags"]` is bracketed
+# by a pair of timing events on the launch stream (used by bench.py for the roofline). Sites are the
+# kernels' roles in the pass: "qkv", "proj", "fc1", "fc2", "w1", "w2", "w3", "attention", ...
+_probe: dict = {"tags": frozenset(), "events": {}}
 
 
-def set_probe(tag: str | None) -> None:
-    _probe["tag"] = tag
-    _probe["events"] = []
+def set_probe(tags) -> None:
+    """Probe the named launch sites (a name, an iterable of names, or None for none)."""
+    if tags is None:
+        tags = ()
+    elif isinstance(tags, str):
+        tags = (tags,)
+    _probe["tags"] = frozenset(tags)
+    _probe["events"] = {}
 
 
-def probe_events() -> list:
+def probe_events() -> dict:
+    """{site: [(start event, end event), ...]} of the probed launches since set_probe."""
     return _probe["events"]
 
 
 def _launch(tag: str, t: torch.Tensor, name: str, *args) -> None:
-    if _probe["tag"] != tag:
+    if tag not in _probe["tags"]:
         call(name, *args)
         return
     s = torch.cuda.current_stream(t.device)
@@ -45,7 +52,7 @@ def _launch(tag: str, t: torch.Tensor, name: str, *args) -> None:
     e0.record(s)
     call(name, *args)
     e1.record(s)
-    _probe["events"].append((e0, e1))
+    _probe["events"].setdefault(tag, []).append((e0, e1))
 
 
 def _ptr(t: torch.Tensor | None) -> P:
@@ -449,7 +456,7 @@ def linear_qkv_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor
     _require(q_out.is_contiguous() and q_out.shape == (M, H, Dh), "linear_qkv_rope_kv: q_out must be contiguous [M, H, Dh]")
     _require(sin.dtype == cos.dtype == torch.float32 and sin.stride(1) == 1 and cos.stride() == sin.stride(),
              "linear_qkv_rope_kv: fp32 RoPE tables with contiguous rows")
-    _launch("gemm0", x, "oudjat_linear_qkv_rope_kv", _ptr(x), M, Kd, x.stride(0), _ptr(weight), weight.stride(0),
+    _launch("qkv", x, "oudjat_linear_qkv_rope_kv", _ptr(x), M, Kd, x.stride(0), _ptr(weight), weight.stride(0),
             _ptr(None if bias is None else bias.contiguous()), H, Dh, _ptr(sin), _ptr(cos), sin.stride(0),
             _ptr(patch_mask), _ptr(_index(rope_idx, "rope_idx")), _ptr(_index(batch_idx, "batch_idx")),
             _ptr(_index(token_idx, "token_idx")), _ptr(kv_cache), kv_cache.stride(0), kv_cache.stride(1), _ptr(q_out),
@@ -470,8 +477,9 @@ def linear_kernel_name(M: int, N: int, K: int, epilogue: int = _lib.EPI_BIAS) ->
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
            epilogue: int = _lib.EPI_BIAS, gamma: torch.Tensor | None = None, resid: torch.Tensor | None = None,
-           out: torch.Tensor | None = None) -> torch.Tensor:
-    """bf16 x[..., K] . weight[N, K]^T with a fused epilogue (see include/oudjat.h)."""
+           out: torch.Tensor | None = None, site: str = "linear") -> torch.Tensor:
+    """bf16 x[..., K] . weight[N, K]^T with a fused epilogue (see include/oudjat.h). `site` names the
+    launch for the timing probe ("proj", "fc1", "fc2", "w1", "w2", "w3", ...)."""
     _require_cuda(x, weight, bias, gamma, resid, out)
     _require(x.dtype == weight.dtype == torch.bfloat16, "linear: bf16 only")
     K = x.shape[-1]
@@ -487,7 +495,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     if resid is not None:
         r2 = resid.reshape(-1, N)
         _require(r2.stride(1) == 1 and r2.shape[0] == M, "linear: resid must be [M, N] with contiguous rows")
-    _launch(f"gemm{int(epilogue)}", x, "oudjat_linear_bf16", _ptr(x2), M, K, x2.stride(0), _ptr(weight), N, weight.stride(0),
+    _launch(site, x, "oudjat_linear_bf16", _ptr(x2), M, K, x2.stride(0), _ptr(weight), N, weight.stride(0),
          _ptr(None if bias is None else bias.contiguous()), int(epilogue),
          _ptr(None if gamma is None else gamma.contiguous()), _ptr(r2), 0 if r2 is None else r2.stride(0), _ptr(o2),
          o2.stride(0), _stream(x))

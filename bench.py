@@ -1,20 +1,24 @@
 """Benchmark: one DINOv3 token-correction pass on one MI355X.
 
-Workload (BASELINE.json metric "ms per correction pass + corrected tokens/s, ViT-L/16 512px, 25%
+Default workload (BASELINE.json metric "ms per correction pass + corrected tokens/s, ViT-L/16 512px, 25%
 keep"): ViT-L/16 at 512 px, B=16 (1029 tokens per image), 24 blocks, bf16, random-init weights, top
 25% of the 1024 patches per image (k=256) selected by importance = ||delta_p||_2 with
-delta ~ Laplace(0,1). One step = one full correction pass through the executor API
-(`DINOv3ClassifierExecutor.correct_forward`, i.e. `run_dinov3_correct_block` for every layer):
-the importance reduction, the top-k plan (recomputed every pass) and all 24 correction blocks. The K/V and
+delta ~ Laplace(0,1). `--config` selects the other BASELINE shapes (ViT-S, ViT-B, ViT-7B at B=4, keep
+10%) and `--keep` the sweep points. One step = one full correction pass through the executor API
+(`DINOv3ClassifierExecutor.correct_forward`, i.e. `run_dinov3_correct_block` for every layer): the
+importance reduction, the top-k plan (recomputed every pass) and all correction blocks. The K/V and
 blocks_out_sum caches come from an untimed approximate pass over the base tokens.
 
-Output: one JSON line on stdout. `value` = corrected tokens/s = B*k / pass time; `ms_per_step` =
-ms per correction pass. By default the step is recorded once into a HIP graph and the timed steps
-are replays (every kernel of the pass runs each step; `config.eager_ms_per_step` is the same K steps
-launched one kernel at a time, `--graph 0` reports that instead). `roofline` is for the dominant
-kernel, timed live with HIP events around each of its launches in the eager steps; `cpu_baseline`
-times the CPU oracle (the reference's eager op sequence on bf16 CPU tensors) on a bounded sample of
-the same workload.
+Output: one JSON line on stdout. `value` = corrected tokens/s = B*k / pass time; `ms_per_step` = ms
+per correction pass. The step is recorded once into a HIP graph and the timed steps are replays (every
+kernel of the pass runs each step; `config.eager_ms_per_step` is the same K steps launched one kernel
+at a time, `--graph 0` reports that instead).
+
+`roofline` is for the dominant kernel: every MFMA launch site of the pass (qkv, proj, the MLP GEMMs,
+attention) is timed with HIP events around each launch in separate eager steps, and the site with the
+largest share of the pass is reported, with all sites under `roofline.sites`. `cpu_baseline` times the
+CPU oracle (the reference's eager op sequence on bf16 CPU tensors) on the same inputs, weights and
+caches as the GPU run, with one torch thread per CPU this process may run on.
 
 Only one GPU is used: `--gpus N` with N > 1 exits with an explanation.
 """
@@ -24,7 +28,6 @@ from __future__ import annotations
 import argparse
 import ctypes
 import json
-import math
 import os
 import statistics
 import sys
@@ -38,11 +41,15 @@ METRIC = "ms per correction pass + corrected tokens/s, ViT-L/16 512px, 25% keep"
 PEAK_BF16_TFLOPS = 2500.0     # MI355X dense bf16 MFMA
 PEAK_HBM_GBS = 8000.0         # MI355X HBM3E
 
-SHAPES = {  # name: (backbone, embed, heads, mlp, depth, img)
-    "vits16_224": ("vits16", 384, 6, 1536, 12, 224),
-    "vitb16_512": ("vitb16", 768, 12, 3072, 12, 512),
-    "vitl16_512": ("vitl16", 1024, 16, 4096, 24, 512),
+# name: (backbone, embed, heads, ffn hidden, depth, img, ffn kind, default batch, default keep)
+SHAPES = {
+    "vits16_224": ("vits16", 384, 6, 1536, 12, 224, "mlp", 1, 0.5),
+    "vitb16_512": ("vitb16", 768, 12, 3072, 12, 512, "mlp", 8, 0.25),
+    "vitl16_512": ("vitl16", 1024, 16, 4096, 24, 512, "mlp", 16, 0.25),
+    "vit7b16_1024": ("vit7b16", 4096, 32, 8192, 40, 1024, "swiglu", 4, 0.1),
 }
+MFMA_SITES = {"mlp": ("qkv", "proj", "fc1", "fc2", "attention"),
+              "swiglu": ("qkv", "proj", "w1", "w2", "w3", "attention")}
 
 
 def _roctx():
@@ -60,88 +67,96 @@ def _roctx():
     return None
 
 
-def kernel_work(tag: str, B: int, T: int, N: int, C: int, H: int, mlp: int):
-    """Algorithmic work of one launch at a site: (amount, unit, bound)."""
+def site_work(site: str, B: int, T: int, N: int, C: int, H: int, hid: int):
+    """Algorithmic work of one launch at a site: (amount in TFLOP or GB, unit, bound)."""
     M = B * T
-    if tag == "gemm0":   # qkv
-        return 2.0 * M * C * 3 * C / 1e12, "TFLOP/s", "mfma"
-    if tag == "gemm1":   # fc1 + GELU
-        return 2.0 * M * C * mlp / 1e12, "TFLOP/s", "mfma"
-    if tag == "gemm2":   # proj + LayerScale + residual
-        return 2.0 * M * C * C / 1e12, "TFLOP/s", "mfma"
-    if tag == "gemm3":   # fc2 + LayerScale
-        return 2.0 * M * mlp * C / 1e12, "TFLOP/s", "mfma"
-    if tag == "attention":
-        return 4.0 * B * H * T * N * (C // H) / 1e12, "TFLOP/s", "mfma"
-    if tag == "reconstruct":  # fused minimum: 3 B N C + 2 M C bf16 elements + row map
-        return (3.0 * B * N * C * 2 + 2.0 * M * C * 2 + 4.0 * B * N) / 1e9, "GB/s", "hbm"
-    if tag == "packed_residual":  # read x_act, x_attn, mlp; write x_new, blocks_out_sum rows; row ids
+    flops = {"qkv": 2.0 * M * C * 3 * C, "proj": 2.0 * M * C * C, "fc1": 2.0 * M * C * hid,
+             "fc2": 2.0 * M * hid * C, "w1": 2.0 * M * C * hid, "w2": 2.0 * M * C * hid,
+             "w3": 2.0 * M * hid * C, "attention": 4.0 * B * H * T * N * (C // H)}
+    if site in flops:
+        return flops[site] / 1e12, "TFLOP/s", "mfma"
+    if site == "packed_residual":  # read x_act, x_attn, mlp; write x_new, blocks_out_sum rows; row ids
         return (5.0 * M * C * 2 + 16.0 * M) / 1e9, "GB/s", "hbm"
-    if tag == "gather_rows":
+    if site == "gather_rows":
         return (2.0 * M * C * 2 + 16.0 * M) / 1e9, "GB/s", "hbm"
-    if tag == "qkv_post":  # read qkv rows, write q packed + k,v cache rows
-        return (2.0 * M * 3 * C * 2 + 16.0 * M) / 1e9, "GB/s", "hbm"
-    if tag == "layernorm":
+    if site == "layernorm":
         return (2.0 * M * C * 2) / 1e9, "GB/s", "hbm"
-    raise ValueError(tag)
+    raise ValueError(site)
 
 
-def probe_kernel_name(tag: str, B: int, T: int, C: int, mlp: int):
+def site_kernel_name(site: str, B: int, T: int, C: int, hid: int):
     """Kernel a GEMM launch site runs in this build (None for other sites)."""
     from appcorr_amd import _lib
     from appcorr_amd import kernels as K
 
     M = B * T
-    shapes = {"gemm0": (M, 3 * C, C, 5), "gemm1": (M, mlp, C, _lib.EPI_BIAS_GELU),
-              "gemm2": (M, C, C, _lib.EPI_BIAS_LS_RESID), "gemm3": (M, C, mlp, _lib.EPI_BIAS_LS)}
-    if tag not in shapes:
+    shapes = {"qkv": (M, 3 * C, C, 5), "proj": (M, C, C, _lib.EPI_BIAS_LS_RESID),
+              "fc1": (M, hid, C, _lib.EPI_BIAS_GELU), "fc2": (M, C, hid, _lib.EPI_BIAS_LS),
+              "w1": (M, hid, C, _lib.EPI_BIAS_SILU_MUL), "w2": (M, hid, C, _lib.EPI_BIAS),
+              "w3": (M, C, hid, _lib.EPI_BIAS_LS)}
+    if site not in shapes:
         return None
-    return K.linear_kernel_name(*shapes[tag])
+    return K.linear_kernel_name(*shapes[site])
 
 
-def cpu_baseline(name: str, B: int, keep: float, budget_s: float):
-    """Oracle (reference eager op order, bf16 CPU tensors) on a bounded sample: one correction block
-    of the same shape, repeated until ~budget_s; scaled to a full pass (plan + depth x block)."""
+def _cpu_model() -> str:
+    try:
+        for line in open("/proc/cpuinfo"):
+            if line.lower().startswith("model name"):
+                return line.split(":", 1)[1].strip()
+    except OSError:
+        pass
+    return "unknown"
+
+
+def cpu_baseline(name: str, blocks, x_full, caches, hint, k: int, budget_s: float):
+    """The oracle (the reference's eager op sequence on bf16 CPU tensors, with the top-k plan) on the
+    GPU run's own weights, layer-0 tokens, K/V + blocks_out_sum caches and importance scores, one torch
+    thread per CPU this process may run on (nproc). 3 warm-up and 10 timed passes, median; when 13
+    passes would exceed `budget_s`, the same over the first n blocks, scaled to the full depth."""
     import torch
 
     from oracle import model as OM
     from oracle import plan as OP
 
-    nthreads = int(os.environ.get("OMP_NUM_THREADS") or os.cpu_count() or 1)
-    torch.set_num_threads(nthreads)
+    nproc = len(os.sched_getaffinity(0))
+    torch.set_num_threads(nproc)
     cfg = OM.CONFIGS[name]
-    w = OM.make_block_weights(cfg, 0, depth=1)[0]
-    g = torch.Generator().manual_seed(7)
-    N, C, H, D = cfg.num_tokens, cfg.dim, cfg.heads, cfg.head_dim
-    x = torch.randn(B, N, C, generator=g).to(torch.bfloat16)
-    imp = torch.rand(B, cfg.num_patches, generator=g)
-    cache = {"layer0_kv": torch.randn(B, N, 2, H, D, generator=g).to(torch.bfloat16),
-             "layer0_blocks_out_sum": (torch.randn(B, N, C, generator=g) * 0.01).to(torch.bfloat16)}
-    rope = OM.rope_tables(cfg)
-    k = OP.keep_count(cfg.num_patches, keep)
+    B, N = x_full.shape[0], x_full.shape[1]
     dind = OM.full_dindice(cfg, B).numpy()
-    t0 = time.perf_counter()
-    plan = OP.build_plan(imp.numpy(), k, dind, cfg.num_pretokens, N)
-    t_plan = time.perf_counter() - t0
-    times = []
-    with torch.no_grad():
-        OM.correct_block(cfg, w, x, plan, rope, cache, "layer0", mode="bf16")  # warm-up
-        start = time.perf_counter()
-        while len(times) < 10 and (time.perf_counter() - start < budget_s or len(times) < 2):
-            t0 = time.perf_counter()
-            OM.correct_block(cfg, w, x, plan, rope, cache, "layer0", mode="bf16")
-            times.append(time.perf_counter() - t0)
-    blk = statistics.median(times)
-    pass_s = t_plan + cfg.depth * blk
+    depth = len(blocks)
+
+    rope = OM.rope_tables(cfg)
+
+    def run(n_blk):
+        cache = dict(caches)
+        t0 = time.perf_counter()
+        plan = OP.build_plan(hint.numpy(), k, dind, cfg.num_pretokens, N)
+        x = x_full
+        with torch.no_grad():
+            for i in range(n_blk):
+                x, cache = OM.correct_block(cfg, blocks[i], x, plan, rope, cache, f"layer{i}", mode="bf16")
+        return time.perf_counter() - t0
+
+    t1 = run(1)  # one block, also a warm-up
+    n_blk = depth if 13 * t1 * depth <= budget_s else max(1, int(budget_s / (13 * t1)))
+    n_blk = min(n_blk, depth)
+    for _ in range(3):
+        run(n_blk)
+    times = [run(n_blk) for _ in range(10)]
+    med = statistics.median(times)
+    pass_s = med * depth / n_blk
+    what = "full passes" if n_blk == depth else f"the first {n_blk} of {depth} blocks (+ the plan), scaled x{depth / n_blk:g}"
     return {
         "value": B * k / pass_s,
         "unit": "corrected tokens/s",
-        "cores": torch.get_num_threads(),
+        "cores": nproc,
         "kind": "port",
-        "sample": (f"1 of {cfg.depth} blocks ({name}, B={B}, k={k}, bf16 torch CPU eager ops), median of "
-                   f"{len(times)} runs = {blk * 1e3:.1f} ms/block, plus the top-k plan ({t_plan * 1e3:.1f} ms); "
-                   f"scaled to a {cfg.depth}-block pass = {pass_s * 1e3:.0f} ms"),
-        "ms_per_pass": pass_s * 1e3,
+        "sample": (f"{name} B={B} k={k}, the GPU run's weights, tokens, caches and importance; bf16 torch CPU eager "
+                   f"ops ({what}), 3 warm-up + 10 timed, median {med * 1e3:.1f} ms -> {pass_s * 1e3:.0f} ms per pass"),
+        "ms_per_pass": round(pass_s * 1e3, 2),
+        "cpu_model": _cpu_model(),
+        "os_cpu_count": os.cpu_count(),
     }
 
 
@@ -151,15 +166,16 @@ def main():
     ap.add_argument("--steps", type=int, default=20)
     ap.add_argument("--warmup", type=int, default=5)
     ap.add_argument("--config", default="vitl16_512", choices=sorted(SHAPES))
-    ap.add_argument("--batch", type=int, default=16)
-    ap.add_argument("--keep", type=float, default=0.25)
-    ap.add_argument("--probe", default="gemm1", help="launch site timed for the roofline (gemm0..3, attention, ...)")
+    ap.add_argument("--batch", type=int, default=None, help="images per pass (default: the config's)")
+    ap.add_argument("--keep", type=float, default=None, help="token keep ratio (default: the config's)")
+    ap.add_argument("--precision", default="bf16", help="correct_precision of the executor")
     ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline sampling (0 = skip)")
     ap.add_argument("--cache", default="approx", choices=("approx", "random"),
                     help="fill the K/V + residual caches with the approximate pass (default) or random values")
     ap.add_argument("--graph", type=int, default=1,
                     help="1: record the step into a HIP graph and time its replays (the eager time is reported "
                          "alongside); 0: time eager launches only")
+    ap.add_argument("--probe", type=int, default=1, help="1: time every MFMA launch site in extra eager steps")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="before the timed steps, copy this many MiB device-to-device once (a plain copy of known "
                          "size that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -182,17 +198,18 @@ def main():
     dev = torch.device("cuda", 0)
     torch.cuda.set_device(dev)
     _lib.verify_runtime(0)
-    bb, C, H, mlp, depth, img = SHAPES[args.config]
-    B = args.batch
+    bb, C, H, hid, depth, img, ffn, b_dflt, keep_dflt = SHAPES[args.config]
+    B = args.batch or b_dflt
+    keep = keep_dflt if args.keep is None else args.keep
     grid = img // 16
     P = grid * grid
     N = 5 + P
-    k = min(int(P * args.keep), P)
+    k = min(int(P * keep), P)
     T = 5 + k
 
     config = ExperimentConfig(model_name=f"dinov3_classifier_{bb}", batch_size=B, image_shape=(img, img, 3),
-                              backbone=bb, appcorr_kwargs={
-                                  "method": "partial_token", "token_keep_ratio": args.keep,
+                              backbone=bb, correct_precision=args.precision, appcorr_kwargs={
+                                  "method": "partial_token", "token_keep_ratio": keep,
                                   "mobile_pscore": "residual_energy", "mobile_pscore_weight": 1.0,
                                   "server_pscore_weight": 0.0, "pscore_fusion": "add"})
     ex = DINOv3ClassifierExecutor(dev)
@@ -203,16 +220,18 @@ def main():
     x_base = torch.randn(B, N, C, generator=g, device=dev)
     # u uniform on the open interval (-1, 1) as torch.distributions.Laplace samples it: u = rand - 0.5
     # with log1p(-2|u|) gives -inf whenever rand returns exactly 0 (about once per 2^24 draws, i.e.
-    # about once in this 16.7M-element tensor), which turns a whole image into NaN downstream.
+    # about once in a 16.7M-element tensor), which turns a whole image into NaN downstream.
     eps = torch.finfo(torch.float32).eps
     u = torch.rand(B, P, C, generator=g, device=dev) * (2.0 - eps) + (eps - 1.0)
     delta = -torch.sign(u) * torch.log1p(-u.abs())
+    del u
     if not bool(torch.isfinite(delta).all()):
         raise RuntimeError("bench: non-finite synthetic residual")
     x_full = x_base.clone()
     x_full[:, 5:] += delta
     context = {"input_tokens": x_base.to(torch.bfloat16).contiguous(),
                "rope_sincos": ex.model.rope_embed(H=grid, W=grid)}
+    del x_base
     dind = torch.arange(N, device=dev).unsqueeze(0).expand(B, -1).contiguous()
     context["group_plans"] = {1: make_group_plan(dind, 5)}
     with torch.no_grad():
@@ -229,6 +248,7 @@ def main():
                 context["cache_feature"][f"layer{i}_blocks_out_sum"] = (
                     torch.randn(B, N, C, generator=g, device=dev) * 0.01).to(torch.bfloat16)
     context["input_tokens"] = x_full.to(torch.bfloat16).contiguous()
+    del x_full
     params = {"layers": (0, depth), "group_id": 1}
 
     def step():
@@ -255,31 +275,34 @@ def main():
             roctx.roctxProfilerResume(0)
         s = torch.cuda.current_stream()
 
-        def timed(fn):
+        def timed(fn, steps):
             a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
             torch.cuda.synchronize()
             w0 = time.perf_counter()
             a.record(s)
-            for _ in range(args.steps):
+            for _ in range(steps):
                 fn()
             b.record(s)
             torch.cuda.synchronize()
-            return a.elapsed_time(b) / args.steps, time.perf_counter() - w0
+            return a.elapsed_time(b) / steps, time.perf_counter() - w0
 
-        # Eager launches, with the probe on the roofline launch site.
-        K.set_probe(args.probe)
-        ms_eager, wall_eager = timed(step)
-        events = K.probe_events()
-        K.set_probe(None)
+        ms_eager, wall_eager = timed(step, args.steps)
         ms, wall = ms_eager, wall_eager
         if args.graph:
             from appcorr_amd.graphs import capture
 
             replay = capture(step, dev, warmup=1)
-            ms, wall = timed(replay)
+            ms, wall = timed(replay, args.steps)
         if roctx is not None:
             roctx.roctxProfilerPause(0)
-        # The corrected tokens of the last timed pass must be finite (outside the timed region).
+        # Per-site launch times, in eager steps of their own (the events do not touch the timed steps).
+        events = {}
+        if args.probe:
+            K.set_probe(MFMA_SITES[ffn])
+            timed(step, max(3, args.steps // 4))
+            events = K.probe_events()
+            K.set_probe(None)
+        # The corrected tokens of the last pass must be finite (outside the timed region).
         out = context["current_feature"]
         if not bool(torch.isfinite(out.float()).all()):
             raise RuntimeError("bench: the correction pass produced non-finite tokens")
@@ -287,38 +310,60 @@ def main():
 
     roof = None
     if events:
-        durs = [a.elapsed_time(b) for a, b in events]
-        avg_ms = sum(durs) / len(durs)
-        amount, unit, bound = kernel_work(args.probe, B, T, N, C, H, mlp)
-        achieved = amount / (avg_ms / 1e3)
-        peak = PEAK_BF16_TFLOPS if bound == "mfma" else PEAK_HBM_GBS
-        roof = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
-                "frac": round(achieved / peak, 4), "traffic": None, "kernel": args.probe,
-                "launches": len(durs), "avg_us": round(avg_ms * 1e3, 2)}
+        sites = {}
+        probe_steps = max(3, args.steps // 4)
+        for site, evs in events.items():
+            durs = [a.elapsed_time(b) for a, b in evs]
+            avg_ms = sum(durs) / len(durs)
+            amount, unit, bound = site_work(site, B, T, N, C, H, hid)
+            achieved = amount / (avg_ms / 1e3)
+            peak = PEAK_BF16_TFLOPS if bound == "mfma" else PEAK_HBM_GBS
+            per_pass = len(durs) / probe_steps
+            sites[site] = {"bound": bound, "achieved": round(achieved, 2), "peak": peak, "unit": unit,
+                           "frac": round(achieved / peak, 4), "avg_us": round(avg_ms * 1e3, 2),
+                           "launches_per_pass": per_pass,
+                           "share_of_pass": round(avg_ms * per_pass / ms, 4)}
+        dom = max(sites, key=lambda x: sites[x]["avg_us"] * sites[x]["launches_per_pass"])
+        roof = dict(sites[dom])
+        roof.update({"kernel": dom, "traffic": None})
         # HBM bytes per launch of this kernel at this workload, from the committed rocprofv3
         # FETCH_SIZE / WRITE_SIZE summary (appcorr_amd.profiling traffic), when one exists.
-        tkey = f"{args.probe}@{args.config}/b{B}/k{k}"
+        tkey = f"{dom}@{args.config}/b{B}/k{k}"
         tpath = os.path.join(ROOT, "profiles", "traffic.json")
         if os.path.exists(tpath):
             rec = json.load(open(tpath)).get(tkey)
-            running = probe_kernel_name(args.probe, B, T, C, mlp)
+            running = site_kernel_name(dom, B, T, C, hid)
             if rec and (running is None or rec["kernel"] == running):
                 roof["traffic"] = rec["traffic_bytes"]
                 roof["traffic_source"] = f"profiles/traffic.json[{tkey}] ({rec['kernel']})"
             elif rec:
                 roof["traffic_source"] = (f"profiles/traffic.json[{tkey}] was measured on {rec['kernel']}, "
                                           f"this build runs {running}: not used")
+        roof["sites"] = {kk: {f: v[f] for f in ("achieved", "frac", "avg_us", "launches_per_pass", "share_of_pass")}
+                         for kk, v in sites.items()}
 
     cpu = None
     if args.cpu_budget > 0:
-        cpu = cpu_baseline(args.config, B, args.keep, args.cpu_budget)
-    flops = depth * (2 * B * T * C * (3 * C + C + 2 * mlp) + 4 * B * H * T * N * (C // H))
+        from oracle.model import CONFIGS
+
+        cfg_name = next(n for n in CONFIGS if n == args.config)
+        blocks = []
+        for blk in ex.model.blocks:
+            blocks.append({kk: v.detach().to("cpu") for kk, v in blk.state_dict().items()})
+        caches = {kk: v.to("cpu") for kk, v in context["cache_feature"].items()
+                  if isinstance(v, torch.Tensor) and (kk.endswith("_kv") or kk.endswith("_blocks_out_sum"))}
+        cpu = cpu_baseline(cfg_name, blocks, context["input_tokens"].cpu(), caches,
+                           context["mobile_pscore_hint_map"].cpu(), k, args.cpu_budget)
+    attn_flops = 4 * B * H * T * N * (C // H)
+    gemm_flops = 2 * B * T * C * (4 * C + (2 if ffn == "mlp" else 3) * hid)
+    flops = depth * (gemm_flops + attn_flops)
     line = {
         "metric": METRIC, "value": round(value, 1), "unit": "corrected tokens/s", "n_gpus": 1,
         "steps": args.steps, "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
         "scaling": "weak", "vs_baseline": None, "dtype": "bf16", "data": "synthetic",
         "config": {"workload": f"dinov3_{args.config}_correction", "batch": B, "tokens_per_image": N,
-                   "keep_ratio": args.keep, "k": k, "selected_rows": B * T, "blocks": depth,
+                   "keep_ratio": keep, "k": k, "selected_rows": B * T, "blocks": depth,
+                   "correct_precision": args.precision,
                    "pass_tflop": round(flops / 1e12, 4), "pass_tflops_achieved": round(flops / (ms / 1e3) / 1e12, 1),
                    "wall_ms_per_step": round(wall * 1e3 / args.steps, 4),
                    "launch": "hip_graph" if args.graph else "eager",

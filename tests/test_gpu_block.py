@@ -16,6 +16,7 @@ import pytest
 import torch
 
 from appcorr_amd.dinov3 import SelfAttentionBlock, dinov3_backbone
+from appcorr_amd.dinov3.layers import correct_blocks_packed
 from oracle import model as OM
 from oracle import plan as OP
 from tests.util import assert_bits_equal, assert_propagated_close, bf16_ulp, close_stats
@@ -78,6 +79,74 @@ def test_single_block_identical_inputs(dev, name, B, ratio):
                             what="blocks_out_sum")
     assert_bits_equal(gcache["_partial_token_query_plan_cache"][next(iter(gcache["_partial_token_query_plan_cache"]))]
                       .update_indice, plan.update_indice, "update_indice")
+
+
+def test_vit7b_block_identical_inputs(dev):
+    """ViT-7B widths (C = 4096, 32 heads of 128, SwiGLU hidden 8192, no qkv bias) at 1024 px (N = 4101),
+    B = 1, keep 10 % (k = 409, T = 414): one block fed the same synthetic cache on both sides (the fp64
+    approx pass over 4101 tokens of this width is too heavy for the CPU oracle), against the fp64
+    oracle; then two blocks run packed equal two blocks run one by one, bit for bit.
+
+    At this width a last-bit difference anywhere (the attention's bf16 probabilities, an fp32
+    accumulation order over K = 4096 or 8192) reaches about half of the output roundings through the
+    SwiGLU and the 8192-deep w3 reduction, so the selected rows are held to the yardstick of the
+    reference's own bf16 op sequence (torch's CPU kernels, the oracle's "bf16" mode) on the same inputs:
+    no further from the fp64 oracle than twice that sequence's own distance."""
+    cfg = OM.CONFIGS["vit7b16_1024"]
+    B, ratio = 1, 0.1
+    N, C, H, D, P = cfg.num_tokens, cfg.dim, cfg.heads, cfg.head_dim, cfg.num_patches
+    print("vit7b block B=1 N=4101 keep=0.1", flush=True)
+    weights = OM.make_block_weights(cfg, 0, gamma=1.0, bias_std=0.05, ln_std=0.1, depth=2)
+    g = torch.Generator().manual_seed(5)
+    x_full = torch.randn(B, N, C, generator=g).to(torch.bfloat16)
+    cache = {}
+    for i in range(2):
+        cache[f"layer{i}_kv"] = torch.randn(B, N, 2, H, D, generator=g).to(torch.bfloat16)
+        cache[f"layer{i}_blocks_out_sum"] = (torch.randn(B, N, C, generator=g) * 0.1).to(torch.bfloat16)
+    imp = torch.rand(B, P, generator=g)
+    rope = OM.rope_tables(cfg)
+    k = OP.keep_count(P, ratio)
+    dind = OM.full_dindice(cfg, B)
+    plan = OP.build_plan(imp.numpy(), k, dind.numpy(), cfg.num_pretokens, N)
+    x_ref, cache_ref = OM.correct_block(cfg, weights[0], x_full, plan, rope,
+                                        {k_: v.clone() for k_, v in cache.items()}, "layer0")
+    blocks = _gpu_blocks(cfg, weights, dev)
+    r = (rope[0].to(dev), rope[1].to(dev))
+    kw = dict(token_keep_ratio=ratio, mobile_pscore_hint=imp.to(dev), **KW)
+    gcache = _gpu_cache(cache, dev)
+    with torch.no_grad():
+        x_got, gcache = blocks[0].correct(x_full.to(dev), dind.to(dev), r, gcache, "layer0", **kw)
+    sel = np.zeros((B, N), dtype=bool)
+    sel[plan.active_batch_idx, plan.active_token_idx] = True
+    assert int(sel.sum()) == B * (5 + k)
+    st = torch.from_numpy(sel)
+    assert_bits_equal(x_got.cpu()[~st], x_ref[~st], "unselected rows")
+    assert_bits_equal(gcache["layer0_kv"].cpu()[~st], cache["layer0_kv"][~st], "unselected K/V rows")
+    x16, cache16 = OM.correct_block(cfg, weights[0], x_full, plan, rope,
+                                    {k_: v.clone() for k_, v in cache.items()}, "layer0", mode="bf16")
+    for what, got, ref, eager in (("x_out", x_got.cpu()[st], x_ref[st], x16[st]),
+                                  ("kv", gcache["layer0_kv"].cpu()[st], cache_ref["layer0_kv"][st],
+                                   cache16["layer0_kv"][st]),
+                                  ("bos", gcache["layer0_blocks_out_sum"].cpu()[st],
+                                   cache_ref["layer0_blocks_out_sum"][st], cache16["layer0_blocks_out_sum"][st])):
+        mx, mean = close_stats(got, ref)
+        mx16, mean16 = close_stats(eager, ref)
+        print(f"  {what}: gpu vs fp64 max {mx:.4g} mean {mean:.4g}; bf16 eager vs fp64 max {mx16:.4g} "
+              f"mean {mean16:.4g}", flush=True)
+        assert mean <= 2.0 * mean16 + 1e-6, f"{what}: mean {mean:.4g} vs eager {mean16:.4g}"
+        assert mx <= 2.0 * mx16 + 2.0 ** -7 * float(ref.float().abs().max()), f"{what}: max {mx:.4g} vs {mx16:.4g}"
+    # two blocks: the packed run (the executor's path for a shared plan) equals the per-block path
+    ca, cb = _gpu_cache(cache, dev), _gpu_cache(cache, dev)
+    dd = dind.to(dev)
+    with torch.no_grad():
+        xa, ca = correct_blocks_packed(blocks, x_full.to(dev), dd, r, ca, ["layer0", "layer1"], **kw)
+        xb = x_full.to(dev)
+        for i, blk in enumerate(blocks):
+            xb, cb = blk.correct(xb, dd, r, cb, f"layer{i}", **kw)
+    assert_bits_equal(xa, xb.cpu(), "packed x_out")
+    for i in range(2):
+        for key in (f"layer{i}_kv", f"layer{i}_blocks_out_sum"):
+            assert_bits_equal(ca[key], cb[key].cpu(), f"packed {key}")
 
 
 def _run_pass(cfg, weights, x_base, x_full, imp, rope, ratio, dev, B):

@@ -51,7 +51,8 @@ def _check_gemm(dev, got, x, w, b, what):
 @pytest.mark.parametrize("M,N,Kd", [(4176, 3072, 1024), (4176, 1024, 1024), (4176, 4096, 1024), (4176, 1024, 4096),
                                     (103, 1152, 384), (1, 64, 64), (130, 192, 128), (1656, 8192, 4096),
                                     (1712, 3072, 1024), (1712, 4096, 1024), (8272, 3072, 1024), (8272, 4096, 1024),
-                                    (1656, 12288, 4096), (1656, 4096, 4096), (1656, 4096, 8192)])
+                                    (1656, 12288, 4096), (1656, 4096, 4096), (1656, 4096, 8192),
+                                    (414, 12288, 4096), (414, 4096, 4096), (414, 8192, 4096), (414, 4096, 8192)])
 def test_linear_bias(dev, M, N, Kd):
     x, w, b = _rand((M, Kd), 1), _rand((N, Kd), 2, 0.02), _rand((N,), 3, 0.1)
     got = K.linear(x.to(dev), w.to(dev), b.to(dev))
@@ -112,9 +113,10 @@ def test_linear_layerscale(dev):
     assert_bits_equal(got, F64.mul(base, g), "fc2+ls")
 
 
-def test_linear_silu_mul(dev):
-    xd, wd, bd, base = _epi_case(dev, 600, 1024, 512, 18)
-    x2 = _rand((600, 1024), 21)
+@pytest.mark.parametrize("M,N,Kd", [(600, 1024, 512), (414, 8192, 4096)])
+def test_linear_silu_mul(dev, M, N, Kd):
+    xd, wd, bd, base = _epi_case(dev, M, N, Kd, 18)
+    x2 = _rand((M, N), 21)
     got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_SILU_MUL, resid=x2.to(dev))
     assert_bf16_close(got, F64.silu_mul(base, x2), max_ulps=1, max_frac_off=1e-3, what="swiglu")
 
@@ -184,7 +186,8 @@ def test_qkv_rope_kv_scatter_bit_exact(dev, B, T, H, D):
 
 
 @pytest.mark.parametrize("B,T,H,D,Kd", [(16, 261, 16, 64, 1024), (1, 103, 6, 64, 384), (2, 50, 32, 128, 512),
-                                        (16, 107, 16, 64, 1024), (16, 517, 16, 64, 1024), (4, 414, 32, 128, 4096)])
+                                        (16, 107, 16, 64, 1024), (16, 517, 16, 64, 1024), (4, 414, 32, 128, 4096),
+                                        (1, 414, 32, 128, 4096)])
 def test_linear_qkv_rope_kv_fused_equals_unfused(dev, B, T, H, D, Kd):
     """The fused QKV GEMM (qkv never materialised). Its raw bf16(acc + bias) values, taken from a run
     with no patch rows (no RoPE), are checked against the fp64 oracle like every GEMM; the pinned
@@ -235,7 +238,8 @@ def _check_attention(got, qb, kv, scale, ref, what):
 
 @pytest.mark.parametrize("B,T,N,H,D", [(16, 261, 1029, 16, 64), (1, 103, 201, 6, 64), (2, 1029, 1029, 16, 64),
                                        (2, 7, 70, 4, 64), (1, 100, 4101, 32, 128), (3, 64, 64, 2, 64),
-                                       (2, 269, 333, 4, 64), (1, 272, 1029, 3, 64)])
+                                       (2, 269, 333, 4, 64), (1, 272, 1029, 3, 64), (1, 414, 4101, 32, 128),
+                                       (4, 414, 4101, 32, 128)])
 def test_sparse_query_attention(dev, B, T, N, H, D):
     q = _rand((B * T, H, D), 28)
     kv = _rand((B, N, 2, H, D), 29)
