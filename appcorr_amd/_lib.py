@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be loaded before the HIP library, see module docstring
 
 LIB_PATH = Path(__file__).resolve().parent / "liboudjat_hip.so"
-ABI_VERSION = 6
+ABI_VERSION = 7
 
 OK = 0
 STATUS_NAMES = {
@@ -79,13 +79,13 @@ SIGNATURES: dict[str, list] = {
     "oudjat_rope_active_inplace": [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "oudjat_qkv_rope_kv_scatter": [_p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _p, _p],
     "oudjat_layernorm_rows": [_p, _i64, _i64, _i64, _p, _p, _f32, _p, _i64, _p],
-    "oudjat_linear_bf16": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i32, _p, _p, _i64, _p, _i64, _p],
+    "oudjat_linear_bf16": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i32, _p, _p, _i64, _p, _i64, _f32, _p],
     "oudjat_linear_kernel_name": [_i64, _i64, _i64, _i32, ctypes.c_char_p, _i64],
     "oudjat_packed_residual_persist": [_p, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p],
     "oudjat_packed_residual_persist_ln": [_p, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _f32, _p, _p],
     "oudjat_fold_residual_rows": [_p, _i64, _i64, _p, _p, _p, _i64, _p, _p],
     "oudjat_linear_qkv_rope_kv": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p, _p,
-                                  _i64, _i64, _p, _p],
+                                  _i64, _i64, _p, _f32, _p],
     "oudjat_sparse_query_attention": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32, _p,
                                       _i64, _p],
     "oudjat_nvfp4_quantize": [_p, _i64, _i64, _i64, _p, _p, _p, _p],
@@ -93,6 +93,11 @@ SIGNATURES: dict[str, list] = {
     "oudjat_query_attention_prob": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p, _p, _i64,
                                     _i32, _p],
     "oudjat_pseudo_query": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
+    "oudjat_nvfp4_quantize_dequantize": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p],
+    "oudjat_fp8_quantize_dequantize": [_p, _i64, _i64, _i64, _p, _i32, _p, _i64, _p],
+    "oudjat_scale_bias_rows": [_p, _i64, _i64, _i64, _f32, _p, _p, _p, _i64, _p],
+    "oudjat_swiglu_scaled": [_p, _f32, _p, _p, _f32, _p, _i64, _i64, _p, _p],
+    "oudjat_amax_update": [_p, _i64, _i64, _i64, _p, _p],
     "oudjat_query_attention_prob_noalloc": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p,
                                             _i64, _i32, _p],
 }

@@ -63,12 +63,16 @@ struct QkvArgs {
   uint16_t* q_out;
 };
 
+// The first rounding point of every epilogue is v = bf16(acc * acc_scale + bias) (one fp32 rounding:
+// with acc_scale = 1 exactly bf16(acc + bias)); acc_scale carries the per-tensor factors of an FP8
+// GEMM, which apply to the fp32 accumulator before its rounding.
 struct EpiArgs {
   const uint16_t* bias;
   const uint16_t* gamma;
   const uint16_t* resid;
   int64_t ldr;
   QkvArgs qkv;
+  float acc_scale;
 };
 
 // Two fp32 -> packed bf16 pair (low half = a) with the hardware round-to-nearest-even convert.
@@ -117,9 +121,7 @@ __device__ __forceinline__ uint32_t gelu_pair_bits(uint32_t w, const uint16_t* l
 
 template <int EPI>
 __device__ __forceinline__ float epilogue(float acc, int64_t row, int64_t col, const EpiArgs& ea) {
-  float v = acc;
-  if (ea.bias) v += bf16_to_f32(ea.bias[col]);
-  v = round_bf16(v);
+  float v = round_bf16(__builtin_fmaf(acc, ea.acc_scale, ea.bias ? bf16_to_f32(ea.bias[col]) : 0.0f));
   if (EPI == OUDJAT_EPI_BIAS_GELU) {
     v = __uint_as_float(gelu_bf16_bits(__float_as_uint(v) >> 16, g_gelu_lut) << 16);
   } else if (EPI == OUDJAT_EPI_BIAS_LS_RESID) {
@@ -485,8 +487,10 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FM][FN], unsign
       for (int i = 0; i < FM; ++i) {
         const int rl = wm0 + i * 32 + (lane & 31);
         uint2 w;
-        w.x = cvt_pk_bf16(acc[i][j][4 * g + 0] + b0, acc[i][j][4 * g + 1] + b1);
-        w.y = cvt_pk_bf16(acc[i][j][4 * g + 2] + b2, acc[i][j][4 * g + 3] + b3);
+        w.x = cvt_pk_bf16(__builtin_fmaf(acc[i][j][4 * g + 0], ea.acc_scale, b0),
+                          __builtin_fmaf(acc[i][j][4 * g + 1], ea.acc_scale, b1));
+        w.y = cvt_pk_bf16(__builtin_fmaf(acc[i][j][4 * g + 2], ea.acc_scale, b2),
+                          __builtin_fmaf(acc[i][j][4 * g + 3], ea.acc_scale, b3));
         *reinterpret_cast<uint2*>(ct + rl * LDT + cl) = w;
       }
     }
@@ -937,8 +941,8 @@ __device__ __forceinline__ void r16_epilogue(f32x4_t (&acc)[FMB][FNB], unsigned 
 #pragma unroll
       for (int i = 0; i < FMB; ++i) {
         uint2 w;
-        w.x = cvt_pk_bf16(acc[i][j][0] + b0, acc[i][j][1] + b1);
-        w.y = cvt_pk_bf16(acc[i][j][2] + b2, acc[i][j][3] + b3);
+        w.x = cvt_pk_bf16(__builtin_fmaf(acc[i][j][0], ea.acc_scale, b0), __builtin_fmaf(acc[i][j][1], ea.acc_scale, b1));
+        w.y = cvt_pk_bf16(__builtin_fmaf(acc[i][j][2], ea.acc_scale, b2), __builtin_fmaf(acc[i][j][3], ea.acc_scale, b3));
         *reinterpret_cast<uint2*>(ct + (wm * WM + i * 16 + (lane & 15)) * LDT + cl) = w;
       }
     }
@@ -969,8 +973,10 @@ __device__ __forceinline__ void r16_epilogue(f32x4_t (&acc)[FMB][FNB], unsigned 
         for (int i = 0; i < HB; ++i) {
           if (rb0 + i >= FMB) continue;
           uint2 w;
-          w.x = cvt_pk_bf16(acc[i][j][0] + b0, acc[i][j][1] + b1);
-          w.y = cvt_pk_bf16(acc[i][j][2] + b2, acc[i][j][3] + b3);
+          w.x = cvt_pk_bf16(__builtin_fmaf(acc[i][j][0], ea.acc_scale, b0),
+                            __builtin_fmaf(acc[i][j][1], ea.acc_scale, b1));
+          w.y = cvt_pk_bf16(__builtin_fmaf(acc[i][j][2], ea.acc_scale, b2),
+                            __builtin_fmaf(acc[i][j][3], ea.acc_scale, b3));
           *reinterpret_cast<uint2*>(ct + ((rb0 + i) * 16 + (lane & 15)) * LDT + cl) = w;
         }
       }
@@ -1612,7 +1618,7 @@ using namespace oudjat;
 
 extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W, int64_t N,
                                   int64_t ldw, const uint16_t* bias, int epi, const uint16_t* gamma,
-                                  const uint16_t* resid, int64_t ldr, uint16_t* C, int64_t ldc,
+                                  const uint16_t* resid, int64_t ldr, uint16_t* C, int64_t ldc, float acc_scale,
                                   oudjat_stream_t stream) {
   OUDJAT_REQUIRE(M >= 0 && N >= 0 && K >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_bf16: negative size");
   OUDJAT_REQUIRE(epi >= OUDJAT_EPI_BIAS && epi <= OUDJAT_EPI_BIAS_SILU_MUL, OUDJAT_ERR_INVALID_ARGUMENT,
@@ -1638,6 +1644,7 @@ extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64
   ea.gamma = gamma;
   ea.resid = resid;
   ea.ldr = ldr;
+  ea.acc_scale = acc_scale;
   return launch_gemm(choose_cfg(M, N, K, aligned_io), A, M, K, lda, W, N, ldw, epi, ea, C, ldc, as_stream(stream),
                      "linear_bf16");
 }
@@ -1648,7 +1655,7 @@ extern "C" int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K
                                          const uint8_t* patch_mask, const int64_t* rope_idx,
                                          const int64_t* batch_idx, const int64_t* token_idx, uint16_t* kv,
                                          int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
-                                         oudjat_stream_t stream) {
+                                         float acc_scale, oudjat_stream_t stream) {
   OUDJAT_REQUIRE(M >= 0 && K >= 0 && H > 0 && Dh > 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_qkv_rope_kv: bad size");
   if (M == 0) return OUDJAT_OK;
   const int64_t N = 3 * H * Dh;
@@ -1668,6 +1675,7 @@ extern "C" int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K
                  "linear_qkv_rope_kv: dimensions must fit in int32");
   EpiArgs ea{};
   ea.bias = bias;
+  ea.acc_scale = acc_scale;
   ea.qkv = QkvArgs{(int)H, (int)Dh, sin_table, cos_table, table_stride, patch_mask, rope_idx, batch_idx, token_idx,
                    kv, kv_stride_b, kv_stride_n, q_out};
   return launch_gemm(choose_qkv_cfg(M, N, K, Dh), A, M, K, lda, W, N, ldw, kEpiQkv, ea, nullptr, 0, as_stream(stream),

@@ -118,10 +118,16 @@ __device__ __forceinline__ uint32_t nvfp4_codes8(const float* f, float tot, floa
 // and write its 32 CT bytes of codes (8 each). The block scale is computed once per block; the 4
 // scale bytes of a row within a scale tile are contiguous in the swizzled layout and go to LDS as one
 // word from the tile's first lane of the row; the CT finished tiles are stored at the end.
-template <int CT>
+//
+// XH: also write xh[row, col] = e2m1(code) * e4m3(scale) as bf16 -- the block-scaled value without the
+// tensor scale, exact in bf16 (at most 2 + 4 significant bits, magnitudes 2^-10 .. 2688): the operand
+// a bf16 MFMA GEMM multiplies in place of the packed tensor, as a block-scaled FP4 GEMM does. qd / sc
+// may then be NULL (only xh written).
+template <int CT, bool XH>
 __global__ __launch_bounds__(256) void nvfp4_quantize_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t K,
                                                              int64_t sm, const float* __restrict__ tsp,
-                                                             uint8_t* __restrict__ qd, uint8_t* __restrict__ sc) {
+                                                             uint8_t* __restrict__ qd, uint8_t* __restrict__ sc,
+                                                             uint16_t* __restrict__ xh, int64_t xs) {
   constexpr int LPR = 4 * CT;        // lanes per row
   constexpr int RPP = 256 / LPR;     // rows per pass
   const int pm = blockIdx.y;
@@ -154,12 +160,33 @@ __global__ __launch_bounds__(256) void nvfp4_quantize_kernel(const uint16_t* __r
     nvfp4_block_scale(amax, ts, code, tot);
     const float y = 1.0f / tot;
     const uint32_t w0 = nvfp4_codes8(f, tot, y), w1 = nvfp4_codes8(f + 8, tot, y);
-    if (ok) *reinterpret_cast<uint2*>(qd + row * (K >> 1) + (col >> 1)) = make_uint2(w0, w1);
+    if (ok && qd) *reinterpret_cast<uint2*>(qd + row * (K >> 1) + (col >> 1)) = make_uint2(w0, w1);
+    if constexpr (XH) {
+      if (ok) {
+        const float s = e4m3_decode(code);
+        float h[16];
+#pragma unroll
+        for (int half = 0; half < 2; ++half) {
+          const uint32_t w = half ? w1 : w0;
+          const auto v0 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 0);
+          const auto v1 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 1);
+          const auto v2 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 2);
+          const auto v3 = __builtin_amdgcn_cvt_scalef32_pk_f32_fp4(w, 1.0f, 3);
+          const float e2[8] = {v0[0], v0[1], v1[0], v1[1], v2[0], v2[1], v3[0], v3[1]};
+#pragma unroll
+          for (int e = 0; e < 8; ++e) h[half * 8 + e] = e2[e] * s;
+        }
+        uint4* d = reinterpret_cast<uint4*>(xh + row * xs + col);
+        d[0] = pack8(h);
+        d[1] = pack8(h + 8);
+      }
+    }
     // Scale bytes of the row's 4 blocks of this tile (zero for blocks past K or rows past M).
     const uint32_t b = ok ? code : 0u;
     const uint32_t b1 = __shfl_down(b, 1, 64), b2 = __shfl_down(b, 2, 64), b3 = __shfl_down(b, 3, 64);
     if ((j & 3) == 0) sscale[(j / 4) * 128 + (r & 31) * 4 + (r >> 5)] = b | (b1 << 8) | (b2 << 16) | (b3 << 24);
   }
+  if (!sc) return;  // uniform over the workgroup
   // The workgroup's CT scale tiles (512 bytes each, consecutive in the swizzled layout) leave as
   // whole 16-byte stores instead of 4-byte pieces spread over the passes.
   __syncthreads();
@@ -248,10 +275,35 @@ extern "C" int oudjat_nvfp4_quantize(const uint16_t* x, int64_t M, int64_t K, in
   const int ct = nvfp4_tiles_per_wg(M, K);
   dim3 grid((unsigned)cdiv(K, 64 * ct), (unsigned)cdiv(M, 128));
   hipStream_t st = as_stream(stream);
-  if (ct == 4) nvfp4_quantize_kernel<4><<<grid, 256, 0, st>>>(x, M, K, sm, ts, qdata, scales);
-  else if (ct == 2) nvfp4_quantize_kernel<2><<<grid, 256, 0, st>>>(x, M, K, sm, ts, qdata, scales);
-  else nvfp4_quantize_kernel<1><<<grid, 256, 0, st>>>(x, M, K, sm, ts, qdata, scales);
+  if (ct == 4) nvfp4_quantize_kernel<4, false><<<grid, 256, 0, st>>>(x, M, K, sm, ts, qdata, scales, nullptr, 0);
+  else if (ct == 2) nvfp4_quantize_kernel<2, false><<<grid, 256, 0, st>>>(x, M, K, sm, ts, qdata, scales, nullptr, 0);
+  else nvfp4_quantize_kernel<1, false><<<grid, 256, 0, st>>>(x, M, K, sm, ts, qdata, scales, nullptr, 0);
   return check_launch("nvfp4_quantize");
+}
+
+extern "C" int oudjat_nvfp4_quantize_dequantize(const uint16_t* x, int64_t M, int64_t K, int64_t sm,
+                                                const float* ts, uint8_t* qdata, uint8_t* scales, uint16_t* xhat,
+                                                int64_t xhat_stride, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(M >= 0 && K >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "nvfp4_quantize_dequantize: negative size");
+  OUDJAT_REQUIRE(K % 16 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE,
+                 "nvfp4_quantize_dequantize: K=%lld must be a multiple of 16", (long long)K);
+  if (M == 0 || K == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(x && ts && xhat && ((qdata == nullptr) == (scales == nullptr)), OUDJAT_ERR_INVALID_ARGUMENT,
+                 "nvfp4_quantize_dequantize: null pointer (qdata and scales are given together or not at all)");
+  OUDJAT_REQUIRE(sm % 8 == 0 && sm >= K && aligned(x, 16) && xhat_stride % 8 == 0 && xhat_stride >= K &&
+                     aligned(xhat, 16) && (!qdata || (aligned(qdata, 8) && aligned(scales, 4))),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "nvfp4_quantize_dequantize: 16-byte aligned rows required");
+  OUDJAT_REQUIRE(cdiv(M, 128) < 65536, OUDJAT_ERR_TOO_LARGE, "nvfp4_quantize_dequantize: M too large");
+  const int ct = nvfp4_tiles_per_wg(M, K);
+  dim3 grid((unsigned)cdiv(K, 64 * ct), (unsigned)cdiv(M, 128));
+  hipStream_t st = as_stream(stream);
+  if (ct == 4)
+    nvfp4_quantize_kernel<4, true><<<grid, 256, 0, st>>>(x, M, K, sm, ts, qdata, scales, xhat, xhat_stride);
+  else if (ct == 2)
+    nvfp4_quantize_kernel<2, true><<<grid, 256, 0, st>>>(x, M, K, sm, ts, qdata, scales, xhat, xhat_stride);
+  else
+    nvfp4_quantize_kernel<1, true><<<grid, 256, 0, st>>>(x, M, K, sm, ts, qdata, scales, xhat, xhat_stride);
+  return check_launch("nvfp4_quantize_dequantize");
 }
 
 extern "C" int oudjat_nvfp4_dequantize(const uint8_t* qdata, const uint8_t* scales, const float* ts, int64_t M,

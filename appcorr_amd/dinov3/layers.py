@@ -34,6 +34,26 @@ from torch import Tensor, nn
 
 from .. import _lib
 from .. import kernels as K
+from . import lowp as LP
+
+
+def _linear_route(mod: nn.Module, x: Tensor, site: str, *, bias: Tensor | None = None, **kw) -> Tensor:
+    """One correction linear on its route: FP8 (the e4m3 operand as exact bf16 values, the per-tensor
+    scales on the fp32 accumulator; fp8_fast_linear.py:174-196) when `mod` is a frozen FastFP8Linear,
+    else bf16 -- a plain nn.Linear, or a low-precision linear still calibrating, whose observer sees
+    the input first (fp4_fast_linear.py:255-259). `bias` overrides mod.bias (the masked qkv bias)."""
+    b = mod.bias if bias is None else bias
+    if LP.low_precision_state(mod) == "fp8":
+        return K.linear(mod.quantize(x), mod.weight_hat, b, site=site, acc_scale=mod.acc_scale_f, **kw)
+    if isinstance(mod, LP._LowPrecisionLinear):
+        mod.observe(x)
+    return K.linear(x, mod.weight, b, site=site, **kw)
+
+
+def _fp4_raw(mod: "LP.FastFP4Linear", x: Tensor, site: str):
+    """A frozen FastFP4Linear's torch._scaled_mm output bf16(x_hat . W_hat^T) with the factors of its
+    epilogue: (raw, out_scale, bias) (fp4_fast_linear.py:221-249)."""
+    return mod.forward_raw(x, site=site), mod.out_scale_f, mod.bias
 
 
 # ------------------------------------------------------------------------------------------------
@@ -163,7 +183,10 @@ class SelfAttention(nn.Module):
         """
         kv = cache_feature[f"{tag}_kv"]
         q_packed, attn = self._qkv_attention(x_sel, rope, kv, fixed_query_state)
-        out = K.linear(attn, self.proj.weight, self.proj.bias, site="proj")
+        if LP.low_precision_state(self.proj) == "fp4":
+            out = K.scale_bias(*_fp4_raw(self.proj, attn, "proj"))
+        else:
+            out = _linear_route(self.proj, attn, "proj")
         return out, cache_feature
 
     def _qkv_attention(self, xn: Tensor, rope, kv: Tensor, qs: PackedQueryState):
@@ -174,11 +197,25 @@ class SelfAttention(nn.Module):
             raise ValueError(f"packed rows {M} do not split evenly over {B} images")
         T = M // B
         q = torch.empty((M, H, D), device=xn.device, dtype=torch.bfloat16)
-        if K.qkv_fusable(H, D):
-            K.linear_qkv_rope_kv(xn, self.qkv.weight, self.qkv_bias(), rope, qs.active_patch_mask, qs.active_rope_idx,
-                                 qs.active_batch_idx, qs.active_token_idx, kv, q)
+        mod = self.qkv
+        state = LP.low_precision_state(mod)
+        if state == "fp4":
+            # NVFP4: raw GEMM output, then scale and bias (fp4_fast_linear.py:251-283), then RoPE / K-V
+            raw, s, b = _fp4_raw(mod, xn, "qkv")
+            qkv = K.scale_bias(raw, s, b, out=raw)
+        elif K.qkv_fusable(H, D):
+            if state == "fp8":
+                a, w, s = mod.quantize(xn), mod.weight_hat, mod.acc_scale_f
+            else:
+                if isinstance(mod, LP._LowPrecisionLinear):
+                    mod.observe(xn)
+                a, w, s = xn, mod.weight, 1.0
+            K.linear_qkv_rope_kv(a, w, self.qkv_bias(), rope, qs.active_patch_mask, qs.active_rope_idx,
+                                 qs.active_batch_idx, qs.active_token_idx, kv, q, acc_scale=s)
+            qkv = None
         else:
-            qkv = K.linear(xn, self.qkv.weight, self.qkv_bias(), site="qkv")
+            qkv = _linear_route(mod, xn, "qkv", bias=self.qkv_bias())
+        if qkv is not None:
             K.qkv_rope_kv_scatter(qkv.view(M, 3, H, D), rope, qs.active_patch_mask, qs.active_rope_idx,
                                   qs.active_batch_idx, qs.active_token_idx, kv, q)
         attn = K.sparse_query_attention(q, kv, T, self.scale)
@@ -235,14 +272,27 @@ class SelfAttentionBlock(nn.Module):
         return self._ones
 
     def _mlp_scaled(self, xn: Tensor) -> Tensor:
-        """gamma2 * MLP(xn) with GELU / SwiGLU and LayerScale fused into the GEMM epilogues."""
+        """gamma2 * MLP(xn) with GELU / SwiGLU and LayerScale fused into the GEMM epilogues; the SwiGLU
+        linears in their low-precision route when the block is a converted view (dinov3/lowp.py)."""
         g2 = self._gamma(self.ls2, xn)
         if isinstance(self.mlp, Mlp):
             h = K.linear(xn, self.mlp.fc1.weight, self.mlp.fc1.bias, epilogue=_lib.EPI_BIAS_GELU, site="fc1")
             return K.linear(h, self.mlp.fc2.weight, self.mlp.fc2.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g2, site="fc2")
-        x2 = K.linear(xn, self.mlp.w2.weight, self.mlp.w2.bias, site="w2")
-        h = K.linear(xn, self.mlp.w1.weight, self.mlp.w1.bias, epilogue=_lib.EPI_BIAS_SILU_MUL, resid=x2, site="w1")
-        return K.linear(h, self.mlp.w3.weight, self.mlp.w3.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g2, site="w3")
+        w1, w2, w3 = self.mlp.w1, self.mlp.w2, self.mlp.w3
+        states = {LP.low_precision_state(m) for m in (w1, w2, w3)}
+        if "fp4" in states:
+            if states != {"fp4"}:
+                raise RuntimeError("SwiGLU linears partially calibrated: freeze all three NVFP4 linears together")
+            # ffn_layers.py:84-115 with FastFP4Linear: both epilogues folded into the SwiGLU kernel
+            # (token_update.py:620-669), then w3 with its scale-and-bias and the LayerScale.
+            r1, s1, b1 = _fp4_raw(w1, xn, "w1")
+            r2, s2, b2 = _fp4_raw(w2, xn, "w2")
+            h = K.swiglu_scaled(r1, s1, b1, r2, s2, b2)
+            r3, s3, b3 = _fp4_raw(w3, h, "w3")
+            return K.scale_bias(r3, s3, b3, gamma=g2, out=r3)
+        x2 = _linear_route(w2, xn, "w2")
+        h = _linear_route(w1, xn, "w1", epilogue=_lib.EPI_BIAS_SILU_MUL, resid=x2)
+        return _linear_route(w3, h, "w3", epilogue=_lib.EPI_BIAS_LS, gamma=g2)
 
     # -- dispatch (block.py:274-310) --------------------------------------------------------------
 
@@ -556,9 +606,13 @@ class SelfAttentionBlock(nn.Module):
         if xn is None:
             xn = K.layer_norm(x_act, self.norm1.weight, self.norm1.bias, self.norm1.eps)   # block.py:1114
         _, attn = self.attn._qkv_attention(xn, rope, kv, qs)                         # attention.py:415-523
-        x_attn = K.linear(attn, self.attn.proj.weight, self.attn.proj.bias,          # attention.py:532 +
-                          epilogue=_lib.EPI_BIAS_LS_RESID, gamma=self._gamma(self.ls1, x_act),
-                          resid=x_act, site="proj")                                  # block.py:1129-1134
+        g1 = self._gamma(self.ls1, x_act)
+        proj = self.attn.proj
+        if LP.low_precision_state(proj) == "fp4":                                    # proj_precision "fp4"
+            x_attn = K.fused_layerscale_add(x_act, K.scale_bias(*_fp4_raw(proj, attn, "proj")), g1)
+        else:
+            x_attn = _linear_route(proj, attn, "proj", epilogue=_lib.EPI_BIAS_LS_RESID,  # attention.py:532 +
+                                   gamma=g1, resid=x_act)                             # block.py:1129-1134
         mlp = self._mlp_scaled(K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps))  # :1141
         return x_attn, mlp
 

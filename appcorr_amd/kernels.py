@@ -440,10 +440,12 @@ def qkv_fusable(H: int, Dh: int) -> bool:
 
 def linear_qkv_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, rope,
                        patch_mask: torch.Tensor, rope_idx: torch.Tensor, batch_idx: torch.Tensor,
-                       token_idx: torch.Tensor, kv_cache: torch.Tensor, q_out: torch.Tensor) -> None:
+                       token_idx: torch.Tensor, kv_cache: torch.Tensor, q_out: torch.Tensor,
+                       acc_scale: float = 1.0) -> None:
     """One kernel for attention.py:415-454: qkv = x . weight^T + bias, RoPE on q and k of patch rows,
     k and v written into kv_cache [B, N, 2, H, Dh] rows (b, t) in place, q written to q_out [M, H, Dh].
-    The qkv tensor itself is never materialised."""
+    The qkv tensor itself is never materialised. `acc_scale` multiplies the fp32 accumulator before
+    its first rounding (an FP8 GEMM's per-tensor scales)."""
     sin, cos = rope
     _require_cuda(x, weight, bias, patch_mask, rope_idx, batch_idx, token_idx, kv_cache, q_out, sin, cos)
     M, Kd = x.shape
@@ -460,7 +462,7 @@ def linear_qkv_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor
             _ptr(None if bias is None else bias.contiguous()), H, Dh, _ptr(sin), _ptr(cos), sin.stride(0),
             _ptr(patch_mask), _ptr(_index(rope_idx, "rope_idx")), _ptr(_index(batch_idx, "batch_idx")),
             _ptr(_index(token_idx, "token_idx")), _ptr(kv_cache), kv_cache.stride(0), kv_cache.stride(1), _ptr(q_out),
-            _stream(x))
+            float(acc_scale), _stream(x))
 
 
 # ------------------------------------------------------------------------------------------------
@@ -477,9 +479,10 @@ def linear_kernel_name(M: int, N: int, K: int, epilogue: int = _lib.EPI_BIAS) ->
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
            epilogue: int = _lib.EPI_BIAS, gamma: torch.Tensor | None = None, resid: torch.Tensor | None = None,
-           out: torch.Tensor | None = None, site: str = "linear") -> torch.Tensor:
+           out: torch.Tensor | None = None, site: str = "linear", acc_scale: float = 1.0) -> torch.Tensor:
     """bf16 x[..., K] . weight[N, K]^T with a fused epilogue (see include/oudjat.h). `site` names the
-    launch for the timing probe ("proj", "fc1", "fc2", "w1", "w2", "w3", ...)."""
+    launch for the timing probe ("proj", "fc1", "fc2", "w1", "w2", "w3", ...). `acc_scale` multiplies
+    the fp32 accumulator before the epilogue's first rounding (an FP8 GEMM's per-tensor scales)."""
     _require_cuda(x, weight, bias, gamma, resid, out)
     _require(x.dtype == weight.dtype == torch.bfloat16, "linear: bf16 only")
     K = x.shape[-1]
@@ -498,7 +501,7 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     _launch(site, x, "oudjat_linear_bf16", _ptr(x2), M, K, x2.stride(0), _ptr(weight), N, weight.stride(0),
          _ptr(None if bias is None else bias.contiguous()), int(epilogue),
          _ptr(None if gamma is None else gamma.contiguous()), _ptr(r2), 0 if r2 is None else r2.stride(0), _ptr(o2),
-         o2.stride(0), _stream(x))
+         o2.stride(0), float(acc_scale), _stream(x))
     return out
 
 
@@ -603,6 +606,90 @@ def dequantize_nvfp4(qdata: torch.Tensor, scale: torch.Tensor, tensor_scale: tor
     out = torch.empty((M, K), device=qdata.device, dtype=torch.bfloat16)
     _launch("nvfp4_dequantize", qdata, "oudjat_nvfp4_dequantize", _ptr(qdata), _ptr(s), _ptr(ts), M, K, _ptr(out), out.stride(0), _stream(qdata))
     return out
+
+
+def _rows_bf16(x: torch.Tensor, what: str) -> torch.Tensor:
+    _require(x.dtype == torch.bfloat16 and x.stride(-1) == 1, f"{what}: bf16 with contiguous rows required")
+    x2 = x.reshape(-1, x.shape[-1])
+    _require(x2.stride(1) == 1, f"{what}: rows must be contiguous")
+    return x2
+
+
+def nvfp4_quantize_dequantize(x: torch.Tensor, tensor_scale: torch.Tensor, *, packed: bool = False):
+    """The NVFP4 operand of an FP4 linear (fp4_fast_linear.py:171-219): xhat = e2m1(q) * e4m3(s), the
+    block-scaled values without the tensor scale, as bf16 [.., K] (exact). With packed=True also
+    returns the reference's (qdata, scales) bytes: (xhat, qdata, scales)."""
+    _require_cuda(x, tensor_scale)
+    x2 = _rows_bf16(x, "nvfp4_quantize_dequantize")
+    M, K = x2.shape
+    _require(K % 16 == 0, f"nvfp4: K must be a multiple of the 16-element block, got {K}")
+    ts = tensor_scale.reshape(1).to(torch.float32)
+    xhat = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16)
+    q = s = None
+    if packed:
+        q = torch.empty((M, K // 2), device=x.device, dtype=torch.uint8)
+        s = torch.empty((nvfp4_scale_numel(M, K),), device=x.device, dtype=torch.uint8)
+    _launch("nvfp4_qdq", x, "oudjat_nvfp4_quantize_dequantize", _ptr(x2), M, K, x2.stride(0), _ptr(ts), _ptr(q),
+            _ptr(s), _ptr(xhat), K, _stream(x))
+    return (xhat, q, s.view(torch.float8_e4m3fn)) if packed else xhat
+
+
+FP8_ACTIVATION = 0   # e4m3(clamp(x * inv_scale)), fp32 product (the compiled activation quantizer)
+FP8_WEIGHT = 1       # e4m3(clamp(bf16(x / bf16(scale))))      (the eager weight quantizer)
+
+
+def fp8_quantize_dequantize(x: torch.Tensor, scale: torch.Tensor, mode: int = FP8_ACTIVATION) -> torch.Tensor:
+    """FastFP8Linear's e4m3 operand as its exact bf16 value (fp8_fast_linear.py:71-73, 123-125).
+    `scale`: a device scalar -- the bf16 inverse scale for FP8_ACTIVATION, the fp32 scale for FP8_WEIGHT."""
+    _require_cuda(x, scale)
+    x2 = _rows_bf16(x, "fp8_quantize_dequantize")
+    M, K = x2.shape
+    s = scale.reshape(1).to(torch.float32)
+    out = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16)
+    _launch("fp8_qdq", x, "oudjat_fp8_quantize_dequantize", _ptr(x2), M, K, x2.stride(0), _ptr(s), int(mode), _ptr(out),
+            K, _stream(x))
+    return out
+
+
+def scale_bias(x: torch.Tensor, scale: float, bias: torch.Tensor | None = None, gamma: torch.Tensor | None = None,
+               out: torch.Tensor | None = None) -> torch.Tensor:
+    """bf16(x * scale + bias), then bf16(. * gamma) when gamma is given (scale_bias_inplace_triton,
+    token_update.py:571-617, and the LayerScale after it). `out` may be x (in place)."""
+    _require_cuda(x, bias, gamma, out)
+    x2 = _rows_bf16(x, "scale_bias")
+    M, N = x2.shape
+    for t, nm in ((bias, "bias"), (gamma, "gamma")):
+        _require(t is None or (t.dtype == torch.bfloat16 and t.numel() == N), f"scale_bias: {nm} must be bf16 [N]")
+    if out is None:
+        out = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16)
+    o2 = out.reshape(-1, N)
+    _launch("scale_bias", x, "oudjat_scale_bias_rows", _ptr(x2), M, N, x2.stride(0), float(scale),
+            _ptr(None if bias is None else bias.contiguous()), _ptr(None if gamma is None else gamma.contiguous()),
+            _ptr(o2), o2.stride(0), _stream(x))
+    return out
+
+
+def swiglu_scaled(x1: torch.Tensor, s1: float, b1: torch.Tensor | None, x2: torch.Tensor, s2: float,
+                  b2: torch.Tensor | None) -> torch.Tensor:
+    """silu(x1 * s1 + b1) * (x2 * s2 + b2) -> bf16, written into x1 (fused_swiglu_epilogue_triton,
+    token_update.py:620-669)."""
+    _require_cuda(x1, x2, b1, b2)
+    _require(x1.shape == x2.shape and x1.is_contiguous() and x2.is_contiguous() and x1.dtype == x2.dtype == torch.bfloat16,
+             "swiglu_scaled: contiguous bf16 tensors of one shape")
+    _require((b1 is None) == (b2 is None), "swiglu_scaled: both biases or neither")
+    N = x1.shape[-1]
+    M = x1.numel() // N if N else 0
+    _launch("swiglu", x1, "oudjat_swiglu_scaled", _ptr(x1), float(s1), _ptr(None if b1 is None else b1.contiguous()),
+            _ptr(x2), float(s2), _ptr(None if b2 is None else b2.contiguous()), M, N, _ptr(x1), _stream(x1))
+    return x1
+
+
+def amax_update(x: torch.Tensor, amax: torch.Tensor) -> None:
+    """amax = max(amax, max |x|) in place (a device fp32 scalar; NaN propagates)."""
+    _require_cuda(x, amax)
+    _require(amax.dtype == torch.float32 and amax.numel() == 1 and amax.is_contiguous(), "amax_update: fp32 scalar")
+    x2 = _rows_bf16(x, "amax_update")
+    call("oudjat_amax_update", _ptr(x2), x2.shape[0], x2.shape[1], x2.stride(0), _ptr(amax), _stream(x))
 
 
 # Reference spellings, for call sites written against the Triton wrappers.

@@ -198,18 +198,23 @@ int oudjat_layernorm_rows(const uint16_t* x, int64_t rows, int64_t C, int64_t x_
  * and the LayerScale / residual ops folded into their epilogues (block.py:1129-1141); the SwiGLU
  * gate silu(w1 x) * (w2 x) (ffn_layers.py:106-115) is the SILU_MUL epilogue with resid = w2 x.
  * bias, gamma, resid may be NULL where the epilogue does not use them (bias NULL = 0).
+ * acc_scale multiplies the fp32 accumulator before the first rounding: every epilogue starts from
+ * bf16(acc * acc_scale + bias) (one rounding; 1.0 gives bf16(acc + bias) exactly). It carries the
+ * per-tensor scales of an FP8 GEMM (torch._scaled_mm's scale_a * scale_b, fp8_fast_linear.py:187-194)
+ * whose e4m3 operands were passed as their exact bf16 values.
  * K % 64 == 0, N % 64 == 0, all leading dimensions % 8 == 0 and 16-byte aligned pointers. */
 int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
                        int64_t N, int64_t ldw, const uint16_t* bias, int epilogue,
                        const uint16_t* gamma, const uint16_t* resid, int64_t ldr, uint16_t* C,
-                       int64_t ldc, oudjat_stream_t stream);
+                       int64_t ldc, float acc_scale, oudjat_stream_t stream);
 
 /* Rows 6-9 fused into the QKV GEMM -- SelfAttention.correct_partial_token up to the attention call
  * (appcorr/models/dinov3/layers/attention.py:415-454): qkv = A . W^T + bias for A [M, K] and
  * W [3*H*Dh, K] (never materialised), then RoPE on q and k of patch rows (rotate-half, fp32, tables
  * [*, Dh] fp32 with row stride table_stride), q written packed into q_out [M, H, Dh] and k, v into
  * kv[b, t, 0|1, H, Dh] at b = batch_idx[m], t = token_idx[m] (strides in elements).
- * Same arithmetic as oudjat_linear_bf16 (OUDJAT_EPI_BIAS) followed by oudjat_qkv_rope_kv_scatter.
+ * Same arithmetic as oudjat_linear_bf16 (OUDJAT_EPI_BIAS, same acc_scale) followed by
+ * oudjat_qkv_rope_kv_scatter.
  * K % 64 == 0, Dh in {16, 32, 64, 128}, H*Dh % 128 == 0; 16-byte aligned operands and rows. */
 int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
                               int64_t ldw, const uint16_t* bias, int64_t H, int64_t Dh,
@@ -217,7 +222,7 @@ int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K, int64_t l
                               const uint8_t* patch_mask, const int64_t* rope_idx,
                               const int64_t* batch_idx, const int64_t* token_idx, uint16_t* kv,
                               int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
-                              oudjat_stream_t stream);
+                              float acc_scale, oudjat_stream_t stream);
 
 /* Row 10 -- sparse-query attention: for each image b, head h and query t < T,
  *   out[b*T + t, h*Dh:(h+1)*Dh] = softmax(q . K^T * scale) . V over ALL N cached keys, no mask.
@@ -296,6 +301,45 @@ int oudjat_nvfp4_quantize(const uint16_t* x, int64_t M, int64_t K, int64_t strid
 int oudjat_nvfp4_dequantize(const uint8_t* qdata, const uint8_t* scales, const float* tensor_scale,
                             int64_t M, int64_t K, uint16_t* out, int64_t out_stride,
                             oudjat_stream_t stream);
+
+/* NVFP4 activation operand of the FP4 correction linears -- FastFP4Linear._quantize
+ * (offload/server/model/fp4_fast_linear.py:171-219) with the same arithmetic as oudjat_nvfp4_quantize,
+ * additionally writing xhat[m, k] = e2m1(q) * e4m3(s) (bf16, exact: the block-scaled value without
+ * the tensor scale, which is what a block-scaled FP4 GEMM multiplies). qdata and scales may both be
+ * NULL (only xhat written). Same shape / alignment rules as oudjat_nvfp4_quantize; xhat 16-byte
+ * aligned with xhat_stride % 8 == 0. */
+int oudjat_nvfp4_quantize_dequantize(const uint16_t* x, int64_t M, int64_t K, int64_t stride_m,
+                                     const float* tensor_scale, uint8_t* qdata, uint8_t* scales,
+                                     uint16_t* xhat, int64_t xhat_stride, oudjat_stream_t stream);
+
+/* FP8 (e4m3fn, per-tensor scale) operand of FastFP8Linear (fp8_fast_linear.py), written as its exact
+ * bf16 value: mode 0 (activations, fp8_fast_linear.py:71-73, 183-186): out = e4m3(clamp(x * s, +-448))
+ * with the fp32 product, *scale = the bf16 inverse activation scale; mode 1 (the weight,
+ * fp8_fast_linear.py:123-125): out = e4m3(clamp(bf16(x / bf16(*scale)), +-448)). e4m3 rounding is to
+ * nearest even. K % 8 == 0, 16-byte aligned rows. */
+int oudjat_fp8_quantize_dequantize(const uint16_t* x, int64_t M, int64_t K, int64_t stride_m,
+                                   const float* scale, int mode, uint16_t* out, int64_t out_stride,
+                                   oudjat_stream_t stream);
+
+/* The NVFP4 linears' output epilogue, scale_bias_inplace_triton (token_update.py:571-617):
+ * out = bf16(x * scale + bias[col]) over [M, N] (bias may be NULL: bf16(x * scale)); with gamma
+ * (may be NULL) out = bf16(that * gamma[col]), the block's LayerScale (layer_scale.py:28-29). out may
+ * alias x. N % 8 == 0, 16-byte aligned rows. */
+int oudjat_scale_bias_rows(const uint16_t* x, int64_t M, int64_t N, int64_t x_stride, float scale,
+                           const uint16_t* bias, const uint16_t* gamma, uint16_t* out, int64_t out_stride,
+                           oudjat_stream_t stream);
+
+/* The SwiGLU pair's fused NVFP4 epilogue, fused_swiglu_epilogue_triton (token_update.py:620-669):
+ * a = x1 * s1 + b1, b = x2 * s2 + b2 (fp32), out = bf16(silu(a) * b) over contiguous [M, N]; b1 and b2
+ * are both NULL or both given. out may alias x1. N % 8 == 0, 16-byte aligned. */
+int oudjat_swiglu_scaled(const uint16_t* x1, float s1, const uint16_t* b1, const uint16_t* x2, float s2,
+                         const uint16_t* b2, int64_t M, int64_t N, uint16_t* out, oudjat_stream_t stream);
+
+/* Calibration observer of the low-precision linears (fp4_fast_linear.py:256-259,
+ * fp8_fast_linear.py:176-179): *amax = max(*amax, max |x|) over rows [M, K] (NaN propagates).
+ * K % 8 == 0, 16-byte aligned rows. */
+int oudjat_amax_update(const uint16_t* x, int64_t M, int64_t K, int64_t stride_m, float* amax,
+                       oudjat_stream_t stream);
 
 #ifdef __cplusplus
 }

@@ -389,8 +389,12 @@ def approx_pass(cfg: ViTConfig, blocks: list, x: torch.Tensor, rope, mode: str =
 
 
 def correct_block(cfg: ViTConfig, blk: dict, x: torch.Tensor, plan, rope, cache: dict, tag: str,
-                  mode: str = "f64", inplace_cache: bool = True):
+                  mode: str = "f64", inplace_cache: bool = True, lowp: dict | None = None):
     """One partial-token correction block. `plan` is an oracle.plan.Plan (numpy) for this block.
+
+    `lowp` (SwiGLU blocks): {linear name: (kind, act_scale)} for "attn.qkv", "attn.proj", "mlp.w1",
+    "mlp.w2", "mlp.w3", kind "fp4" or "fp8" -- the correction linears of the reference's low-precision
+    controller after calibration (oracle/lowp.py); the rest of the block is unchanged.
 
     bf16 rounding points (reference materialisations): x_act (gather, exact); LN1 out; qkv out;
     q/k after RoPE (fp32 math); K/V cache rows; SDPA out; proj out; x_attn = x_act + g1 * proj
@@ -412,7 +416,11 @@ def correct_block(cfg: ViTConfig, blk: dict, x: torch.Tensor, plan, rope, cache:
 
     x_act = x[bi, ti]                                                        # block.py:1111
     xn = ops.ln(x_act, blk["norm1.weight"], blk["norm1.bias"], cfg.ln_eps)   # :1114
-    qkv = ops.linear(xn, blk["attn.qkv.weight"], masked_qkv_bias(blk)).reshape(M, 3, H, D)  # attention.py:415
+    if lowp is not None:
+        from . import lowp as LPO
+        qkv = LPO.linear_out(lowp["attn.qkv"], xn, blk["attn.qkv.weight"], blk.get("attn.qkv.bias")).reshape(M, 3, H, D)
+    else:
+        qkv = ops.linear(xn, blk["attn.qkv.weight"], masked_qkv_bias(blk)).reshape(M, 3, H, D)  # attention.py:415
     q, k, v = qkv[:, 0], qkv[:, 1], qkv[:, 2]
     pm = torch.from_numpy(plan.active_patch_mask)
     ri = torch.from_numpy(plan.active_rope_idx)
@@ -424,10 +432,22 @@ def correct_block(cfg: ViTConfig, blk: dict, x: torch.Tensor, plan, rope, cache:
     qb = q.reshape(B, T, H, D).transpose(1, 2)                               # q_pad, BTHD (:473-495)
     attn = ops.sdpa(qb, kv[:, :, 0].transpose(1, 2), kv[:, :, 1].transpose(1, 2), D ** -0.5)  # :497-502
     attn = attn.transpose(1, 2).reshape(M, C)                                # :508-523
-    proj = ops.linear(attn, blk["attn.proj.weight"], blk["attn.proj.bias"])  # :532
+    if lowp is not None:
+        proj = LPO.linear_out(lowp["attn.proj"], attn, blk["attn.proj.weight"], blk["attn.proj.bias"])
+    else:
+        proj = ops.linear(attn, blk["attn.proj.weight"], blk["attn.proj.bias"])  # :532
     x_attn = ops.fma_add(x_act, proj, blk["ls1.gamma"])                      # block.py:1129-1134
-    mlp = ops.mul(_mlp(ops, cfg, blk, ops.ln(x_attn, blk["norm2.weight"], blk["norm2.bias"], cfg.ln_eps)),
-                  blk["ls2.gamma"])                                          # :1141
+    xn2 = ops.ln(x_attn, blk["norm2.weight"], blk["norm2.bias"], cfg.ln_eps)
+    if lowp is not None and lowp["mlp.w1"][0] == "fp4":
+        mlp = LPO.swiglu_mlp(lowp, blk, xn2, blk["ls2.gamma"])
+    elif lowp is not None:   # FP8: the unfused SwiGLU of ffn_layers.py:108-115 on FP8 linears
+        x1 = LPO.linear_out(lowp["mlp.w1"], xn2, blk["mlp.w1.weight"], blk.get("mlp.w1.bias"))
+        x2 = LPO.linear_out(lowp["mlp.w2"], xn2, blk["mlp.w2.weight"], blk.get("mlp.w2.bias"))
+        h = ops.silu_mul(x1, x2)
+        mlp = ops.mul(LPO.linear_out(lowp["mlp.w3"], h, blk["mlp.w3.weight"], blk.get("mlp.w3.bias")),
+                      blk["ls2.gamma"])
+    else:
+        mlp = ops.mul(_mlp(ops, cfg, blk, xn2), blk["ls2.gamma"])            # :1141
     x_out = ops.add(x, bos)                                                  # :1143-1149
     x_out[bi, ti] = ops.add(x_attn, mlp)                                     # :1151-1158
     bos[bi, ti] = ops.add(ops.sub(x_attn, x_act), mlp)                       # :1177-1179
