@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be loaded before the HIP library, see module docstring
 
 LIB_PATH = Path(__file__).resolve().parent / "liboudjat_hip.so"
-ABI_VERSION = 7
+ABI_VERSION = 8
 
 OK = 0
 STATUS_NAMES = {
@@ -70,6 +70,9 @@ SIGNATURES: dict[str, list] = {
     "oudjat_selftest": [_p],
     "oudjat_patch_importance": [_p, _i64, _i64, _i64, _i32, _p, _p],
     "oudjat_topk_plan": [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
+    "oudjat_threshold_keep": [_p, _i64, _i64, _i64, _f32, _p, _p, _p],
+    "oudjat_threshold_plan": [_p, _i64, _i64, _i64, _f32, _i64, _i32, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p,
+                              _p, _p, _p, _p, _p],
     "oudjat_plan_stats": [_p, _i64, _i64, _i64, _p, _p, _p],
     "oudjat_gather_rows": [_p, _i64, _i64, _i64, _p, _p, _i64, _p, _i64, _p],
     "oudjat_scatter_rows": [_p, _i64, _i64, _i64, _p, _p, _i64, _p, _i64, _p],

@@ -63,6 +63,10 @@ def _fp4_raw(mod: "LP.FastFP4Linear", x: Tensor, site: str):
 
 @dataclass
 class PackedQueryState:
+    """The packed rows of one plan, B x T of them (T = pretokens + patch slots). For the padded
+    threshold builder the reference keeps only the rows at query_valid_mask; here the other slots are
+    packed rows too, each repeating its image's last valid row, so they compute and write back exactly
+    what that row does, and the rows at query_valid_mask are the reference's active rows."""
     active_batch_idx: Tensor
     active_pos_idx: Tensor
     active_token_idx: Tensor
@@ -510,19 +514,41 @@ class SelfAttentionBlock(nn.Module):
         if cvm is not None:
             combined = combined.masked_fill(~cvm.to(combined.device), float("-inf"))
         Pn = dindice_patches.shape[1]
-        ratio = float(kw["token_keep_ratio"])
-        k = Pn if ratio >= 1.0 else min(int(Pn * ratio), Pn)
         scores = combined.to(torch.float32).contiguous()
-        tp = K.topk_plan(scores, k, dindice.contiguous(), num_pretokens, N)
-        T = num_pretokens + k
+        thres = kw["token_keep_thres"]
+        all_valid = True
+        if thres is None:                                       # top-k (block.py:377-394, 397-490)
+            ratio = float(kw["token_keep_ratio"])
+            k = Pn if ratio >= 1.0 else min(int(Pn * ratio), Pn)
+            tp = K.topk_plan(scores, k, dindice.contiguous(), num_pretokens, N)
+            valid = None
+        elif kw["token_keep_cap"] > 0:                          # fixed width, sync-free (block.py:492-560)
+            width = max(0, min(int(kw["token_keep_cap"]), Pn))
+            tp = K.threshold_plan(scores, thres, dindice.contiguous(), num_pretokens, width, padded=False,
+                                  num_tokens=N)
+            valid = None
+        else:                                                   # padded (block.py:562-621)
+            # The width is the largest kept count, read back to the host as the reference's .item()
+            # does (block.py:570); rows past an image's count are not queries.
+            _, counts = K.threshold_keep(scores, thres)
+            counts_h = counts.cpu()
+            width = int(counts_h.max()) if B > 0 else 0
+            if num_pretokens == 0 and width > 0 and int(counts_h.min()) == 0:
+                raise NotImplementedError("padded threshold plan with num_pretokens == 0: an image that keeps no "
+                                          "candidate has no row to stand in for its padding; set token_keep_cap")
+            tp = K.threshold_plan(scores, thres, dindice.contiguous(), num_pretokens, width, padded=True,
+                                  num_tokens=N)
+            valid = tp.query_valid
+            all_valid = bool(B <= 1 or valid.numel() == 0 or bool((counts_h == width).all()))
+        T = tp.update_indice.shape[1]
+        if valid is None:
+            valid = torch.ones((B, T), device=x.device, dtype=torch.bool)
         qs = PackedQueryState(
             active_batch_idx=tp.active_batch_idx, active_pos_idx=tp.active_pos_idx,
-            active_token_idx=tp.active_token_idx,
-            query_valid_mask=torch.ones((B, T), device=x.device, dtype=torch.bool),
+            active_token_idx=tp.active_token_idx, query_valid_mask=valid,
             active_query_pos_padded=torch.arange(T, device=x.device, dtype=torch.long).unsqueeze(0).expand(B, -1),
-            active_query_mask=None, all_valid=True, active_patch_mask=tp.active_patch_mask,
+            active_query_mask=valid, all_valid=all_valid, active_patch_mask=tp.active_patch_mask,
             active_rope_idx=tp.active_rope_idx, row_slot=tp.row_slot)
-        qs.active_query_mask = qs.query_valid_mask
         keep = tp.keep_mask
         stats = K.plan_stats(scores, keep)  # block.py:762-788 in one launch
         return PartialTokenQueryPlan(
@@ -541,6 +567,8 @@ class SelfAttentionBlock(nn.Module):
             "token_keep_ratio": kwargs.get("token_keep_ratio", 0.2),
             "token_keep_thres": None if kwargs.get("token_keep_thres") in (None, "", "null", "None")
             else float(kwargs["token_keep_thres"]),
+            # > 0 with a threshold: the fixed-width, sync-free builder (block.py:949-951, 1055-1062)
+            "token_keep_cap": int(kwargs.get("token_keep_cap", 0) or 0),
             "server_pscore_weight": float(kwargs.get("server_pscore_weight", 1.0)),
             "server_pscore": str(kwargs.get("server_pscore", "cls_attn_prob")),
             "mobile_pscore": str(kwargs.get("mobile_pscore", "none")),
@@ -554,9 +582,6 @@ class SelfAttentionBlock(nn.Module):
         if kw["server_pscore"] not in self._VALID_SERVER_PSCORES:
             raise ValueError(f"Unknown server_pscore '{kw['server_pscore']}'. "
                              f"Available values: {sorted(self._VALID_SERVER_PSCORES)}")
-        if kw["token_keep_thres"] is not None:
-            raise NotImplementedError("threshold token selection (token_keep_thres) is not part of this build; "
-                                      "use token_keep_ratio (top-k)")
         if x.dtype != torch.bfloat16 or x.dim() != 3:
             raise ValueError("correct_partial_token expects x [B, N, C] bf16")
         B, N, C = x.shape

@@ -348,6 +348,69 @@ def topk_plan(scores: torch.Tensor, k: int, dindice: torch.Tensor, num_pretokens
     return TopkPlan(upd, abat, apos, atok, pmask, ridx, keep, slot)
 
 
+@dataclass
+class ThresholdPlan(TopkPlan):
+    query_valid: torch.Tensor | None = None   # [B, T] bool
+    kept_count: torch.Tensor | None = None    # [B] int32
+
+
+def _check_threshold_scores(scores: torch.Tensor, what: str):
+    _require(scores.dtype == torch.float32 and scores.dim() == 2 and (scores.numel() == 0 or scores.stride(1) == 1),
+             f"{what}: scores must be [B, P] fp32 with contiguous rows")
+
+
+def threshold_keep(scores: torch.Tensor, thres: float) -> tuple[torch.Tensor, torch.Tensor]:
+    """keep = scores >= thres (fp32 compare, block.py:374-376) and the kept count per image:
+    (keep [B, P] bool, kept_count [B] int32)."""
+    _require_cuda(scores)
+    _check_threshold_scores(scores, "threshold_keep")
+    B, Pn = scores.shape
+    keep = torch.empty((B, Pn), device=scores.device, dtype=torch.bool)
+    cnt = torch.empty((B,), device=scores.device, dtype=torch.int32)
+    _launch("threshold_keep", scores, "oudjat_threshold_keep", _ptr(scores), B, Pn, max(scores.stride(0), Pn),
+            float(thres), _ptr(keep), _ptr(cnt), _stream(scores))
+    return keep, cnt
+
+
+def threshold_plan(scores: torch.Tensor, thres: float, dindice: torch.Tensor, num_pretokens: int, width: int,
+                   padded: bool, num_tokens: int | None = None) -> ThresholdPlan:
+    """Threshold selection and its packed plan at `width` patch slots per image (T = pre + width).
+
+    padded=False: the fixed-width builder of token_keep_cap (block.py:492-560) -- slots past an
+    image's kept count repeat its last kept candidate (candidate 0 if none), all valid.
+    padded=True: the padded builder (block.py:562-621) at width = the largest kept count --
+    update_indice holds 0 and query_valid False past the count; the packed rows repeat the image's
+    last valid row, so the rows at query_valid are the reference's compacted active rows.
+    """
+    _require_cuda(scores, dindice)
+    _check_threshold_scores(scores, "threshold_plan")
+    _require(dindice.dtype == torch.long and dindice.dim() == 2 and dindice.stride(1) == 1,
+             "threshold_plan: dindice must be [B, pre + P] int64 with contiguous rows")
+    B, Pn = scores.shape
+    _require(dindice.shape[0] == B and dindice.shape[1] == num_pretokens + Pn, "threshold_plan: dindice shape mismatch")
+    width = int(width)
+    _require(0 <= width <= Pn, f"threshold_plan: width={width} outside [0, {Pn}]")
+    T = num_pretokens + width
+    dev = scores.device
+    upd = torch.empty((B, T), device=dev, dtype=torch.long)
+    abat = torch.empty((B * T,), device=dev, dtype=torch.long)
+    apos = torch.empty_like(abat)
+    atok = torch.empty_like(abat)
+    pmask = torch.empty((B * T,), device=dev, dtype=torch.bool)
+    ridx = torch.empty_like(abat)
+    qvalid = torch.empty((B, T), device=dev, dtype=torch.bool)
+    keep = torch.empty((B, Pn), device=dev, dtype=torch.bool)
+    cnt = torch.empty((B,), device=dev, dtype=torch.int32)
+    slot = None
+    if num_tokens is not None:
+        slot = torch.empty((B, int(num_tokens)), device=dev, dtype=torch.int32)
+    _launch("threshold_plan", scores, "oudjat_threshold_plan", _ptr(scores), B, Pn, max(scores.stride(0), Pn),
+            float(thres), width, 1 if padded else 0, _ptr(dindice), dindice.stride(0), num_pretokens,
+            0 if num_tokens is None else int(num_tokens), _ptr(upd), _ptr(abat), _ptr(apos), _ptr(atok), _ptr(pmask),
+            _ptr(ridx), _ptr(qvalid), _ptr(keep), _ptr(cnt), _ptr(slot), _stream(scores))
+    return ThresholdPlan(upd, abat, apos, atok, pmask, ridx, keep, slot, qvalid, cnt)
+
+
 def plan_stats(scores: torch.Tensor, keep: torch.Tensor) -> torch.Tensor:
     """The plan's statistics in one launch (block.py:762-788): fp32 [5] = (sum(scores * keep),
     sum(scores), sum(keep), B * P, B) for scores [B, P] fp32 and the bool keep mask [B, P]."""

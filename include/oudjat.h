@@ -99,6 +99,39 @@ int oudjat_topk_plan(const float* scores, int64_t B, int64_t P, int64_t score_st
                      uint8_t* active_patch_mask, int64_t* active_rope_idx, uint8_t* keep_mask,
                      int32_t* row_slot, oudjat_stream_t stream);
 
+/* Threshold selection (next-rank row f3) -- the kept mask and per-image kept count of
+ * _select_patch_keep_mask's threshold branch (appcorr/models/dinov3/layers/block.py:374-376):
+ * keep_mask[b, p] = scores[b, p] >= thres, compared in fp32 as torch compares an fp32 tensor with a
+ * Python float (the float rounded to fp32 first; NaN never kept); kept_count[b] int32. keep_mask may
+ * be NULL. This is what the padded builder (block.py:562-621) reads back to size its plan. */
+int oudjat_threshold_keep(const float* scores, int64_t B, int64_t P, int64_t score_stride_b, float thres,
+                          uint8_t* keep_mask, int32_t* kept_count, oudjat_stream_t stream);
+
+/* Threshold selection and its packed query plan at a fixed width of `width` patch slots (T =
+ * num_pre + width rows per image, M = B * T). Replaces _build_packed_query_state_thres_static
+ * (block.py:492-560, fill_mode 0, width = min(token_keep_cap, P)) and _build_packed_query_state
+ * (block.py:562-621, fill_mode 1, width = the largest kept count from oudjat_threshold_keep).
+ * Kept candidates (scores >= thres, as above) fill slots num_pre.. in candidate order; kept ranks at
+ * or past `width` are dropped. Slots past an image's kept count:
+ *   fill_mode 0: the image's last kept candidate (candidate 0 if it keeps none), query_valid 1 --
+ *     block.py:536-541;
+ *   fill_mode 1: update_indice 0 and query_valid 0 (block.py:571-599); the packed rows (active_*)
+ *     repeat the image's last valid row -- its last kept candidate, else its last pretoken -- which
+ *     computes and writes exactly what that row does, so the rows at query_valid equal the
+ *     reference's compacted PackedQueryState. An image with no valid row at all (num_pre == 0 and
+ *     nothing kept) must not reach this mode; the caller checks kept_count first.
+ * Outputs: update_indice [B, T], active_batch_idx/pos_idx/token_idx [M], active_patch_mask [M],
+ * active_rope_idx [M] as oudjat_topk_plan; query_valid [B, T] (1 byte); keep_mask [B, P] (may be
+ * NULL); kept_count [B] int32; row_slot [B, num_tokens] int32 = the first packed row holding the token,
+ * or -1 (may be NULL). Limits: width <= P <= 16384, num_tokens * 4 bytes <= 144 KiB. */
+int oudjat_threshold_plan(const float* scores, int64_t B, int64_t P, int64_t score_stride_b, float thres,
+                          int64_t width, int fill_mode, const int64_t* dindice, int64_t dindice_stride_b,
+                          int64_t num_pre, int64_t num_tokens, int64_t* update_indice,
+                          int64_t* active_batch_idx, int64_t* active_pos_idx, int64_t* active_token_idx,
+                          uint8_t* active_patch_mask, int64_t* active_rope_idx, uint8_t* query_valid,
+                          uint8_t* keep_mask, int32_t* kept_count, int32_t* row_slot,
+                          oudjat_stream_t stream);
+
 /* Rows 4 and 11 -- dst[i, :] = src[batch_idx[i], token_idx[i], :] for row_bytes contiguous bytes.
  * Replaces gather_rows_triton (appcorr/models/dinov3/layers/triton_kernels/token_update.py:455-473).
  * Strides are in bytes. */

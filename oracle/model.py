@@ -390,7 +390,9 @@ def approx_pass(cfg: ViTConfig, blocks: list, x: torch.Tensor, rope, mode: str =
 
 def correct_block(cfg: ViTConfig, blk: dict, x: torch.Tensor, plan, rope, cache: dict, tag: str,
                   mode: str = "f64", inplace_cache: bool = True, lowp: dict | None = None):
-    """One partial-token correction block. `plan` is an oracle.plan.Plan (numpy) for this block.
+    """One partial-token correction block. `plan` is an oracle.plan.Plan (numpy) for this block: its
+    active_* rows are the queries (compacted for the padded threshold builder), scattered into the
+    padded [B, T] query buffer by (active_batch_idx, active_pos_idx) for the attention.
 
     `lowp` (SwiGLU blocks): {linear name: (kind, act_scale)} for "attn.qkv", "attn.proj", "mlp.w1",
     "mlp.w2", "mlp.w3", kind "fp4" or "fp8" -- the correction linears of the reference's low-precision
@@ -429,9 +431,11 @@ def correct_block(cfg: ViTConfig, blk: dict, x: torch.Tensor, plan, rope, cache:
     k = torch.where(pm[:, None, None], rope_rotate(k, s_sel, c_sel), k)
     kv[bi, ti, 0] = k                                                        # attention.py:444-454
     kv[bi, ti, 1] = v
-    qb = q.reshape(B, T, H, D).transpose(1, 2)                               # q_pad, BTHD (:473-495)
-    attn = ops.sdpa(qb, kv[:, :, 0].transpose(1, 2), kv[:, :, 1].transpose(1, 2), D ** -0.5)  # :497-502
-    attn = attn.transpose(1, 2).reshape(M, C)                                # :508-523
+    pi = torch.from_numpy(plan.active_pos_idx)
+    q_pad = q.new_zeros((B, T, H, D))                                        # q_pad, BTHD (:456-495);
+    q_pad[bi, pi] = q                                                        # pad rows are never read back
+    attn = ops.sdpa(q_pad.transpose(1, 2), kv[:, :, 0].transpose(1, 2), kv[:, :, 1].transpose(1, 2), D ** -0.5)
+    attn = attn.transpose(1, 2)[bi, pi].reshape(M, C)                        # :497-523
     if lowp is not None:
         proj = LPO.linear_out(lowp["attn.proj"], attn, blk["attn.proj.weight"], blk["attn.proj.bias"])
     else:

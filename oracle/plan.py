@@ -95,3 +95,97 @@ def plan_stats(scores: np.ndarray, keep: np.ndarray) -> np.ndarray:
     with np.errstate(invalid="ignore"):
         kept_mass = float((s * kf).sum())
     return np.array([kept_mass, float(s.sum()), float(kf.sum()), float(B * P), float(B)], dtype=np.float64)
+
+
+# ------------------------------------------------------------------------------------------------
+# Threshold selection (block.py:374-376) and its two builders (block.py:492-560, 562-621)
+# ------------------------------------------------------------------------------------------------
+
+
+def threshold_keep(scores: np.ndarray, thres: float) -> np.ndarray:
+    """block.py:374-376, `combined_patch_scores >= token_keep_thres`: torch compares an fp32 tensor with
+    a Python float in fp32, the float rounded to the nearest fp32 first; NaN is never kept."""
+    s = np.asarray(scores, dtype=np.float32)
+    with np.errstate(invalid="ignore"):
+        return s >= np.float32(thres)
+
+
+@dataclass
+class ThresholdPlan(Plan):
+    """The reference's PackedQueryState for threshold selection (its active_* are the compacted rows
+    at query_valid_mask), plus `rows`: the same plan at a fixed B x T packed layout in which every slot
+    that is not a query repeats its image's last valid row -- the layout the GPU path runs."""
+    query_valid_mask: np.ndarray = None   # [B, T] bool
+    kept_count: np.ndarray = None         # [B] int64
+    all_valid: bool = True
+    rows: Plan = None
+
+
+def _rows_plan(upd_rows: np.ndarray, valid: np.ndarray, keep: np.ndarray, num_pretokens: int,
+               num_tokens: int) -> Plan:
+    B, T = upd_rows.shape
+    tok = upd_rows.reshape(-1)
+    row_slot = np.full((B, num_tokens), -1, dtype=np.int32)
+    for b in range(B):
+        for s in range(T):
+            t = upd_rows[b, s]
+            if valid[b, s] and 0 <= t < num_tokens and row_slot[b, t] < 0:
+                row_slot[b, t] = b * T + s          # the first slot that holds the token
+    return Plan(update_indice=upd_rows, active_batch_idx=np.repeat(np.arange(B, dtype=np.int64), T),
+                active_pos_idx=np.tile(np.arange(T, dtype=np.int64), B), active_token_idx=tok.copy(),
+                active_patch_mask=tok >= num_pretokens, active_rope_idx=np.maximum(tok - num_pretokens, 0),
+                keep_mask=keep, row_slot=row_slot)
+
+
+def threshold_plan(scores: np.ndarray, thres: float, dindice: np.ndarray, num_pretokens: int, num_tokens: int,
+                   keep_cap: int = 0) -> ThresholdPlan:
+    """keep_cap > 0: _build_packed_query_state_thres_static (block.py:492-560) -- width
+    K = min(keep_cap, P); slot j of image b holds its kept candidate number min(j, count_b - 1) in
+    candidate order (candidate 0 when it keeps none), so a row keeping more than K drops its last kept
+    candidates; every slot is a query.
+    keep_cap == 0: _build_packed_query_state (block.py:562-621) -- width = the largest kept count;
+    slots past an image's count hold token 0 and are not queries; the active rows are the queries in
+    row-major order; all_valid is True for B <= 1 or no slots, else whether every count equals the
+    largest."""
+    dindice = np.asarray(dindice, dtype=np.int64)
+    B = dindice.shape[0]
+    P = dindice.shape[1] - num_pretokens
+    keep = threshold_keep(scores, thres).reshape(B, P)
+    count = keep.sum(axis=1).astype(np.int64)
+    pre = dindice[:, :num_pretokens]
+    patches = dindice[:, num_pretokens:]
+    kept = [np.flatnonzero(keep[b]) for b in range(B)]
+    static = keep_cap > 0
+    W = max(0, min(int(keep_cap), P)) if static else (int(count.max()) if B else 0)
+    upd_p = np.zeros((B, W), dtype=np.int64)
+    valid_p = np.zeros((B, W), dtype=bool)
+    rows_p = np.zeros((B, W), dtype=np.int64)
+    for b in range(B):
+        c = int(count[b])
+        for j in range(W):
+            if static:
+                cand = int(kept[b][min(j, c - 1)]) if c > 0 else 0
+                upd_p[b, j] = rows_p[b, j] = patches[b, cand]
+                valid_p[b, j] = True
+            elif j < c:
+                upd_p[b, j] = rows_p[b, j] = patches[b, kept[b][j]]
+                valid_p[b, j] = True
+            else:
+                # not a query: token 0 in update_indice; the packed row repeats the last valid row
+                last = patches[b, kept[b][c - 1]] if c > 0 else (pre[b, -1] if num_pretokens > 0 else 0)
+                rows_p[b, j] = last
+    upd = np.concatenate([pre, upd_p], axis=1)
+    valid = np.concatenate([np.ones((B, num_pretokens), dtype=bool), valid_p], axis=1)
+    rows_tok = np.concatenate([pre, rows_p], axis=1)
+    bi, pi = np.nonzero(valid)
+    tok = upd[bi, pi]
+    T = upd.shape[1]
+    if static:
+        all_valid = True
+    else:
+        all_valid = True if (B <= 1 or valid.size == 0) else bool(np.all(count == W))
+    rows = _rows_plan(rows_tok, valid, keep, num_pretokens, num_tokens)
+    return ThresholdPlan(update_indice=upd, active_batch_idx=bi.astype(np.int64), active_pos_idx=pi.astype(np.int64),
+                         active_token_idx=tok.astype(np.int64), active_patch_mask=tok >= num_pretokens,
+                         active_rope_idx=np.maximum(tok - num_pretokens, 0), keep_mask=keep, row_slot=rows.row_slot,
+                         query_valid_mask=valid, kept_count=count, all_valid=all_valid, rows=rows)

@@ -94,11 +94,16 @@ def test_product_path_refuses_cpu_tensors():
         K.layer_norm(x.view(-1, 16), torch.ones(16, dtype=torch.bfloat16), torch.zeros(16, dtype=torch.bfloat16))
 
 
-def test_threshold_selection_not_implemented():
-    blk = SelfAttentionBlock(64, 4)
-    with pytest.raises(NotImplementedError):
-        blk.correct(torch.zeros(1, 9, 64), torch.arange(9)[None], None, {}, "layer0", token_keep_thres=0.5,
-                    token_keep_ratio=None, appcorr_method="partial_token")
+@pytest.mark.parametrize("cap", [0, 4])
+def test_threshold_selection_has_no_cpu_fallback(cap):
+    """Both threshold builders reach the HIP plan kernels, which refuse CPU tensors."""
+    blk = SelfAttentionBlock(64, 4).to(torch.bfloat16)
+    kv = torch.zeros(1, 9, 2, 4, 16, dtype=torch.bfloat16)
+    cache = {"layer0_kv": kv, "layer0_blocks_out_sum": torch.zeros(1, 9, 64, dtype=torch.bfloat16)}
+    with pytest.raises(ValueError, match="GPU only"):
+        blk.correct(torch.zeros(1, 9, 64, dtype=torch.bfloat16), torch.arange(9)[None], None, cache, "layer0",
+                    token_keep_thres="0.5", token_keep_cap=cap, num_pretokens=1, server_pscore_weight=0.0,
+                    appcorr_method="partial_token")
 
 
 def test_bench_refuses_more_than_one_gpu():
