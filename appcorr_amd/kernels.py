@@ -437,6 +437,74 @@ def patch_importance(delta: torch.Tensor, mode: int = _lib.IMPORTANCE_L2) -> tor
     return out.view(delta.shape[:-1])
 
 
+_PIXEL_DTYPES = {torch.uint8: 0, torch.int16: 1, torch.float32: 2}
+
+
+def patch_residual_score(curr: torch.Tensor, prev: torch.Tensor | None, patch: tuple[int, int],
+                         mode: int = _lib.IMPORTANCE_RMS, image_idx: torch.Tensor | None = None) -> torch.Tensor:
+    """Per-patch score of the pixel residual curr - prev of HWC images [B, H, W, C] (uint8, int16 or
+    fp32; prev None: curr already is the residual) -> [n, (H/ph) * (W/pw)] fp32, n = len(image_idx) or B.
+    RMS is dinov3_classifier.py:91-122; RMS / ENERGY of one residual crop is progressive.py:14-22."""
+    _require_cuda(curr, prev, image_idx)
+    _require(curr.dim() == 4 and curr.is_contiguous() and curr.dtype in _PIXEL_DTYPES,
+             "patch_residual_score: curr must be a contiguous [B, H, W, C] uint8 / int16 / fp32 tensor")
+    _require(prev is None or (prev.shape == curr.shape and prev.dtype == curr.dtype and prev.is_contiguous()),
+             "patch_residual_score: prev must match curr")
+    _require(image_idx is None or (image_idx.dtype == torch.long and image_idx.dim() == 1 and image_idx.is_contiguous()),
+             "patch_residual_score: image_idx must be a contiguous int64 vector")
+    B, H, W, C = curr.shape
+    ph, pw = patch
+    n = B if image_idx is None else image_idx.numel()
+    out = torch.empty((n, (H // ph) * (W // pw)), device=curr.device, dtype=torch.float32)
+    _launch("residual_score", curr, "oudjat_patch_residual_score", _ptr(curr), _ptr(prev), _PIXEL_DTYPES[curr.dtype],
+            B, _ptr(image_idx), n, H, W, C, ph, pw, int(mode), _ptr(out), _stream(curr))
+    return out
+
+
+@dataclass
+class ResidualPruneKeep:
+    keep: torch.Tensor          # [B, P] bool
+    kept_count: torch.Tensor    # [B] int32
+    kept_mass: torch.Tensor     # [B] fp32
+    full_mass: torch.Tensor     # [B] fp32
+
+
+def residual_prune_keep(rms: torch.Tensor, spatial: torch.Tensor, threshold: float, min_keep: int) -> ResidualPruneKeep:
+    """The kept set of image-residual token pruning (dinov3_classifier.py:143-160): keep a candidate
+    whose residual RMS reaches `threshold` or that is among the `min_keep` largest of its image."""
+    _require_cuda(rms, spatial)
+    _require(rms.dtype == torch.float32 and rms.dim() == 2 and rms.stride(1) == 1, "residual_prune_keep: rms [B, G] fp32")
+    _require(spatial.dtype == torch.long and spatial.dim() == 2 and spatial.shape[0] == rms.shape[0]
+             and (spatial.numel() == 0 or spatial.stride(1) == 1), "residual_prune_keep: spatial [B, P] int64")
+    B, P = spatial.shape
+    dev = rms.device
+    keep = torch.empty((B, P), device=dev, dtype=torch.bool)
+    cnt = torch.empty((B,), device=dev, dtype=torch.int32)
+    km = torch.empty((B,), device=dev, dtype=torch.float32)
+    fm = torch.empty((B,), device=dev, dtype=torch.float32)
+    _launch("residual_prune", rms, "oudjat_residual_prune_keep", _ptr(rms), B, max(rms.stride(0), rms.shape[1]),
+            rms.shape[1], _ptr(spatial), max(spatial.stride(0), P), P, float(threshold), int(min_keep), _ptr(keep),
+            _ptr(cnt), _ptr(km), _ptr(fm), _stream(rms))
+    return ResidualPruneKeep(keep, cnt, km, fm)
+
+
+def residual_prune_compact(keep: torch.Tensor, spatial: torch.Tensor, dindice: torch.Tensor, num_pretokens: int,
+                           width: int) -> tuple[torch.Tensor, torch.Tensor]:
+    """(pruned_dindice [B, pre + width], kept_local_idx [B, width]) of dinov3_classifier.py:163-196."""
+    _require_cuda(keep, spatial, dindice)
+    B, P = spatial.shape
+    _require(keep.dtype == torch.bool and keep.shape == (B, P) and keep.is_contiguous(), "residual_prune_compact: keep")
+    _require(dindice.dtype == torch.long and dindice.dim() == 2 and dindice.stride(1) == 1 and dindice.shape[0] == B,
+             "residual_prune_compact: dindice [B, pre + P] int64")
+    _require(0 <= width <= P, f"residual_prune_compact: width {width} outside [0, {P}]")
+    pruned = torch.empty((B, num_pretokens + width), device=keep.device, dtype=torch.long)
+    local = torch.empty((B, width), device=keep.device, dtype=torch.long)
+    _launch("residual_prune", keep, "oudjat_residual_prune_compact", _ptr(keep), B, P, _ptr(spatial),
+            max(spatial.stride(0), P), _ptr(dindice), dindice.stride(0), num_pretokens, width, _ptr(pruned),
+            _ptr(local), _stream(keep))
+    return pruned, local
+
+
 # ------------------------------------------------------------------------------------------------
 # LayerNorm, RoPE, QKV post-processing (block.py:1114,1141; rope.py:186-240; attention.py:415-454)
 # ------------------------------------------------------------------------------------------------

@@ -15,6 +15,8 @@ from typing import Any, Dict
 import numpy as np
 import torch
 
+from .. import _lib
+from .. import kernels as K
 from ..dinov3.backbone import dinov3_backbone
 from .base import ModelExecutor
 from .protocol import Task, normalize_appcorr_kwargs
@@ -49,30 +51,42 @@ class GroupCorrectionPlan:
 
 
 def make_group_plan(dindice: torch.Tensor, num_pretokens: int) -> GroupCorrectionPlan:
-    """A correction group over the candidate tokens `dindice` [B, pre + P] (no image-residual pruning)."""
+    """A correction group over the candidate tokens `dindice` [B, pre + P] without image-residual pruning
+    (dinov3_classifier.py:231-281 with token_prune_enabled False)."""
     B = dindice.shape[0]
     P = dindice.shape[1] - num_pretokens
     dev = dindice.device
     count = torch.full((B,), P, device=dev, dtype=torch.int32)
     zeros = torch.zeros((B,), device=dev, dtype=torch.float32)
+    # every query position valid: the query state of dinov3_classifier.py:199-229, built without a
+    # host read
+    q = dindice.shape[1]
+    pos = torch.arange(q, device=dev, dtype=torch.long)
+    qs = QueryState(query_pos_idx=pos.unsqueeze(0).expand(B, -1), query_valid_mask=torch.ones((B, q), device=dev,
+                                                                                             dtype=torch.bool),
+                    active_batch_idx=torch.arange(B, device=dev, dtype=torch.long).repeat_interleave(q),
+                    active_pos_idx=pos.repeat(B), active_token_idx=dindice.reshape(-1), active_query_pos=pos.repeat(B),
+                    active_query_pos_padded=pos.unsqueeze(0).expand(B, -1),
+                    active_query_mask=torch.ones((B, q), device=dev, dtype=torch.bool), all_valid=True)
     return GroupCorrectionPlan(
         num_pretokens=num_pretokens, prefix_dindice=dindice[:, :num_pretokens],
         group_patch_dindice=dindice[:, num_pretokens:],
         group_patch_keep_local_idx=torch.arange(P, device=dev, dtype=torch.long).unsqueeze(0).expand(B, -1),
-        full_dindice=dindice, pruned_dindice=dindice, query_state=None, kept_patch_count=count,
+        full_dindice=dindice, pruned_dindice=dindice, query_state=qs, kept_patch_count=count,
         full_patch_count=count.clone(), kept_residual_mass=zeros, full_residual_mass=zeros.clone())
 
 
-def _patch_count_sums(plan: GroupCorrectionPlan) -> torch.Tensor:
-    """fp32 [2] = (0 + kept_patch_count.sum(), 0 + full_patch_count.sum()), computed once per pair
-    of count tensors (a plan whose count tensors are replaced gets new sums)."""
-    cached = getattr(plan, "_count_sums", None)
-    if cached is None or cached[0] is not plan.kept_patch_count or cached[1] is not plan.full_patch_count:
-        sums = torch.stack([plan.kept_patch_count.sum(dtype=torch.float32),
-                            plan.full_patch_count.sum(dtype=torch.float32)]) + 0.0
-        cached = (plan.kept_patch_count, plan.full_patch_count, sums)
-        plan._count_sums = cached
-    return cached[2]
+def _plan_sums(plan: GroupCorrectionPlan) -> torch.Tensor:
+    """fp32 [4] = 0 + (kept_patch_count.sum(), full_patch_count.sum(), kept_residual_mass.sum(),
+    full_residual_mass.sum()), computed once per set of plan tensors (a plan whose tensors are
+    replaced gets new sums)."""
+    src = (plan.kept_patch_count, plan.full_patch_count, plan.kept_residual_mass, plan.full_residual_mass)
+    cached = getattr(plan, "_sums", None)
+    if cached is None or any(a is not b for a, b in zip(cached[0], src)):
+        sums = torch.stack([t.sum(dtype=torch.float32) for t in src]) + 0.0
+        cached = (src, sums)
+        plan._sums = cached
+    return cached[1]
 
 
 class DINOv3ClassifierExecutor(ModelExecutor):
@@ -101,7 +115,121 @@ class DINOv3ClassifierExecutor(ModelExecutor):
         self.configure_dinov3_approx_precision(self.model, config)
         self.configure_dinov3_correct_precision(self.model, config)
 
+    @staticmethod
+    def _patch_grid(config: Any) -> tuple[int, int, int, int]:
+        H, W = config.image_shape[:2]
+        ph, pw = (config.patch_size, config.patch_size) if isinstance(config.patch_size, int) else config.patch_size
+        return H // ph, W // pw, ph, pw
+
+    def _get_active_batch_indices(self, context: Dict[str, Any], full_batch_size: int) -> torch.Tensor:
+        """dinov3_classifier.py:48-51."""
+        if "active_indices" in context and len(context["active_indices"]) < full_batch_size:
+            return context["active_indices"].to(device=self.device, dtype=torch.long)
+        return torch.arange(full_batch_size, device=self.device, dtype=torch.long)
+
+    def _build_mobile_pscore_hint_map(self, task: Task, context: Dict[str, Any], config: Any, batch_size: int,
+                                      num_patches: int) -> torch.Tensor:
+        """dinov3_classifier.py:53-89: the payload's per-patch pscore_hint at the finest transmitted
+        level, scattered into [B, P] (active images only) and row-normalised."""
+        hint_map = torch.zeros((batch_size, num_patches), device=self.device, dtype=torch.float32)
+        target = min(config.transmission_kwargs.get("pyramid_levels", [0]))
+        payload = task.payload if task is not None else []
+        if "active_indices" in context and len(context["active_indices"]) < config.batch_size:
+            idx_map = {orig: local for local, orig in enumerate(context["active_indices"].tolist())}
+            valid = [p for p in payload
+                     if p.image_idx in idx_map and p.res_level == target and 0 <= p.spatial_idx < num_patches]
+            b_list = [idx_map[p.image_idx] for p in valid]
+        else:
+            valid = [p for p in payload if p.res_level == target and 0 <= p.spatial_idx < num_patches]
+            b_list = [p.image_idx for p in valid]
+        if not valid:
+            return hint_map
+        b_t = torch.tensor(b_list, device=self.device, dtype=torch.long)
+        s_t = torch.tensor([p.spatial_idx for p in valid], device=self.device, dtype=torch.long)
+        h_t = torch.tensor([float(getattr(p, "pscore_hint", 0.0)) for p in valid], device=self.device,
+                           dtype=torch.float32)
+        hint_map[b_t, s_t] = h_t
+        return self._normalize_patch_score_map(hint_map)
+
+    def _compute_patch_residual_rms(self, context: Dict[str, Any], config: Any,
+                                    active_indices: torch.Tensor) -> torch.Tensor | None:
+        """dinov3_classifier.py:91-122: per-patch RMS of the decoded frame minus the previous one
+        ([B_active, gh * gw] fp32), in one HIP kernel on the uint8 frames."""
+        curr_np, prev_np = context.get("input_hr_np"), context.get("prev_input_hr_np")
+        if curr_np is None or prev_np is None:
+            return None
+        curr = torch.as_tensor(np.ascontiguousarray(curr_np)).to(self.device, non_blocking=True)
+        prev = torch.as_tensor(np.ascontiguousarray(prev_np)).to(self.device, non_blocking=True)
+        if curr.ndim != 4 or prev.ndim != 4:
+            return None
+        if curr.dtype not in (torch.uint8, torch.int16, torch.float32):
+            curr, prev = curr.float(), prev.float()
+        gh, gw, ph, pw = self._patch_grid(config)
+        if tuple(curr.shape[1:3]) != (gh * ph, gw * pw):
+            raise ValueError(f"decoded frames {tuple(curr.shape)} do not tile into {gh}x{gw} patches of {ph}x{pw}")
+        return K.patch_residual_score(curr.contiguous(), prev.contiguous(), (ph, pw), _lib.IMPORTANCE_RMS,
+                                      image_idx=active_indices.contiguous())
+
+    def _apply_image_residual_token_pruning(self, dindice: torch.Tensor, spatial_indices: torch.Tensor,
+                                            patch_residual_rms: torch.Tensor | None, threshold: float, min_keep: int):
+        """dinov3_classifier.py:124-197: keep the candidates whose residual RMS reaches the threshold or
+        that are among the min_keep largest, then compact them (one host read of the largest count, as
+        the reference's .item())."""
+        B, P = spatial_indices.shape
+        num_pre = dindice.shape[1] - P
+        dev = dindice.device
+        full_count = torch.full((B,), P, device=dev, dtype=torch.int32)
+        zeros = torch.zeros((B,), device=dev, dtype=torch.float32)
+        full_idx = torch.arange(P, device=dev, dtype=torch.long).unsqueeze(0).expand(B, -1)
+        if patch_residual_rms is None or P == 0:
+            return dindice, full_count.clone(), full_count, zeros, zeros.clone(), full_idx
+        spatial = spatial_indices.contiguous()
+        pk = K.residual_prune_keep(patch_residual_rms.contiguous(), spatial, threshold, min_keep)
+        width = int(pk.kept_count.max().item()) if B > 0 else 0
+        if width == P:
+            return dindice, pk.kept_count, full_count, pk.kept_mass, pk.full_mass, full_idx
+        pruned, local = K.residual_prune_compact(pk.keep, spatial, dindice.contiguous(), num_pre, width)
+        return pruned, pk.kept_count, full_count, pk.kept_mass, pk.full_mass, local
+
+    @staticmethod
+    def _build_fixed_query_state(dindice: torch.Tensor, kept_patch_count: torch.Tensor, num_pretokens: int) -> QueryState:
+        """dinov3_classifier.py:199-229 (the group plan's query metadata; the blocks build their own plan)."""
+        B, q = dindice.shape
+        dev = dindice.device
+        pos = torch.arange(q, device=dev, dtype=torch.long).unsqueeze(0).expand(B, -1)
+        lengths = kept_patch_count.to(device=dev, dtype=torch.long) + num_pretokens
+        valid = pos < lengths.unsqueeze(1)
+        bi, pi = valid.nonzero(as_tuple=True)
+        max_active = int(lengths.max().item()) if lengths.numel() > 0 else 0
+        if max_active > 0:
+            padded = torch.arange(max_active, device=dev, dtype=torch.long).unsqueeze(0).expand(B, -1)
+            amask = padded < lengths.unsqueeze(1)
+        else:
+            padded = torch.empty((B, 0), device=dev, dtype=torch.long)
+            amask = torch.empty((B, 0), device=dev, dtype=torch.bool)
+        return QueryState(query_pos_idx=pos, query_valid_mask=valid, active_batch_idx=bi, active_pos_idx=pi,
+                          active_token_idx=dindice[bi, pi], active_query_pos=pi, active_query_pos_padded=padded,
+                          active_query_mask=amask,
+                          all_valid=bool(torch.all(lengths == q).item()) if lengths.numel() > 0 else True)
+
+    def _build_group_plan(self, dindice: torch.Tensor, spatial_indices: torch.Tensor,
+                          patch_residual_rms: torch.Tensor | None, num_pretokens: int, token_prune_enabled: bool,
+                          token_prune_threshold: float, token_prune_min_keep: int) -> GroupCorrectionPlan:
+        """dinov3_classifier.py:231-281."""
+        plan = make_group_plan(dindice, num_pretokens)
+        pruned = dindice
+        if token_prune_enabled:
+            (pruned, plan.kept_patch_count, plan.full_patch_count, plan.kept_residual_mass, plan.full_residual_mass,
+             plan.group_patch_keep_local_idx) = self._apply_image_residual_token_pruning(
+                dindice, spatial_indices, patch_residual_rms, token_prune_threshold, token_prune_min_keep)
+        if pruned is not dindice or token_prune_enabled:
+            plan.query_state = self._build_fixed_query_state(pruned, plan.kept_patch_count, num_pretokens)
+        plan.pruned_dindice = pruned
+        return plan
+
     def preprocess(self, batch_data: Any, task: Task, context: Dict[str, Any], config: Any):
+        """dinov3_classifier.py:330-527: normalised input, the request's patch -> group map, the mobile
+        hint map, and one correction plan per transmitted group (image-residual pruning optional)."""
         t = batch_data if isinstance(batch_data, torch.Tensor) else torch.from_numpy(np.asarray(batch_data))
         t = t.to(self.device, non_blocking=True)
         if t.ndim != 4:
@@ -112,33 +240,51 @@ class DINOv3ClassifierExecutor(ModelExecutor):
         t = t.float()
         if is_u8:
             t = t / 255.0
-        context["input_tensor"] = (t - self.norm_mean) / self.norm_std
-        H, W = config.image_shape[:2]
-        ph = pw = config.patch_size if isinstance(config.patch_size, int) else config.patch_size[0]
-        num_patches = (H // ph) * (W // pw)
-        B = t.shape[0]
+        t = (t - self.norm_mean) / self.norm_std
+        sliced = "active_indices" in context and len(context["active_indices"]) < config.batch_size
+        if sliced:
+            t = t[context["active_indices"]]
+        context["input_tensor"] = t
+        gh, gw, _, _ = self._patch_grid(config)
+        num_patches = gh * gw
         if "group_map" not in context:
-            context["group_map"] = torch.full((B, num_patches), -1, device=self.device, dtype=torch.long)
+            context["group_map"] = torch.full((t.shape[0], num_patches), -1, device=self.device, dtype=torch.long)
         gm = context["group_map"]
-        hint = torch.zeros((B, num_patches), device=self.device, dtype=torch.float32)
-        if task is not None and task.payload:
-            b = torch.tensor([p.image_idx for p in task.payload], device=self.device)
-            s = torch.tensor([p.spatial_idx for p in task.payload], device=self.device)
-            g = torch.tensor([p.group_id for p in task.payload], device=self.device)
-            h = torch.tensor([float(p.pscore_hint) for p in task.payload], device=self.device)
-            gm[b, s] = g
-            hint[b, s] = h
-        context["mobile_pscore_hint_map"] = self._normalize_patch_score_map(hint)
+        payload = task.payload if task is not None else []
+        if sliced:
+            idx_map = {orig: local for local, orig in enumerate(context["active_indices"].tolist())}
+            payload = [p for p in payload if p.image_idx in idx_map]
+            b_list = [idx_map[p.image_idx] for p in payload]
+        else:
+            b_list = [p.image_idx for p in payload]
+        s_list = [p.spatial_idx for p in payload]
+        g_list = [p.group_id for p in payload]
+        if b_list:
+            b_t = torch.tensor(b_list, device=self.device, dtype=torch.long)
+            s_t = torch.tensor(s_list, device=self.device, dtype=torch.long)
+            g_t = torch.tensor(g_list, device=self.device, dtype=torch.long)
+            gm[b_t, s_t] = g_t
+        context["mobile_pscore_hint_map"] = self._build_mobile_pscore_hint_map(task, context, config, t.shape[0],
+                                                                               num_patches)
         num_pre = self.model.num_pretokens
+        B = gm.shape[0]
+        opts = normalize_appcorr_kwargs(config.appcorr_kwargs, config.transmission_kwargs)
+        active = self._get_active_batch_indices(context, config.batch_size)
+        rms = self._compute_patch_residual_rms(context, config, active)
         plans = self._get_group_plans(context)
         plans.clear()
+        if not b_list:
+            return
         pre = torch.arange(num_pre, device=self.device).unsqueeze(0).expand(B, -1)
-        for gid in sorted(set(int(v) for v in gm.unique().tolist()) - {-1}):
+        for gid in sorted(set(g_list)):
             try:
-                spatial = torch.where(gm == gid)[1].view(B, -1)
+                spatial = s_t[g_t == gid].view(B, -1)
             except RuntimeError:
-                continue  # non-uniform group size across images (reference skips these too)
-            plans[gid] = make_group_plan(torch.cat([pre, spatial + num_pre], dim=1), num_pre)
+                print(f"!!! [Executor] Non-uniform group {gid} size detected. Fallback skip.")
+                continue
+            plans[gid] = self._build_group_plan(torch.cat([pre, spatial + num_pre], dim=1), spatial, rms, num_pre,
+                                                opts["token_prune_enabled"], opts["token_prune_threshold"],
+                                                opts["token_prune_min_keep"])
 
     def prepare_tokens(self, task: Task, context: Dict[str, Any], config: Any):
         if "input_tensor" not in context:
@@ -183,17 +329,20 @@ class DINOv3ClassifierExecutor(ModelExecutor):
         x = context.get("input_tokens")
         opts = normalize_appcorr_kwargs(config.appcorr_kwargs, config.transmission_kwargs)
         hint = context.get("mobile_pscore_hint_map")
-        # total = total + count.sum() for the two counters (dinov3_classifier.py:618-634), with the
-        # group plan's sums computed once and both additions in one launch.
-        keys = ("_token_prune_kept_patch_total", "_token_prune_full_patch_total")
-        sums = _patch_count_sums(plan)
-        prev = [cache.get(k) for k in keys]
-        if prev[0] is None and prev[1] is None:
-            cache[keys[0]], cache[keys[1]] = sums[0], sums[1]
-        else:
-            prev = [x.new_zeros((), dtype=torch.float32) if p is None else p for p in prev]
-            for k, t in zip(keys, torch._foreach_add(prev, [sums[0], sums[1]])):
-                cache[k] = t
+        # total = total + value.sum() for the four pruning counters (dinov3_classifier.py:618-634), with
+        # the group plan's sums computed once and the additions in one launch.
+        if plan.query_state is not None:
+            keys = ("_token_prune_kept_patch_total", "_token_prune_full_patch_total",
+                    "_token_prune_kept_residual_mass_total", "_token_prune_full_residual_mass_total")
+            sums = _plan_sums(plan)
+            prev = [cache.get(k) for k in keys]
+            if all(p is None for p in prev):
+                for k, v in zip(keys, sums.unbind(0)):
+                    cache[k] = v
+            else:
+                prev = [x.new_zeros((), dtype=torch.float32) if p is None else p for p in prev]
+                for k, t in zip(keys, torch._foreach_add(prev, list(sums.unbind(0)))):
+                    cache[k] = t
         self.begin_dinov3_correct_event()
         block_kwargs = dict(
             appcorr_method=opts["method"], token_keep_ratio=opts["token_keep_ratio"],
@@ -236,7 +385,8 @@ class DINOv3ClassifierExecutor(ModelExecutor):
 
         stat_keys = ("_token_pscore_kept_mass_total", "_token_pscore_full_mass_total", "_partial_token_kept_patch_total",
                      "_partial_token_full_patch_total", "_partial_token_sample_total",
-                     "_token_prune_kept_patch_total", "_token_prune_full_patch_total")
+                     "_token_prune_kept_patch_total", "_token_prune_full_patch_total",
+                     "_token_prune_kept_residual_mass_total", "_token_prune_full_residual_mass_total")
 
         def run():
             cache = context.setdefault("cache_feature", {})

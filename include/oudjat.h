@@ -72,6 +72,44 @@ int oudjat_selftest(oudjat_stream_t stream);
 int oudjat_patch_importance(const float* delta, int64_t rows, int64_t dim, int64_t row_stride,
                             int mode, float* out, oudjat_stream_t stream);
 
+/* Next-rank row f4 -- per-patch pixel-residual importance of HWC images, the residual formed on the
+ * fly. Replaces _compute_patch_residual_rms (offload/server/model/dinov3_classifier.py:91-122:
+ * mode RMS, curr / prev the decoded frames, image_idx the active images) and the mobile crop scores
+ * _compute_patch_residual_rms / _energy (offload/policies/transmission/progressive.py:14-22: prev
+ * NULL, curr the int16 Laplacian residual).
+ * curr, prev [n_images, H, W, C] row-major, dtype 0 = uint8, 1 = int16, 2 = fp32; prev may be NULL;
+ * image_idx [n_out] int64 selects the images scored (NULL: images 0 .. n_out-1; an index outside
+ * [0, n_images) scores NaN). out [n_out, (H/ph) * (W/pw)] fp32, patches row-major.
+ * d = fp32(curr) - fp32(prev); each d*d rounded to fp32; the sum over the patch's ph*pw*C values
+ * in float64 in a fixed order (exact for uint8 / int16), then rounded: ENERGY = fp32(sum),
+ * RMS = sqrt(fp32(sum / n)), L2 = sqrt(fp32(sum)), square roots correctly rounded.
+ * Requires H % ph == 0, W % pw == 0, (W/pw) * ph <= 8192. */
+int oudjat_patch_residual_score(const void* curr, const void* prev, int dtype, int64_t n_images,
+                                const int64_t* image_idx, int64_t n_out, int64_t H, int64_t W, int64_t C,
+                                int64_t ph, int64_t pw, int mode, float* out, oudjat_stream_t stream);
+
+/* Next-rank row f4 -- image-residual token pruning, the kept set and its statistics:
+ * _apply_image_residual_token_pruning (offload/server/model/dinov3_classifier.py:124-196, :143-154).
+ * r[b, p] = rms[b, spatial[b, p]] (NaN for an index outside [0, G)); keep = r >= thres (fp32) or r
+ * among the min(min_keep, P) largest of the row (torch.topk; ties to the lower candidate index, NaN
+ * largest, as oudjat_topk_plan). keep [B, P] (1 byte), kept_count [B] int32,
+ * kept_mass[b] = sum_p r * keep, full_mass[b] = sum_p r (float64 sums in a fixed order, rounded to fp32;
+ * an unkept inf / NaN makes kept_mass NaN as r * keep.float() does). P <= 16384. */
+int oudjat_residual_prune_keep(const float* rms, int64_t B, int64_t rms_stride_b, int64_t G,
+                               const int64_t* spatial, int64_t spatial_stride_b, int64_t P, float thres,
+                               int64_t min_keep, uint8_t* keep, int32_t* kept_count, float* kept_mass,
+                               float* full_mass, oudjat_stream_t stream);
+
+/* Next-rank row f4 -- the pruned candidate list (dinov3_classifier.py:163-196) at `width` (the largest
+ * kept count, read back by the caller as the reference does): pruned_dindice [B, num_pre + width] =
+ * dindice[b, :num_pre], then spatial[b, p] + num_pre of the kept candidates in candidate order, then
+ * num_pre (a zero spatial index) for the rest; kept_local_idx [B, width] = the kept candidate
+ * positions, 0 past the count. */
+int oudjat_residual_prune_compact(const uint8_t* keep, int64_t B, int64_t P, const int64_t* spatial,
+                                  int64_t spatial_stride_b, const int64_t* dindice, int64_t dindice_stride_b,
+                                  int64_t num_pre, int64_t width, int64_t* pruned_dindice,
+                                  int64_t* kept_local_idx, oudjat_stream_t stream);
+
 /* Rows 2+3 -- top-k selection and the sync-free packed query plan, one workgroup per image.
  * Replaces torch.topk in _select_patch_keep_mask (appcorr/models/dinov3/layers/block.py:358-395)
  * and _build_packed_query_state_fixed_k / _all_keep (block.py:397-490).
