@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be loaded before the HIP library, see module docstring
 
 LIB_PATH = Path(__file__).resolve().parent / "liboudjat_hip.so"
-ABI_VERSION = 9
+ABI_VERSION = 10
 
 OK = 0
 STATUS_NAMES = {
@@ -71,6 +71,8 @@ SIGNATURES: dict[str, list] = {
     "oudjat_patch_importance": [_p, _i64, _i64, _i64, _i32, _p, _p],
     "oudjat_topk_plan": [_p, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _p, _p, _p, _p, _p, _p, _p, _p, _p],
     "oudjat_threshold_keep": [_p, _i64, _i64, _i64, _f32, _p, _p, _p],
+    "oudjat_patch_attention_prob": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _f32, _i32, _p, _p, _i64,
+                                    _p],
     "oudjat_patch_residual_score": [_p, _p, _i32, _i64, _p, _i64, _i64, _i64, _i64, _i64, _i64, _i32, _p, _p],
     "oudjat_residual_prune_keep": [_p, _i64, _i64, _i64, _p, _i64, _i64, _f32, _i64, _p, _p, _p, _p, _p],
     "oudjat_residual_prune_compact": [_p, _i64, _i64, _p, _i64, _p, _i64, _i64, _i64, _p, _p, _p],

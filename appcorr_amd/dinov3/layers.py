@@ -355,12 +355,18 @@ class SelfAttentionBlock(nn.Module):
 
     def _server_pscore(self, q: Tensor, kv: Tensor, kind: str, num_patches: int) -> Tensor:
         """The approx pass's server score (attention.py:241-273) from the queries q [B, N, H, Dh] and the
-        cache kv [B, N, 2, H, Dh] (both after RoPE), with the reference's bf16 rounding points:
+        cache kv [B, N, 2, H, Dh] (both after RoPE), with the reference's rounding points:
+          patch_attn_prob(_layermean): mean over heads, then over all queries, of the full softmax
+          (:251-253), bf16 [B, N]; patch_attn_prob_layermean on 32 heads of 128 with N <= 4096 takes the
+          fused key-side sum from the row log-sum-exp instead (:241-250, attention_pscore.py:100-131);
           patch_pseudo_attn_prob(_layermean): softmax of the pseudo query (:254-261), bf16 [B, N];
           any other kind (cls_attn_prob, cls_attn_prob_layermean, random: the reference's else branch,
           :266-271): softmax of the cls query over all keys, mean over heads, fp32 [B, N]."""
         if kind in self._PATCH_ATTN_PSCORES:
-            raise NotImplementedError(f"server_pscore {kind!r} is not produced by this build's approx pass")
+            B, N, H, D = q.shape
+            fused = kind == "patch_attn_prob_layermean" and H == 32 and D == 128 and 0 < N <= 4096
+            return K.patch_attention_prob(q.reshape(B * N, H, D), kv, self.attn.scale,
+                                          K.PATTN_LSE if fused else K.PATTN_DENSE)
         if kind in self._PSEUDO_ATTN_PSCORES:
             qp = K.pseudo_query(q[:, q.shape[1] - num_patches:])
             return K.query_attention_prob(qp, kv, self.attn.scale, out_dtype=torch.bfloat16)

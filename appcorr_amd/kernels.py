@@ -690,6 +690,33 @@ def query_attention_prob(q: torch.Tensor, kv_cache: torch.Tensor, scale: float, 
     return out
 
 
+PATTN_DENSE = 0   # patch_attn_prob: torch's bf16 rounding points (attention.py:251-253)
+PATTN_LSE = 1     # the fused key-side sum from the row log-sum-exp (attention_pscore.py:20-98)
+
+
+def patch_attention_prob(q: torch.Tensor, kv_cache: torch.Tensor, scale: float, mode: int = PATTN_DENSE,
+                         workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """The mean attention probability of every key over heads and all queries -> [B, N] bf16.
+
+    q [B * N, H, Dh] (the approx pass's packed queries after RoPE, contiguous heads), kv_cache
+    [B, N, 2, H, Dh] (K after RoPE). `workspace` (fp32, >= 2*B*H*N) holds the row statistics; one is
+    allocated when not given."""
+    _require_cuda(q, kv_cache, workspace)
+    _kv_k_view_ok(kv_cache)
+    B, N, _, H, Dh = kv_cache.shape
+    _require(q.dim() == 3 and q.shape == (B * N, H, Dh) and q.stride(2) == 1 and q.stride(1) == Dh
+             and q.dtype == torch.bfloat16, "patch_attention_prob: q must be [B*N, H, Dh] bf16 with packed heads")
+    if workspace is None:
+        workspace = torch.empty((2 * B * H * N,), device=q.device, dtype=torch.float32)
+    _require(workspace.dtype == torch.float32 and workspace.is_contiguous() and workspace.numel() >= 2 * B * H * N,
+             "patch_attention_prob: workspace must be contiguous fp32 with 2*B*H*N elements")
+    out = torch.empty((B, N), device=q.device, dtype=torch.bfloat16)
+    _launch("pscore", q, "oudjat_patch_attention_prob", _ptr(q), q.stride(0), B, N, H, Dh, _ptr(kv_cache),
+            kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(3), float(scale), int(mode), _ptr(workspace),
+            _ptr(out), N, _stream(q))
+    return out
+
+
 def pseudo_query(q_patch: torch.Tensor) -> torch.Tensor:
     """The pseudo query of patch_pseudo_attn_prob (attention.py:254-259): q_patch [B, P, H, Dh] (patch
     queries after RoPE, any strides with a contiguous head dim) -> [B, H, Dh] bf16."""

@@ -348,6 +348,24 @@ int oudjat_query_attention_prob_noalloc(const uint16_t* q, int64_t q_stride_b, i
 int oudjat_pseudo_query(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_t, int64_t q_stride_h,
                         int64_t B, int64_t P, int64_t H, int64_t Dh, uint16_t* out, oudjat_stream_t stream);
 
+/* Approximate-pass dense server score: the mean attention probability of every key over heads and all
+ * N queries, without materialising the [B, H, N, N] probabilities (next-rank row f1).
+ *   mode 0 (patch_attn_prob, attention.py:251-253): s = bf16(bf16(q . k) * scale),
+ *     p = bf16(exp(s - max) / sum) (torch softmax of the bf16 scores), hm = bf16(fl(sum_h p) * fl(1/H)),
+ *     out[b, n] = bf16(fl(sum_t hm[t, n]) * fl(1/N));
+ *   mode 1 (patch_attn_prob_layermean on 32 heads of 128, N <= 4096: the fused kernel of
+ *     triton_kernels/attention_pscore.py:20-98, 172-241): s = (q . k) * scale in fp32,
+ *     p = exp2(s log2e - lse log2e) from the row log-sum-exp, out = bf16(fl(sum_{t,h} p) * fl(1/(H N))).
+ * q [B * N, H, Dh] packed rows (row stride q_row_stride elements, after RoPE); K [b, n, h, :] at
+ * kv + b*kv_stride_b + n*kv_stride_n + h*kv_stride_h (the K half of {tag}_kv). q . k is an fp32 MFMA
+ * accumulation and exp is the fp32 device exponential: agreement with an exact evaluation is to fp32
+ * rounding before each bf16 rounding. workspace: 2 * B * H * N fp32 (row statistics). out [B, N] bf16
+ * (row stride out_stride_b). Dh in {64, 128}; 16-byte aligned rows. */
+int oudjat_patch_attention_prob(const uint16_t* q, int64_t q_row_stride, int64_t B, int64_t N, int64_t H,
+                                int64_t Dh, const uint16_t* kv, int64_t kv_stride_b, int64_t kv_stride_n,
+                                int64_t kv_stride_h, float scale, int mode, float* workspace, uint16_t* out,
+                                int64_t out_stride_b, oudjat_stream_t stream);
+
 /* Introspection, no counterpart in the reference: writes to buf (NUL-terminated) the demangled name,
  * as rocprofv3 prints it, of the kernel oudjat_linear_bf16 launches for an M x N x K product with
  * epilogue epi (16-byte aligned operands); epi = 5 names the oudjat_linear_qkv_rope_kv kernel

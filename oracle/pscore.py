@@ -72,7 +72,7 @@ def _mean_bf16(p: np.ndarray, axis: int) -> np.ndarray:
 
 def _scores(q: np.ndarray, k: np.ndarray, scale: float) -> np.ndarray:
     """s = bf16(bf16(q . K^T) * scale) for q [B, H, T, D] and k [B, N, H, D] (bf16 values, fp32)."""
-    raw = np.einsum("bhtd,bnhd->bhtn", q.astype(np.float64), k.astype(np.float64))
+    raw = np.matmul(q.astype(np.float64), k.astype(np.float64).transpose(0, 2, 3, 1))   # [B, H, T, N]
     return _bf(_bf_from_exact(raw) * np.float32(scale))
 
 
@@ -123,7 +123,7 @@ def patch_attn_prob_fused(q: np.ndarray, k: np.ndarray, scale: float) -> np.ndar
     once. Exact (float64) evaluation; the reference's own fp32 kernel sums with atomics in no fixed
     order, so a device result agrees within fp32 rounding before the final bf16 rounding."""
     B, H, T, D = q.shape
-    s = np.einsum("bhtd,bnhd->bhtn", q.astype(np.float64), k.astype(np.float64)) * float(scale)
+    s = np.matmul(q.astype(np.float64), k.astype(np.float64).transpose(0, 2, 3, 1)) * float(scale)
     mx = s.max(axis=-1, keepdims=True)
     lse = mx + np.log(np.exp(s - mx).sum(axis=-1, keepdims=True))
     p = np.exp(s - lse)

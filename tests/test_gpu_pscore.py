@@ -140,3 +140,69 @@ def test_per_layer_plan_uses_the_cached_score(dev):
     k = OP.keep_count(cfg.num_patches, ratio)
     ref = OP.build_plan(score[:, 5:], k, dind.cpu().numpy(), 5, cfg.num_tokens)
     assert_bits_equal(cache["layer0_update_indice"], ref.update_indice, "update_indice")
+
+
+def _bf16_ulps(got: torch.Tensor, ref: torch.Tensor) -> np.ndarray:
+    g = got.float().cpu().numpy().astype(np.float64)
+    r = ref.float().cpu().numpy().astype(np.float64)
+    e = np.floor(np.log2(np.maximum(np.abs(r), 2.0 ** -126)))
+    return np.abs(g - r) / 2.0 ** (e - 7)
+
+
+@pytest.mark.parametrize("B,H,N,D,mode", [(1, 6, 201, 64, K.PATTN_DENSE), (2, 16, 1029, 64, K.PATTN_DENSE),
+                                          (1, 32, 301, 128, K.PATTN_DENSE), (1, 32, 1029, 128, K.PATTN_LSE),
+                                          (2, 4, 77, 64, K.PATTN_LSE)])
+def test_patch_attention_prob_vs_oracle(dev, B, H, N, D, mode):
+    """The dense score (and the fused key-side score) against the exact evaluation: the kernel's fp32
+    MFMA accumulation, fp32 exponential and fp32 sums over heads and queries move a value by at most one
+    bf16 step, and only where it sits next to a rounding boundary."""
+    print(f"patch_attention_prob B={B} H={H} N={N} D={D} mode={mode}", flush=True)
+    q, kv, qd, kvd = _qkv(B, H, N, D, 11 + N, dev)
+    got = K.patch_attention_prob(qd.reshape(B * N, H, D), kvd, D ** -0.5, mode)
+    qh = np.ascontiguousarray(q.float().numpy().transpose(0, 2, 1, 3))
+    kn = kv[:, :, 0].float().numpy()
+    fn = PS.patch_attn_prob if mode == K.PATTN_DENSE else PS.patch_attn_prob_fused
+    ref = torch.from_numpy(fn(qh, kn, D ** -0.5)).to(torch.bfloat16)
+    u = _bf16_ulps(got, ref)
+    print(f"  ulps: max {u.max():.3g}, differing {float((u > 0).mean()):.4%}", flush=True)
+    assert u.max() <= 1.0 and float((u > 0).mean()) <= 0.02
+
+
+def test_patch_attention_prob_vit7b_mass(dev):
+    """ViT-7B at 1024 px (N = 4101 > 4096: the dense path even for the layer-mean kind): every query's
+    probabilities sum to one, so the key scores of an image sum to one up to the bf16 roundings."""
+    B, H, N, D = 1, 32, 4101, 128
+    q, kv, qd, kvd = _qkv(B, H, N, D, 3, dev)
+    got = K.patch_attention_prob(qd.reshape(B * N, H, D), kvd, D ** -0.5, K.PATTN_DENSE).float()
+    assert bool((got >= 0).all())
+    tot = float(got.sum())
+    assert abs(tot - 1.0) < 2e-2, tot
+
+
+@pytest.mark.parametrize("kind", ["patch_attn_prob", "patch_attn_prob_layermean"])
+def test_approx_block_caches_the_dense_score(dev, kind):
+    cfg = OM.CONFIGS["vits16_224"]
+    B = 2
+    w = OM.make_block_weights(cfg, 0, gamma=1.0, bias_std=0.05, ln_std=0.1, depth=1)[0]
+    x_base, _, _, _ = OM.make_inputs(cfg, B, 1)
+    rope = OM.rope_tables(cfg)
+    r = (rope[0].to(dev), rope[1].to(dev))
+    blk = _block(cfg, w, dev)
+    x = x_base.to(dev)
+    with torch.no_grad():
+        _, cache = blk.approx(x, r, {}, "layer0", server_pscore=kind, server_pscore_weight=1.0)
+        N, C = cfg.num_tokens, cfg.dim
+        xn = K.layer_norm(x.reshape(B * N, C), blk.norm1.weight, blk.norm1.bias, blk.norm1.eps)
+        kv2 = torch.empty_like(cache["layer0_kv"])
+        from appcorr_amd.dinov3.layers import PackedQueryState
+        tok = torch.arange(N, device=dev)
+        qs = PackedQueryState(torch.arange(B, device=dev).repeat_interleave(N), tok.repeat(B), tok.repeat(B),
+                              None, None, None, True, (tok >= 5).repeat(B), (tok - 5).clamp_min(0).repeat(B))
+        q, _ = blk.attn._qkv_attention(xn, r, kv2, qs)
+    torch.cuda.synchronize()
+    got = cache["layer0_server_pscore"]
+    qn = q.view(B, N, cfg.heads, cfg.head_dim).cpu()
+    ref = OM.server_score(kind, qn, cache["layer0_kv"][:, :, 0].cpu(), cfg.num_patches, cfg.head_dim ** -0.5)
+    assert got.dtype == ref.dtype == torch.bfloat16
+    u = _bf16_ulps(got, ref)
+    assert u.max() <= 1.0 and float((u > 0).mean()) <= 0.02, (u.max(), float((u > 0).mean()))
