@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be loaded before the HIP library, see module docstring
 
 LIB_PATH = Path(__file__).resolve().parent / "liboudjat_hip.so"
-ABI_VERSION = 10
+ABI_VERSION = 11
 
 OK = 0
 STATUS_NAMES = {
@@ -87,7 +87,9 @@ SIGNATURES: dict[str, list] = {
     "oudjat_rope_active_inplace": [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "oudjat_qkv_rope_kv_scatter": [_p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _p, _p],
     "oudjat_layernorm_rows": [_p, _i64, _i64, _i64, _p, _p, _f32, _p, _i64, _p],
-    "oudjat_linear_bf16": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i32, _p, _p, _i64, _p, _i64, _f32, _p],
+    "oudjat_linear_bf16": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i32, _p, _p, _i64, _p, _i64, _f32, _p, _i64,
+                           _p],
+    "oudjat_linear_workspace_elems": [_i64, _i64, _i64, _i32],
     "oudjat_linear_kernel_name": [_i64, _i64, _i64, _i32, ctypes.c_char_p, _i64],
     "oudjat_packed_residual_persist": [_p, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p],
     "oudjat_packed_residual_persist_ln": [_p, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _f32, _p, _p],
@@ -109,7 +111,8 @@ SIGNATURES: dict[str, list] = {
     "oudjat_query_attention_prob_noalloc": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p,
                                             _i64, _i32, _p],
 }
-_RESTYPES = {"oudjat_status_string": ctypes.c_char_p, "oudjat_last_error": ctypes.c_char_p}
+_RESTYPES = {"oudjat_status_string": ctypes.c_char_p, "oudjat_last_error": ctypes.c_char_p,
+             "oudjat_linear_workspace_elems": ctypes.c_int64}
 
 _lock = threading.Lock()
 _lib = None

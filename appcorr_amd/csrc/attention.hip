@@ -347,11 +347,14 @@ __device__ __forceinline__ int kv_slot(int row, int chunk) { return row * 128 + 
 // light_split: 0, or kLightParts when the launch has one workgroup per (image, head) whose last
 // query wave is light; that wave's work is then done by kLightParts waves (the last ones), part p
 // taking the key tiles t with t % NST == p, and merged at the end (see the light path below).
+// full_split: 1, or 2 (small T, one workgroup per (image, head)): each full query wave's work is done
+// by two waves, part p taking the tiles of stages p and p + 2, merged at the end like the light
+// parts, so that a workgroup of few query waves still puts two or three waves on every SIMD.
 template <int NST>
 __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     const uint16_t* __restrict__ q, int64_t qrs, int T, const uint16_t* __restrict__ kv, int64_t kvb, int64_t kvn,
     int64_t kvkv, int64_t kvh, int N, float scale_log2, uint16_t* __restrict__ out, int64_t ors,
-    int waves_per_wg, int light_split) {
+    int waves_per_wg, int light_split, int full_split) {
   constexpr int DH = 64, QK_STEPS = 4, OB = 2;
   constexpr int TILEB = kKeyTile * 128;  // one K (or V) tile: 64 rows of 128 bytes
   constexpr int STAGE = 2 * TILEB;
@@ -364,10 +367,16 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, g = lane >> 5;
-  // Query wave of this wave, and its part of a split light wave (-1: not split).
-  const int lpart = (light_split && wave >= waves_per_wg - 1) ? wave - (waves_per_wg - 1) : -1;
-  const int q0 = (blockIdx.x * waves_per_wg + (lpart >= 0 ? waves_per_wg - 1 : wave)) * 32;
+  // Query wave of this wave, its part of a split full wave (fpart, 0 without a split) and its part of
+  // a split light wave (lpart, -1: not split). Full query waves 0 .. nfq - 1 take waves
+  // [0, nfq * full_split), the split light wave the kLightParts waves after them.
+  const int nfq = light_split ? waves_per_wg - 1 : waves_per_wg;
+  const int lpart = (light_split && wave >= nfq * full_split) ? wave - nfq * full_split : -1;
+  const int fpart = lpart >= 0 ? 0 : wave % full_split;
+  const int qwave = lpart >= 0 ? waves_per_wg - 1 : wave / full_split;
+  const int q0 = (blockIdx.x * waves_per_wg + qwave) * 32;
   const bool active = q0 < T;
+  const bool merged = light_split || full_split > 1;  // the parts meet in LDS after the key loop
 
   const uint16_t* kbase = kv + (int64_t)b * kvb + (int64_t)h * kvh;
   const uint32_t bytes = (uint32_t)((int64_t)N * kvn * 2);
@@ -551,10 +560,38 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
       }
     };
     Scores sa, sb;
-    pipeline(sa, sb, scores, finish, std::integral_constant<int, (1 << NST) - 1>{});
+    pipeline(sa, sb, scores, finish, full_split > 1 ? (0x5 << fpart) : (1 << NST) - 1);
 
+    if (merged) {
+      // Every wave has passed its last tile's reads after the first barrier, so the stages are free.
+      // Full-wave parts park behind the light parts' area: m, l, o[2][16] for 64 lanes per wave.
+      constexpr int LIGHT_AREA = (kLightParts - 1) * 18 * 64;
+      constexpr int FSTRIDE = 34 * 64;
+      float* fpark = reinterpret_cast<float*>(smem) + LIGHT_AREA + qwave * FSTRIDE;
+      block_barrier();
+      if (full_split > 1 && fpart == 1) {
+        fpark[lane] = m_i;
+        fpark[64 + lane] = l_i;
+#pragma unroll
+        for (int d = 0; d < OB; ++d)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) fpark[(2 + 16 * d + v) * 64 + lane] = o[d][v];
+      }
+      block_barrier();
+      if (full_split > 1 && fpart == 0) {
+        const float m1 = fpark[lane], l1 = fpark[64 + lane];
+        const float m = fmaxf(m_i, m1);  // part 0 holds tile 0: m is finite
+        const float a0 = __builtin_amdgcn_exp2f((m_i - m) * scale_log2);
+        const float a1 = __builtin_amdgcn_exp2f((m1 - m) * scale_log2);
+        l_i = fmaf(l1, a1, l_i * a0);
+#pragma unroll
+        for (int d = 0; d < OB; ++d)
+#pragma unroll
+          for (int v = 0; v < 16; ++v) o[d][v] = fmaf(fpark[(2 + 16 * d + v) * 64 + lane], a1, o[d][v] * a0);
+      }
+    }
     const int qr = q0 + l32;
-    if (active && qr < T) {
+    if (active && qr < T && fpart == 0) {
       const float inv = 1.0f / l_i;
       uint16_t* orow = out + ((int64_t)b * T + qr) * ors + (int64_t)h * DH;
 #pragma unroll
@@ -567,10 +604,6 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
           for (int e = 0; e < 4; ++e) w[e] = (__bf16)(o[d][4 * r4 + e] * inv);
           *reinterpret_cast<bf16x4_t*>(orow + d * 32 + 8 * r4 + 4 * g) = w;
         }
-    }
-    if (light_split) {  // the two barriers of the light parts' merge below
-      block_barrier();
-      block_barrier();
     }
   } else {
     // ---- Light wave (<= 16 queries left, e.g. the 5 of T = 261 after 8 full waves): 16 queries on
@@ -689,12 +722,12 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     static_assert(kLightParts == NST, "one light part per stage");
     pipeline(sa, sb, scores, finish, lpart >= 0 ? 1 << lpart : (1 << NST) - 1);
 
-    if (light_split) {
+    if (merged) {
       // Every wave has passed its last tile's reads after the first barrier, so the stages are free.
       constexpr int PSTRIDE = 18 * 64;  // floats per part: m, l, o[4][4] for 64 lanes
       float* park = reinterpret_cast<float*>(smem);
       block_barrier();
-      if (lpart > 0) {
+      if (light_split && lpart > 0) {
         float* pp = park + (lpart - 1) * PSTRIDE;
         pp[lane] = m_i;
         pp[64 + lane] = l_i;
@@ -704,7 +737,7 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
           for (int e = 0; e < 4; ++e) pp[(2 + 4 * d + e) * 64 + lane] = o[d][e];
       }
       block_barrier();
-      if (lpart == 0) {
+      if (light_split && lpart == 0) {
         float mp[kLightParts], lp[kLightParts];
         mp[0] = m_i;
         lp[0] = l_i;
@@ -754,6 +787,15 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
 
 static constexpr int kAttnStages = 4;
 
+// Two waves per full query wave (the buffer-load kernel's full_split) when a single workgroup per
+// (image, head) would otherwise have fewer than 8 waves, as long as the split still has the 8 loader
+// waves, fits the workgroup and leaves room for the parked partials (4 full waves at most).
+static int full_split_for(int64_t n_wg, int64_t nfq, int light_parts) {
+  if (n_wg != 1 || nfq > 4) return 1;
+  const int64_t waves = 2 * nfq + light_parts;
+  return (waves >= 8 && waves <= kDmaMaxWaves && nfq + (light_parts ? 1 : 0) < 8) ? 2 : 1;
+}
+
 }  // namespace oudjat
 
 using namespace oudjat;
@@ -782,9 +824,11 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
   if (w < kMinWaves) w = kMinWaves;
   dim3 grid((unsigned)n_wg, (unsigned)H, (unsigned)B);
   hipStream_t st = as_stream(stream);
-  // Buffer-load kernel for Dh = 64 with >= 8 waves (its byte offsets must fit 31 bits); the
-  // register-staged kernel otherwise.
-  const bool dma = Dh == 64 && w >= 8 && N * kvn * 2 < ((int64_t)1 << 31);
+  // Buffer-load kernel for Dh = 64 with >= 8 waves, counting the waves of split full and light
+  // query waves (its byte offsets must fit 31 bits); the register-staged kernel otherwise.
+  const bool small_split = n_wg == 1 && w < 8 && full_split_for(n_wg, (T - (w - 1) * 32 <= 16) ? w - 1 : w,
+                                                               (T - (w - 1) * 32 <= 16) ? kLightParts : 0) > 1;
+  const bool dma = Dh == 64 && (w >= 8 || small_split) && N * kvn * 2 < ((int64_t)1 << 31);
   if (dma) {
     const size_t lds_dma = (size_t)kAttnStages * 2 * kKeyTile * 128;
     static_assert((size_t)kAttnStages * 2 * kKeyTile * 128 <= 64 * 1024, "needs no larger-LDS attribute");
@@ -793,9 +837,14 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
     const int64_t last = T - (w - 1) * 32;
     const int split = (n_wg == 1 && last >= 1 && last <= 16 && w - 1 + kLightParts <= kDmaMaxWaves) ? kLightParts : 0;
     static_assert((kLightParts - 1) * 18 * 64 * 4 <= kAttnStages * 2 * kKeyTile * 128, "merge area");
-    const int threads = (split ? w - 1 + kLightParts : w) * 64;
+    const int nfq = split ? w - 1 : w;
+    const int fsplit = full_split_for(n_wg, nfq, split);
+    static_assert(((kLightParts - 1) * 18 + 4 * 34) * 64 * 4 <= kAttnStages * 2 * kKeyTile * 128,
+                  "merge area of the light parts and of four split full waves");
+    const int threads = (nfq * fsplit + (split ? kLightParts : 0)) * 64;
     sq_attention_dma_kernel<kAttnStages><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,
-                                                                          (int)N, scale_log2, out, ors, w, split);
+                                                                          (int)N, scale_log2, out, ors, w, split,
+                                                                          fsplit);
     return check_launch("sparse_query_attention");
   }
   const void* fn = Dh == 128 ? (const void*)sq_attention_kernel<128, kMinWaves, false>

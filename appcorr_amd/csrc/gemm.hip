@@ -34,6 +34,7 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <algorithm>
 #include <atomic>
 #include <mutex>
 #include <type_traits>
@@ -48,6 +49,11 @@ static constexpr int kNumXcd = 8;
 // Epilogue kind beyond the public ones: QKV projection followed by RoPE on q and k of patch rows,
 // q written packed and k, v written into the K/V cache rows (used by oudjat_linear_qkv_rope_kv).
 static constexpr int kEpiQkv = 5;
+// Split-K partial: the 16-row-block kernel over one K slice (blockIdx.y) writes its fp32 accumulator
+// tile to slice blockIdx.y of a [S, M, N] workspace; splitk_reduce_kernel sums the slices in order
+// and applies the epilogue.
+static constexpr int kEpiPartial = 6;
+static constexpr int kNumEpi = 7;
 
 struct QkvArgs {
   int H, Dh;
@@ -929,6 +935,22 @@ __device__ __forceinline__ void r16_epilogue(f32x4_t (&acc)[FMB][FNB], unsigned 
         }
     }
   }
+  if constexpr (EPI == kEpiPartial) {
+    // fp32 partial tile: lane holds 4 consecutive columns of row (lane & 15) of each 16-row block.
+    float* P = reinterpret_cast<float*>(C) + (int64_t)blockIdx.y * M * ldc;
+    const int rb0 = KSPLIT == 2 ? kg * HB : 0;
+#pragma unroll
+    for (int j = 0; j < FNB; ++j) {
+      const int col = n0 + wn0 + j * 16 + 4 * (lane >> 4);
+#pragma unroll
+      for (int i = 0; i < HB; ++i) {
+        if (rb0 + i >= FMB) continue;
+        const int row = m0 + wm * WM + (rb0 + i) * 16 + (lane & 15);
+        if (row < M) *reinterpret_cast<f32x4_t*>(P + (int64_t)row * ldc + col) = acc[i][j];
+      }
+    }
+    return;
+  }
   if constexpr (WGM > 1 && KSPLIT == 1 && RED == 0 && BM * LDT * 2 <= TILE_BYTES) {
 #pragma unroll
     for (int j = 0; j < FNB; ++j) {
@@ -1012,6 +1034,10 @@ void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t 
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int kLutOff = r16_lut_offset(BM, BN, WGM, WGN, KSPLIT, BK, NST);
   if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) load_gelu_table<NT>(smem + kLutOff);
+  if constexpr (EPI == kEpiPartial) {  // K slice blockIdx.y of length K (lda, ldw stay the full strides)
+    A += (int64_t)blockIdx.y * K;
+    W += (int64_t)blockIdx.y * K;
+  }
 
   const int tiles_n = (N + BN - 1) / BN;
   const int tiles_m = (M + BM - 1) / BM;
@@ -1415,6 +1441,32 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
                                                            ldc);
 }
 
+// Split-K second half: C[m, n] = epilogue(P[0, m, n] + P[1, m, n] + ... + P[S-1, m, n]), the slices
+// summed in order (fp32), the epilogue as the tile kernels apply it. One thread per 8 columns.
+template <int EPI>
+__global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ P, int S, int M, int N,
+                                                            EpiArgs ea, uint16_t* __restrict__ C, int64_t ldc) {
+  const int64_t per_row = N >> 3;
+  const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+  if (gid >= (int64_t)M * per_row) return;
+  const int64_t row = gid / per_row;
+  const int64_t col = (gid - row * per_row) * 8;
+  const int64_t slice = (int64_t)M * N;
+  const float* p = P + row * N + col;
+  float4 a0 = *reinterpret_cast<const float4*>(p), a1 = *reinterpret_cast<const float4*>(p + 4);
+  for (int sl = 1; sl < S; ++sl) {
+    const float4 b0 = *reinterpret_cast<const float4*>(p + sl * slice);
+    const float4 b1 = *reinterpret_cast<const float4*>(p + sl * slice + 4);
+    a0.x += b0.x; a0.y += b0.y; a0.z += b0.z; a0.w += b0.w;
+    a1.x += b1.x; a1.y += b1.y; a1.z += b1.z; a1.w += b1.w;
+  }
+  const float acc[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+  float v[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) v[e] = epilogue<EPI>(acc[e], row, col + e, ea);
+  *reinterpret_cast<uint4*>(C + row * ldc + col) = pack8(v);
+}
+
 // ------------------------------------------------------------------------------------------------
 // Configurations and dispatch
 // ------------------------------------------------------------------------------------------------
@@ -1424,7 +1476,8 @@ typedef void (*gemm_fn)(const uint16_t*, int, int, int64_t, const uint16_t*, int
 
 struct GemmCfg {
   int bm, bn, wgm, wgn, pf;  // pf: register prefetch depth; 0 = direct-to-LDS; -1 = pipelined; -2 = 16-row
-  gemm_fn fn[6];             // by epilogue; fn[kEpiQkv] only for the direct-to-LDS families
+  gemm_fn fn[kNumEpi];       // by epilogue; fn[kEpiQkv] only for the direct-to-LDS families, fn[kEpiPartial]
+                             // only for the 16-row-block family
   int bk, nst, ks;           // 16-row kernel: K tile depth, LDS stages, K groups
   int fb;                    // 16-row kernel: fragments read one K tile ahead
 };
@@ -1455,7 +1508,8 @@ struct GemmCfg {
     gemm_bf16_r16_kernel<BM, BN, WGM, WGN, KS, BK, NST, FB, 2>,                                          \
     gemm_bf16_r16_kernel<BM, BN, WGM, WGN, KS, BK, NST, FB, 3>,                                          \
     gemm_bf16_r16_kernel<BM, BN, WGM, WGN, KS, BK, NST, FB, 4>,                                          \
-    gemm_bf16_r16_kernel<BM, BN, WGM, WGN, KS, BK, NST, FB, kEpiQkv>},                                   \
+    gemm_bf16_r16_kernel<BM, BN, WGM, WGN, KS, BK, NST, FB, kEpiQkv>,                                    \
+    gemm_bf16_r16_kernel<BM, BN, WGM, WGN, KS, BK, NST, FB, kEpiPartial>},                               \
    BK, NST, KS, FB}
 
 // pf = -3: ping-pong kernel (8 waves: a 2 x 4 wave grid, 64-deep K tiles in two stages).
@@ -1563,6 +1617,28 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
 }
 
 
+// Split-K for the 144 x 128 16-row-block tiles when they leave most CUs idle: S K slices (S * tiles
+// <= 256 workgroups in one round), each slice a whole number of K tiles. Returns the configuration
+// and S (S = 1: no split). Every public epilogue: their tile forms are epilogue<EPI> element by
+// element.
+static int choose_splitk(int64_t M, int64_t N, int64_t K, int epi, int* S_out) {
+  *S_out = 1;
+  if (N % 128 != 0 || epi >= kEpiQkv) return -1;
+  const int64_t tiles = cdiv(M, 144) * (N / 128);
+  if (tiles >= 128) return -1;
+  for (int S = (int)std::min<int64_t>(4, 256 / std::max<int64_t>(tiles, 1)); S >= 2; --S) {
+    if (K % ((int64_t)S * 128) == 0 && K / S >= 256) {
+      *S_out = S;
+      return 29;
+    }
+    if (K % ((int64_t)S * 64) == 0 && K / S >= 256) {
+      *S_out = S;
+      return 23;
+    }
+  }
+  return -1;
+}
+
 // Fused QKV: tiles must cover whole heads (Dh | BN; a tile may span the q / k / v boundaries).
 // 288 x 192 (ping-pong) tiles when the plain choice would leave more CUs idle in its single round.
 static int choose_qkv_cfg(int64_t M, int64_t N, int64_t K, int64_t Dh) {
@@ -1578,7 +1654,7 @@ static int choose_qkv_cfg(int64_t M, int64_t N, int64_t K, int64_t Dh) {
 // Launches configuration `ci` with epilogue `epi` (arguments already validated).
 static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W, int64_t N,
                        int64_t ldw, int epi, const EpiArgs& ea, uint16_t* C, int64_t ldc, hipStream_t stream,
-                       const char* what) {
+                       const char* what, int splits = 1) {
   const GemmCfg& cfg = kCfgs[ci];
   const int64_t tiles = cdiv(M, cfg.bm) * cdiv(N, cfg.bn);
   OUDJAT_REQUIRE(tiles < ((int64_t)1 << 31), OUDJAT_ERR_TOO_LARGE, "%s: too many tiles", what);
@@ -1595,7 +1671,7 @@ static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t 
   OUDJAT_REQUIRE(fn != nullptr, OUDJAT_ERR_UNSUPPORTED_SHAPE, "%s: no kernel for this epilogue", what);
   if (lds > 64 * 1024) {
     // Once per kernel and device (also keeps the call out of captured launch sequences).
-    static std::atomic<uint8_t> attr_set[64][kNumCfgs][6];
+    static std::atomic<uint8_t> attr_set[64][kNumCfgs][kNumEpi];
     int dev = 0;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "%s: hipGetDevice: %s", what, hipGetErrorString(e));
@@ -1607,8 +1683,44 @@ static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t 
     }
   }
   const int threads = cfg.wgm * cfg.wgn * (cfg.pf <= -2 ? cfg.ks : 1) * 64;
-  hipLaunchKernelGGL(fn, dim3((unsigned)tiles), dim3(threads), lds, stream, A, (int)M, (int)K, lda, W, (int)N, ldw, ea,
-                     C, ldc, kGroupM);
+  // A split launch (epi == kEpiPartial) runs K / splits per workgroup, slice = blockIdx.y.
+  hipLaunchKernelGGL(fn, dim3((unsigned)tiles, (unsigned)splits), dim3(threads), lds, stream, A, (int)M,
+                     (int)(K / splits), lda, W, (int)N, ldw, ea, C, ldc, kGroupM);
+  return check_launch(what);
+}
+
+// Split-K: the partial launch into the fp32 workspace [S, M, N], then the reduce + epilogue launch.
+static int launch_gemm_splitk(int ci, int S, const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                              int64_t N, int64_t ldw, int epi, const EpiArgs& ea, uint16_t* C, int64_t ldc,
+                              float* ws, hipStream_t stream, const char* what) {
+  int st = launch_gemm(ci, A, M, K, lda, W, N, ldw, kEpiPartial, ea, reinterpret_cast<uint16_t*>(ws), N, stream,
+                       what, S);
+  if (st != OUDJAT_OK) return st;
+  if (epi == OUDJAT_EPI_BIAS_GELU) {
+    st = ensure_gelu_table();
+    if (st != OUDJAT_OK) return st;
+  }
+  const int64_t items = M * (N / 8);
+  const dim3 grid((unsigned)cdiv(items, 256));
+  switch (epi) {
+    case OUDJAT_EPI_BIAS:
+      splitk_reduce_kernel<OUDJAT_EPI_BIAS><<<grid, 256, 0, stream>>>(ws, S, (int)M, (int)N, ea, C, ldc);
+      break;
+    case OUDJAT_EPI_BIAS_GELU:
+      splitk_reduce_kernel<OUDJAT_EPI_BIAS_GELU><<<grid, 256, 0, stream>>>(ws, S, (int)M, (int)N, ea, C, ldc);
+      break;
+    case OUDJAT_EPI_BIAS_LS_RESID:
+      splitk_reduce_kernel<OUDJAT_EPI_BIAS_LS_RESID><<<grid, 256, 0, stream>>>(ws, S, (int)M, (int)N, ea, C, ldc);
+      break;
+    case OUDJAT_EPI_BIAS_LS:
+      splitk_reduce_kernel<OUDJAT_EPI_BIAS_LS><<<grid, 256, 0, stream>>>(ws, S, (int)M, (int)N, ea, C, ldc);
+      break;
+    case OUDJAT_EPI_BIAS_SILU_MUL:
+      splitk_reduce_kernel<OUDJAT_EPI_BIAS_SILU_MUL><<<grid, 256, 0, stream>>>(ws, S, (int)M, (int)N, ea, C, ldc);
+      break;
+    default:
+      return set_error(OUDJAT_ERR_UNSUPPORTED_SHAPE, "%s: no split-K reduce for epilogue %d", what, epi);
+  }
   return check_launch(what);
 }
 
@@ -1619,7 +1731,7 @@ using namespace oudjat;
 extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W, int64_t N,
                                   int64_t ldw, const uint16_t* bias, int epi, const uint16_t* gamma,
                                   const uint16_t* resid, int64_t ldr, uint16_t* C, int64_t ldc, float acc_scale,
-                                  oudjat_stream_t stream) {
+                                  float* workspace, int64_t workspace_elems, oudjat_stream_t stream) {
   OUDJAT_REQUIRE(M >= 0 && N >= 0 && K >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_bf16: negative size");
   OUDJAT_REQUIRE(epi >= OUDJAT_EPI_BIAS && epi <= OUDJAT_EPI_BIAS_SILU_MUL, OUDJAT_ERR_INVALID_ARGUMENT,
                  "linear_bf16: bad epilogue %d", epi);
@@ -1645,8 +1757,22 @@ extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64
   ea.resid = resid;
   ea.ldr = ldr;
   ea.acc_scale = acc_scale;
+  if (workspace && aligned_io && aligned(workspace, 16)) {
+    int S = 1;
+    const int ci = choose_splitk(M, N, K, epi, &S);
+    if (ci >= 0 && S > 1 && (int64_t)S * M * N <= workspace_elems)
+      return launch_gemm_splitk(ci, S, A, M, K, lda, W, N, ldw, epi, ea, C, ldc, workspace, as_stream(stream),
+                                "linear_bf16");
+  }
   return launch_gemm(choose_cfg(M, N, K, aligned_io), A, M, K, lda, W, N, ldw, epi, ea, C, ldc, as_stream(stream),
                      "linear_bf16");
+}
+
+// fp32 elements of workspace a linear_bf16 call of this shape can use for split K (0: it never splits).
+extern "C" int64_t oudjat_linear_workspace_elems(int64_t M, int64_t N, int64_t K, int epi) {
+  int S = 1;
+  if (M <= 0 || N <= 0 || K <= 0 || choose_splitk(M, N, K, epi, &S) < 0 || S <= 1) return 0;
+  return (int64_t)S * M * N;
 }
 
 extern "C" int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
@@ -1688,7 +1814,10 @@ extern "C" int oudjat_linear_kernel_name(int64_t M, int64_t N, int64_t K, int ep
   OUDJAT_REQUIRE(buf && buflen > 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_kernel_name: no buffer");
   OUDJAT_REQUIRE(M > 0 && N > 0 && K > 0 && epi >= 0 && epi <= kEpiQkv, OUDJAT_ERR_INVALID_ARGUMENT,
                  "linear_kernel_name: bad arguments");
-  const GemmCfg& c = kCfgs[epi == kEpiQkv ? choose_qkv_cfg(M, N, K, 64) : choose_cfg(M, N, K, true)];
+  int S = 1;
+  const int sk = epi == kEpiQkv ? -1 : choose_splitk(M, N, K, epi, &S);
+  if (sk >= 0 && S > 1) epi = kEpiPartial;  // split K (with a workspace): the partial kernel, then the reduce
+  const GemmCfg& c = kCfgs[sk >= 0 && S > 1 ? sk : (epi == kEpiQkv ? choose_qkv_cfg(M, N, K, 64) : choose_cfg(M, N, K, true))];
   int n;
   if (c.pf == -3)
     n = snprintf(buf, (size_t)buflen, "oudjat::gemm_bf16_pp_kernel<%d, %d, %d>", c.bm, c.bn, epi);

@@ -1,6 +1,7 @@
 """Standalone timings of the HBM-bound kernels of the correction path at the BASELINE shapes.
 
     python -m appcorr_amd.kernel_bench [--iters N] [--only name,name]
+    python -m appcorr_amd.kernel_bench --gemm      (the pass GEMM shapes, this build vs torch F.linear)
 
 One JSON line per kernel and shape: microseconds per launch (a HIP graph of back-to-back launches
 replayed between two events, inputs resident in HBM and rotated over copies that together exceed
@@ -141,10 +142,50 @@ def run(iters: int = 10, only=None) -> list[dict]:
     return out
 
 
+# The GEMMs of the correction pass: (site, M, N, K, epilogue of the pass) -- ViT-L/16 512 px, B = 16,
+# keep 25 % (M = 4176) and ViT-7B at 1024 px, B = 4, keep 10 % (M = 1656; w1 / w2 as one 16384-wide
+# product are two 8192-wide products here, as the pass runs them).
+GEMM_SHAPES = (
+    ("vitl16 qkv", 4176, 3072, 1024, _lib.EPI_BIAS),
+    ("vitl16 proj", 4176, 1024, 1024, _lib.EPI_BIAS_LS_RESID),
+    ("vitl16 fc1", 4176, 4096, 1024, _lib.EPI_BIAS_GELU),
+    ("vitl16 fc2", 4176, 1024, 4096, _lib.EPI_BIAS_LS),
+    ("vit7b16 qkv", 1656, 12288, 4096, _lib.EPI_BIAS),
+    ("vit7b16 proj", 1656, 4096, 4096, _lib.EPI_BIAS_LS_RESID),
+    ("vit7b16 w1", 1656, 8192, 4096, _lib.EPI_BIAS),
+    ("vit7b16 w3", 1656, 4096, 8192, _lib.EPI_BIAS_LS),
+)
+
+
+def run_gemms(iters: int = 10) -> list[dict]:
+    """Each pass GEMM shape with this build's kernel (the pass's epilogue) and with torch's
+    F.linear (hipBLASLt / rocBLAS, bias epilogue only) on the same bf16 operands, same timing."""
+    dev = torch.device("cuda", 0)
+    g = torch.Generator(device=dev).manual_seed(3)
+    out = []
+    for name, M, N, Kd, epi in GEMM_SHAPES:
+        a = torch.randn(M, Kd, generator=g, device=dev).to(torch.bfloat16)
+        w = (torch.randn(N, Kd, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        bias = (torch.randn(N, generator=g, device=dev) * 0.02).to(torch.bfloat16)
+        gamma = torch.full((N,), 0.5, device=dev, dtype=torch.bfloat16)
+        resid = torch.randn(M, N, generator=g, device=dev).to(torch.bfloat16) if epi == _lib.EPI_BIAS_LS_RESID else None
+        c = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+        ours = _time([lambda: K.linear(a, w, bias, epilogue=epi, gamma=gamma, resid=resid, out=c)], iters)
+        lib = _time([lambda: torch.nn.functional.linear(a, w, bias)], iters)
+        flop = 2.0 * M * N * Kd
+        out.append({"kernel": "gemm", "site": name, "M": M, "N": N, "K": Kd, "epilogue": epi,
+                    "ours_us": round(ours, 2), "library_us": round(lib, 2),
+                    "ours_tflops": round(flop / ours / 1e6, 1), "library_tflops": round(flop / lib / 1e6, 1)})
+        del a, w, bias, gamma, resid, c
+    return out
+
+
 def main(argv=None):
     ap = argparse.ArgumentParser(description=__doc__.split("\n")[0])
     ap.add_argument("--iters", type=int, default=10, help="graph replays per timing run")
     ap.add_argument("--only", default=None, help="comma-separated kernel names")
+    ap.add_argument("--gemm", action="store_true",
+                    help="time the pass GEMM shapes against torch's F.linear (hipBLASLt) instead")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="end with a plain copy of this many MiB through gather_rows (4 KiB rows, source "
                          "evicted from the caches first): the calibration dispatch for HBM byte counters")
@@ -154,7 +195,7 @@ def main(argv=None):
     _lib.verify_runtime(0)
     only = set(args.only.split(",")) if args.only else None
     with torch.no_grad():
-        for d in run(args.iters, only):
+        for d in (run_gemms(args.iters) if args.gemm else run(args.iters, only)):
             print(json.dumps(d), flush=True)
         if args.calib_copy_mib > 0:
             dev = torch.device("cuda", 0)

@@ -608,6 +608,28 @@ def linear_kernel_name(M: int, N: int, K: int, epilogue: int = _lib.EPI_BIAS) ->
     return buf.value.decode()
 
 
+_WS_ELEMS: dict = {}
+_GEMM_WS: dict = {}
+
+
+def _gemm_workspace(x: torch.Tensor, M: int, N: int, K: int, epilogue: int) -> torch.Tensor | None:
+    """The split-K scratch of one GEMM: a buffer per (device, stream), grown to the largest need and
+    reused by every GEMM launched on that stream (launches on one stream run in order)."""
+    key = (M, N, K, epilogue)
+    elems = _WS_ELEMS.get(key)
+    if elems is None:
+        elems = int(_lib.load().oudjat_linear_workspace_elems(M, N, K, epilogue))
+        _WS_ELEMS[key] = elems
+    if elems <= 0:
+        return None
+    skey = (x.device, _lib.stream_of(x))
+    buf = _GEMM_WS.get(skey)
+    if buf is None or buf.numel() < elems:
+        buf = torch.empty(elems, device=x.device, dtype=torch.float32)
+        _GEMM_WS[skey] = buf
+    return buf
+
+
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
            epilogue: int = _lib.EPI_BIAS, gamma: torch.Tensor | None = None, resid: torch.Tensor | None = None,
            out: torch.Tensor | None = None, site: str = "linear", acc_scale: float = 1.0) -> torch.Tensor:
@@ -629,10 +651,11 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
     if resid is not None:
         r2 = resid.reshape(-1, N)
         _require(r2.stride(1) == 1 and r2.shape[0] == M, "linear: resid must be [M, N] with contiguous rows")
+    ws = _gemm_workspace(x, M, N, K, int(epilogue))
     _launch(site, x, "oudjat_linear_bf16", _ptr(x2), M, K, x2.stride(0), _ptr(weight), N, weight.stride(0),
          _ptr(None if bias is None else bias.contiguous()), int(epilogue),
          _ptr(None if gamma is None else gamma.contiguous()), _ptr(r2), 0 if r2 is None else r2.stride(0), _ptr(o2),
-         o2.stride(0), float(acc_scale), _stream(x))
+         o2.stride(0), float(acc_scale), _ptr(ws), 0 if ws is None else ws.numel(), _stream(x))
     return out
 
 

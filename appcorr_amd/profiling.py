@@ -18,6 +18,12 @@
         Markdown table per (kernel, grid size): median duration from a `--kernel-trace` run and HBM
         read / write bytes per dispatch from the two counter runs, scaled as in `traffic`. For the
         standalone kernels of `python -m appcorr_amd.kernel_bench --calib-copy-mib 1024`.
+
+    python -m appcorr_amd.profiling mfma <kernel_trace.csv> <sq_counter_collection.csv>
+            <kernel substrings, comma-separated> <title> <command>
+        Markdown table per (kernel, grid size) of the matrix-core counters of one `rocprofv3 --pmc`
+        run (SQ_INSTS_MFMA, SQ_INSTS_VALU, SQ_INSTS_VALU_MFMA_MOPS_BF16, SQ_VALU_MFMA_BUSY_CYCLES) with
+        the median duration from a `--kernel-trace` run.
 """
 
 from __future__ import annotations
@@ -159,11 +165,45 @@ def kernels(trace_csv: str, fetch_csv: str, write_csv: str, calib: str, calib_by
     return "\n".join(lines)
 
 
+def mfma(trace_csv: str, sq_csv: str, subs, title: str, cmd: str) -> str:
+    """Per (kernel, grid) of the kernels named by `subs`: MFMA and VALU instruction counts, the bf16 MFMA
+    work (SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512 FLOP), the matrix-pipe busy cycles, and the median
+    duration from a kernel-trace run; the pipe's busy fraction is taken against 1024 SIMDs at the
+    2.4 GHz the 2.5 PFLOP/s dense bf16 peak is quoted at."""
+    dur = _groups(trace_csv, "duration")
+    cnt = defaultdict(lambda: defaultdict(list))
+    for r in csv.DictReader(open(sq_csv)):
+        thr = int(r["Grid_Size"]) if "Grid_Size" in r else \
+            int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+        cnt[(r["Kernel_Name"], thr)][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    lines = [f"# {title}", "", "Commands (run from the repository root on one MI355X):", "", "```", cmd, "```", "",
+             "Counters averaged per dispatch; FLOP = SQ_INSTS_VALU_MFMA_MOPS_BF16 x 512; MFMA busy = "
+             "SQ_VALU_MFMA_BUSY_CYCLES / (1024 SIMDs x 2.4 GHz x duration).", "",
+             "| kernel | grid threads | dispatches | avg us (trace) | GFLOP | TFLOP/s | MFMA insts | VALU insts | "
+             "VALU : MFMA | MFMA busy |", "|---|---:|---:|---:|---:|---:|---:|---:|---:|---:|"]
+    for key in sorted(cnt, key=lambda k: (_short(k[0]), k[1])):
+        name, thr = key
+        if not any(sub in name for sub in subs) or key not in dur:
+            continue
+        c = {n: sum(v) / len(v) for n, v in cnt[key].items()}
+        d = sorted(dur[key])
+        us = d[len(d) // 2] / 1e3
+        flop = c.get("SQ_INSTS_VALU_MFMA_MOPS_BF16", 0.0) * 512.0
+        mf, va = c.get("SQ_INSTS_MFMA", 0.0), c.get("SQ_INSTS_VALU", 0.0)
+        busy = c.get("SQ_VALU_MFMA_BUSY_CYCLES", 0.0) / (1024 * 2.4e3 * us)
+        n = len(next(iter(cnt[key].values())))
+        lines.append(f"| `{_short(name)}` | {thr} | {n} | {us:.2f} | {flop / 1e9:.2f} | {flop / us / 1e6:.0f} | "
+                     f"{mf:.0f} | {va:.0f} | {va / mf if mf else float('nan'):.1f} | {100 * busy:.1f}% |")
+    return "\n".join(lines)
+
+
 def main(argv):
     if len(argv) >= 5 and argv[0] == "kernel-stats":
         print(kernel_stats(argv[1], int(argv[2]), argv[3], argv[4]))
     elif len(argv) >= 9 and argv[0] == "traffic":
         print(traffic(argv[1], argv[2], argv[3], argv[4], float(argv[5]), argv[6], argv[7], argv[8]))
+    elif len(argv) >= 6 and argv[0] == "mfma":
+        print(mfma(argv[1], argv[2], argv[3].split(","), argv[4], argv[5]))
     elif len(argv) >= 9 and argv[0] == "kernels":
         print(kernels(argv[1], argv[2], argv[3], argv[4], float(argv[5]), argv[6].split(","), argv[7], argv[8]))
     else:

@@ -273,11 +273,22 @@ int oudjat_layernorm_rows(const uint16_t* x, int64_t rows, int64_t C, int64_t x_
  * bf16(acc * acc_scale + bias) (one rounding; 1.0 gives bf16(acc + bias) exactly). It carries the
  * per-tensor scales of an FP8 GEMM (torch._scaled_mm's scale_a * scale_b, fp8_fast_linear.py:187-194)
  * whose e4m3 operands were passed as their exact bf16 values.
+ * workspace (fp32, workspace_elems elements, may be NULL): scratch for split K. When the output tiles
+ * of a shape would leave most of the GPU idle (a small M), the call may split K over S slices that run
+ * side by side, writing fp32 partial tiles to the workspace, and sum them in slice order in a second
+ * launch that applies the epilogue; it does so only if S * M * N <= workspace_elems
+ * (oudjat_linear_workspace_elems gives that size; 0: the shape never splits). A split result differs
+ * from the unsplit one only in the fp32 summation order; both are deterministic.
  * K % 64 == 0, N % 64 == 0, all leading dimensions % 8 == 0 and 16-byte aligned pointers. */
 int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
                        int64_t N, int64_t ldw, const uint16_t* bias, int epilogue,
                        const uint16_t* gamma, const uint16_t* resid, int64_t ldr, uint16_t* C,
-                       int64_t ldc, float acc_scale, oudjat_stream_t stream);
+                       int64_t ldc, float acc_scale, float* workspace, int64_t workspace_elems,
+                       oudjat_stream_t stream);
+
+/* The workspace (fp32 elements) oudjat_linear_bf16 can use for an M x N x K product with this
+ * epilogue; 0 when it would not split K. No counterpart in the reference (cuBLAS sizes its own). */
+int64_t oudjat_linear_workspace_elems(int64_t M, int64_t N, int64_t K, int epilogue);
 
 /* Rows 6-9 fused into the QKV GEMM -- SelfAttention.correct_partial_token up to the attention call
  * (appcorr/models/dinov3/layers/attention.py:415-454): qkv = A . W^T + bias for A [M, K] and

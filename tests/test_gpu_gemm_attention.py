@@ -121,6 +121,45 @@ def test_linear_silu_mul(dev, M, N, Kd):
     assert_bf16_close(got, F64.silu_mul(base, x2), max_ulps=1, max_frac_off=1e-3, what="swiglu")
 
 
+# Split K: shapes whose 144 x 128 tiles leave most CUs idle (ViT-L keep 10 %: M = 1712; ViT-B fc2;
+# a 40-tile product split four ways). The partial tiles and the in-order fp32 sum of the slices stay
+# within the accumulation bound; the epilogues read the same sums, so each equals the oracle's epilogue
+# applied to the split GEMM's own bf16(acc + bias) (exactly, or to 1 ulp for GELU).
+SPLIT_SHAPES = [(1712, 1024, 4096), (1712, 1024, 1024), (2088, 768, 3072), (600, 1024, 2048)]
+
+
+@pytest.mark.parametrize("M,N,Kd", SPLIT_SHAPES)
+def test_linear_split_k(dev, M, N, Kd):
+    print(f"split-K GEMM {M}x{N}x{Kd}", flush=True)
+    for epi in (_lib.EPI_BIAS, _lib.EPI_BIAS_LS, _lib.EPI_BIAS_LS_RESID, _lib.EPI_BIAS_GELU, _lib.EPI_BIAS_SILU_MUL):
+        assert _lib.load().oudjat_linear_workspace_elems(M, N, Kd, epi) >= 2 * M * N
+    xd, wd, bd, base = _epi_case(dev, M, N, Kd, 40)
+    again = K.linear(xd, wd, bd)
+    assert_bits_equal(again, base, "split-K repeat")
+    g, r = _rand((N,), 44), _rand((M, N), 45)
+    got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_LS, gamma=g.to(dev))
+    assert_bits_equal(got, F64.mul(base, g), "split-K + ls")
+    got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_LS_RESID, gamma=g.to(dev), resid=r.to(dev))
+    assert_bits_equal(got, F64.fma_add(r, base, g), "split-K + ls + resid")
+    got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_GELU)
+    assert_bf16_close(got, F64.gelu(base), max_ulps=1, max_frac_off=1e-3, what="split-K + gelu")
+    got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_SILU_MUL, resid=r.to(dev))
+    assert_bf16_close(got, F64.silu_mul(base, r), max_ulps=1, max_frac_off=1e-3, what="split-K + swiglu")
+
+
+def test_linear_without_workspace_does_not_split(dev):
+    """The C ABI without a workspace runs the one-launch kernel: same bound, and the workspace size
+    query is 0 for a shape that fills the GPU."""
+    M, N, Kd = 1712, 1024, 4096
+    assert _lib.load().oudjat_linear_workspace_elems(4176, 1024, 4096, _lib.EPI_BIAS_LS) == 0
+    x, w, b = _rand((M, Kd), 50), _rand((N, Kd), 51, 0.02), _rand((N,), 52, 0.1)
+    xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
+    out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
+    _lib.call("oudjat_linear_bf16", K._ptr(xd), M, Kd, Kd, K._ptr(wd), N, Kd, K._ptr(bd), _lib.EPI_BIAS, None, None, 0,
+              K._ptr(out), N, 1.0, None, 0, K._stream(xd))
+    _check_gemm(dev, out, x, w, b, "unsplit")
+
+
 @pytest.mark.parametrize("rows,C", [(4176, 1024), (103, 384), (1656, 4096), (7, 8192)])
 def test_layer_norm(dev, rows, C):
     """|got - oracle| <= ulp(oracle) + 64 u rstd |w| max|x_row| (fp32 statistics vs fp64)."""
@@ -253,12 +292,15 @@ def test_sparse_query_attention(dev, B, T, N, H, D):
 
 @pytest.mark.parametrize("B,T,N,H,scale_up", [(16, 261, 1029, 16, 1.0), (2, 300, 777, 4, 1.0), (1, 256, 64, 3, 1.0),
                                                (2, 260, 65, 2, 1.0), (2, 261, 300, 2, 8.0), (16, 107, 1029, 16, 1.0),
-                                               (16, 517, 1029, 16, 1.0)])
+                                               (16, 517, 1029, 16, 1.0), (2, 128, 1029, 4, 1.0), (2, 137, 1029, 4, 1.0),
+                                               (2, 103, 201, 6, 8.0)])
 def test_attention_buffer_load_kernel_shapes(dev, B, T, N, H, scale_up):
     """Dh = 64 with >= 8 waves runs the kernel that loads K/V tiles straight into LDS and reads V^T
     through LDS transpose reads, with the light last wave (T % 32 in 1..16: T = 261, 260, 300, 517)
     split over four waves: one key tile, a ragged last tile of one key, 10 waves, large logits, and
-    the ViT-L keep-10 % / 50 % query counts (T = 107, 517), all against the float64 reference."""
+    the ViT-L keep-10 % / 50 % query counts (T = 107, 517); at few query waves (T = 103, 107, 128, 137)
+    each full wave's key tiles are split over two waves and merged; all against the float64
+    reference, and repeated launches are bit-identical."""
     D = 64
     q = (_rand((B * T, H, D), 40).float() * scale_up).to(torch.bfloat16)
     kv = (_rand((B, N, 2, H, D), 41).float() * scale_up).to(torch.bfloat16)

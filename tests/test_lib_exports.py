@@ -52,16 +52,16 @@ def _expect(status_name, fn, *args):
 def test_linear_rejects_bad_shapes_before_launch():
     # K not a multiple of 64
     _expect("OUDJAT_ERR_UNSUPPORTED_SHAPE", "oudjat_linear_bf16", ctypes.c_void_p(16), 4, 100, 100,
-            ctypes.c_void_p(16), 64, 100, NULL, 0, NULL, NULL, 0, ctypes.c_void_p(16), 64, 1.0, NULL)
+            ctypes.c_void_p(16), 64, 100, NULL, 0, NULL, NULL, 0, ctypes.c_void_p(16), 64, 1.0, NULL, 0, NULL)
     # bad epilogue id
     _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_linear_bf16", NULL, 4, 64, 64, NULL, 64, 64, NULL, 9, NULL, NULL, 0,
-            NULL, 64, 1.0, NULL)
+            NULL, 64, 1.0, NULL, 0, NULL)
     # LayerScale epilogue without gamma
     _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_linear_bf16", ctypes.c_void_p(16), 4, 64, 64, ctypes.c_void_p(16),
-            64, 64, NULL, 3, NULL, NULL, 0, ctypes.c_void_p(16), 64, 1.0, NULL)
+            64, 64, NULL, 3, NULL, NULL, 0, ctypes.c_void_p(16), 64, 1.0, NULL, 0, NULL)
     # misaligned A
     _expect("OUDJAT_ERR_UNSUPPORTED_LAYOUT", "oudjat_linear_bf16", ctypes.c_void_p(18), 4, 64, 64,
-            ctypes.c_void_p(16), 64, 64, NULL, 0, NULL, NULL, 0, ctypes.c_void_p(16), 64, 1.0, NULL)
+            ctypes.c_void_p(16), 64, 64, NULL, 0, NULL, NULL, 0, ctypes.c_void_p(16), 64, 1.0, NULL, 0, NULL)
 
 
 def test_low_precision_entry_points_reject_bad_arguments():
