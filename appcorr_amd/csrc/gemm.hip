@@ -1599,20 +1599,25 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   // 128 x 128 direct-to-LDS tiles otherwise (two workgroups per CU balance a ragged second round
   // better); the register-staged kernel for N % 128 != 0.
   if (N % 128 != 0) return 8;
-  const int64_t tiles256 = cdiv(M, 256) * cdiv(N, 256);
-  if (N % 256 == 0 && tiles256 >= 128 && tiles256 <= 256) return 15;
-  // 288 x 256 (ping-pong) tiles with 128-byte operand rows when they fill three quarters or more of
-  // the CUs.
+  // 288 x 256 / 288 x 192 (ping-pong) tiles with 128-byte operand rows when they fill three quarters
+  // or more of the CUs in one round: ahead of the 256 x 256 pipelined tiles, which they beat at every
+  // such shape measured (ViT-7B w1 1656 x 8192 x 4096: 94 against 111 us; a plain 4176 x 3072 x 1024
+  // product: 28.5 against 33.3 us).
   const int64_t tiles288 = cdiv(M, 288) * (N / 256);
   if (N % 256 == 0 && tiles288 >= 192 && tiles288 <= 256) return 27;
   const int64_t tiles288n = cdiv(M, 288) * (N / 192);
   if (N % 192 == 0 && tiles288n >= 192 && tiles288n <= 256) return 28;
+  const int64_t tiles256 = cdiv(M, 256) * cdiv(N, 256);
+  if (N % 256 == 0 && tiles256 >= 128 && tiles256 <= 256) return 15;
   // 144-row tiles (one round of 128..256 workgroups) when 256 x 256 tiles do not fit one round.
   const int64_t tm144 = cdiv(M, 144);
   if (N % 512 == 0 && tm144 * (N / 512) >= 128 && tm144 * (N / 512) <= 256) return 22;
   // 128-deep K tiles (half the barriers and load batches of the 64-deep ones; the two K groups still
   // take alternate 32-deep steps, so the result is the same bit for bit) when K allows.
   if (tm144 * (N / 128) >= 128 && tm144 * (N / 128) <= 256) return K % 128 == 0 ? 29 : 23;
+  // A round and a half of 288 x 192 tiles still beats 128 x 128 tiles (ViT-7B qkv, 1656 x 12288 x
+  // 4096: 170 against 183 us).
+  if (N % 192 == 0 && tiles288n > 256 && tiles288n <= 400) return 28;
   return 11;
 }
 
