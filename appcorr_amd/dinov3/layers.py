@@ -34,6 +34,7 @@ from torch import Tensor, nn
 
 from .. import _lib
 from .. import kernels as K
+from ..tracing import annotate, trace_range
 from . import lowp as LP
 
 
@@ -300,12 +301,14 @@ class SelfAttentionBlock(nn.Module):
 
     # -- dispatch (block.py:274-310) --------------------------------------------------------------
 
+    @annotate("approx")
     def approx(self, x: Tensor, rope, cache_feature: Dict, tag: str, **kwargs):
         method = kwargs.get("appcorr_method", "partial_token")
         if method != "partial_token":
             raise NotImplementedError(f"appcorr_method {method!r} is not part of this build (partial_token only)")
         return self.approx_partial_token(x, rope, cache_feature, tag, **kwargs)
 
+    @annotate("correct")
     def correct(self, x: Tensor, dindice: Tensor, rope, cache_feature: Dict, tag: str, **kwargs):
         method = kwargs.get("appcorr_method", "partial_token")
         if method != "partial_token":
@@ -495,6 +498,7 @@ class SelfAttentionBlock(nn.Module):
         for k, t in zip(keys, torch._foreach_add(prev, vals)):
             cache_feature[k] = t
 
+    @annotate("build_packed_query_state")
     def _build_query_plan(self, x: Tensor, dindice: Tensor, rope, cache_feature: Dict, tag: str, kw: dict,
                           num_pretokens: int) -> PartialTokenQueryPlan:
         B, N, _ = x.shape
@@ -634,19 +638,22 @@ class SelfAttentionBlock(nn.Module):
         """The block's arithmetic on the packed selected rows (block.py:1111-1141): returns
         (x_attn, mlp); the K/V cache rows of the selected tokens are rewritten in place. `xn`, when
         given, is norm1(x_act) already computed (by the previous block's fused residual step)."""
-        if xn is None:
-            xn = K.layer_norm(x_act, self.norm1.weight, self.norm1.bias, self.norm1.eps)   # block.py:1114
-        _, attn = self.attn._qkv_attention(xn, rope, kv, qs)                         # attention.py:415-523
-        g1 = self._gamma(self.ls1, x_act)
-        proj = self.attn.proj
-        if LP.low_precision_state(proj) == "fp4":                                    # proj_precision "fp4"
-            x_attn = K.fused_layerscale_add(x_act, K.scale_bias(*_fp4_raw(proj, attn, "proj")), g1)
-        else:
-            x_attn = _linear_route(proj, attn, "proj", epilogue=_lib.EPI_BIAS_LS_RESID,  # attention.py:532 +
-                                   gamma=g1, resid=x_act)                             # block.py:1129-1134
-        mlp = self._mlp_scaled(K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps))  # :1141
+        with trace_range("correct_attn"):
+            if xn is None:
+                xn = K.layer_norm(x_act, self.norm1.weight, self.norm1.bias, self.norm1.eps)   # block.py:1114
+            _, attn = self.attn._qkv_attention(xn, rope, kv, qs)                         # attention.py:415-523
+            g1 = self._gamma(self.ls1, x_act)
+            proj = self.attn.proj
+            if LP.low_precision_state(proj) == "fp4":                                    # proj_precision "fp4"
+                x_attn = K.fused_layerscale_add(x_act, K.scale_bias(*_fp4_raw(proj, attn, "proj")), g1)
+            else:
+                x_attn = _linear_route(proj, attn, "proj", epilogue=_lib.EPI_BIAS_LS_RESID,  # attention.py:532 +
+                                       gamma=g1, resid=x_act)                             # block.py:1129-1134
+        with trace_range("correct_ffn"):
+            mlp = self._mlp_scaled(K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps))  # :1141
         return x_attn, mlp
 
+    @annotate("correct_partial_token")
     def correct_partial_token(self, x: Tensor, dindice: Tensor, rope, cache_feature: Dict, tag: str, **kwargs):
         plan, _, kv, bos = self._prepare_correction(x, dindice, rope, cache_feature, tag, kwargs)
         qs = plan.fixed_query_state
@@ -667,6 +674,7 @@ class SelfAttentionBlock(nn.Module):
         return out, cache_feature
 
 
+@annotate("correct_blocks_packed")
 def correct_blocks_packed(blocks, x: Tensor, dindice: Tensor, rope, cache_feature: Dict, tags, **kwargs):
     """A run of correction blocks with one query plan, the selected rows kept packed between blocks.
 

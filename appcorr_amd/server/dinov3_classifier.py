@@ -18,6 +18,7 @@ import torch
 from .. import _lib
 from .. import kernels as K
 from ..dinov3.backbone import dinov3_backbone
+from ..tracing import trace_range
 from .base import ModelExecutor
 from .protocol import Task, normalize_appcorr_kwargs
 
@@ -305,11 +306,12 @@ class DINOv3ClassifierExecutor(ModelExecutor):
         cache = context.get("cache_feature", {})
         rope = context.get("rope_sincos")
         self.begin_dinov3_approx_event()
-        for lidx in range(start, end):
-            x, cache = self.run_dinov3_approx_block(lidx, x, rope, cache, tag=f"layer{lidx}",
-                                                    appcorr_method=opts["method"],
-                                                    server_pscore=opts["server_pscore"],
-                                                    server_pscore_weight=opts["server_pscore_weight"])
+        with trace_range(f"approx_forward|layers={start}-{end}"):
+            for lidx in range(start, end):
+                x, cache = self.run_dinov3_approx_block(lidx, x, rope, cache, tag=f"layer{lidx}",
+                                                        appcorr_method=opts["method"],
+                                                        server_pscore=opts["server_pscore"],
+                                                        server_pscore_weight=opts["server_pscore_weight"])
         context["current_feature"] = x
         context["cache_feature"] = cache
         return self.dinov3_approx_event_metadata()
@@ -344,26 +346,27 @@ class DINOv3ClassifierExecutor(ModelExecutor):
                 for k, t in zip(keys, torch._foreach_add(prev, list(sums.unbind(0)))):
                     cache[k] = t
         self.begin_dinov3_correct_event()
-        block_kwargs = dict(
-            appcorr_method=opts["method"], token_keep_ratio=opts["token_keep_ratio"],
-            token_keep_thres=opts["token_keep_thres"], mobile_pscore=opts["mobile_pscore"],
-            mobile_pscore_weight=opts["mobile_pscore_weight"], mobile_pscore_hint=hint,
-            server_pscore=opts["server_pscore"], server_pscore_weight=opts["server_pscore_weight"],
-            pscore_fusion=opts["pscore_fusion"], sdpa_query_bucket_size=opts["sdpa_query_bucket_size"],
-            attn_col_alive_ratio=opts["attn_col_alive_ratio"], fixed_query_state=plan.query_state,
-            group_plan=plan, attn_cache_key=group_id, debug=False)
-        # With a query plan shared by every layer the selected rows stay packed across the whole run
-        # (bit-identical to the per-block loop below, one gather and one full-tensor write in total).
-        res = None
-        if self.packed_correction and self._dinov3_correct_precision is not None and end > start:
-            res = self._dinov3_correct_precision.run_blocks_packed(range(start, end), x, dindice, rope, cache,
-                                                                   **block_kwargs)
-        if res is not None:
-            x, cache = res
-        else:
-            for lidx in range(start, end):
-                x, cache = self.run_dinov3_correct_block(lidx, x, dindice, rope, cache, f"layer{lidx}",
-                                                         source_key=f"layer{lidx}", **block_kwargs)
+        with trace_range(f"correct_forward|group={group_id}|layers={start}-{end}"):
+            block_kwargs = dict(
+                appcorr_method=opts["method"], token_keep_ratio=opts["token_keep_ratio"],
+                token_keep_thres=opts["token_keep_thres"], mobile_pscore=opts["mobile_pscore"],
+                mobile_pscore_weight=opts["mobile_pscore_weight"], mobile_pscore_hint=hint,
+                server_pscore=opts["server_pscore"], server_pscore_weight=opts["server_pscore_weight"],
+                pscore_fusion=opts["pscore_fusion"], sdpa_query_bucket_size=opts["sdpa_query_bucket_size"],
+                attn_col_alive_ratio=opts["attn_col_alive_ratio"], fixed_query_state=plan.query_state,
+                group_plan=plan, attn_cache_key=group_id, debug=False)
+            # With a query plan shared by every layer the selected rows stay packed across the whole run
+            # (bit-identical to the per-block loop below, one gather and one full-tensor write in total).
+            res = None
+            if self.packed_correction and self._dinov3_correct_precision is not None and end > start:
+                res = self._dinov3_correct_precision.run_blocks_packed(range(start, end), x, dindice, rope, cache,
+                                                                       **block_kwargs)
+            if res is not None:
+                x, cache = res
+            else:
+                for lidx in range(start, end):
+                    x, cache = self.run_dinov3_correct_block(lidx, x, dindice, rope, cache, f"layer{lidx}",
+                                                             source_key=f"layer{lidx}", **block_kwargs)
         context["current_feature"] = x
         context["cache_feature"] = cache
         return self.dinov3_correct_event_metadata()

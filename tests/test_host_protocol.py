@@ -148,3 +148,21 @@ def test_device_pointer_array_lives_with_its_holder():
     assert tuple(ptrs) not in keys, "array over a tensor the holder dropped must be evicted"
     assert tuple(ptrs[:1]) in keys and store[("cpu", tuple(ptrs[:1]))] is one
     assert K.device_pointer_array(ptrs, "cpu", None) is not a         # no holder: a fresh array each call
+
+
+def test_trace_ranges_nest_and_survive_exceptions():
+    """roctx ranges (the reference's NVTX annotations) are balanced even when the body raises."""
+    from appcorr_amd import tracing
+
+    @tracing.annotate("outer")
+    def f(fail):
+        with tracing.trace_range("inner"):
+            if fail:
+                raise KeyError("x")
+        return 3
+
+    assert f(False) == 3
+    with pytest.raises(KeyError):
+        f(True)
+    with tracing.trace_range("after"):
+        pass
