@@ -1267,6 +1267,10 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
 
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int kLutOff = r16_lut_offset(BM, BN, WGM, WGN, 1, BK, NST);
+  if constexpr (EPI == kEpiPartial) {  // K slice blockIdx.y of length K (lda, ldw stay the full strides)
+    A += (int64_t)blockIdx.y * K;
+    W += (int64_t)blockIdx.y * K;
+  }
   // The GELU table (10 KB) is only needed by the epilogue: its loads are issued here, ahead of the
   // first K tiles (so they retire first and no wait holds the tiles back), and the registers are
   // written to LDS after the K loop.
@@ -1516,7 +1520,8 @@ struct GemmCfg {
 #define OUDJAT_GEMM_PP_CFG(BM, BN)                                                                        \
   {BM, BN, 2, 4, -3,                                                                                     \
    {gemm_bf16_pp_kernel<BM, BN, 0>, gemm_bf16_pp_kernel<BM, BN, 1>, gemm_bf16_pp_kernel<BM, BN, 2>,      \
-    gemm_bf16_pp_kernel<BM, BN, 3>, gemm_bf16_pp_kernel<BM, BN, 4>, gemm_bf16_pp_kernel<BM, BN, kEpiQkv>}, \
+    gemm_bf16_pp_kernel<BM, BN, 3>, gemm_bf16_pp_kernel<BM, BN, 4>, gemm_bf16_pp_kernel<BM, BN, kEpiQkv>,  \
+    gemm_bf16_pp_kernel<BM, BN, kEpiPartial>},                                                            \
    64, 2, 1, 0}
 
 static const GemmCfg kCfgs[] = {
@@ -1622,26 +1627,38 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
 }
 
 
-// Split-K for the 144 x 128 16-row-block tiles when they leave most CUs idle: S K slices (S * tiles
-// <= 256 workgroups in one round), each slice a whole number of K tiles. Returns the configuration
-// and S (S = 1: no split). Every public epilogue: their tile forms are epilogue<EPI> element by
-// element.
+// Split K when the output tiles leave most CUs idle: S K-slices side by side (S * tiles <= 256
+// workgroups, one round), each a whole number of K tiles. Candidates: the 144 x 128 16-row-block
+// tiles with slices at least 1024 deep, and the 288 x 256 ping-pong tiles with slices at least 4096
+// deep (measured: ViT-7B w3, 1656 x 4096 x 8192, 138 -> 128 us; with 1024- or 2048-deep slices the
+// partial stores and the reduce cost more than the halved operand stream saves: ViT-L fc2 49 ->
+// 68 us, ViT-7B proj 78 -> 90 us). Among those whose split fills at least 160 CUs, the one that
+// streams the fewest operand bytes per workgroup. Returns the configuration and S (-1 / S = 1: no
+// split). Every public epilogue: their tile forms are epilogue<EPI> element by element.
 static int choose_splitk(int64_t M, int64_t N, int64_t K, int epi, int* S_out) {
   *S_out = 1;
   if (N % 128 != 0 || epi >= kEpiQkv) return -1;
-  const int64_t tiles = cdiv(M, 144) * (N / 128);
-  if (tiles >= 128) return -1;
-  for (int S = (int)std::min<int64_t>(4, 256 / std::max<int64_t>(tiles, 1)); S >= 2; --S) {
-    if (K % ((int64_t)S * 128) == 0 && K / S >= 256) {
-      *S_out = S;
-      return 29;
-    }
-    if (K % ((int64_t)S * 64) == 0 && K / S >= 256) {
-      *S_out = S;
-      return 23;
+  struct Cand { int ci, bm, bn, bk, min_slice; };
+  const Cand cands[] = {{29, 144, 128, 128, 1024}, {23, 144, 128, 64, 1024}, {27, 288, 256, 64, 4096}};
+  int best = -1, best_s = 1;
+  int64_t best_bytes = 0;
+  for (const Cand& c : cands) {
+    if (N % c.bn != 0) continue;
+    const int64_t tiles = cdiv(M, c.bm) * (N / c.bn);
+    if (tiles >= 128) continue;  // fills the GPU without a split
+    for (int S = (int)std::min<int64_t>(4, 256 / std::max<int64_t>(tiles, 1)); S >= 2; --S) {
+      if (K % ((int64_t)S * c.bk) != 0 || K / S < c.min_slice || S * tiles < 160) continue;
+      const int64_t bytes = (int64_t)(c.bm + c.bn) * (K / S);
+      if (best < 0 || bytes < best_bytes) {
+        best = c.ci;
+        best_s = S;
+        best_bytes = bytes;
+      }
+      break;
     }
   }
-  return -1;
+  *S_out = best_s;
+  return best;
 }
 
 // Fused QKV: tiles must cover whole heads (Dh | BN; a tile may span the q / k / v boundaries).

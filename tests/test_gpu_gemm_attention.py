@@ -121,11 +121,12 @@ def test_linear_silu_mul(dev, M, N, Kd):
     assert_bf16_close(got, F64.silu_mul(base, x2), max_ulps=1, max_frac_off=1e-3, what="swiglu")
 
 
-# Split K: shapes whose 144 x 128 tiles leave most CUs idle (ViT-L keep 10 %: M = 1712; ViT-B fc2;
-# a 40-tile product split four ways). The partial tiles and the in-order fp32 sum of the slices stay
-# within the accumulation bound; the epilogues read the same sums, so each equals the oracle's epilogue
-# applied to the split GEMM's own bf16(acc + bias) (exactly, or to 1 ulp for GELU).
-SPLIT_SHAPES = [(1712, 1024, 4096), (1712, 1024, 1024), (2088, 768, 3072), (600, 1024, 2048)]
+# Split K: shapes whose tiles leave most CUs idle -- 144 x 128 tiles in two slices (ViT-L keep 10 %
+# fc2, M = 1712; ViT-B fc2) and 288 x 256 ping-pong tiles in two slices (ViT-7B w3, K = 8192). The
+# partial tiles and the in-order fp32 sum of the slices stay within the accumulation bound; the
+# epilogues read the same sums, so each equals the oracle's epilogue applied to the split GEMM's own
+# bf16(acc + bias) (exactly, or to 1 ulp for GELU and SiLU).
+SPLIT_SHAPES = [(1712, 1024, 4096), (2088, 768, 3072), (1656, 4096, 8192)]
 
 
 @pytest.mark.parametrize("M,N,Kd", SPLIT_SHAPES)
@@ -151,7 +152,7 @@ def test_linear_without_workspace_does_not_split(dev):
     """The C ABI without a workspace runs the one-launch kernel: same bound, and the workspace size
     query is 0 for a shape that fills the GPU."""
     M, N, Kd = 1712, 1024, 4096
-    assert _lib.load().oudjat_linear_workspace_elems(4176, 1024, 4096, _lib.EPI_BIAS_LS) == 0
+    assert _lib.load().oudjat_linear_workspace_elems(4176, 4096, 1024, _lib.EPI_BIAS_GELU) == 0
     x, w, b = _rand((M, Kd), 50), _rand((N, Kd), 51, 0.02), _rand((N,), 52, 0.1)
     xd, wd, bd = x.to(dev), w.to(dev), b.to(dev)
     out = torch.empty(M, N, device=dev, dtype=torch.bfloat16)
