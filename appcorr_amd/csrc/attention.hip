@@ -350,11 +350,15 @@ __device__ __forceinline__ int kv_slot(int row, int chunk) { return row * 128 + 
 // full_split: 1, or 2 (small T, one workgroup per (image, head)): each full query wave's work is done
 // by two waves, part p taking the tiles of stages p and p + 2, merged at the end like the light
 // parts, so that a workgroup of few query waves still puts two or three waves on every SIMD.
-template <int NST>
+// full_split is a template parameter so that without it the full waves' stage mask is a constant and
+// each tile's S^T MFMAs and the previous tile's softmax stay in one basic block (interleaved).
+template <int NST, int FSPLIT>
 __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     const uint16_t* __restrict__ q, int64_t qrs, int T, const uint16_t* __restrict__ kv, int64_t kvb, int64_t kvn,
     int64_t kvkv, int64_t kvh, int N, float scale_log2, uint16_t* __restrict__ out, int64_t ors,
-    int waves_per_wg, int light_split, int full_split) {
+    int waves_per_wg, int light_split) {
+  constexpr int full_split = FSPLIT;
+  static_assert(FSPLIT == 1 || FSPLIT == 2, "full_split");
   constexpr int DH = 64, QK_STEPS = 4, OB = 2;
   constexpr int TILEB = kKeyTile * 128;  // one K (or V) tile: 64 rows of 128 bytes
   constexpr int STAGE = 2 * TILEB;
@@ -560,7 +564,10 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
       }
     };
     Scores sa, sb;
-    pipeline(sa, sb, scores, finish, full_split > 1 ? (0x5 << fpart) : (1 << NST) - 1);
+    if constexpr (FSPLIT > 1)
+      pipeline(sa, sb, scores, finish, 0x5 << fpart);
+    else
+      pipeline(sa, sb, scores, finish, std::integral_constant<int, (1 << NST) - 1>{});
 
     if (merged) {
       // Every wave has passed its last tile's reads after the first barrier, so the stages are free.
@@ -842,9 +849,14 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
     static_assert(((kLightParts - 1) * 18 + 4 * 34) * 64 * 4 <= kAttnStages * 2 * kKeyTile * 128,
                   "merge area of the light parts and of four split full waves");
     const int threads = (nfq * fsplit + (split ? kLightParts : 0)) * 64;
-    sq_attention_dma_kernel<kAttnStages><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,
-                                                                          (int)N, scale_log2, out, ors, w, split,
-                                                                          fsplit);
+    if (fsplit > 1)
+      sq_attention_dma_kernel<kAttnStages, 2><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv,
+                                                                               kvh, (int)N, scale_log2, out, ors, w,
+                                                                               split);
+    else
+      sq_attention_dma_kernel<kAttnStages, 1><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv,
+                                                                               kvh, (int)N, scale_log2, out, ors, w,
+                                                                               split);
     return check_launch("sparse_query_attention");
   }
   const void* fn = Dh == 128 ? (const void*)sq_attention_kernel<128, kMinWaves, false>
