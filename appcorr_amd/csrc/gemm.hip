@@ -1555,6 +1555,8 @@ static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_PP_CFG(288, 256),  // 27: ping-pong 288 x 256
     OUDJAT_GEMM_PP_CFG(288, 192),  // 28: ping-pong 288 x 192
     OUDJAT_GEMM_R16_CFG(144, 128, 1, 4, 2, 128, 2, false),  // 29: N = C GEMMs with K % 128 == 0
+    OUDJAT_GEMM_PP_CFG(224, 256),  // 30: ping-pong 224 x 256 (a full round where 288 rows leave CUs idle)
+    OUDJAT_GEMM_PP_CFG(192, 256),  // 31: ping-pong 192 x 256 (two rounds or a little less)
 };
 static constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -1609,6 +1611,10 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   // such shape measured (ViT-7B w1 1656 x 8192 x 4096: 94 against 111 us; a plain 4176 x 3072 x 1024
   // product: 28.5 against 33.3 us).
   const int64_t tiles288 = cdiv(M, 288) * (N / 256);
+  // 224 x 256 ping-pong tiles when they fill at least seven eighths of one round that 288 x 256 tiles
+  // fill less (ViT-7B w1 / w2, 1656 x 8192 x 4096: 256 against 192 tiles, 92.7 against 103.4 us).
+  const int64_t tiles224 = cdiv(M, 224) * (N / 256);
+  if (N % 256 == 0 && tiles224 >= 224 && tiles224 <= 256 && tiles288 < tiles224) return 30;
   if (N % 256 == 0 && tiles288 >= 192 && tiles288 <= 256) return 27;
   const int64_t tiles288n = cdiv(M, 288) * (N / 192);
   if (N % 192 == 0 && tiles288n >= 192 && tiles288n <= 256) return 28;
@@ -1620,8 +1626,12 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   // 128-deep K tiles (half the barriers and load batches of the 64-deep ones; the two K groups still
   // take alternate 32-deep steps, so the result is the same bit for bit) when K allows.
   if (tm144 * (N / 128) >= 128 && tm144 * (N / 128) <= 256) return K % 128 == 0 ? 29 : 23;
-  // A round and a half of 288 x 192 tiles still beats 128 x 128 tiles (ViT-7B qkv, 1656 x 12288 x
-  // 4096: 170 against 183 us).
+  // Between one and a half and two rounds of 192 x 256 ping-pong tiles (ViT-7B qkv, 1656 x 12288 x
+  // 4096: 432 tiles, 162.6 us, against 177.9 for a round and a half of 288 x 192 tiles and 185.4 for
+  // 128 x 128 tiles; also whole heads of Dh = 128 for the fused QKV epilogue, which 192 is not).
+  const int64_t tiles192 = cdiv(M, 192) * (N / 256);
+  if (N % 256 == 0 && tiles192 > 384 && tiles192 <= 512) return 31;
+  // A round and a half of 288 x 192 tiles still beats 128 x 128 tiles.
   if (N % 192 == 0 && tiles288n > 256 && tiles288n <= 400) return 28;
   return 11;
 }

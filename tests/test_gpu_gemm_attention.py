@@ -113,7 +113,7 @@ def test_linear_layerscale(dev):
     assert_bits_equal(got, F64.mul(base, g), "fc2+ls")
 
 
-@pytest.mark.parametrize("M,N,Kd", [(600, 1024, 512), (414, 8192, 4096)])
+@pytest.mark.parametrize("M,N,Kd", [(600, 1024, 512), (414, 8192, 4096), (1656, 8192, 4096)])
 def test_linear_silu_mul(dev, M, N, Kd):
     xd, wd, bd, base = _epi_case(dev, M, N, Kd, 18)
     x2 = _rand((M, N), 21)
