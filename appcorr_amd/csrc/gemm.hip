@@ -1656,8 +1656,17 @@ static int choose_splitk(int64_t M, int64_t N, int64_t K, int epi, int* S_out) {
     if (N % c.bn != 0) continue;
     const int64_t tiles = cdiv(M, c.bm) * (N / c.bn);
     if (tiles >= 128) continue;  // fills the GPU without a split
-    for (int S = (int)std::min<int64_t>(4, 256 / std::max<int64_t>(tiles, 1)); S >= 2; --S) {
-      if (K % ((int64_t)S * c.bk) != 0 || K / S < c.min_slice || S * tiles < 160) continue;
+    // A product of a few dozen 144 x 128 tiles at most with a long K loop (ViT-S at B = 1, fc2: 103
+    // rows, 3 tiles, K = 1536) splits deep, down to two K tiles per slice, on those tiles: its partial
+    // tiles are a few megabytes at most, while unsplit each workgroup would stream all of K alone on
+    // an idle GPU (16.2 against 23.5 us in 12 slices). With K < 1024 the second launch costs more
+    // than the split saves (ViT-S proj and fc1, K = 384: 13.7 -> 15.2 and 12.5 -> 14.5 us in 3).
+    const bool tiny = c.bm == 144 && tiles <= 32 && K >= 1024;
+    const int s_max = tiny ? 16 : 4;
+    const int64_t min_slice = tiny ? 2 * c.bk : c.min_slice;
+    const int64_t min_wgs = tiny ? 2 * tiles : 160;
+    for (int S = (int)std::min<int64_t>(s_max, 256 / std::max<int64_t>(tiles, 1)); S >= 2; --S) {
+      if (K % ((int64_t)S * c.bk) != 0 || K / S < min_slice || S * tiles < min_wgs) continue;
       const int64_t bytes = (int64_t)(c.bm + c.bn) * (K / S);
       if (best < 0 || bytes < best_bytes) {
         best = c.ci;

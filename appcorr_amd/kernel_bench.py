@@ -117,6 +117,28 @@ def run(iters: int = 10, only=None) -> list[dict]:
                    max(2, iters // 4))
         out.append(_line("read_reference", (nb,), us, nb, {"note": "torch sum, 512 MiB"}))
         del srcs, dsts, sums
+    for (M, Kd) in ((1656, 4096),):  # the ViT-7B fp4 pass's activation quantize-dequantize (x-hat only)
+        if not want("nvfp4_qdq"):
+            break
+        x = nvfp4_input(M, Kd, dev)
+        ts = (x.float().abs().amax() / (448.0 * 6.0)).reshape(1).to(torch.float32)
+        nbytes = 2 * M * Kd * 2
+        xs = [x] + [x.clone() for _ in range(_copies(nbytes) - 1)]
+        us = _time([(lambda xi=xi: K.nvfp4_quantize_dequantize(xi, ts)) for xi in xs], iters)
+        out.append(_line("nvfp4_qdq", (M, Kd), us, nbytes, {"copies": len(xs)}))
+        del x, xs
+    for (M, C) in ((4176, 1024), (1656, 4096)):  # norm2 of the ViT-L / ViT-7B passes
+        if not want("layernorm_rows"):
+            break
+        nbytes = 2 * M * C * 2
+        xs = [torch.randn(M, C, device=dev).to(torch.bfloat16) for _ in range(_copies(nbytes))]
+        w = torch.randn(C, device=dev).to(torch.bfloat16)
+        b = torch.randn(C, device=dev).to(torch.bfloat16)
+        outs = [torch.empty(M, C, device=dev, dtype=torch.bfloat16) for _ in range(2)]
+        us = _time([(lambda xi=xi, i=i: K.layer_norm(xi, w, b, 1e-6, out=outs[i % 2])) for i, xi in enumerate(xs)],
+                   iters)
+        out.append(_line("layernorm_rows", (M, C), us, nbytes, {"copies": len(xs)}))
+        del xs, outs
     B, N, C, H, Dh, k = 16, 1029, 1024, 16, 64, 256
     T = 5 + k
     g = torch.Generator(device=dev).manual_seed(1)

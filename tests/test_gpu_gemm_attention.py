@@ -122,11 +122,12 @@ def test_linear_silu_mul(dev, M, N, Kd):
 
 
 # Split K: shapes whose tiles leave most CUs idle -- 144 x 128 tiles in two slices (ViT-L keep 10 %
-# fc2, M = 1712; ViT-B fc2) and 288 x 256 ping-pong tiles in two slices (ViT-7B w3, K = 8192). The
+# fc2, M = 1712; ViT-B fc2), 288 x 256 ping-pong tiles in two slices (ViT-7B w3, K = 8192) and the
+# ViT-S B = 1 fc2 (103 rows, 12 slices). The
 # partial tiles and the in-order fp32 sum of the slices stay within the accumulation bound; the
 # epilogues read the same sums, so each equals the oracle's epilogue applied to the split GEMM's own
 # bf16(acc + bias) (exactly, or to 1 ulp for GELU and SiLU).
-SPLIT_SHAPES = [(1712, 1024, 4096), (2088, 768, 3072), (1656, 4096, 8192)]
+SPLIT_SHAPES = [(1712, 1024, 4096), (2088, 768, 3072), (1656, 4096, 8192), (103, 384, 1536)]
 
 
 @pytest.mark.parametrize("M,N,Kd", SPLIT_SHAPES)
