@@ -315,6 +315,25 @@ def test_attention_buffer_load_kernel_shapes(dev, B, T, N, H, scale_up):
     assert_bits_equal(again, got, "repeat launch")
 
 
+@pytest.mark.parametrize("B,T,N,H,scale_up", [(4, 414, 4101, 32, 1.0), (1, 7, 64, 2, 1.0), (2, 257, 65, 3, 1.0),
+                                               (1, 300, 300, 4, 8.0), (2, 512, 1029, 2, 1.0), (1, 33, 129, 1, 1.0)])
+def test_attention_buffer_load_kernel_dh128(dev, B, T, N, H, scale_up):
+    """Dh = 128 runs the buffer-load kernel with 256-byte K / V rows and 8 waves per workgroup, the
+    query waves spread over ceil(waves / 8) workgroups (ViT-7B T = 414: 7 and 6); one key tile, a
+    ragged last tile of one key, one query wave, spare waves that only load, large logits; against
+    the float64 reference, and repeated launches are bit-identical."""
+    D = 128
+    q = (_rand((B * T, H, D), 42).float() * scale_up).to(torch.bfloat16)
+    kv = (_rand((B, N, 2, H, D), 43).float() * scale_up).to(torch.bfloat16)
+    got = K.sparse_query_attention(q.to(dev), kv.to(dev), T, D ** -0.5).cpu()
+    qb = q.reshape(B, T, H, D).transpose(1, 2)
+    o64 = F64.sdpa(qb, kv[:, :, 0].transpose(1, 2), kv[:, :, 1].transpose(1, 2), D ** -0.5)
+    o64 = o64.transpose(1, 2).reshape(B * T, H * D)
+    _check_attention(got, qb, kv, D ** -0.5, o64, f"attention dh128 {B},{T},{N},{H} x{scale_up}")
+    again = K.sparse_query_attention(q.to(dev), kv.to(dev), T, D ** -0.5).cpu()
+    assert_bits_equal(again, got, "repeat launch")
+
+
 def test_sparse_query_attention_peaked_softmax(dev):
     # Large logits: the online max rescaling must keep exp() in range.
     B, T, N, H, D = 2, 40, 300, 2, 64
