@@ -342,16 +342,7 @@ __device__ __forceinline__ int kv_swz(int row) {
   const int m = (row >> 1) & 7;
   return m ^ ((m & 1) << 2);
 }
-// 256-byte rows (Dh = 128, 16 chunks; one row spans all 64 banks): chunk ^ sw(row) with sw swapping
-// the two 2-bit fields of row % 16, a bijection on 16 consecutive keys (so those keys at one chunk --
-// the S^T operand reads -- cover all 64 banks) that gives the 4 keys of one 4x16 transpose read 4
-// different aligned groups of 4 chunks. sw(row + 16 j) = sw(row).
-__device__ __forceinline__ int kv_swz128(int row) { return ((row & 3) << 2) | ((row >> 2) & 3); }
-template <int DH>
-__device__ __forceinline__ int kv_slot(int row, int chunk) {
-  if constexpr (DH == 64) return row * 128 + ((chunk ^ kv_swz(row)) << 4);
-  else return row * 256 + ((chunk ^ kv_swz128(row)) << 4);
-}
+__device__ __forceinline__ int kv_slot(int row, int chunk) { return row * 128 + ((chunk ^ kv_swz(row)) << 4); }
 
 // light_split: 0, or kLightParts when the launch has one workgroup per (image, head) whose last
 // query wave is light; that wave's work is then done by kLightParts waves (the last ones), part p
@@ -361,21 +352,15 @@ __device__ __forceinline__ int kv_slot(int row, int chunk) {
 // parts, so that a workgroup of few query waves still puts two or three waves on every SIMD.
 // full_split is a template parameter so that without it the full waves' stage mask is a constant and
 // each tile's S^T MFMAs and the previous tile's softmax stay in one basic block (interleaved).
-// DH = 128 (ViT-7B): full waves only (no light or full split), 8 waves (two per SIMD, <= 256
-// registers each), 256-byte K / V rows, each of the 8 loader waves issuing two 1 KB loads of K and
-// two of V per tile; the stages (4 x 32 KB) need the larger-LDS attribute.
-template <int NST, int FSPLIT, int DH>
-__global__ __launch_bounds__(DH == 64 ? kDmaMaxWaves * 64 : 512) void sq_attention_dma_kernel(
+template <int NST, int FSPLIT>
+__global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     const uint16_t* __restrict__ q, int64_t qrs, int T, const uint16_t* __restrict__ kv, int64_t kvb, int64_t kvn,
     int64_t kvkv, int64_t kvh, int N, float scale_log2, uint16_t* __restrict__ out, int64_t ors,
     int waves_per_wg, int light_split) {
   constexpr int full_split = FSPLIT;
   static_assert(FSPLIT == 1 || FSPLIT == 2, "full_split");
-  static_assert(DH == 64 || (DH == 128 && FSPLIT == 1), "head dim");
-  constexpr int QK_STEPS = DH / 16, OB = DH / 32;
-  constexpr int ROWB = DH * 2;
-  constexpr int TILEB = kKeyTile * ROWB;  // one K (or V) tile: 64 rows of ROWB bytes
-  constexpr int LPT = DH == 64 ? 2 : 4;   // loads per tile and loader wave
+  constexpr int DH = 64, QK_STEPS = 4, OB = 2;
+  constexpr int TILEB = kKeyTile * 128;  // one K (or V) tile: 64 rows of 128 bytes
   constexpr int STAGE = 2 * TILEB;
   static_assert(NST >= 2, "stages");
   typedef short i16x4_t __attribute__((ext_vector_type(4)));
@@ -394,42 +379,32 @@ __global__ __launch_bounds__(DH == 64 ? kDmaMaxWaves * 64 : 512) void sq_attenti
   const int fpart = lpart >= 0 ? 0 : wave % full_split;
   const int qwave = lpart >= 0 ? waves_per_wg - 1 : wave / full_split;
   const int q0 = (blockIdx.x * waves_per_wg + qwave) * 32;
-  // (Dh = 128 launches 8 waves whatever the query waves per workgroup: the spare ones only load.)
-  const bool active = qwave < waves_per_wg && q0 < T;
+  const bool active = q0 < T;
   const bool merged = light_split || full_split > 1;  // the parts meet in LDS after the key loop
 
   const uint16_t* kbase = kv + (int64_t)b * kvb + (int64_t)h * kvh;
   const uint32_t bytes = (uint32_t)((int64_t)N * kvn * 2);
   const i32x4_t rsrc_k = make_buffer_rsrc(kbase, bytes);
   const i32x4_t rsrc_v = make_buffer_rsrc(kbase + kvkv, bytes);
-  // Loader wave w fills tile rows 8 w .. 8 w + 7 of K and of V: one 1 KB load each at Dh = 64 (8
-  // rows of 128 bytes, 8 lanes a row), two at Dh = 128 (4 rows of 256 bytes each, 16 lanes a row).
   const bool loader = wave < 8;
-  constexpr int LPR = ROWB / 16;  // lanes per row
-  const int lrow = 8 * wave + lane / LPR;  // tile row of this lane's first load
-  const uint32_t off0 = (uint32_t)lrow * (uint32_t)kvn * 2u +
-                        (uint32_t)(((lane % LPR) ^ (DH == 64 ? kv_swz(lrow) : kv_swz128(lrow))) << 4);
+  const int lrow = 8 * wave + (lane >> 3);                  // tile row this lane loads
+  const uint32_t off0 = (uint32_t)lrow * (uint32_t)kvn * 2u + (uint32_t)(((lane & 7) ^ kv_swz(lrow)) << 4);
   const uint32_t tstep = (uint32_t)kKeyTile * (uint32_t)kvn * 2u;
-  // Dh = 128: the second load's rows are 4 further on, with their own chunk swizzle.
-  const uint32_t off1 = DH == 64 ? 0u : (uint32_t)(lrow + 4) * (uint32_t)kvn * 2u +
-                                           (uint32_t)(((lane % LPR) ^ kv_swz128(lrow + 4)) << 4);
   const int ntiles = (N + kKeyTile - 1) / kKeyTile;
   auto issue = [&](int stage, int t) __attribute__((always_inline)) {
     if (loader) {
-      unsigned char* base = smem + stage * STAGE + wave * (8 * ROWB);
+      unsigned char* base = smem + stage * STAGE + wave * 1024;
       buffer_load_lds16(rsrc_k, base, off0 + (uint32_t)t * tstep);
-      if constexpr (DH == 128) buffer_load_lds16(rsrc_k, base + 1024, off1 + (uint32_t)t * tstep);
       buffer_load_lds16(rsrc_v, base + TILEB, off0 + (uint32_t)t * tstep);
-      if constexpr (DH == 128) buffer_load_lds16(rsrc_v, base + TILEB + 1024, off1 + (uint32_t)t * tstep);
     }
   };
-  // At most n tiles after the one needed may still be in flight (LPT loads per tile per loader).
+  // At most n tiles after the one needed may still be in flight (two loads per tile per loader).
   static_assert(NST <= 5, "wait_tiles covers up to three tiles in flight");
   auto wait_tiles = [&](int n) __attribute__((always_inline)) {
     if (n <= 0) wait_vmcnt<0>();
-    else if (n == 1) wait_vmcnt<LPT>();
-    else if (n == 2) wait_vmcnt<2 * LPT>();
-    else wait_vmcnt<3 * LPT>();
+    else if (n == 1) wait_vmcnt<2>();
+    else if (n == 2) wait_vmcnt<4>();
+    else wait_vmcnt<6>();
   };
 
   // The prologue of the K/V pipeline is common to both wave kinds below.
@@ -475,7 +450,7 @@ __global__ __launch_bounds__(DH == 64 ? kDmaMaxWaves * 64 : 512) void sq_attenti
     if (t + 2 < ntiles) step(I2{}, t + 2, sa, sb);
   };
 
-  if (DH == 128 || T - q0 > 16) {
+  if (T - q0 > 16) {
     // ---- Full wave: 32 queries on v_mfma_f32_32x32x16_bf16 (layout in the file comment). ----
     bf16x8_t qf[QK_STEPS];
     {
@@ -499,7 +474,7 @@ __global__ __launch_bounds__(DH == 64 ? kDmaMaxWaves * 64 : 512) void sq_attenti
     // address are compile-time offsets.
     int koff[QK_STEPS];
 #pragma unroll
-    for (int kstep = 0; kstep < QK_STEPS; ++kstep) koff[kstep] = kv_slot<DH>(l32, kstep * 2 + g);
+    for (int kstep = 0; kstep < QK_STEPS; ++kstep) koff[kstep] = kv_slot(l32, kstep * 2 + g);
     int voff[OB][2];
     {
       const int sl = lane & 15, hh = (lane >> 4) & 1;
@@ -507,8 +482,8 @@ __global__ __launch_bounds__(DH == 64 ? kDmaMaxWaves * 64 : 512) void sq_attenti
       for (int db = 0; db < OB; ++db) {
         const int dcol = 32 * db + 16 * hh + 4 * (sl & 3);  // first of the 4 dims this lane addresses
         const int k1 = 4 * g + (sl >> 2);                   // key of k-step 0 (first run)
-        voff[db][0] = TILEB + kv_slot<DH>(k1, dcol >> 3) + ((dcol >> 2) & 1) * 8;
-        voff[db][1] = TILEB + kv_slot<DH>(k1 + 8, dcol >> 3) + ((dcol >> 2) & 1) * 8;
+        voff[db][0] = TILEB + kv_slot(k1, dcol >> 3) + ((dcol >> 2) & 1) * 8;
+        voff[db][1] = TILEB + kv_slot(k1 + 8, dcol >> 3) + ((dcol >> 2) & 1) * 8;
       }
     }
 
@@ -522,7 +497,7 @@ __global__ __launch_bounds__(DH == 64 ? kDmaMaxWaves * 64 : 512) void sq_attenti
         bf16x8_t kf[QK_STEPS];
 #pragma unroll
         for (int kstep = 0; kstep < QK_STEPS; ++kstep)
-          kf[kstep] = as_bf16x8(*reinterpret_cast<const uint4*>(st + koff[kstep] + kb * 32 * ROWB));
+          kf[kstep] = as_bf16x8(*reinterpret_cast<const uint4*>(st + koff[kstep] + kb * 32 * 128));
         const f32x16_t zero = {};
         sc.s[kb] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(kf[0], qf[0], zero, 0, 0, 0);
 #pragma unroll
@@ -579,9 +554,9 @@ __global__ __launch_bounds__(DH == 64 ? kDmaMaxWaves * 64 : 512) void sq_attenti
 #pragma unroll
         for (int j = 0; j < 4; ++j) {
           const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) i16x4_t*)(st + voff[db][0] + j * 16 * ROWB));
+              (__attribute__((address_space(3))) i16x4_t*)(st + voff[db][0] + j * 16 * 128));
           const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
-              (__attribute__((address_space(3))) i16x4_t*)(st + voff[db][1] + j * 16 * ROWB));
+              (__attribute__((address_space(3))) i16x4_t*)(st + voff[db][1] + j * 16 * 128));
           typedef short i16x8_t __attribute__((ext_vector_type(8)));
           const i16x8_t both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
           o[db] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, both), pf[j], o[db], 0, 0, 0);
@@ -594,7 +569,7 @@ __global__ __launch_bounds__(DH == 64 ? kDmaMaxWaves * 64 : 512) void sq_attenti
     else
       pipeline(sa, sb, scores, finish, std::integral_constant<int, (1 << NST) - 1>{});
 
-    if constexpr (DH == 64) if (merged) {
+    if (merged) {
       // Every wave has passed its last tile's reads after the first barrier, so the stages are free.
       // Full-wave parts park behind the light parts' area: m, l, o[2][16] for 64 lanes per wave.
       constexpr int LIGHT_AREA = (kLightParts - 1) * 18 * 64;
@@ -637,7 +612,7 @@ __global__ __launch_bounds__(DH == 64 ? kDmaMaxWaves * 64 : 512) void sq_attenti
           *reinterpret_cast<bf16x4_t*>(orow + d * 32 + 8 * r4 + 4 * g) = w;
         }
     }
-  } else if constexpr (DH == 64) {
+  } else {
     // ---- Light wave (<= 16 queries left, e.g. the 5 of T = 261 after 8 full waves): 16 queries on
     // v_mfma_f32_16x16x32_bf16, half the MFMA and softmax work of a full wave. 8 full waves and one
     // light wave would put three waves on one SIMD, which every other SIMD then waits for at each
@@ -669,14 +644,14 @@ __global__ __launch_bounds__(DH == 64 ? kDmaMaxWaves * 64 : 512) void sq_attenti
     float m_i = -INFINITY, l_i = 0.0f;
     int koff[2];
 #pragma unroll
-    for (int ks = 0; ks < 2; ++ks) koff[ks] = kv_slot<64>(l16, 4 * ks + G);
+    for (int ks = 0; ks < 2; ++ks) koff[ks] = kv_slot(l16, 4 * ks + G);
     int voff[4][2];
 #pragma unroll
     for (int db = 0; db < 4; ++db) {
       const int dcol = 16 * db + 4 * (l16 & 3);  // first of the 4 dims this lane addresses
       const int k1 = 4 * G + (l16 >> 2);         // key of k-step 0 (first run)
-      voff[db][0] = TILEB + kv_slot<64>(k1, dcol >> 3) + ((dcol >> 2) & 1) * 8;
-      voff[db][1] = TILEB + kv_slot<64>(k1 + 16, dcol >> 3) + ((dcol >> 2) & 1) * 8;
+      voff[db][0] = TILEB + kv_slot(k1, dcol >> 3) + ((dcol >> 2) & 1) * 8;
+      voff[db][1] = TILEB + kv_slot(k1 + 16, dcol >> 3) + ((dcol >> 2) & 1) * 8;
     }
     struct Scores16 {
       f32x4_t s[4];
@@ -875,34 +850,13 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
                   "merge area of the light parts and of four split full waves");
     const int threads = (nfq * fsplit + (split ? kLightParts : 0)) * 64;
     if (fsplit > 1)
-      sq_attention_dma_kernel<kAttnStages, 2, 64><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv,
+      sq_attention_dma_kernel<kAttnStages, 2><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv,
                                                                                kvh, (int)N, scale_log2, out, ors, w,
                                                                                split);
     else
-      sq_attention_dma_kernel<kAttnStages, 1, 64><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv,
+      sq_attention_dma_kernel<kAttnStages, 1><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv,
                                                                                kvh, (int)N, scale_log2, out, ors, w,
                                                                                split);
-    return check_launch("sparse_query_attention");
-  }
-  if (Dh == 128 && N * kvn * 2 < ((int64_t)1 << 31)) {
-    // Buffer-load kernel for Dh = 128: 8 waves per workgroup (all of them load), the query waves
-    // spread evenly over the workgroups of an (image, head) (ViT-7B, T = 414: 7 and 6 of 13).
-    const size_t lds_dma = (size_t)kAttnStages * 2 * kKeyTile * 256;
-    const void* fn128 = (const void*)sq_attention_dma_kernel<kAttnStages, 1, 128>;
-    static std::atomic<uint8_t> attr128[64];
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "sparse_query_attention: %s", hipGetErrorString(e));
-    if (!attr128[dev & 63].load(std::memory_order_acquire)) {
-      e = hipFuncSetAttribute(fn128, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds_dma);
-      if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "sparse_query_attention: %s", hipGetErrorString(e));
-      attr128[dev & 63].store(1, std::memory_order_release);
-    }
-    const int64_t n128 = cdiv(waves, 8);
-    const int w128 = (int)cdiv(waves, n128);
-    dim3 grid128((unsigned)n128, (unsigned)H, (unsigned)B);
-    sq_attention_dma_kernel<kAttnStages, 1, 128><<<grid128, 8 * 64, lds_dma, st>>>(
-        q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N, scale_log2, out, ors, w128, 0);
     return check_launch("sparse_query_attention");
   }
   const void* fn = Dh == 128 ? (const void*)sq_attention_kernel<128, kMinWaves, false>

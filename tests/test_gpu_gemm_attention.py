@@ -317,10 +317,9 @@ def test_attention_buffer_load_kernel_shapes(dev, B, T, N, H, scale_up):
 
 @pytest.mark.parametrize("B,T,N,H,scale_up", [(4, 414, 4101, 32, 1.0), (1, 7, 64, 2, 1.0), (2, 257, 65, 3, 1.0),
                                                (1, 300, 300, 4, 8.0), (2, 512, 1029, 2, 1.0), (1, 33, 129, 1, 1.0)])
-def test_attention_buffer_load_kernel_dh128(dev, B, T, N, H, scale_up):
-    """Dh = 128 runs the buffer-load kernel with 256-byte K / V rows and 8 waves per workgroup, the
-    query waves spread over ceil(waves / 8) workgroups (ViT-7B T = 414: 7 and 6); one key tile, a
-    ragged last tile of one key, one query wave, spare waves that only load, large logits; against
+def test_attention_dh128_shapes(dev, B, T, N, H, scale_up):
+    """Dh = 128 (ViT-7B heads): the query waves spread over ceil(waves / 8) workgroups (T = 414: 7
+    and 6 waves), one key tile, a ragged last tile of one key, one query wave, large logits; against
     the float64 reference, and repeated launches are bit-identical."""
     D = 128
     q = (_rand((B * T, H, D), 42).float() * scale_up).to(torch.bfloat16)
