@@ -1446,7 +1446,10 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
 }
 
 // Split-K second half: C[m, n] = epilogue(P[0, m, n] + P[1, m, n] + ... + P[S-1, m, n]), the slices
-// summed in order (fp32), the epilogue as the tile kernels apply it. One thread per 8 columns.
+// summed in order (fp32), the epilogue as the tile kernels apply it (epilogue<EPI>'s arithmetic). One
+// thread per 8 columns; the per-column bias / gamma and the residual or gate row segment are read as
+// vectors (the split path runs only with the aligned epilogue operands of `aligned_io`), and every
+// load of a thread is issued before its first add.
 template <int EPI>
 __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restrict__ P, int S, int M, int N,
                                                             EpiArgs ea, uint16_t* __restrict__ C, int64_t ldc) {
@@ -1457,17 +1460,45 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   const int64_t col = (gid - row * per_row) * 8;
   const int64_t slice = (int64_t)M * N;
   const float* p = P + row * N + col;
+  float bias[8], side[8], g[8];
+  if (ea.bias) {
+    const uint2 b0 = *reinterpret_cast<const uint2*>(ea.bias + col);
+    const uint2 b1 = *reinterpret_cast<const uint2*>(ea.bias + col + 4);
+    bias[0] = lo_bf16(b0.x); bias[1] = hi_bf16(b0.x); bias[2] = lo_bf16(b0.y); bias[3] = hi_bf16(b0.y);
+    bias[4] = lo_bf16(b1.x); bias[5] = hi_bf16(b1.x); bias[6] = lo_bf16(b1.y); bias[7] = hi_bf16(b1.y);
+  } else {
+#pragma unroll
+    for (int e = 0; e < 8; ++e) bias[e] = 0.0f;
+  }
+  if constexpr (EPI == OUDJAT_EPI_BIAS_LS || EPI == OUDJAT_EPI_BIAS_LS_RESID)
+    unpack8(*reinterpret_cast<const uint4*>(ea.gamma + col), g);
+  if constexpr (EPI == OUDJAT_EPI_BIAS_LS_RESID || EPI == OUDJAT_EPI_BIAS_SILU_MUL)
+    unpack8(*reinterpret_cast<const uint4*>(ea.resid + row * ea.ldr + col), side);
   float4 a0 = *reinterpret_cast<const float4*>(p), a1 = *reinterpret_cast<const float4*>(p + 4);
-  for (int sl = 1; sl < S; ++sl) {
-    const float4 b0 = *reinterpret_cast<const float4*>(p + sl * slice);
-    const float4 b1 = *reinterpret_cast<const float4*>(p + sl * slice + 4);
+  if (S == 2) {
+    const float4 b0 = *reinterpret_cast<const float4*>(p + slice);
+    const float4 b1 = *reinterpret_cast<const float4*>(p + slice + 4);
     a0.x += b0.x; a0.y += b0.y; a0.z += b0.z; a0.w += b0.w;
     a1.x += b1.x; a1.y += b1.y; a1.z += b1.z; a1.w += b1.w;
+  } else {
+    for (int sl = 1; sl < S; ++sl) {
+      const float4 b0 = *reinterpret_cast<const float4*>(p + sl * slice);
+      const float4 b1 = *reinterpret_cast<const float4*>(p + sl * slice + 4);
+      a0.x += b0.x; a0.y += b0.y; a0.z += b0.z; a0.w += b0.w;
+      a1.x += b1.x; a1.y += b1.y; a1.z += b1.z; a1.w += b1.w;
+    }
   }
   const float acc[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
   float v[8];
 #pragma unroll
-  for (int e = 0; e < 8; ++e) v[e] = epilogue<EPI>(acc[e], row, col + e, ea);
+  for (int e = 0; e < 8; ++e) {
+    float x = round_bf16(__builtin_fmaf(acc[e], ea.acc_scale, bias[e]));
+    if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) x = __uint_as_float(gelu_bf16_bits(__float_as_uint(x) >> 16, g_gelu_lut) << 16);
+    else if constexpr (EPI == OUDJAT_EPI_BIAS_LS_RESID) x = fmaf(x, g[e], side[e]);
+    else if constexpr (EPI == OUDJAT_EPI_BIAS_LS) x = x * g[e];
+    else if constexpr (EPI == OUDJAT_EPI_BIAS_SILU_MUL) x = round_bf16(x / (1.0f + expf(-x))) * side[e];
+    v[e] = x;
+  }
   *reinterpret_cast<uint4*>(C + row * ldc + col) = pack8(v);
 }
 
