@@ -426,28 +426,37 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
   using I3 = std::integral_constant<int, 3>;
   // `stages`: bit s set when this wave computes the tiles held in stage s (all of them, except for
   // the parts of a split light wave).
-  auto pipeline = [&](auto& sa, auto& sb, auto&& scores, auto&& finish, auto stages) __attribute__((always_inline)) {
-    if (active && (stages & 1)) scores(sa, smem);
-    auto step = [&](auto stage_c, int t, auto& cur, auto& nxt) __attribute__((always_inline)) {
+  // `act`: `active`, or std::true_type where the caller knows the wave is active (the full waves:
+  // T - q0 > 16), so that no branch separates a tile's S^T MFMAs from the previous tile's softmax and
+  // the scheduler can interleave them. The steps of the main loop never hold the last (ragged) key
+  // tile, so their softmax has no masking branch either (`mask_c` false).
+  using BF = std::false_type;
+  using BT = std::true_type;
+  auto pipeline = [&](auto& sa, auto& sb, auto&& scores, auto&& finish, auto stages, auto act)
+                      __attribute__((always_inline)) {
+    if (act && (stages & 1)) scores(sa, smem);
+    auto step = [&](auto stage_c, int t, auto& cur, auto& nxt, auto last_c) __attribute__((always_inline)) {
       constexpr int SG = decltype(stage_c)::value;  // stage of tile t
-      if (t + 1 < ntiles) {
+      constexpr bool TAIL = decltype(last_c)::value;  // the step may hold the last tile
+      if (!TAIL || t + 1 < ntiles) {
         wait_tiles(min(NST - 3, ntiles - 2 - t));
         block_barrier();
         if (t + NST - 1 < ntiles) issue((SG + NST - 1) % NST, t + NST - 1);
-        if (active && ((stages >> ((SG + 1) % NST)) & 1)) scores(nxt, smem + ((SG + 1) % NST) * STAGE);
+        if (act && ((stages >> ((SG + 1) % NST)) & 1)) scores(nxt, smem + ((SG + 1) % NST) * STAGE);
       }
-      if (active && ((stages >> SG) & 1)) finish(cur, smem + SG * STAGE, t);
+      if (act && ((stages >> SG) & 1)) finish(cur, smem + SG * STAGE, t, last_c);
     };
     int t = 0;
-    for (; t + NST <= ntiles; t += NST) {
-      step(I0{}, t, sa, sb);
-      step(I1{}, t + 1, sb, sa);
-      step(I2{}, t + 2, sa, sb);
-      step(I3{}, t + 3, sb, sa);
+    for (; t + NST < ntiles; t += NST) {
+      step(I0{}, t, sa, sb, BF{});
+      step(I1{}, t + 1, sb, sa, BF{});
+      step(I2{}, t + 2, sa, sb, BF{});
+      step(I3{}, t + 3, sb, sa, BF{});
     }
-    if (t < ntiles) step(I0{}, t, sa, sb);
-    if (t + 1 < ntiles) step(I1{}, t + 1, sb, sa);
-    if (t + 2 < ntiles) step(I2{}, t + 2, sa, sb);
+    if (t < ntiles) step(I0{}, t, sa, sb, BT{});
+    if (t + 1 < ntiles) step(I1{}, t + 1, sb, sa, BT{});
+    if (t + 2 < ntiles) step(I2{}, t + 2, sa, sb, BT{});
+    if (t + 3 < ntiles) step(I3{}, t + 3, sb, sa, BT{});
   };
 
   if (T - q0 > 16) {
@@ -506,9 +515,9 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
       }
     };
     // Online softmax of tile t and O^T += V^T . P^T with V from stage `st`.
-    auto finish = [&](Scores& sc, const unsigned char* st, int t) __attribute__((always_inline)) {
+    auto finish = [&](Scores& sc, const unsigned char* st, int t, auto mask_c) __attribute__((always_inline)) {
       f32x16_t (&s)[2] = sc.s;
-      if ((t + 1) * kKeyTile > N) {
+      if (decltype(mask_c)::value && (t + 1) * kKeyTile > N) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
@@ -565,9 +574,9 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     };
     Scores sa, sb;
     if constexpr (FSPLIT > 1)
-      pipeline(sa, sb, scores, finish, 0x5 << fpart);
+      pipeline(sa, sb, scores, finish, 0x5 << fpart, BT{});
     else
-      pipeline(sa, sb, scores, finish, std::integral_constant<int, (1 << NST) - 1>{});
+      pipeline(sa, sb, scores, finish, std::integral_constant<int, (1 << NST) - 1>{}, BT{});
 
     if (merged) {
       // Every wave has passed its last tile's reads after the first barrier, so the stages are free.
@@ -666,9 +675,9 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
         sc.s[kb] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qf[1], sc.s[kb], 0, 0, 0);
       }
     };
-    auto finish = [&](Scores16& sc, const unsigned char* st, int t) __attribute__((always_inline)) {
+    auto finish = [&](Scores16& sc, const unsigned char* st, int t, auto mask_c) __attribute__((always_inline)) {
       f32x4_t (&s)[4] = sc.s;
-      if ((t + 1) * kKeyTile > N) {
+      if (decltype(mask_c)::value && (t + 1) * kKeyTile > N) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
@@ -727,7 +736,7 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     };
     Scores16 sa, sb;
     static_assert(kLightParts == NST, "one light part per stage");
-    pipeline(sa, sb, scores, finish, lpart >= 0 ? 1 << lpart : (1 << NST) - 1);
+    pipeline(sa, sb, scores, finish, lpart >= 0 ? 1 << lpart : (1 << NST) - 1, active);
 
     if (merged) {
       // Every wave has passed its last tile's reads after the first barrier, so the stages are free.
