@@ -1647,21 +1647,38 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   const int64_t tiles224 = cdiv(M, 224) * (N / 256);
   if (N % 256 == 0 && tiles224 >= 224 && tiles224 <= 256 && tiles288 < tiles224) return 30;
   if (N % 256 == 0 && tiles288 >= 192 && tiles288 <= 256) return 27;
+  // Two rounds of 288-, 224- or 192-row ping-pong tiles 256 wide, whichever fills them most (ViT-L
+  // keep 50 %, M = 8272: fc1 4096 wide, 464 tiles of 288 x 256, 62.7 us; qkv 3072 wide, 444 tiles of
+  // 224 x 256, 53.7 us, where 128 x 128 tiles took 85.0 and 73.3 us; ViT-7B qkv, 1656 x 12288 x 4096:
+  // 432 tiles of 192 x 256, 162.6 us, against 177.9 for a round and a half of 288 x 192 tiles and
+  // 185.4 for 128 x 128 tiles; 192 x 256 also takes whole heads of Dh = 128 for the fused QKV
+  // epilogue, which 192-wide tiles do not).
+  if (N % 256 == 0) {
+    const int64_t tiles192 = cdiv(M, 192) * (N / 256);
+    int best = -1;
+    int64_t best_tiles = 0;
+    const int64_t cand_tiles[3] = {tiles288, tiles224, tiles192};
+    const int cand_cfg[3] = {27, 30, 31};
+    for (int c = 0; c < 3; ++c)
+      if (cand_tiles[c] > 256 && cand_tiles[c] <= 512 && cand_tiles[c] > best_tiles) {
+        best = cand_cfg[c];
+        best_tiles = cand_tiles[c];
+      }
+    if (best >= 0 && best_tiles > 384) return best;
+  }
   const int64_t tiles288n = cdiv(M, 288) * (N / 192);
   if (N % 192 == 0 && tiles288n >= 192 && tiles288n <= 256) return 28;
+  // Half a round or more of 256 x 256 tiles: 224 x 256 ping-pong tiles if they still fit one round
+  // (ViT-L keep 50 %, 8272 x 1024: 148 tiles, proj 27.5 us and fc2 78.3 us against 34.9 and 101.4 for
+  // the 132 pipelined 256 x 256 tiles), else those.
   const int64_t tiles256 = cdiv(M, 256) * cdiv(N, 256);
-  if (N % 256 == 0 && tiles256 >= 128 && tiles256 <= 256) return 15;
+  if (N % 256 == 0 && tiles256 >= 128 && tiles256 <= 256) return tiles224 <= 256 ? 30 : 15;
   // 144-row tiles (one round of 128..256 workgroups) when 256 x 256 tiles do not fit one round.
   const int64_t tm144 = cdiv(M, 144);
   if (N % 512 == 0 && tm144 * (N / 512) >= 128 && tm144 * (N / 512) <= 256) return 22;
   // 128-deep K tiles (half the barriers and load batches of the 64-deep ones; the two K groups still
   // take alternate 32-deep steps, so the result is the same bit for bit) when K allows.
   if (tm144 * (N / 128) >= 128 && tm144 * (N / 128) <= 256) return K % 128 == 0 ? 29 : 23;
-  // Between one and a half and two rounds of 192 x 256 ping-pong tiles (ViT-7B qkv, 1656 x 12288 x
-  // 4096: 432 tiles, 162.6 us, against 177.9 for a round and a half of 288 x 192 tiles and 185.4 for
-  // 128 x 128 tiles; also whole heads of Dh = 128 for the fused QKV epilogue, which 192 is not).
-  const int64_t tiles192 = cdiv(M, 192) * (N / 256);
-  if (N % 256 == 0 && tiles192 > 384 && tiles192 <= 512) return 31;
   // A round and a half of 288 x 192 tiles still beats 128 x 128 tiles.
   if (N % 192 == 0 && tiles288n > 256 && tiles288n <= 400) return 28;
   return 11;
