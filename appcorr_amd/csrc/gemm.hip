@@ -1668,17 +1668,23 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   }
   const int64_t tiles288n = cdiv(M, 288) * (N / 192);
   if (N % 192 == 0 && tiles288n >= 192 && tiles288n <= 256) return 28;
-  // Half a round or more of 256 x 256 tiles: 224 x 256 ping-pong tiles if they still fit one round
-  // (ViT-L keep 50 %, 8272 x 1024: 148 tiles, proj 27.5 us and fc2 78.3 us against 34.9 and 101.4 for
-  // the 132 pipelined 256 x 256 tiles), else those.
+  // Half a round or more of 256 x 256 tiles: 192 x 256 or 224 x 256 ping-pong tiles if they still fit
+  // one round (ViT-L keep 50 %, 8272 x 1024: 176 tiles of 192 x 256, proj 28.7 us and fc2 77.8 us,
+  // against 30.6 / 82.3 for 224 x 256 and 34.9 / 101.4 for the 132 pipelined 256 x 256 tiles), else
+  // those.
   const int64_t tiles256 = cdiv(M, 256) * cdiv(N, 256);
-  if (N % 256 == 0 && tiles256 >= 128 && tiles256 <= 256) return tiles224 <= 256 ? 30 : 15;
+  if (N % 256 == 0 && tiles256 >= 128 && tiles256 <= 256)
+    return cdiv(M, 192) * (N / 256) <= 256 ? 31 : (tiles224 <= 256 ? 30 : 15);
   // 144-row tiles (one round of 128..256 workgroups) when 256 x 256 tiles do not fit one round.
   const int64_t tm144 = cdiv(M, 144);
   if (N % 512 == 0 && tm144 * (N / 512) >= 128 && tm144 * (N / 512) <= 256) return 22;
   // 128-deep K tiles (half the barriers and load batches of the 64-deep ones; the two K groups still
   // take alternate 32-deep steps, so the result is the same bit for bit) when K allows.
   if (tm144 * (N / 128) >= 128 && tm144 * (N / 128) <= 256) return K % 128 == 0 ? 29 : 23;
+  // A short-K product of a quarter to a half round of 144 x 128 tiles still runs best on them (ViT-L
+  // keep 10 % proj, 1712 x 1024 x 1024, 96 tiles: 15.0 us; ViT-B proj, 2088 x 768 x 768, 90 tiles:
+  // 12.7 us; 128 x 128 tiles: 17.2 and 13.3 us).
+  if (K <= 1024 && tm144 * (N / 128) >= 64 && tm144 * (N / 128) < 128) return K % 128 == 0 ? 29 : 23;
   // A round and a half of 288 x 192 tiles still beats 128 x 128 tiles.
   if (N % 192 == 0 && tiles288n > 256 && tiles288n <= 400) return 28;
   return 11;

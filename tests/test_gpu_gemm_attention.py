@@ -52,7 +52,8 @@ def _check_gemm(dev, got, x, w, b, what):
                                     (103, 1152, 384), (1, 64, 64), (130, 192, 128), (1656, 8192, 4096),
                                     (1712, 3072, 1024), (1712, 4096, 1024), (8272, 3072, 1024), (8272, 4096, 1024),
                                     (1656, 12288, 4096), (1656, 4096, 4096), (1656, 4096, 8192),
-                                    (414, 12288, 4096), (414, 4096, 4096), (414, 8192, 4096), (414, 4096, 8192)])
+                                    (414, 12288, 4096), (414, 4096, 4096), (414, 8192, 4096), (414, 4096, 8192),
+                                    (1712, 1024, 1024), (2088, 768, 768), (8272, 1024, 1024), (8272, 1024, 4096)])
 def test_linear_bias(dev, M, N, Kd):
     x, w, b = _rand((M, Kd), 1), _rand((N, Kd), 2, 0.02), _rand((N,), 3, 0.1)
     got = K.linear(x.to(dev), w.to(dev), b.to(dev))
