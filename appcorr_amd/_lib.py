@@ -98,6 +98,9 @@ SIGNATURES: dict[str, list] = {
                                   _i64, _i64, _p, _f32, _p],
     "oudjat_sparse_query_attention": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32, _p,
                                       _i64, _p],
+    "oudjat_sparse_query_attention_ws": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32,
+                                         _p, _i64, _p, _i64, _p],
+    "oudjat_sparse_query_attention_workspace_elems": [_i64, _i64, _i64, _i64, _i64],
     "oudjat_nvfp4_quantize": [_p, _i64, _i64, _i64, _p, _p, _p, _p],
     "oudjat_nvfp4_dequantize": [_p, _p, _p, _i64, _i64, _p, _i64, _p],
     "oudjat_query_attention_prob": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _f32, _p, _p, _i64,
@@ -112,7 +115,8 @@ SIGNATURES: dict[str, list] = {
                                             _i64, _i32, _p],
 }
 _RESTYPES = {"oudjat_status_string": ctypes.c_char_p, "oudjat_last_error": ctypes.c_char_p,
-             "oudjat_linear_workspace_elems": ctypes.c_int64}
+             "oudjat_linear_workspace_elems": ctypes.c_int64,
+             "oudjat_sparse_query_attention_workspace_elems": ctypes.c_int64}
 
 _lock = threading.Lock()
 _lib = None

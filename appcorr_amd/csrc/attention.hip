@@ -352,11 +352,17 @@ __device__ __forceinline__ int kv_slot(int row, int chunk) { return row * 128 + 
 // parts, so that a workgroup of few query waves still puts two or three waves on every SIMD.
 // full_split is a template parameter so that without it the full waves' stage mask is a constant and
 // each tile's S^T MFMAs and the previous tile's softmax stay in one basic block (interleaved).
-template <int NST, int FSPLIT>
+// Key-part workspace of a split launch, per (image, head, part): the running max of each query
+// (kv_part_rows(T) floats, T rounded up to 4 so the rows below stay 16-byte aligned), its sum (as
+// many), then its unnormalised 64-dim output rows (T x 64).
+__host__ __device__ __forceinline__ int64_t kv_part_rows(int64_t T) { return (T + 3) & ~(int64_t)3; }
+__host__ __device__ __forceinline__ int64_t kv_part_stride(int64_t T) { return 2 * kv_part_rows(T) + 64 * T; }
+
+template <int NST, int FSPLIT, bool KVS>
 __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     const uint16_t* __restrict__ q, int64_t qrs, int T, const uint16_t* __restrict__ kv, int64_t kvb, int64_t kvn,
     int64_t kvkv, int64_t kvh, int N, float scale_log2, uint16_t* __restrict__ out, int64_t ors,
-    int waves_per_wg, int light_split) {
+    int waves_per_wg, int light_split, float* __restrict__ part_ws, int kv_parts) {
   constexpr int full_split = FSPLIT;
   static_assert(FSPLIT == 1 || FSPLIT == 2, "full_split");
   constexpr int DH = 64, QK_STEPS = 4, OB = 2;
@@ -368,6 +374,8 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
   extern __shared__ __align__(16) unsigned char smem[];
 
   const int b = blockIdx.z, h = blockIdx.y;
+  // KVS: one query workgroup per (image, head) and blockIdx.x = key part (contiguous tile ranges).
+  const int qblk = KVS ? 0 : (int)blockIdx.x;
   const int lane = threadIdx.x & 63;
   const int wave = __builtin_amdgcn_readfirstlane(threadIdx.x >> 6);
   const int l32 = lane & 31, g = lane >> 5;
@@ -378,7 +386,7 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
   const int lpart = (light_split && wave >= nfq * full_split) ? wave - nfq * full_split : -1;
   const int fpart = lpart >= 0 ? 0 : wave % full_split;
   const int qwave = lpart >= 0 ? waves_per_wg - 1 : wave / full_split;
-  const int q0 = (blockIdx.x * waves_per_wg + qwave) * 32;
+  const int q0 = (qblk * waves_per_wg + qwave) * 32;
   const bool active = q0 < T;
   const bool merged = light_split || full_split > 1;  // the parts meet in LDS after the key loop
 
@@ -388,9 +396,16 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
   const i32x4_t rsrc_v = make_buffer_rsrc(kbase + kvkv, bytes);
   const bool loader = wave < 8;
   const int lrow = 8 * wave + (lane >> 3);                  // tile row this lane loads
-  const uint32_t off0 = (uint32_t)lrow * (uint32_t)kvn * 2u + (uint32_t)(((lane & 7) ^ kv_swz(lrow)) << 4);
   const uint32_t tstep = (uint32_t)kKeyTile * (uint32_t)kvn * 2u;
-  const int ntiles = (N + kKeyTile - 1) / kKeyTile;
+  // Key tiles of this workgroup: [tb, tb + ntiles); tiles are numbered from tb in the loops below.
+  int tb = 0, ntiles = (N + kKeyTile - 1) / kKeyTile;
+  if constexpr (KVS) {
+    const int per = (ntiles + kv_parts - 1) / kv_parts;
+    tb = (int)blockIdx.x * per;
+    ntiles = min(per, ntiles - tb);
+  }
+  const uint32_t off0 = (uint32_t)lrow * (uint32_t)kvn * 2u + (uint32_t)(((lane & 7) ^ kv_swz(lrow)) << 4) +
+                        (uint32_t)tb * tstep;
   auto issue = [&](int stage, int t) __attribute__((always_inline)) {
     if (loader) {
       unsigned char* base = smem + stage * STAGE + wave * 1024;
@@ -517,12 +532,12 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     // Online softmax of tile t and O^T += V^T . P^T with V from stage `st`.
     auto finish = [&](Scores& sc, const unsigned char* st, int t, auto mask_c) __attribute__((always_inline)) {
       f32x16_t (&s)[2] = sc.s;
-      if (decltype(mask_c)::value && (t + 1) * kKeyTile > N) {
+      if (decltype(mask_c)::value && (tb + t + 1) * kKeyTile > N) {
 #pragma unroll
         for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
           for (int v = 0; v < 16; ++v)
-            if (t * kKeyTile + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3) >= N) s[kb][v] = -INFINITY;
+            if ((tb + t) * kKeyTile + kb * 32 + 8 * (v >> 2) + 4 * g + (v & 3) >= N) s[kb][v] = -INFINITY;
       }
       float mq[4];  // four short chains, combined as a tree
 #pragma unroll
@@ -600,6 +615,7 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
         const float a0 = __builtin_amdgcn_exp2f((m_i - m) * scale_log2);
         const float a1 = __builtin_amdgcn_exp2f((m1 - m) * scale_log2);
         l_i = fmaf(l1, a1, l_i * a0);
+        m_i = m;  // l_i and o are now relative to m (read by a key-part write)
 #pragma unroll
         for (int d = 0; d < OB; ++d)
 #pragma unroll
@@ -607,7 +623,21 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
       }
     }
     const int qr = q0 + l32;
-    if (active && qr < T && fpart == 0) {
+    if (KVS && active && qr < T && fpart == 0) {
+      // This key part's unnormalised output, running max and sum (sq_attention_merge_kernel).
+      float* ws = part_ws + ((int64_t)(b * (int)gridDim.y + h) * kv_parts + (int)blockIdx.x) * kv_part_stride(T);
+      if (g == 0) {
+        ws[qr] = m_i;
+        ws[kv_part_rows(T) + qr] = l_i;
+      }
+      float* orow = ws + 2 * (int64_t)kv_part_rows(T) + (int64_t)qr * DH;
+#pragma unroll
+      for (int d = 0; d < OB; ++d)
+#pragma unroll
+        for (int r4 = 0; r4 < 4; ++r4)
+          *reinterpret_cast<f32x4_t*>(orow + d * 32 + 8 * r4 + 4 * g) =
+              f32x4_t{o[d][4 * r4], o[d][4 * r4 + 1], o[d][4 * r4 + 2], o[d][4 * r4 + 3]};
+    } else if (active && qr < T && fpart == 0) {
       const float inv = 1.0f / l_i;
       uint16_t* orow = out + ((int64_t)b * T + qr) * ors + (int64_t)h * DH;
 #pragma unroll
@@ -677,12 +707,12 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     };
     auto finish = [&](Scores16& sc, const unsigned char* st, int t, auto mask_c) __attribute__((always_inline)) {
       f32x4_t (&s)[4] = sc.s;
-      if (decltype(mask_c)::value && (t + 1) * kKeyTile > N) {
+      if (decltype(mask_c)::value && (tb + t + 1) * kKeyTile > N) {
 #pragma unroll
         for (int kb = 0; kb < 4; ++kb)
 #pragma unroll
           for (int v = 0; v < 4; ++v)
-            if (t * kKeyTile + 16 * kb + 4 * G + v >= N) s[kb][v] = -INFINITY;
+            if ((tb + t) * kKeyTile + 16 * kb + 4 * G + v >= N) s[kb][v] = -INFINITY;
       }
       float mq[4];
 #pragma unroll
@@ -772,6 +802,7 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
         l_i = lp[0] * a[0];
 #pragma unroll
         for (int p = 1; p < kLightParts; ++p) l_i = fmaf(lp[p], a[p], l_i);
+        m_i = m;  // l_i and o are now relative to m (read by a key-part write)
 #pragma unroll
         for (int d = 0; d < 4; ++d)
 #pragma unroll
@@ -786,7 +817,16 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
 
     // O^T[16 db + 4 G + v][query l16]: 4 consecutive dims per lane and block.
     const int qr = q0 + l16;
-    if (active && qr < T && lpart <= 0) {
+    if (KVS && active && qr < T && lpart <= 0) {
+      float* ws = part_ws + ((int64_t)(b * (int)gridDim.y + h) * kv_parts + (int)blockIdx.x) * kv_part_stride(T);
+      if (G == 0) {
+        ws[qr] = m_i;
+        ws[kv_part_rows(T) + qr] = l_i;
+      }
+      float* orow = ws + 2 * (int64_t)kv_part_rows(T) + (int64_t)qr * DH;
+#pragma unroll
+      for (int d = 0; d < 4; ++d) *reinterpret_cast<f32x4_t*>(orow + 16 * d + 4 * G) = o[d];
+    } else if (active && qr < T && lpart <= 0) {
       const float inv = 1.0f / l_i;
       uint16_t* orow = out + ((int64_t)b * T + qr) * ors + (int64_t)h * DH;
 #pragma unroll
@@ -802,6 +842,68 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
 }
 
 static constexpr int kAttnStages = 4;
+static constexpr int kNumCus = 256;     // MI355X
+static constexpr int kMaxKvParts = 8;
+static constexpr int kMinTilesSaved = 8;
+
+// Merge of the key parts of a split launch. Per (row, head) part p left its running (reference) max
+// m_p, its sum l_p and its unnormalised output o_p, both relative to m_p; with m = max_p m_p and
+// a_p = 2^((m_p - m) * scale_log2): l = sum_p a_p l_p, out = bf16((sum_p a_p o_p) * (1 / l)), summed
+// in part order. Every part holds at least one key, so every m_p is finite. Thread = (row, head, 8 dims).
+template <int P>
+__global__ __launch_bounds__(256) void sq_attention_merge_kernel(const float* __restrict__ ws, int B, int T, int H,
+                                                                 float scale_log2, uint16_t* __restrict__ out,
+                                                                 int64_t ors) {
+  const int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x;
+  if (i >= (int64_t)B * T * H * 8) return;
+  const int c = (int)(i & 7);
+  const int64_t rh = i >> 3;
+  const int h = (int)(rh % H);
+  const int64_t row = rh / H;  // b * T + query
+  const int b = (int)(row / T), qr = (int)(row - (int64_t)b * T);
+  const int64_t pstride = kv_part_stride(T);
+  const int64_t tp = kv_part_rows(T);
+  const float* base = ws + (int64_t)(b * H + h) * P * pstride;
+  // Every load first (one round of memory latency), then the arithmetic.
+  float mp[P], lp[P];
+  f32x4_t x0[P], x1[P];
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const float* pb = base + p * pstride;
+    mp[p] = pb[qr];
+    lp[p] = pb[tp + qr];
+    const f32x4_t* src = reinterpret_cast<const f32x4_t*>(pb + 2 * tp + (int64_t)qr * 64 + 8 * c);
+    x0[p] = src[0];
+    x1[p] = src[1];
+  }
+  float m = mp[0];
+#pragma unroll
+  for (int p = 1; p < P; ++p) m = fmaxf(m, mp[p]);
+  float l = 0.0f, o[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) o[e] = 0.0f;
+#pragma unroll
+  for (int p = 0; p < P; ++p) {
+    const float a = __builtin_amdgcn_exp2f((mp[p] - m) * scale_log2);
+    l = fmaf(lp[p], a, l);
+#pragma unroll
+    for (int e = 0; e < 4; ++e) {
+      o[e] = fmaf(x0[p][e], a, o[e]);
+      o[4 + e] = fmaf(x1[p][e], a, o[4 + e]);
+    }
+  }
+  const float inv = 1.0f / l;
+  typedef __bf16 bf16x4_t __attribute__((ext_vector_type(4)));
+  bf16x4_t w0, w1;
+#pragma unroll
+  for (int e = 0; e < 4; ++e) {
+    w0[e] = (__bf16)(o[e] * inv);
+    w1[e] = (__bf16)(o[4 + e] * inv);
+  }
+  uint16_t* orow = out + row * ors + (int64_t)h * 64 + 8 * c;
+  *reinterpret_cast<bf16x4_t*>(orow) = w0;
+  *reinterpret_cast<bf16x4_t*>(orow + 4) = w1;
+}
 
 // Two waves per full query wave (the buffer-load kernel's full_split) when a single workgroup per
 // (image, head) would otherwise have fewer than 8 waves, as long as the split still has the 8 loader
@@ -816,10 +918,61 @@ static int full_split_for(int64_t n_wg, int64_t nfq, int light_parts) {
 
 using namespace oudjat;
 
-extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int64_t B, int64_t T, int64_t H,
-                                             int64_t Dh, const uint16_t* kv, int64_t kvb, int64_t kvn, int64_t kvkv,
-                                             int64_t kvh, int64_t N, float scale, uint16_t* out, int64_t ors,
-                                             oudjat_stream_t stream) {
+// Launch shape of a sparse_query_attention call: query workgroups per (image, head), waves per
+// workgroup, and for the buffer-load kernel its light split, full split and key parts.
+struct AttnShape {
+  int64_t n_wg;
+  int w;
+  bool dma;
+  int split, nfq, fsplit, kv_parts;
+};
+
+static AttnShape attn_shape(int64_t B, int64_t T, int64_t H, int64_t Dh, int64_t N, bool offsets_fit) {
+  AttnShape s{};
+  const int64_t waves = cdiv(T, 32);
+  s.n_wg = cdiv(waves, Dh == 64 ? kMaxWaves64 : kMaxWaves128);
+  s.w = (int)cdiv(waves, s.n_wg);
+  if (s.w < kMinWaves) s.w = kMinWaves;
+  // Buffer-load kernel for Dh = 64 with >= 8 waves, counting the waves of split full and light
+  // query waves (its byte offsets must fit 31 bits); the register-staged kernel otherwise.
+  const int w = s.w;
+  const bool small_split = s.n_wg == 1 && w < 8 && full_split_for(s.n_wg, (T - (w - 1) * 32 <= 16) ? w - 1 : w,
+                                                                 (T - (w - 1) * 32 <= 16) ? kLightParts : 0) > 1;
+  s.dma = Dh == 64 && (w >= 8 || small_split) && offsets_fit;
+  s.kv_parts = 1;
+  if (!s.dma) return s;
+  // One workgroup per (image, head) whose last query wave is light (1..16 queries): that wave is
+  // split over kLightParts waves (its merge area, 3 parts of 18 x 64 floats, fits the stages).
+  const int64_t last = T - (w - 1) * 32;
+  s.split = (s.n_wg == 1 && last >= 1 && last <= 16 && w - 1 + kLightParts <= kDmaMaxWaves) ? kLightParts : 0;
+  s.nfq = s.split ? w - 1 : w;
+  s.fsplit = full_split_for(s.n_wg, s.nfq, s.split);
+  // Key parts: with one workgroup per (image, head) and fewer than half as many (image, head) pairs
+  // as CUs, the key tiles are dealt to up to kMaxKvParts workgroups per pair in contiguous ranges
+  // (as many as one round of workgroups on the CUs holds), and a merge launch combines them.
+  const int64_t pairs = B * H;
+  const int64_t ntiles = cdiv(N, kKeyTile);
+  if (s.n_wg == 1 && 2 * pairs <= kNumCus) {
+    int64_t parts = std::min<int64_t>(std::min<int64_t>(kNumCus / pairs, ntiles), kMaxKvParts);
+    const int64_t per = cdiv(ntiles, parts);
+    parts = cdiv(ntiles, per);
+    // Worth it only when each workgroup is spared at least kMinTilesSaved key tiles (~1 us each),
+    // against the merge launch (~3-5 us).
+    if (parts >= 2 && ntiles - per >= kMinTilesSaved) s.kv_parts = (int)parts;
+  }
+  return s;
+}
+
+// fp32 elements of the key-part workspace: per (image, head, part) the running max and sum of each
+// query and its unnormalised output row.
+static int64_t attn_workspace_elems(int64_t B, int64_t T, int64_t H, int kv_parts) {
+  return kv_parts > 1 ? B * H * kv_parts * kv_part_stride(T) : 0;
+}
+
+static int sparse_query_attention_impl(const uint16_t* q, int64_t qrs, int64_t B, int64_t T, int64_t H, int64_t Dh,
+                                       const uint16_t* kv, int64_t kvb, int64_t kvn, int64_t kvkv, int64_t kvh,
+                                       int64_t N, float scale, uint16_t* out, int64_t ors, float* workspace,
+                                       int64_t workspace_elems, oudjat_stream_t stream) {
   OUDJAT_REQUIRE(B >= 0 && T >= 0 && H >= 0 && N >= 0, OUDJAT_ERR_INVALID_ARGUMENT,
                  "sparse_query_attention: negative size");
   if (B == 0 || T == 0 || H == 0) return OUDJAT_OK;
@@ -834,38 +987,57 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
   OUDJAT_REQUIRE(N < ((int64_t)1 << 30) && T < ((int64_t)1 << 30), OUDJAT_ERR_TOO_LARGE,
                  "sparse_query_attention: N or T too large");
   const float scale_log2 = scale * 1.4426950408889634f;
-  const int64_t waves = cdiv(T, 32);
-  const int64_t n_wg = cdiv(waves, Dh == 64 ? kMaxWaves64 : kMaxWaves128);
-  int w = (int)cdiv(waves, n_wg);
-  if (w < kMinWaves) w = kMinWaves;
-  dim3 grid((unsigned)n_wg, (unsigned)H, (unsigned)B);
+  const AttnShape s = attn_shape(B, T, H, Dh, N, N * kvn * 2 < ((int64_t)1 << 31));
+  const int w = s.w;
+  dim3 grid((unsigned)s.n_wg, (unsigned)H, (unsigned)B);
   hipStream_t st = as_stream(stream);
-  // Buffer-load kernel for Dh = 64 with >= 8 waves, counting the waves of split full and light
-  // query waves (its byte offsets must fit 31 bits); the register-staged kernel otherwise.
-  const bool small_split = n_wg == 1 && w < 8 && full_split_for(n_wg, (T - (w - 1) * 32 <= 16) ? w - 1 : w,
-                                                               (T - (w - 1) * 32 <= 16) ? kLightParts : 0) > 1;
-  const bool dma = Dh == 64 && (w >= 8 || small_split) && N * kvn * 2 < ((int64_t)1 << 31);
-  if (dma) {
+  if (s.dma) {
     const size_t lds_dma = (size_t)kAttnStages * 2 * kKeyTile * 128;
     static_assert((size_t)kAttnStages * 2 * kKeyTile * 128 <= 64 * 1024, "needs no larger-LDS attribute");
-    // One workgroup per (image, head) whose last query wave is light (1..16 queries): that wave is
-    // split over kLightParts waves (its merge area, 3 parts of 18 x 64 floats, fits the stages).
-    const int64_t last = T - (w - 1) * 32;
-    const int split = (n_wg == 1 && last >= 1 && last <= 16 && w - 1 + kLightParts <= kDmaMaxWaves) ? kLightParts : 0;
     static_assert((kLightParts - 1) * 18 * 64 * 4 <= kAttnStages * 2 * kKeyTile * 128, "merge area");
-    const int nfq = split ? w - 1 : w;
-    const int fsplit = full_split_for(n_wg, nfq, split);
     static_assert(((kLightParts - 1) * 18 + 4 * 34) * 64 * 4 <= kAttnStages * 2 * kKeyTile * 128,
                   "merge area of the light parts and of four split full waves");
-    const int threads = (nfq * fsplit + (split ? kLightParts : 0)) * 64;
-    if (fsplit > 1)
-      sq_attention_dma_kernel<kAttnStages, 2><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv,
-                                                                               kvh, (int)N, scale_log2, out, ors, w,
-                                                                               split);
+    const int threads = (s.nfq * s.fsplit + (s.split ? kLightParts : 0)) * 64;
+    const int split = s.split;
+    const bool kvs = s.kv_parts > 1 && workspace && aligned(workspace, 16) &&
+                     attn_workspace_elems(B, T, H, s.kv_parts) <= workspace_elems;
+    if (kvs) {
+      dim3 pgrid((unsigned)s.kv_parts, (unsigned)H, (unsigned)B);
+      if (s.fsplit > 1)
+        sq_attention_dma_kernel<kAttnStages, 2, true><<<pgrid, threads, lds_dma, st>>>(
+            q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N, scale_log2, out, ors, w, split, workspace, s.kv_parts);
+      else
+        sq_attention_dma_kernel<kAttnStages, 1, true><<<pgrid, threads, lds_dma, st>>>(
+            q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N, scale_log2, out, ors, w, split, workspace, s.kv_parts);
+      const int rc = check_launch("sparse_query_attention");
+      if (rc != OUDJAT_OK) return rc;
+      const unsigned mgrid = (unsigned)cdiv(B * T * H * 8, 256);
+      switch (s.kv_parts) {
+#define OUDJAT_MERGE(PV)                                                                                     \
+  case PV:                                                                                                    \
+    sq_attention_merge_kernel<PV><<<mgrid, 256, 0, st>>>(workspace, (int)B, (int)T, (int)H, scale_log2, out, ors); \
+    break;
+        OUDJAT_MERGE(2)
+        OUDJAT_MERGE(3)
+        OUDJAT_MERGE(4)
+        OUDJAT_MERGE(5)
+        OUDJAT_MERGE(6)
+        OUDJAT_MERGE(7)
+        OUDJAT_MERGE(8)
+#undef OUDJAT_MERGE
+        default:
+          return set_error(OUDJAT_ERR_INVALID_ARGUMENT, "sparse_query_attention: %d key parts", s.kv_parts);
+      }
+      return check_launch("sparse_query_attention (merge)");
+    }
+    if (s.fsplit > 1)
+      sq_attention_dma_kernel<kAttnStages, 2, false><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv,
+                                                                                      kvh, (int)N, scale_log2, out, ors,
+                                                                                      w, split, nullptr, 1);
     else
-      sq_attention_dma_kernel<kAttnStages, 1><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv,
-                                                                               kvh, (int)N, scale_log2, out, ors, w,
-                                                                               split);
+      sq_attention_dma_kernel<kAttnStages, 1, false><<<grid, threads, lds_dma, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv,
+                                                                                      kvh, (int)N, scale_log2, out, ors,
+                                                                                      w, split, nullptr, 1);
     return check_launch("sparse_query_attention");
   }
   const void* fn = Dh == 128 ? (const void*)sq_attention_kernel<128, kMinWaves, false>
@@ -895,4 +1067,31 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
     sq_attention_kernel<64, kMinWaves, false><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,
                                                                          (int)N, scale_log2, out, ors, w);
   return check_launch("sparse_query_attention");
+}
+
+extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int64_t B, int64_t T, int64_t H,
+                                             int64_t Dh, const uint16_t* kv, int64_t kvb, int64_t kvn, int64_t kvkv,
+                                             int64_t kvh, int64_t N, float scale, uint16_t* out, int64_t ors,
+                                             oudjat_stream_t stream) {
+  return sparse_query_attention_impl(q, qrs, B, T, H, Dh, kv, kvb, kvn, kvkv, kvh, N, scale, out, ors, nullptr, 0,
+                                     stream);
+}
+
+extern "C" int oudjat_sparse_query_attention_ws(const uint16_t* q, int64_t qrs, int64_t B, int64_t T, int64_t H,
+                                                int64_t Dh, const uint16_t* kv, int64_t kvb, int64_t kvn,
+                                                int64_t kvkv, int64_t kvh, int64_t N, float scale, uint16_t* out,
+                                                int64_t ors, float* workspace, int64_t workspace_elems,
+                                                oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(workspace_elems >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "sparse_query_attention: negative workspace size");
+  return sparse_query_attention_impl(q, qrs, B, T, H, Dh, kv, kvb, kvn, kvkv, kvh, N, scale, out, ors, workspace,
+                                     workspace_elems, stream);
+}
+
+extern "C" int64_t oudjat_sparse_query_attention_workspace_elems(int64_t B, int64_t T, int64_t H, int64_t Dh,
+                                                                 int64_t N) {
+  if (B <= 0 || T <= 0 || H <= 0 || N <= 0 || Dh != 64 || B > 65535 || H > 65535 || N >= ((int64_t)1 << 30) ||
+      T >= ((int64_t)1 << 30))
+    return 0;
+  const AttnShape s = attn_shape(B, T, H, Dh, N, true);
+  return s.dma ? attn_workspace_elems(B, T, H, s.kv_parts) : 0;
 }

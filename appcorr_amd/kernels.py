@@ -609,25 +609,29 @@ def linear_kernel_name(M: int, N: int, K: int, epilogue: int = _lib.EPI_BIAS) ->
 
 
 _WS_ELEMS: dict = {}
-_GEMM_WS: dict = {}
+_STREAM_WS: dict = {}
+
+
+def _stream_workspace(x: torch.Tensor, elems: int) -> torch.Tensor:
+    """fp32 scratch of one launch sequence (split-K GEMM partials, attention key parts): a buffer per
+    (device, stream), grown to the largest need and reused by every launch on that stream (launches
+    on one stream run in order, and none keeps data in it past its own launches)."""
+    skey = (x.device, _lib.stream_of(x))
+    buf = _STREAM_WS.get(skey)
+    if buf is None or buf.numel() < elems:
+        buf = torch.empty(elems, device=x.device, dtype=torch.float32)
+        _STREAM_WS[skey] = buf
+    return buf
 
 
 def _gemm_workspace(x: torch.Tensor, M: int, N: int, K: int, epilogue: int) -> torch.Tensor | None:
-    """The split-K scratch of one GEMM: a buffer per (device, stream), grown to the largest need and
-    reused by every GEMM launched on that stream (launches on one stream run in order)."""
-    key = (M, N, K, epilogue)
+    """The split-K scratch of one GEMM (None: this shape never splits)."""
+    key = ("gemm", M, N, K, epilogue)
     elems = _WS_ELEMS.get(key)
     if elems is None:
         elems = int(_lib.load().oudjat_linear_workspace_elems(M, N, K, epilogue))
         _WS_ELEMS[key] = elems
-    if elems <= 0:
-        return None
-    skey = (x.device, _lib.stream_of(x))
-    buf = _GEMM_WS.get(skey)
-    if buf is None or buf.numel() < elems:
-        buf = torch.empty(elems, device=x.device, dtype=torch.float32)
-        _GEMM_WS[skey] = buf
-    return buf
+    return _stream_workspace(x, elems) if elems > 0 else None
 
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
@@ -672,6 +676,18 @@ def sparse_query_attention(q: torch.Tensor, kv_cache: torch.Tensor, T: int, scal
              and q.stride(1) == Dh, "attention: q must be [B*T, H, Dh] with packed heads")
     if out is None:
         out = torch.empty((B * T, H * Dh), device=q.device, dtype=torch.bfloat16)
+    key = ("attention", B, T, H, Dh, N)
+    elems = _WS_ELEMS.get(key)
+    if elems is None:
+        elems = int(_lib.load().oudjat_sparse_query_attention_workspace_elems(B, T, H, Dh, N))
+        _WS_ELEMS[key] = elems
+    if elems > 0:
+        # Few (image, head) pairs: the keys are split over several workgroups per pair and merged.
+        ws = _stream_workspace(q, elems)
+        _launch("attention", q, "oudjat_sparse_query_attention_ws", _ptr(q), q.stride(0), B, T, H, Dh, _ptr(kv_cache),
+                kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(2), kv_cache.stride(3), N, float(scale),
+                _ptr(out), out.stride(0), _ptr(ws), ws.numel(), _stream(q))
+        return out
     _launch("attention", q, "oudjat_sparse_query_attention", _ptr(q), q.stride(0), B, T, H, Dh, _ptr(kv_cache), kv_cache.stride(0),
          kv_cache.stride(1), kv_cache.stride(2), kv_cache.stride(3), N, float(scale), _ptr(out), out.stride(0),
          _stream(q))

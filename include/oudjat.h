@@ -318,6 +318,26 @@ int oudjat_sparse_query_attention(const uint16_t* q, int64_t q_row_stride, int64
                                   int64_t N, float scale, uint16_t* out, int64_t out_row_stride,
                                   oudjat_stream_t stream);
 
+/* Row 10 with a workspace (the same SDPA call site, attention.py:456-532): the same result as
+ * oudjat_sparse_query_attention, except that when few (image, head) pairs would leave most CUs idle
+ * (Dh = 64, B*H at most half the CU count) the keys are split into contiguous ranges over several
+ * workgroups per pair, whose fp32 partial outputs, running maxima and sums go to `workspace` and
+ * are merged by a second launch (deterministic, in range order; within the unsplit kernel's error
+ * bound, since each range rounds its probabilities to bf16 relative to its own running max, results
+ * may differ from the unsplit ones by a bf16 ulp or two). It splits only if workspace is 16-byte aligned and
+ * holds oudjat_sparse_query_attention_workspace_elems(B, T, H, Dh, N) fp32 elements; otherwise, or
+ * when that size is 0, it runs exactly as oudjat_sparse_query_attention. */
+int oudjat_sparse_query_attention_ws(const uint16_t* q, int64_t q_row_stride, int64_t B, int64_t T,
+                                     int64_t H, int64_t Dh, const uint16_t* kv, int64_t kv_stride_b,
+                                     int64_t kv_stride_n, int64_t kv_stride_kv, int64_t kv_stride_h,
+                                     int64_t N, float scale, uint16_t* out, int64_t out_row_stride,
+                                     float* workspace, int64_t workspace_elems, oudjat_stream_t stream);
+
+/* fp32 elements of workspace oudjat_sparse_query_attention_ws uses for this shape (0: it never
+ * splits the keys of this shape). */
+int64_t oudjat_sparse_query_attention_workspace_elems(int64_t B, int64_t T, int64_t H, int64_t Dh,
+                                                      int64_t N);
+
 /* Approximate-pass server score with one query per (image, head) -- cls_attn_prob and, with the
  * pseudo query of oudjat_pseudo_query, patch_pseudo_attn_prob (the cache producer,
  * appcorr/models/dinov3/layers/attention.py:254-273):

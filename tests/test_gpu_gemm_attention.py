@@ -316,6 +316,51 @@ def test_attention_buffer_load_kernel_shapes(dev, B, T, N, H, scale_up):
     assert_bits_equal(again, got, "repeat launch")
 
 
+def _attention_call(entry, q, kv, B, T, H, N, out, *ws):
+    lib = _lib.load()
+    st = torch.cuda.current_stream().cuda_stream
+    rc = getattr(lib, entry)(q.data_ptr(), q.stride(0), B, T, H, 64, kv.data_ptr(), kv.stride(0), kv.stride(1),
+                             kv.stride(2), kv.stride(3), N, 64 ** -0.5, out.data_ptr(), out.stride(0), *ws, st)
+    assert rc == 0, _lib.load().oudjat_last_error()
+
+
+@pytest.mark.parametrize("B,T,N,H,scale_up", [(8, 261, 1029, 12, 1.0), (1, 103, 1029, 6, 1.0), (2, 300, 777, 4, 8.0),
+                                               (1, 272, 577, 2, 1.0), (3, 107, 1029, 16, 1.0), (1, 5, 1029, 1, 1.0),
+                                               (2, 32, 1100, 4, 1.0)])
+def test_attention_key_split(dev, B, T, N, H, scale_up):
+    """Few (image, head) pairs with many key tiles (ViT-B at B = 8: 96 pairs of 17 tiles): the keys are
+    dealt in contiguous tile ranges to several workgroups per pair, whose fp32 partials a second
+    launch merges (with the light-wave split, the 16-query light wave, the two-wave split of few
+    query waves, a ragged last tile of one key, and large logits inside the parts).
+    Both the split and the unsplit kernel against the float64 reference with the same bound (each
+    part rounds its probabilities to bf16 relative to its own running max, so the two differ by about
+    a P rounding, which the bound covers); deterministic; and with a workspace one element short the
+    entry runs the unsplit kernel bit for bit. Few key tiles (ViT-S: 197 keys) are not split."""
+    D = 64
+    lib = _lib.load()
+    assert int(lib.oudjat_sparse_query_attention_workspace_elems(1, 103, 6, D, 197)) == 0
+    elems = int(lib.oudjat_sparse_query_attention_workspace_elems(B, T, H, D, N))
+    assert elems > 0, "this shape is expected to split its keys"
+    q = (_rand((B * T, H, D), 44).float() * scale_up).to(torch.bfloat16).to(dev)
+    kv = (_rand((B, N, 2, H, D), 45).float() * scale_up).to(torch.bfloat16).to(dev)
+    got = K.sparse_query_attention(q, kv, T, D ** -0.5)
+    qb = q.cpu().reshape(B, T, H, D).transpose(1, 2)
+    kvc = kv.cpu()
+    o64 = F64.sdpa(qb, kvc[:, :, 0].transpose(1, 2), kvc[:, :, 1].transpose(1, 2), D ** -0.5)
+    o64 = o64.transpose(1, 2).reshape(B * T, H * D)
+    _check_attention(got.cpu(), qb, kvc, D ** -0.5, o64, f"split attention {B},{T},{N},{H} x{scale_up}")
+    plain = torch.empty_like(got)
+    _attention_call("oudjat_sparse_query_attention", q, kv, B, T, H, N, plain)
+    _check_attention(plain.cpu(), qb, kvc, D ** -0.5, o64, f"unsplit attention {B},{T},{N},{H} x{scale_up}")
+    again = torch.empty_like(got)
+    ws = torch.empty(elems, device=dev, dtype=torch.float32)
+    _attention_call("oudjat_sparse_query_attention_ws", q, kv, B, T, H, N, again, ws.data_ptr(), elems)
+    assert_bits_equal(again.cpu(), got.cpu(), "repeat launch")
+    short = torch.empty_like(got)
+    _attention_call("oudjat_sparse_query_attention_ws", q, kv, B, T, H, N, short, ws.data_ptr(), elems - 1)
+    assert_bits_equal(short.cpu(), plain.cpu(), "workspace too small: unsplit kernel")
+
+
 @pytest.mark.parametrize("B,T,N,H,scale_up", [(4, 414, 4101, 32, 1.0), (1, 7, 64, 2, 1.0), (2, 257, 65, 3, 1.0),
                                                (1, 300, 300, 4, 8.0), (2, 512, 1029, 2, 1.0), (1, 33, 129, 1, 1.0)])
 def test_attention_dh128_shapes(dev, B, T, N, H, scale_up):
