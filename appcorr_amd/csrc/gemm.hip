@@ -1588,6 +1588,8 @@ static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_R16_CFG(144, 128, 1, 4, 2, 128, 2, false),  // 29: N = C GEMMs with K % 128 == 0
     OUDJAT_GEMM_PP_CFG(224, 256),  // 30: ping-pong 224 x 256 (a full round where 288 rows leave CUs idle)
     OUDJAT_GEMM_PP_CFG(192, 256),  // 31: ping-pong 192 x 256 (two rounds or a little less)
+    OUDJAT_GEMM_DMA_CFG(128, 32, 4, 1),  // 32: tiny grids (128 x 32, four waves of 32 x 32)
+    OUDJAT_GEMM_DMA_CFG(128, 64, 2, 2),  // 33: tiny fused-QKV grids (whole 64-wide heads)
 };
 static constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -1629,10 +1631,19 @@ static int ensure_gelu_table() {
 // Rows of output tiles each XCD sweeps before moving to the next tile column (L2 reuse of the W panel).
 constexpr int kGroupM = 8;
 
+// A grid of at most 32 tiles of 128 x 128 (ViT-S at B = 1: 103 selected rows) leaves most CUs idle
+// and each workgroup streams its whole K alone: 128 x 32 tiles give four times the workgroups at 5/8
+// of the operand bytes each. Measured in the ViT-S pass (kernel trace, 128 x 128 -> 128 x 32): proj
+// 384 x 384 10.5 -> 7.4 us, fc1 1536 x 384 10.0 -> 7.1 us. Long-K tiny products still split K when
+// given a workspace (choose_splitk: ViT-S fc2, K = 1536, 13.4 us in 12 slices against 15.0 us for
+// unsplit 128 x 32 tiles, whose weights then stream from HBM).
+static bool tiny_grid(int64_t M, int64_t N) { return N % 32 == 0 && cdiv(M, 128) * cdiv(N, 128) <= 32; }
+
 // aligned_io: C, resid 16-byte aligned with ldc, ldr % 8 == 0 and bias 8-byte aligned, which the
 // vector epilogues need; otherwise the register-staged kernel with 2-byte stores runs.
 static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   if (!aligned_io) return 8;
+  if (tiny_grid(M, N)) return 32;
   // 256 x 256 pipelined tiles when their grid fills between half and all of the CUs in one round;
   // 128 x 128 direct-to-LDS tiles otherwise (two workgroups per CU balance a ragged second round
   // better); the register-staged kernel for N % 128 != 0.
@@ -1737,6 +1748,7 @@ static int choose_splitk(int64_t M, int64_t N, int64_t K, int epi, int* S_out) {
 // Fused QKV: tiles must cover whole heads (Dh | BN; a tile may span the q / k / v boundaries).
 // 288 x 192 (ping-pong) tiles when the plain choice would leave more CUs idle in its single round.
 static int choose_qkv_cfg(int64_t M, int64_t N, int64_t K, int64_t Dh) {
+  if (tiny_grid(M, N) && 64 % Dh == 0 && N % 64 == 0) return 33;  // ViT-S at B = 1: 10.5 -> 8.2 us
   int ci = choose_cfg(M, N, K, true);
   const int64_t tiles288n = cdiv(M, 288) * (N / 192);
   if (N % 192 == 0 && tiles288n >= 192 && tiles288n <= 256 &&

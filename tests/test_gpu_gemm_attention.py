@@ -123,12 +123,12 @@ def test_linear_silu_mul(dev, M, N, Kd):
 
 
 # Split K: shapes whose tiles leave most CUs idle -- 144 x 128 tiles in two slices (ViT-L keep 10 %
-# fc2, M = 1712; ViT-B fc2), 288 x 256 ping-pong tiles in two slices (ViT-7B w3, K = 8192) and the
-# ViT-S B = 1 fc2 (103 rows, 12 slices). The
+# fc2, M = 1712; ViT-B fc2), 288 x 256 ping-pong tiles in two slices (ViT-7B w3, K = 8192) and a
+# ViT-S-width product of 103 rows with a long K (16 slices). The
 # partial tiles and the in-order fp32 sum of the slices stay within the accumulation bound; the
 # epilogues read the same sums, so each equals the oracle's epilogue applied to the split GEMM's own
 # bf16(acc + bias) (exactly, or to 1 ulp for GELU and SiLU).
-SPLIT_SHAPES = [(1712, 1024, 4096), (2088, 768, 3072), (1656, 4096, 8192), (103, 384, 1536)]
+SPLIT_SHAPES = [(1712, 1024, 4096), (2088, 768, 3072), (1656, 4096, 8192), (103, 384, 4096)]
 
 
 @pytest.mark.parametrize("M,N,Kd", SPLIT_SHAPES)
@@ -148,6 +148,28 @@ def test_linear_split_k(dev, M, N, Kd):
     assert_bf16_close(got, F64.gelu(base), max_ulps=1, max_frac_off=1e-3, what="split-K + gelu")
     got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_SILU_MUL, resid=r.to(dev))
     assert_bf16_close(got, F64.silu_mul(base, r), max_ulps=1, max_frac_off=1e-3, what="split-K + swiglu")
+
+
+@pytest.mark.parametrize("M,N,Kd", [(103, 384, 384), (103, 1536, 384), (103, 384, 768), (1, 64, 64), (300, 192, 192)])
+def test_linear_tiny_grid(dev, M, N, Kd):
+    """Grids of at most 32 tiles of 128 x 128 with K < 1024 (the ViT-S B = 1 proj and fc1; one row;
+    three tile rows) run on 128 x 32 tiles: within the accumulation bound of the oracle, and every
+    epilogue equals the oracle's epilogue applied to the same bf16(acc + bias). (With K >= 1024 and
+    a workspace they split K instead: test_linear_split_k.)"""
+    lib = _lib.load()
+    for epi in (_lib.EPI_BIAS, _lib.EPI_BIAS_LS, _lib.EPI_BIAS_LS_RESID, _lib.EPI_BIAS_GELU, _lib.EPI_BIAS_SILU_MUL):
+        assert lib.oudjat_linear_workspace_elems(M, N, Kd, epi) == 0
+        assert "gemm_bf16_dma_kernel<128, 32, 4, 1" in K.linear_kernel_name(M, N, Kd, epi)
+    xd, wd, bd, base = _epi_case(dev, M, N, Kd, 60)
+    g, r = _rand((N,), 64), _rand((M, N), 65)
+    got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_LS, gamma=g.to(dev))
+    assert_bits_equal(got, F64.mul(base, g), "tiny + ls")
+    got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_LS_RESID, gamma=g.to(dev), resid=r.to(dev))
+    assert_bits_equal(got, F64.fma_add(r, base, g), "tiny + ls + resid")
+    got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_GELU)
+    assert_bf16_close(got, F64.gelu(base), max_ulps=1, max_frac_off=1e-3, what="tiny + gelu")
+    got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_SILU_MUL, resid=r.to(dev))
+    assert_bf16_close(got, F64.silu_mul(base, r), max_ulps=1, max_frac_off=1e-3, what="tiny + swiglu")
 
 
 def test_linear_without_workspace_does_not_split(dev):
