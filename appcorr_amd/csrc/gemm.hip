@@ -1692,10 +1692,12 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   // 128-deep K tiles (half the barriers and load batches of the 64-deep ones; the two K groups still
   // take alternate 32-deep steps, so the result is the same bit for bit) when K allows.
   if (tm144 * (N / 128) >= 128 && tm144 * (N / 128) <= 256) return K % 128 == 0 ? 29 : 23;
-  // A short-K product of a quarter to a half round of 144 x 128 tiles still runs best on them (ViT-L
-  // keep 10 % proj, 1712 x 1024 x 1024, 96 tiles: 15.0 us; ViT-B proj, 2088 x 768 x 768, 90 tiles:
-  // 12.7 us; 128 x 128 tiles: 17.2 and 13.3 us).
-  if (K <= 1024 && tm144 * (N / 128) >= 64 && tm144 * (N / 128) < 128) return K % 128 == 0 ? 29 : 23;
+  // A short-K product of a quarter to a half round of 144 x 128 tiles runs best on 128 x 32 tiles,
+  // four to five workgroups per CU (ViT-L keep 10 % proj, 1712 x 1024 x 1024: 16.1 -> 15.1 us; ViT-B
+  // proj, 2088 x 768 x 768: 13.5 -> 12.5 us; weights from HBM, HIP graph). 128 x 128 tiles: 20.3 and
+  // 16.6 us; at a full round and more (the headline proj, 4176 rows) 128 x 32 tiles lose (27.6 against
+  // 17.6 us).
+  if (K <= 1024 && tm144 * (N / 128) >= 64 && tm144 * (N / 128) < 128) return 32;
   // A round and a half of 288 x 192 tiles still beats 128 x 128 tiles.
   if (N % 192 == 0 && tiles288n > 256 && tiles288n <= 400) return 28;
   return 11;
