@@ -112,12 +112,27 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
 
   extern __shared__ __align__(16) unsigned char smem[];
 
-  const int b = blockIdx.z, h = blockIdx.y;
+  // The query workgroups of one (image, head) all stream the same K/V: numbered so that they run on
+  // one XCD (dispatch places workgroup i on XCD i % 8) and share its L2. Workgroup i = x + 8 s on
+  // XCD x takes query block s % nq of pair 8 (s / nq) + x; a bijection when the pair count is a
+  // multiple of 8, else the launch order is kept.
+  int qblk = blockIdx.x, h = blockIdx.y, b = blockIdx.z;
+  {
+    const int nq = gridDim.x, pairs = gridDim.y * gridDim.z;
+    if (nq > 1 && pairs % 8 == 0) {
+      const int lin = blockIdx.x + nq * (blockIdx.y + gridDim.y * blockIdx.z);
+      const int x = lin & 7, sl = lin >> 3;
+      const int pair = 8 * (sl / nq) + x;
+      qblk = sl % nq;
+      h = pair % gridDim.y;
+      b = pair / gridDim.y;
+    }
+  }
   const int nthreads = blockDim.x;
   const int tid = threadIdx.x;
   const int lane = tid & 63, wave = tid >> 6;
   const int l32 = lane & 31, g = lane >> 5;
-  const int q0 = (blockIdx.x * waves_per_wg + wave) * 32;
+  const int q0 = (qblk * waves_per_wg + wave) * 32;
   const bool active = q0 < T;
 
   // Q^T fragments (B operand of S^T): lane -> query q0 + l32, head dims ks*16 + 8g .. +7.
