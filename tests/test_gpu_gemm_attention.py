@@ -114,6 +114,17 @@ def test_linear_layerscale(dev):
     assert_bits_equal(got, F64.mul(base, g), "fc2+ls")
 
 
+def test_linear_layerscale_residual_7b_proj(dev):
+    """The ViT-7B proj (1656 x 4096 x 4096, 16-row-block 128 x 256 tiles): LayerScale + residual on the
+    same accumulators as the plain GEMM, bit-exact."""
+    assert "gemm_bf16_r16_kernel<128, 256, 2, 4, 1, 64, 3" in K.linear_kernel_name(1656, 4096, 4096,
+                                                                                 _lib.EPI_BIAS_LS_RESID)
+    xd, wd, bd, base = _epi_case(dev, 1656, 4096, 4096, 70)
+    g, r = _rand((4096,), 73), _rand((1656, 4096), 74)
+    got = K.linear(xd, wd, bd, epilogue=_lib.EPI_BIAS_LS_RESID, gamma=g.to(dev), resid=r.to(dev))
+    assert_bits_equal(got, F64.fma_add(r, base, g), "7B proj + ls + resid")
+
+
 @pytest.mark.parametrize("M,N,Kd", [(600, 1024, 512), (414, 8192, 4096), (1656, 8192, 4096)])
 def test_linear_silu_mul(dev, M, N, Kd):
     xd, wd, bd, base = _epi_case(dev, M, N, Kd, 18)
