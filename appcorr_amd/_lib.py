@@ -90,6 +90,9 @@ SIGNATURES: dict[str, list] = {
     "oudjat_linear_bf16": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i32, _p, _p, _i64, _p, _i64, _f32, _p, _i64,
                            _p],
     "oudjat_linear_workspace_elems": [_i64, _i64, _i64, _i32],
+    "oudjat_linear_splitk_partial": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p, _p],
+    "oudjat_splitk_ls_packed_residual": [_p, _i64, _p, _p, _f32, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p,
+                                         _p, _f32, _p, _p],
     "oudjat_linear_kernel_name": [_i64, _i64, _i64, _i32, ctypes.c_char_p, _i64],
     "oudjat_packed_residual_persist": [_p, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p],
     "oudjat_packed_residual_persist_ln": [_p, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _f32, _p, _p],

@@ -1883,6 +1883,31 @@ extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64
                      "linear_bf16");
 }
 
+// The partial GEMM of a split-K product alone (see oudjat.h): the consumer reduces the slices.
+extern "C" int oudjat_linear_splitk_partial(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                                            int64_t N, int64_t ldw, float* workspace, int64_t workspace_elems,
+                                            int64_t* slices, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(M > 0 && N > 0 && K > 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_splitk_partial: bad size");
+  OUDJAT_REQUIRE(A && W && workspace && slices, OUDJAT_ERR_INVALID_ARGUMENT, "linear_splitk_partial: null pointer");
+  OUDJAT_REQUIRE(K % kBK == 0 && N % 64 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE,
+                 "linear_splitk_partial: K %% %d == 0 and N %% 64 == 0 required", kBK);
+  OUDJAT_REQUIRE(lda % 8 == 0 && ldw % 8 == 0 && lda >= K && ldw >= K && aligned(A, 16) && aligned(W, 16) &&
+                     aligned(workspace, 16),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "linear_splitk_partial: operands must be 16-byte aligned, ld %% 8 == 0");
+  OUDJAT_REQUIRE(M < ((int64_t)1 << 31) && N < ((int64_t)1 << 31) && K < ((int64_t)1 << 31), OUDJAT_ERR_TOO_LARGE,
+                 "linear_splitk_partial: dimensions must fit in int32");
+  int S = 1;
+  const int ci = choose_splitk(M, N, K, OUDJAT_EPI_BIAS_LS, &S);
+  OUDJAT_REQUIRE(ci >= 0 && S > 1 && (int64_t)S * M * N <= workspace_elems, OUDJAT_ERR_UNSUPPORTED_SHAPE,
+                 "linear_splitk_partial: %lld x %lld x %lld does not split K (or the workspace is short)",
+                 (long long)M, (long long)N, (long long)K);
+  *slices = S;
+  EpiArgs ea{};
+  ea.acc_scale = 1.0f;
+  return launch_gemm(ci, A, M, K, lda, W, N, ldw, kEpiPartial, ea, reinterpret_cast<uint16_t*>(workspace), N,
+                     as_stream(stream), "linear_splitk_partial", S);
+}
+
 // fp32 elements of workspace a linear_bf16 call of this shape can use for split K (0: it never splits).
 extern "C" int64_t oudjat_linear_workspace_elems(int64_t M, int64_t N, int64_t K, int epi) {
   int S = 1;

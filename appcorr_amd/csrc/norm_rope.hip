@@ -117,6 +117,67 @@ __global__ __launch_bounds__(kNormThreads) void packed_residual_ln_kernel(
   layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, ln_out + row * C);
 }
 
+// The split-K reduce of a LayerScale projection (fc2 / w3) fused with the packed residual step and
+// the next block's LayerNorm: mlp = bf16(bf16(sum_s P[s] * acc_scale + b) * gamma), the slices summed
+// in order from slice 0 (splitk_reduce_kernel's arithmetic), then exactly packed_residual_ln_kernel
+// (x_new, the blocks_out_sum row, and LayerNorm(x_new) when w is given). One wave per row.
+template <int CH>
+__global__ __launch_bounds__(kNormThreads) void splitk_ls_residual_ln_kernel(
+    const float* __restrict__ P, int S, const uint16_t* __restrict__ fb, const uint16_t* __restrict__ fg,
+    float acc_scale, const uint16_t* __restrict__ xa, const uint16_t* __restrict__ xt, int64_t rows, int C,
+    const int64_t* __restrict__ bi, const int64_t* __restrict__ ti, uint16_t* __restrict__ bos, int64_t bsb,
+    int64_t bsn, uint16_t* __restrict__ xn, const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
+    float eps, uint16_t* __restrict__ ln_out) {
+  const int64_t row = (int64_t)blockIdx.x * kNormRowsPerWg + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int chunks = C >> 3;
+  const int64_t slice = rows * (int64_t)C;
+  const uint4* av = reinterpret_cast<const uint4*>(xa + row * C);
+  const uint4* tv = reinterpret_cast<const uint4*>(xt + row * C);
+  uint4* ov = reinterpret_cast<uint4*>(xn + row * C);
+  uint4* bv = reinterpret_cast<uint4*>(bos + bi[row] * bsb + ti[row] * bsn);
+  float v[CH][8];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) {
+      const float* p = P + row * C + 8 * c;
+      float4 a0 = *reinterpret_cast<const float4*>(p), a1 = *reinterpret_cast<const float4*>(p + 4);
+      for (int sl = 1; sl < S; ++sl) {
+        const float4 b0 = *reinterpret_cast<const float4*>(p + sl * slice);
+        const float4 b1 = *reinterpret_cast<const float4*>(p + sl * slice + 4);
+        a0.x += b0.x; a0.y += b0.y; a0.z += b0.z; a0.w += b0.w;
+        a1.x += b1.x; a1.y += b1.y; a1.z += b1.z; a1.w += b1.w;
+      }
+      const float acc[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
+      float fbias[8], g[8], xm[8], fa[8], ft[8], fm[8], fo[8], fbo[8];
+      if (fb) {
+        unpack8(reinterpret_cast<const uint4*>(fb)[c], fbias);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) fbias[e] = 0.0f;
+      }
+      unpack8(reinterpret_cast<const uint4*>(fg)[c], g);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) xm[e] = round_bf16(__builtin_fmaf(acc[e], acc_scale, fbias[e])) * g[e];
+      unpack8(pack8(xm), fm);  // the bf16 mlp row, as the unfused step reads it back
+      unpack8(av[c], fa);
+      unpack8(tv[c], ft);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        fo[e] = ft[e] + fm[e];
+        fbo[e] = round_bf16(ft[e] - fa[e]) + fm[e];
+      }
+      const uint4 o = pack8(fo);
+      ov[c] = o;
+      bv[c] = pack8(fbo);
+      unpack8(o, v[j]);
+    }
+  }
+  if (w) layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, ln_out + row * C);
+}
+
 // Thread = (row, head, chunk of 8 in the left half). Rows with patch_mask == 0 are left untouched.
 __global__ __launch_bounds__(256) void rope_active_inplace_kernel(
     uint16_t* q, int64_t qst, int64_t qsh, uint16_t* k, int64_t kst, int64_t ksh, const float* __restrict__ sin_t,
@@ -295,4 +356,39 @@ extern "C" int oudjat_packed_residual_persist_ln(const uint16_t* x_act, const ui
   else OUDJAT_PRLN(16);
 #undef OUDJAT_PRLN
   return check_launch("packed_residual_persist_ln");
+}
+
+extern "C" int oudjat_splitk_ls_packed_residual(const float* partials, int64_t slices, const uint16_t* fc_bias,
+                                                const uint16_t* ls_gamma, float acc_scale, const uint16_t* x_act,
+                                                const uint16_t* x_attn, int64_t rows, int64_t C,
+                                                const int64_t* batch_idx, const int64_t* token_idx, uint16_t* bos,
+                                                int64_t bos_stride_b, int64_t bos_stride_n, uint16_t* x_new,
+                                                const uint16_t* ln_w, const uint16_t* ln_b, float eps,
+                                                uint16_t* ln_out, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(rows >= 0 && C > 0 && slices >= 1, OUDJAT_ERR_INVALID_ARGUMENT, "splitk_ls_packed_residual: bad size");
+  if (rows == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(partials && ls_gamma && x_act && x_attn && batch_idx && token_idx && bos && x_new &&
+                     (ln_w == nullptr) == (ln_b == nullptr) && (ln_w == nullptr) == (ln_out == nullptr),
+                 OUDJAT_ERR_INVALID_ARGUMENT, "splitk_ls_packed_residual: null pointer (LayerNorm w, b, out together)");
+  OUDJAT_REQUIRE(C % 8 == 0 && aligned(partials, 16) && aligned(ls_gamma, 16) && (!fc_bias || aligned(fc_bias, 16)) &&
+                     aligned(x_act, 16) && aligned(x_attn, 16) && aligned(bos, 16) && aligned(x_new, 16) &&
+                     (!ln_w || (aligned(ln_w, 16) && aligned(ln_b, 16) && aligned(ln_out, 16))) &&
+                     bos_stride_b % 8 == 0 && bos_stride_n % 8 == 0,
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "splitk_ls_packed_residual: 16-byte aligned rows, C %% 8 == 0");
+  OUDJAT_REQUIRE(C <= 8192 && slices < 65536, OUDJAT_ERR_TOO_LARGE, "splitk_ls_packed_residual: C=%lld > 8192",
+                 (long long)C);
+  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg);
+  hipStream_t st = as_stream(stream);
+#define OUDJAT_SKRL(CHV)                                                                                        \
+  splitk_ls_residual_ln_kernel<CHV><<<grid, kNormThreads, 0, st>>>(partials, (int)slices, fc_bias, ls_gamma,      \
+                                                                   acc_scale, x_act, x_attn, rows, (int)C,        \
+                                                                   batch_idx, token_idx, bos, bos_stride_b,       \
+                                                                   bos_stride_n, x_new, ln_w, ln_b, eps, ln_out)
+  if (C <= 512) OUDJAT_SKRL(1);
+  else if (C <= 1024) OUDJAT_SKRL(2);
+  else if (C <= 2048) OUDJAT_SKRL(4);
+  else if (C <= 4096) OUDJAT_SKRL(8);
+  else OUDJAT_SKRL(16);
+#undef OUDJAT_SKRL
+  return check_launch("splitk_ls_packed_residual");
 }

@@ -634,10 +634,14 @@ class SelfAttentionBlock(nn.Module):
             raise ValueError("{tag}_blocks_out_sum must be contiguous")
         return plan, key, kv, bos
 
-    def _correct_rows(self, x_act: Tensor, rope, kv: Tensor, qs: PackedQueryState, xn: Tensor | None = None):
+    def _correct_rows(self, x_act: Tensor, rope, kv: Tensor, qs: PackedQueryState, xn: Tensor | None = None,
+                      residual=None):
         """The block's arithmetic on the packed selected rows (block.py:1111-1141): returns
         (x_attn, mlp); the K/V cache rows of the selected tokens are rewritten in place. `xn`, when
-        given, is norm1(x_act) already computed (by the previous block's fused residual step)."""
+        given, is norm1(x_act) already computed (by the previous block's fused residual step).
+        `residual` = (blocks_out_sum, next block's norm1 or None): when the last MLP product splits K,
+        its reduce runs fused with the packed residual step, and the second value returned is then
+        (x_new, norm1(x_new) or None) instead of mlp (see _mlp_scaled_residual)."""
         with trace_range("correct_attn"):
             if xn is None:
                 xn = K.layer_norm(x_act, self.norm1.weight, self.norm1.bias, self.norm1.eps)   # block.py:1114
@@ -650,8 +654,55 @@ class SelfAttentionBlock(nn.Module):
                 x_attn = _linear_route(proj, attn, "proj", epilogue=_lib.EPI_BIAS_LS_RESID,  # attention.py:532 +
                                        gamma=g1, resid=x_act)                             # block.py:1129-1134
         with trace_range("correct_ffn"):
-            mlp = self._mlp_scaled(K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps))  # :1141
+            xn2 = K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps)  # :1141
+            if residual is not None:
+                fused = self._mlp_scaled_residual(xn2, x_act, x_attn, qs, *residual)
+                if fused is not None:
+                    return x_attn, fused
+            mlp = self._mlp_scaled(xn2)
         return x_attn, mlp
+
+    def _mlp_scaled_residual(self, xn: Tensor, x_act: Tensor, x_attn: Tensor, qs: PackedQueryState, bos: Tensor,
+                             next_norm):
+        """_mlp_scaled followed by the packed residual step (block.py:1140-1186) and the next block's
+        norm1, with the last product's split-K reduce and the residual step in one kernel: (x_new,
+        norm1(x_new) or None), bit-identical to the unfused steps. None (nothing computed) unless the
+        MLP is bf16 throughout (GELU fc1 / fc2, or SwiGLU w1 / w2 / w3 as plain linears), its last
+        product splits K (small row counts: ViT-S / ViT-B, ViT-L keep 10 %) and the width is at most
+        1024: the fused step runs a wave per row, which at the ViT-7B width (4096, w3 in two slices)
+        was slower than the element-parallel reduce plus the residual step (pass 31.65 -> 31.77 ms),
+        while ViT-S / ViT-B / ViT-L keep 10 % gained 4.5 / 1.8 / 1.3 %."""
+        ln = None if next_norm is None else (next_norm.weight, next_norm.bias, next_norm.eps)
+        M = xn.shape[0]
+        if x_act.shape[1] > 1024:
+            return None
+        if isinstance(self.mlp, Mlp):
+            fc1, last = self.mlp.fc1, self.mlp.fc2
+        elif all(type(m) is nn.Linear for m in (self.mlp.w1, self.mlp.w2, self.mlp.w3)):
+            fc1, last = None, self.mlp.w3
+        else:
+            return None
+        if not K.linear_splits_k(M, last.out_features, last.in_features):
+            return None
+        g2 = self._gamma(self.ls2, xn)
+        if fc1 is not None:
+            h = K.linear(xn, fc1.weight, fc1.bias, epilogue=_lib.EPI_BIAS_GELU, site="fc1")
+            site = "fc2"
+        else:
+            x2 = K.linear(xn, self.mlp.w2.weight, self.mlp.w2.bias, site="w2")
+            h = K.linear(xn, self.mlp.w1.weight, self.mlp.w1.bias, epilogue=_lib.EPI_BIAS_SILU_MUL, resid=x2,
+                         site="w1")
+            site = "w3"
+        out = K.linear_ls_packed_residual(h, last.weight, last.bias, g2, x_act, x_attn, qs.active_batch_idx,
+                                          qs.active_token_idx, bos, ln, site=site)
+        if out is None:  # an operand the fused step cannot take: the unfused last product and step
+            mlp = K.linear(h, last.weight, last.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g2, site=site)
+            if ln is None:
+                return K.packed_residual_persist(x_act, x_attn, mlp, qs.active_batch_idx, qs.active_token_idx,
+                                                 bos), None
+            return K.packed_residual_persist_ln(x_act, x_attn, mlp, qs.active_batch_idx, qs.active_token_idx, bos,
+                                                *ln)
+        return out
 
     @annotate("correct_partial_token")
     def correct_partial_token(self, x: Tensor, dindice: Tensor, rope, cache_feature: Dict, tag: str, **kwargs):
@@ -716,8 +767,11 @@ def correct_blocks_packed(blocks, x: Tensor, dindice: Tensor, rope, cache_featur
         if plan is not plan0:
             raise RuntimeError("blocks of one packed run resolved different query plans")
         if x_p.shape[0] > 0:
-            x_attn, mlp = blk._correct_rows(x_p, rope, kv, qs, xn=xn)
-            if i + 1 < len(blocks):
+            nxt = blocks[i + 1].norm1 if i + 1 < len(blocks) else None
+            x_attn, mlp = blk._correct_rows(x_p, rope, kv, qs, xn=xn, residual=(bos, nxt))
+            if isinstance(mlp, tuple):  # the residual step ran fused with the last MLP product
+                x_p, xn = mlp
+            elif i + 1 < len(blocks):
                 n1 = blocks[i + 1].norm1
                 x_p, xn = K.packed_residual_persist_ln(x_p, x_attn, mlp, qs.active_batch_idx, qs.active_token_idx,
                                                        bos, n1.weight, n1.bias, n1.eps)

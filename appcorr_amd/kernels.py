@@ -247,6 +247,53 @@ def packed_residual_persist_ln(x_act: torch.Tensor, x_attn: torch.Tensor, mlp: t
     return x_new, ln_out
 
 
+def linear_splits_k(M: int, N: int, K: int) -> bool:
+    """Whether an M x N x K LayerScale product (fc2, w3) splits K given a workspace."""
+    key = ("gemm", M, N, K, _lib.EPI_BIAS_LS)
+    elems = _WS_ELEMS.get(key)
+    if elems is None:
+        elems = int(_lib.load().oudjat_linear_workspace_elems(M, N, K, _lib.EPI_BIAS_LS))
+        _WS_ELEMS[key] = elems
+    return elems > 0
+
+
+def linear_ls_packed_residual(h: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, gamma: torch.Tensor,
+                              x_act: torch.Tensor, x_attn: torch.Tensor, batch_idx: torch.Tensor,
+                              token_idx: torch.Tensor, blocks_out_sum: torch.Tensor, ln=None, site: str = "fc2"):
+    """mlp = bf16(bf16(h . W^T + bias) * gamma) split K, its reduce fused with packed_residual_persist_ln
+    (or packed_residual_persist when `ln` is None): returns (x_new, LN(x_new) or None), bit-identical to
+    linear(..., EPI_BIAS_LS) followed by that residual step. `ln` = (weight, bias, eps) of the next block's
+    norm1. Returns None when the product does not split K or an operand is not 16-byte aligned (the
+    caller then runs the two steps)."""
+    M, Kd = h.shape
+    N = weight.shape[0]
+    if not linear_splits_k(M, N, Kd):
+        return None
+    tensors = [h, weight, gamma, x_act, x_attn] + ([bias] if bias is not None else [])
+    if ln is not None:
+        tensors += [ln[0], ln[1]]
+    if any(t.data_ptr() % 16 for t in tensors) or h.stride(1) != 1 or weight.stride(1) != 1:
+        return None
+    _require_cuda(h, weight, bias, gamma, x_act, x_attn, batch_idx, token_idx, blocks_out_sum)
+    _require(x_act.shape == x_attn.shape == (M, N) and x_act.is_contiguous() and x_attn.is_contiguous()
+             and x_act.dtype == x_attn.dtype == torch.bfloat16, "linear_ls_packed_residual: x_act / x_attn [M, N] bf16")
+    _require(blocks_out_sum.dim() == 3 and blocks_out_sum.shape[2] == N and blocks_out_sum.stride(2) == 1,
+             "linear_ls_packed_residual: blocks_out_sum must be [B, N, C] with contiguous rows")
+    elems = int(_lib.load().oudjat_linear_workspace_elems(M, N, Kd, _lib.EPI_BIAS_LS))
+    ws = _stream_workspace(h, elems)
+    slices = ctypes.c_int64(0)
+    _launch(site, h, "oudjat_linear_splitk_partial", _ptr(h), M, Kd, h.stride(0), _ptr(weight), N, weight.stride(0),
+            _ptr(ws), ws.numel(), ctypes.addressof(slices), _stream(h))
+    x_new = torch.empty_like(x_act)
+    ln_out = torch.empty_like(x_act) if ln is not None else None
+    lw, lb, eps = (ln[0].contiguous(), ln[1].contiguous(), float(ln[2])) if ln is not None else (None, None, 0.0)
+    _launch("packed_residual", x_act, "oudjat_splitk_ls_packed_residual", _ptr(ws), slices.value, _ptr(bias),
+            _ptr(gamma.contiguous()), 1.0, _ptr(x_act), _ptr(x_attn), M, N, _ptr(_index(batch_idx, "batch_idx")),
+            _ptr(_index(token_idx, "token_idx")), _ptr(blocks_out_sum), blocks_out_sum.stride(0),
+            blocks_out_sum.stride(1), _ptr(x_new), _ptr(lw), _ptr(lb), eps, _ptr(ln_out), _stream(x_act))
+    return x_new, ln_out
+
+
 POINTER_ARRAYS_KEY = "_oudjat_device_pointer_arrays"
 
 

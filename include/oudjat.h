@@ -290,6 +290,31 @@ int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64_t lda, con
  * epilogue; 0 when it would not split K. No counterpart in the reference (cuBLAS sizes its own). */
 int64_t oudjat_linear_workspace_elems(int64_t M, int64_t N, int64_t K, int epilogue);
 
+/* Rows 13 + 14-16 across a kernel boundary -- the fc2 (or SwiGLU w3) product of a correction block,
+ * split K, with its reduce left to the residual step (ffn_layers.py:24-115 into block.py:1140-1186):
+ * the partial GEMM of oudjat_linear_bf16 alone. Writes the S fp32 slices [S, M, N] of A . W^T to
+ * workspace and S to *slices (host memory); fails with OUDJAT_ERR_UNSUPPORTED_SHAPE when the product
+ * would not split K (oudjat_linear_workspace_elems(M, N, K, OUDJAT_EPI_BIAS_LS) == 0) or the workspace
+ * is shorter than that. Same operand rules as oudjat_linear_bf16; 16-byte aligned workspace. */
+int oudjat_linear_splitk_partial(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                                 int64_t N, int64_t ldw, float* workspace, int64_t workspace_elems,
+                                 int64_t* slices, oudjat_stream_t stream);
+
+/* The reduce of oudjat_linear_splitk_partial's slices with the LayerScale epilogue, fused with
+ * oudjat_packed_residual_persist_ln (block.py:1140-1186, then :1114 of the next block):
+ * mlp = bf16(bf16(sum_s partials[s] * acc_scale + fc_bias) * ls_gamma) (slices summed in order, as
+ * oudjat_linear_bf16's split-K reduce), then x_new, the blocks_out_sum rows and LayerNorm(x_new)
+ * exactly as oudjat_packed_residual_persist_ln computes them from that mlp. ln_w, ln_b and ln_out are
+ * all NULL for the last block of a run (no LayerNorm). partials [slices, rows, C] fp32; fc_bias may be
+ * NULL; 16-byte aligned rows, C % 8 == 0, C <= 8192. */
+int oudjat_splitk_ls_packed_residual(const float* partials, int64_t slices, const uint16_t* fc_bias,
+                                     const uint16_t* ls_gamma, float acc_scale, const uint16_t* x_act,
+                                     const uint16_t* x_attn, int64_t rows, int64_t C,
+                                     const int64_t* batch_idx, const int64_t* token_idx, uint16_t* bos,
+                                     int64_t bos_stride_b, int64_t bos_stride_n, uint16_t* x_new,
+                                     const uint16_t* ln_w, const uint16_t* ln_b, float eps, uint16_t* ln_out,
+                                     oudjat_stream_t stream);
+
 /* Rows 6-9 fused into the QKV GEMM -- SelfAttention.correct_partial_token up to the attention call
  * (appcorr/models/dinov3/layers/attention.py:415-454): qkv = A . W^T + bias for A [M, K] and
  * W [3*H*Dh, K] (never materialised), then RoPE on q and k of patch rows (rotate-half, fp32, tables

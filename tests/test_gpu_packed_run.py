@@ -183,3 +183,42 @@ def test_packed_residual_ln_equals_unfused(dev, B, N, C, M):
     assert_bits_equal(x_f, x_u.cpu(), "x_new")
     assert_bits_equal(bos_f, bos_u.cpu(), "blocks_out_sum")
     assert_bits_equal(ln_f, ln_u.cpu(), "LayerNorm(x_new)")
+
+
+@pytest.mark.parametrize("B,N,C,hid,M,with_ln", [(1, 201, 384, 1536, 103, True), (16, 1029, 1024, 4096, 1712, True),
+                                                 (3, 40, 384, 1536, 72, False), (4, 700, 4096, 8192, 1656, True)])
+def test_splitk_ls_residual_equals_unfused(dev, B, N, C, hid, M, with_ln):
+    """The last MLP product split K with its reduce fused into the residual step (ViT-S fc2 in 12
+    slices, ViT-L keep-10 % fc2 and ViT-7B w3 in 2, with and without the next block's LayerNorm)
+    equals linear(EPI_BIAS_LS) followed by packed_residual_persist(_ln), bit for bit."""
+    from appcorr_amd import _lib
+    assert K.linear_splits_k(M, C, hid)
+    rng = np.random.default_rng(C + M)
+    flat = np.sort(rng.choice(B * N, M, replace=False))
+    bi = torch.from_numpy(flat // N).to(dev)
+    ti = torch.from_numpy(flat % N).to(dev)
+    h = _rand_bf16((M, hid), 11).to(dev)
+    w = _rand_bf16((C, hid), 12, 0.02).to(dev)
+    fb = _rand_bf16((C,), 13, 0.1).to(dev)
+    g = _rand_bf16((C,), 14, 0.5).to(dev)
+    x_act = _rand_bf16((M, C), 15).to(dev)
+    x_attn = (x_act.float() + _rand_bf16((M, C), 16, 0.5).float().to(dev)).to(torch.bfloat16)
+    bos0 = _rand_bf16((B, N, C), 17, 0.1).to(dev)
+    lw = (1.0 + _rand_bf16((C,), 18, 0.2).float()).to(torch.bfloat16).to(dev)
+    lb = _rand_bf16((C,), 19, 0.1).to(dev)
+    ln = (lw, lb, 1e-6) if with_ln else None
+    bos_u, bos_f = bos0.clone(), bos0.clone()
+    mlp = K.linear(h, w, fb, epilogue=_lib.EPI_BIAS_LS, gamma=g)
+    if with_ln:
+        x_u, ln_u = K.packed_residual_persist_ln(x_act, x_attn, mlp, bi, ti, bos_u, lw, lb, 1e-6)
+    else:
+        x_u, ln_u = K.packed_residual_persist(x_act, x_attn, mlp, bi, ti, bos_u), None
+    out = K.linear_ls_packed_residual(h, w, fb, g, x_act, x_attn, bi, ti, bos_f, ln)
+    assert out is not None
+    x_f, ln_f = out
+    assert_bits_equal(x_f, x_u.cpu(), "x_new")
+    assert_bits_equal(bos_f, bos_u.cpu(), "blocks_out_sum")
+    if with_ln:
+        assert_bits_equal(ln_f, ln_u.cpu(), "LayerNorm(x_new)")
+    else:
+        assert ln_f is None
