@@ -359,7 +359,8 @@ def _attention_call(entry, q, kv, B, T, H, N, out, *ws):
 
 @pytest.mark.parametrize("B,T,N,H,scale_up", [(8, 261, 1029, 12, 1.0), (1, 103, 1029, 6, 1.0), (2, 300, 777, 4, 8.0),
                                                (1, 272, 577, 2, 1.0), (3, 107, 1029, 16, 1.0), (1, 5, 1029, 1, 1.0),
-                                               (2, 32, 1100, 4, 1.0)])
+                                               (2, 32, 1100, 4, 1.0), (2, 256, 1029, 4, 1.0), (1, 33, 700, 3, 1.0),
+                                               (2, 16, 900, 2, 1.0)])
 def test_attention_key_split(dev, B, T, N, H, scale_up):
     """Few (image, head) pairs with many key tiles (ViT-B at B = 8: 96 pairs of 17 tiles): the keys are
     dealt in contiguous tile ranges to several workgroups per pair, whose fp32 partials a second
