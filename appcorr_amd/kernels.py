@@ -657,15 +657,22 @@ def linear_kernel_name(M: int, N: int, K: int, epilogue: int = _lib.EPI_BIAS) ->
 
 _WS_ELEMS: dict = {}
 _STREAM_WS: dict = {}
+_RETIRED_WS: list = []
 
 
 def _stream_workspace(x: torch.Tensor, elems: int) -> torch.Tensor:
     """fp32 scratch of one launch sequence (split-K GEMM partials, attention key parts): a buffer per
     (device, stream), grown to the largest need and reused by every launch on that stream (launches
-    on one stream run in order, and none keeps data in it past its own launches)."""
+    on one stream run in order, and none keeps data in it past its own launches). A buffer that is
+    outgrown stays allocated for the life of the process: a HIP graph recorded earlier on that
+    stream holds its address, and freeing it would let the allocator hand the memory to a tensor
+    that the graph's replays would then overwrite."""
     skey = (x.device, _lib.stream_of(x))
     buf = _STREAM_WS.get(skey)
     if buf is None or buf.numel() < elems:
+        if buf is not None:  # grown geometrically, so few buffers are ever retired
+            _RETIRED_WS.append(buf)
+            elems = max(elems, 2 * buf.numel())
         buf = torch.empty(elems, device=x.device, dtype=torch.float32)
         _STREAM_WS[skey] = buf
     return buf

@@ -150,6 +150,24 @@ def test_device_pointer_array_lives_with_its_holder():
     assert K.device_pointer_array(ptrs, "cpu", None) is not a         # no holder: a fresh array each call
 
 
+def test_stream_workspace_keeps_outgrown_buffers(monkeypatch):
+    """The per-stream fp32 scratch is reused while it is large enough; when it grows, the old buffer
+    stays allocated (a graph recorded on that stream keeps its address) and the new one at least
+    doubles, so only a few buffers are ever retired."""
+    from appcorr_amd import _lib
+    monkeypatch.setattr(_lib, "stream_of", lambda t: 12345)
+    monkeypatch.setattr(K, "_STREAM_WS", {})
+    monkeypatch.setattr(K, "_RETIRED_WS", [])
+    x = torch.zeros(1)
+    a = K._stream_workspace(x, 100)
+    assert a.numel() == 100 and K._stream_workspace(x, 60) is a
+    b = K._stream_workspace(x, 150)
+    assert b is not a and b.numel() == 200 and K._RETIRED_WS == [a]
+    c = K._stream_workspace(x, 1000)
+    assert c.numel() == 1000 and K._RETIRED_WS[-1] is b
+    assert K._stream_workspace(x, 1000) is c and len(K._RETIRED_WS) == 2
+
+
 def test_trace_ranges_nest_and_survive_exceptions():
     """roctx ranges (the reference's NVTX annotations) are balanced even when the body raises."""
     from appcorr_amd import tracing
