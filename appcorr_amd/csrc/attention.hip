@@ -13,8 +13,9 @@
 //     of that MFMA is taken from the accumulator layout: lane group g supplies keys
 //     16j + 4g + {0..3} and 16j + 8 + 4g + {0..3} of k-step j, and V^T is read in that same order;
 //   * K (the A operand of the first product) is read from LDS in its natural row layout.
-// V is transposed once per tile while it is written to LDS (Vt[d][key], rows padded by 8 bytes so
-// the 8-byte fragment reads of 32 consecutive d rows are conflict-free).
+// V stays in its natural [key][dim] rows in LDS, like K; the V^T operand comes from them through
+// the LDS transpose read (ds_read_tr16_b64, its lane mapping described above the buffer-load
+// kernel).
 //
 // One workgroup per (image, head) covers up to 10 query waves = 320 queries (8 for Dh = 128); larger T
 // is split evenly over several workgroups. At the headline shape (T = 261: 8 full waves and a last
@@ -22,8 +23,6 @@
 // last wave's key tiles among 4 waves, so each workgroup runs 12. K/V tiles of 64 keys are double-buffered in LDS with the next tile's global loads in
 // flight during the current tile's MFMAs, so each (image, head) streams its K/V once.
 #include <stdlib.h>
-
-#include <atomic>
 
 #include <type_traits>
 
@@ -99,11 +98,10 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
     const uint16_t* __restrict__ q, int64_t qrs, int T, const uint16_t* __restrict__ kv, int64_t kvb, int64_t kvn,
     int64_t kvkv, int64_t kvh, int N, float scale_log2, uint16_t* __restrict__ out, int64_t ors,
     int waves_per_wg) {
-  constexpr int CPR = DH / 8;                 // 16-byte chunks per K row
-  constexpr int KROWB = DH * 2;               // bytes per K row in LDS
-  constexpr int VTROW = kKeyTile * 2 + 8;     // bytes per Vt row (64 keys + 8 bytes of padding)
+  constexpr int CPR = DH / 8;                 // 16-byte chunks per K / V row
+  constexpr int KROWB = DH * 2;               // bytes per K / V row in LDS
   constexpr int KSTAGE = kKeyTile * KROWB;
-  constexpr int VSTAGE = DH * VTROW;
+  constexpr int VSTAGE = kKeyTile * KROWB;
   constexpr int STAGE = KSTAGE + VSTAGE;
   constexpr int QK_STEPS = DH / 16;
   constexpr int OB = DH / 32;
@@ -111,6 +109,7 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
   constexpr int IT = (ITEMS + MINW * 64 - 1) / (MINW * 64);
 
   extern __shared__ __align__(16) unsigned char smem[];
+  typedef short i16x4_t __attribute__((ext_vector_type(4)));
 
   // The query workgroups of one (image, head) all stream the same K/V: numbered so that they run on
   // one XCD (dispatch places workgroup i on XCD i % 8) and share its L2. Workgroup i = x + 8 s on
@@ -173,9 +172,7 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
         const int kk = c / CPR, kc = c - kk * CPR;       // K: row-major, 8 lanes per 128-byte row
         const int nk = t * kKeyTile + kk;
         if (nk < N) r.k[i] = *reinterpret_cast<const u32x4_t*>(kbase + (int64_t)nk * kvn + kc * 8);
-        const int vk = c % kKeyTile, vc = c / kKeyTile;  // V: 64 consecutive keys per wave, one chunk
-        const int nv = t * kKeyTile + vk;
-        if (nv < N) r.v[i] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)nv * kvn + vc * 8);
+        if (nk < N) r.v[i] = *reinterpret_cast<const u32x4_t*>(vbase + (int64_t)nk * kvn + kc * 8);
       }
     }
   };
@@ -187,21 +184,32 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
       const int c = tid + i * nthreads;
       if (c < ITEMS) {
         const int kk = c / CPR, kc = c - kk * CPR;
-        *reinterpret_cast<u32x4_t*>(ks + kk * KROWB + ((kc ^ (kk & (CPR - 1))) << 4)) = r.k[i];
-        const int vk = c % kKeyTile, vc = c / kKeyTile;
-#pragma unroll
-        for (int e = 0; e < 4; ++e) {
-          const uint32_t w = r.v[i][e];
-          *reinterpret_cast<uint16_t*>(vs + (vc * 8 + 2 * e) * VTROW + vk * 2) = (uint16_t)(w & 0xffffu);
-          *reinterpret_cast<uint16_t*>(vs + (vc * 8 + 2 * e + 1) * VTROW + vk * 2) = (uint16_t)(w >> 16);
-        }
+        const int slot = kk * KROWB + ((kc ^ (kk & (CPR - 1))) << 4);
+        *reinterpret_cast<u32x4_t*>(ks + slot) = r.k[i];
+        *reinterpret_cast<u32x4_t*>(vs + slot) = r.v[i];
       }
     }
   };
 
+  // V^T fragment sources of d-block d: lane (g, 16-lane half hh, s = lane % 16) addresses dims
+  // 32 d + 16 hh + 4 (s % 4) .. + 3 of key 4 g + s / 4 (first run of k-step 0) and of that key + 8
+  // (second run); k-step j adds 16 j keys, whose swizzle is the same.
+  int voff[OB][2];
+  {
+    const int sl = lane & 15, hh = (lane >> 4) & 1;
+#pragma unroll
+    for (int d = 0; d < OB; ++d) {
+      const int dcol = 32 * d + 16 * hh + 4 * (sl & 3);
+#pragma unroll
+      for (int run = 0; run < 2; ++run) {
+        const int key = 4 * g + (sl >> 2) + 8 * run;
+        voff[d][run] = KSTAGE + key * KROWB + (((dcol >> 3) ^ (key & (CPR - 1))) << 4) + ((dcol >> 2) & 1) * 8;
+      }
+    }
+  }
+
   auto compute = [&](int stage, int t) __attribute__((always_inline)) {
     const unsigned char* ks = smem + stage * STAGE;
-    const unsigned char* vs = ks + KSTAGE;
     // S^T blocks: s[kb][v] = S^T[key kb*32 + 8(v/4) + 4g + v%4][query l32]
     // The K fragments of a 32-key block (both blocks for Dh = 64) are read before its MFMAs so the
     // reads overlap.
@@ -273,13 +281,15 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
     }
 #pragma unroll
     for (int d = 0; d < OB; ++d) {
-      const unsigned char* vrow = vs + (d * 32 + l32) * VTROW;
 #pragma unroll
       for (int j = 0; j < 4; ++j) {
-        const uint2 lo = *reinterpret_cast<const uint2*>(vrow + (16 * j + 4 * g) * 2);
-        const uint2 hi = *reinterpret_cast<const uint2*>(vrow + (16 * j + 8 + 4 * g) * 2);
-        const bf16x8_t vf = as_bf16x8(make_uint4(lo.x, lo.y, hi.x, hi.y));
-        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(vf, pf[j], o[d], 0, 0, 0);
+        const i16x4_t lo = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4_t*)(ks + voff[d][0] + j * 16 * KROWB));
+        const i16x4_t hi = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+            (__attribute__((address_space(3))) i16x4_t*)(ks + voff[d][1] + j * 16 * KROWB));
+        typedef short i16x8_t __attribute__((ext_vector_type(8)));
+        const i16x8_t both = {lo[0], lo[1], lo[2], lo[3], hi[0], hi[1], hi[2], hi[3]};
+        o[d] = __builtin_amdgcn_mfma_f32_32x32x16_bf16(__builtin_bit_cast(bf16x8_t, both), pf[j], o[d], 0, 0, 0);
       }
     }
   };
@@ -1055,23 +1065,9 @@ static int sparse_query_attention_impl(const uint16_t* q, int64_t qrs, int64_t B
                                                                                       w, split, nullptr, 1);
     return check_launch("sparse_query_attention");
   }
-  const void* fn = Dh == 128 ? (const void*)sq_attention_kernel<128, kMinWaves, false>
-                  : w >= 8  ? (const void*)sq_attention_kernel<64, 8, true>
-                            : (const void*)sq_attention_kernel<64, kMinWaves, false>;
-  const size_t lds = Dh == 64 ? 2 * (64 * 128 + 64 * 136) : 2 * (64 * 256 + 128 * 136);
-  if (lds > 64 * 1024) {
-    // Once per kernel instance and device.
-    static std::atomic<uint8_t> attr_set[64][3];
-    int dev = 0;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "sparse_query_attention: %s", hipGetErrorString(e));
-    const int which = Dh == 128 ? 0 : (w >= 8 ? 1 : 2);
-    if (!attr_set[dev & 63][which].load(std::memory_order_acquire)) {
-      e = hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)lds);
-      if (e != hipSuccess) return set_error(OUDJAT_ERR_HIP, "sparse_query_attention: %s", hipGetErrorString(e));
-      attr_set[dev & 63][which].store(1, std::memory_order_release);
-    }
-  }
+  // Two stages of one K and one V tile (64 keys x Dh bf16 each): 32 KB at Dh = 64, 64 KB at
+  // Dh = 128, within the default dynamic LDS limit.
+  const size_t lds = 2 * 2 * (size_t)kKeyTile * Dh * 2;
   if (Dh == 128)
     sq_attention_kernel<128, kMinWaves, false><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,
                                                                           (int)N, scale_log2, out, ors, w);
