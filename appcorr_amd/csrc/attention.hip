@@ -273,7 +273,7 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
     m_i = m_new;
     // Rescale the output only when some query's reference max moved (alpha != 1 somewhere in the
     // wave).
-    if (DH == 128 || __builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+    if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
 #pragma unroll
       for (int d = 0; d < OB; ++d)
 #pragma unroll
