@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be loaded before the HIP library, see module docstring
 
 LIB_PATH = Path(__file__).resolve().parent / "liboudjat_hip.so"
-ABI_VERSION = 11
+ABI_VERSION = 12
 
 OK = 0
 STATUS_NAMES = {
@@ -111,6 +111,11 @@ SIGNATURES: dict[str, list] = {
     "oudjat_pseudo_query": [_p, _i64, _i64, _i64, _i64, _i64, _i64, _i64, _p, _p],
     "oudjat_nvfp4_quantize_dequantize": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p],
     "oudjat_fp8_quantize_dequantize": [_p, _i64, _i64, _i64, _p, _i32, _p, _i64, _p],
+    "oudjat_fp8_quantize": [_p, _i64, _i64, _i64, _p, _i32, _p, _i64, _p],
+    "oudjat_linear_fp8": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i32, _p, _p, _i64, _p, _i64, _f32, _p],
+    "oudjat_linear_qkv_rope_kv_fp8": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p,
+                                      _p, _i64, _i64, _p, _f32, _p],
+    "oudjat_linear_fp8_kernel_name": [_i64, _i64, _i64, _i32, ctypes.c_char_p, _i64],
     "oudjat_scale_bias_rows": [_p, _i64, _i64, _i64, _f32, _p, _p, _p, _i64, _p],
     "oudjat_swiglu_scaled": [_p, _f32, _p, _p, _f32, _p, _i64, _i64, _p, _p],
     "oudjat_amax_update": [_p, _i64, _i64, _i64, _p, _p],

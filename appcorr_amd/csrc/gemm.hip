@@ -1251,11 +1251,16 @@ void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t 
 // 0 waits for all of its loads of tile u + 1 at the end of compute(2u + 1); group 1 for its W rows
 // at the end of mem(2u + 1) and for its A rows at the end of compute(2u + 1).
 // ------------------------------------------------------------------------------------------------
-template <int BM, int BN, int EPI>
+template <int BM, int BN, int EPI, bool F8 = false>
 __global__ __launch_bounds__(512) __attribute__((amdgpu_waves_per_eu(2, 2)))
-void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t lda, const uint16_t* __restrict__ W,
+void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A16, int M, int K, int64_t lda, const uint16_t* __restrict__ W16,
                          int N, int64_t ldw, EpiArgs ea, uint16_t* __restrict__ C, int64_t ldc, int group_m) {
+  // F8: the operands are OCP e4m3 codes (one byte per element, A16 / W16 point at bytes, lda / ldw and
+  // K count elements) on v_mfma_f32_16x16x128_f8f6f4; the LDS stages hold the same 128-byte rows, so
+  // a K tile is 128 elements deep instead of 64.
+  constexpr int EB = F8 ? 1 : 2;                   // bytes per operand element
   constexpr int BK = 64, NST = 2, WGM = 2, WGN = 4;
+  constexpr int BKE = 2 * BK / EB;                 // K elements per 128-byte LDS row
   using L = R16Layout<BK>;
   constexpr int WM = BM / WGM, WN = BN / WGN;
   constexpr int FMB = WM / 16, FNB = WN / 16;
@@ -1267,9 +1272,11 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
 
   extern __shared__ __align__(16) unsigned char smem[];
   constexpr int kLutOff = r16_lut_offset(BM, BN, WGM, WGN, 1, BK, NST);
+  const unsigned char* A = reinterpret_cast<const unsigned char*>(A16);
+  const unsigned char* W = reinterpret_cast<const unsigned char*>(W16);
   if constexpr (EPI == kEpiPartial) {  // K slice blockIdx.y of length K (lda, ldw stay the full strides)
-    A += (int64_t)blockIdx.y * K;
-    W += (int64_t)blockIdx.y * K;
+    A += (int64_t)blockIdx.y * K * EB;
+    W += (int64_t)blockIdx.y * K * EB;
   }
   // The GELU table (10 KB) is only needed by the epilogue: its loads are issued here, ahead of the
   // first K tiles (so they retire first and no wait holds the tiles back), and the registers are
@@ -1311,22 +1318,22 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
   // (its row plus its swizzled chunk); instruction j adds j * 4 * RPL rows. The range starts are
   // even, so a lane's chunk swizzle is the same for all of its instructions. Rows at or past M / N
   // fall outside the buffer descriptors and load as zeros.
-  const i32x4_t rsrc_a = make_buffer_rsrc(A, (uint32_t)((int64_t)M * lda * 2));
-  const i32x4_t rsrc_w = make_buffer_rsrc(W, (uint32_t)((int64_t)N * ldw * 2));
-  const uint32_t step_a = (uint32_t)(4 * RPL) * (uint32_t)lda * 2u;
-  const uint32_t step_w = (uint32_t)(4 * RPL) * (uint32_t)ldw * 2u;
+  const i32x4_t rsrc_a = make_buffer_rsrc(A, (uint32_t)((int64_t)M * lda * EB));
+  const i32x4_t rsrc_w = make_buffer_rsrc(W, (uint32_t)((int64_t)N * ldw * EB));
+  const uint32_t step_a = (uint32_t)(4 * RPL) * (uint32_t)lda * (uint32_t)EB;
+  const uint32_t step_w = (uint32_t)(4 * RPL) * (uint32_t)ldw * (uint32_t)EB;
   auto lane_offset = [&](int ib, bool w_rows) __attribute__((always_inline)) {
     const int lrow = lane / L::kChunks, lslot = lane % L::kChunks;
     const int row0 = (ib + lw) * RPL + lrow;
     const int chunk = lslot ^ ((row0 / L::kRowsPerLine) % L::kChunks);
-    return w_rows ? (uint32_t)((n0 + row0 - BM) * (uint32_t)ldw * 2u + chunk * 16)
-                  : (uint32_t)((m0 + row0) * (uint32_t)lda * 2u + chunk * 16);
+    return w_rows ? (uint32_t)((n0 + row0 - BM) * (uint32_t)ldw * (uint32_t)EB + chunk * 16)
+                  : (uint32_t)((m0 + row0) * (uint32_t)lda * (uint32_t)EB + chunk * 16);
   };
   const int ib_w = NIA + g * (NIW / 2), ib_a = g * (NIA / 2);
   const uint32_t vw = lane_offset(ib_w, true), va = lane_offset(ib_a, false);
   auto issue_w = [&](int kt) __attribute__((always_inline)) {
     unsigned char* base = smem + (kt % NST) * STAGE;
-    const uint32_t koff = (uint32_t)(kt * BK * 2);
+    const uint32_t koff = (uint32_t)(kt * 2 * BK);
     constexpr int CW = NIW / 2;
 #pragma unroll
     for (int j = 0; j < (CW + 3) / 4; ++j)
@@ -1335,7 +1342,7 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
   };
   auto issue_a = [&](int kt) __attribute__((always_inline)) {
     unsigned char* base = smem + (kt % NST) * STAGE;
-    const uint32_t koff = (uint32_t)(kt * BK * 2);
+    const uint32_t koff = (uint32_t)(kt * 2 * BK);
     constexpr int CA = NIA / 2;
 #pragma unroll
     for (int j = 0; j < (CA + 3) / 4; ++j)
@@ -1356,10 +1363,19 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
 #pragma unroll
     for (int j = 0; j < FNB; ++j) acc[i][j] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
 
-  // Fragments of one 32-deep step (16x16x32): lane l reads row l % 16 of a 16-row block at K chunk
-  // 4 * (j % 2) + l / 16 of tile j / 2's stage.
-  bf16x8_t fa[FMB], fb[FNB];
-  const int KT = K / BK;
+  // bf16 -- fragments of one 32-deep step (16x16x32): lane l reads row l % 16 of a 16-row block at K
+  // chunk 4 * (j % 2) + l / 16 of tile j / 2's stage.
+  // F8 -- one v_mfma_f32_16x16x128_f8f6f4 covers a whole 128-deep tile: lane l feeds 32 bytes of row
+  // l % 16, chunks 2 (l / 16) and 2 (l / 16) + 1, from both operands alike (an MFMA pairs the same lane
+  // group and byte slot of its two sources, so a consistent assignment is all the product needs). The
+  // tile's two steps split the row blocks instead of K: step 2u reads the W fragments (kept for both
+  // steps) and row blocks [0, FH), step 2u + 1 the row blocks [FH, FMB), which keeps the fragment
+  // registers near the bf16 kernel's; the step parity is a compile-time constant of the F8 loop.
+  typedef int i32x8_t __attribute__((ext_vector_type(8)));
+  constexpr int FH = (FMB + 1) / 2;
+  bf16x8_t fa[F8 ? 1 : FMB], fb[F8 ? 1 : FNB];
+  i32x8_t fa8[F8 ? FH : 1], fb8[F8 ? FNB : 1];
+  const int KT = K / BKE;
   const int S = 2 * KT;
   auto read_frags = [&](int j) __attribute__((always_inline)) {
     const unsigned char* st = smem + ((j >> 1) % NST) * STAGE;
@@ -1378,6 +1394,34 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
 #pragma unroll
       for (int jj = 0; jj < FNB; ++jj)
         acc[i][jj] = __builtin_amdgcn_mfma_f32_16x16x32_bf16(fb[jj], fa[i], acc[i][jj], 0, 0, 0);
+  };
+  auto rd32 = [&](const unsigned char* st, int r) __attribute__((always_inline)) {
+    const int c0 = 2 * (lane >> 4);
+    const uint4 lo = *reinterpret_cast<const uint4*>(st + L::swz(r, c0));
+    const uint4 hi = *reinterpret_cast<const uint4*>(st + L::swz(r, c0 + 1));
+    return i32x8_t{(int)lo.x, (int)lo.y, (int)lo.z, (int)lo.w, (int)hi.x, (int)hi.y, (int)hi.z, (int)hi.w};
+  };
+  auto read_frags8 = [&](int j, auto odd_c) __attribute__((always_inline)) {
+    const unsigned char* st = smem + ((j >> 1) % NST) * STAGE;
+    if constexpr (!decltype(odd_c)::value) {
+#pragma unroll
+      for (int jj = 0; jj < FNB; ++jj) fb8[jj] = rd32(st, BM + wn0 + jj * 16 + (lane & 15));
+#pragma unroll
+      for (int i = 0; i < FH; ++i) fa8[i] = rd32(st, wm0 + i * 16 + (lane & 15));
+    } else {
+#pragma unroll
+      for (int i = 0; i < FMB - FH; ++i) fa8[i] = rd32(st, wm0 + (FH + i) * 16 + (lane & 15));
+    }
+  };
+  auto mfmas8 = [&](auto odd_c) __attribute__((always_inline)) {
+    constexpr int I0 = decltype(odd_c)::value ? FH : 0;
+    constexpr int NI8 = decltype(odd_c)::value ? FMB - FH : FH;
+#pragma unroll
+    for (int i = 0; i < NI8; ++i)
+#pragma unroll
+      for (int jj = 0; jj < FNB; ++jj)
+        acc[I0 + i][jj] =
+            __builtin_amdgcn_mfma_scale_f32_16x16x128_f8f6f4(fb8[jj], fa8[i], acc[I0 + i][jj], 0, 0, 0, 0, 0, 0);
   };
   // n_arows: this wave's A-row loads of a tile (issued after its W rows).
   const int n_arows = (NIA / 2) / 4 + (lw < (NIA / 2) % 4 ? 1 : 0);
@@ -1409,6 +1453,25 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
     mfmas();
     if ((j & 1) == 1 && (j >> 1) + 1 < KT) wait_vmcnt<0>();  // group 0: all of tile u + 1; group 1: its A rows
   };
+  // The F8 steps: the same phases and loads, the parity fixed at compile time.
+  auto step8 = [&](int j, auto odd_c) __attribute__((always_inline)) {
+    constexpr bool ODD = decltype(odd_c)::value;
+    read_frags8(j, odd_c);
+    const int u = j >> 1;
+    if (u >= 1 && u + 1 < KT) {
+      if constexpr (!ODD) issue_w(u + 1);
+      else issue_a(u + 1);
+    }
+    if constexpr (ODD) {
+      if (g == 1 && u + 1 < KT) wait_n(n_arows);
+    }
+    block_barrier();
+    mfmas8(odd_c);
+    if constexpr (ODD) {
+      if (u + 1 < KT) wait_vmcnt<0>();
+    }
+    block_barrier();
+  };
 
   issue_tile(0);
   if (KT > 1) {
@@ -1418,7 +1481,16 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t l
     wait_vmcnt<0>();
   }
   block_barrier();
-  if (g == 0) {
+  if constexpr (F8) {
+    using Even = std::false_type;
+    using Odd = std::true_type;
+    if (g == 1) block_barrier();
+    for (int j = 0; j < S; j += 2) {
+      step8(j, Even{});
+      step8(j + 1, Odd{});
+    }
+    if (g == 0) block_barrier();
+  } else if (g == 0) {
     for (int j = 0; j < S; ++j) {
       mem_phase(j);
       block_barrier();
@@ -1555,6 +1627,15 @@ struct GemmCfg {
     gemm_bf16_pp_kernel<BM, BN, kEpiPartial>},                                                            \
    64, 2, 1, 0}
 
+// pf = -4: the ping-pong kernel on e4m3 operands (oudjat_linear_fp8; no GELU epilogue -- the FP8 route
+// serves the SwiGLU blocks' linears -- and no split K).
+#define OUDJAT_GEMM_PP8_CFG(BM, BN)                                                                       \
+  {BM, BN, 2, 4, -4,                                                                                     \
+   {gemm_bf16_pp_kernel<BM, BN, 0, true>, nullptr, gemm_bf16_pp_kernel<BM, BN, 2, true>,                  \
+    gemm_bf16_pp_kernel<BM, BN, 3, true>, gemm_bf16_pp_kernel<BM, BN, 4, true>,                           \
+    gemm_bf16_pp_kernel<BM, BN, kEpiQkv, true>, nullptr},                                                 \
+   64, 2, 1, 0}
+
 static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_CFG(128, 128, 2, 2, 1),  // 0
     OUDJAT_GEMM_CFG(128, 128, 2, 2, 2),  // 1
@@ -1591,6 +1672,10 @@ static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_DMA_CFG(128, 32, 4, 1),  // 32: tiny grids (128 x 32, four waves of 32 x 32)
     OUDJAT_GEMM_DMA_CFG(128, 64, 2, 2),  // 33: tiny fused-QKV grids (whole 64-wide heads)
     OUDJAT_GEMM_R16_CFG(128, 256, 2, 4, 1, 64, 3, false),  // 34: long-K products of ~one round of 128 x 256
+    OUDJAT_GEMM_PP8_CFG(288, 256),  // 35: FP8 ping-pong tiles
+    OUDJAT_GEMM_PP8_CFG(224, 256),  // 36
+    OUDJAT_GEMM_PP8_CFG(192, 256),  // 37
+    OUDJAT_GEMM_PP8_CFG(128, 256),  // 38
 };
 static constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -1766,6 +1851,29 @@ static int choose_qkv_cfg(int64_t M, int64_t N, int64_t K, int64_t Dh) {
   return ci;
 }
 
+// FP8 products (e4m3 operands: half the operand bytes per K of bf16) on the FP8 ping-pong tiles, chosen
+// as for bf16: one round of 224- or 288-row tiles; else two rounds of whichever of 288, 224 and 192 rows
+// fills them most; else one round of 192-row tiles; else 128-row tiles (ViT-7B at B = 4, M = 1656: qkv
+// 432 tiles of 192 x 256, proj and w3 208 of 128 x 256, w1 / w2 256 of 224 x 256). N % 256 == 0.
+static int choose_cfg_fp8(int64_t M, int64_t N) {
+  const int64_t t288 = cdiv(M, 288) * (N / 256), t224 = cdiv(M, 224) * (N / 256);
+  const int64_t t192 = cdiv(M, 192) * (N / 256);
+  if (t224 >= 224 && t224 <= 256 && t288 < t224) return 36;
+  if (t288 >= 192 && t288 <= 256) return 35;
+  int best = -1;
+  int64_t best_tiles = 0;
+  const int64_t cand_tiles[3] = {t288, t224, t192};
+  const int cand_cfg[3] = {35, 36, 37};
+  for (int c = 0; c < 3; ++c)
+    if (cand_tiles[c] > 256 && cand_tiles[c] <= 512 && cand_tiles[c] > best_tiles) {
+      best = cand_cfg[c];
+      best_tiles = cand_tiles[c];
+    }
+  if (best >= 0 && best_tiles > 384) return best;
+  if (t192 >= 192 && t192 <= 256) return 37;
+  return 38;
+}
+
 // Launches configuration `ci` with epilogue `epi` (arguments already validated).
 static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W, int64_t N,
                        int64_t ldw, int epi, const EpiArgs& ea, uint16_t* C, int64_t ldc, hipStream_t stream,
@@ -1776,7 +1884,7 @@ static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t 
   // K stages, or (direct-to-LDS kernels) the bf16 output tile of the epilogue if that is larger.
   size_t lds = cfg.pf < 0 ? (size_t)kStages * (cfg.bm + cfg.bn) * 64 : (size_t)2 * (cfg.bm + cfg.bn) * 128;
   if (cfg.pf <= 0) lds = lds > (size_t)cfg.bm * (cfg.bn + 8) * 2 ? lds : (size_t)cfg.bm * (cfg.bn + 8) * 2;
-  if (cfg.pf == -2 || cfg.pf == -3) lds = r16_lut_offset(cfg.bm, cfg.bn, cfg.wgm, cfg.wgn, cfg.ks, cfg.bk, cfg.nst);
+  if (cfg.pf <= -2) lds = r16_lut_offset(cfg.bm, cfg.bn, cfg.wgm, cfg.wgn, cfg.ks, cfg.bk, cfg.nst);
   if (cfg.pf <= 0 && epi == OUDJAT_EPI_BIAS_GELU) lds += kGeluLut * sizeof(uint16_t);
   if (epi == OUDJAT_EPI_BIAS_GELU) {
     const int st = ensure_gelu_table();
@@ -1948,6 +2056,8 @@ extern "C" int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K
                      "linear_qkv_rope_kv");
 }
 
+static int kernel_name_of(const GemmCfg& c, int epi, char* buf, int64_t buflen);
+
 // Kernel a linear_bf16 call of this shape would launch, as the demangled name profilers print
 // (aligned operands assumed). For matching profile summaries to the running build.
 extern "C" int oudjat_linear_kernel_name(int64_t M, int64_t N, int64_t K, int epi, char* buf, int64_t buflen) {
@@ -1958,8 +2068,22 @@ extern "C" int oudjat_linear_kernel_name(int64_t M, int64_t N, int64_t K, int ep
   const int sk = epi == kEpiQkv ? -1 : choose_splitk(M, N, K, epi, &S);
   if (sk >= 0 && S > 1) epi = kEpiPartial;  // split K (with a workspace): the partial kernel, then the reduce
   const GemmCfg& c = kCfgs[sk >= 0 && S > 1 ? sk : (epi == kEpiQkv ? choose_qkv_cfg(M, N, K, 64) : choose_cfg(M, N, K, true))];
+  return kernel_name_of(c, epi, buf, buflen);
+}
+
+// The same for oudjat_linear_fp8 (epi = 5: oudjat_linear_qkv_rope_kv_fp8).
+extern "C" int oudjat_linear_fp8_kernel_name(int64_t M, int64_t N, int64_t K, int epi, char* buf, int64_t buflen) {
+  OUDJAT_REQUIRE(buf && buflen > 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_fp8_kernel_name: no buffer");
+  OUDJAT_REQUIRE(M > 0 && N > 0 && K > 0 && N % 256 == 0 && epi >= 0 && epi <= kEpiQkv, OUDJAT_ERR_INVALID_ARGUMENT,
+                 "linear_fp8_kernel_name: bad arguments");
+  return kernel_name_of(kCfgs[choose_cfg_fp8(M, N)], epi, buf, buflen);
+}
+
+static int kernel_name_of(const GemmCfg& c, int epi, char* buf, int64_t buflen) {
   int n;
-  if (c.pf == -3)
+  if (c.pf == -4)
+    n = snprintf(buf, (size_t)buflen, "oudjat::gemm_bf16_pp_kernel<%d, %d, %d, true>", c.bm, c.bn, epi);
+  else if (c.pf == -3)
     n = snprintf(buf, (size_t)buflen, "oudjat::gemm_bf16_pp_kernel<%d, %d, %d>", c.bm, c.bn, epi);
   else if (c.pf == -2)
     n = snprintf(buf, (size_t)buflen, "oudjat::gemm_bf16_r16_kernel<%d, %d, %d, %d, %d, %d, %d, %s, %d>", c.bm, c.bn,
@@ -1973,4 +2097,83 @@ extern "C" int oudjat_linear_kernel_name(int64_t M, int64_t N, int64_t K, int ep
                  epi);
   OUDJAT_REQUIRE(n >= 0 && n < buflen, OUDJAT_ERR_INVALID_ARGUMENT, "linear_kernel_name: buffer too small");
   return OUDJAT_OK;
+}
+
+// ------------------------------------------------------------------------------------------------
+// FP8 (e4m3fn) products: torch._scaled_mm of FastFP8Linear (fp8_fast_linear.py:174-196) on the
+// native FP8 MFMA. Operand and output rules as oudjat_linear_bf16 except: one byte per operand
+// element, K % 128 == 0, N % 256 == 0, lda % 16 == 0 and ldw % 16 == 0 (16-byte rows), aligned
+// epilogue operands, no GELU epilogue, no split K.
+// ------------------------------------------------------------------------------------------------
+
+static int check_fp8_operands(const uint8_t* A, int64_t M, int64_t K, int64_t lda, const uint8_t* W, int64_t N,
+                              int64_t ldw, const char* what) {
+  OUDJAT_REQUIRE(A && W, OUDJAT_ERR_INVALID_ARGUMENT, "%s: null operand", what);
+  OUDJAT_REQUIRE(K > 0 && K % 128 == 0 && N % 256 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE,
+                 "%s: need K %% 128 == 0 and N %% 256 == 0 (K=%lld, N=%lld)", what, (long long)K, (long long)N);
+  OUDJAT_REQUIRE(lda % 16 == 0 && ldw % 16 == 0 && lda >= K && ldw >= K && aligned(A, 16) && aligned(W, 16),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "%s: 16-byte aligned operand rows required", what);
+  OUDJAT_REQUIRE(M < ((int64_t)1 << 31) && N < ((int64_t)1 << 31) && M * lda < ((int64_t)1 << 32) &&
+                     N * ldw < ((int64_t)1 << 32),
+                 OUDJAT_ERR_TOO_LARGE, "%s: operands beyond 4 GiB or 2^31 rows", what);
+  return OUDJAT_OK;
+}
+
+extern "C" int oudjat_linear_fp8(const uint8_t* A, int64_t M, int64_t K, int64_t lda, const uint8_t* W, int64_t N,
+                                 int64_t ldw, const uint16_t* bias, int epi, const uint16_t* gamma,
+                                 const uint16_t* resid, int64_t ldr, uint16_t* C, int64_t ldc, float acc_scale,
+                                 oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(M >= 0 && N >= 0 && K >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_fp8: negative size");
+  OUDJAT_REQUIRE(epi == OUDJAT_EPI_BIAS || epi == OUDJAT_EPI_BIAS_LS_RESID || epi == OUDJAT_EPI_BIAS_LS ||
+                     epi == OUDJAT_EPI_BIAS_SILU_MUL,
+                 OUDJAT_ERR_INVALID_ARGUMENT, "linear_fp8: unsupported epilogue %d", epi);
+  if (M == 0 || N == 0) return OUDJAT_OK;
+  const int st = check_fp8_operands(A, M, K, lda, W, N, ldw, "linear_fp8");
+  if (st != OUDJAT_OK) return st;
+  OUDJAT_REQUIRE(C, OUDJAT_ERR_INVALID_ARGUMENT, "linear_fp8: null output");
+  OUDJAT_REQUIRE((epi != OUDJAT_EPI_BIAS_LS && epi != OUDJAT_EPI_BIAS_LS_RESID) || gamma, OUDJAT_ERR_INVALID_ARGUMENT,
+                 "linear_fp8: epilogue needs gamma");
+  OUDJAT_REQUIRE((epi != OUDJAT_EPI_BIAS_LS_RESID && epi != OUDJAT_EPI_BIAS_SILU_MUL) || resid,
+                 OUDJAT_ERR_INVALID_ARGUMENT, "linear_fp8: epilogue needs resid");
+  OUDJAT_REQUIRE(aligned(C, 16) && ldc % 8 == 0 && ldc >= N && (!bias || aligned(bias, 8)) &&
+                     (!gamma || aligned(gamma, 16)) && (!resid || (aligned(resid, 16) && ldr % 8 == 0)),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "linear_fp8: 16-byte aligned output, residual and gamma rows required");
+  EpiArgs ea{};
+  ea.bias = bias;
+  ea.gamma = gamma;
+  ea.resid = resid;
+  ea.ldr = ldr;
+  ea.acc_scale = acc_scale;
+  return launch_gemm(choose_cfg_fp8(M, N), reinterpret_cast<const uint16_t*>(A), M, K, lda,
+                     reinterpret_cast<const uint16_t*>(W), N, ldw, epi, ea, C, ldc, as_stream(stream), "linear_fp8");
+}
+
+extern "C" int oudjat_linear_qkv_rope_kv_fp8(const uint8_t* A, int64_t M, int64_t K, int64_t lda, const uint8_t* W,
+                                             int64_t ldw, const uint16_t* bias, int64_t H, int64_t Dh,
+                                             const float* sin_table, const float* cos_table, int64_t table_stride,
+                                             const uint8_t* patch_mask, const int64_t* rope_idx,
+                                             const int64_t* batch_idx, const int64_t* token_idx, uint16_t* kv,
+                                             int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
+                                             float acc_scale, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(M >= 0 && K >= 0 && H > 0 && Dh > 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_qkv_rope_kv_fp8: bad size");
+  if (M == 0) return OUDJAT_OK;
+  const int64_t N = 3 * H * Dh;
+  OUDJAT_REQUIRE(kv && q_out && sin_table && cos_table && patch_mask && rope_idx && batch_idx && token_idx,
+                 OUDJAT_ERR_INVALID_ARGUMENT, "linear_qkv_rope_kv_fp8: null pointer");
+  OUDJAT_REQUIRE(Dh % 16 == 0 && 128 % Dh == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE,
+                 "linear_qkv_rope_kv_fp8: need Dh in {16, 32, 64, 128} (Dh=%lld)", (long long)Dh);
+  const int st = check_fp8_operands(A, M, K, lda, W, N, ldw, "linear_qkv_rope_kv_fp8");
+  if (st != OUDJAT_OK) return st;
+  OUDJAT_REQUIRE((!bias || aligned(bias, 8)) && aligned(kv, 16) && aligned(q_out, 16) && kv_stride_b % 8 == 0 &&
+                     kv_stride_n % 8 == 0 && table_stride % 4 == 0 && aligned(sin_table, 16) && aligned(cos_table, 16),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT,
+                 "linear_qkv_rope_kv_fp8: 16-byte aligned outputs and rows, strides %% 8 == 0, tables 16-byte rows");
+  EpiArgs ea{};
+  ea.bias = bias;
+  ea.acc_scale = acc_scale;
+  ea.qkv = QkvArgs{(int)H, (int)Dh, sin_table, cos_table, table_stride, patch_mask, rope_idx, batch_idx, token_idx,
+                   kv, kv_stride_b, kv_stride_n, q_out};
+  return launch_gemm(choose_cfg_fp8(M, N), reinterpret_cast<const uint16_t*>(A), M, K, lda,
+                     reinterpret_cast<const uint16_t*>(W), N, ldw, kEpiQkv, ea, nullptr, 0, as_stream(stream),
+                     "linear_qkv_rope_kv_fp8");
 }

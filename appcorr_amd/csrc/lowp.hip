@@ -63,6 +63,32 @@ __global__ void __launch_bounds__(kLpThreads) fp8_qdq_kernel(const uint16_t* __r
   *reinterpret_cast<uint4*>(out + row * os + c) = pack8(f);
 }
 
+// The same quantizer writing the e4m3fn codes themselves (one byte per element, the operands of the
+// native FP8 GEMM): sign bit | magnitude code; NaN gives the NaN code 0x7f with its sign.
+__global__ void __launch_bounds__(kLpThreads) fp8_quantize_kernel(const uint16_t* __restrict__ x, int64_t M, int64_t K,
+                                                                  int64_t sm, const float* __restrict__ scalep,
+                                                                  int mode, uint8_t* __restrict__ out, int64_t os) {
+  const int64_t chunks = K >> 3;
+  const int64_t i = (int64_t)blockIdx.x * kLpThreads + threadIdx.x;
+  if (i >= M * chunks) return;
+  const int64_t row = i / chunks, c = (i - row * chunks) * 8;
+  float s = *scalep;
+  if (mode == 1) s = round_bf16(s);
+  float f[8];
+  unpack8(*reinterpret_cast<const uint4*>(x + row * sm + c), f);
+  uint32_t code[8];
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float v = mode == 0 ? f[e] * s : round_bf16((float)((double)f[e] / (double)s));
+    const uint32_t sign = (__float_as_uint(v) >> 31) << 7;
+    code[e] = sign | (v != v ? 0x7fu : e4m3_code_abs(fminf(fabsf(v), 448.0f)));
+  }
+  uint2 w;
+  w.x = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);
+  w.y = code[4] | (code[5] << 8) | (code[6] << 16) | (code[7] << 24);
+  *reinterpret_cast<uint2*>(out + row * os + c) = w;
+}
+
 // NVFP4 output epilogue: out = bf16(v * s + b) over [M, N] (the fp32 multiply-add contracted to one
 // rounding when a bias is present, as the reference's Triton kernel compiles it; v * s without one),
 // and with gamma additionally bf16(that * gamma[col]) (the block's LayerScale on the result).
@@ -171,6 +197,21 @@ extern "C" int oudjat_fp8_quantize_dequantize(const uint16_t* x, int64_t M, int6
   fp8_qdq_kernel<<<(unsigned)cdiv(n, kLpThreads), kLpThreads, 0, as_stream(stream)>>>(x, M, K, stride_m, scale, mode,
                                                                                       out, out_stride);
   return check_launch("fp8_quantize_dequantize");
+}
+
+extern "C" int oudjat_fp8_quantize(const uint16_t* x, int64_t M, int64_t K, int64_t stride_m, const float* scale,
+                                   int mode, uint8_t* out, int64_t out_stride, oudjat_stream_t stream) {
+  int st = launch_rows("fp8_quantize", M, K);
+  if (st != OUDJAT_OK) return st;
+  OUDJAT_REQUIRE(mode == 0 || mode == 1, OUDJAT_ERR_INVALID_ARGUMENT, "fp8_quantize: mode %d", mode);
+  if (M == 0 || K == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(x && scale && out, OUDJAT_ERR_INVALID_ARGUMENT, "fp8_quantize: null pointer");
+  OUDJAT_REQUIRE(aligned(x, 16) && aligned(out, 8) && stride_m % 8 == 0 && out_stride % 8 == 0,
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "fp8_quantize: 16-byte aligned input rows, 8-byte aligned output rows");
+  const int64_t n = M * (K / 8);
+  fp8_quantize_kernel<<<(unsigned)cdiv(n, kLpThreads), kLpThreads, 0, as_stream(stream)>>>(x, M, K, stride_m, scale,
+                                                                                           mode, out, out_stride);
+  return check_launch("fp8_quantize");
 }
 
 extern "C" int oudjat_scale_bias_rows(const uint16_t* x, int64_t M, int64_t N, int64_t x_stride, float scale,

@@ -39,13 +39,14 @@ from . import lowp as LP
 
 
 def _linear_route(mod: nn.Module, x: Tensor, site: str, *, bias: Tensor | None = None, **kw) -> Tensor:
-    """One correction linear on its route: FP8 (the e4m3 operand as exact bf16 values, the per-tensor
-    scales on the fp32 accumulator; fp8_fast_linear.py:174-196) when `mod` is a frozen FastFP8Linear,
-    else bf16 -- a plain nn.Linear, or a low-precision linear still calibrating, whose observer sees
-    the input first (fp4_fast_linear.py:255-259). `bias` overrides mod.bias (the masked qkv bias)."""
+    """One correction linear on its route: FP8 (e4m3 operands on the FP8 MFMA, or their exact bf16
+    values where the FP8 GEMM does not take the shape; the per-tensor scales on the fp32 accumulator;
+    fp8_fast_linear.py:174-196) when `mod` is a frozen FastFP8Linear, else bf16 -- a plain nn.Linear,
+    or a low-precision linear still calibrating, whose observer sees the input first
+    (fp4_fast_linear.py:255-259). `bias` overrides mod.bias (the masked qkv bias)."""
     b = mod.bias if bias is None else bias
     if LP.low_precision_state(mod) == "fp8":
-        return K.linear(mod.quantize(x), mod.weight_hat, b, site=site, acc_scale=mod.acc_scale_f, **kw)
+        return mod.linear(x, b, site, **kw)
     if isinstance(mod, LP._LowPrecisionLinear):
         mod.observe(x)
     return K.linear(x, mod.weight, b, site=site, **kw)
@@ -208,6 +209,11 @@ class SelfAttention(nn.Module):
             # NVFP4: raw GEMM output, then scale and bias (fp4_fast_linear.py:251-283), then RoPE / K-V
             raw, s, b = _fp4_raw(mod, xn, "qkv")
             qkv = K.scale_bias(raw, s, b, out=raw)
+        elif state == "fp8" and mod.native and K.qkv_fusable(H, D):
+            K.linear_qkv_rope_kv_fp8(mod.quantize_codes(xn), mod.weight_q, self.qkv_bias(), rope, qs.active_patch_mask,
+                                     qs.active_rope_idx, qs.active_batch_idx, qs.active_token_idx, kv, q,
+                                     acc_scale=mod.acc_scale_f)
+            qkv = None
         elif K.qkv_fusable(H, D):
             if state == "fp8":
                 a, w, s = mod.quantize(xn), mod.weight_hat, mod.acc_scale_f

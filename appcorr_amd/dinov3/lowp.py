@@ -6,12 +6,13 @@ module starts *calibrating* (the block runs its exact bf16 GEMM while an observe
 max |x| of the module's input), and `freeze_activation_scale` bakes a static activation scale from that
 maximum, after which the block runs the low-precision route.
 
-gfx950 has no MFMA for NVFP4 (16-element blocks, e4m3 scales), and every value the reference's scaled
-GEMMs multiply is exact in bf16 (e2m1 code x e4m3 block scale; an e4m3 code). So each operand is
-quantized with the reference's rounding and kept as those exact bf16 values (`weight_hat`, once at
-construction; the activation per call), and the bf16 MFMA GEMM with fp32 accumulation computes the
-scaled GEMM's products and sum, up to the order of the fp32 additions. The per-tensor factors follow
-the reference:
+gfx950 has no MFMA for NVFP4 (16-element blocks, e4m3 scales), and every value an NVFP4 GEMM multiplies
+(e2m1 code x e4m3 block scale) is exact in bf16. So the NVFP4 operands are quantized with the
+reference's rounding and kept as those exact bf16 values (`weight_hat`, once at construction; the
+activation per call), and the bf16 MFMA GEMM with fp32 accumulation computes the scaled GEMM's
+products and sum, up to the order of the fp32 additions. FP8 (OCP e4m3) is native on gfx950: the FP8
+linears keep e4m3 codes and run the FP8 MFMA (exact products, fp32 accumulation). The per-tensor
+factors follow the reference:
   NVFP4: raw = bf16(A_hat . W_hat^T) (torch._scaled_mm, out_dtype bf16), then raw * out_scale + bias in
          fp32 (scale_bias_inplace_triton), out_scale = bf16(act_scale * weight_scale);
   FP8:   bf16(acc * act_scale * weight_scale + bias) (torch._scaled_mm with scales and bias), applied
@@ -136,7 +137,12 @@ class FastFP4Linear(_LowPrecisionLinear):
 
 
 class FastFP8Linear(_LowPrecisionLinear):
-    """nn.Linear in FP8 e4m3 with per-tensor scales (fp8_fast_linear.py:83-196)."""
+    """nn.Linear in FP8 e4m3 with per-tensor scales (fp8_fast_linear.py:83-196).
+
+    Where the native FP8 GEMM takes the shape (K % 128 == 0, N % 256 == 0: every ViT-7B linear) the
+    weight is kept as its e4m3 codes (`weight_q`) and the product runs on the FP8 MFMA with the
+    activation quantized to codes per call; otherwise as the codes' exact bf16 values (`weight_hat`)
+    on the bf16 MFMA. Both compute the same exact products with fp32 accumulation."""
 
     def __init__(self, linear: nn.Linear, bucket_rows: int = 0) -> None:
         if linear.in_features % 16 or linear.out_features % 16:
@@ -144,11 +150,18 @@ class FastFP8Linear(_LowPrecisionLinear):
                              f"{linear.in_features}x{linear.out_features}")
         super().__init__(linear)
         self.bucket_rows = max(0, int(bucket_rows))
+        self.native = K.fp8_gemm_supported(self.in_features, self.out_features)
         with torch.no_grad():
             self.weight_scale = (_amax(self.weight) / E4M3_MAX).clamp(min=1e-12)
-            self.weight_hat = K.fp8_quantize_dequantize(self.weight, self.weight_scale, K.FP8_WEIGHT)
+            if self.native:
+                self.weight_q = K.fp8_quantize(self.weight, self.weight_scale.reshape(1), K.FP8_WEIGHT)
+                self.weight_hat = None
+            else:
+                self.weight_q = None
+                self.weight_hat = K.fp8_quantize_dequantize(self.weight, self.weight_scale, K.FP8_WEIGHT)
         self.act_scale = torch.zeros((), device=self.weight.device, dtype=torch.float32)
         self.act_inv_scale = torch.zeros((), device=self.weight.device, dtype=torch.bfloat16)
+        self._act_inv_f32 = torch.zeros(1, device=self.weight.device, dtype=torch.float32)
         self.acc_scale_f = 0.0
 
     @torch.no_grad()
@@ -162,12 +175,26 @@ class FastFP8Linear(_LowPrecisionLinear):
         scale = (self.amax.float() / E4M3_MAX).clamp(min=1e-12)
         self.act_scale = scale
         self.act_inv_scale = (1.0 / scale).to(torch.bfloat16)
+        self._act_inv_f32 = self.act_inv_scale.float().reshape(1)  # the quantizer's fp32 operand, once
         self.acc_scale_f = float(self.act_scale * self.weight_scale)
         self.calibrating = False
         return True
 
     def quantize(self, x2d: torch.Tensor) -> torch.Tensor:
-        return K.fp8_quantize_dequantize(x2d, self.act_inv_scale, K.FP8_ACTIVATION)
+        """The activation's e4m3 values as bf16 (the operand of the bf16-MFMA route)."""
+        return K.fp8_quantize_dequantize(x2d, self._act_inv_f32, K.FP8_ACTIVATION)
+
+    def quantize_codes(self, x2d: torch.Tensor) -> torch.Tensor:
+        """The activation's e4m3fn codes, uint8 (the operand of the native FP8 GEMM)."""
+        return K.fp8_quantize(x2d, self._act_inv_f32, K.FP8_ACTIVATION)
+
+    def linear(self, x: torch.Tensor, bias: torch.Tensor | None, site: str, **kw) -> torch.Tensor:
+        """The frozen linear's output: bf16(acc * act_scale * weight_scale + bias) with the epilogue of
+        `kw` (fp8_fast_linear.py:174-196)."""
+        if self.native:
+            return K.linear_fp8(self.quantize_codes(x), self.weight_q, bias, acc_scale=self.acc_scale_f, site=site,
+                                **kw)
+        return K.linear(self.quantize(x), self.weight_hat, bias, site=site, acc_scale=self.acc_scale_f, **kw)
 
     def extra_repr(self) -> str:
         return f"in={self.in_features}, out={self.out_features}, state={'calibrating' if self.calibrating else 'fp8'}"

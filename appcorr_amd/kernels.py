@@ -25,7 +25,7 @@ P = ctypes.c_void_p
 # Optional live timing of launch sites: every launch at a site named in `_probe["tags"]` is bracketed
 # by a pair of timing events on the launch stream (used by bench.py for the roofline). Sites are the
 # kernels' roles in the pass: "qkv", "proj", "fc1", "fc2", "w1", "w2", "w3", "attention", ...
-_probe: dict = {"tags": frozenset(), "events": {}}
+_probe: dict = {"tags": frozenset(), "events": {}, "gaps": []}
 
 
 def set_probe(tags) -> None:
@@ -36,6 +36,7 @@ def set_probe(tags) -> None:
         tags = (tags,)
     _probe["tags"] = frozenset(tags)
     _probe["events"] = {}
+    _probe["gaps"] = []
 
 
 def probe_events() -> dict:
@@ -43,16 +44,24 @@ def probe_events() -> dict:
     return _probe["events"]
 
 
+def probe_gaps() -> list:
+    """[(event, event), ...]: after each probed launch's end event a third event is recorded right
+    away; the time between the two is what an empty bracket reads (the events' own overhead)."""
+    return _probe["gaps"]
+
+
 def _launch(tag: str, t: torch.Tensor, name: str, *args) -> None:
     if tag not in _probe["tags"]:
         call(name, *args)
         return
     s = torch.cuda.current_stream(t.device)
-    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
     e0.record(s)
     call(name, *args)
     e1.record(s)
+    e2.record(s)
     _probe["events"].setdefault(tag, []).append((e0, e1))
+    _probe["gaps"].append((e1, e2))
 
 
 def _ptr(t: torch.Tensor | None) -> P:
@@ -643,9 +652,74 @@ def linear_qkv_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor
             float(acc_scale), _stream(x))
 
 
+def linear_qkv_rope_kv_fp8(x8: torch.Tensor, w8: torch.Tensor, bias: torch.Tensor | None, rope,
+                           patch_mask: torch.Tensor, rope_idx: torch.Tensor, batch_idx: torch.Tensor,
+                           token_idx: torch.Tensor, kv_cache: torch.Tensor, q_out: torch.Tensor,
+                           acc_scale: float) -> None:
+    """linear_qkv_rope_kv on e4m3fn codes (uint8 x8 [M, K], w8 [3 H Dh, K]) on the FP8 MFMA: the FP8 qkv
+    linear (fp8_fast_linear.py:174-196) with its scales on the accumulator, then RoPE and the K/V write."""
+    sin, cos = rope
+    _require_cuda(x8, w8, bias, patch_mask, rope_idx, batch_idx, token_idx, kv_cache, q_out, sin, cos)
+    M, Kd = x8.shape
+    _require(x8.dtype == w8.dtype == torch.uint8 and x8.stride(1) == 1 and w8.stride(1) == 1,
+             "linear_qkv_rope_kv_fp8: e4m3 code (uint8) operands with contiguous rows")
+    _require(kv_cache.dim() == 5 and kv_cache.shape[2] == 2 and trailing_is_packed(kv_cache, 2),
+             "linear_qkv_rope_kv_fp8: kv_cache must be [B, N, 2, H, Dh] with packed rows")
+    H, Dh = kv_cache.shape[3], kv_cache.shape[4]
+    _require(w8.shape == (3 * H * Dh, Kd), "linear_qkv_rope_kv_fp8: weight must be [3 H Dh, K]")
+    _require(q_out.is_contiguous() and q_out.shape == (M, H, Dh), "linear_qkv_rope_kv_fp8: q_out must be contiguous")
+    _require(sin.dtype == cos.dtype == torch.float32 and sin.stride(1) == 1 and cos.stride() == sin.stride(),
+             "linear_qkv_rope_kv_fp8: fp32 RoPE tables with contiguous rows")
+    _launch("qkv", x8, "oudjat_linear_qkv_rope_kv_fp8", _ptr(x8), M, Kd, x8.stride(0), _ptr(w8), w8.stride(0),
+            _ptr(None if bias is None else bias.contiguous()), H, Dh, _ptr(sin), _ptr(cos), sin.stride(0),
+            _ptr(patch_mask), _ptr(_index(rope_idx, "rope_idx")), _ptr(_index(batch_idx, "batch_idx")),
+            _ptr(_index(token_idx, "token_idx")), _ptr(kv_cache), kv_cache.stride(0), kv_cache.stride(1), _ptr(q_out),
+            float(acc_scale), _stream(x8))
+
+
 # ------------------------------------------------------------------------------------------------
 # GEMM and attention
 # ------------------------------------------------------------------------------------------------
+
+
+def fp8_gemm_supported(in_features: int, out_features: int) -> bool:
+    """Whether linear_fp8 (the native FP8 MFMA GEMM) takes a weight of this shape: K % 128, N % 256."""
+    return in_features % 128 == 0 and out_features % 256 == 0
+
+
+def linear_fp8(x8: torch.Tensor, w8: torch.Tensor, bias: torch.Tensor | None = None, *, acc_scale: float,
+               epilogue: int = _lib.EPI_BIAS, gamma: torch.Tensor | None = None, resid: torch.Tensor | None = None,
+               out: torch.Tensor | None = None, site: str = "linear") -> torch.Tensor:
+    """bf16 epilogue(acc * acc_scale + bias) with acc = x8 . w8^T over e4m3fn codes (uint8 x8 [.., K],
+    w8 [N, K]) on the FP8 MFMA: torch._scaled_mm of FastFP8Linear with its per-tensor scales
+    (fp8_fast_linear.py:174-196). Epilogues as `linear` (no GELU)."""
+    _require_cuda(x8, w8, bias, gamma, resid, out)
+    _require(x8.dtype == w8.dtype == torch.uint8, "linear_fp8: e4m3 code (uint8) operands")
+    K = x8.shape[-1]
+    N = w8.shape[0]
+    _require(w8.shape[1] == K and w8.stride(1) == 1, "linear_fp8: weight must be [N, K] with contiguous rows")
+    x2 = x8.reshape(-1, K)
+    _require(x2.stride(1) == 1, "linear_fp8: input rows must be contiguous")
+    M = x2.shape[0]
+    if out is None:
+        out = torch.empty((*x8.shape[:-1], N), device=x8.device, dtype=torch.bfloat16)
+    o2 = out.view(-1, N)
+    r2 = None
+    if resid is not None:
+        r2 = resid.reshape(-1, N)
+        _require(r2.stride(1) == 1 and r2.shape[0] == M, "linear_fp8: resid must be [M, N] with contiguous rows")
+    _launch(site, x8, "oudjat_linear_fp8", _ptr(x2), M, K, x2.stride(0), _ptr(w8), N, w8.stride(0),
+            _ptr(None if bias is None else bias.contiguous()), int(epilogue),
+            _ptr(None if gamma is None else gamma.contiguous()), _ptr(r2), 0 if r2 is None else r2.stride(0), _ptr(o2),
+            o2.stride(0), float(acc_scale), _stream(x8))
+    return out
+
+
+def linear_fp8_kernel_name(M: int, N: int, K: int, epilogue: int = _lib.EPI_BIAS) -> str:
+    """Demangled name of the kernel `linear_fp8` launches (epilogue 5: linear_qkv_rope_kv_fp8)."""
+    buf = ctypes.create_string_buffer(256)
+    call("oudjat_linear_fp8_kernel_name", M, N, K, epilogue, buf, len(buf))
+    return buf.value.decode()
 
 
 def linear_kernel_name(M: int, N: int, K: int, epilogue: int = _lib.EPI_BIAS) -> str:
@@ -657,25 +731,36 @@ def linear_kernel_name(M: int, N: int, K: int, epilogue: int = _lib.EPI_BIAS) ->
 
 _WS_ELEMS: dict = {}
 _STREAM_WS: dict = {}
-_RETIRED_WS: list = []
+_RETIRED_WS: dict = {}
 
 
 def _stream_workspace(x: torch.Tensor, elems: int) -> torch.Tensor:
     """fp32 scratch of one launch sequence (split-K GEMM partials, attention key parts): a buffer per
     (device, stream), grown to the largest need and reused by every launch on that stream (launches
     on one stream run in order, and none keeps data in it past its own launches). A buffer that is
-    outgrown stays allocated for the life of the process: a HIP graph recorded earlier on that
-    stream holds its address, and freeing it would let the allocator hand the memory to a tensor
-    that the graph's replays would then overwrite."""
+    outgrown stays allocated (listed under its stream in _RETIRED_WS): a HIP graph recorded earlier on
+    that stream holds its address, and freeing it would let the allocator hand the memory to a tensor
+    that the graph's replays would then overwrite. graphs.capture takes a recorded stream's buffers
+    out of both tables (take_stream_workspaces), so each graph owns the scratch its kernels use."""
     skey = (x.device, _lib.stream_of(x))
     buf = _STREAM_WS.get(skey)
     if buf is None or buf.numel() < elems:
         if buf is not None:  # grown geometrically, so few buffers are ever retired
-            _RETIRED_WS.append(buf)
+            _RETIRED_WS.setdefault(skey, []).append(buf)
             elems = max(elems, 2 * buf.numel())
         buf = torch.empty(elems, device=x.device, dtype=torch.float32)
         _STREAM_WS[skey] = buf
     return buf
+
+
+def take_stream_workspaces(device: torch.device, stream: int) -> list:
+    """Remove and return every scratch buffer created for launches on `stream` (raw hipStream_t) of
+    `device`: the current one and those it outgrew. The caller keeps them alive as long as anything
+    recorded on that stream may still run; later launches on the stream get a fresh buffer."""
+    skey = (torch.device(device), stream)
+    bufs = _RETIRED_WS.pop(skey, [])
+    cur = _STREAM_WS.pop(skey, None)
+    return bufs + ([cur] if cur is not None else [])
 
 
 def _gemm_workspace(x: torch.Tensor, M: int, N: int, K: int, epilogue: int) -> torch.Tensor | None:
@@ -899,6 +984,20 @@ def fp8_quantize_dequantize(x: torch.Tensor, scale: torch.Tensor, mode: int = FP
     out = torch.empty(x.shape, device=x.device, dtype=torch.bfloat16)
     _launch("fp8_qdq", x, "oudjat_fp8_quantize_dequantize", _ptr(x2), M, K, x2.stride(0), _ptr(s), int(mode), _ptr(out),
             K, _stream(x))
+    return out
+
+
+def fp8_quantize(x: torch.Tensor, scale: torch.Tensor, mode: int = FP8_ACTIVATION) -> torch.Tensor:
+    """FastFP8Linear's e4m3 operand as its e4m3fn codes, uint8 [.., K] (the same quantizer as
+    fp8_quantize_dequantize). `scale`: an fp32 device scalar (the bf16 inverse scale's value for
+    FP8_ACTIVATION, the fp32 scale for FP8_WEIGHT)."""
+    _require_cuda(x, scale)
+    _require(scale.dtype == torch.float32 and scale.numel() == 1, "fp8_quantize: scale must be one fp32 value")
+    x2 = _rows_bf16(x, "fp8_quantize")
+    M, K = x2.shape
+    out = torch.empty(x.shape, device=x.device, dtype=torch.uint8)
+    _launch("fp8_q", x, "oudjat_fp8_quantize", _ptr(x2), M, K, x2.stride(0), _ptr(scale), int(mode), _ptr(out), K,
+            _stream(x))
     return out
 
 

@@ -381,7 +381,13 @@ class DINOv3ClassifierExecutor(ModelExecutor):
         dict's K/V and blocks_out_sum tensors, the group plan); refresh their contents in place
         between replays.
         context["current_feature"] after a replay holds that replay's output. Outputs equal an eager
-        correct_forward bit for bit; the running statistics in the cache hold one pass's values.
+        correct_forward bit for bit. The running statistics (`_token_pscore_*_total`, ...) continue
+        from the values the cache held before recording: the graph writes one pass's statistics, and
+        each replay adds them into the running totals (one small launch after the graph), which the
+        cache then holds. With a plan shared by the layers (one addition per pass) the totals equal
+        those of eager passes bit for bit; with per-layer plans a pass's layer values are summed
+        before they are added (the fp32 association differs). The warm-up and recording passes are
+        not counted.
         """
         from appcorr_amd.dinov3.layers import SelfAttentionBlock
         from appcorr_amd.graphs import capture
@@ -398,8 +404,26 @@ class DINOv3ClassifierExecutor(ModelExecutor):
                 cache.pop(k, None)
             self.correct_forward(params, context, config)
 
+        cache0 = context.setdefault("cache_feature", {})
+        base = {k: cache0[k].clone() for k in stat_keys if torch.is_tensor(cache0.get(k))}
         with torch.no_grad():
-            return capture(run, self.device, warmup)
+            replay = capture(run, self.device, warmup)
+        cache = context["cache_feature"]
+        per_pass = {k: cache[k] for k in stat_keys if torch.is_tensor(cache.get(k))}  # written by every replay
+        totals = {k: base[k] if k in base else torch.zeros_like(v) for k, v in per_pass.items()}
+        keys = list(per_pass)
+
+        def replay_and_accumulate() -> None:
+            replay()
+            if keys:
+                torch._foreach_add_([totals[k] for k in keys], [per_pass[k] for k in keys])
+                cache.update(totals)
+
+        replay_and_accumulate.graph = replay.graph
+        replay_and_accumulate.replay = replay
+        if keys:
+            cache.update(totals)
+        return replay_and_accumulate
 
     def head_inference(self, task: Task, context: Dict[str, Any], config: Any) -> Dict[str, Any]:
         feat = context.get("current_feature")

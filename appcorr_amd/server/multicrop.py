@@ -6,7 +6,9 @@ correction GEMM sees all their selected rows at once (offload/server/model/dinov
 agree are grouped into buckets, each bucket's per-layer caches are concatenated along the batch,
 the correction blocks run once over the bucket with `candidate_valid_mask`, and the updated caches
 are split back to their crops (:1707-1785). This module is that caller side, built on the block's
-own threshold / top-k plan kernels; nothing in it computes on the host.
+own threshold / top-k plan kernels. It reads nothing back from the device except in union_dindices
+(the per-row unique lengths, which torch.unique needs on the host there as in the reference); whether
+a bucket has padded slots is known from the host-side candidate counts.
 
 Padded candidate slots repeat the crop's last real candidate and score -inf, so neither a threshold
 nor top-k selects them; with a threshold the kept set of each crop is exactly the one it has alone
@@ -33,6 +35,7 @@ class CropItem:
     mobile_pscore_hint: torch.Tensor | None = None
     prefix: str = ""
     cand_valid: torch.Tensor | None = field(default=None, repr=False)
+    n_padded: int = 0  # padded candidate slots per row (set by pad_crop_candidates)
 
 
 def pad_crop_candidates(items: Sequence[CropItem]) -> None:
@@ -45,10 +48,12 @@ def pad_crop_candidates(items: Sequence[CropItem]) -> None:
         d = it.dindice
         n_cand = int(d.shape[1]) - it.num_pre
         valid = torch.ones((d.shape[0], n_cand), dtype=torch.bool, device=d.device)
+        it.n_padded = 0
         if 0 < n_cand < max_cand:
             pad = max_cand - n_cand
             it.dindice = torch.cat([d, d[:, -1:].expand(-1, pad)], dim=1)
             valid = torch.cat([valid, torch.zeros((d.shape[0], pad), dtype=torch.bool, device=d.device)], dim=1)
+            it.n_padded = pad
         it.cand_valid = valid
 
 
@@ -169,9 +174,8 @@ def correct_crops_batched(run_block: RunBlock, items: List[CropItem], start_l: i
             raise RuntimeError("crops of one bucket have caches that cannot be batched")
         x = torch.cat([it.input_tokens for it in group], dim=0)
         dind = torch.cat([it.dindice for it in group], dim=0)
-        cv = torch.cat([it.cand_valid for it in group], dim=0)
-        if bool(cv.all()):
-            cv = None  # nothing padded
+        # nothing padded (known on the host): no mask
+        cv = torch.cat([it.cand_valid for it in group], dim=0) if any(it.n_padded for it in group) else None
         hints = [it.mobile_pscore_hint for it in group]
         hint = None if any(h is None for h in hints) else torch.cat(hints, dim=0)
         for l in range(start_l, end_l):

@@ -138,7 +138,8 @@ def cpu_baseline(name: str, blocks, x_full, caches, hint, k: int, budget_s: floa
                 x, cache = OM.correct_block(cfg, blocks[i], x, plan, rope, cache, f"layer{i}", mode="bf16")
         return time.perf_counter() - t0
 
-    t1 = run(1)  # one block, also a warm-up
+    run(1)  # one block: warm-up (first-call costs of the CPU kernels)
+    t1 = run(1)
     n_blk = depth if 13 * t1 * depth <= budget_s else max(1, int(budget_s / (13 * t1)))
     n_blk = min(n_blk, depth)
     for _ in range(3):
@@ -169,7 +170,8 @@ def main():
     ap.add_argument("--batch", type=int, default=None, help="images per pass (default: the config's)")
     ap.add_argument("--keep", type=float, default=None, help="token keep ratio (default: the config's)")
     ap.add_argument("--precision", default="bf16", help="correct_precision of the executor")
-    ap.add_argument("--cpu-budget", type=float, default=20.0, help="seconds of CPU-baseline sampling (0 = skip)")
+    ap.add_argument("--cpu-budget", type=float, default=45.0,
+                    help="seconds of CPU-baseline sampling (0 = skip); full passes whenever 13 of them fit")
     ap.add_argument("--cache", default="approx", choices=("approx", "random"),
                     help="fill the K/V + residual caches with the approximate pass (default) or random values")
     ap.add_argument("--graph", type=int, default=1,
@@ -301,6 +303,7 @@ def main():
             K.set_probe(MFMA_SITES[ffn])
             timed(step, max(3, args.steps // 4))
             events = K.probe_events()
+            gaps = [a.elapsed_time(b) for a, b in K.probe_gaps()]
             K.set_probe(None)
         # The corrected tokens of the last pass must be finite (outside the timed region).
         out = context["current_feature"]
@@ -341,6 +344,10 @@ def main():
                                           f"this build runs {running}: not used")
         roof["sites"] = {kk: {f: v[f] for f in ("achieved", "frac", "avg_us", "launches_per_pass", "share_of_pass")}
                          for kk, v in sites.items()}
+        roof["timing"] = ("HIP events recorded on the launch stream around every launch of each site, in eager "
+                          "probe steps after the timed replays; avg_us is the mean bracket, which includes the "
+                          "events' own overhead (event_gap_us: an empty bracket recorded after each launch)")
+        roof["event_gap_us"] = round(1e3 * sum(gaps) / max(1, len(gaps)), 3)
 
     cpu = None
     if args.cpu_budget > 0:

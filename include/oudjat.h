@@ -466,6 +466,40 @@ int oudjat_fp8_quantize_dequantize(const uint16_t* x, int64_t M, int64_t K, int6
                                    const float* scale, int mode, uint16_t* out, int64_t out_stride,
                                    oudjat_stream_t stream);
 
+/* The FP8 operand as its e4m3fn codes, one byte per element (the operands of oudjat_linear_fp8):
+ * the same quantizer as oudjat_fp8_quantize_dequantize (mode 0 activations, mode 1 the weight;
+ * fp8_fast_linear.py:71-73, 123-125, 183-186), out[m, k] = sign << 7 | magnitude code (NaN: 0x7f with
+ * its sign). K % 8 == 0, 16-byte aligned input rows, 8-byte aligned output rows. */
+int oudjat_fp8_quantize(const uint16_t* x, int64_t M, int64_t K, int64_t stride_m, const float* scale, int mode,
+                        uint8_t* out, int64_t out_stride, oudjat_stream_t stream);
+
+/* torch._scaled_mm of FastFP8Linear (fp8_fast_linear.py:174-196; the reference's FP8 correction
+ * linears) on gfx950's FP8 MFMA: acc = A . W^T over e4m3fn codes A [M, K], W [N, K] (one byte per
+ * element, row strides lda, ldw in elements), exact products accumulated in fp32, then the epilogue
+ * of oudjat_linear_bf16 with acc_scale = scale_a * scale_b (OUDJAT_EPI_BIAS, _BIAS_LS_RESID, _BIAS_LS,
+ * _BIAS_SILU_MUL). The result equals oudjat_linear_bf16 on the codes' exact bf16 values up to the
+ * order of the fp32 additions. K % 128 == 0, N % 256 == 0, lda % 16 == 0, ldw % 16 == 0, 16-byte
+ * aligned operands, output, residual and gamma rows (OUDJAT_ERR_UNSUPPORTED_SHAPE / _LAYOUT
+ * otherwise). */
+int oudjat_linear_fp8(const uint8_t* A, int64_t M, int64_t K, int64_t lda, const uint8_t* W, int64_t N, int64_t ldw,
+                      const uint16_t* bias, int epilogue, const uint16_t* gamma, const uint16_t* resid, int64_t ldr,
+                      uint16_t* C, int64_t ldc, float acc_scale, oudjat_stream_t stream);
+
+/* oudjat_linear_qkv_rope_kv with e4m3fn code operands on the FP8 MFMA (the FP8 qkv linear of a
+ * correction block, fp8_fast_linear.py:174-196 into attention.py:415-454): same outputs and epilogue
+ * arithmetic, acc_scale = scale_a * scale_b. K % 128 == 0, 3 * H * Dh % 256 == 0, Dh in {16, 32, 64,
+ * 128}, lda % 16 == 0, ldw % 16 == 0. */
+int oudjat_linear_qkv_rope_kv_fp8(const uint8_t* A, int64_t M, int64_t K, int64_t lda, const uint8_t* W, int64_t ldw,
+                                  const uint16_t* bias, int64_t H, int64_t Dh, const float* sin_table,
+                                  const float* cos_table, int64_t table_stride, const uint8_t* patch_mask,
+                                  const int64_t* rope_idx, const int64_t* batch_idx, const int64_t* token_idx,
+                                  uint16_t* kv, int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
+                                  float acc_scale, oudjat_stream_t stream);
+
+/* Introspection, no counterpart in the reference: the kernel oudjat_linear_fp8 launches for an
+ * M x N x K product with epilogue epi (5: oudjat_linear_qkv_rope_kv_fp8), as rocprofv3 prints it. */
+int oudjat_linear_fp8_kernel_name(int64_t M, int64_t N, int64_t K, int epi, char* buf, int64_t buflen);
+
 /* The NVFP4 linears' output epilogue, scale_bias_inplace_triton (token_update.py:571-617):
  * out = bf16(x * scale + bias[col]) over [M, N] (bias may be NULL: bf16(x * scale)); with gamma
  * (may be NULL) out = bf16(that * gamma[col]), the block's LayerScale (layer_scale.py:28-29). out may

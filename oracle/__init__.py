@@ -13,6 +13,16 @@ Modules
   model    DINOv3 block: weights, RoPE tables, approx and correct passes
                                                                 (block.py:312-349, 942-1191;
                                                                  attention.py:215-278, 393-534)
+  pscore   server scores of the approx pass: cls / pseudo-query attention probability and the
+           dense / log-sum-exp patch attention probability  (attention.py:241-273;
+                                                                 attention_pscore.py:20-98)
+  lowp     NVFP4 / FP8 correction linears, scale-and-bias and SwiGLU epilogues
+                                                                (fp4_fast_linear.py:103-283;
+                                                                 fp8_fast_linear.py:71-196;
+                                                                 token_update.py:571-669)
+  importance pixel-residual patch scores, image-residual token pruning
+                                                                (dinov3_classifier.py:91-197;
+                                                                 progressive.py:14-22)
 
 How each function is pinned (the checks live in tests/test_oracle_*.py):
   plan     brute-force ranking on small inputs; torch.topk on distinct scores; KATs (k=0, k=P,
@@ -24,6 +34,13 @@ How each function is pinned (the checks live in tests/test_oracle_*.py):
   model    LayerNorm / GELU / SDPA against torch.nn.functional; RoPE against the relative-position
            identity of rotations; correction at 100% keep against the full (approx) forward;
            k = 0 gives x + blocks_out_sum exactly
+  pscore   torch's own bf16 CPU ops on the same q and K; identical keys give 1/N; a dominant key
+           takes the mass; the pseudo query's zero-mean clamp
+  lowp     OCP e4m3 known answers through torch's float8_e4m3fn cast; a double-rounding case; every
+           x_hat an e2m1 grid value times its block scale; exact GEMMs against float64 products;
+           SwiGLU closed forms
+  importance the reference's own torch / numpy op sequences; constant-residual closed forms;
+           hand-derived pruning plans (min-keep rescue, "an image keeps everything")
 Parity of the third-party pieces the reference delegates to (torchao's e2m1 packer nibble order and
 NaN handling, Triton's default fp32 divide, torch.topk tie order, cuDNN/cuBLAS accumulation order)
 cannot be pinned without running the reference on its hardware: "parity unpinned" for those.

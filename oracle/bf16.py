@@ -11,11 +11,15 @@ import torch
 
 
 def f32_to_bf16_bits(a) -> np.ndarray:
-    u = np.asarray(a, dtype=np.float32).view(np.uint32).astype(np.uint64)
-    nan = (u & 0x7FFFFFFF) > 0x7F800000
-    r = ((u + 0x7FFF + ((u >> 16) & 1)) >> 16).astype(np.uint16)
-    r = np.where(nan, np.uint16(0x7FC0), r)
-    return r
+    """Round-to-nearest-even fp32 -> bf16 bits. uint32 arithmetic: the rounding increment carries out
+    of 32 bits only for NaN patterns (|u| > 0x7F800000), whose result is replaced by the quiet NaN."""
+    u = np.asarray(a, dtype=np.float32).view(np.uint32)
+    nan = (u & np.uint32(0x7FFFFFFF)) > np.uint32(0x7F800000)
+    r = np.asarray((u >> np.uint32(16)) & np.uint32(1), dtype=np.uint32)
+    r += u
+    r += np.uint32(0x7FFF)
+    r >>= np.uint32(16)
+    return np.where(nan, np.uint16(0x7FC0), r.astype(np.uint16))
 
 
 def bf16_bits_to_f32(b) -> np.ndarray:

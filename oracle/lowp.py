@@ -19,14 +19,16 @@ SwiGLU consumer), with the block flow of oracle.model.correct_block.
 e4m3 conversions use torch's CPU float8_e4m3fn cast (round to nearest even, pinned in
 tests/test_oracle_nvfp4.py).
 
-Parity unpinned: torch._scaled_mm's / cuBLASLt's fp32 accumulation order and where it applies the two
-scales (taken here as the exact acc times the fp32 product of the scales); Triton's fp32 exp and
+Scales computed from a maximum divide as torch does on a GPU tensor (cuda_scalar_div: times the fp32
+reciprocal). Parity unpinned: torch._scaled_mm's / cuBLASLt's fp32 accumulation order and where it
+applies the two scales (taken here as the exact acc times the fp32 product of the scales); Triton's fp32 exp and
 division inside sigmoid; whether the reference's scale-and-bias contracts to an FMA (taken: yes).
 """
 
 from __future__ import annotations
 
 import contextlib
+import hashlib
 
 import numpy as np
 import torch
@@ -95,13 +97,42 @@ def _matmul_exact(a: np.ndarray, b: np.ndarray) -> np.ndarray:
     return np.asarray(a, dtype=np.float64) @ np.asarray(b, dtype=np.float64).T
 
 
+_WEIGHT_MEMO: dict = {}
+
+
+def _memo_weight(kind: str, w: np.ndarray, scale: float, fn):
+    """fn(w, scale) for a weight, remembered by the content of w (blake2b) and the scale: a quantized
+    weight is a pure function of both, and the repeated oracle evaluations of one test (exact,
+    fp32-accumulating) then quantize each weight once."""
+    w = np.ascontiguousarray(w, dtype=np.float32)
+    key = (kind, w.shape, float(np.float32(scale)), hashlib.blake2b(w, digest_size=16).digest())
+    hit = _WEIGHT_MEMO.get(key)
+    if hit is None:
+        if len(_WEIGHT_MEMO) >= 16:
+            _WEIGHT_MEMO.clear()
+        hit = fn(w, scale)
+        _WEIGHT_MEMO[key] = hit
+    return hit
+
+
+def cuda_scalar_div(a, b: float) -> np.float32:
+    """fp32 a / Python float b as torch evaluates it on a GPU tensor -- the reference's scales are such
+    divisions of device tensors (torchao's per_tensor_amax_to_scale, amax / (448 * 6); FastFP8Linear's
+    amax / 448, fp8_fast_linear.py:122, 164-168): a times the reciprocal of b rounded to fp32 on the
+    host (aten/src/ATen/native/cuda/BinaryDivTrueKernel.cu, the scalar-divisor case), which differs from
+    the IEEE quotient by one ulp for some a. Pinned against torch's own device division
+    (tests/test_gpu_lowp.py::test_scale_division_is_torchs)."""
+    return np.float32(np.float32(a) * (np.float32(1.0) / np.float32(b)))
+
+
 def fp4_weight_scale(w: np.ndarray) -> np.float32:
-    return Q.per_tensor_amax_to_scale(float(np.abs(np.asarray(w, dtype=np.float32)).max()))
+    """per_tensor_amax_to_scale(amax(|W|)) on the device: amax * fp32(1 / 2688) (fp4_fast_linear.py:129-133)."""
+    return cuda_scalar_div(np.abs(np.asarray(w, dtype=np.float32)).max(), E4M3_MAX * 6.0)
 
 
 def fp4_raw(x: np.ndarray, act_scale: float, w: np.ndarray, w_scale: float) -> np.ndarray:
     """bf16(x_hat . W_hat^T) as fp32 (torch._scaled_mm with NVFP4 operands, out_dtype bf16)."""
-    return round_bf16(_f32(_matmul_exact(nvfp4_xhat(x, act_scale), nvfp4_xhat(w, w_scale))))
+    return round_bf16(_f32(_matmul_exact(nvfp4_xhat(x, act_scale), _memo_weight("fp4", w, w_scale, nvfp4_xhat))))
 
 
 def fp4_out_scale(act_scale: float, w_scale: float) -> np.float32:
@@ -134,7 +165,7 @@ def swiglu_scaled(raw1, s1, b1, raw2, s2, b2) -> np.ndarray:
 def fp8_linear(x: np.ndarray, act_scale: float, w: np.ndarray, w_scale: float, bias: np.ndarray | None) -> np.ndarray:
     """bf16(acc * (act_scale * w_scale) + bias), acc the exact sum of the e4m3 products."""
     inv = round_bf16(np.float32(1.0) / np.float32(act_scale))
-    acc = _matmul_exact(fp8_act(x, inv), fp8_weight(w, w_scale))
+    acc = _matmul_exact(fp8_act(x, inv), _memo_weight("fp8", w, w_scale, fp8_weight))
     alpha = np.float64(np.float32(np.float32(act_scale) * np.float32(w_scale)))
     r = acc * alpha
     if bias is not None:
@@ -143,14 +174,14 @@ def fp8_linear(x: np.ndarray, act_scale: float, w: np.ndarray, w_scale: float, b
 
 
 def fp8_weight_scale(w: np.ndarray) -> np.float32:
-    """max(amax(|W|) / 448, 1e-12) in fp32 (fp8_fast_linear.py:122)."""
-    return np.float32(max(np.float32(np.abs(np.asarray(w, dtype=np.float32)).max()) / np.float32(E4M3_MAX),
+    """max(amax(|W|) / 448, 1e-12) in fp32, the division as on the device (fp8_fast_linear.py:122)."""
+    return np.float32(max(cuda_scalar_div(np.abs(np.asarray(w, dtype=np.float32)).max(), E4M3_MAX),
                           np.float32(1e-12)))
 
 
 def fp8_act_scale(amax_: float) -> np.float32:
-    """max(amax / 448, 1e-12) (fp8_fast_linear.py:164-168)."""
-    return np.float32(max(np.float32(amax_) / np.float32(E4M3_MAX), np.float32(1e-12)))
+    """max(amax / 448, 1e-12), the division as on the device (fp8_fast_linear.py:164-168)."""
+    return np.float32(max(cuda_scalar_div(amax_, E4M3_MAX), np.float32(1e-12)))
 
 
 def linear_out(route, x: torch.Tensor, w: torch.Tensor, b: torch.Tensor | None) -> torch.Tensor:
@@ -182,8 +213,8 @@ def swiglu_mlp(routes: dict, blk: dict, x: torch.Tensor, gamma: torch.Tensor) ->
                   for n in ("w1", "w2", "w3"))
     xh = nvfp4_xhat(xn, sa1)
     ws1, ws2, ws3 = fp4_weight_scale(w1), fp4_weight_scale(w2), fp4_weight_scale(w3)
-    raw1 = round_bf16(_f32(_matmul_exact(xh, nvfp4_xhat(w1, ws1))))
-    raw2 = round_bf16(_f32(_matmul_exact(xh, nvfp4_xhat(w2, ws2))))
+    raw1 = round_bf16(_f32(_matmul_exact(xh, _memo_weight("fp4", w1, ws1, nvfp4_xhat))))
+    raw2 = round_bf16(_f32(_matmul_exact(xh, _memo_weight("fp4", w2, ws2, nvfp4_xhat))))
     sa2 = routes["mlp.w2"][1]
     h = swiglu_scaled(raw1, fp4_out_scale(sa1, ws1), b1, raw2, fp4_out_scale(sa2, ws2), b2)
     raw3 = fp4_raw(h, sa3, w3, ws3)

@@ -388,6 +388,29 @@ def approx_pass(cfg: ViTConfig, blocks: list, x: torch.Tensor, rope, mode: str =
 # ------------------------------------------------------------------------------------------------
 
 
+def qkv_rope_rows(cfg: ViTConfig, blk: dict, xn: torch.Tensor, plan, rope, mode: str = "f64",
+                  lowp: dict | None = None):
+    """q, k, v [M, H, D] of the selected rows from their norm1 output xn [M, C]: the qkv projection
+    (attention.py:415; the low-precision route of `lowp["attn.qkv"]` when given) and RoPE on q and k of
+    patch rows (attention.py:428-438); k and v are what the K/V cache rows receive (bf16 on store)."""
+    ops = _MODES[mode]
+    H, D = cfg.heads, cfg.head_dim
+    M = xn.shape[0]
+    sin, cos = rope
+    if lowp is not None:
+        from . import lowp as LPO
+        qkv = LPO.linear_out(lowp["attn.qkv"], xn, blk["attn.qkv.weight"], blk.get("attn.qkv.bias")).reshape(M, 3, H, D)
+    else:
+        qkv = ops.linear(xn, blk["attn.qkv.weight"], masked_qkv_bias(blk)).reshape(M, 3, H, D)
+    q, k, v = qkv[:, 0], qkv[:, 1], qkv[:, 2]
+    pm = torch.from_numpy(plan.active_patch_mask)
+    ri = torch.from_numpy(plan.active_rope_idx)
+    s_sel, c_sel = sin[ri][:, None], cos[ri][:, None]
+    q = torch.where(pm[:, None, None], rope_rotate(q, s_sel, c_sel), q)
+    k = torch.where(pm[:, None, None], rope_rotate(k, s_sel, c_sel), k)
+    return q, k, v
+
+
 def correct_block(cfg: ViTConfig, blk: dict, x: torch.Tensor, plan, rope, cache: dict, tag: str,
                   mode: str = "f64", inplace_cache: bool = True, lowp: dict | None = None):
     """One partial-token correction block. `plan` is an oracle.plan.Plan (numpy) for this block: its
@@ -406,7 +429,6 @@ def correct_block(cfg: ViTConfig, blk: dict, x: torch.Tensor, plan, rope, cache:
     ops = _MODES[mode]
     B, N, C = x.shape
     H, D = cfg.heads, cfg.head_dim
-    sin, cos = rope
     bi = torch.from_numpy(plan.active_batch_idx)
     ti = torch.from_numpy(plan.active_token_idx)
     M = bi.numel()
@@ -418,17 +440,9 @@ def correct_block(cfg: ViTConfig, blk: dict, x: torch.Tensor, plan, rope, cache:
 
     x_act = x[bi, ti]                                                        # block.py:1111
     xn = ops.ln(x_act, blk["norm1.weight"], blk["norm1.bias"], cfg.ln_eps)   # :1114
+    q, k, v = qkv_rope_rows(cfg, blk, xn, plan, rope, mode, lowp)            # attention.py:415-438
     if lowp is not None:
         from . import lowp as LPO
-        qkv = LPO.linear_out(lowp["attn.qkv"], xn, blk["attn.qkv.weight"], blk.get("attn.qkv.bias")).reshape(M, 3, H, D)
-    else:
-        qkv = ops.linear(xn, blk["attn.qkv.weight"], masked_qkv_bias(blk)).reshape(M, 3, H, D)  # attention.py:415
-    q, k, v = qkv[:, 0], qkv[:, 1], qkv[:, 2]
-    pm = torch.from_numpy(plan.active_patch_mask)
-    ri = torch.from_numpy(plan.active_rope_idx)
-    s_sel, c_sel = sin[ri][:, None], cos[ri][:, None]
-    q = torch.where(pm[:, None, None], rope_rotate(q, s_sel, c_sel), q)    # attention.py:428-438
-    k = torch.where(pm[:, None, None], rope_rotate(k, s_sel, c_sel), k)
     kv[bi, ti, 0] = k                                                        # attention.py:444-454
     kv[bi, ti, 1] = v
     pi = torch.from_numpy(plan.active_pos_idx)

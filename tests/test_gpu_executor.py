@@ -87,6 +87,10 @@ def _check_rope(cfg, ctx):
     ("vits16_224", 1, 12, 0.5, None),
     ("vits16_224", 1, 12, 0.5, 1.0),
     ("vitl16_512", 2, 2, 0.25, 1.0),
+    # The headline's depth and width (all 24 ViT-L blocks, keep 25 %): how rounding differences
+    # compound over the full pass, at the reference init and with every increment at full size.
+    pytest.param("vitl16_512", 2, 24, 0.25, None, marks=pytest.mark.timeout(600)),
+    pytest.param("vitl16_512", 2, 24, 0.25, 1.0, marks=pytest.mark.timeout(600)),
 ])
 def test_executor_mobile_hint_plan(dev, key, B, depth, ratio, gamma):
     print(f"executor mobile-hint {key} B={B} depth={depth} keep={ratio} gamma={gamma}", flush=True)

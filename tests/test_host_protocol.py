@@ -152,20 +152,46 @@ def test_device_pointer_array_lives_with_its_holder():
 
 def test_stream_workspace_keeps_outgrown_buffers(monkeypatch):
     """The per-stream fp32 scratch is reused while it is large enough; when it grows, the old buffer
-    stays allocated (a graph recorded on that stream keeps its address) and the new one at least
-    doubles, so only a few buffers are ever retired."""
+    stays allocated under its stream (a graph recorded on that stream keeps its address) and the new
+    one at least doubles, so only a few buffers are ever retired."""
     from appcorr_amd import _lib
     monkeypatch.setattr(_lib, "stream_of", lambda t: 12345)
     monkeypatch.setattr(K, "_STREAM_WS", {})
-    monkeypatch.setattr(K, "_RETIRED_WS", [])
+    monkeypatch.setattr(K, "_RETIRED_WS", {})
     x = torch.zeros(1)
+    key = (x.device, 12345)
     a = K._stream_workspace(x, 100)
     assert a.numel() == 100 and K._stream_workspace(x, 60) is a
     b = K._stream_workspace(x, 150)
-    assert b is not a and b.numel() == 200 and K._RETIRED_WS == [a]
+    assert b is not a and b.numel() == 200 and K._RETIRED_WS == {key: [a]}
     c = K._stream_workspace(x, 1000)
-    assert c.numel() == 1000 and K._RETIRED_WS[-1] is b
-    assert K._stream_workspace(x, 1000) is c and len(K._RETIRED_WS) == 2
+    assert c.numel() == 1000 and K._RETIRED_WS[key][-1] is b
+    assert K._stream_workspace(x, 1000) is c and len(K._RETIRED_WS[key]) == 2
+
+
+def test_stream_workspaces_are_per_stream_and_taken_by_a_graph(monkeypatch):
+    """Launch sequences on different streams get different scratch buffers; taking a stream's buffers
+    (what graphs.capture does after recording on its own stream) hands over the current one and the
+    ones it outgrew, leaves the other streams' untouched, and the next launch on that stream gets a
+    fresh buffer instead of the one the graph now owns."""
+    from appcorr_amd import _lib
+    cur = {"s": 1}
+    monkeypatch.setattr(_lib, "stream_of", lambda t: cur["s"])
+    monkeypatch.setattr(K, "_STREAM_WS", {})
+    monkeypatch.setattr(K, "_RETIRED_WS", {})
+    x = torch.zeros(1)
+    a1 = K._stream_workspace(x, 10)
+    cur["s"] = 2
+    b1 = K._stream_workspace(x, 10)
+    b2 = K._stream_workspace(x, 50)
+    assert a1 is not b1 and b2 is not b1
+    owned = K.take_stream_workspaces(x.device, 2)
+    assert len(owned) == 2 and owned[0] is b1 and owned[1] is b2
+    assert (x.device, 2) not in K._STREAM_WS and (x.device, 2) not in K._RETIRED_WS
+    assert K._STREAM_WS[(x.device, 1)] is a1
+    b3 = K._stream_workspace(x, 10)
+    assert b3 is not b1 and b3 is not b2 and b3.numel() == 10
+    assert K.take_stream_workspaces(x.device, 99) == []
 
 
 def test_trace_ranges_nest_and_survive_exceptions():

@@ -124,3 +124,28 @@ def test_linear_kernel_name_reports_a_gemm_kernel():
     name = K.linear_kernel_name(4176, 4096, 1024, _lib.EPI_BIAS_GELU)
     assert name.startswith("oudjat::gemm_bf16_") and name.endswith(", 1>"), name
     assert K.linear_kernel_name(64, 64, 64).startswith("oudjat::gemm_bf16_")
+
+
+def test_fp8_gemm_entry_points_reject_bad_arguments():
+    """The native FP8 GEMM: K % 128, N % 256, 16-byte rows, no GELU, all checked before any launch."""
+    A, W, C = ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16)
+    ok = dict(M=4, K=128, lda=128, N=256, ldw=128)
+
+    def lin(epi=0, **kv):
+        a = dict(ok, **kv)
+        return ("oudjat_linear_fp8", A, a["M"], a["K"], a["lda"], W, a["N"], a["ldw"], NULL, epi, NULL, NULL, 0, C,
+                a["N"], 1.0, NULL)
+
+    _expect("OUDJAT_ERR_UNSUPPORTED_SHAPE", *lin(K=192, lda=192))
+    _expect("OUDJAT_ERR_UNSUPPORTED_SHAPE", *lin(N=192))
+    _expect("OUDJAT_ERR_UNSUPPORTED_LAYOUT", *lin(lda=136))
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", *lin(epi=1))   # GELU: not an FP8 route
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", *lin(epi=3))   # LayerScale without gamma
+    _expect("OUDJAT_ERR_UNSUPPORTED_SHAPE", "oudjat_fp8_quantize", ctypes.c_void_p(16), 4, 12, 16,
+            ctypes.c_void_p(16), 0, ctypes.c_void_p(16), 16, NULL)
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_linear_qkv_rope_kv_fp8", A, 4, 128, 128, W, 128, NULL, 2, 64,
+            NULL, NULL, 0, NULL, NULL, NULL, NULL, NULL, 0, 0, NULL, 1.0, NULL)
+    from appcorr_amd import kernels as K
+    assert K.linear_fp8_kernel_name(1656, 12288, 4096, 5) == "oudjat::gemm_bf16_pp_kernel<192, 256, 5, true>"
+    assert K.linear_fp8_kernel_name(1656, 4096, 8192, 3) == "oudjat::gemm_bf16_pp_kernel<128, 256, 3, true>"
+    assert K.fp8_gemm_supported(4096, 12288) and not K.fp8_gemm_supported(384, 1152)
