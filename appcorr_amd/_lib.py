@@ -112,6 +112,12 @@ SIGNATURES: dict[str, list] = {
     "oudjat_nvfp4_quantize_dequantize": [_p, _i64, _i64, _i64, _p, _p, _p, _p, _i64, _p],
     "oudjat_fp8_quantize_dequantize": [_p, _i64, _i64, _i64, _p, _i32, _p, _i64, _p],
     "oudjat_fp8_quantize": [_p, _i64, _i64, _i64, _p, _i32, _p, _i64, _p],
+    "oudjat_layernorm_rows_nvfp4": [_p, _i64, _i64, _i64, _p, _p, _f32, _p, _p, _i64, _p],
+    "oudjat_packed_residual_persist_ln_nvfp4": [_p, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p, _p, _f32,
+                                                _p, _p, _p],
+    "oudjat_swiglu_scaled_nvfp4": [_p, _f32, _p, _p, _f32, _p, _i64, _i64, _p, _p, _p],
+    "oudjat_qkv_rope_kv_scatter_scaled": [_p, _i64, _i64, _i64, _f32, _p, _p, _p, _i64, _p, _p, _p, _p, _p, _i64,
+                                          _i64, _p, _p],
     "oudjat_linear_fp8": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i32, _p, _p, _i64, _p, _i64, _f32, _p],
     "oudjat_linear_qkv_rope_kv_fp8": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p,
                                       _p, _i64, _i64, _p, _f32, _p],

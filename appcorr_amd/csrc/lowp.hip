@@ -11,7 +11,7 @@
 //     file's scale_bias (out = raw * s + b, fp32, one rounding) or, for the SwiGLU pair, the fused
 //     silu(raw1 * s1 + b1) * (raw2 * s2 + b2) epilogue (token_update.py:571-669);
 //   FP8 (scales inside the GEMM): bf16(acc * (sa * sb) + b) by the GEMM's accumulator scale.
-#include "common.hpp"
+#include "nvfp4.hpp"
 
 namespace oudjat {
 namespace {
@@ -115,11 +115,16 @@ __global__ void __launch_bounds__(kLpThreads) scale_bias_kernel(const uint16_t* 
 
 // The SwiGLU pair's fused NVFP4 epilogue (token_update.py:620-631): a = x1 s1 + b1, b = x2 s2 + b2
 // (fp32; contracted with a bias as above), out = bf16((a * sigmoid(a)) * b), sigmoid(a) = 1 / (1 + e^-a).
+// XH: the row written is the NVFP4 operand x_hat (tensor scale *xh_ts) of that bf16 output -- the input
+// of the NVFP4 w3 linear -- as nvfp4_quantize_dequantize gives it; a 16-element block is the chunk
+// pair of threads 2k, 2k + 1 (N % 16 == 0).
+template <bool XH>
 __global__ void __launch_bounds__(kLpThreads) swiglu_scaled_kernel(const uint16_t* __restrict__ x1, float s1,
                                                                    const uint16_t* __restrict__ b1,
                                                                    const uint16_t* __restrict__ x2, float s2,
                                                                    const uint16_t* __restrict__ b2, int64_t M,
-                                                                   int64_t N, uint16_t* __restrict__ out) {
+                                                                   int64_t N, uint16_t* __restrict__ out,
+                                                                   const float* __restrict__ xh_ts) {
   const int64_t chunks = N >> 3;
   const int64_t i = (int64_t)blockIdx.x * kLpThreads + threadIdx.x;
   if (i >= M * chunks) return;
@@ -138,7 +143,14 @@ __global__ void __launch_bounds__(kLpThreads) swiglu_scaled_kernel(const uint16_
     const float silu = av * (1.0f / (1.0f + expf(-av)));
     a[e] = silu * bv;
   }
-  *reinterpret_cast<uint4*>(out + row * N + c) = pack8(a);
+  if constexpr (XH) {
+    float h[8];
+    unpack8(pack8(a), a);  // the bf16 output the quantizer reads
+    nvfp4_xhat8_pair(a, *xh_ts, h);
+    *reinterpret_cast<uint4*>(out + row * N + c) = pack8(h);
+  } else {
+    *reinterpret_cast<uint4*>(out + row * N + c) = pack8(a);
+  }
 }
 
 // amax[0] = max(amax[0], max |x|) over rows [M, K] (the calibration observer's running maximum).
@@ -230,19 +242,37 @@ extern "C" int oudjat_scale_bias_rows(const uint16_t* x, int64_t M, int64_t N, i
   return check_launch("scale_bias_rows");
 }
 
-extern "C" int oudjat_swiglu_scaled(const uint16_t* x1, float s1, const uint16_t* b1, const uint16_t* x2, float s2,
-                                    const uint16_t* b2, int64_t M, int64_t N, uint16_t* out, oudjat_stream_t stream) {
-  int st = launch_rows("swiglu_scaled", M, N);
+static int swiglu_launch(const uint16_t* x1, float s1, const uint16_t* b1, const uint16_t* x2, float s2,
+                         const uint16_t* b2, int64_t M, int64_t N, const float* xh_ts, uint16_t* out,
+                         oudjat_stream_t stream, const char* what) {
+  int st = launch_rows(what, M, N);
   if (st != OUDJAT_OK) return st;
   if (M == 0 || N == 0) return OUDJAT_OK;
   OUDJAT_REQUIRE(x1 && x2 && out && ((b1 == nullptr) == (b2 == nullptr)), OUDJAT_ERR_INVALID_ARGUMENT,
-                 "swiglu_scaled: null pointer (both biases or neither)");
+                 "%s: null pointer (both biases or neither)", what);
   OUDJAT_REQUIRE(aligned(x1, 16) && aligned(x2, 16) && aligned(out, 16) && (!b1 || (aligned(b1, 16) && aligned(b2, 16))),
-                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "swiglu_scaled: 16-byte aligned rows required");
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "%s: 16-byte aligned rows required", what);
   const int64_t n = M * (N / 8);
-  swiglu_scaled_kernel<<<(unsigned)cdiv(n, kLpThreads), kLpThreads, 0, as_stream(stream)>>>(x1, s1, b1, x2, s2, b2, M,
-                                                                                            N, out);
-  return check_launch("swiglu_scaled");
+  const unsigned grid = (unsigned)cdiv(n, kLpThreads);
+  if (xh_ts) {
+    OUDJAT_REQUIRE(N % 16 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE, "%s: NVFP4 output needs N %% 16 == 0", what);
+    swiglu_scaled_kernel<true><<<grid, kLpThreads, 0, as_stream(stream)>>>(x1, s1, b1, x2, s2, b2, M, N, out, xh_ts);
+  } else {
+    swiglu_scaled_kernel<false><<<grid, kLpThreads, 0, as_stream(stream)>>>(x1, s1, b1, x2, s2, b2, M, N, out, nullptr);
+  }
+  return check_launch(what);
+}
+
+extern "C" int oudjat_swiglu_scaled(const uint16_t* x1, float s1, const uint16_t* b1, const uint16_t* x2, float s2,
+                                    const uint16_t* b2, int64_t M, int64_t N, uint16_t* out, oudjat_stream_t stream) {
+  return swiglu_launch(x1, s1, b1, x2, s2, b2, M, N, nullptr, out, stream, "swiglu_scaled");
+}
+
+extern "C" int oudjat_swiglu_scaled_nvfp4(const uint16_t* x1, float s1, const uint16_t* b1, const uint16_t* x2,
+                                          float s2, const uint16_t* b2, int64_t M, int64_t N,
+                                          const float* tensor_scale, uint16_t* xhat, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(tensor_scale || M == 0 || N == 0, OUDJAT_ERR_INVALID_ARGUMENT, "swiglu_scaled_nvfp4: null tensor scale");
+  return swiglu_launch(x1, s1, b1, x2, s2, b2, M, N, tensor_scale, xhat, stream, "swiglu_scaled_nvfp4");
 }
 
 extern "C" int oudjat_amax_update(const uint16_t* x, int64_t M, int64_t K, int64_t stride_m, float* amax,

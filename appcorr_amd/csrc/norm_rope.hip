@@ -1,6 +1,6 @@
 // LayerNorm over selected rows, rotate-half RoPE on the active rows, and the fused post-QKV step
 // (RoPE + in-place K/V cache rewrite + packed query write).
-#include "common.hpp"
+#include "nvfp4.hpp"
 
 namespace oudjat {
 
@@ -10,10 +10,15 @@ static constexpr int kNormRowsPerWg = kNormThreads / 64;
 // LayerNorm of one row held by one wave: lane l holds chunks l + 64 j (j < CH, 8 values each, as
 // fp32 from bf16). Statistics are fp32: mean, then the biased variance around it. Shared by the
 // standalone kernel and the fused residual kernel so both give the same bits.
+// xh_ts (NULL: plain LayerNorm): the row written is instead the NVFP4 operand x_hat of the bf16
+// LayerNorm output with tensor scale *xh_ts -- what nvfp4_quantize_dequantize gives on the output
+// (a 16-element block is the chunk pair of lanes l, l ^ 1). The LayerNorm values themselves are the
+// same either way.
 template <int CH>
 __device__ __forceinline__ void layernorm_row(const float (&v)[CH][8], int lane, int chunks, int C,
                                               const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
-                                              float eps, uint16_t* __restrict__ out_row) {
+                                              float eps, uint16_t* __restrict__ out_row,
+                                              const float* __restrict__ xh_ts = nullptr) {
   float sum = 0.0f;
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
@@ -41,17 +46,37 @@ __device__ __forceinline__ void layernorm_row(const float (&v)[CH][8], int lane,
   const uint4* wv = reinterpret_cast<const uint4*>(w);
   const uint4* bv = reinterpret_cast<const uint4*>(bias);
   uint4* ov = reinterpret_cast<uint4*>(out_row);
+  if (xh_ts == nullptr) {
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = lane + 64 * j;
+      if (c < chunks) {
+        float fw[8], fb[8], y[8];
+        unpack8(wv[c], fw);
+        unpack8(bv[c], fb);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) y[e] = fmaf(fw[e], (v[j][e] - mean) * rstd, fb[e]);
+        ov[c] = pack8(y);
+      }
+    }
+    return;
+  }
+  const float ts = *xh_ts;
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
     const int c = lane + 64 * j;
+    float y[8] = {0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f, 0.0f};
     if (c < chunks) {
-      float fw[8], fb[8], y[8];
+      float fw[8], fb[8];
       unpack8(wv[c], fw);
       unpack8(bv[c], fb);
 #pragma unroll
       for (int e = 0; e < 8; ++e) y[e] = fmaf(fw[e], (v[j][e] - mean) * rstd, fb[e]);
-      ov[c] = pack8(y);
+      unpack8(pack8(y), y);  // the bf16 LayerNorm output the quantizer reads
     }
+    float h[8];
+    nvfp4_xhat8_pair(y, ts, h);  // every lane takes part (the block maximum is a lane-pair exchange)
+    if (c < chunks) ov[c] = pack8(h);
   }
 }
 
@@ -61,7 +86,8 @@ template <int CH>
 __global__ __launch_bounds__(kNormThreads) void layernorm_kernel(const uint16_t* __restrict__ x, int64_t rows, int C,
                                                                int64_t xs, const uint16_t* __restrict__ w,
                                                                const uint16_t* __restrict__ bias, float eps,
-                                                               uint16_t* __restrict__ out, int64_t os) {
+                                                               uint16_t* __restrict__ out, int64_t os,
+                                                               const float* __restrict__ xh_ts) {
   const int64_t row = (int64_t)blockIdx.x * kNormRowsPerWg + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
@@ -73,7 +99,7 @@ __global__ __launch_bounds__(kNormThreads) void layernorm_kernel(const uint16_t*
     const int c = lane + 64 * j;
     if (c < chunks) unpack8(xv[c], v[j]);
   }
-  layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, out + row * os);
+  layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, out + row * os, xh_ts);
 }
 
 // The residual step of a correction block on packed selected rows fused with the next block's
@@ -84,7 +110,7 @@ __global__ __launch_bounds__(kNormThreads) void packed_residual_ln_kernel(
     const uint16_t* __restrict__ xa, const uint16_t* __restrict__ xt, const uint16_t* __restrict__ mlp, int64_t rows,
     int C, const int64_t* __restrict__ bi, const int64_t* __restrict__ ti, uint16_t* __restrict__ bos, int64_t bsb,
     int64_t bsn, uint16_t* __restrict__ xn, const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
-    float eps, uint16_t* __restrict__ ln_out) {
+    float eps, uint16_t* __restrict__ ln_out, const float* __restrict__ xh_ts) {
   const int64_t row = (int64_t)blockIdx.x * kNormRowsPerWg + (threadIdx.x >> 6);
   if (row >= rows) return;
   const int lane = threadIdx.x & 63;
@@ -114,7 +140,7 @@ __global__ __launch_bounds__(kNormThreads) void packed_residual_ln_kernel(
       unpack8(o, v[j]);
     }
   }
-  layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, ln_out + row * C);
+  layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, ln_out + row * C, xh_ts);
 }
 
 // The split-K reduce of a LayerScale projection (fc2 / w3) fused with the packed residual step and
@@ -216,11 +242,15 @@ __global__ __launch_bounds__(256) void rope_active_inplace_kernel(
 
 // Post-QKV step: qkv [M, 3, H, Dh] -> RoPE(q), RoPE(k) on patch rows; q -> q_out [M, H, Dh];
 // k, v -> kv[b, t, 0 | 1, h, :] (the [2, H, Dh] part of a cache row is contiguous).
+// SCALED: qkv holds the raw product of an NVFP4 qkv linear, and every value is first taken through its
+// scale-and-bias epilogue, bf16(raw * s + bias[col]) (bf16(raw * s) without a bias), exactly as
+// scale_bias_kernel writes it; RoPE and the writes then proceed on those values.
+template <bool SCALED>
 __global__ __launch_bounds__(256) void qkv_rope_kv_scatter_kernel(
     const uint16_t* __restrict__ qkv, int64_t M, int H, int Dh, const float* __restrict__ sin_t,
     const float* __restrict__ cos_t, int64_t tst, const uint8_t* __restrict__ pm, const int64_t* __restrict__ ridx,
     const int64_t* __restrict__ bi, const int64_t* __restrict__ ti, uint16_t* __restrict__ kv, int64_t kvb,
-    int64_t kvn, uint16_t* __restrict__ qo) {
+    int64_t kvn, uint16_t* __restrict__ qo, float sc, const uint16_t* __restrict__ sbias) {
   const int half = Dh >> 1;
   const int cph = half >> 3;
   const int64_t gid = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
@@ -237,8 +267,30 @@ __global__ __launch_bounds__(256) void qkv_rope_kv_scatter_kernel(
   uint4 q_r = *reinterpret_cast<const uint4*>(src + d0 + half);
   uint4 k_l = *reinterpret_cast<const uint4*>(src + HD + d0);
   uint4 k_r = *reinterpret_cast<const uint4*>(src + HD + d0 + half);
-  const uint4 v_l = *reinterpret_cast<const uint4*>(src + 2 * HD + d0);
-  const uint4 v_r = *reinterpret_cast<const uint4*>(src + 2 * HD + d0 + half);
+  uint4 v_l = *reinterpret_cast<const uint4*>(src + 2 * HD + d0);
+  uint4 v_r = *reinterpret_cast<const uint4*>(src + 2 * HD + d0 + half);
+  if constexpr (SCALED) {
+    auto sb8 = [&](uint4 u, int64_t col) __attribute__((always_inline)) {
+      float f[8], b[8];
+      unpack8(u, f);
+      if (sbias) {
+        unpack8(*reinterpret_cast<const uint4*>(sbias + col), b);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = __builtin_fmaf(f[e], sc, b[e]);
+      } else {
+#pragma unroll
+        for (int e = 0; e < 8; ++e) f[e] = f[e] * sc;
+      }
+      return pack8(f);
+    };
+    const int64_t c0 = (int64_t)h * Dh + d0;
+    q_l = sb8(q_l, c0);
+    q_r = sb8(q_r, c0 + half);
+    k_l = sb8(k_l, HD + c0);
+    k_r = sb8(k_r, HD + c0 + half);
+    v_l = sb8(v_l, 2 * HD + c0);
+    v_r = sb8(v_r, 2 * HD + c0 + half);
+  }
   if (pm[row]) {
     const int64_t tr = ridx[row];
     float cl[8], cr[8], sl[8], sr[8];
@@ -272,23 +324,37 @@ __global__ __launch_bounds__(256) void qkv_rope_kv_scatter_kernel(
 
 using namespace oudjat;
 
-extern "C" int oudjat_layernorm_rows(const uint16_t* x, int64_t rows, int64_t C, int64_t xs, const uint16_t* w,
-                                     const uint16_t* b, float eps, uint16_t* out, int64_t os, oudjat_stream_t stream) {
-  OUDJAT_REQUIRE(rows >= 0 && C > 0, OUDJAT_ERR_INVALID_ARGUMENT, "layernorm_rows: bad size");
+static int layernorm_launch(const uint16_t* x, int64_t rows, int64_t C, int64_t xs, const uint16_t* w,
+                            const uint16_t* b, float eps, const float* xh_ts, uint16_t* out, int64_t os,
+                            oudjat_stream_t stream, const char* what) {
+  OUDJAT_REQUIRE(rows >= 0 && C > 0, OUDJAT_ERR_INVALID_ARGUMENT, "%s: bad size", what);
   if (rows == 0) return OUDJAT_OK;
-  OUDJAT_REQUIRE(x && w && b && out, OUDJAT_ERR_INVALID_ARGUMENT, "layernorm_rows: null pointer");
+  OUDJAT_REQUIRE(x && w && b && out, OUDJAT_ERR_INVALID_ARGUMENT, "%s: null pointer", what);
   OUDJAT_REQUIRE(C % 8 == 0 && xs % 8 == 0 && os % 8 == 0 && aligned(x, 16) && aligned(out, 16) && aligned(w, 16) &&
                      aligned(b, 16),
-                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "layernorm_rows: 16-byte aligned rows with C %% 8 == 0 required");
-  OUDJAT_REQUIRE(C <= 8192, OUDJAT_ERR_TOO_LARGE, "layernorm_rows: C=%lld > 8192", (long long)C);
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "%s: 16-byte aligned rows with C %% 8 == 0 required", what);
+  OUDJAT_REQUIRE(!xh_ts || C % 16 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE, "%s: NVFP4 output needs C %% 16 == 0", what);
+  OUDJAT_REQUIRE(C <= 8192, OUDJAT_ERR_TOO_LARGE, "%s: C=%lld > 8192", what, (long long)C);
   const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg);
   hipStream_t st = as_stream(stream);
-  if (C <= 512) layernorm_kernel<1><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os);
-  else if (C <= 1024) layernorm_kernel<2><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os);
-  else if (C <= 2048) layernorm_kernel<4><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os);
-  else if (C <= 4096) layernorm_kernel<8><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os);
-  else layernorm_kernel<16><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os);
-  return check_launch("layernorm_rows");
+  if (C <= 512) layernorm_kernel<1><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os, xh_ts);
+  else if (C <= 1024) layernorm_kernel<2><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os, xh_ts);
+  else if (C <= 2048) layernorm_kernel<4><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os, xh_ts);
+  else if (C <= 4096) layernorm_kernel<8><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os, xh_ts);
+  else layernorm_kernel<16><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os, xh_ts);
+  return check_launch(what);
+}
+
+extern "C" int oudjat_layernorm_rows(const uint16_t* x, int64_t rows, int64_t C, int64_t xs, const uint16_t* w,
+                                     const uint16_t* b, float eps, uint16_t* out, int64_t os, oudjat_stream_t stream) {
+  return layernorm_launch(x, rows, C, xs, w, b, eps, nullptr, out, os, stream, "layernorm_rows");
+}
+
+extern "C" int oudjat_layernorm_rows_nvfp4(const uint16_t* x, int64_t rows, int64_t C, int64_t xs, const uint16_t* w,
+                                           const uint16_t* b, float eps, const float* tensor_scale, uint16_t* xhat,
+                                           int64_t xhat_stride, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(tensor_scale || rows == 0, OUDJAT_ERR_INVALID_ARGUMENT, "layernorm_rows_nvfp4: null tensor scale");
+  return layernorm_launch(x, rows, C, xs, w, b, eps, tensor_scale, xhat, xhat_stride, stream, "layernorm_rows_nvfp4");
 }
 
 extern "C" int oudjat_rope_active_inplace(uint16_t* q, int64_t qst, int64_t qsh, uint16_t* k, int64_t kst, int64_t ksh,
@@ -309,23 +375,79 @@ extern "C" int oudjat_rope_active_inplace(uint16_t* q, int64_t qst, int64_t qsh,
   return check_launch("rope_active_inplace");
 }
 
+static int qkv_rope_kv_scatter_launch(const uint16_t* qkv, int64_t M, int64_t H, int64_t Dh, const float* sin_t,
+                                      const float* cos_t, int64_t tst, const uint8_t* pm, const int64_t* ridx,
+                                      const int64_t* bi, const int64_t* ti, uint16_t* kv, int64_t kvb, int64_t kvn,
+                                      uint16_t* qo, bool scaled, float sc, const uint16_t* sbias,
+                                      oudjat_stream_t stream, const char* what) {
+  OUDJAT_REQUIRE(M >= 0 && H > 0 && Dh > 0, OUDJAT_ERR_INVALID_ARGUMENT, "%s: bad size", what);
+  if (M == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(qkv && sin_t && cos_t && pm && ridx && bi && ti && kv && qo, OUDJAT_ERR_INVALID_ARGUMENT,
+                 "%s: null pointer", what);
+  OUDJAT_REQUIRE(Dh % 16 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE, "%s: Dh=%lld must be a multiple of 16", what,
+                 (long long)Dh);
+  OUDJAT_REQUIRE(kvb % 8 == 0 && kvn % 8 == 0 && tst % 8 == 0 && aligned(qkv, 16) && aligned(kv, 16) &&
+                     aligned(qo, 16) && aligned(sin_t, 16) && aligned(cos_t, 16) && (!sbias || aligned(sbias, 16)),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "%s: 16-byte aligned rows required", what);
+  const int64_t threads = M * H * (Dh / 16);
+  const unsigned grid = (unsigned)cdiv(threads, 256);
+  if (scaled)
+    qkv_rope_kv_scatter_kernel<true><<<grid, 256, 0, as_stream(stream)>>>(qkv, M, (int)H, (int)Dh, sin_t, cos_t, tst,
+                                                                           pm, ridx, bi, ti, kv, kvb, kvn, qo, sc,
+                                                                           sbias);
+  else
+    qkv_rope_kv_scatter_kernel<false><<<grid, 256, 0, as_stream(stream)>>>(qkv, M, (int)H, (int)Dh, sin_t, cos_t, tst,
+                                                                            pm, ridx, bi, ti, kv, kvb, kvn, qo, 1.0f,
+                                                                            nullptr);
+  return check_launch(what);
+}
+
 extern "C" int oudjat_qkv_rope_kv_scatter(const uint16_t* qkv, int64_t M, int64_t H, int64_t Dh, const float* sin_t,
                                           const float* cos_t, int64_t tst, const uint8_t* pm, const int64_t* ridx,
                                           const int64_t* bi, const int64_t* ti, uint16_t* kv, int64_t kvb,
                                           int64_t kvn, uint16_t* qo, oudjat_stream_t stream) {
-  OUDJAT_REQUIRE(M >= 0 && H > 0 && Dh > 0, OUDJAT_ERR_INVALID_ARGUMENT, "qkv_rope_kv_scatter: bad size");
-  if (M == 0) return OUDJAT_OK;
-  OUDJAT_REQUIRE(qkv && sin_t && cos_t && pm && ridx && bi && ti && kv && qo, OUDJAT_ERR_INVALID_ARGUMENT,
-                 "qkv_rope_kv_scatter: null pointer");
-  OUDJAT_REQUIRE(Dh % 16 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE, "qkv_rope_kv_scatter: Dh=%lld must be a multiple of 16",
-                 (long long)Dh);
-  OUDJAT_REQUIRE(kvb % 8 == 0 && kvn % 8 == 0 && tst % 8 == 0 && aligned(qkv, 16) && aligned(kv, 16) &&
-                     aligned(qo, 16) && aligned(sin_t, 16) && aligned(cos_t, 16),
-                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "qkv_rope_kv_scatter: 16-byte aligned rows required");
-  const int64_t threads = M * H * (Dh / 16);
-  qkv_rope_kv_scatter_kernel<<<(unsigned)cdiv(threads, 256), 256, 0, as_stream(stream)>>>(
-      qkv, M, (int)H, (int)Dh, sin_t, cos_t, tst, pm, ridx, bi, ti, kv, kvb, kvn, qo);
-  return check_launch("qkv_rope_kv_scatter");
+  return qkv_rope_kv_scatter_launch(qkv, M, H, Dh, sin_t, cos_t, tst, pm, ridx, bi, ti, kv, kvb, kvn, qo, false, 1.0f,
+                                    nullptr, stream, "qkv_rope_kv_scatter");
+}
+
+extern "C" int oudjat_qkv_rope_kv_scatter_scaled(const uint16_t* qkv_raw, int64_t M, int64_t H, int64_t Dh,
+                                                 float scale, const uint16_t* bias, const float* sin_t,
+                                                 const float* cos_t, int64_t tst, const uint8_t* pm,
+                                                 const int64_t* ridx, const int64_t* bi, const int64_t* ti,
+                                                 uint16_t* kv, int64_t kvb, int64_t kvn, uint16_t* qo,
+                                                 oudjat_stream_t stream) {
+  return qkv_rope_kv_scatter_launch(qkv_raw, M, H, Dh, sin_t, cos_t, tst, pm, ridx, bi, ti, kv, kvb, kvn, qo, true,
+                                    scale, bias, stream, "qkv_rope_kv_scatter_scaled");
+}
+
+static int packed_residual_ln_launch(const uint16_t* x_act, const uint16_t* x_attn, const uint16_t* mlp,
+                                     int64_t rows, int64_t C, const int64_t* batch_idx, const int64_t* token_idx,
+                                     uint16_t* bos, int64_t bos_stride_b, int64_t bos_stride_n, uint16_t* x_new,
+                                     const uint16_t* ln_w, const uint16_t* ln_b, float eps, const float* xh_ts,
+                                     uint16_t* ln_out, oudjat_stream_t stream, const char* what) {
+  OUDJAT_REQUIRE(rows >= 0 && C > 0, OUDJAT_ERR_INVALID_ARGUMENT, "%s: bad size", what);
+  if (rows == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(x_act && x_attn && mlp && batch_idx && token_idx && bos && x_new && ln_w && ln_b && ln_out,
+                 OUDJAT_ERR_INVALID_ARGUMENT, "%s: null pointer", what);
+  OUDJAT_REQUIRE(C % 8 == 0 && aligned(x_act, 16) && aligned(x_attn, 16) && aligned(mlp, 16) && aligned(bos, 16) &&
+                     aligned(x_new, 16) && aligned(ln_w, 16) && aligned(ln_b, 16) && aligned(ln_out, 16) &&
+                     bos_stride_b % 8 == 0 && bos_stride_n % 8 == 0,
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "%s: 16-byte aligned rows, C %% 8 == 0", what);
+  OUDJAT_REQUIRE(!xh_ts || C % 16 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE, "%s: NVFP4 output needs C %% 16 == 0", what);
+  OUDJAT_REQUIRE(C <= 8192, OUDJAT_ERR_TOO_LARGE, "%s: C=%lld > 8192", what, (long long)C);
+  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg);
+  hipStream_t st = as_stream(stream);
+#define OUDJAT_PRLN(CHV)                                                                                        \
+  packed_residual_ln_kernel<CHV><<<grid, kNormThreads, 0, st>>>(x_act, x_attn, mlp, rows, (int)C, batch_idx,     \
+                                                                token_idx, bos, bos_stride_b, bos_stride_n, x_new, \
+                                                                ln_w, ln_b, eps, ln_out, xh_ts)
+  if (C <= 512) OUDJAT_PRLN(1);
+  else if (C <= 1024) OUDJAT_PRLN(2);
+  else if (C <= 2048) OUDJAT_PRLN(4);
+  else if (C <= 4096) OUDJAT_PRLN(8);
+  else OUDJAT_PRLN(16);
+#undef OUDJAT_PRLN
+  return check_launch(what);
 }
 
 extern "C" int oudjat_packed_residual_persist_ln(const uint16_t* x_act, const uint16_t* x_attn, const uint16_t* mlp,
@@ -334,28 +456,22 @@ extern "C" int oudjat_packed_residual_persist_ln(const uint16_t* x_act, const ui
                                                  int64_t bos_stride_n, uint16_t* x_new, const uint16_t* ln_w,
                                                  const uint16_t* ln_b, float eps, uint16_t* ln_out,
                                                  oudjat_stream_t stream) {
-  OUDJAT_REQUIRE(rows >= 0 && C > 0, OUDJAT_ERR_INVALID_ARGUMENT, "packed_residual_persist_ln: bad size");
-  if (rows == 0) return OUDJAT_OK;
-  OUDJAT_REQUIRE(x_act && x_attn && mlp && batch_idx && token_idx && bos && x_new && ln_w && ln_b && ln_out,
-                 OUDJAT_ERR_INVALID_ARGUMENT, "packed_residual_persist_ln: null pointer");
-  OUDJAT_REQUIRE(C % 8 == 0 && aligned(x_act, 16) && aligned(x_attn, 16) && aligned(mlp, 16) && aligned(bos, 16) &&
-                     aligned(x_new, 16) && aligned(ln_w, 16) && aligned(ln_b, 16) && aligned(ln_out, 16) &&
-                     bos_stride_b % 8 == 0 && bos_stride_n % 8 == 0,
-                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "packed_residual_persist_ln: 16-byte aligned rows, C %% 8 == 0");
-  OUDJAT_REQUIRE(C <= 8192, OUDJAT_ERR_TOO_LARGE, "packed_residual_persist_ln: C=%lld > 8192", (long long)C);
-  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg);
-  hipStream_t st = as_stream(stream);
-#define OUDJAT_PRLN(CHV)                                                                                        \
-  packed_residual_ln_kernel<CHV><<<grid, kNormThreads, 0, st>>>(x_act, x_attn, mlp, rows, (int)C, batch_idx,     \
-                                                                token_idx, bos, bos_stride_b, bos_stride_n, x_new, \
-                                                                ln_w, ln_b, eps, ln_out)
-  if (C <= 512) OUDJAT_PRLN(1);
-  else if (C <= 1024) OUDJAT_PRLN(2);
-  else if (C <= 2048) OUDJAT_PRLN(4);
-  else if (C <= 4096) OUDJAT_PRLN(8);
-  else OUDJAT_PRLN(16);
-#undef OUDJAT_PRLN
-  return check_launch("packed_residual_persist_ln");
+  return packed_residual_ln_launch(x_act, x_attn, mlp, rows, C, batch_idx, token_idx, bos, bos_stride_b, bos_stride_n,
+                                   x_new, ln_w, ln_b, eps, nullptr, ln_out, stream, "packed_residual_persist_ln");
+}
+
+extern "C" int oudjat_packed_residual_persist_ln_nvfp4(const uint16_t* x_act, const uint16_t* x_attn,
+                                                       const uint16_t* mlp, int64_t rows, int64_t C,
+                                                       const int64_t* batch_idx, const int64_t* token_idx,
+                                                       uint16_t* bos, int64_t bos_stride_b, int64_t bos_stride_n,
+                                                       uint16_t* x_new, const uint16_t* ln_w, const uint16_t* ln_b,
+                                                       float eps, const float* tensor_scale, uint16_t* xhat,
+                                                       oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(tensor_scale || rows == 0, OUDJAT_ERR_INVALID_ARGUMENT,
+                 "packed_residual_persist_ln_nvfp4: null tensor scale");
+  return packed_residual_ln_launch(x_act, x_attn, mlp, rows, C, batch_idx, token_idx, bos, bos_stride_b, bos_stride_n,
+                                   x_new, ln_w, ln_b, eps, tensor_scale, xhat, stream,
+                                   "packed_residual_persist_ln_nvfp4");
 }
 
 extern "C" int oudjat_splitk_ls_packed_residual(const float* partials, int64_t slices, const uint16_t* fc_bias,

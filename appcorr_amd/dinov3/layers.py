@@ -52,6 +52,12 @@ def _linear_route(mod: nn.Module, x: Tensor, site: str, *, bias: Tensor | None =
     return K.linear(x, mod.weight, b, site=site, **kw)
 
 
+def _fp4_scale(mod: nn.Module) -> Tensor | None:
+    """The NVFP4 activation scale of a frozen FastFP4Linear (its input's producer then writes the NVFP4
+    operand x_hat directly), else None."""
+    return mod.act_scale if LP.low_precision_state(mod) == "fp4" else None
+
+
 def _fp4_raw(mod: "LP.FastFP4Linear", x: Tensor, site: str):
     """A frozen FastFP4Linear's torch._scaled_mm output bf16(x_hat . W_hat^T) with the factors of its
     epilogue: (raw, out_scale, bias) (fp4_fast_linear.py:221-249)."""
@@ -195,7 +201,10 @@ class SelfAttention(nn.Module):
             out = _linear_route(self.proj, attn, "proj")
         return out, cache_feature
 
-    def _qkv_attention(self, xn: Tensor, rope, kv: Tensor, qs: PackedQueryState):
+    def _qkv_attention(self, xn: Tensor, rope, kv: Tensor, qs: PackedQueryState, xn_is_xhat: bool = False):
+        """q, K/V rows and the attention output of the packed rows from their norm1 output xn -- for a
+        frozen NVFP4 qkv linear, xn may already be its NVFP4 operand x_hat (xn_is_xhat: the producer wrote
+        it)."""
         M, C = xn.shape
         H, D = self.num_heads, self.head_dim
         B = kv.shape[0]
@@ -206,9 +215,13 @@ class SelfAttention(nn.Module):
         mod = self.qkv
         state = LP.low_precision_state(mod)
         if state == "fp4":
-            # NVFP4: raw GEMM output, then scale and bias (fp4_fast_linear.py:251-283), then RoPE / K-V
-            raw, s, b = _fp4_raw(mod, xn, "qkv")
-            qkv = K.scale_bias(raw, s, b, out=raw)
+            # NVFP4: raw GEMM output (fp4_fast_linear.py:221-249), then its scale and bias
+            # (fp4_fast_linear.py:251-283) applied on the way into RoPE and the K/V write (one kernel)
+            xh = xn if xn_is_xhat else mod.quantize(xn)
+            raw = K.linear(xh, mod.weight_hat, None, site="qkv")
+            K.qkv_rope_kv_scatter(raw.view(M, 3, H, D), rope, qs.active_patch_mask, qs.active_rope_idx,
+                                  qs.active_batch_idx, qs.active_token_idx, kv, q, scale=mod.out_scale_f, bias=mod.bias)
+            qkv = None
         elif state == "fp8" and mod.native and K.qkv_fusable(H, D):
             K.linear_qkv_rope_kv_fp8(mod.quantize_codes(xn), mod.weight_q, self.qkv_bias(), rope, qs.active_patch_mask,
                                      qs.active_rope_idx, qs.active_batch_idx, qs.active_token_idx, kv, q,
@@ -282,9 +295,11 @@ class SelfAttentionBlock(nn.Module):
             self._ones = torch.ones(like.shape[-1], device=like.device, dtype=torch.bfloat16)
         return self._ones
 
-    def _mlp_scaled(self, xn: Tensor) -> Tensor:
+    def _mlp_scaled(self, xn: Tensor, xn_is_xhat: bool = False) -> Tensor:
         """gamma2 * MLP(xn) with GELU / SwiGLU and LayerScale fused into the GEMM epilogues; the SwiGLU
-        linears in their low-precision route when the block is a converted view (dinov3/lowp.py)."""
+        linears in their low-precision route when the block is a converted view (dinov3/lowp.py). With
+        NVFP4 linears xn may already be w1's NVFP4 operand x_hat (xn_is_xhat), and the SwiGLU kernel
+        writes w3's x_hat directly."""
         g2 = self._gamma(self.ls2, xn)
         if isinstance(self.mlp, Mlp):
             h = K.linear(xn, self.mlp.fc1.weight, self.mlp.fc1.bias, epilogue=_lib.EPI_BIAS_GELU, site="fc1")
@@ -296,11 +311,13 @@ class SelfAttentionBlock(nn.Module):
                 raise RuntimeError("SwiGLU linears partially calibrated: freeze all three NVFP4 linears together")
             # ffn_layers.py:84-115 with FastFP4Linear: both epilogues folded into the SwiGLU kernel
             # (token_update.py:620-669), then w3 with its scale-and-bias and the LayerScale.
-            r1, s1, b1 = _fp4_raw(w1, xn, "w1")
-            r2, s2, b2 = _fp4_raw(w2, xn, "w2")
-            h = K.swiglu_scaled(r1, s1, b1, r2, s2, b2)
-            r3, s3, b3 = _fp4_raw(w3, h, "w3")
-            return K.scale_bias(r3, s3, b3, gamma=g2, out=r3)
+            # (w2 takes the activation w1 quantized: SharedFP4Activation, fp4_fast_linear.py:71-100)
+            xh = xn if xn_is_xhat else w1.quantize(xn)
+            r1 = K.linear(xh, w1.weight_hat, None, site="w1")
+            r2 = K.linear(xh, w2.weight_hat, None, site="w2")
+            xh3 = K.swiglu_scaled(r1, w1.out_scale_f, w1.bias, r2, w2.out_scale_f, w2.bias, nvfp4_scale=w3.act_scale)
+            r3 = K.linear(xh3, w3.weight_hat, None, site="w3")
+            return K.scale_bias(r3, w3.out_scale_f, w3.bias, gamma=g2, out=r3)
         x2 = _linear_route(w2, xn, "w2")
         h = _linear_route(w1, xn, "w1", epilogue=_lib.EPI_BIAS_SILU_MUL, resid=x2)
         return _linear_route(w3, h, "w3", epilogue=_lib.EPI_BIAS_LS, gamma=g2)
@@ -641,7 +658,7 @@ class SelfAttentionBlock(nn.Module):
         return plan, key, kv, bos
 
     def _correct_rows(self, x_act: Tensor, rope, kv: Tensor, qs: PackedQueryState, xn: Tensor | None = None,
-                      residual=None):
+                      residual=None, xn_is_xhat: bool = False):
         """The block's arithmetic on the packed selected rows (block.py:1111-1141): returns
         (x_attn, mlp); the K/V cache rows of the selected tokens are rewritten in place. `xn`, when
         given, is norm1(x_act) already computed (by the previous block's fused residual step).
@@ -649,9 +666,11 @@ class SelfAttentionBlock(nn.Module):
         its reduce runs fused with the packed residual step, and the second value returned is then
         (x_new, norm1(x_new) or None) instead of mlp (see _mlp_scaled_residual)."""
         with trace_range("correct_attn"):
-            if xn is None:
-                xn = K.layer_norm(x_act, self.norm1.weight, self.norm1.bias, self.norm1.eps)   # block.py:1114
-            _, attn = self.attn._qkv_attention(xn, rope, kv, qs)                         # attention.py:415-523
+            if xn is None:   # block.py:1114 (an NVFP4 qkv linear's x_hat, written by the LayerNorm itself)
+                ts1 = _fp4_scale(self.attn.qkv)
+                xn = K.layer_norm(x_act, self.norm1.weight, self.norm1.bias, self.norm1.eps, nvfp4_scale=ts1)
+                xn_is_xhat = ts1 is not None
+            _, attn = self.attn._qkv_attention(xn, rope, kv, qs, xn_is_xhat)           # attention.py:415-523
             g1 = self._gamma(self.ls1, x_act)
             proj = self.attn.proj
             if LP.low_precision_state(proj) == "fp4":                                    # proj_precision "fp4"
@@ -660,12 +679,13 @@ class SelfAttentionBlock(nn.Module):
                 x_attn = _linear_route(proj, attn, "proj", epilogue=_lib.EPI_BIAS_LS_RESID,  # attention.py:532 +
                                        gamma=g1, resid=x_act)                             # block.py:1129-1134
         with trace_range("correct_ffn"):
-            xn2 = K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps)  # :1141
-            if residual is not None:
+            ts2 = None if isinstance(self.mlp, Mlp) else _fp4_scale(self.mlp.w1)
+            xn2 = K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps, nvfp4_scale=ts2)  # :1141
+            if residual is not None and ts2 is None:
                 fused = self._mlp_scaled_residual(xn2, x_act, x_attn, qs, *residual)
                 if fused is not None:
                     return x_attn, fused
-            mlp = self._mlp_scaled(xn2)
+            mlp = self._mlp_scaled(xn2, xn_is_xhat=ts2 is not None)
         return x_attn, mlp
 
     def _mlp_scaled_residual(self, xn: Tensor, x_act: Tensor, x_attn: Tensor, qs: PackedQueryState, bos: Tensor,
@@ -765,6 +785,7 @@ def correct_blocks_packed(blocks, x: Tensor, dindice: Tensor, rope, cache_featur
     x_p = K.gather_rows(xc, qs.active_batch_idx, qs.active_token_idx) if M else xc.new_empty((0, xc.shape[-1]))
     bos_list = []
     xn = None  # norm1 of the next block on x_p, from the fused residual + LayerNorm step
+    xn_is_xhat = False  # ... written as the next block's NVFP4 qkv operand
     for i, (blk, tag) in enumerate(zip(blocks, tags)):
         if i == 0:
             plan, kv, bos = plan0, cache_feature[f"{tag}_kv"], cache_feature[f"{tag}_blocks_out_sum"]
@@ -773,14 +794,17 @@ def correct_blocks_packed(blocks, x: Tensor, dindice: Tensor, rope, cache_featur
         if plan is not plan0:
             raise RuntimeError("blocks of one packed run resolved different query plans")
         if x_p.shape[0] > 0:
-            nxt = blocks[i + 1].norm1 if i + 1 < len(blocks) else None
-            x_attn, mlp = blk._correct_rows(x_p, rope, kv, qs, xn=xn, residual=(bos, nxt))
+            ts_next = _fp4_scale(blocks[i + 1].attn.qkv) if i + 1 < len(blocks) else None
+            nxt = blocks[i + 1].norm1 if i + 1 < len(blocks) and ts_next is None else None
+            x_attn, mlp = blk._correct_rows(x_p, rope, kv, qs, xn=xn, residual=(bos, nxt), xn_is_xhat=xn_is_xhat)
             if isinstance(mlp, tuple):  # the residual step ran fused with the last MLP product
                 x_p, xn = mlp
+                xn_is_xhat = False
             elif i + 1 < len(blocks):
                 n1 = blocks[i + 1].norm1
                 x_p, xn = K.packed_residual_persist_ln(x_p, x_attn, mlp, qs.active_batch_idx, qs.active_token_idx,
-                                                       bos, n1.weight, n1.bias, n1.eps)
+                                                       bos, n1.weight, n1.bias, n1.eps, nvfp4_scale=ts_next)
+                xn_is_xhat = ts_next is not None
             else:
                 x_p = K.packed_residual_persist(x_p, x_attn, mlp, qs.active_batch_idx, qs.active_token_idx, bos)
         bos_list.append(bos)

@@ -25,7 +25,7 @@ P = ctypes.c_void_p
 # Optional live timing of launch sites: every launch at a site named in `_probe["tags"]` is bracketed
 # by a pair of timing events on the launch stream (used by bench.py for the roofline). Sites are the
 # kernels' roles in the pass: "qkv", "proj", "fc1", "fc2", "w1", "w2", "w3", "attention", ...
-_probe: dict = {"tags": frozenset(), "events": {}, "gaps": []}
+_probe: dict = {"tags": frozenset(), "events": {}}
 
 
 def set_probe(tags) -> None:
@@ -36,7 +36,6 @@ def set_probe(tags) -> None:
         tags = (tags,)
     _probe["tags"] = frozenset(tags)
     _probe["events"] = {}
-    _probe["gaps"] = []
 
 
 def probe_events() -> dict:
@@ -44,24 +43,16 @@ def probe_events() -> dict:
     return _probe["events"]
 
 
-def probe_gaps() -> list:
-    """[(event, event), ...]: after each probed launch's end event a third event is recorded right
-    away; the time between the two is what an empty bracket reads (the events' own overhead)."""
-    return _probe["gaps"]
-
-
 def _launch(tag: str, t: torch.Tensor, name: str, *args) -> None:
     if tag not in _probe["tags"]:
         call(name, *args)
         return
     s = torch.cuda.current_stream(t.device)
-    e0, e1, e2 = (torch.cuda.Event(enable_timing=True) for _ in range(3))
+    e0, e1 = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
     e0.record(s)
     call(name, *args)
     e1.record(s)
-    e2.record(s)
     _probe["events"].setdefault(tag, []).append((e0, e1))
-    _probe["gaps"].append((e1, e2))
 
 
 def _ptr(t: torch.Tensor | None) -> P:
@@ -233,12 +224,22 @@ def packed_residual_persist(x_act: torch.Tensor, x_attn: torch.Tensor, mlp: torc
     return x_new
 
 
+def _nvfp4_scale(ts: torch.Tensor | None, what: str) -> torch.Tensor | None:
+    if ts is not None:
+        _require(ts.dtype == torch.float32 and ts.numel() == 1 and ts.is_cuda,
+                 f"{what}: the NVFP4 tensor scale must be one fp32 value on the device")
+    return ts
+
+
 def packed_residual_persist_ln(x_act: torch.Tensor, x_attn: torch.Tensor, mlp: torch.Tensor, batch_idx: torch.Tensor,
                                token_idx: torch.Tensor, blocks_out_sum: torch.Tensor, ln_weight: torch.Tensor,
-                               ln_bias: torch.Tensor, eps: float):
+                               ln_bias: torch.Tensor, eps: float, nvfp4_scale: torch.Tensor | None = None):
     """packed_residual_persist fused with the next block's first LayerNorm: returns (x_new, LN(x_new)),
-    the LayerNorm bit-identical to layer_norm(x_new) (block.py:1140-1179, then :1114 of the next block)."""
+    the LayerNorm bit-identical to layer_norm(x_new) (block.py:1140-1179, then :1114 of the next block).
+    With nvfp4_scale (the next qkv linear's NVFP4 activation scale) the second tensor is instead the
+    NVFP4 operand x_hat of LN(x_new), as nvfp4_quantize_dequantize would give it."""
     _require_cuda(x_act, x_attn, mlp, batch_idx, token_idx, blocks_out_sum, ln_weight, ln_bias)
+    ts = _nvfp4_scale(nvfp4_scale, "packed_residual_persist_ln")
     for t, nm in ((x_act, "x_act"), (x_attn, "x_attn"), (mlp, "mlp")):
         _require(t.dtype == torch.bfloat16 and t.dim() == 2 and t.is_contiguous() and t.shape == x_act.shape,
                  f"packed_residual_persist_ln: {nm} must be contiguous bf16 [M, C]")
@@ -249,10 +250,14 @@ def packed_residual_persist_ln(x_act: torch.Tensor, x_attn: torch.Tensor, mlp: t
              "packed_residual_persist_ln: bf16 LayerNorm parameters of size C")
     x_new = torch.empty_like(x_act)
     ln_out = torch.empty_like(x_act)
-    _launch("packed_residual", x_act, "oudjat_packed_residual_persist_ln", _ptr(x_act), _ptr(x_attn), _ptr(mlp), M, C,
-            _ptr(_index(batch_idx, "batch_idx")), _ptr(_index(token_idx, "token_idx")), _ptr(blocks_out_sum),
-            blocks_out_sum.stride(0), blocks_out_sum.stride(1), _ptr(x_new), _ptr(ln_weight.contiguous()),
-            _ptr(ln_bias.contiguous()), float(eps), _ptr(ln_out), _stream(x_act))
+    args = (_ptr(x_act), _ptr(x_attn), _ptr(mlp), M, C, _ptr(_index(batch_idx, "batch_idx")),
+            _ptr(_index(token_idx, "token_idx")), _ptr(blocks_out_sum), blocks_out_sum.stride(0),
+            blocks_out_sum.stride(1), _ptr(x_new), _ptr(ln_weight.contiguous()), _ptr(ln_bias.contiguous()), float(eps))
+    if ts is None:
+        _launch("packed_residual", x_act, "oudjat_packed_residual_persist_ln", *args, _ptr(ln_out), _stream(x_act))
+    else:
+        _launch("packed_residual", x_act, "oudjat_packed_residual_persist_ln_nvfp4", *args, _ptr(ts), _ptr(ln_out),
+                _stream(x_act))
     return x_new, ln_out
 
 
@@ -567,17 +572,26 @@ def residual_prune_compact(keep: torch.Tensor, spatial: torch.Tensor, dindice: t
 
 
 def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float = 1e-5,
-               out: torch.Tensor | None = None) -> torch.Tensor:
+               out: torch.Tensor | None = None, nvfp4_scale: torch.Tensor | None = None) -> torch.Tensor:
+    """LayerNorm of bf16 rows (fp32 statistics). With nvfp4_scale (the consuming linear's NVFP4 activation
+    scale) the result is instead the NVFP4 operand x_hat of LayerNorm(x), as nvfp4_quantize_dequantize
+    would give it on the LayerNorm output."""
     _require_cuda(x, weight, bias)
     _require(x.dtype == weight.dtype == bias.dtype == torch.bfloat16, "layer_norm: bf16 only")
+    ts = _nvfp4_scale(nvfp4_scale, "layer_norm")
     C = x.shape[-1]
     x2 = x.reshape(-1, C)
     _require(x2.stride(1) == 1, "layer_norm: rows must be contiguous")
     if out is None:
         out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
     o2 = out.view(-1, C)
-    _launch("layernorm", x, "oudjat_layernorm_rows", _ptr(x2), x2.shape[0], C, x2.stride(0), _ptr(weight.contiguous()),
-         _ptr(bias.contiguous()), float(eps), _ptr(o2), o2.stride(0), _stream(x))
+    if ts is None:
+        _launch("layernorm", x, "oudjat_layernorm_rows", _ptr(x2), x2.shape[0], C, x2.stride(0),
+                _ptr(weight.contiguous()), _ptr(bias.contiguous()), float(eps), _ptr(o2), o2.stride(0), _stream(x))
+    else:
+        _launch("layernorm", x, "oudjat_layernorm_rows_nvfp4", _ptr(x2), x2.shape[0], C, x2.stride(0),
+                _ptr(weight.contiguous()), _ptr(bias.contiguous()), float(eps), _ptr(ts), _ptr(o2), o2.stride(0),
+                _stream(x))
     return out
 
 
@@ -605,11 +619,25 @@ def apply_rope_active_inplace(q_active: torch.Tensor, k_active: torch.Tensor, ro
 
 def qkv_rope_kv_scatter(qkv: torch.Tensor, rope, patch_mask: torch.Tensor, rope_idx: torch.Tensor,
                         batch_idx: torch.Tensor, token_idx: torch.Tensor, kv_cache: torch.Tensor,
-                        q_out: torch.Tensor) -> None:
+                        q_out: torch.Tensor, scale: float | None = None, bias: torch.Tensor | None = None) -> None:
     """qkv [M, 3, H, Dh] -> RoPE on q/k of patch rows; k, v rows written into kv_cache [B, N, 2, H, Dh]
-    in place; q written to q_out [M, H, Dh]."""
+    in place; q written to q_out [M, H, Dh]. With `scale` (an NVFP4 qkv linear), qkv is that linear's raw
+    product and each value first becomes bf16(raw * scale + bias) (scale_bias's arithmetic)."""
     sin, cos = rope
-    _require_cuda(qkv, patch_mask, rope_idx, batch_idx, token_idx, kv_cache, q_out, sin, cos)
+    _require_cuda(qkv, patch_mask, rope_idx, batch_idx, token_idx, kv_cache, q_out, sin, cos, bias)
+    if scale is not None:
+        M, three, H, Dh = qkv.shape
+        _require(bias is None or (bias.dtype == torch.bfloat16 and bias.numel() == 3 * H * Dh),
+                 "qkv_rope_kv_scatter: bias must be bf16 [3 H Dh]")
+        _require(three == 3 and qkv.is_contiguous() and qkv.dtype == torch.bfloat16, "qkv must be contiguous [M,3,H,Dh]")
+        _require(kv_cache.dim() == 5 and kv_cache.shape[2:] == (2, H, Dh) and trailing_is_packed(kv_cache, 2),
+                 "kv_cache must be [B, N, 2, H, Dh] with packed rows")
+        _require(q_out.is_contiguous() and q_out.shape == (M, H, Dh), "q_out must be contiguous [M, H, Dh]")
+        _launch("qkv_post", qkv, "oudjat_qkv_rope_kv_scatter_scaled", _ptr(qkv), M, H, Dh, float(scale),
+                _ptr(None if bias is None else bias.contiguous()), _ptr(sin), _ptr(cos), sin.stride(0),
+                _ptr(patch_mask), _ptr(rope_idx), _ptr(batch_idx), _ptr(token_idx), _ptr(kv_cache),
+                kv_cache.stride(0), kv_cache.stride(1), _ptr(q_out), _stream(qkv))
+        return
     M, three, H, Dh = qkv.shape
     _require(three == 3 and qkv.is_contiguous() and qkv.dtype == torch.bfloat16, "qkv must be contiguous [M,3,H,Dh]")
     _require(kv_cache.dim() == 5 and kv_cache.shape[2:] == (2, H, Dh) and trailing_is_packed(kv_cache, 2),
@@ -1020,17 +1048,23 @@ def scale_bias(x: torch.Tensor, scale: float, bias: torch.Tensor | None = None, 
 
 
 def swiglu_scaled(x1: torch.Tensor, s1: float, b1: torch.Tensor | None, x2: torch.Tensor, s2: float,
-                  b2: torch.Tensor | None) -> torch.Tensor:
+                  b2: torch.Tensor | None, nvfp4_scale: torch.Tensor | None = None) -> torch.Tensor:
     """silu(x1 * s1 + b1) * (x2 * s2 + b2) -> bf16, written into x1 (fused_swiglu_epilogue_triton,
-    token_update.py:620-669)."""
+    token_update.py:620-669). With nvfp4_scale (the NVFP4 w3 linear's activation scale) x1 receives
+    instead the NVFP4 operand x_hat of that output."""
     _require_cuda(x1, x2, b1, b2)
     _require(x1.shape == x2.shape and x1.is_contiguous() and x2.is_contiguous() and x1.dtype == x2.dtype == torch.bfloat16,
              "swiglu_scaled: contiguous bf16 tensors of one shape")
     _require((b1 is None) == (b2 is None), "swiglu_scaled: both biases or neither")
+    ts = _nvfp4_scale(nvfp4_scale, "swiglu_scaled")
     N = x1.shape[-1]
     M = x1.numel() // N if N else 0
-    _launch("swiglu", x1, "oudjat_swiglu_scaled", _ptr(x1), float(s1), _ptr(None if b1 is None else b1.contiguous()),
-            _ptr(x2), float(s2), _ptr(None if b2 is None else b2.contiguous()), M, N, _ptr(x1), _stream(x1))
+    args = (_ptr(x1), float(s1), _ptr(None if b1 is None else b1.contiguous()), _ptr(x2), float(s2),
+            _ptr(None if b2 is None else b2.contiguous()), M, N)
+    if ts is None:
+        _launch("swiglu", x1, "oudjat_swiglu_scaled", *args, _ptr(x1), _stream(x1))
+    else:
+        _launch("swiglu", x1, "oudjat_swiglu_scaled_nvfp4", *args, _ptr(ts), _ptr(x1), _stream(x1))
     return x1
 
 

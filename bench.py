@@ -303,7 +303,6 @@ def main():
             K.set_probe(MFMA_SITES[ffn])
             timed(step, max(3, args.steps // 4))
             events = K.probe_events()
-            gaps = [a.elapsed_time(b) for a, b in K.probe_gaps()]
             K.set_probe(None)
         # The corrected tokens of the last pass must be finite (outside the timed region).
         out = context["current_feature"]
@@ -345,9 +344,8 @@ def main():
         roof["sites"] = {kk: {f: v[f] for f in ("achieved", "frac", "avg_us", "launches_per_pass", "share_of_pass")}
                          for kk, v in sites.items()}
         roof["timing"] = ("HIP events recorded on the launch stream around every launch of each site, in eager "
-                          "probe steps after the timed replays; avg_us is the mean bracket, which includes the "
-                          "events' own overhead (event_gap_us: an empty bracket recorded after each launch)")
-        roof["event_gap_us"] = round(1e3 * sum(gaps) / max(1, len(gaps)), 3)
+                          "probe steps after the timed replays; avg_us is the mean bracket, a few us above the "
+                          "kernel's own duration (rocprofv3 kernel trace)")
 
     cpu = None
     if args.cpu_budget > 0:

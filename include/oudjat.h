@@ -496,6 +496,40 @@ int oudjat_linear_qkv_rope_kv_fp8(const uint8_t* A, int64_t M, int64_t K, int64_
                                   uint16_t* kv, int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
                                   float acc_scale, oudjat_stream_t stream);
 
+/* Producers of the NVFP4 operand (fp4_fast_linear.py:171-219 folded into the kernel that makes the
+ * linear's input; no separate quantize pass): each writes x_hat = e2m1 * e4m3-scale (bf16, exactly what
+ * oudjat_nvfp4_quantize_dequantize gives on the bf16 tensor it would otherwise write) with tensor
+ * scale *tensor_scale, 16-element blocks along the row (C or N % 16 == 0).
+ *   oudjat_layernorm_rows_nvfp4: of LayerNorm(x) (norm1 -> the NVFP4 qkv linear, norm2 -> w1 / w2,
+ *     block.py:1114, 1141); other arguments as oudjat_layernorm_rows.
+ *   oudjat_packed_residual_persist_ln_nvfp4: of the next block's LayerNorm(x_new); x_new and the
+ *     blocks_out_sum rows as oudjat_packed_residual_persist_ln.
+ *   oudjat_swiglu_scaled_nvfp4: of the SwiGLU output (the NVFP4 w3 linear's input, ffn_layers.py:106-115
+ *     with token_update.py:620-669); other arguments as oudjat_swiglu_scaled. */
+int oudjat_layernorm_rows_nvfp4(const uint16_t* x, int64_t rows, int64_t C, int64_t x_stride, const uint16_t* weight,
+                                const uint16_t* bias, float eps, const float* tensor_scale, uint16_t* xhat,
+                                int64_t xhat_stride, oudjat_stream_t stream);
+int oudjat_packed_residual_persist_ln_nvfp4(const uint16_t* x_act, const uint16_t* x_attn, const uint16_t* mlp,
+                                            int64_t rows, int64_t C, const int64_t* batch_idx,
+                                            const int64_t* token_idx, uint16_t* bos, int64_t bos_stride_b,
+                                            int64_t bos_stride_n, uint16_t* x_new, const uint16_t* ln_w,
+                                            const uint16_t* ln_b, float eps, const float* tensor_scale,
+                                            uint16_t* xhat, oudjat_stream_t stream);
+int oudjat_swiglu_scaled_nvfp4(const uint16_t* x1, float s1, const uint16_t* b1, const uint16_t* x2, float s2,
+                               const uint16_t* b2, int64_t M, int64_t N, const float* tensor_scale, uint16_t* xhat,
+                               oudjat_stream_t stream);
+
+/* oudjat_qkv_rope_kv_scatter on the raw product of an NVFP4 qkv linear: every value first goes through
+ * the linear's scale-and-bias epilogue bf16(raw * scale + bias[col]) (bf16(raw * scale) for a NULL
+ * bias; scale_bias_inplace_triton, token_update.py:571-617), then RoPE and the K/V / q writes
+ * (attention.py:415-454). 16-byte aligned bias. */
+int oudjat_qkv_rope_kv_scatter_scaled(const uint16_t* qkv_raw, int64_t M, int64_t H, int64_t Dh, float scale,
+                                      const uint16_t* bias, const float* sin_table, const float* cos_table,
+                                      int64_t table_stride, const uint8_t* patch_mask, const int64_t* rope_idx,
+                                      const int64_t* batch_idx, const int64_t* token_idx, uint16_t* kv,
+                                      int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
+                                      oudjat_stream_t stream);
+
 /* Introspection, no counterpart in the reference: the kernel oudjat_linear_fp8 launches for an
  * M x N x K product with epilogue epi (5: oudjat_linear_qkv_rope_kv_fp8), as rocprofv3 prints it. */
 int oudjat_linear_fp8_kernel_name(int64_t M, int64_t N, int64_t K, int epi, char* buf, int64_t buflen);

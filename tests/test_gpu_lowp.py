@@ -350,3 +350,102 @@ def _controller_block(dev, precision, cfg, B, ratio):
           f"bits alone: {kv_ln:.4g}), yardstick {kv_yard:.4g}, route effect {kv_route:.4g}", flush=True)
     assert kv_rest <= max(2.0 * kv_yard, 1e-2 * kv_route), (kv_rest, kv_yard, kv_route)
     assert kv_impl <= kv_ln + kv_rest + 1e-6 * kv_route, (kv_impl, kv_ln, kv_rest)
+
+
+@pytest.mark.parametrize("M,C", [(103, 384), (1656, 4096), (517, 3072), (64, 8192)])
+def test_nvfp4_producers_equal_quantize_after(dev, M, C):
+    """The producers that write the NVFP4 operand directly (LayerNorm, the fused residual + LayerNorm,
+    the SwiGLU epilogue) give bit for bit nvfp4_quantize_dequantize of what they write otherwise, and
+    the scaled post-QKV scatter equals scale_bias followed by the plain scatter."""
+    g = torch.Generator().manual_seed(M + C)
+    x = (torch.randn(M, C, generator=g) * 3).to(torch.bfloat16).to(dev)
+    w = (1 + 0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
+    b = (0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
+    ts = torch.tensor(float(Q.per_tensor_amax_to_scale(4.0)), device=dev)
+    ln = K.layer_norm(x, w, b, 1e-6)
+    assert_bits_equal(K.layer_norm(x, w, b, 1e-6, nvfp4_scale=ts), K.nvfp4_quantize_dequantize(ln, ts).cpu(),
+                      "layer_norm -> x_hat")
+    # the packed residual step with the next block's norm1 as x_hat
+    B, N = 4, (M + 3) // 4 + 7
+    bi = torch.arange(M, device=dev) % B
+    ti = torch.arange(M, device=dev) // B
+    xa, mlp = (torch.randn(2, M, C, generator=g) * 0.5).to(torch.bfloat16).to(dev).unbind(0)
+    bos1 = torch.zeros(B, N, C, device=dev, dtype=torch.bfloat16)
+    bos2 = bos1.clone()
+    xn1, l1 = K.packed_residual_persist_ln(xa, x, mlp, bi, ti, bos1, w, b, 1e-6)
+    xn2, l2 = K.packed_residual_persist_ln(xa, x, mlp, bi, ti, bos2, w, b, 1e-6, nvfp4_scale=ts)
+    assert_bits_equal(xn2, xn1.cpu(), "x_new")
+    assert_bits_equal(bos2, bos1.cpu(), "blocks_out_sum rows")
+    assert_bits_equal(l2, K.nvfp4_quantize_dequantize(l1, ts).cpu(), "residual LayerNorm -> x_hat")
+    # the SwiGLU epilogue writing w3's operand
+    r1, r2 = (torch.randn(2, M, C, generator=g) * 4).to(torch.bfloat16).to(dev).unbind(0)
+    b1, b2 = (0.1 * torch.randn(2, C, generator=g)).to(torch.bfloat16).to(dev).unbind(0)
+    h = K.swiglu_scaled(r1.clone(), 0.37, b1, r2, 0.11, b2)
+    hx = K.swiglu_scaled(r1.clone(), 0.37, b1, r2, 0.11, b2, nvfp4_scale=ts)
+    assert_bits_equal(hx, K.nvfp4_quantize_dequantize(h, ts).cpu(), "swiglu -> x_hat")
+    if C % 3 == 0 and (C // 3) % 64 == 0:   # the scaled post-QKV scatter on a [M, 3, H, Dh] raw product
+        H, D = C // 3 // 64, 64
+        raw = x.view(M, 3, H, D)
+        pm = (torch.arange(M, device=dev) % 3 != 0)
+        ridx = torch.arange(M, device=dev) % 17
+        tab = torch.randn(32, D, generator=g).to(dev)
+        rope = (tab.sin().contiguous(), tab.cos().contiguous())
+        bq = (0.1 * torch.randn(C, generator=g)).to(torch.bfloat16).to(dev)
+        for bias in (None, bq):
+            kv1 = torch.zeros(B, N, 2, H, D, device=dev, dtype=torch.bfloat16)
+            kv2, q1, q2 = kv1.clone(), torch.empty(M, H, D, device=dev, dtype=torch.bfloat16), \
+                torch.empty(M, H, D, device=dev, dtype=torch.bfloat16)
+            K.qkv_rope_kv_scatter(K.scale_bias(x, 0.013, bias).view(M, 3, H, D), rope, pm, ridx, bi, ti, kv1, q1)
+            K.qkv_rope_kv_scatter(raw, rope, pm, ridx, bi, ti, kv2, q2, scale=0.013, bias=bias)
+            assert_bits_equal(kv2, kv1.cpu(), "scaled scatter K/V")
+            assert_bits_equal(q2, q1.cpu(), "scaled scatter q")
+
+
+@pytest.mark.parametrize("precision", ["fp4", "fp8"])
+def test_packed_low_precision_run_equals_blockwise(dev, precision):
+    """Three frozen SwiGLU blocks: the packed run (fused producers of the NVFP4 operands across block
+    boundaries) equals the controller's block-by-block run bit for bit."""
+    cfg = OM.with_overrides(_swiglu_cfg(), depth=3)
+    B, ratio = 2, 0.25
+    N, C, H, D, P = cfg.num_tokens, cfg.dim, cfg.heads, cfg.head_dim, cfg.num_patches
+    ws = OM.make_block_weights(cfg, 0, gamma=1.0, bias_std=0.05, ln_std=0.1, depth=3)
+    blocks = []
+    for w in ws:
+        blk = SelfAttentionBlock(C, H, ffn_ratio=3.0, qkv_bias=False, init_values=1.0, ffn_layer="swiglu64",
+                                 mask_k_bias=True)
+        blk.load_state_dict(w, strict=True)
+        blocks.append(blk.to(device=dev, dtype=torch.bfloat16))
+    g = torch.Generator().manual_seed(9)
+    x = torch.randn(B, N, C, generator=g).to(torch.bfloat16).to(dev)
+    cache = {}
+    for i in range(3):
+        cache[f"layer{i}_kv"] = torch.randn(B, N, 2, H, D, generator=g).to(torch.bfloat16).to(dev)
+        cache[f"layer{i}_blocks_out_sum"] = (torch.randn(B, N, C, generator=g) * 0.1).to(torch.bfloat16).to(dev)
+    imp = torch.rand(B, P, generator=g).to(dev)
+    rope = OM.rope_tables(cfg)
+    r = (rope[0].to(dev), rope[1].to(dev))
+    dind = OM.full_dindice(cfg, B).to(dev)
+    kw = dict(token_keep_ratio=ratio, mobile_pscore="residual_energy", mobile_pscore_weight=1.0,
+              mobile_pscore_hint=imp, server_pscore_weight=0.0)
+    ctrl = DINOv3CorrectPrecisionController(nn.ModuleList(blocks), precision=precision, device=dev)
+
+    def blockwise():
+        c = {k: v.clone() for k, v in cache.items()}
+        y = x
+        with torch.no_grad():
+            for i in range(3):
+                y, c = ctrl.run_block(i, y, dind, r, c, f"layer{i}", **kw)
+        return y, c
+
+    ctrl.begin_event()
+    blockwise()                      # calibration
+    ctrl.begin_event()               # freeze
+    y_b, c_b = blockwise()
+    c_p = {k: v.clone() for k, v in cache.items()}
+    with torch.no_grad():
+        y_p, c_p = ctrl.run_blocks_packed(range(3), x, dind, r, c_p, **kw)
+    torch.cuda.synchronize()
+    assert_bits_equal(y_p, y_b.cpu(), f"{precision} packed run")
+    for i in range(3):
+        for s_ in ("kv", "blocks_out_sum"):
+            assert_bits_equal(c_p[f"layer{i}_{s_}"], c_b[f"layer{i}_{s_}"].cpu(), f"layer{i}_{s_}")

@@ -103,6 +103,7 @@ def test_zero_sized_calls_are_noops():
     _lib.call("oudjat_scatter_rows", NULL, 0, 0, 2048, NULL, NULL, 0, NULL, 2048, NULL)
     _lib.call("oudjat_layernorm_rows", NULL, 0, 1024, 1024, NULL, NULL, 1e-5, NULL, 1024, NULL)
     _lib.call("oudjat_nvfp4_quantize", NULL, 0, 1024, 1024, NULL, NULL, NULL, NULL)
+    _lib.call("oudjat_layernorm_rows_nvfp4", NULL, 0, 1024, 1024, NULL, NULL, 1e-5, NULL, NULL, 1024, NULL)
 
 
 def test_wrappers_refuse_cpu_tensors():
