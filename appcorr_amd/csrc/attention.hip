@@ -93,11 +93,14 @@ __device__ __forceinline__ float prob_row_sum(const bf16x8_t (&pf)[4]) {
 // MINW: fewest waves a launch of this instance uses (sizes the per-thread share of a K/V tile);
 // DOUBLE_SET: prefetch K/V two tiles ahead through two register sets (needs the registers that only
 // the Dh = 64, >= 8-wave instance has to spare).
-template <int DH, int MINW, bool DOUBLE_SET>
+// LSE: also write each query's row log-sum-exp (natural log) of the scaled scores to lse[b][h][t],
+// from an fp32 sum of the unrounded probabilities kept beside the bf16-weight sum that normalises
+// the output (the output is the same bit for bit either way).
+template <int DH, int MINW, bool DOUBLE_SET, bool LSE = false>
 __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void sq_attention_kernel(
     const uint16_t* __restrict__ q, int64_t qrs, int T, const uint16_t* __restrict__ kv, int64_t kvb, int64_t kvn,
     int64_t kvkv, int64_t kvh, int N, float scale_log2, uint16_t* __restrict__ out, int64_t ors,
-    int waves_per_wg) {
+    int waves_per_wg, float* __restrict__ lse) {
   constexpr int CPR = DH / 8;                 // 16-byte chunks per K / V row
   constexpr int KROWB = DH * 2;               // bytes per K / V row in LDS
   constexpr int KSTAGE = kKeyTile * KROWB;
@@ -152,6 +155,7 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
 #pragma unroll
     for (int v = 0; v < 16; ++v) o[d][v] = 0.0f;
   float m_i = -INFINITY, l_i = 0.0f;
+  float lf = 0.0f;  // LSE: this lane's half of the fp32 probability sum
 
   const uint16_t* kbase = kv + (int64_t)b * kvb + (int64_t)h * kvh;
   const uint16_t* vbase = kbase + kvkv;
@@ -255,10 +259,14 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
     const float m_new = softmax_ref_max(m_i, mx, scale_log2);
     const float alpha = __builtin_amdgcn_exp2f((m_i - m_new) * scale_log2);
     const float mc = m_new * scale_log2;
+    if constexpr (LSE) lf *= alpha;
 #pragma unroll
     for (int kb = 0; kb < 2; ++kb)
 #pragma unroll
-      for (int v = 0; v < 16; ++v) s[kb][v] = __builtin_amdgcn_exp2f(fmaf(s[kb][v], scale_log2, -mc));
+      for (int v = 0; v < 16; ++v) {
+        s[kb][v] = __builtin_amdgcn_exp2f(fmaf(s[kb][v], scale_log2, -mc));
+        if constexpr (LSE) lf += s[kb][v];
+      }
     // P^T fragments: k-step j covers keys 16j + {4g..4g+3} and 16j + 8 + {4g..4g+3}.
     bf16x8_t pf[4];
 #pragma unroll
@@ -343,6 +351,15 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
         for (int e = 0; e < 4; ++e) w[e] = (__bf16)(o[d][4 * r4 + e] * inv);
         *reinterpret_cast<bf16x4_t*>(orow + d * 32 + 8 * r4 + 4 * g) = w;
       }
+  }
+  if constexpr (LSE) {
+    // lse = ln(sum_k exp(s_k * scale)) = (m * scale * log2 e + log2 l) * ln 2, with the probabilities
+    // exp2(s * scale * log2 e - m * scale * log2 e) of the loop (m the reference max).
+    if (active) {
+      const float lt = xor32_sum(lf);
+      if (g == 0 && qr < T)
+        lse[((int64_t)b * gridDim.y + h) * T + qr] = (m_i * scale_log2 + log2f(lt)) * 0.6931471805599453f;
+    }
   }
 }
 
@@ -997,7 +1014,7 @@ static int64_t attn_workspace_elems(int64_t B, int64_t T, int64_t H, int kv_part
 static int sparse_query_attention_impl(const uint16_t* q, int64_t qrs, int64_t B, int64_t T, int64_t H, int64_t Dh,
                                        const uint16_t* kv, int64_t kvb, int64_t kvn, int64_t kvkv, int64_t kvh,
                                        int64_t N, float scale, uint16_t* out, int64_t ors, float* workspace,
-                                       int64_t workspace_elems, oudjat_stream_t stream) {
+                                       int64_t workspace_elems, float* lse, oudjat_stream_t stream) {
   OUDJAT_REQUIRE(B >= 0 && T >= 0 && H >= 0 && N >= 0, OUDJAT_ERR_INVALID_ARGUMENT,
                  "sparse_query_attention: negative size");
   if (B == 0 || T == 0 || H == 0) return OUDJAT_OK;
@@ -1016,6 +1033,22 @@ static int sparse_query_attention_impl(const uint16_t* q, int64_t qrs, int64_t B
   const int w = s.w;
   dim3 grid((unsigned)s.n_wg, (unsigned)H, (unsigned)B);
   hipStream_t st = as_stream(stream);
+  if (lse) {
+    // The register-staged kernel with the row log-sum-exp (at Dh = 128 the kernel every call runs;
+    // at Dh = 64 its output equals the buffer-load kernel's on every row of a full query wave).
+    OUDJAT_REQUIRE(aligned(lse, 4), OUDJAT_ERR_UNSUPPORTED_LAYOUT, "sparse_query_attention: lse alignment");
+    const size_t lds = 2 * 2 * (size_t)kKeyTile * Dh * 2;
+    if (Dh == 128)
+      sq_attention_kernel<128, kMinWaves, false, true><<<grid, w * 64, lds, st>>>(
+          q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N, scale_log2, out, ors, w, lse);
+    else if (w >= 8)
+      sq_attention_kernel<64, 8, true, true><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,
+                                                                      (int)N, scale_log2, out, ors, w, lse);
+    else
+      sq_attention_kernel<64, kMinWaves, false, true><<<grid, w * 64, lds, st>>>(
+          q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N, scale_log2, out, ors, w, lse);
+    return check_launch("sparse_query_attention (lse)");
+  }
   if (s.dma) {
     const size_t lds_dma = (size_t)kAttnStages * 2 * kKeyTile * 128;
     static_assert((size_t)kAttnStages * 2 * kKeyTile * 128 <= 64 * 1024, "needs no larger-LDS attribute");
@@ -1070,13 +1103,13 @@ static int sparse_query_attention_impl(const uint16_t* q, int64_t qrs, int64_t B
   const size_t lds = 2 * 2 * (size_t)kKeyTile * Dh * 2;
   if (Dh == 128)
     sq_attention_kernel<128, kMinWaves, false><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,
-                                                                          (int)N, scale_log2, out, ors, w);
+                                                                          (int)N, scale_log2, out, ors, w, nullptr);
   else if (w >= 8)
     sq_attention_kernel<64, 8, true><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N,
-                                                                scale_log2, out, ors, w);
+                                                                scale_log2, out, ors, w, nullptr);
   else
     sq_attention_kernel<64, kMinWaves, false><<<grid, w * 64, lds, st>>>(q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh,
-                                                                         (int)N, scale_log2, out, ors, w);
+                                                                         (int)N, scale_log2, out, ors, w, nullptr);
   return check_launch("sparse_query_attention");
 }
 
@@ -1085,7 +1118,7 @@ extern "C" int oudjat_sparse_query_attention(const uint16_t* q, int64_t qrs, int
                                              int64_t kvh, int64_t N, float scale, uint16_t* out, int64_t ors,
                                              oudjat_stream_t stream) {
   return sparse_query_attention_impl(q, qrs, B, T, H, Dh, kv, kvb, kvn, kvkv, kvh, N, scale, out, ors, nullptr, 0,
-                                     stream);
+                                     nullptr, stream);
 }
 
 extern "C" int oudjat_sparse_query_attention_ws(const uint16_t* q, int64_t qrs, int64_t B, int64_t T, int64_t H,
@@ -1095,7 +1128,17 @@ extern "C" int oudjat_sparse_query_attention_ws(const uint16_t* q, int64_t qrs, 
                                                 oudjat_stream_t stream) {
   OUDJAT_REQUIRE(workspace_elems >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "sparse_query_attention: negative workspace size");
   return sparse_query_attention_impl(q, qrs, B, T, H, Dh, kv, kvb, kvn, kvkv, kvh, N, scale, out, ors, workspace,
-                                     workspace_elems, stream);
+                                     workspace_elems, nullptr, stream);
+}
+
+extern "C" int oudjat_sparse_query_attention_lse(const uint16_t* q, int64_t qrs, int64_t B, int64_t T, int64_t H,
+                                                 int64_t Dh, const uint16_t* kv, int64_t kvb, int64_t kvn,
+                                                 int64_t kvkv, int64_t kvh, int64_t N, float scale, uint16_t* out,
+                                                 int64_t ors, float* lse, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(lse != nullptr || B == 0 || T == 0 || H == 0, OUDJAT_ERR_INVALID_ARGUMENT,
+                 "sparse_query_attention: null lse");
+  return sparse_query_attention_impl(q, qrs, B, T, H, Dh, kv, kvb, kvn, kvkv, kvh, N, scale, out, ors, nullptr, 0,
+                                     lse, stream);
 }
 
 extern "C" int64_t oudjat_sparse_query_attention_workspace_elems(int64_t B, int64_t T, int64_t H, int64_t Dh,

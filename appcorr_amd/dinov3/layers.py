@@ -201,10 +201,11 @@ class SelfAttention(nn.Module):
             out = _linear_route(self.proj, attn, "proj")
         return out, cache_feature
 
-    def _qkv_attention(self, xn: Tensor, rope, kv: Tensor, qs: PackedQueryState, xn_is_xhat: bool = False):
+    def _qkv_attention(self, xn: Tensor, rope, kv: Tensor, qs: PackedQueryState, xn_is_xhat: bool = False,
+                       lse: Tensor | None = None):
         """q, K/V rows and the attention output of the packed rows from their norm1 output xn -- for a
         frozen NVFP4 qkv linear, xn may already be its NVFP4 operand x_hat (xn_is_xhat: the producer wrote
-        it)."""
+        it). lse (fp32 [B, H, T]) receives the attention's row log-sum-exp when given."""
         M, C = xn.shape
         H, D = self.num_heads, self.head_dim
         B = kv.shape[0]
@@ -242,7 +243,7 @@ class SelfAttention(nn.Module):
         if qkv is not None:
             K.qkv_rope_kv_scatter(qkv.view(M, 3, H, D), rope, qs.active_patch_mask, qs.active_rope_idx,
                                   qs.active_batch_idx, qs.active_token_idx, kv, q)
-        attn = K.sparse_query_attention(q, kv, T, self.scale)
+        attn = K.sparse_query_attention(q, kv, T, self.scale, lse=lse)
         return q, attn
 
 
@@ -362,7 +363,11 @@ class SelfAttentionBlock(nn.Module):
         kv = torch.empty((B, N, 2, H, D), device=dev, dtype=torch.bfloat16)
         cache_feature[f"{tag}_kv"] = kv
         xn = K.layer_norm(x2, self.norm1.weight, self.norm1.bias, self.norm1.eps)
-        q, attn = self.attn._qkv_attention(xn, rope, kv, qs)
+        # The fused key-side score reads the attention's own row log-sum-exp (one more pass over the
+        # scores), as the reference takes cuDNN's (attention_pscore.py:172-241).
+        lse = (torch.empty((B, H, N), device=dev, dtype=torch.float32)
+               if self._fused_patch_score(server_pscore, H, D, N) else None)
+        q, attn = self.attn._qkv_attention(xn, rope, kv, qs, lse=lse)
         g1 = self._gamma(self.ls1, x2)
         inc = K.linear(attn, self.attn.proj.weight, self.attn.proj.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g1,
                        site="proj")
@@ -373,24 +378,33 @@ class SelfAttentionBlock(nn.Module):
         out = K.fused_layerscale_add(x_attn, mlp, ones).view(B, N, C)
         if server_pscore not in ("none", "disabled"):
             cache_feature[f"{tag}_server_pscore"] = self._server_pscore(q.view(B, N, H, D), kv, server_pscore,
-                                                                        N - prefix)
+                                                                        N - prefix, lse=lse)
         return out, cache_feature
 
     _PATCH_ATTN_PSCORES = frozenset({"patch_attn_prob", "patch_attn_prob_layermean"})
     _PSEUDO_ATTN_PSCORES = frozenset({"patch_pseudo_attn_prob", "patch_pseudo_attn_prob_layermean"})
 
-    def _server_pscore(self, q: Tensor, kv: Tensor, kind: str, num_patches: int) -> Tensor:
+    @classmethod
+    def _fused_patch_score(cls, kind: str, H: int, D: int, N: int) -> bool:
+        """The reference's fused key-side score applies (attention.py:241-250; the shape limits of
+        attention_pscore.py:100-131)."""
+        return kind == "patch_attn_prob_layermean" and H == 32 and D == 128 and 0 < N <= 4096
+
+    def _server_pscore(self, q: Tensor, kv: Tensor, kind: str, num_patches: int, lse: Tensor | None = None) -> Tensor:
         """The approx pass's server score (attention.py:241-273) from the queries q [B, N, H, Dh] and the
         cache kv [B, N, 2, H, Dh] (both after RoPE), with the reference's rounding points:
           patch_attn_prob(_layermean): mean over heads, then over all queries, of the full softmax
           (:251-253), bf16 [B, N]; patch_attn_prob_layermean on 32 heads of 128 with N <= 4096 takes the
-          fused key-side sum from the row log-sum-exp instead (:241-250, attention_pscore.py:100-131);
+          fused key-side sum from the row log-sum-exp instead (:241-250, attention_pscore.py:100-131) --
+          the attention's own (lse [B, H, N]) when the caller has it, else computed here;
           patch_pseudo_attn_prob(_layermean): softmax of the pseudo query (:254-261), bf16 [B, N];
           any other kind (cls_attn_prob, cls_attn_prob_layermean, random: the reference's else branch,
           :266-271): softmax of the cls query over all keys, mean over heads, fp32 [B, N]."""
         if kind in self._PATCH_ATTN_PSCORES:
             B, N, H, D = q.shape
-            fused = kind == "patch_attn_prob_layermean" and H == 32 and D == 128 and 0 < N <= 4096
+            fused = self._fused_patch_score(kind, H, D, N)
+            if fused and lse is not None:
+                return K.patch_attention_prob_from_lse(q.reshape(B * N, H, D), kv, self.attn.scale, lse)
             return K.patch_attention_prob(q.reshape(B * N, H, D), kv, self.attn.scale,
                                           K.PATTN_LSE if fused else K.PATTN_DENSE)
         if kind in self._PSEUDO_ATTN_PSCORES:

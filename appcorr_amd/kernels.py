@@ -831,11 +831,13 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
 
 
 def sparse_query_attention(q: torch.Tensor, kv_cache: torch.Tensor, T: int, scale: float,
-                           out: torch.Tensor | None = None) -> torch.Tensor:
+                           out: torch.Tensor | None = None, lse: torch.Tensor | None = None) -> torch.Tensor:
     """softmax(q . K^T * scale) . V per image over all cached keys.
 
-    q [B*T, H, Dh] packed (rows b*T + t), kv_cache [B, N, 2, H, Dh] (K post-RoPE), -> [B*T, H*Dh]."""
-    _require_cuda(q, kv_cache)
+    q [B*T, H, Dh] packed (rows b*T + t), kv_cache [B, N, 2, H, Dh] (K post-RoPE), -> [B*T, H*Dh].
+    lse: optional contiguous fp32 [B, H, T] that receives each query's row log-sum-exp of the scaled
+    scores (what cuDNN's SDPA returns beside its output, attention_pscore.py:136-168)."""
+    _require_cuda(q, kv_cache, lse)
     _require(q.dtype == kv_cache.dtype == torch.bfloat16, "attention: bf16 only")
     B, N, two, H, Dh = kv_cache.shape
     _require(two == 2 and kv_cache.stride(4) == 1 and kv_cache.stride(3) == Dh, "attention: kv heads must be packed")
@@ -843,6 +845,13 @@ def sparse_query_attention(q: torch.Tensor, kv_cache: torch.Tensor, T: int, scal
              and q.stride(1) == Dh, "attention: q must be [B*T, H, Dh] with packed heads")
     if out is None:
         out = torch.empty((B * T, H * Dh), device=q.device, dtype=torch.bfloat16)
+    if lse is not None:
+        _require(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (B, H, T),
+                 "attention: lse must be contiguous fp32 [B, H, T]")
+        _launch("attention", q, "oudjat_sparse_query_attention_lse", _ptr(q), q.stride(0), B, T, H, Dh,
+                _ptr(kv_cache), kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(2), kv_cache.stride(3), N,
+                float(scale), _ptr(out), out.stride(0), _ptr(lse), _stream(q))
+        return out
     key = ("attention", B, T, H, Dh, N)
     elems = _WS_ELEMS.get(key)
     if elems is None:
@@ -919,6 +928,31 @@ def patch_attention_prob(q: torch.Tensor, kv_cache: torch.Tensor, scale: float, 
     out = torch.empty((B, N), device=q.device, dtype=torch.bfloat16)
     _launch("pscore", q, "oudjat_patch_attention_prob", _ptr(q), q.stride(0), B, N, H, Dh, _ptr(kv_cache),
             kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(3), float(scale), int(mode), _ptr(workspace),
+            _ptr(out), N, _stream(q))
+    return out
+
+
+def patch_attention_prob_from_lse(q: torch.Tensor, kv_cache: torch.Tensor, scale: float,
+                                  lse: torch.Tensor, workspace: torch.Tensor | None = None) -> torch.Tensor:
+    """PATTN_LSE's key-side score from the attention's own row log-sum-exp (lse [B, H, N] fp32, as
+    sparse_query_attention(..., lse=) writes it for T = N): one pass over the scores instead of three
+    (attention_pscore.py:172-241 after cuDNN's LSE). Same q / kv_cache contract as
+    patch_attention_prob; `workspace` (fp32, >= B*H*N) takes the partial column sums, one is allocated
+    when not given."""
+    _require_cuda(q, kv_cache, lse, workspace)
+    _kv_k_view_ok(kv_cache)
+    B, N, _, H, Dh = kv_cache.shape
+    _require(q.dim() == 3 and q.shape == (B * N, H, Dh) and q.stride(2) == 1 and q.stride(1) == Dh
+             and q.dtype == torch.bfloat16, "patch_attention_prob: q must be [B*N, H, Dh] bf16 with packed heads")
+    _require(lse.dtype == torch.float32 and lse.is_contiguous() and tuple(lse.shape) == (B, H, N),
+             "patch_attention_prob: lse must be contiguous fp32 [B, H, N]")
+    if workspace is None:
+        workspace = torch.empty((B * H * N,), device=q.device, dtype=torch.float32)
+    _require(workspace.dtype == torch.float32 and workspace.is_contiguous() and workspace.numel() >= B * H * N,
+             "patch_attention_prob: workspace must be contiguous fp32 with B*H*N elements")
+    out = torch.empty((B, N), device=q.device, dtype=torch.bfloat16)
+    _launch("pscore", q, "oudjat_patch_attention_prob_lse", _ptr(q), q.stride(0), B, N, H, Dh, _ptr(kv_cache),
+            kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(3), float(scale), _ptr(lse), _ptr(workspace),
             _ptr(out), N, _stream(q))
     return out
 

@@ -178,6 +178,11 @@ def main():
                     help="1: record the step into a HIP graph and time its replays (the eager time is reported "
                          "alongside); 0: time eager launches only")
     ap.add_argument("--probe", type=int, default=1, help="1: time every MFMA launch site in extra eager steps")
+    ap.add_argument("--approx-steps", type=int, default=0,
+                    help="after the correction timing, time this many approximate passes (the cache producer, "
+                         "eager launches) with --approx-pscore as the server score; reported under approx_pass")
+    ap.add_argument("--approx-pscore", default="patch_attn_prob_layermean",
+                    help="server_pscore of the timed approximate passes (weight 1)")
     ap.add_argument("--calib-copy-mib", type=int, default=0,
                     help="before the timed steps, copy this many MiB device-to-device once (a plain copy of known "
                          "size that calibrates rocprofv3 FETCH_SIZE / WRITE_SIZE counters)")
@@ -308,6 +313,25 @@ def main():
         out = context["current_feature"]
         if not bool(torch.isfinite(out.float()).all()):
             raise RuntimeError("bench: the correction pass produced non-finite tokens")
+        # The approximate pass (every token through every block, caching K/V, the residual sums and the
+        # server score), timed on its own context so the correction's caches stay as they are.
+        approx = None
+        if args.approx_steps > 0:
+            akw = dict(config.appcorr_kwargs)
+            akw.update(server_pscore=args.approx_pscore, server_pscore_weight=1.0)
+            aconfig = ExperimentConfig(model_name=config.model_name, batch_size=B, image_shape=config.image_shape,
+                                       backbone=bb, correct_precision=args.precision, appcorr_kwargs=akw)
+            actx = {"input_tokens": context["input_tokens"], "rope_sincos": context["rope_sincos"],
+                    "group_plans": context["group_plans"]}
+
+            def astep():
+                ex.approx_forward({"layers": (0, depth)}, actx, aconfig)
+
+            astep()
+            ams, _ = timed(astep, args.approx_steps)
+            approx = {"ms_per_pass": round(ams, 4), "server_pscore": args.approx_pscore, "steps": args.approx_steps,
+                      "launch": "eager", "tokens_per_s": round(B * N / (ams / 1e3), 1)}
+            del actx
     value = B * k / (ms / 1e3)
 
     roof = None
@@ -375,6 +399,8 @@ def main():
                    "eager_ms_per_step": round(ms_eager, 4)},
         "roofline": roof, "cpu_baseline": cpu,
     }
+    if approx is not None:
+        line["approx_pass"] = approx
     print(json.dumps(line), flush=True)
 
 

@@ -358,6 +358,17 @@ int oudjat_sparse_query_attention_ws(const uint16_t* q, int64_t q_row_stride, in
                                      int64_t N, float scale, uint16_t* out, int64_t out_row_stride,
                                      float* workspace, int64_t workspace_elems, oudjat_stream_t stream);
 
+/* Row 10 in the approximate pass with the row log-sum-exp (the cuDNN SDPA call that returns its LSE,
+ * appcorr/models/dinov3/layers/triton_kernels/attention_pscore.py:136-168): the output of
+ * oudjat_sparse_query_attention (bit for bit at Dh = 128; at Dh = 64 the register-staged kernel,
+ * bit-identical on every row of a full 32-query wave) and lse[(b*H + h)*T + t] = ln sum_n exp(q . k_n *
+ * scale), fp32, from an fp32 sum of the unrounded probabilities. lse: B*H*T fp32, 4-byte aligned. */
+int oudjat_sparse_query_attention_lse(const uint16_t* q, int64_t q_row_stride, int64_t B, int64_t T,
+                                      int64_t H, int64_t Dh, const uint16_t* kv, int64_t kv_stride_b,
+                                      int64_t kv_stride_n, int64_t kv_stride_kv, int64_t kv_stride_h,
+                                      int64_t N, float scale, uint16_t* out, int64_t out_row_stride,
+                                      float* lse, oudjat_stream_t stream);
+
 /* fp32 elements of workspace oudjat_sparse_query_attention_ws uses for this shape (0: it never
  * splits the keys of this shape). */
 int64_t oudjat_sparse_query_attention_workspace_elems(int64_t B, int64_t T, int64_t H, int64_t Dh,
@@ -421,6 +432,17 @@ int oudjat_patch_attention_prob(const uint16_t* q, int64_t q_row_stride, int64_t
                                 int64_t Dh, const uint16_t* kv, int64_t kv_stride_b, int64_t kv_stride_n,
                                 int64_t kv_stride_h, float scale, int mode, float* workspace, uint16_t* out,
                                 int64_t out_stride_b, oudjat_stream_t stream);
+
+/* Mode 1 of oudjat_patch_attention_prob given the attention's row log-sum-exp instead of computing it
+ * (the key-side kernel of attention_pscore.py:20-98 after cuDNN's LSE, :172-241): one pass over the
+ * scores, out[b, n] = bf16(fl(sum_{t,h} exp2(s log2e - lse[(b*H + h)*N + t] log2e)) * fl(1/(H N))),
+ * the sum in fp32 over head groups added in a fixed order (the reference's atomics have none).
+ * lse: B*H*N fp32 as oudjat_sparse_query_attention_lse writes it (T = N); workspace: B*H*N fp32
+ * (partial column sums); other arguments as oudjat_patch_attention_prob. */
+int oudjat_patch_attention_prob_lse(const uint16_t* q, int64_t q_row_stride, int64_t B, int64_t N, int64_t H,
+                                    int64_t Dh, const uint16_t* kv, int64_t kv_stride_b, int64_t kv_stride_n,
+                                    int64_t kv_stride_h, float scale, const float* lse, float* workspace,
+                                    uint16_t* out, int64_t out_stride_b, oudjat_stream_t stream);
 
 /* Introspection, no counterpart in the reference: writes to buf (NUL-terminated) the demangled name,
  * as rocprofv3 prints it, of the kernel oudjat_linear_bf16 launches for an M x N x K product with

@@ -117,15 +117,28 @@ def patch_attn_prob(q: np.ndarray, k: np.ndarray, scale: float) -> np.ndarray:
     return _mean_bf16(ph, axis=1)                                 # [B, N]
 
 
+def _scaled_scores(q: np.ndarray, k: np.ndarray, scale: float) -> np.ndarray:
+    """q [B, H, T, D], k [B, N, H, D] -> q . k * scale [B, H, T, N] in float64."""
+    return np.matmul(q.astype(np.float64), k.astype(np.float64).transpose(0, 2, 3, 1)) * float(scale)
+
+
+def row_logsumexp(q: np.ndarray, k: np.ndarray, scale: float) -> np.ndarray:
+    """The row log-sum-exp SDPA returns beside its output (attention_pscore.py:136-168, cuDNN's LSE):
+    lse[b, h, t] = ln sum_n exp(q[b, h, t] . k[b, n, h] * scale), natural log, exact (float64) evaluation
+    with the max taken out. q [B, H, T, D], k [B, N, H, D] -> [B, H, T]."""
+    s = _scaled_scores(q, k, scale)
+    mx = s.max(axis=-1, keepdims=True)
+    return (mx + np.log(np.exp(s - mx).sum(axis=-1, keepdims=True)))[..., 0]
+
+
 def patch_attn_prob_fused(q: np.ndarray, k: np.ndarray, scale: float) -> np.ndarray:
     """Fused key-side score (attention_pscore.py:20-98): p = exp(q.k * scale - lse) in fp32 from
     the row log-sum-exp of SDPA, summed over all queries and heads, times 1/(H N), rounded to bf16
     once. Exact (float64) evaluation; the reference's own fp32 kernel sums with atomics in no fixed
     order, so a device result agrees within fp32 rounding before the final bf16 rounding."""
     B, H, T, D = q.shape
-    s = np.matmul(q.astype(np.float64), k.astype(np.float64).transpose(0, 2, 3, 1)) * float(scale)
-    mx = s.max(axis=-1, keepdims=True)
-    lse = mx + np.log(np.exp(s - mx).sum(axis=-1, keepdims=True))
+    s = _scaled_scores(q, k, scale)
+    lse = row_logsumexp(q, k, scale)[..., None]
     p = np.exp(s - lse)
     col = p.sum(axis=(1, 2)) * (1.0 / float(H * T))
     return _bf(_f32(col))

@@ -8,7 +8,10 @@
     the lower candidate index), so the default per-layer plan selects the oracle's tokens;
   * inside the approx block the cached {tag}_server_pscore equals the oracle applied to the block's own
     q and K, for cls_attn_prob (fp32), the pseudo score (bf16) and "random" (the reference computes the
-    cls score for it and draws the random control at plan time, attention.py:266-271).
+    cls score for it and draws the random control at plan time, attention.py:266-271);
+  * the attention's row log-sum-exp (what cuDNN's SDPA hands the reference's fused score) against the
+    float64 row log-sum-exp, with the attention output unchanged, and the fused score computed from it
+    against the oracle, alone and inside an approx block of 32 heads of 128.
 """
 
 import numpy as np
@@ -206,3 +209,74 @@ def test_approx_block_caches_the_dense_score(dev, kind):
     assert got.dtype == ref.dtype == torch.bfloat16
     u = _bf16_ulps(got, ref)
     assert u.max() <= 1.0 and float((u > 0).mean()) <= 0.02, (u.max(), float((u > 0).mean()))
+
+
+@pytest.mark.parametrize("B,H,N,D", [(1, 32, 1029, 128), (2, 4, 77, 64), (1, 8, 300, 64)])
+def test_attention_row_lse_and_fused_score(dev, B, H, N, D):
+    """sparse_query_attention(..., lse=) over all N queries of an image: the output equals the call
+    without lse (bit for bit at Dh = 128, where both run the register-staged kernel), lse is the float64
+    row log-sum-exp of the same bf16 q and K within 2e-4 (fp32 score accumulation, fp32 exponentials and
+    an fp32 sum of up to N probabilities; a wrong log base or a dropped max is off by > 0.1), and the
+    key-side score computed from it is within the fused score's bound of the oracle."""
+    print(f"attention lse B={B} H={H} N={N} D={D}", flush=True)
+    q, kv, qd, kvd = _qkv(B, H, N, D, 5 + N, dev)
+    qp = qd.reshape(B * N, H, D)
+    scale = D ** -0.5
+    lse = torch.full((B, H, N), float("nan"), device=dev)
+    out = K.sparse_query_attention(qp, kvd, N, scale, lse=lse)
+    if D == 128:
+        assert_bits_equal(out, K.sparse_query_attention(qp, kvd, N, scale).cpu(), "attention output with lse")
+    qh = np.ascontiguousarray(q.float().numpy().transpose(0, 2, 1, 3))
+    kn = kv[:, :, 0].float().numpy()
+    ref = PS.row_logsumexp(qh, kn, scale)
+    err = np.abs(lse.cpu().numpy().astype(np.float64) - ref)
+    print(f"  lse max err {err.max():.3g}", flush=True)
+    assert np.isfinite(err).all() and err.max() <= 2e-4
+    got = K.patch_attention_prob_from_lse(qp, kvd, scale, lse)
+    want = torch.from_numpy(PS.patch_attn_prob_fused(qh, kn, scale)).to(torch.bfloat16)
+    u = _bf16_ulps(got, want)
+    print(f"  score ulps: max {u.max():.3g}, differing {float((u > 0).mean()):.4%}", flush=True)
+    assert u.max() <= 1.0 and float((u > 0).mean()) <= 0.02
+
+
+def test_approx_block_fused_score_from_the_attention_lse(dev):
+    """An approx block of 32 heads of 128 (the ViT-7B width at 224 px, N = 201) caching
+    patch_attn_prob_layermean: the fused score now comes from the attention's own log-sum-exp and
+    still equals the oracle's fused score of the block's q and K within its bound."""
+    cfg = OM.with_overrides(OM.CONFIGS["vit7b16_1024"], img_size=224, name="vit7b16_224")
+    B = 1
+    w = OM.make_block_weights(cfg, 0, gamma=1.0, bias_std=0.05, ln_std=0.1, depth=1)[0]
+    x_base, _, _, _ = OM.make_inputs(cfg, B, 1)
+    rope = OM.rope_tables(cfg)
+    r = (rope[0].to(dev), rope[1].to(dev))
+    blk = SelfAttentionBlock(cfg.dim, cfg.heads, ffn_ratio=3.0, qkv_bias=cfg.qkv_bias, init_values=1.0,
+                             ffn_layer="swiglu64", mask_k_bias=True)
+    blk.load_state_dict(w)
+    blk = blk.to(device=dev, dtype=torch.bfloat16)
+    x = x_base.to(dev)
+    kind = "patch_attn_prob_layermean"
+    assert blk._fused_patch_score(kind, cfg.heads, cfg.head_dim, cfg.num_tokens)
+    with torch.no_grad():
+        _, cache = blk.approx(x, r, {}, "layer0", server_pscore=kind, server_pscore_weight=1.0)
+        N, C = cfg.num_tokens, cfg.dim
+        xn = K.layer_norm(x.reshape(B * N, C), blk.norm1.weight, blk.norm1.bias, blk.norm1.eps)
+        kv2 = torch.empty_like(cache["layer0_kv"])
+        from appcorr_amd.dinov3.layers import PackedQueryState
+        tok = torch.arange(N, device=dev)
+        qs = PackedQueryState(torch.arange(B, device=dev).repeat_interleave(N), tok.repeat(B), tok.repeat(B),
+                              None, None, None, True, (tok >= 5).repeat(B), (tok - 5).clamp_min(0).repeat(B))
+        q, _ = blk.attn._qkv_attention(xn, r, kv2, qs)
+        # the score the stats-based LSE mode gives on the same q and K (no attention log-sum-exp)
+        stats_score = K.patch_attention_prob(q.view(B * N, cfg.heads, cfg.head_dim), cache["layer0_kv"],
+                                             cfg.head_dim ** -0.5, K.PATTN_LSE)
+    torch.cuda.synchronize()
+    assert_bits_equal(kv2, cache["layer0_kv"], "recomputed K/V")
+    got = cache["layer0_server_pscore"]
+    qn = q.view(B, N, cfg.heads, cfg.head_dim).cpu()
+    ref = OM.server_score(kind, qn, cache["layer0_kv"][:, :, 0].cpu(), cfg.num_patches, cfg.head_dim ** -0.5)
+    assert got.dtype == ref.dtype == torch.bfloat16
+    u = _bf16_ulps(got, ref)
+    print(f"block score ulps: max {u.max():.3g}, differing {float((u > 0).mean()):.4%}", flush=True)
+    assert u.max() <= 1.0 and float((u > 0).mean()) <= 0.02
+    v = _bf16_ulps(got, stats_score)
+    assert v.max() <= 1.0 and float((v > 0).mean()) <= 0.02

@@ -95,6 +95,28 @@ def test_nvfp4_rejects_k_not_multiple_of_16():
 def test_attention_rejects_unsupported_head_dim():
     _expect("OUDJAT_ERR_UNSUPPORTED_SHAPE", "oudjat_sparse_query_attention", ctypes.c_void_p(16), 96, 1, 4, 1, 96,
             ctypes.c_void_p(16), 0, 0, 0, 0, 8, 0.1, ctypes.c_void_p(16), 96, NULL)
+    _expect("OUDJAT_ERR_UNSUPPORTED_SHAPE", "oudjat_sparse_query_attention_lse", ctypes.c_void_p(16), 96, 1, 4, 1,
+            96, ctypes.c_void_p(16), 0, 0, 0, 0, 8, 0.1, ctypes.c_void_p(16), 96, ctypes.c_void_p(16), NULL)
+
+
+def test_lse_entry_points_reject_bad_arguments():
+    # no lse buffer for a non-empty call
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_sparse_query_attention_lse", ctypes.c_void_p(16), 128, 1, 4, 1,
+            128, ctypes.c_void_p(16), 0, 0, 0, 0, 8, 0.1, ctypes.c_void_p(16), 128, NULL, NULL)
+    # misaligned lse
+    _expect("OUDJAT_ERR_UNSUPPORTED_LAYOUT", "oudjat_sparse_query_attention_lse", ctypes.c_void_p(16), 128, 1, 4, 1,
+            128, ctypes.c_void_p(16), 2048, 256, 128, 128, 8, 0.1, ctypes.c_void_p(16), 128, ctypes.c_void_p(18), NULL)
+    _expect("OUDJAT_ERR_UNSUPPORTED_SHAPE", "oudjat_patch_attention_prob_lse", ctypes.c_void_p(16), 96, 1, 8, 1, 96,
+            ctypes.c_void_p(16), 0, 0, 96, 0.1, ctypes.c_void_p(16), ctypes.c_void_p(16), ctypes.c_void_p(16), 8, NULL)
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_patch_attention_prob_lse", ctypes.c_void_p(16), 128, 1, 8, 1, 128,
+            ctypes.c_void_p(16), 0, 0, 128, 0.1, NULL, ctypes.c_void_p(16), ctypes.c_void_p(16), 8, NULL)
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_patch_attention_prob_lse", ctypes.c_void_p(16), 128, 1, 8, 1, 128,
+            ctypes.c_void_p(16), 0, 0, 128, 0.1, ctypes.c_void_p(16), NULL, ctypes.c_void_p(16), 8, NULL)
+    # zero-sized calls touch nothing
+    _lib.call("oudjat_sparse_query_attention_lse", NULL, 128, 0, 4, 1, 128, NULL, 0, 0, 0, 0, 8, 0.1, NULL, 128,
+              NULL, NULL)
+    _lib.call("oudjat_patch_attention_prob_lse", NULL, 128, 0, 8, 1, 128, NULL, 0, 0, 128, 0.1, NULL, NULL, NULL, 8,
+              NULL)
 
 
 def test_zero_sized_calls_are_noops():

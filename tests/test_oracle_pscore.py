@@ -6,7 +6,9 @@
     value falls within an fp32 ulp of a bf16 rounding boundary);
   * closed forms: identical keys give p = bf16(1/N) everywhere; a dominant key takes all the mass;
     the scores of one image sum to 1 within the bf16 rounding of its N entries;
-  * the fused (log-sum-exp) score against float64 softmax column means.
+  * the fused (log-sum-exp) score against float64 softmax column means;
+  * the row log-sum-exp against torch.logsumexp of the float64 scores, and its closed form for
+    identical keys (s + ln N).
 """
 
 import math
@@ -123,3 +125,20 @@ def test_patch_attn_prob_fused_matches_float64_softmax():
     u = _ulps(got, want)
     assert float(u.max()) <= 1.0 and float((u == 0).mean()) >= 0.99
     assert math.isclose(float(got.astype(np.float64).sum()), 1.0, rel_tol=N * 2.0 ** -8)
+
+
+def test_row_logsumexp_matches_torch_and_closed_form():
+    B, H, N, D = 2, 3, 97, 64
+    q, k = _qk(B, H, N, D, seed=21, qscale=3.0)
+    scale = D ** -0.5
+    s = q.double() @ k.double().permute(0, 2, 3, 1) * scale                  # [B, H, N, N]
+    want = torch.logsumexp(s, dim=-1).numpy()
+    got = PS.row_logsumexp(q.float().numpy(), k.float().numpy(), scale)
+    assert got.shape == (B, H, N)
+    np.testing.assert_allclose(got, want, rtol=0, atol=1e-12)
+    assert bool((got >= s.max(dim=-1).values.numpy() - 1e-12).all())
+    # identical keys: every score of a query is the same s, so lse = s + ln N
+    k1 = k[:, :1].expand(B, N, H, D).contiguous()
+    s1 = (q.double() @ k1.double().permute(0, 2, 3, 1) * scale)[..., 0]
+    got1 = PS.row_logsumexp(q.float().numpy(), k1.float().numpy(), scale)
+    np.testing.assert_allclose(got1, s1.numpy() + math.log(N), rtol=0, atol=1e-11)
