@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be loaded before the HIP library, see module docstring
 
 LIB_PATH = Path(__file__).resolve().parent / "liboudjat_hip.so"
-ABI_VERSION = 13
+ABI_VERSION = 14
 
 OK = 0
 STATUS_NAMES = {
@@ -106,6 +106,8 @@ SIGNATURES: dict[str, list] = {
     "oudjat_sparse_query_attention_workspace_elems": [_i64, _i64, _i64, _i64, _i64],
     "oudjat_sparse_query_attention_lse": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32,
                                           _p, _i64, _p, _p],
+    "oudjat_patch_attention_prob_workspace_elems": [_i64, _i64, _i64, _i32],
+    "oudjat_gather_rows_ln": [_p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _f32, _p, _p, _p, _p],
     "oudjat_patch_attention_prob_lse": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _f32, _p, _p, _p,
                                         _i64, _p],
     "oudjat_nvfp4_quantize": [_p, _i64, _i64, _i64, _p, _p, _p, _p],
@@ -134,7 +136,8 @@ SIGNATURES: dict[str, list] = {
 }
 _RESTYPES = {"oudjat_status_string": ctypes.c_char_p, "oudjat_last_error": ctypes.c_char_p,
              "oudjat_linear_workspace_elems": ctypes.c_int64,
-             "oudjat_sparse_query_attention_workspace_elems": ctypes.c_int64}
+             "oudjat_sparse_query_attention_workspace_elems": ctypes.c_int64,
+             "oudjat_patch_attention_prob_workspace_elems": ctypes.c_int64}
 
 _lock = threading.Lock()
 _lib = None

@@ -1742,6 +1742,10 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   // 224 x 256 ping-pong tiles when they fill at least seven eighths of one round that 288 x 256 tiles
   // fill less (ViT-7B w1 / w2, 1656 x 8192 x 4096: 256 against 192 tiles, 92.7 against 103.4 us).
   const int64_t tiles224 = cdiv(M, 224) * (N / 256);
+  // Beyond two rounds of 288 x 256 tiles (the approximate pass, every token of the batch: M = B N)
+  // those tiles in as many rounds as it takes, in place of 128 x 128 tiles (ViT-L approximate pass
+  // 18.1 -> 16.5 ms, ViT-7B 337.7 -> 256.5 ms; 224 x 256 and 192 x 256 tiles came between).
+  if (N % 256 == 0 && tiles288 > 512) return 27;
   if (N % 256 == 0 && tiles224 >= 224 && tiles224 <= 256 && tiles288 < tiles224) return 30;
   if (N % 256 == 0 && tiles288 >= 192 && tiles288 <= 256) return 27;
   // Two rounds of 288-, 224- or 192-row ping-pong tiles 256 wide, whichever fills them most (ViT-L

@@ -102,6 +102,42 @@ __global__ __launch_bounds__(kNormThreads) void layernorm_kernel(const uint16_t*
   layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, out + row * os, xh_ts);
 }
 
+// The gather of a packed run's selected rows fused with the first block's LayerNorm: packed row i is
+// x[batch_idx[i], token_idx[i]], copied byte for byte to x_out, and its LayerNorm (or the NVFP4 operand
+// of it) goes to ln_out with layernorm_kernel's arithmetic (the same bits).
+template <int CH>
+__global__ __launch_bounds__(kNormThreads) void gather_ln_kernel(const uint16_t* __restrict__ x, int64_t sb,
+                                                                int64_t sn, const int64_t* __restrict__ bidx,
+                                                                const int64_t* __restrict__ tidx, int64_t rows, int C,
+                                                                const uint16_t* __restrict__ w,
+                                                                const uint16_t* __restrict__ bias, float eps,
+                                                                uint16_t* __restrict__ x_out,
+                                                                uint16_t* __restrict__ ln_out,
+                                                                const float* __restrict__ xh_ts) {
+  const int64_t row = (int64_t)blockIdx.x * kNormRowsPerWg + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int chunks = C >> 3;
+  const uint4* xv = reinterpret_cast<const uint4*>(x + bidx[row] * sb + tidx[row] * sn);
+  uint4* ov = reinterpret_cast<uint4*>(x_out + row * C);
+  uint4 raw[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) raw[j] = xv[c];
+  }
+  float v[CH][8];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) {
+      ov[c] = raw[j];
+      unpack8(raw[j], v[j]);
+    }
+  }
+  layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, ln_out + row * C, xh_ts);
+}
+
 // The residual step of a correction block on packed selected rows fused with the next block's
 // LayerNorm: x_new = bf16(x_attn + mlp), blocks_out_sum[b_i, t_i] = bf16(bf16(x_attn - x_act) + mlp)
 // and ln_out = LayerNorm(x_new) (of the bf16 x_new, exactly as the standalone kernel computes it).
@@ -355,6 +391,36 @@ extern "C" int oudjat_layernorm_rows_nvfp4(const uint16_t* x, int64_t rows, int6
                                            int64_t xhat_stride, oudjat_stream_t stream) {
   OUDJAT_REQUIRE(tensor_scale || rows == 0, OUDJAT_ERR_INVALID_ARGUMENT, "layernorm_rows_nvfp4: null tensor scale");
   return layernorm_launch(x, rows, C, xs, w, b, eps, tensor_scale, xhat, xhat_stride, stream, "layernorm_rows_nvfp4");
+}
+
+extern "C" int oudjat_gather_rows_ln(const uint16_t* x, int64_t stride_b, int64_t stride_n, int64_t C,
+                                     const int64_t* batch_idx, const int64_t* token_idx, int64_t rows,
+                                     const uint16_t* w, const uint16_t* b, float eps, const float* tensor_scale,
+                                     uint16_t* x_out, uint16_t* ln_out, oudjat_stream_t stream) {
+  const char* what = "gather_rows_ln";
+  OUDJAT_REQUIRE(rows >= 0 && C > 0, OUDJAT_ERR_INVALID_ARGUMENT, "%s: bad size", what);
+  if (rows == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(x && batch_idx && token_idx && w && b && x_out && ln_out, OUDJAT_ERR_INVALID_ARGUMENT,
+                 "%s: null pointer", what);
+  OUDJAT_REQUIRE(C % 8 == 0 && stride_b % 8 == 0 && stride_n % 8 == 0 && aligned(x, 16) && aligned(x_out, 16) &&
+                     aligned(ln_out, 16) && aligned(w, 16) && aligned(b, 16) && aligned(batch_idx, 8) &&
+                     aligned(token_idx, 8),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "%s: 16-byte aligned rows with C %% 8 == 0 required", what);
+  OUDJAT_REQUIRE(!tensor_scale || C % 16 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE, "%s: NVFP4 output needs C %% 16 == 0",
+                 what);
+  OUDJAT_REQUIRE(C <= 8192, OUDJAT_ERR_TOO_LARGE, "%s: C=%lld > 8192", what, (long long)C);
+  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg);
+  hipStream_t st = as_stream(stream);
+#define OUDJAT_GATHER_LN(CHV)                                                                                     \
+  gather_ln_kernel<CHV><<<grid, kNormThreads, 0, st>>>(x, stride_b, stride_n, batch_idx, token_idx, rows, (int)C, w, \
+                                                       b, eps, x_out, ln_out, tensor_scale)
+  if (C <= 512) OUDJAT_GATHER_LN(1);
+  else if (C <= 1024) OUDJAT_GATHER_LN(2);
+  else if (C <= 2048) OUDJAT_GATHER_LN(4);
+  else if (C <= 4096) OUDJAT_GATHER_LN(8);
+  else OUDJAT_GATHER_LN(16);
+#undef OUDJAT_GATHER_LN
+  return check_launch(what);
 }
 
 extern "C" int oudjat_rope_active_inplace(uint16_t* q, int64_t qst, int64_t qsh, uint16_t* k, int64_t kst, int64_t ksh,

@@ -796,10 +796,18 @@ def correct_blocks_packed(blocks, x: Tensor, dindice: Tensor, rope, cache_featur
     inplace = bool(kwargs.get("inplace_residual_add", False)) and not torch.is_grad_enabled()
     xc = x if x.is_contiguous() else x.contiguous()
     M = qs.active_token_idx.numel()
-    x_p = K.gather_rows(xc, qs.active_batch_idx, qs.active_token_idx) if M else xc.new_empty((0, xc.shape[-1]))
+    # norm1 of the next block on x_p (from the gather for block 0, from the fused residual + LayerNorm
+    # step after that), written as that block's NVFP4 qkv operand when xn_is_xhat
+    xn, xn_is_xhat = None, False
+    if M:
+        ts0 = _fp4_scale(blocks[0].attn.qkv)
+        n1 = blocks[0].norm1
+        x_p, xn = K.gather_rows_ln(xc, qs.active_batch_idx, qs.active_token_idx, n1.weight, n1.bias, n1.eps,
+                                   nvfp4_scale=ts0)
+        xn_is_xhat = ts0 is not None
+    else:
+        x_p = xc.new_empty((0, xc.shape[-1]))
     bos_list = []
-    xn = None  # norm1 of the next block on x_p, from the fused residual + LayerNorm step
-    xn_is_xhat = False  # ... written as the next block's NVFP4 qkv operand
     for i, (blk, tag) in enumerate(zip(blocks, tags)):
         if i == 0:
             plan, kv, bos = plan0, cache_feature[f"{tag}_kv"], cache_feature[f"{tag}_blocks_out_sum"]

@@ -595,6 +595,29 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: f
     return out
 
 
+def gather_rows_ln(src: torch.Tensor, batch_idx: torch.Tensor, token_idx: torch.Tensor, weight: torch.Tensor,
+                   bias: torch.Tensor, eps: float = 1e-5,
+                   nvfp4_scale: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
+    """(gather_rows(src, batch_idx, token_idx), layer_norm of those rows) in one launch, bit-identical to
+    the two calls; src [B, N, C] bf16 with contiguous rows. With nvfp4_scale the second result is the
+    NVFP4 operand x_hat of the LayerNorm, as layer_norm(..., nvfp4_scale=) gives it."""
+    _require_cuda(src, batch_idx, token_idx, weight, bias)
+    _require(src.dim() == 3 and src.stride(2) == 1 and src.dtype == weight.dtype == bias.dtype == torch.bfloat16,
+             "gather_rows_ln: src must be [B, N, C] bf16 with contiguous rows")
+    ts = _nvfp4_scale(nvfp4_scale, "gather_rows_ln")
+    bi, ti = _index(batch_idx, "batch_idx"), _index(token_idx, "token_idx")
+    _require(bi.numel() == ti.numel(), "gather_rows_ln: index length mismatch")
+    n, C = bi.numel(), src.shape[2]
+    x_out = torch.empty((n, C), device=src.device, dtype=src.dtype)
+    ln_out = torch.empty((n, C), device=src.device, dtype=src.dtype)
+    if n == 0:
+        return x_out, ln_out
+    _launch("gather_rows", src, "oudjat_gather_rows_ln", _ptr(src), src.stride(0), src.stride(1), C, _ptr(bi),
+            _ptr(ti), n, _ptr(weight.contiguous()), _ptr(bias.contiguous()), float(eps), _ptr(ts), _ptr(x_out),
+            _ptr(ln_out), _stream(src))
+    return x_out, ln_out
+
+
 def apply_rope_active_inplace(q_active: torch.Tensor, k_active: torch.Tensor, rope, patch_mask: torch.Tensor,
                               rope_idx: torch.Tensor) -> None:
     """Rotate-half RoPE on [T, H, Dh] q and k views in place, fp32 math; rows with patch_mask False
@@ -914,17 +937,18 @@ def patch_attention_prob(q: torch.Tensor, kv_cache: torch.Tensor, scale: float, 
     """The mean attention probability of every key over heads and all queries -> [B, N] bf16.
 
     q [B * N, H, Dh] (the approx pass's packed queries after RoPE, contiguous heads), kv_cache
-    [B, N, 2, H, Dh] (K after RoPE). `workspace` (fp32, >= 2*B*H*N) holds the row statistics; one is
-    allocated when not given."""
+    [B, N, 2, H, Dh] (K after RoPE). `workspace` (fp32, >= oudjat_patch_attention_prob_workspace_elems)
+    holds the row statistics and partial column sums; one is allocated when not given."""
     _require_cuda(q, kv_cache, workspace)
     _kv_k_view_ok(kv_cache)
     B, N, _, H, Dh = kv_cache.shape
     _require(q.dim() == 3 and q.shape == (B * N, H, Dh) and q.stride(2) == 1 and q.stride(1) == Dh
              and q.dtype == torch.bfloat16, "patch_attention_prob: q must be [B*N, H, Dh] bf16 with packed heads")
+    need = int(_lib.load().oudjat_patch_attention_prob_workspace_elems(B, N, H, int(mode)))
     if workspace is None:
-        workspace = torch.empty((2 * B * H * N,), device=q.device, dtype=torch.float32)
-    _require(workspace.dtype == torch.float32 and workspace.is_contiguous() and workspace.numel() >= 2 * B * H * N,
-             "patch_attention_prob: workspace must be contiguous fp32 with 2*B*H*N elements")
+        workspace = torch.empty((need,), device=q.device, dtype=torch.float32)
+    _require(workspace.dtype == torch.float32 and workspace.is_contiguous() and workspace.numel() >= need,
+             f"patch_attention_prob: workspace must be contiguous fp32 with {need} elements")
     out = torch.empty((B, N), device=q.device, dtype=torch.bfloat16)
     _launch("pscore", q, "oudjat_patch_attention_prob", _ptr(q), q.stride(0), B, N, H, Dh, _ptr(kv_cache),
             kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(3), float(scale), int(mode), _ptr(workspace),

@@ -47,7 +47,7 @@ def kernel_stats(path: str, passes: int, title: str, cmd: str) -> str:
     setup = [r for r in rows if int(r["Calls"]) % passes != 0]
     ptot = sum(float(r["TotalDurationNs"]) for r in per)
     out = [f"# {title}", "", "Command (run from the repository root on one MI355X):", "", "```", cmd, "```", "",
-           f"`rocprofv3 --kernel-trace --stats` kernel_stats.csv, {passes} correction passes in the trace "
+           f"`rocprofv3 --kernel-trace --stats` kernel_stats.csv, {passes} passes in the trace "
            "(warm-up + timed); per-pass time = total / passes.", "",
            "| kernel | calls | avg us | per-pass us | share |", "|---|---:|---:|---:|---:|"]
     for r in sorted(per, key=lambda r: -float(r["TotalDurationNs"])):
@@ -56,7 +56,7 @@ def kernel_stats(path: str, passes: int, title: str, cmd: str) -> str:
             continue
         out.append(f"| `{_short(r['Name'])}` | {r['Calls']} | {float(r['AverageNs']) / 1e3:.2f} | "
                    f"{t / passes / 1e3:.1f} | {100 * t / ptot:.1f}% |")
-    out.append(f"| **correction pass, all kernels** | | | **{ptot / passes / 1e3:.1f}** | 100% |")
+    out.append(f"| **one pass, all kernels** | | | **{ptot / passes / 1e3:.1f}** | 100% |")
     out += ["", "One-time setup kernels in the same trace (synthetic data and cache generation, not part of a pass):",
             ""]
     out += [f"- `{_short(r['Name'])}`: {r['Calls']} calls, {float(r['TotalDurationNs']) / 1e3:.0f} us total"

@@ -426,12 +426,17 @@ int oudjat_pseudo_query(const uint16_t* q, int64_t q_stride_b, int64_t q_stride_
  * q [B * N, H, Dh] packed rows (row stride q_row_stride elements, after RoPE); K [b, n, h, :] at
  * kv + b*kv_stride_b + n*kv_stride_n + h*kv_stride_h (the K half of {tag}_kv). q . k is an fp32 MFMA
  * accumulation and exp is the fp32 device exponential: agreement with an exact evaluation is to fp32
- * rounding before each bf16 rounding. workspace: 2 * B * H * N fp32 (row statistics). out [B, N] bf16
- * (row stride out_stride_b). Dh in {64, 128}; 16-byte aligned rows. */
+ * rounding before each bf16 rounding. workspace: oudjat_patch_attention_prob_workspace_elems(B, N, H,
+ * mode) fp32 (row statistics, then partial column sums). out [B, N] bf16 (row stride out_stride_b).
+ * Dh in {64, 128}; 16-byte aligned rows. */
 int oudjat_patch_attention_prob(const uint16_t* q, int64_t q_row_stride, int64_t B, int64_t N, int64_t H,
                                 int64_t Dh, const uint16_t* kv, int64_t kv_stride_b, int64_t kv_stride_n,
                                 int64_t kv_stride_h, float scale, int mode, float* workspace, uint16_t* out,
                                 int64_t out_stride_b, oudjat_stream_t stream);
+
+/* fp32 elements of the workspace oudjat_patch_attention_prob needs for this shape and mode (the same
+ * call site, attention.py:241-253): 2*B*H*N, plus B*ceil(N/128)*N in mode 0. */
+int64_t oudjat_patch_attention_prob_workspace_elems(int64_t B, int64_t N, int64_t H, int mode);
 
 /* Mode 1 of oudjat_patch_attention_prob given the attention's row log-sum-exp instead of computing it
  * (the key-side kernel of attention_pscore.py:20-98 after cuDNN's LSE, :172-241): one pass over the
@@ -531,6 +536,18 @@ int oudjat_linear_qkv_rope_kv_fp8(const uint8_t* A, int64_t M, int64_t K, int64_
 int oudjat_layernorm_rows_nvfp4(const uint16_t* x, int64_t rows, int64_t C, int64_t x_stride, const uint16_t* weight,
                                 const uint16_t* bias, float eps, const float* tensor_scale, uint16_t* xhat,
                                 int64_t xhat_stride, oudjat_stream_t stream);
+
+/* Rows 4 and 5 fused for the first block of a packed run (the gather of the selected rows,
+ * token_update.py:455-473, then norm1, block.py:1114): packed row i = x[batch_idx[i], token_idx[i]]
+ * (x with element strides stride_b, stride_n, rows of C contiguous bf16) is copied to x_out [rows, C]
+ * byte for byte, and its LayerNorm goes to ln_out [rows, C] -- bit-identical to oudjat_gather_rows
+ * followed by oudjat_layernorm_rows, or with tensor_scale non-NULL to oudjat_layernorm_rows_nvfp4
+ * (the NVFP4 operand of the LayerNorm output). int64 indices; 16-byte aligned rows, C % 8 == 0
+ * (C % 16 == 0 for the NVFP4 output), C <= 8192. */
+int oudjat_gather_rows_ln(const uint16_t* x, int64_t stride_b, int64_t stride_n, int64_t C,
+                          const int64_t* batch_idx, const int64_t* token_idx, int64_t rows, const uint16_t* w,
+                          const uint16_t* b, float eps, const float* tensor_scale, uint16_t* x_out,
+                          uint16_t* ln_out, oudjat_stream_t stream);
 int oudjat_packed_residual_persist_ln_nvfp4(const uint16_t* x_act, const uint16_t* x_attn, const uint16_t* mlp,
                                             int64_t rows, int64_t C, const int64_t* batch_idx,
                                             const int64_t* token_idx, uint16_t* bos, int64_t bos_stride_b,

@@ -53,7 +53,9 @@ def _check_gemm(dev, got, x, w, b, what):
                                     (1712, 3072, 1024), (1712, 4096, 1024), (8272, 3072, 1024), (8272, 4096, 1024),
                                     (1656, 12288, 4096), (1656, 4096, 4096), (1656, 4096, 8192),
                                     (414, 12288, 4096), (414, 4096, 4096), (414, 8192, 4096), (414, 4096, 8192),
-                                    (1712, 1024, 1024), (2088, 768, 768), (8272, 1024, 1024), (8272, 1024, 4096)])
+                                    (1712, 1024, 1024), (2088, 768, 768), (8272, 1024, 1024), (8272, 1024, 4096),
+                                    # approximate-pass grids (M = B N), several rounds of 288 x 256 tiles
+                                    (16464, 4096, 1024), (16404, 8192, 4096), (16404, 4096, 4096)])
 def test_linear_bias(dev, M, N, Kd):
     x, w, b = _rand((M, Kd), 1), _rand((N, Kd), 2, 0.02), _rand((N,), 3, 0.1)
     got = K.linear(x.to(dev), w.to(dev), b.to(dev))
@@ -262,7 +264,7 @@ def test_qkv_rope_kv_scatter_bit_exact(dev, B, T, H, D):
 
 @pytest.mark.parametrize("B,T,H,D,Kd", [(16, 261, 16, 64, 1024), (1, 103, 6, 64, 384), (2, 50, 32, 128, 512),
                                         (16, 107, 16, 64, 1024), (16, 517, 16, 64, 1024), (4, 414, 32, 128, 4096),
-                                        (1, 414, 32, 128, 4096)])
+                                        (1, 414, 32, 128, 4096), (16, 1029, 16, 64, 1024), (4, 1029, 32, 128, 4096)])
 def test_linear_qkv_rope_kv_fused_equals_unfused(dev, B, T, H, D, Kd):
     """The fused QKV GEMM (qkv never materialised). Its raw bf16(acc + bias) values, taken from a run
     with no patch rows (no RoPE), are checked against the fp64 oracle like every GEMM; the pinned

@@ -34,6 +34,24 @@ def test_gather_rows(dev, B, N, C, T):
     assert_bits_equal(got, ref, "gather_rows")
 
 
+@pytest.mark.parametrize("B,N,C,T,fp4", [(16, 1029, 1024, 261, False), (4, 1029, 4096, 414, False),
+                                         (1, 201, 384, 103, False), (3, 7, 8, 5, False), (4, 1029, 4096, 414, True),
+                                         (2, 40, 384, 17, True)])
+def test_gather_rows_ln_equals_gather_then_layernorm(dev, B, N, C, T, fp4):
+    """The packed run's first step (gather + block 0's norm1, optionally as the NVFP4 qkv operand) in one
+    launch: the gathered rows equal the oracle's gather and the LayerNorm equals the standalone kernel's
+    on them, bit for bit (the standalone kernel is pinned against the oracle elsewhere)."""
+    x = _rand_bf16((B, N, C), 2)
+    bi, ti = _sel(B, N, T, 3)
+    w = (1.0 + 0.1 * _rand_bf16((C,), 4).float()).to(torch.bfloat16).to(dev)
+    b = (0.1 * _rand_bf16((C,), 5).float()).to(torch.bfloat16).to(dev)
+    ts = torch.tensor([0.37], device=dev) if fp4 else None
+    xd = x.to(dev)
+    xp, xn = K.gather_rows_ln(xd, bi.to(dev), ti.to(dev), w, b, 1e-6, nvfp4_scale=ts)
+    assert_bits_equal(xp, R.gather_rows(bits(x), bi.numpy(), ti.numpy()), "gathered rows")
+    assert_bits_equal(xn, K.layer_norm(xp, w, b, 1e-6, nvfp4_scale=ts).cpu(), "LayerNorm of the gathered rows")
+
+
 def test_gather_rows_empty(dev):
     x = _rand_bf16((2, 5, 64), 0).to(dev)
     e = torch.empty(0, dtype=torch.long, device=dev)
