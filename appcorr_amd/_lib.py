@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be loaded before the HIP library, see module docstring
 
 LIB_PATH = Path(__file__).resolve().parent / "liboudjat_hip.so"
-ABI_VERSION = 14
+ABI_VERSION = 15
 
 OK = 0
 STATUS_NAMES = {
@@ -35,6 +35,7 @@ EPI_BIAS_GELU = 1
 EPI_BIAS_LS_RESID = 2
 EPI_BIAS_LS = 3
 EPI_BIAS_SILU_MUL = 4
+EPI_RAW_BF16 = 16  # flag: round the accumulator to bf16 before the scale and bias (NVFP4 linears)
 
 QUERY_PROB_NOALLOC_MAX = 1 << 20  # OUDJAT_QUERY_PROB_NOALLOC_MAX: fp32 elements of the no-alloc scratch array
 
@@ -99,6 +100,8 @@ SIGNATURES: dict[str, list] = {
     "oudjat_fold_residual_rows": [_p, _i64, _i64, _p, _p, _p, _i64, _p, _p],
     "oudjat_linear_qkv_rope_kv": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p, _p,
                                   _i64, _i64, _p, _f32, _p],
+    "oudjat_linear_qkv_rope_kv_nvfp4": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p,
+                                        _p, _p, _i64, _i64, _p, _f32, _p],
     "oudjat_sparse_query_attention": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32, _p,
                                       _i64, _p],
     "oudjat_sparse_query_attention_ws": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32,
@@ -107,6 +110,7 @@ SIGNATURES: dict[str, list] = {
     "oudjat_sparse_query_attention_lse": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32,
                                           _p, _i64, _p, _p],
     "oudjat_patch_attention_prob_workspace_elems": [_i64, _i64, _i64, _i32],
+    "oudjat_residual_pair": [_p, _p, _p, _i64, _i64, _p, _p, _p],
     "oudjat_gather_rows_ln": [_p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _f32, _p, _p, _p, _p],
     "oudjat_patch_attention_prob_lse": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _f32, _p, _p, _p,
                                         _i64, _p],

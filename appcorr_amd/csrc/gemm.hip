@@ -79,7 +79,24 @@ struct EpiArgs {
   int64_t ldr;
   QkvArgs qkv;
   float acc_scale;
+  // NVFP4 linears (OUDJAT_EPI_RAW_BF16): the accumulator is rounded to bf16 before acc_scale and the
+  // bias, v = bf16(bf16(acc) * acc_scale + bias) -- the reference's _scaled_mm writes its bf16 output
+  // and scales it afterwards (fp4_fast_linear.py:221-283).
+  int raw_round;
 };
+
+// The accumulators of a tile rounded to bf16 in place (OUDJAT_EPI_RAW_BF16), once, before the
+// epilogue's first rounding point.
+template <typename V, int FM, int FN>
+__device__ __forceinline__ void round_acc_bf16(V (&acc)[FM][FN]) {
+  constexpr int NV = sizeof(V) / sizeof(float);
+#pragma unroll
+  for (int i = 0; i < FM; ++i)
+#pragma unroll
+    for (int j = 0; j < FN; ++j)
+#pragma unroll
+      for (int v = 0; v < NV; ++v) acc[i][j][v] = round_bf16(acc[i][j][v]);
+}
 
 // Two fp32 -> packed bf16 pair (low half = a) with the hardware round-to-nearest-even convert.
 typedef float f32x2_t __attribute__((ext_vector_type(2)));
@@ -127,7 +144,8 @@ __device__ __forceinline__ uint32_t gelu_pair_bits(uint32_t w, const uint16_t* l
 
 template <int EPI>
 __device__ __forceinline__ float epilogue(float acc, int64_t row, int64_t col, const EpiArgs& ea) {
-  float v = round_bf16(__builtin_fmaf(acc, ea.acc_scale, ea.bias ? bf16_to_f32(ea.bias[col]) : 0.0f));
+  const float a = ea.raw_round ? round_bf16(acc) : acc;
+  float v = round_bf16(__builtin_fmaf(a, ea.acc_scale, ea.bias ? bf16_to_f32(ea.bias[col]) : -0.0f));
   if (EPI == OUDJAT_EPI_BIAS_GELU) {
     v = __uint_as_float(gelu_bf16_bits(__float_as_uint(v) >> 16, g_gelu_lut) << 16);
   } else if (EPI == OUDJAT_EPI_BIAS_LS_RESID) {
@@ -473,10 +491,11 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
 }
 
 template <int BM, int BN, int FM, int FN, int NW, int EPI>
-__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FM][FN], unsigned char* smem, const uint16_t* lut,
+__device__ __forceinline__ void store_tile(f32x16_t (&acc)[FM][FN], unsigned char* smem, const uint16_t* lut,
                                            int wm0, int wn0, int m0, int n0, int M, const EpiArgs& ea,
                                            uint16_t* __restrict__ C, int64_t ldc) {
   const int lane = threadIdx.x & 63;
+  if (ea.raw_round) round_acc_bf16(acc);
   constexpr int LDT = BN + 8;
   uint16_t* ct = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
@@ -484,7 +503,7 @@ __device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FM][FN], unsign
 #pragma unroll
     for (int g = 0; g < 4; ++g) {
       const int cl = wn0 + j * 32 + g * 8 + 4 * (lane >> 5);
-      float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+      float b0 = -0.0f, b1 = -0.0f, b2 = -0.0f, b3 = -0.0f;
       if (ea.bias) {
         const uint2 bw = *reinterpret_cast<const uint2*>(ea.bias + n0 + cl);
         b0 = lo_bf16(bw.x); b1 = hi_bf16(bw.x); b2 = lo_bf16(bw.y); b3 = hi_bf16(bw.y);
@@ -951,11 +970,12 @@ __device__ __forceinline__ void r16_epilogue(f32x4_t (&acc)[FMB][FNB], unsigned 
     }
     return;
   }
+  if (ea.raw_round) round_acc_bf16(acc);
   if constexpr (WGM > 1 && KSPLIT == 1 && RED == 0 && BM * LDT * 2 <= TILE_BYTES) {
 #pragma unroll
     for (int j = 0; j < FNB; ++j) {
       const int cl = wn0 + j * 16 + 4 * (lane >> 4);
-      float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+      float b0 = -0.0f, b1 = -0.0f, b2 = -0.0f, b3 = -0.0f;
       if (ea.bias) {
         const uint2 bw = *reinterpret_cast<const uint2*>(ea.bias + n0 + cl);
         b0 = lo_bf16(bw.x); b1 = hi_bf16(bw.x); b2 = lo_bf16(bw.y); b3 = hi_bf16(bw.y);
@@ -986,7 +1006,7 @@ __device__ __forceinline__ void r16_epilogue(f32x4_t (&acc)[FMB][FNB], unsigned 
 #pragma unroll
       for (int j = 0; j < FNB; ++j) {
         const int cl = wn0 + j * 16 + 4 * (lane >> 4);
-        float b0 = 0.0f, b1 = 0.0f, b2 = 0.0f, b3 = 0.0f;
+        float b0 = -0.0f, b1 = -0.0f, b2 = -0.0f, b3 = -0.0f;
         if (ea.bias) {
           const uint2 bw = *reinterpret_cast<const uint2*>(ea.bias + n0 + cl);
           b0 = lo_bf16(bw.x); b1 = hi_bf16(bw.x); b2 = lo_bf16(bw.y); b3 = hi_bf16(bw.y);
@@ -1540,7 +1560,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
     bias[4] = lo_bf16(b1.x); bias[5] = hi_bf16(b1.x); bias[6] = lo_bf16(b1.y); bias[7] = hi_bf16(b1.y);
   } else {
 #pragma unroll
-    for (int e = 0; e < 8; ++e) bias[e] = 0.0f;
+    for (int e = 0; e < 8; ++e) bias[e] = -0.0f;  // fma(a, s, -0) = a * s, the sign of a zero kept
   }
   if constexpr (EPI == OUDJAT_EPI_BIAS_LS || EPI == OUDJAT_EPI_BIAS_LS_RESID)
     unpack8(*reinterpret_cast<const uint4*>(ea.gamma + col), g);
@@ -1564,7 +1584,7 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   float v[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    float x = round_bf16(__builtin_fmaf(acc[e], ea.acc_scale, bias[e]));
+    float x = round_bf16(__builtin_fmaf(ea.raw_round ? round_bf16(acc[e]) : acc[e], ea.acc_scale, bias[e]));
     if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) x = __uint_as_float(gelu_bf16_bits(__float_as_uint(x) >> 16, g_gelu_lut) << 16);
     else if constexpr (EPI == OUDJAT_EPI_BIAS_LS_RESID) x = fmaf(x, g[e], side[e]);
     else if constexpr (EPI == OUDJAT_EPI_BIAS_LS) x = x * g[e];
@@ -1960,6 +1980,8 @@ extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64
                                   const uint16_t* resid, int64_t ldr, uint16_t* C, int64_t ldc, float acc_scale,
                                   float* workspace, int64_t workspace_elems, oudjat_stream_t stream) {
   OUDJAT_REQUIRE(M >= 0 && N >= 0 && K >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_bf16: negative size");
+  const int raw_round = (epi & OUDJAT_EPI_RAW_BF16) != 0;
+  epi &= ~OUDJAT_EPI_RAW_BF16;
   OUDJAT_REQUIRE(epi >= OUDJAT_EPI_BIAS && epi <= OUDJAT_EPI_BIAS_SILU_MUL, OUDJAT_ERR_INVALID_ARGUMENT,
                  "linear_bf16: bad epilogue %d", epi);
   if (M == 0 || N == 0) return OUDJAT_OK;
@@ -1984,6 +2006,7 @@ extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64
   ea.resid = resid;
   ea.ldr = ldr;
   ea.acc_scale = acc_scale;
+  ea.raw_round = raw_round;
   if (workspace && aligned_io && aligned(workspace, 16)) {
     int S = 1;
     const int ci = choose_splitk(M, N, K, epi, &S);
@@ -2022,18 +2045,18 @@ extern "C" int oudjat_linear_splitk_partial(const uint16_t* A, int64_t M, int64_
 
 // fp32 elements of workspace a linear_bf16 call of this shape can use for split K (0: it never splits).
 extern "C" int64_t oudjat_linear_workspace_elems(int64_t M, int64_t N, int64_t K, int epi) {
+  epi &= ~OUDJAT_EPI_RAW_BF16;
   int S = 1;
   if (M <= 0 || N <= 0 || K <= 0 || choose_splitk(M, N, K, epi, &S) < 0 || S <= 1) return 0;
   return (int64_t)S * M * N;
 }
 
-extern "C" int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
-                                         int64_t ldw, const uint16_t* bias, int64_t H, int64_t Dh,
-                                         const float* sin_table, const float* cos_table, int64_t table_stride,
-                                         const uint8_t* patch_mask, const int64_t* rope_idx,
-                                         const int64_t* batch_idx, const int64_t* token_idx, uint16_t* kv,
-                                         int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
-                                         float acc_scale, oudjat_stream_t stream) {
+static int linear_qkv_rope_kv_impl(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                                   int64_t ldw, const uint16_t* bias, int64_t H, int64_t Dh, const float* sin_table,
+                                   const float* cos_table, int64_t table_stride, const uint8_t* patch_mask,
+                                   const int64_t* rope_idx, const int64_t* batch_idx, const int64_t* token_idx,
+                                   uint16_t* kv, int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
+                                   float acc_scale, int raw_round, oudjat_stream_t stream) {
   OUDJAT_REQUIRE(M >= 0 && K >= 0 && H > 0 && Dh > 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_qkv_rope_kv: bad size");
   if (M == 0) return OUDJAT_OK;
   const int64_t N = 3 * H * Dh;
@@ -2054,10 +2077,36 @@ extern "C" int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K
   EpiArgs ea{};
   ea.bias = bias;
   ea.acc_scale = acc_scale;
+  ea.raw_round = raw_round;
   ea.qkv = QkvArgs{(int)H, (int)Dh, sin_table, cos_table, table_stride, patch_mask, rope_idx, batch_idx, token_idx,
                    kv, kv_stride_b, kv_stride_n, q_out};
   return launch_gemm(choose_qkv_cfg(M, N, K, Dh), A, M, K, lda, W, N, ldw, kEpiQkv, ea, nullptr, 0, as_stream(stream),
                      "linear_qkv_rope_kv");
+}
+
+extern "C" int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                                         int64_t ldw, const uint16_t* bias, int64_t H, int64_t Dh,
+                                         const float* sin_table, const float* cos_table, int64_t table_stride,
+                                         const uint8_t* patch_mask, const int64_t* rope_idx,
+                                         const int64_t* batch_idx, const int64_t* token_idx, uint16_t* kv,
+                                         int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
+                                         float acc_scale, oudjat_stream_t stream) {
+  return linear_qkv_rope_kv_impl(A, M, K, lda, W, ldw, bias, H, Dh, sin_table, cos_table, table_stride, patch_mask,
+                                 rope_idx, batch_idx, token_idx, kv, kv_stride_b, kv_stride_n, q_out, acc_scale, 0,
+                                 stream);
+}
+
+extern "C" int oudjat_linear_qkv_rope_kv_nvfp4(const uint16_t* A, int64_t M, int64_t K, int64_t lda,
+                                               const uint16_t* W, int64_t ldw, const uint16_t* bias, int64_t H,
+                                               int64_t Dh, const float* sin_table, const float* cos_table,
+                                               int64_t table_stride, const uint8_t* patch_mask,
+                                               const int64_t* rope_idx, const int64_t* batch_idx,
+                                               const int64_t* token_idx, uint16_t* kv, int64_t kv_stride_b,
+                                               int64_t kv_stride_n, uint16_t* q_out, float out_scale,
+                                               oudjat_stream_t stream) {
+  return linear_qkv_rope_kv_impl(A, M, K, lda, W, ldw, bias, H, Dh, sin_table, cos_table, table_stride, patch_mask,
+                                 rope_idx, batch_idx, token_idx, kv, kv_stride_b, kv_stride_n, q_out, out_scale, 1,
+                                 stream);
 }
 
 static int kernel_name_of(const GemmCfg& c, int epi, char* buf, int64_t buflen);

@@ -89,12 +89,23 @@ __global__ void __launch_bounds__(kPsThreads) query_prob_kernel(const uint16_t* 
   float qa[8];
   unpack8(*reinterpret_cast<const uint4*>(q + b * q_sb + h * q_sh + lane_in_key * 8), qa);
   const uint16_t* kb = k + b * k_sb + h * k_sh + lane_in_key * 8;
-  for (int n0 = 0; n0 < N; n0 += kKeysPerIter) {
-    const int n = n0 + key_slot;
-    double part = 0.0;
-    if (n < N) part = dot8_f64(qa, *reinterpret_cast<const uint4*>(kb + (int64_t)n * k_sn));
-    const double dot = group_sum_f64(part, L);
-    if (n < N && lane_in_key == 0) srow[n] = round_bf16(round_bf16((float)dot) * scale);
+  // kUnroll key rows per thread group in flight before their dot products (each sum is exact, so the
+  // grouping changes no bit).
+  constexpr int kUnroll = 8;
+  for (int n0 = 0; n0 < N; n0 += kKeysPerIter * kUnroll) {
+    uint4 kr[kUnroll];
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int n = n0 + u * kKeysPerIter + key_slot;
+      kr[u] = make_uint4(0, 0, 0, 0);
+      if (n < N) kr[u] = *reinterpret_cast<const uint4*>(kb + (int64_t)n * k_sn);
+    }
+#pragma unroll
+    for (int u = 0; u < kUnroll; ++u) {
+      const int n = n0 + u * kKeysPerIter + key_slot;
+      const double dot = group_sum_f64(dot8_f64(qa, kr[u]), L);
+      if (n < N && lane_in_key == 0) srow[n] = round_bf16(round_bf16((float)dot) * scale);
+    }
   }
   __syncthreads();
   float m = -INFINITY;

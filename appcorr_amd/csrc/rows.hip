@@ -249,6 +249,53 @@ __global__ __launch_bounds__(kRowThreads) void layerscale_add_kernel(
   }
 }
 
+// The approximate block's two residual sums in one pass (block.py:336-347): the cached
+// blocks_out_sum = bf16(inc + mlp) (inc = ls1(attn)) and the block output bf16(x_attn + mlp). One wave
+// per row, every load of the row issued before the first store.
+template <int CH>
+__global__ __launch_bounds__(kRowThreads) void residual_pair_kernel(const uint16_t* __restrict__ inc,
+                                                                   const uint16_t* __restrict__ xa,
+                                                                   const uint16_t* __restrict__ mlp, int64_t rows,
+                                                                   int64_t C, uint16_t* __restrict__ bos,
+                                                                   uint16_t* __restrict__ out) {
+  const int64_t row = (int64_t)blockIdx.x * kRowsPerWg + (threadIdx.x >> 6);
+  if (row >= rows) return;
+  const int lane = threadIdx.x & 63;
+  const int chunks = (int)(C >> 3);
+  const uint4* iv = reinterpret_cast<const uint4*>(inc + row * C);
+  const uint4* av = reinterpret_cast<const uint4*>(xa + row * C);
+  const uint4* mv = reinterpret_cast<const uint4*>(mlp + row * C);
+  uint4 ri[CH], ra[CH], rm[CH];
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) {
+      ri[j] = iv[c];
+      ra[j] = av[c];
+      rm[j] = mv[c];
+    }
+  }
+  uint4* bv = reinterpret_cast<uint4*>(bos + row * C);
+  uint4* ov = reinterpret_cast<uint4*>(out + row * C);
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) {
+      float fi[8], fa[8], fm[8], fb[8], fo[8];
+      unpack8(ri[j], fi);
+      unpack8(ra[j], fa);
+      unpack8(rm[j], fm);
+#pragma unroll
+      for (int e = 0; e < 8; ++e) {
+        fb[e] = fi[e] + fm[e];
+        fo[e] = fa[e] + fm[e];
+      }
+      bv[c] = pack8(fb);
+      ov[c] = pack8(fo);
+    }
+  }
+}
+
 // vec: rows are 16-byte aligned with dim % 4 == 0, so a lane reads 16-byte vectors, four in flight
 // (a 1024-wide row is one round of four loads per lane).
 __global__ __launch_bounds__(kRowThreads) void patch_importance_kernel(
@@ -391,6 +438,25 @@ extern "C" int oudjat_fused_layerscale_add(const uint16_t* x, const uint16_t* a,
                  OUDJAT_ERR_UNSUPPORTED_LAYOUT, "fused_layerscale_add: 16-byte aligned rows with C %% 8 == 0 required");
   layerscale_add_kernel<<<(unsigned)cdiv(rows, kRowsPerWg), kRowThreads, 0, as_stream(stream)>>>(x, a, g, rows, C, o);
   return check_launch("fused_layerscale_add");
+}
+
+extern "C" int oudjat_residual_pair(const uint16_t* inc, const uint16_t* x_attn, const uint16_t* mlp, int64_t rows,
+                                    int64_t C, uint16_t* bos, uint16_t* out, oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(rows >= 0 && C >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "residual_pair: negative size");
+  if (rows == 0 || C == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(inc && x_attn && mlp && bos && out, OUDJAT_ERR_INVALID_ARGUMENT, "residual_pair: null pointer");
+  OUDJAT_REQUIRE(C % 8 == 0 && aligned(inc, 16) && aligned(x_attn, 16) && aligned(mlp, 16) && aligned(bos, 16) &&
+                     aligned(out, 16),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "residual_pair: 16-byte aligned rows with C %% 8 == 0 required");
+  OUDJAT_REQUIRE(C <= 8192, OUDJAT_ERR_TOO_LARGE, "residual_pair: C=%lld > 8192", (long long)C);
+  const unsigned grid = (unsigned)cdiv(rows, kRowsPerWg);
+  const hipStream_t st = as_stream(stream);
+  if (C <= 512) residual_pair_kernel<1><<<grid, kRowThreads, 0, st>>>(inc, x_attn, mlp, rows, C, bos, out);
+  else if (C <= 1024) residual_pair_kernel<2><<<grid, kRowThreads, 0, st>>>(inc, x_attn, mlp, rows, C, bos, out);
+  else if (C <= 2048) residual_pair_kernel<4><<<grid, kRowThreads, 0, st>>>(inc, x_attn, mlp, rows, C, bos, out);
+  else if (C <= 4096) residual_pair_kernel<8><<<grid, kRowThreads, 0, st>>>(inc, x_attn, mlp, rows, C, bos, out);
+  else residual_pair_kernel<16><<<grid, kRowThreads, 0, st>>>(inc, x_attn, mlp, rows, C, bos, out);
+  return check_launch("residual_pair");
 }
 
 extern "C" int oudjat_patch_importance(const float* d, int64_t rows, int64_t dim, int64_t rs, int mode, float* out,

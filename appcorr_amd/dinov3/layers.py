@@ -52,16 +52,40 @@ def _linear_route(mod: nn.Module, x: Tensor, site: str, *, bias: Tensor | None =
     return K.linear(x, mod.weight, b, site=site, **kw)
 
 
+_IDENTITY_PLANS: Dict[tuple, "PackedQueryState"] = {}
+
+
+def _identity_query_state(B: int, N: int, prefix: int, dev: torch.device) -> "PackedQueryState":
+    """The approximate pass's plan (every token of every image is a query, T = N), built once per
+    (B, N, prefix, device) and shared by every block and pass: its tensors are only read."""
+    key = (B, N, prefix, str(dev))
+    qs = _IDENTITY_PLANS.get(key)
+    if qs is None:
+        tok = torch.arange(N, device=dev, dtype=torch.long)
+        qs = PackedQueryState(
+            active_batch_idx=torch.arange(B, device=dev, dtype=torch.long).repeat_interleave(N),
+            active_pos_idx=tok.repeat(B), active_token_idx=tok.repeat(B),
+            query_valid_mask=torch.ones((B, N), device=dev, dtype=torch.bool),
+            active_query_pos_padded=tok.unsqueeze(0).expand(B, -1), active_query_mask=None, all_valid=True,
+            active_patch_mask=(tok >= prefix).repeat(B), active_rope_idx=(tok - prefix).clamp_min(0).repeat(B))
+        if len(_IDENTITY_PLANS) >= 16:
+            _IDENTITY_PLANS.clear()
+        _IDENTITY_PLANS[key] = qs
+    return qs
+
+
 def _fp4_scale(mod: nn.Module) -> Tensor | None:
     """The NVFP4 activation scale of a frozen FastFP4Linear (its input's producer then writes the NVFP4
     operand x_hat directly), else None."""
     return mod.act_scale if LP.low_precision_state(mod) == "fp4" else None
 
 
-def _fp4_raw(mod: "LP.FastFP4Linear", x: Tensor, site: str):
-    """A frozen FastFP4Linear's torch._scaled_mm output bf16(x_hat . W_hat^T) with the factors of its
-    epilogue: (raw, out_scale, bias) (fp4_fast_linear.py:221-249)."""
-    return mod.forward_raw(x, site=site), mod.out_scale_f, mod.bias
+def _fp4_linear(mod: "LP.FastFP4Linear", x: Tensor, site: str, epilogue: int = _lib.EPI_BIAS, **kw) -> Tensor:
+    """A frozen FastFP4Linear (fp4_fast_linear.py:221-283): torch._scaled_mm's bf16 output
+    bf16(x_hat . W_hat^T), then bf16(. * out_scale + bias), then `epilogue`'s LayerScale / residual --
+    one GEMM with the accumulator rounded to bf16 before the scale (EPI_RAW_BF16)."""
+    return K.linear(mod.quantize(x), mod.weight_hat, mod.bias, epilogue=epilogue | _lib.EPI_RAW_BF16,
+                    acc_scale=mod.out_scale_f, site=site, **kw)
 
 
 # ------------------------------------------------------------------------------------------------
@@ -196,7 +220,7 @@ class SelfAttention(nn.Module):
         kv = cache_feature[f"{tag}_kv"]
         q_packed, attn = self._qkv_attention(x_sel, rope, kv, fixed_query_state)
         if LP.low_precision_state(self.proj) == "fp4":
-            out = K.scale_bias(*_fp4_raw(self.proj, attn, "proj"))
+            out = _fp4_linear(self.proj, attn, "proj")
         else:
             out = _linear_route(self.proj, attn, "proj")
         return out, cache_feature
@@ -216,12 +240,19 @@ class SelfAttention(nn.Module):
         mod = self.qkv
         state = LP.low_precision_state(mod)
         if state == "fp4":
-            # NVFP4: raw GEMM output (fp4_fast_linear.py:221-249), then its scale and bias
-            # (fp4_fast_linear.py:251-283) applied on the way into RoPE and the K/V write (one kernel)
+            # NVFP4: the bf16 GEMM output (fp4_fast_linear.py:221-249), then its scale and bias
+            # (fp4_fast_linear.py:251-283) and RoPE and the K/V write -- in the GEMM's epilogue when it
+            # takes whole heads, else on the way into RoPE and the K/V write (one kernel)
             xh = xn if xn_is_xhat else mod.quantize(xn)
-            raw = K.linear(xh, mod.weight_hat, None, site="qkv")
-            K.qkv_rope_kv_scatter(raw.view(M, 3, H, D), rope, qs.active_patch_mask, qs.active_rope_idx,
-                                  qs.active_batch_idx, qs.active_token_idx, kv, q, scale=mod.out_scale_f, bias=mod.bias)
+            if K.qkv_fusable(H, D):
+                K.linear_qkv_rope_kv(xh, mod.weight_hat, mod.bias, rope, qs.active_patch_mask, qs.active_rope_idx,
+                                     qs.active_batch_idx, qs.active_token_idx, kv, q, acc_scale=mod.out_scale_f,
+                                     raw_bf16=True)
+            else:
+                raw = K.linear(xh, mod.weight_hat, None, site="qkv")
+                K.qkv_rope_kv_scatter(raw.view(M, 3, H, D), rope, qs.active_patch_mask, qs.active_rope_idx,
+                                      qs.active_batch_idx, qs.active_token_idx, kv, q, scale=mod.out_scale_f,
+                                      bias=mod.bias)
             qkv = None
         elif state == "fp8" and mod.native and K.qkv_fusable(H, D):
             K.linear_qkv_rope_kv_fp8(mod.quantize_codes(xn), mod.weight_q, self.qkv_bias(), rope, qs.active_patch_mask,
@@ -317,8 +348,9 @@ class SelfAttentionBlock(nn.Module):
             r1 = K.linear(xh, w1.weight_hat, None, site="w1")
             r2 = K.linear(xh, w2.weight_hat, None, site="w2")
             xh3 = K.swiglu_scaled(r1, w1.out_scale_f, w1.bias, r2, w2.out_scale_f, w2.bias, nvfp4_scale=w3.act_scale)
-            r3 = K.linear(xh3, w3.weight_hat, None, site="w3")
-            return K.scale_bias(r3, w3.out_scale_f, w3.bias, gamma=g2, out=r3)
+            # w3's scale and bias, then the LayerScale, in its GEMM epilogue (bf16(bf16(acc) s + b) * gamma)
+            return K.linear(xh3, w3.weight_hat, w3.bias, epilogue=_lib.EPI_BIAS_LS | _lib.EPI_RAW_BF16, gamma=g2,
+                            acc_scale=w3.out_scale_f, site="w3")
         x2 = _linear_route(w2, xn, "w2")
         h = _linear_route(w1, xn, "w1", epilogue=_lib.EPI_BIAS_SILU_MUL, resid=x2)
         return _linear_route(w3, h, "w3", epilogue=_lib.EPI_BIAS_LS, gamma=g2)
@@ -352,13 +384,7 @@ class SelfAttentionBlock(nn.Module):
         H, D = self.attn.num_heads, self.attn.head_dim
         prefix = N - rope[0].shape[0] if rope is not None else N
         dev = x.device
-        tok = torch.arange(N, device=dev, dtype=torch.long)
-        qs = PackedQueryState(
-            active_batch_idx=torch.arange(B, device=dev, dtype=torch.long).repeat_interleave(N),
-            active_pos_idx=tok.repeat(B), active_token_idx=tok.repeat(B),
-            query_valid_mask=torch.ones((B, N), device=dev, dtype=torch.bool),
-            active_query_pos_padded=tok.unsqueeze(0).expand(B, -1), active_query_mask=None, all_valid=True,
-            active_patch_mask=(tok >= prefix).repeat(B), active_rope_idx=(tok - prefix).clamp_min(0).repeat(B))
+        qs = _identity_query_state(B, N, prefix, dev)
         x2 = x.reshape(B * N, C)
         kv = torch.empty((B, N, 2, H, D), device=dev, dtype=torch.bfloat16)
         cache_feature[f"{tag}_kv"] = kv
@@ -374,8 +400,9 @@ class SelfAttentionBlock(nn.Module):
         ones = self._gamma(nn.Identity(), x2)
         x_attn = K.fused_layerscale_add(x2, inc, ones)                       # x + ls1(attn)
         mlp = self._mlp_scaled(K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps))
-        cache_feature[f"{tag}_blocks_out_sum"] = K.fused_layerscale_add(inc, mlp, ones).view(B, N, C)
-        out = K.fused_layerscale_add(x_attn, mlp, ones).view(B, N, C)
+        bos, out = K.residual_pair(inc, x_attn, mlp)  # block.py:336-347: inc + mlp cached, x_attn + mlp out
+        cache_feature[f"{tag}_blocks_out_sum"] = bos.view(B, N, C)
+        out = out.view(B, N, C)
         if server_pscore not in ("none", "disabled"):
             cache_feature[f"{tag}_server_pscore"] = self._server_pscore(q.view(B, N, H, D), kv, server_pscore,
                                                                         N - prefix, lse=lse)
@@ -688,7 +715,7 @@ class SelfAttentionBlock(nn.Module):
             g1 = self._gamma(self.ls1, x_act)
             proj = self.attn.proj
             if LP.low_precision_state(proj) == "fp4":                                    # proj_precision "fp4"
-                x_attn = K.fused_layerscale_add(x_act, K.scale_bias(*_fp4_raw(proj, attn, "proj")), g1)
+                x_attn = _fp4_linear(proj, attn, "proj", epilogue=_lib.EPI_BIAS_LS_RESID, gamma=g1, resid=x_act)
             else:
                 x_attn = _linear_route(proj, attn, "proj", epilogue=_lib.EPI_BIAS_LS_RESID,  # attention.py:532 +
                                        gamma=g1, resid=x_act)                             # block.py:1129-1134

@@ -595,6 +595,21 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: f
     return out
 
 
+def residual_pair(inc: torch.Tensor, x_attn: torch.Tensor, mlp: torch.Tensor) -> tuple[torch.Tensor, torch.Tensor]:
+    """(bf16(inc + mlp), bf16(x_attn + mlp)) of three same-shape bf16 tensors with contiguous rows, in one
+    launch: the approximate block's cached blocks_out_sum and its output (block.py:336-347)."""
+    _require_cuda(inc, x_attn, mlp)
+    _require(inc.shape == x_attn.shape == mlp.shape and inc.dtype == x_attn.dtype == mlp.dtype == torch.bfloat16
+             and inc.is_contiguous() and x_attn.is_contiguous() and mlp.is_contiguous(),
+             "residual_pair: three contiguous bf16 tensors of one shape")
+    C = inc.shape[-1]
+    rows = inc.numel() // max(C, 1)
+    bos, out = torch.empty_like(inc), torch.empty_like(inc)
+    _launch("residual", inc, "oudjat_residual_pair", _ptr(inc), _ptr(x_attn), _ptr(mlp), rows, C, _ptr(bos),
+            _ptr(out), _stream(inc))
+    return bos, out
+
+
 def gather_rows_ln(src: torch.Tensor, batch_idx: torch.Tensor, token_idx: torch.Tensor, weight: torch.Tensor,
                    bias: torch.Tensor, eps: float = 1e-5,
                    nvfp4_scale: torch.Tensor | None = None) -> tuple[torch.Tensor, torch.Tensor]:
@@ -679,11 +694,12 @@ def qkv_fusable(H: int, Dh: int) -> bool:
 def linear_qkv_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, rope,
                        patch_mask: torch.Tensor, rope_idx: torch.Tensor, batch_idx: torch.Tensor,
                        token_idx: torch.Tensor, kv_cache: torch.Tensor, q_out: torch.Tensor,
-                       acc_scale: float = 1.0) -> None:
+                       acc_scale: float = 1.0, raw_bf16: bool = False) -> None:
     """One kernel for attention.py:415-454: qkv = x . weight^T + bias, RoPE on q and k of patch rows,
     k and v written into kv_cache [B, N, 2, H, Dh] rows (b, t) in place, q written to q_out [M, H, Dh].
     The qkv tensor itself is never materialised. `acc_scale` multiplies the fp32 accumulator before
-    its first rounding (an FP8 GEMM's per-tensor scales)."""
+    its first rounding (an FP8 GEMM's per-tensor scales). raw_bf16: an NVFP4 linear (x and weight its
+    x_hat operands, acc_scale its output scale): qkv = bf16(bf16(x . weight^T) * acc_scale + bias)."""
     sin, cos = rope
     _require_cuda(x, weight, bias, patch_mask, rope_idx, batch_idx, token_idx, kv_cache, q_out, sin, cos)
     M, Kd = x.shape
@@ -696,7 +712,8 @@ def linear_qkv_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor
     _require(q_out.is_contiguous() and q_out.shape == (M, H, Dh), "linear_qkv_rope_kv: q_out must be contiguous [M, H, Dh]")
     _require(sin.dtype == cos.dtype == torch.float32 and sin.stride(1) == 1 and cos.stride() == sin.stride(),
              "linear_qkv_rope_kv: fp32 RoPE tables with contiguous rows")
-    _launch("qkv", x, "oudjat_linear_qkv_rope_kv", _ptr(x), M, Kd, x.stride(0), _ptr(weight), weight.stride(0),
+    entry = "oudjat_linear_qkv_rope_kv_nvfp4" if raw_bf16 else "oudjat_linear_qkv_rope_kv"
+    _launch("qkv", x, entry, _ptr(x), M, Kd, x.stride(0), _ptr(weight), weight.stride(0),
             _ptr(None if bias is None else bias.contiguous()), H, Dh, _ptr(sin), _ptr(cos), sin.stride(0),
             _ptr(patch_mask), _ptr(_index(rope_idx, "rope_idx")), _ptr(_index(batch_idx, "batch_idx")),
             _ptr(_index(token_idx, "token_idx")), _ptr(kv_cache), kv_cache.stride(0), kv_cache.stride(1), _ptr(q_out),
@@ -829,7 +846,8 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
            out: torch.Tensor | None = None, site: str = "linear", acc_scale: float = 1.0) -> torch.Tensor:
     """bf16 x[..., K] . weight[N, K]^T with a fused epilogue (see include/oudjat.h). `site` names the
     launch for the timing probe ("proj", "fc1", "fc2", "w1", "w2", "w3", ...). `acc_scale` multiplies
-    the fp32 accumulator before the epilogue's first rounding (an FP8 GEMM's per-tensor scales)."""
+    the fp32 accumulator before the epilogue's first rounding (an FP8 GEMM's per-tensor scales); with
+    `epilogue | EPI_RAW_BF16` (an NVFP4 linear) the accumulator is rounded to bf16 before it."""
     _require_cuda(x, weight, bias, gamma, resid, out)
     _require(x.dtype == weight.dtype == torch.bfloat16, "linear: bf16 only")
     K = x.shape[-1]

@@ -19,6 +19,12 @@
         read / write bytes per dispatch from the two counter runs, scaled as in `traffic`. For the
         standalone kernels of `python -m appcorr_amd.kernel_bench --calib-copy-mib 1024`.
 
+    python -m appcorr_amd.profiling stalls <kernel_trace.csv> <counter_collection.csv,...>
+            <kernel substrings, comma-separated> <title> <command>
+        Markdown table per kernel of the memory-path and issue counters of several `rocprofv3 --pmc`
+        runs (L2 latency and hit rate, fabric latency of L2 misses, texture-data waits, LDS bank
+        conflicts, wave issue / wait fractions, TLB misses).
+
     python -m appcorr_amd.profiling mfma <kernel_trace.csv> <sq_counter_collection.csv>
             <kernel substrings, comma-separated> <title> <command>
         Markdown table per (kernel, grid size) of the matrix-core counters of one `rocprofv3 --pmc`
@@ -197,6 +203,56 @@ def mfma(trace_csv: str, sq_csv: str, subs, title: str, cmd: str) -> str:
     return "\n".join(lines)
 
 
+# Derived figures of the stall summary: (label, numerator counter, denominator counter, format).
+_STALL_RATIOS = [
+    ("L2 read latency seen by the vector L1 (clk)", "TCP_TCC_READ_REQ_LATENCY_sum", "TCP_TCC_READ_REQ_sum", "{:.0f}"),
+    ("L2 hit rate", "TCC_HIT_sum", None, "{:.2f}"),
+    ("L2-miss fabric latency (clk)", "TCC_EA0_RDREQ_LEVEL_sum", "TCC_EA0_RDREQ_sum", "{:.0f}"),
+    ("TD waiting on L2 data / TD busy", "TD_TC_STALL_sum", "TD_TD_BUSY_sum", "{:.2f}"),
+    ("LDS bank-conflict cycles / LDS-active cycles", "SQ_LDS_BANK_CONFLICT", "SQ_LDS_IDX_ACTIVE", "{:.3f}"),
+    ("wave cycles waiting (any)", "SQ_WAIT_ANY", "SQ_WAVE_CYCLES", "{:.2f}"),
+    ("wave cycles waiting to issue", "SQ_WAIT_INST_ANY", "SQ_WAVE_CYCLES", "{:.2f}"),
+    ("wave cycles issuing", "SQ_ACTIVE_INST_ANY", "SQ_WAVE_CYCLES", "{:.2f}"),
+    ("UTCL1 (TLB) misses per dispatch", "TCP_UTCL1_TRANSLATION_MISS_sum", None, "{:.0f}"),
+]
+
+
+def stalls(trace_csv: str, counter_csvs, subs, title: str, cmd: str) -> str:
+    """Per (kernel, grid) of the kernels named by `subs`: the memory-path and issue counters of several
+    `rocprofv3 --pmc` runs (one counter group each) averaged per dispatch, and the ratios of
+    _STALL_RATIOS, with the median duration from a `--kernel-trace` run."""
+    dur = _groups(trace_csv, "duration")
+    cnt = defaultdict(lambda: defaultdict(list))
+    for path in counter_csvs:
+        for r in csv.DictReader(open(path)):
+            thr = int(r["Grid_Size"]) if "Grid_Size" in r else \
+                int(r["Grid_Size_X"]) * int(r["Grid_Size_Y"]) * int(r["Grid_Size_Z"])
+            cnt[(r["Kernel_Name"], thr)][r["Counter_Name"]].append(float(r["Counter_Value"]))
+    keys = [k for k in sorted(cnt, key=lambda k: (_short(k[0]), k[1])) if any(x in k[0] for x in subs) and k in dur]
+    lines = [f"# {title}", "", "Commands (run from the repository root on one MI355X):", "", "```", cmd, "```", "",
+             "Counters averaged per dispatch (each counter group from its own run of the same command).", "",
+             "| figure | " + " | ".join(f"`{_short(k[0])}`" for k in keys) + " |",
+             "|---|" + "---:|" * len(keys)]
+    avg = [{n: sum(v) / len(v) for n, v in cnt[k].items()} for k in keys]
+    lines.append("| median duration (us, trace) | " +
+                 " | ".join(f"{sorted(dur[k])[len(dur[k]) // 2] / 1e3:.2f}" for k in keys) + " |")
+    for label, num, den, fmt in _STALL_RATIOS:
+        vals = []
+        for c in avg:
+            if num not in c or (den is not None and den not in c):
+                vals.append("-")
+                continue
+            if num == "TCC_HIT_sum":
+                tot = c["TCC_HIT_sum"] + c.get("TCC_MISS_sum", 0.0)
+                vals.append(fmt.format(c[num] / tot) if tot else "-")
+            elif den is None:
+                vals.append(fmt.format(c[num]))
+            else:
+                vals.append(fmt.format(c[num] / c[den]) if c[den] else "-")
+        lines.append(f"| {label} | " + " | ".join(vals) + " |")
+    return "\n".join(lines)
+
+
 def main(argv):
     if len(argv) >= 5 and argv[0] == "kernel-stats":
         print(kernel_stats(argv[1], int(argv[2]), argv[3], argv[4]))
@@ -204,6 +260,8 @@ def main(argv):
         print(traffic(argv[1], argv[2], argv[3], argv[4], float(argv[5]), argv[6], argv[7], argv[8]))
     elif len(argv) >= 6 and argv[0] == "mfma":
         print(mfma(argv[1], argv[2], argv[3].split(","), argv[4], argv[5]))
+    elif len(argv) >= 6 and argv[0] == "stalls":
+        print(stalls(argv[1], argv[2].split(","), argv[3].split(","), argv[4], argv[5]))
     elif len(argv) >= 9 and argv[0] == "kernels":
         print(kernels(argv[1], argv[2], argv[3], argv[4], float(argv[5]), argv[6].split(","), argv[7], argv[8]))
     else:

@@ -46,7 +46,11 @@ enum oudjat_epilogue {
   OUDJAT_EPI_BIAS_GELU = 1,     /* C = bf16(gelu_erf(bf16(acc + bias)))                  */
   OUDJAT_EPI_BIAS_LS_RESID = 2, /* C = bf16(resid + bf16(acc + bias) * gamma)            */
   OUDJAT_EPI_BIAS_LS = 3,       /* C = bf16(bf16(acc + bias) * gamma)                    */
-  OUDJAT_EPI_BIAS_SILU_MUL = 4  /* C = bf16(bf16(silu(bf16(acc + bias))) * resid)        */
+  OUDJAT_EPI_BIAS_SILU_MUL = 4, /* C = bf16(bf16(silu(bf16(acc + bias))) * resid)        */
+  /* Flag OR-ed into any of the above (oudjat_linear_bf16): the accumulator is first rounded to bf16
+   * and then scaled, bf16(acc + bias) becoming bf16(bf16(acc) * acc_scale + bias) -- an NVFP4 linear's
+   * bf16 _scaled_mm output followed by its scale and bias (fp4_fast_linear.py:221-283). */
+  OUDJAT_EPI_RAW_BF16 = 16
 };
 
 /* Importance modes for oudjat_patch_importance. */
@@ -238,6 +242,13 @@ int oudjat_fold_residual_rows(const uint16_t* x, int64_t rows, int64_t C, const 
 int oudjat_fused_layerscale_add(const uint16_t* x, const uint16_t* attn, const uint16_t* gamma,
                                 int64_t rows, int64_t C, uint16_t* out, oudjat_stream_t stream);
 
+/* The approximate block's two residual sums in one launch (block.py:336-347, the cache producer):
+ * bos = bf16(inc + mlp) (inc = ls1(attn), the cached {tag}_blocks_out_sum) and out = bf16(x_attn + mlp)
+ * (the block output), all [rows, C] bf16 contiguous -- the same bits as two oudjat_fused_layerscale_add
+ * calls with a gamma of ones. 16-byte aligned rows, C % 8 == 0, C <= 8192. */
+int oudjat_residual_pair(const uint16_t* inc, const uint16_t* x_attn, const uint16_t* mlp, int64_t rows, int64_t C,
+                         uint16_t* bos, uint16_t* out, oudjat_stream_t stream);
+
 /* Row 7 -- rotate-half RoPE on q and k rows [n, H, Dh] in place, fp32 math, rows with
  * patch_mask == 0 untouched; table row rope_idx[i] of sin/cos [*, Dh] fp32.
  * Replaces apply_rope_active_inplace_triton (appcorr/models/dinov3/layers/triton_kernels/rope.py:186-240). */
@@ -330,6 +341,19 @@ int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K, int64_t l
                               const int64_t* batch_idx, const int64_t* token_idx, uint16_t* kv,
                               int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
                               float acc_scale, oudjat_stream_t stream);
+
+/* oudjat_linear_qkv_rope_kv for an NVFP4 qkv linear (fp4_fast_linear.py:221-283, then
+ * attention.py:415-454): qkv = bf16(bf16(A . W^T) * out_scale + bias) (bias NULL: bf16(bf16(A . W^T) *
+ * out_scale)), A the NVFP4 operand x_hat and W the weight's x_hat, then the same RoPE and K/V / q writes;
+ * equal to oudjat_linear_bf16 (OUDJAT_EPI_BIAS | OUDJAT_EPI_RAW_BF16) followed by
+ * oudjat_qkv_rope_kv_scatter_scaled. Same requirements as oudjat_linear_qkv_rope_kv. */
+int oudjat_linear_qkv_rope_kv_nvfp4(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                                    int64_t ldw, const uint16_t* bias, int64_t H, int64_t Dh,
+                                    const float* sin_table, const float* cos_table, int64_t table_stride,
+                                    const uint8_t* patch_mask, const int64_t* rope_idx, const int64_t* batch_idx,
+                                    const int64_t* token_idx, uint16_t* kv, int64_t kv_stride_b,
+                                    int64_t kv_stride_n, uint16_t* q_out, float out_scale,
+                                    oudjat_stream_t stream);
 
 /* Row 10 -- sparse-query attention: for each image b, head h and query t < T,
  *   out[b*T + t, h*Dh:(h+1)*Dh] = softmax(q . K^T * scale) . V over ALL N cached keys, no mask.

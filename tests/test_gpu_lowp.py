@@ -449,3 +449,62 @@ def test_packed_low_precision_run_equals_blockwise(dev, precision):
     for i in range(3):
         for s_ in ("kv", "blocks_out_sum"):
             assert_bits_equal(c_p[f"layer{i}_{s_}"], c_b[f"layer{i}_{s_}"].cpu(), f"layer{i}_{s_}")
+
+
+@pytest.mark.parametrize("M,N,Kd", [(1656, 4096, 8192), (1656, 4096, 4096), (414, 8192, 4096), (4176, 1024, 4096),
+                                    (300, 384, 384)])
+def test_raw_bf16_epilogues_equal_scale_bias_after(dev, M, N, Kd):
+    """An NVFP4 linear's scale, bias and LayerScale (residual) folded into its GEMM (EPI_RAW_BF16: the
+    accumulator rounded to bf16 first) equal the raw bf16 GEMM followed by the scale-bias kernel (and the
+    LayerScale add) bit for bit -- the GEMM picks its tiles and K split independently of the epilogue, so
+    both read the same accumulators. Includes the ViT-7B w3 shape, whose K splits in two slices."""
+    print(f"raw_bf16 epilogues {M}x{N}x{Kd}", flush=True)
+    x = (_x((M, Kd), 7, outliers=False).float() * 0.5).to(torch.bfloat16).to(dev)
+    w = (_x((N, Kd), 8, outliers=False).float() * 0.02).to(torch.bfloat16).to(dev)
+    b = (_x((N,), 9, outliers=False).float() * 0.1).to(torch.bfloat16).to(dev)
+    g = (1.0 + 0.1 * _x((N,), 10, outliers=False).float()).to(torch.bfloat16).to(dev)
+    r = _x((M, N), 11, outliers=False).to(dev)
+    s = 0.37
+    raw = K.linear(x, w, None)
+    RAW = _lib.EPI_RAW_BF16
+    for bias in (b, None):
+        sb = K.scale_bias(raw, s, bias)
+        got = K.linear(x, w, bias, epilogue=_lib.EPI_BIAS | RAW, acc_scale=s)
+        assert_bits_equal(got, sb.cpu(), f"scale-bias (bias {bias is not None})")
+        got = K.linear(x, w, bias, epilogue=_lib.EPI_BIAS_LS | RAW, gamma=g, acc_scale=s)
+        assert_bits_equal(got, K.scale_bias(raw, s, bias, gamma=g).cpu(), "scale-bias + LayerScale")
+        got = K.linear(x, w, bias, epilogue=_lib.EPI_BIAS_LS_RESID | RAW, gamma=g, resid=r, acc_scale=s)
+        assert_bits_equal(got, K.fused_layerscale_add(r, sb, g).cpu(), "scale-bias + LayerScale + residual")
+
+
+@pytest.mark.parametrize("B,T,H,D,Kd", [(4, 414, 32, 128, 4096), (2, 50, 4, 64, 256)])
+def test_nvfp4_fused_qkv_equals_scaled_scatter(dev, B, T, H, D, Kd):
+    """The NVFP4 qkv linear in the fused QKV kernel (bf16(bf16(acc) s + b), then RoPE and the K/V / q
+    writes) equals the scaled post-QKV scatter applied to that kernel's own bf16 accumulator (taken from
+    a run with scale 1, no bias and no patch rows), bit for bit."""
+    N = 1029
+    M = B * T
+    rng = np.random.default_rng(B + H)
+    toks = np.stack([np.concatenate([np.arange(5), np.sort(rng.choice(np.arange(5, N), T - 5, replace=False))])
+                     for _ in range(B)])
+    tok = torch.from_numpy(toks.reshape(-1).astype(np.int64)).to(dev)
+    bi = torch.arange(B).repeat_interleave(T).to(dev)
+    pm, ri = tok >= 5, (tok - 5).clamp_min(0)
+    cfg = OM.with_overrides(OM.CONFIGS["vit7b16_1024"], dim=H * D, heads=H)
+    sin, cos = (t.to(dev) for t in OM.rope_tables(cfg))
+    x = _x((M, Kd), 12, outliers=False).to(dev)
+    w = (_x((3 * H * D, Kd), 13, outliers=False).float() * 0.02).to(torch.bfloat16).to(dev)
+    b = (_x((3 * H * D,), 14, outliers=False).float() * 0.1).to(torch.bfloat16).to(dev)
+    kv0 = _x((B, N, 2, H, D), 15, outliers=False).to(dev)
+    s = 0.37
+    for bias in (b, None):
+        kv_f, q_f = kv0.clone(), torch.empty((M, H, D), dtype=torch.bfloat16, device=dev)
+        K.linear_qkv_rope_kv(x, w, bias, (sin, cos), pm, ri, bi, tok, kv_f, q_f, acc_scale=s, raw_bf16=True)
+        kv_r, q_r = kv0.clone(), torch.empty((M, H, D), dtype=torch.bfloat16, device=dev)
+        K.linear_qkv_rope_kv(x, w, None, (sin, cos), torch.zeros_like(pm), ri, bi, tok, kv_r, q_r, acc_scale=1.0,
+                             raw_bf16=True)
+        raw = torch.stack([q_r, kv_r[bi, tok, 0], kv_r[bi, tok, 1]], dim=1).contiguous()  # bf16(acc)
+        kv_u, q_u = kv0.clone(), torch.empty((M, H, D), dtype=torch.bfloat16, device=dev)
+        K.qkv_rope_kv_scatter(raw, (sin, cos), pm, ri, bi, tok, kv_u, q_u, scale=s, bias=bias)
+        assert_bits_equal(q_f, q_u.cpu(), f"q (bias {bias is not None})")
+        assert_bits_equal(kv_f, kv_u.cpu(), f"kv (bias {bias is not None})")

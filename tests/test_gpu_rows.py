@@ -52,6 +52,17 @@ def test_gather_rows_ln_equals_gather_then_layernorm(dev, B, N, C, T, fp4):
     assert_bits_equal(xn, K.layer_norm(xp, w, b, 1e-6, nvfp4_scale=ts).cpu(), "LayerNorm of the gathered rows")
 
 
+@pytest.mark.parametrize("rows,C", [(16 * 1029, 1024), (4 * 4101, 4096), (201, 384), (3, 8)])
+def test_residual_pair(dev, rows, C):
+    """The approximate block's blocks_out_sum and output in one launch equal the two LayerScale adds
+    with a gamma of ones (bf16(a + b) each; the add kernel is pinned against the oracle)."""
+    inc, xa, mlp = (_rand_bf16((rows, C), s).to(dev) for s in (6, 7, 8))
+    ones = torch.ones(C, dtype=torch.bfloat16, device=dev)
+    bos, out = K.residual_pair(inc, xa, mlp)
+    assert_bits_equal(bos, K.fused_layerscale_add(inc, mlp, ones).cpu(), "blocks_out_sum")
+    assert_bits_equal(out, K.fused_layerscale_add(xa, mlp, ones).cpu(), "block output")
+
+
 def test_gather_rows_empty(dev):
     x = _rand_bf16((2, 5, 64), 0).to(dev)
     e = torch.empty(0, dtype=torch.long, device=dev)
