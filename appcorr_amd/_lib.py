@@ -100,6 +100,8 @@ SIGNATURES: dict[str, list] = {
     "oudjat_fold_residual_rows": [_p, _i64, _i64, _p, _p, _p, _i64, _p, _p],
     "oudjat_linear_qkv_rope_kv": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p, _p,
                                   _i64, _i64, _p, _f32, _p],
+    "oudjat_linear_swiglu_nvfp4": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _f32, _p, _f32, _p, _p, _p, _i64,
+                                   _p],
     "oudjat_linear_qkv_rope_kv_nvfp4": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p,
                                         _p, _p, _i64, _i64, _p, _f32, _p],
     "oudjat_sparse_query_attention": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32, _p,

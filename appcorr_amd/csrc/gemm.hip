@@ -39,6 +39,7 @@
 #include <mutex>
 #include <type_traits>
 
+#include "nvfp4.hpp"
 #include "common.hpp"
 
 namespace oudjat {
@@ -53,7 +54,11 @@ static constexpr int kEpiQkv = 5;
 // tile to slice blockIdx.y of a [S, M, N] workspace; splitk_reduce_kernel sums the slices in order
 // and applies the epilogue.
 static constexpr int kEpiPartial = 6;
-static constexpr int kNumEpi = 7;
+// SwiGLU of two NVFP4 linears in w2's epilogue (oudjat_linear_swiglu_nvfp4): the tile holds x2 =
+// bf16(acc) (raw rounding, scale 1, no bias); phase 2 reads x1 (w1's bf16 output) as the residual row,
+// forms swiglu_scaled8 and writes the NVFP4 operand x_hat of its bf16 value (w3's input).
+static constexpr int kEpiSwigluXh = 7;
+static constexpr int kNumEpi = 8;
 
 struct QkvArgs {
   int H, Dh;
@@ -79,23 +84,34 @@ struct EpiArgs {
   int64_t ldr;
   QkvArgs qkv;
   float acc_scale;
-  // NVFP4 linears (OUDJAT_EPI_RAW_BF16): the accumulator is rounded to bf16 before acc_scale and the
-  // bias, v = bf16(bf16(acc) * acc_scale + bias) -- the reference's _scaled_mm writes its bf16 output
-  // and scales it afterwards (fp4_fast_linear.py:221-283).
+  // NVFP4 linears (OUDJAT_EPI_RAW_BF16): the accumulator is rounded to bf16 before the scale and the
+  // bias, v = bf16(bf16(acc) * raw_scale + raw_bias) -- the reference's _scaled_mm writes its bf16
+  // output and scales it afterwards (fp4_fast_linear.py:221-283). The first rounding point then runs
+  // with acc_scale = 1 and no bias (it gives bf16(acc) exactly) and raw_scale_bias8 follows it.
   int raw_round;
+  float raw_scale;
+  const uint16_t* raw_bias;
+  // kEpiSwigluXh: w1's scale and bias (x1 = resid rows), w2's scale and bias, w3's NVFP4 tensor scale.
+  float s1, s2;
+  const uint16_t* b1;
+  const uint16_t* b2;
+  const float* xh_ts;
 };
 
-// The accumulators of a tile rounded to bf16 in place (OUDJAT_EPI_RAW_BF16), once, before the
-// epilogue's first rounding point.
-template <typename V, int FM, int FN>
-__device__ __forceinline__ void round_acc_bf16(V (&acc)[FM][FN]) {
-  constexpr int NV = sizeof(V) / sizeof(float);
+// OUDJAT_EPI_RAW_BF16 on 8 consecutive bf16 values of columns col .. col + 7 (already bf16(acc)):
+// bf16(v * raw_scale + raw_bias), or bf16(v * raw_scale) without a bias (scale_bias's arithmetic).
+__device__ __forceinline__ uint4 raw_scale_bias8(uint4 o, int64_t col, const EpiArgs& ea) {
+  float v[8], b[8];
+  unpack8(o, v);
+  if (ea.raw_bias) {
+    unpack8(*reinterpret_cast<const uint4*>(ea.raw_bias + col), b);
 #pragma unroll
-  for (int i = 0; i < FM; ++i)
+    for (int e = 0; e < 8; ++e) v[e] = __builtin_fmaf(v[e], ea.raw_scale, b[e]);
+  } else {
 #pragma unroll
-    for (int j = 0; j < FN; ++j)
-#pragma unroll
-      for (int v = 0; v < NV; ++v) acc[i][j][v] = round_bf16(acc[i][j][v]);
+    for (int e = 0; e < 8; ++e) v[e] = v[e] * ea.raw_scale;
+  }
+  return pack8(v);
 }
 
 // Two fp32 -> packed bf16 pair (low half = a) with the hardware round-to-nearest-even convert.
@@ -144,8 +160,9 @@ __device__ __forceinline__ uint32_t gelu_pair_bits(uint32_t w, const uint16_t* l
 
 template <int EPI>
 __device__ __forceinline__ float epilogue(float acc, int64_t row, int64_t col, const EpiArgs& ea) {
-  const float a = ea.raw_round ? round_bf16(acc) : acc;
-  float v = round_bf16(__builtin_fmaf(a, ea.acc_scale, ea.bias ? bf16_to_f32(ea.bias[col]) : -0.0f));
+  float v = round_bf16(__builtin_fmaf(acc, ea.acc_scale, ea.bias ? bf16_to_f32(ea.bias[col]) : -0.0f));
+  if (ea.raw_round)
+    v = round_bf16(ea.raw_bias ? __builtin_fmaf(v, ea.raw_scale, bf16_to_f32(ea.raw_bias[col])) : v * ea.raw_scale);
   if (EPI == OUDJAT_EPI_BIAS_GELU) {
     v = __uint_as_float(gelu_bf16_bits(__float_as_uint(v) >> 16, g_gelu_lut) << 16);
   } else if (EPI == OUDJAT_EPI_BIAS_LS_RESID) {
@@ -404,6 +421,10 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
         const int hcol = colg - which * HD;  // column within q, k or v
         uint4 lo = *reinterpret_cast<const uint4*>(ct + rl * LDT + c0);
         uint4 hi = *reinterpret_cast<const uint4*>(ct + rl * LDT + c0 + half);
+        if (ea.raw_round) {
+          lo = raw_scale_bias8(lo, colg, ea);
+          hi = raw_scale_bias8(hi, colg + half, ea);
+        }
         if (which < 2 && rope[it]) {
           float l[8], rr[8];
           unpack8(lo, l);
@@ -467,6 +488,23 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
     const int row = m0 + rl, col = n0 + cl;
     if (row >= M) continue;
     uint4 o = *reinterpret_cast<const uint4*>(ct + rl * LDT + cl);
+    if (ea.raw_round) o = raw_scale_bias8(o, col, ea);
+    if constexpr (EPI == kEpiSwigluXh) {
+      // A 16-element NVFP4 block is the chunk pair of threads 2k, 2k + 1 (one row: CPR is even), both
+      // active or both skipped with their row.
+      float x2[8], x1[8], ba[8], bb[8], y[8], h[8];
+      unpack8(o, x2);
+      unpack8(*reinterpret_cast<const uint4*>(ea.resid + (int64_t)row * ea.ldr + col), x1);
+      if (ea.b1) {
+        unpack8(*reinterpret_cast<const uint4*>(ea.b1 + col), ba);
+        unpack8(*reinterpret_cast<const uint4*>(ea.b2 + col), bb);
+      }
+      swiglu_scaled8(x1, ea.s1, ba, x2, ea.s2, bb, ea.b1 != nullptr, y);
+      unpack8(pack8(y), y);  // the bf16 SwiGLU output the quantizer reads
+      nvfp4_xhat8_pair(y, *ea.xh_ts, h);
+      *reinterpret_cast<uint4*>(C + (int64_t)row * ldc + col) = pack8(h);
+      continue;
+    }
     if constexpr (EPI != OUDJAT_EPI_BIAS && EPI != kEpiQkv) {
       // 16-byte loads of the per-column gamma and the residual / gate row segment.
       float v[8], g[8], r[8];
@@ -491,11 +529,10 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
 }
 
 template <int BM, int BN, int FM, int FN, int NW, int EPI>
-__device__ __forceinline__ void store_tile(f32x16_t (&acc)[FM][FN], unsigned char* smem, const uint16_t* lut,
+__device__ __forceinline__ void store_tile(const f32x16_t (&acc)[FM][FN], unsigned char* smem, const uint16_t* lut,
                                            int wm0, int wn0, int m0, int n0, int M, const EpiArgs& ea,
                                            uint16_t* __restrict__ C, int64_t ldc) {
   const int lane = threadIdx.x & 63;
-  if (ea.raw_round) round_acc_bf16(acc);
   constexpr int LDT = BN + 8;
   uint16_t* ct = reinterpret_cast<uint16_t*>(smem);
 #pragma unroll
@@ -970,7 +1007,6 @@ __device__ __forceinline__ void r16_epilogue(f32x4_t (&acc)[FMB][FNB], unsigned 
     }
     return;
   }
-  if (ea.raw_round) round_acc_bf16(acc);
   if constexpr (WGM > 1 && KSPLIT == 1 && RED == 0 && BM * LDT * 2 <= TILE_BYTES) {
 #pragma unroll
     for (int j = 0; j < FNB; ++j) {
@@ -1584,7 +1620,9 @@ __global__ __launch_bounds__(256) void splitk_reduce_kernel(const float* __restr
   float v[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    float x = round_bf16(__builtin_fmaf(ea.raw_round ? round_bf16(acc[e]) : acc[e], ea.acc_scale, bias[e]));
+    float x = round_bf16(__builtin_fmaf(acc[e], ea.acc_scale, bias[e]));
+    if (ea.raw_round)
+      x = round_bf16(ea.raw_bias ? __builtin_fmaf(x, ea.raw_scale, bf16_to_f32(ea.raw_bias[col + e])) : x * ea.raw_scale);
     if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) x = __uint_as_float(gelu_bf16_bits(__float_as_uint(x) >> 16, g_gelu_lut) << 16);
     else if constexpr (EPI == OUDJAT_EPI_BIAS_LS_RESID) x = fmaf(x, g[e], side[e]);
     else if constexpr (EPI == OUDJAT_EPI_BIAS_LS) x = x * g[e];
@@ -1644,7 +1682,7 @@ struct GemmCfg {
   {BM, BN, 2, 4, -3,                                                                                     \
    {gemm_bf16_pp_kernel<BM, BN, 0>, gemm_bf16_pp_kernel<BM, BN, 1>, gemm_bf16_pp_kernel<BM, BN, 2>,      \
     gemm_bf16_pp_kernel<BM, BN, 3>, gemm_bf16_pp_kernel<BM, BN, 4>, gemm_bf16_pp_kernel<BM, BN, kEpiQkv>,  \
-    gemm_bf16_pp_kernel<BM, BN, kEpiPartial>},                                                            \
+    gemm_bf16_pp_kernel<BM, BN, kEpiPartial>, gemm_bf16_pp_kernel<BM, BN, kEpiSwigluXh>},                 \
    64, 2, 1, 0}
 
 // pf = -4: the ping-pong kernel on e4m3 operands (oudjat_linear_fp8; no GELU epilogue -- the FP8 route
@@ -1984,6 +2022,8 @@ extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64
   epi &= ~OUDJAT_EPI_RAW_BF16;
   OUDJAT_REQUIRE(epi >= OUDJAT_EPI_BIAS && epi <= OUDJAT_EPI_BIAS_SILU_MUL, OUDJAT_ERR_INVALID_ARGUMENT,
                  "linear_bf16: bad epilogue %d", epi);
+  OUDJAT_REQUIRE(!raw_round || epi != OUDJAT_EPI_BIAS_GELU, OUDJAT_ERR_INVALID_ARGUMENT,
+                 "linear_bf16: OUDJAT_EPI_RAW_BF16 does not combine with the GELU epilogue");
   if (M == 0 || N == 0) return OUDJAT_OK;
   OUDJAT_REQUIRE(A && W && C, OUDJAT_ERR_INVALID_ARGUMENT, "linear_bf16: null pointer");
   OUDJAT_REQUIRE((epi != OUDJAT_EPI_BIAS_LS && epi != OUDJAT_EPI_BIAS_LS_RESID) || gamma, OUDJAT_ERR_INVALID_ARGUMENT,
@@ -2006,7 +2046,15 @@ extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64
   ea.resid = resid;
   ea.ldr = ldr;
   ea.acc_scale = acc_scale;
-  ea.raw_round = raw_round;
+  if (raw_round) {  // bf16(acc) at the first rounding point, then the scale and bias
+    OUDJAT_REQUIRE(!bias || aligned(bias, 16), OUDJAT_ERR_UNSUPPORTED_LAYOUT,
+                   "linear_bf16: a raw-rounded epilogue needs a 16-byte aligned bias");
+    ea.raw_round = 1;
+    ea.raw_scale = acc_scale;
+    ea.raw_bias = bias;
+    ea.acc_scale = 1.0f;
+    ea.bias = nullptr;
+  }
   if (workspace && aligned_io && aligned(workspace, 16)) {
     int S = 1;
     const int ci = choose_splitk(M, N, K, epi, &S);
@@ -2016,6 +2064,40 @@ extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64
   }
   return launch_gemm(choose_cfg(M, N, K, aligned_io), A, M, K, lda, W, N, ldw, epi, ea, C, ldc, as_stream(stream),
                      "linear_bf16");
+}
+
+extern "C" int oudjat_linear_swiglu_nvfp4(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                                          int64_t N, int64_t ldw, const uint16_t* x1, int64_t ld1, float s1,
+                                          const uint16_t* b1, float s2, const uint16_t* b2,
+                                          const float* tensor_scale, uint16_t* xhat, int64_t ldc,
+                                          oudjat_stream_t stream) {
+  const char* what = "linear_swiglu_nvfp4";
+  OUDJAT_REQUIRE(M >= 0 && N >= 0 && K >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "%s: negative size", what);
+  if (M == 0 || N == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(A && W && x1 && tensor_scale && xhat && (b1 == nullptr) == (b2 == nullptr),
+                 OUDJAT_ERR_INVALID_ARGUMENT, "%s: null pointer (both biases or neither)", what);
+  OUDJAT_REQUIRE(K > 0 && K % kBK == 0 && N % 256 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE,
+                 "%s: K %% %d == 0 and N %% 256 == 0 required (K=%lld, N=%lld)", what, kBK, (long long)K,
+                 (long long)N);
+  OUDJAT_REQUIRE(lda % 8 == 0 && ldw % 8 == 0 && ld1 % 8 == 0 && ldc % 8 == 0 && lda >= K && ldw >= K && ld1 >= N &&
+                     ldc >= N && aligned(A, 16) && aligned(W, 16) && aligned(x1, 16) && aligned(xhat, 16) &&
+                     (!b1 || (aligned(b1, 16) && aligned(b2, 16))),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "%s: 16-byte aligned operands and rows, ld %% 8 == 0", what);
+  OUDJAT_REQUIRE(M < ((int64_t)1 << 31) && N < ((int64_t)1 << 31) && K < ((int64_t)1 << 31), OUDJAT_ERR_TOO_LARGE,
+                 "%s: dimensions must fit in int32", what);
+  EpiArgs ea{};
+  ea.acc_scale = 1.0f;  // the tile holds x2 = bf16(acc) exactly (no bias at the first rounding point)
+  ea.resid = x1;
+  ea.ldr = ld1;
+  ea.s1 = s1;
+  ea.s2 = s2;
+  ea.b1 = b1;
+  ea.b2 = b2;
+  ea.xh_ts = tensor_scale;
+  // The epilogue exists on the ping-pong tiles; shapes whose choice is another family take 192 x 256.
+  int ci = choose_cfg(M, N, K, true);
+  if (kCfgs[ci].fn[kEpiSwigluXh] == nullptr) ci = 31;
+  return launch_gemm(ci, A, M, K, lda, W, N, ldw, kEpiSwigluXh, ea, xhat, ldc, as_stream(stream), what);
 }
 
 // The partial GEMM of a split-K product alone (see oudjat.h): the consumer reduces the slices.
@@ -2077,7 +2159,15 @@ static int linear_qkv_rope_kv_impl(const uint16_t* A, int64_t M, int64_t K, int6
   EpiArgs ea{};
   ea.bias = bias;
   ea.acc_scale = acc_scale;
-  ea.raw_round = raw_round;
+  if (raw_round) {  // bf16(acc) at the first rounding point, then the scale and bias
+    OUDJAT_REQUIRE(!bias || aligned(bias, 16), OUDJAT_ERR_UNSUPPORTED_LAYOUT,
+                   "linear_qkv_rope_kv_nvfp4: 16-byte aligned bias required");
+    ea.raw_round = 1;
+    ea.raw_scale = acc_scale;
+    ea.raw_bias = bias;
+    ea.acc_scale = 1.0f;
+    ea.bias = nullptr;
+  }
   ea.qkv = QkvArgs{(int)H, (int)Dh, sin_table, cos_table, table_stride, patch_mask, rope_idx, batch_idx, token_idx,
                    kv, kv_stride_b, kv_stride_n, q_out};
   return launch_gemm(choose_qkv_cfg(M, N, K, Dh), A, M, K, lda, W, N, ldw, kEpiQkv, ea, nullptr, 0, as_stream(stream),

@@ -136,13 +136,7 @@ __global__ void __launch_bounds__(kLpThreads) swiglu_scaled_kernel(const uint16_
     unpack8(*reinterpret_cast<const uint4*>(b1 + c), ba);
     unpack8(*reinterpret_cast<const uint4*>(b2 + c), bb);
   }
-#pragma unroll
-  for (int e = 0; e < 8; ++e) {
-    const float av = b1 ? __builtin_fmaf(a[e], s1, ba[e]) : a[e] * s1;
-    const float bv = b1 ? __builtin_fmaf(b[e], s2, bb[e]) : b[e] * s2;
-    const float silu = av * (1.0f / (1.0f + expf(-av)));
-    a[e] = silu * bv;
-  }
+  swiglu_scaled8(a, s1, ba, b, s2, bb, b1 != nullptr, a);
   if constexpr (XH) {
     float h[8];
     unpack8(pack8(a), a);  // the bf16 output the quantizer reads

@@ -121,6 +121,20 @@ __device__ __forceinline__ void nvfp4_xhat8(const float* f, float amax16, float 
 // (which holds the other 8): the block maximum is exchanged between the two lanes. Every lane of the
 // wave must execute this (the exchange reads the partner lane); a lane outside the data passes
 // zeros and discards the result.
+// The SwiGLU pair's fused NVFP4-linear epilogue on 8 elements (token_update.py:620-631): a = x1 s1 + b1
+// and b = x2 s2 + b2 in fp32 (one fma each when there are biases), out = (a * sigmoid(a)) * b with
+// sigmoid(a) = 1 / (1 + e^-a). Shared by the SwiGLU kernel and the w2 GEMM epilogue (the same bits).
+__device__ __forceinline__ void swiglu_scaled8(const float* x1, float s1, const float* ba, const float* x2, float s2,
+                                               const float* bb, bool bias, float* out) {
+#pragma unroll
+  for (int e = 0; e < 8; ++e) {
+    const float av = bias ? __builtin_fmaf(x1[e], s1, ba[e]) : x1[e] * s1;
+    const float bv = bias ? __builtin_fmaf(x2[e], s2, bb[e]) : x2[e] * s2;
+    const float silu = av * (1.0f / (1.0f + expf(-av)));
+    out[e] = silu * bv;
+  }
+}
+
 __device__ __forceinline__ void nvfp4_xhat8_pair(const float* f, float ts, float* out) {
   float am = 0.0f;
 #pragma unroll

@@ -346,8 +346,13 @@ class SelfAttentionBlock(nn.Module):
             # (w2 takes the activation w1 quantized: SharedFP4Activation, fp4_fast_linear.py:71-100)
             xh = xn if xn_is_xhat else w1.quantize(xn)
             r1 = K.linear(xh, w1.weight_hat, None, site="w1")
-            r2 = K.linear(xh, w2.weight_hat, None, site="w2")
-            xh3 = K.swiglu_scaled(r1, w1.out_scale_f, w1.bias, r2, w2.out_scale_f, w2.bias, nvfp4_scale=w3.act_scale)
+            if w2.out_features % 256 == 0:  # w2's GEMM finishes the SwiGLU and writes w3's operand
+                xh3 = K.linear_swiglu_nvfp4(xh, w2.weight_hat, r1, w1.out_scale_f, w1.bias, w2.out_scale_f, w2.bias,
+                                            w3.act_scale, site="w2")
+            else:
+                r2 = K.linear(xh, w2.weight_hat, None, site="w2")
+                xh3 = K.swiglu_scaled(r1, w1.out_scale_f, w1.bias, r2, w2.out_scale_f, w2.bias,
+                                      nvfp4_scale=w3.act_scale)
             # w3's scale and bias, then the LayerScale, in its GEMM epilogue (bf16(bf16(acc) s + b) * gamma)
             return K.linear(xh3, w3.weight_hat, w3.bias, epilogue=_lib.EPI_BIAS_LS | _lib.EPI_RAW_BF16, gamma=g2,
                             acc_scale=w3.out_scale_f, site="w3")

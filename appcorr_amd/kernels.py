@@ -720,6 +720,27 @@ def linear_qkv_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor
             float(acc_scale), _stream(x))
 
 
+def linear_swiglu_nvfp4(xh: torch.Tensor, w2_hat: torch.Tensor, x1: torch.Tensor, s1: float,
+                        b1: torch.Tensor | None, s2: float, b2: torch.Tensor | None, tensor_scale: torch.Tensor,
+                        site: str = "w2") -> torch.Tensor:
+    """w2's NVFP4 GEMM with the SwiGLU of the pair and w3's activation quantizer in its epilogue: from the
+    shared operand xh [M, K], w2's weight x_hat [N, K] and w1's bf16 output x1 [M, N], the NVFP4 operand
+    of bf16(silu(x1 s1 + b1) (bf16(xh . w2^T) s2 + b2)) with w3's tensor scale -- swiglu_scaled(x1, s1, b1,
+    linear(xh, w2_hat), s2, b2, nvfp4_scale=tensor_scale) in one launch. N % 256 == 0."""
+    _require_cuda(xh, w2_hat, x1, b1, b2, tensor_scale)
+    M, Kd = xh.shape
+    N = w2_hat.shape[0]
+    _require(xh.dtype == w2_hat.dtype == x1.dtype == torch.bfloat16 and xh.stride(1) == 1 and w2_hat.stride(1) == 1
+             and w2_hat.shape[1] == Kd and x1.shape == (M, N) and x1.stride(1) == 1,
+             "linear_swiglu_nvfp4: bf16 xh [M, K], w2_hat [N, K], x1 [M, N] with contiguous rows")
+    ts = _nvfp4_scale(tensor_scale, "linear_swiglu_nvfp4")
+    out = torch.empty((M, N), device=xh.device, dtype=torch.bfloat16)
+    _launch(site, xh, "oudjat_linear_swiglu_nvfp4", _ptr(xh), M, Kd, xh.stride(0), _ptr(w2_hat), N, w2_hat.stride(0),
+            _ptr(x1), x1.stride(0), float(s1), _ptr(None if b1 is None else b1.contiguous()), float(s2),
+            _ptr(None if b2 is None else b2.contiguous()), _ptr(ts), _ptr(out), out.stride(0), _stream(xh))
+    return out
+
+
 def linear_qkv_rope_kv_fp8(x8: torch.Tensor, w8: torch.Tensor, bias: torch.Tensor | None, rope,
                            patch_mask: torch.Tensor, rope_idx: torch.Tensor, batch_idx: torch.Tensor,
                            token_idx: torch.Tensor, kv_cache: torch.Tensor, q_out: torch.Tensor,

@@ -47,9 +47,10 @@ enum oudjat_epilogue {
   OUDJAT_EPI_BIAS_LS_RESID = 2, /* C = bf16(resid + bf16(acc + bias) * gamma)            */
   OUDJAT_EPI_BIAS_LS = 3,       /* C = bf16(bf16(acc + bias) * gamma)                    */
   OUDJAT_EPI_BIAS_SILU_MUL = 4, /* C = bf16(bf16(silu(bf16(acc + bias))) * resid)        */
-  /* Flag OR-ed into any of the above (oudjat_linear_bf16): the accumulator is first rounded to bf16
-   * and then scaled, bf16(acc + bias) becoming bf16(bf16(acc) * acc_scale + bias) -- an NVFP4 linear's
-   * bf16 _scaled_mm output followed by its scale and bias (fp4_fast_linear.py:221-283). */
+  /* Flag OR-ed into any of the above but the GELU one (oudjat_linear_bf16): the accumulator is first
+   * rounded to bf16 and then scaled, bf16(acc + bias) becoming bf16(bf16(acc) * acc_scale + bias) -- an
+   * NVFP4 linear's bf16 _scaled_mm output followed by its scale and bias (fp4_fast_linear.py:221-283);
+   * the bias must then be 16-byte aligned. */
   OUDJAT_EPI_RAW_BF16 = 16
 };
 
@@ -354,6 +355,19 @@ int oudjat_linear_qkv_rope_kv_nvfp4(const uint16_t* A, int64_t M, int64_t K, int
                                     const int64_t* token_idx, uint16_t* kv, int64_t kv_stride_b,
                                     int64_t kv_stride_n, uint16_t* q_out, float out_scale,
                                     oudjat_stream_t stream);
+
+/* The SwiGLU pair of NVFP4 linears up to w3's operand in one GEMM (fp4_fast_linear.py:221-283 for w2,
+ * then the fused SwiGLU epilogue, token_update.py:620-669, then w3's activation quantizer): with
+ * x2 = bf16(A . W^T) (A the shared NVFP4 operand x_hat, W w2's weight x_hat [N, K]) and x1 = w1's bf16
+ * output [M, N] (row stride ld1), a = x1 s1 + b1 and b = x2 s2 + b2 in fp32, h = bf16((a sigmoid(a)) b),
+ * and xhat [M, N] (row stride ldc) receives the NVFP4 operand of h with tensor scale *tensor_scale --
+ * bit-identical to oudjat_linear_bf16 (w2, OUDJAT_EPI_BIAS) followed by oudjat_swiglu_scaled_nvfp4 when
+ * both run the same tiles. b1, b2: both or neither. K % 64 == 0, N % 256 == 0; 16-byte aligned
+ * operands and rows. */
+int oudjat_linear_swiglu_nvfp4(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W, int64_t N,
+                               int64_t ldw, const uint16_t* x1, int64_t ld1, float s1, const uint16_t* b1,
+                               float s2, const uint16_t* b2, const float* tensor_scale, uint16_t* xhat, int64_t ldc,
+                               oudjat_stream_t stream);
 
 /* Row 10 -- sparse-query attention: for each image b, head h and query t < T,
  *   out[b*T + t, h*Dh:(h+1)*Dh] = softmax(q . K^T * scale) . V over ALL N cached keys, no mask.

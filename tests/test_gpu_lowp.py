@@ -508,3 +508,29 @@ def test_nvfp4_fused_qkv_equals_scaled_scatter(dev, B, T, H, D, Kd):
         K.qkv_rope_kv_scatter(raw, (sin, cos), pm, ri, bi, tok, kv_u, q_u, scale=s, bias=bias)
         assert_bits_equal(q_f, q_u.cpu(), f"q (bias {bias is not None})")
         assert_bits_equal(kv_f, kv_u.cpu(), f"kv (bias {bias is not None})")
+
+
+@pytest.mark.parametrize("M,N,Kd,same_tiles", [(1656, 8192, 4096, True), (4176, 4096, 1024, True),
+                                               (600, 1024, 512, False)])
+def test_swiglu_nvfp4_gemm_equals_gemm_then_swiglu(dev, M, N, Kd, same_tiles):
+    """w2's NVFP4 GEMM with the SwiGLU and w3's quantizer in its epilogue equals the raw w2 GEMM followed
+    by the SwiGLU kernel writing x_hat, bit for bit where both take the same tiles (the ViT-7B w2 shape);
+    where the plain GEMM would take other tiles (the fused entry keeps ping-pong tiles) the accumulators
+    differ in the last fp32 bit, and at least 99 % of the x_hat values must still agree."""
+    print(f"swiglu nvfp4 gemm {M}x{N}x{Kd}", flush=True)
+    xh = (_x((M, Kd), 16, outliers=False).float() * 0.5).to(torch.bfloat16).to(dev)
+    w2 = (_x((N, Kd), 17, outliers=False).float() * 0.02).to(torch.bfloat16).to(dev)
+    x1 = _x((M, N), 18, outliers=False).to(dev)
+    b1 = (_x((N,), 19, outliers=False).float() * 0.1).to(torch.bfloat16).to(dev)
+    b2 = (_x((N,), 20, outliers=False).float() * 0.1).to(torch.bfloat16).to(dev)
+    ts = torch.tensor([0.013], device=dev)
+    for bias in (True, False):
+        bb1, bb2 = (b1, b2) if bias else (None, None)
+        got = K.linear_swiglu_nvfp4(xh, w2, x1, 0.7, bb1, 1.3, bb2, ts)
+        r2 = K.linear(xh, w2, None)
+        ref = K.swiglu_scaled(x1.clone(), 0.7, bb1, r2, 1.3, bb2, nvfp4_scale=ts)
+        if same_tiles:
+            assert_bits_equal(got, ref.cpu(), f"x_hat (bias {bias})")
+        else:
+            same = float((got == ref).float().mean())
+            assert same >= 0.99, same

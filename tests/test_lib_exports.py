@@ -62,6 +62,23 @@ def test_linear_rejects_bad_shapes_before_launch():
     # misaligned A
     _expect("OUDJAT_ERR_UNSUPPORTED_LAYOUT", "oudjat_linear_bf16", ctypes.c_void_p(18), 4, 64, 64,
             ctypes.c_void_p(16), 64, 64, NULL, 0, NULL, NULL, 0, ctypes.c_void_p(16), 64, 1.0, NULL, 0, NULL)
+    # the raw-bf16 flag does not combine with GELU; it needs a 16-byte aligned bias
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_linear_bf16", ctypes.c_void_p(16), 4, 64, 64, ctypes.c_void_p(16),
+            64, 64, NULL, _lib.EPI_BIAS_GELU | _lib.EPI_RAW_BF16, NULL, NULL, 0, ctypes.c_void_p(16), 64, 1.0, NULL,
+            0, NULL)
+    _expect("OUDJAT_ERR_UNSUPPORTED_LAYOUT", "oudjat_linear_bf16", ctypes.c_void_p(16), 4, 64, 64, ctypes.c_void_p(16),
+            64, 64, ctypes.c_void_p(24), _lib.EPI_BIAS | _lib.EPI_RAW_BF16, NULL, NULL, 0, ctypes.c_void_p(16), 64, 1.0,
+            NULL, 0, NULL)
+
+
+def test_swiglu_nvfp4_gemm_rejects_bad_arguments():
+    # N not a multiple of 256; one bias only
+    _expect("OUDJAT_ERR_UNSUPPORTED_SHAPE", "oudjat_linear_swiglu_nvfp4", ctypes.c_void_p(16), 4, 64, 64,
+            ctypes.c_void_p(16), 128, 64, ctypes.c_void_p(16), 128, 1.0, NULL, 1.0, NULL, ctypes.c_void_p(16),
+            ctypes.c_void_p(16), 128, NULL)
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_linear_swiglu_nvfp4", ctypes.c_void_p(16), 4, 64, 64,
+            ctypes.c_void_p(16), 256, 64, ctypes.c_void_p(16), 256, 1.0, ctypes.c_void_p(16), 1.0, NULL,
+            ctypes.c_void_p(16), ctypes.c_void_p(16), 256, NULL)
 
 
 def test_low_precision_entry_points_reject_bad_arguments():
