@@ -19,6 +19,10 @@
         read / write bytes per dispatch from the two counter runs, scaled as in `traffic`. For the
         standalone kernels of `python -m appcorr_amd.kernel_bench --calib-copy-mib 1024`.
 
+    python -m appcorr_amd.profiling bench-table <title> <command> <bench line file>...
+        Markdown table of bench.py lines (one JSON line per file; FILE.args beside FILE.json holds the
+        arguments of that run).
+
     python -m appcorr_amd.profiling stalls <kernel_trace.csv> <counter_collection.csv,...>
             <kernel substrings, comma-separated> <title> <command>
         Markdown table per kernel of the memory-path and issue counters of several `rocprofv3 --pmc`
@@ -253,6 +257,26 @@ def stalls(trace_csv: str, counter_csvs, subs, title: str, cmd: str) -> str:
     return "\n".join(lines)
 
 
+def bench_table(paths, title: str, cmd: str) -> str:
+    """Markdown table of bench.py lines: each path is a file whose last line is one bench JSON line, and
+    the same path with `.args` in place of `.json` holds the arguments it ran with."""
+    lines = [f"# {title}", "", "Commands (run from the repository root on one MI355X):", "", "```", cmd, "```", "",
+             "| args | workload | B | keep | rows M | precision | ms / pass | corrected tokens/s | pass TFLOP/s | "
+             "dominant site (frac of peak) | sites (us) |", "|---|---|---:|---:|---:|---|---:|---:|---:|---|---|"]
+    for path in paths:
+        d = json.loads(open(path).read().strip().splitlines()[-1])
+        ap = path[:-5] + ".args" if path.endswith(".json") else path + ".args"
+        args = open(ap).read().strip() if os.path.exists(ap) else ""
+        c = d["config"]
+        roof = d.get("roofline") or {}
+        sites = ", ".join(f"{k} {v['avg_us']:.1f}" for k, v in (roof.get("sites") or {}).items())
+        dom = f"{roof.get('kernel')} ({roof.get('frac', 0):.3f})" if roof else "-"
+        lines.append(f"| `{args or '(default)'}` | {c['workload']} | {c['batch']} | {c['keep_ratio']} | "
+                     f"{c['selected_rows']} | {c['correct_precision']} | {d['ms_per_step']:.3f} | {d['value']:,.0f} | "
+                     f"{c['pass_tflops_achieved']} | {dom} | {sites} |")
+    return "\n".join(lines)
+
+
 def main(argv):
     if len(argv) >= 5 and argv[0] == "kernel-stats":
         print(kernel_stats(argv[1], int(argv[2]), argv[3], argv[4]))
@@ -260,6 +284,8 @@ def main(argv):
         print(traffic(argv[1], argv[2], argv[3], argv[4], float(argv[5]), argv[6], argv[7], argv[8]))
     elif len(argv) >= 6 and argv[0] == "mfma":
         print(mfma(argv[1], argv[2], argv[3].split(","), argv[4], argv[5]))
+    elif len(argv) >= 4 and argv[0] == "bench-table":
+        print(bench_table(argv[3:], argv[1], argv[2]))
     elif len(argv) >= 6 and argv[0] == "stalls":
         print(stalls(argv[1], argv[2].split(","), argv[3].split(","), argv[4], argv[5]))
     elif len(argv) >= 9 and argv[0] == "kernels":
