@@ -74,26 +74,22 @@ def kernel_stats(path: str, passes: int, title: str, cmd: str) -> str:
     return "\n".join(out)
 
 
-def _per_kernel(path: str):
-    acc = defaultdict(list)
-    for r in csv.DictReader(open(path)):
-        acc[r["Kernel_Name"]].append(float(r["Counter_Value"]))
-    return acc
-
-
 def traffic(fetch_csv: str, write_csv: str, kernel: str, calib: str, calib_bytes: float, json_out: str, key: str,
             cmd: str) -> str:
-    f, w = _per_kernel(fetch_csv), _per_kernel(write_csv)
+    f, w = _groups(fetch_csv, "Counter_Value"), _groups(write_csv, "Counter_Value")
 
     def pick(d, sub):
-        names = [n for n in d if sub in n]
-        if not names:
+        # the launch grid with the most dispatches of the kernel (a pass's launches, not set-up work
+        # such as the approximate pass that fills the caches, which may run the same kernel on more rows)
+        groups = [k for k in d if sub in k[0]]
+        if not groups:
             raise SystemExit(f"no kernel matching {sub!r}")
-        vals = [v for n in names for v in d[n]]
-        return names[0], sum(vals) / len(vals), len(vals)
+        key = max(groups, key=lambda k: len(d[k]))
+        vals = d[key]
+        return key[0], sum(vals) / len(vals), len(vals)
 
     def largest(d, sub):  # the calibration copy is the largest dispatch of its kernel in the run
-        vals = [v for n in d if sub in n for v in d[n]]
+        vals = [v for k in d if sub in k[0] for v in d[k]]
         if not vals:
             raise SystemExit(f"no kernel matching {sub!r}")
         return max(vals)
