@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be loaded before the HIP library, see module docstring
 
 LIB_PATH = Path(__file__).resolve().parent / "liboudjat_hip.so"
-ABI_VERSION = 15
+ABI_VERSION = 16
 
 OK = 0
 STATUS_NAMES = {
@@ -88,6 +88,7 @@ SIGNATURES: dict[str, list] = {
     "oudjat_rope_active_inplace": [_p, _i64, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _i64, _i64, _i64, _p],
     "oudjat_qkv_rope_kv_scatter": [_p, _i64, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p, _p, _i64, _i64, _p, _p],
     "oudjat_layernorm_rows": [_p, _i64, _i64, _i64, _p, _p, _f32, _p, _i64, _p],
+    "oudjat_layernorm_rows_prefetch": [_p, _i64, _i64, _i64, _p, _p, _f32, _p, _i64, _p, _i64, _p],
     "oudjat_linear_bf16": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i32, _p, _p, _i64, _p, _i64, _f32, _p, _i64,
                            _p],
     "oudjat_linear_workspace_elems": [_i64, _i64, _i64, _i32],

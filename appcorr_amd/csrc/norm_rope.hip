@@ -1,5 +1,7 @@
 // LayerNorm over selected rows, rotate-half RoPE on the active rows, and the fused post-QKV step
 // (RoPE + in-place K/V cache rewrite + packed query write).
+#include <type_traits>
+
 #include "nvfp4.hpp"
 
 namespace oudjat {
@@ -82,24 +84,51 @@ __device__ __forceinline__ void layernorm_row(const float (&v)[CH][8], int lane,
 
 // One wave per row; each lane keeps its CH 16-byte chunks (8 bf16 each) in registers, so the row is
 // read from HBM exactly once.
-template <int CH>
+// PF: the launch also reads one 32-bit word of every 128-byte line of the region [pf, pf + 128 pf_lines)
+// (a lane per line, the lines dealt over all waves of the grid, issued beside the row loads), so that
+// the region sits in the last-level cache when the kernels after this one read it: the weights of a
+// linear that follows, whose first-touch misses would otherwise go to HBM. The words are folded into
+// a register that an empty asm statement consumes (nothing is stored); the output is the same bits.
+template <int CH, bool PF = false>
 __global__ __launch_bounds__(kNormThreads) void layernorm_kernel(const uint16_t* __restrict__ x, int64_t rows, int C,
                                                                int64_t xs, const uint16_t* __restrict__ w,
                                                                const uint16_t* __restrict__ bias, float eps,
                                                                uint16_t* __restrict__ out, int64_t os,
-                                                               const float* __restrict__ xh_ts) {
+                                                               const float* __restrict__ xh_ts,
+                                                               const uint32_t* __restrict__ pf = nullptr,
+                                                               int64_t pf_lines = 0) {
   const int64_t row = (int64_t)blockIdx.x * kNormRowsPerWg + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  if (!PF && row >= rows) return;
   const int lane = threadIdx.x & 63;
   const int chunks = C >> 3;
-  const uint4* xv = reinterpret_cast<const uint4*>(x + row * xs);
-  float v[CH][8];
+  // Every load of the lane is issued before the first use (one memory round trip per wave).
+  uint4 raw[CH];
+  if (row < rows) {
+    const uint4* xv = reinterpret_cast<const uint4*>(x + row * xs);
 #pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    const int c = lane + 64 * j;
-    if (c < chunks) unpack8(xv[c], v[j]);
+    for (int j = 0; j < CH; ++j) {
+      const int c = lane + 64 * j;
+      if (c < chunks) raw[j] = xv[c];
+    }
   }
-  layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, out + row * os, xh_ts);
+  uint32_t touched = 0;
+  const int64_t l0 = (int64_t)blockIdx.x * kNormThreads + threadIdx.x;
+  if (PF && l0 < pf_lines) touched = pf[l0 * 32];
+  if (row < rows) {
+    float v[CH][8];
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = lane + 64 * j;
+      if (c < chunks) unpack8(raw[j], v[j]);
+    }
+    layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, out + row * os, xh_ts);
+  }
+  if constexpr (PF) {
+    // Regions of more lines than the grid has lanes: the rest after the row's work.
+    const int64_t lanes = (int64_t)gridDim.x * kNormThreads;
+    for (int64_t l = l0 + lanes; l < pf_lines; l += lanes) touched ^= pf[l * 32];
+    asm volatile("" ::"v"(touched));
+  }
 }
 
 // The gather of a packed run's selected rows fused with the first block's LayerNorm: packed row i is
@@ -156,15 +185,25 @@ __global__ __launch_bounds__(kNormThreads) void packed_residual_ln_kernel(
   const uint4* mv = reinterpret_cast<const uint4*>(mlp + row * C);
   uint4* ov = reinterpret_cast<uint4*>(xn + row * C);
   uint4* bv = reinterpret_cast<uint4*>(bos + bi[row] * bsb + ti[row] * bsn);
+  uint4 ra[CH], rt[CH], rm[CH];  // every load of the lane in flight before the first use
+#pragma unroll
+  for (int j = 0; j < CH; ++j) {
+    const int c = lane + 64 * j;
+    if (c < chunks) {
+      ra[j] = av[c];
+      rt[j] = tv[c];
+      rm[j] = mv[c];
+    }
+  }
   float v[CH][8];
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
     const int c = lane + 64 * j;
     if (c < chunks) {
       float fa[8], ft[8], fm[8], fo[8], fb[8];
-      unpack8(av[c], fa);
-      unpack8(tv[c], ft);
-      unpack8(mv[c], fm);
+      unpack8(ra[j], fa);
+      unpack8(rt[j], ft);
+      unpack8(rm[j], fm);
 #pragma unroll
       for (int e = 0; e < 8; ++e) {
         fo[e] = ft[e] + fm[e];
@@ -362,8 +401,13 @@ using namespace oudjat;
 
 static int layernorm_launch(const uint16_t* x, int64_t rows, int64_t C, int64_t xs, const uint16_t* w,
                             const uint16_t* b, float eps, const float* xh_ts, uint16_t* out, int64_t os,
-                            oudjat_stream_t stream, const char* what) {
+                            oudjat_stream_t stream, const char* what, const void* pf = nullptr,
+                            int64_t pf_bytes = 0) {
   OUDJAT_REQUIRE(rows >= 0 && C > 0, OUDJAT_ERR_INVALID_ARGUMENT, "%s: bad size", what);
+  OUDJAT_REQUIRE(pf_bytes >= 0 && (pf_bytes == 0 || pf), OUDJAT_ERR_INVALID_ARGUMENT,
+                 "%s: prefetch region of %lld bytes without a pointer", what, (long long)pf_bytes);
+  OUDJAT_REQUIRE(pf_bytes == 0 || aligned(pf, 4), OUDJAT_ERR_UNSUPPORTED_LAYOUT,
+                 "%s: prefetch region must be 4-byte aligned", what);
   if (rows == 0) return OUDJAT_OK;
   OUDJAT_REQUIRE(x && w && b && out, OUDJAT_ERR_INVALID_ARGUMENT, "%s: null pointer", what);
   OUDJAT_REQUIRE(C % 8 == 0 && xs % 8 == 0 && os % 8 == 0 && aligned(x, 16) && aligned(out, 16) && aligned(w, 16) &&
@@ -373,17 +417,35 @@ static int layernorm_launch(const uint16_t* x, int64_t rows, int64_t C, int64_t 
   OUDJAT_REQUIRE(C <= 8192, OUDJAT_ERR_TOO_LARGE, "%s: C=%lld > 8192", what, (long long)C);
   const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg);
   hipStream_t st = as_stream(stream);
-  if (C <= 512) layernorm_kernel<1><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os, xh_ts);
-  else if (C <= 1024) layernorm_kernel<2><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os, xh_ts);
-  else if (C <= 2048) layernorm_kernel<4><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os, xh_ts);
-  else if (C <= 4096) layernorm_kernel<8><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os, xh_ts);
-  else layernorm_kernel<16><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os, xh_ts);
+  const int64_t pf_lines = pf_bytes / 128;  // whole lines; a partial last line is left to the reader
+  const uint32_t* p = static_cast<const uint32_t*>(pf);
+  auto go = [&](auto pf_c) {
+    constexpr bool P = decltype(pf_c)::value;
+#define OUDJAT_LN(CHV) \
+  layernorm_kernel<CHV, P><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os, xh_ts, p, pf_lines)
+    if (C <= 512) OUDJAT_LN(1);
+    else if (C <= 1024) OUDJAT_LN(2);
+    else if (C <= 2048) OUDJAT_LN(4);
+    else if (C <= 4096) OUDJAT_LN(8);
+    else OUDJAT_LN(16);
+#undef OUDJAT_LN
+  };
+  if (pf_lines > 0) go(std::true_type{});
+  else go(std::false_type{});
   return check_launch(what);
 }
 
 extern "C" int oudjat_layernorm_rows(const uint16_t* x, int64_t rows, int64_t C, int64_t xs, const uint16_t* w,
                                      const uint16_t* b, float eps, uint16_t* out, int64_t os, oudjat_stream_t stream) {
   return layernorm_launch(x, rows, C, xs, w, b, eps, nullptr, out, os, stream, "layernorm_rows");
+}
+
+extern "C" int oudjat_layernorm_rows_prefetch(const uint16_t* x, int64_t rows, int64_t C, int64_t xs,
+                                              const uint16_t* w, const uint16_t* b, float eps, uint16_t* out,
+                                              int64_t os, const void* prefetch, int64_t prefetch_bytes,
+                                              oudjat_stream_t stream) {
+  return layernorm_launch(x, rows, C, xs, w, b, eps, nullptr, out, os, stream, "layernorm_rows_prefetch", prefetch,
+                          prefetch_bytes);
 }
 
 extern "C" int oudjat_layernorm_rows_nvfp4(const uint16_t* x, int64_t rows, int64_t C, int64_t xs, const uint16_t* w,

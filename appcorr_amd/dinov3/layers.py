@@ -404,7 +404,8 @@ class SelfAttentionBlock(nn.Module):
                        site="proj")
         ones = self._gamma(nn.Identity(), x2)
         x_attn = K.fused_layerscale_add(x2, inc, ones)                       # x + ls1(attn)
-        mlp = self._mlp_scaled(K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps))
+        mlp = self._mlp_scaled(K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps,
+                                            prefetch=self._mlp_prefetch()))
         bos, out = K.residual_pair(inc, x_attn, mlp)  # block.py:336-347: inc + mlp cached, x_attn + mlp out
         cache_feature[f"{tag}_blocks_out_sum"] = bos.view(B, N, C)
         out = out.view(B, N, C)
@@ -726,13 +727,22 @@ class SelfAttentionBlock(nn.Module):
                                        gamma=g1, resid=x_act)                             # block.py:1129-1134
         with trace_range("correct_ffn"):
             ts2 = None if isinstance(self.mlp, Mlp) else _fp4_scale(self.mlp.w1)
-            xn2 = K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps, nvfp4_scale=ts2)  # :1141
+            xn2 = K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps, nvfp4_scale=ts2,  # :1141
+                               prefetch=self._mlp_prefetch())
             if residual is not None and ts2 is None:
                 fused = self._mlp_scaled_residual(xn2, x_act, x_attn, qs, *residual)
                 if fused is not None:
                     return x_attn, fused
             mlp = self._mlp_scaled(xn2, xn_is_xhat=ts2 is not None)
         return x_attn, mlp
+
+    def _mlp_prefetch(self) -> Tensor | None:
+        """The weight that norm2's launch warms in the last-level cache: fc2's (8 MB at ViT-L), read by
+        the MLP's second GEMM after fc1 and otherwise fetched from HBM on first touch (measured at the
+        headline: fc2 48.7 -> 43.7 us per block). bf16 Mlp only; None otherwise."""
+        if isinstance(self.mlp, Mlp) and LP.low_precision_state(self.mlp.fc2) == "bf16":
+            return self.mlp.fc2.weight
+        return None
 
     def _mlp_scaled_residual(self, xn: Tensor, x_act: Tensor, x_attn: Tensor, qs: PackedQueryState, bos: Tensor,
                              next_norm):

@@ -572,11 +572,16 @@ def residual_prune_compact(keep: torch.Tensor, spatial: torch.Tensor, dindice: t
 
 
 def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: float = 1e-5,
-               out: torch.Tensor | None = None, nvfp4_scale: torch.Tensor | None = None) -> torch.Tensor:
+               out: torch.Tensor | None = None, nvfp4_scale: torch.Tensor | None = None,
+               prefetch: torch.Tensor | None = None) -> torch.Tensor:
     """LayerNorm of bf16 rows (fp32 statistics). With nvfp4_scale (the consuming linear's NVFP4 activation
     scale) the result is instead the NVFP4 operand x_hat of LayerNorm(x), as nvfp4_quantize_dequantize
-    would give it on the LayerNorm output."""
-    _require_cuda(x, weight, bias)
+    would give it on the LayerNorm output.
+
+    prefetch: a contiguous device tensor (a weight read by a later kernel) that the same launch reads
+    once, a word per 128-byte line, so that it is in the last-level cache when that kernel runs; the
+    output is unchanged (bf16 path only)."""
+    _require_cuda(x, weight, bias, prefetch)
     _require(x.dtype == weight.dtype == bias.dtype == torch.bfloat16, "layer_norm: bf16 only")
     ts = _nvfp4_scale(nvfp4_scale, "layer_norm")
     C = x.shape[-1]
@@ -585,7 +590,13 @@ def layer_norm(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor, eps: f
     if out is None:
         out = torch.empty(x.shape, device=x.device, dtype=x.dtype)
     o2 = out.view(-1, C)
-    if ts is None:
+    if ts is None and prefetch is not None:
+        _require(prefetch.is_contiguous() and prefetch.device == x.device, "layer_norm: prefetch must be a contiguous "
+                 "tensor on the rows' device")
+        _launch("layernorm", x, "oudjat_layernorm_rows_prefetch", _ptr(x2), x2.shape[0], C, x2.stride(0),
+                _ptr(weight.contiguous()), _ptr(bias.contiguous()), float(eps), _ptr(o2), o2.stride(0),
+                _ptr(prefetch), prefetch.numel() * prefetch.element_size(), _stream(x))
+    elif ts is None:
         _launch("layernorm", x, "oudjat_layernorm_rows", _ptr(x2), x2.shape[0], C, x2.stride(0),
                 _ptr(weight.contiguous()), _ptr(bias.contiguous()), float(eps), _ptr(o2), o2.stride(0), _stream(x))
     else:

@@ -276,6 +276,18 @@ int oudjat_layernorm_rows(const uint16_t* x, int64_t rows, int64_t C, int64_t x_
                           const uint16_t* weight, const uint16_t* bias, float eps, uint16_t* out,
                           int64_t out_row_stride, oudjat_stream_t stream);
 
+/* Row 5 -- oudjat_layernorm_rows (same output bits) that also reads one 32-bit word of every whole
+ * 128-byte line of the read-only device region [prefetch, prefetch + prefetch_bytes) in the same
+ * launch, so that the region is resident in the last-level cache when the kernels after it run:
+ * block.py:1141's norm2 warming the weights of the MLP's second linear (ffn_layers.py:48), whose
+ * first-touch misses would otherwise wait on HBM. Nothing is written to the region. The reference's
+ * LayerNorm has no such argument (a cache hint with no effect on results). prefetch_bytes >= 0;
+ * prefetch 4-byte aligned and non-NULL when prefetch_bytes > 0; 0 bytes is oudjat_layernorm_rows. */
+int oudjat_layernorm_rows_prefetch(const uint16_t* x, int64_t rows, int64_t C, int64_t x_row_stride,
+                                   const uint16_t* weight, const uint16_t* bias, float eps, uint16_t* out,
+                                   int64_t out_row_stride, const void* prefetch, int64_t prefetch_bytes,
+                                   oudjat_stream_t stream);
+
 /* Rows 6, 11, 12, 13 -- C[M, N] = epilogue(A[M, K] . W[N, K]^T) on bf16 MFMA with fp32 accumulate.
  * Replaces the qkv / proj / fc1 / fc2 nn.Linear calls (attention.py:415,532; ffn_layers.py:43-49)
  * and the LayerScale / residual ops folded into their epilogues (block.py:1129-1141); the SwiGLU

@@ -213,6 +213,23 @@ def test_layer_norm(dev, rows, C):
     assert float((diff > 0).double().mean()) <= 0.01
 
 
+@pytest.mark.parametrize("rows,C,pf_elems,pf_dtype", [(4176, 1024, 4 << 20, torch.bfloat16),
+                                                      (3, 1024, (1 << 20) + 7, torch.float32),
+                                                      (103, 384, 31, torch.bfloat16),
+                                                      (1656, 4096, 1 << 22, torch.bfloat16)])
+def test_layer_norm_prefetch_is_the_same_layer_norm(dev, rows, C, pf_elems, pf_dtype):
+    """Warming a region in the same launch leaves the output bits alone: regions of one line per lane,
+    of many lines per lane (3 rows: a 4-wave grid), below one line, and of a ragged byte count."""
+    x = (_rand((rows, C), 25).float() * 3 + 1).to(torch.bfloat16).to(dev)
+    w, b = _rand((C,), 26).to(dev), _rand((C,), 27).to(dev)
+    region = torch.ones(pf_elems, device=dev, dtype=pf_dtype)
+    want = K.layer_norm(x, w, b, 1e-5)
+    got = K.layer_norm(x, w, b, 1e-5, prefetch=region)
+    torch.cuda.synchronize()
+    assert torch.equal(got.view(torch.int16), want.view(torch.int16))
+    assert bool((region == 1).all())  # read only
+
+
 def _rope_inputs(M, H, D, seed):
     cfg = OM.with_overrides(OM.CONFIGS["vitl16_512"], dim=H * D, heads=H)
     sin, cos = OM.rope_tables(cfg)

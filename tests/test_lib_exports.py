@@ -136,6 +136,19 @@ def test_lse_entry_points_reject_bad_arguments():
               NULL)
 
 
+def test_layernorm_prefetch_rejects_bad_regions():
+    """The cache-warming region is checked before anything else (here with zero rows, so no GPU)."""
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_layernorm_rows_prefetch", NULL, 0, 1024, 1024, NULL, NULL, 1e-5,
+            NULL, 1024, NULL, 4096, NULL)
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_layernorm_rows_prefetch", NULL, 0, 1024, 1024, NULL, NULL, 1e-5,
+            NULL, 1024, ctypes.c_void_p(256), -128, NULL)
+    _expect("OUDJAT_ERR_UNSUPPORTED_LAYOUT", "oudjat_layernorm_rows_prefetch", NULL, 0, 1024, 1024, NULL, NULL, 1e-5,
+            NULL, 1024, ctypes.c_void_p(258), 4096, NULL)
+    _lib.call("oudjat_layernorm_rows_prefetch", NULL, 0, 1024, 1024, NULL, NULL, 1e-5, NULL, 1024,
+              ctypes.c_void_p(256), 4096, NULL)
+    _lib.call("oudjat_layernorm_rows_prefetch", NULL, 0, 1024, 1024, NULL, NULL, 1e-5, NULL, 1024, NULL, 0, NULL)
+
+
 def test_zero_sized_calls_are_noops():
     # Nothing to do -> OK without touching any pointer (and without a GPU).
     _lib.call("oudjat_gather_rows", NULL, 0, 0, 2048, NULL, NULL, 0, NULL, 2048, NULL)
