@@ -9,6 +9,16 @@ namespace oudjat {
 static constexpr int kNormThreads = 256;
 static constexpr int kNormRowsPerWg = kNormThreads / 64;
 
+// Waves per LayerNorm row (see layernorm_row): 1 up to C = 1024; 2 up to 2048 and 4 up to 8192 when
+// the row's 16-byte chunks split into that many equal, even parts (an NVFP4 block of 16 elements is
+// two chunks and must stay in one wave); 1 otherwise. A workgroup holds kNormRowsPerWg / parts rows.
+static int row_parts(int64_t C) {
+  const int64_t chunks = C / 8;
+  if (C <= 1024) return 1;
+  const int n = C <= 2048 ? 2 : 4;
+  return chunks % (2 * n) == 0 ? n : 1;
+}
+
 // LayerNorm of one row held by one wave: lane l holds chunks l + 64 j (j < CH, 8 values each, as
 // fp32 from bf16). Statistics are fp32: mean, then the biased variance around it. Shared by the
 // standalone kernel and the fused residual kernel so both give the same bits.
@@ -16,11 +26,32 @@ static constexpr int kNormRowsPerWg = kNormThreads / 64;
 // LayerNorm output with tensor scale *xh_ts -- what nvfp4_quantize_dequantize gives on the output
 // (a 16-element block is the chunk pair of lanes l, l ^ 1). The LayerNorm values themselves are the
 // same either way.
-template <int CH>
+//
+// Rows wider than 1024 are split over NWR = 2 or 4 waves of one workgroup (row_parts): each wave holds
+// an equal, even number of the row's chunks (`chunks` and the w / bias / out_row pointers are then
+// its part's), the two row sums combine the waves' sums in wave order through `red` (LDS,
+// 2 * kNormRowsPerWg floats: NWR per row slot `slot` for each sum), and a row past the end (`live` false) still takes part in
+// the workgroup barriers but stores nothing. NWR = 1 is the one-wave row above.
+template <int NWR>
+__device__ __forceinline__ float row_parts_sum(float s, float* red, int slot, int part, int lane) {
+  if constexpr (NWR == 1) {
+    return s;
+  } else {
+    if (lane == 0) red[slot * NWR + part] = s;
+    __syncthreads();
+    float t = red[slot * NWR];
+#pragma unroll
+    for (int i = 1; i < NWR; ++i) t += red[slot * NWR + i];
+    return t;
+  }
+}
+
+template <int CH, int NWR = 1>
 __device__ __forceinline__ void layernorm_row(const float (&v)[CH][8], int lane, int chunks, int C,
                                               const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
                                               float eps, uint16_t* __restrict__ out_row,
-                                              const float* __restrict__ xh_ts = nullptr) {
+                                              const float* __restrict__ xh_ts = nullptr, float* red = nullptr,
+                                              int slot = 0, int part = 0, bool live = true) {
   float sum = 0.0f;
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
@@ -30,7 +61,7 @@ __device__ __forceinline__ void layernorm_row(const float (&v)[CH][8], int lane,
       for (int e = 0; e < 8; ++e) sum += v[j][e];
     }
   }
-  const float mean = wave_sum(sum) / (float)C;
+  const float mean = row_parts_sum<NWR>(wave_sum(sum), red, slot, part, lane) / (float)C;
   float sq = 0.0f;
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
@@ -43,7 +74,8 @@ __device__ __forceinline__ void layernorm_row(const float (&v)[CH][8], int lane,
       }
     }
   }
-  const float var = wave_sum(sq) / (float)C;
+  // (a second set of slots: no barrier needed between the two sums)
+  const float var = row_parts_sum<NWR>(wave_sum(sq), red + kNormRowsPerWg, slot, part, lane) / (float)C;
   const float rstd = 1.0f / sqrtf(var + eps);
   const uint4* wv = reinterpret_cast<const uint4*>(w);
   const uint4* bv = reinterpret_cast<const uint4*>(bias);
@@ -58,7 +90,7 @@ __device__ __forceinline__ void layernorm_row(const float (&v)[CH][8], int lane,
         unpack8(bv[c], fb);
 #pragma unroll
         for (int e = 0; e < 8; ++e) y[e] = fmaf(fw[e], (v[j][e] - mean) * rstd, fb[e]);
-        ov[c] = pack8(y);
+        if (live) ov[c] = pack8(y);
       }
     }
     return;
@@ -78,18 +110,18 @@ __device__ __forceinline__ void layernorm_row(const float (&v)[CH][8], int lane,
     }
     float h[8];
     nvfp4_xhat8_pair(y, ts, h);  // every lane takes part (the block maximum is a lane-pair exchange)
-    if (c < chunks) ov[c] = pack8(h);
+    if (live && c < chunks) ov[c] = pack8(h);
   }
 }
 
-// One wave per row; each lane keeps its CH 16-byte chunks (8 bf16 each) in registers, so the row is
-// read from HBM exactly once.
+// One wave per row (NWR waves for rows wider than 1024: layernorm_row); each lane keeps its CH 16-byte
+// chunks (8 bf16 each) in registers, so the row is read from HBM exactly once.
 // PF: the launch also reads one 32-bit word of every 128-byte line of the region [pf, pf + 128 pf_lines)
 // (a lane per line, the lines dealt over all waves of the grid, issued beside the row loads), so that
 // the region sits in the last-level cache when the kernels after this one read it: the weights of a
 // linear that follows, whose first-touch misses would otherwise go to HBM. The words are folded into
 // a register that an empty asm statement consumes (nothing is stored); the output is the same bits.
-template <int CH, bool PF = false>
+template <int CH, int NWR, bool PF = false>
 __global__ __launch_bounds__(kNormThreads) void layernorm_kernel(const uint16_t* __restrict__ x, int64_t rows, int C,
                                                                int64_t xs, const uint16_t* __restrict__ w,
                                                                const uint16_t* __restrict__ bias, float eps,
@@ -97,14 +129,20 @@ __global__ __launch_bounds__(kNormThreads) void layernorm_kernel(const uint16_t*
                                                                const float* __restrict__ xh_ts,
                                                                const uint32_t* __restrict__ pf = nullptr,
                                                                int64_t pf_lines = 0) {
-  const int64_t row = (int64_t)blockIdx.x * kNormRowsPerWg + (threadIdx.x >> 6);
-  if (!PF && row >= rows) return;
+  __shared__ float red[2 * kNormRowsPerWg];
+  const int wave = threadIdx.x >> 6, slot = wave / NWR, part = wave % NWR;
+  const int64_t row = (int64_t)blockIdx.x * (kNormRowsPerWg / NWR) + slot;
+  if (NWR == 1 && !PF && row >= rows) return;
+  const bool live = row < rows;
   const int lane = threadIdx.x & 63;
-  const int chunks = C >> 3;
+  const int chunks = (C >> 3) / NWR;  // this wave's part of the row
+  const int c0 = part * chunks * 8;   // its first column
   // Every load of the lane is issued before the first use (one memory round trip per wave).
   uint4 raw[CH];
-  if (row < rows) {
-    const uint4* xv = reinterpret_cast<const uint4*>(x + row * xs);
+#pragma unroll
+  for (int j = 0; j < CH; ++j) raw[j] = make_uint4(0u, 0u, 0u, 0u);
+  if (live) {
+    const uint4* xv = reinterpret_cast<const uint4*>(x + row * xs + c0);
 #pragma unroll
     for (int j = 0; j < CH; ++j) {
       const int c = lane + 64 * j;
@@ -114,14 +152,12 @@ __global__ __launch_bounds__(kNormThreads) void layernorm_kernel(const uint16_t*
   uint32_t touched = 0;
   const int64_t l0 = (int64_t)blockIdx.x * kNormThreads + threadIdx.x;
   if (PF && l0 < pf_lines) touched = pf[l0 * 32];
-  if (row < rows) {
+  if (NWR > 1 || live) {
     float v[CH][8];
 #pragma unroll
-    for (int j = 0; j < CH; ++j) {
-      const int c = lane + 64 * j;
-      if (c < chunks) unpack8(raw[j], v[j]);
-    }
-    layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, out + row * os, xh_ts);
+    for (int j = 0; j < CH; ++j) unpack8(raw[j], v[j]);
+    layernorm_row<CH, NWR>(v, lane, chunks, C, w + c0, bias + c0, eps, out + (live ? row : 0) * os + c0, xh_ts, red,
+                           slot, part, live);
   }
   if constexpr (PF) {
     // Regions of more lines than the grid has lanes: the rest after the row's work.
@@ -134,7 +170,7 @@ __global__ __launch_bounds__(kNormThreads) void layernorm_kernel(const uint16_t*
 // The gather of a packed run's selected rows fused with the first block's LayerNorm: packed row i is
 // x[batch_idx[i], token_idx[i]], copied byte for byte to x_out, and its LayerNorm (or the NVFP4 operand
 // of it) goes to ln_out with layernorm_kernel's arithmetic (the same bits).
-template <int CH>
+template <int CH, int NWR>
 __global__ __launch_bounds__(kNormThreads) void gather_ln_kernel(const uint16_t* __restrict__ x, int64_t sb,
                                                                 int64_t sn, const int64_t* __restrict__ bidx,
                                                                 const int64_t* __restrict__ tidx, int64_t rows, int C,
@@ -143,107 +179,130 @@ __global__ __launch_bounds__(kNormThreads) void gather_ln_kernel(const uint16_t*
                                                                 uint16_t* __restrict__ x_out,
                                                                 uint16_t* __restrict__ ln_out,
                                                                 const float* __restrict__ xh_ts) {
-  const int64_t row = (int64_t)blockIdx.x * kNormRowsPerWg + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  __shared__ float red[2 * kNormRowsPerWg];
+  const int wave = threadIdx.x >> 6, slot = wave / NWR, part = wave % NWR;
+  const int64_t row = (int64_t)blockIdx.x * (kNormRowsPerWg / NWR) + slot;
+  if (NWR == 1 && row >= rows) return;
+  const bool live = row < rows;
   const int lane = threadIdx.x & 63;
-  const int chunks = C >> 3;
-  const uint4* xv = reinterpret_cast<const uint4*>(x + bidx[row] * sb + tidx[row] * sn);
-  uint4* ov = reinterpret_cast<uint4*>(x_out + row * C);
+  const int chunks = (C >> 3) / NWR;
+  const int c0 = part * chunks * 8;
+  const int64_t r = live ? row : 0;
   uint4 raw[CH];
 #pragma unroll
-  for (int j = 0; j < CH; ++j) {
-    const int c = lane + 64 * j;
-    if (c < chunks) raw[j] = xv[c];
+  for (int j = 0; j < CH; ++j) raw[j] = make_uint4(0u, 0u, 0u, 0u);
+  uint4* ov = reinterpret_cast<uint4*>(x_out + r * C + c0);
+  if (live) {
+    const uint4* xv = reinterpret_cast<const uint4*>(x + bidx[row] * sb + tidx[row] * sn + c0);
+#pragma unroll
+    for (int j = 0; j < CH; ++j) {
+      const int c = lane + 64 * j;
+      if (c < chunks) raw[j] = xv[c];
+    }
   }
   float v[CH][8];
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
     const int c = lane + 64 * j;
-    if (c < chunks) {
-      ov[c] = raw[j];
-      unpack8(raw[j], v[j]);
-    }
+    if (live && c < chunks) ov[c] = raw[j];
+    unpack8(raw[j], v[j]);
   }
-  layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, ln_out + row * C, xh_ts);
+  layernorm_row<CH, NWR>(v, lane, chunks, C, w + c0, bias + c0, eps, ln_out + r * C + c0, xh_ts, red, slot, part,
+                         live);
 }
 
 // The residual step of a correction block on packed selected rows fused with the next block's
 // LayerNorm: x_new = bf16(x_attn + mlp), blocks_out_sum[b_i, t_i] = bf16(bf16(x_attn - x_act) + mlp)
 // and ln_out = LayerNorm(x_new) (of the bf16 x_new, exactly as the standalone kernel computes it).
-template <int CH>
+template <int CH, int NWR>
 __global__ __launch_bounds__(kNormThreads) void packed_residual_ln_kernel(
     const uint16_t* __restrict__ xa, const uint16_t* __restrict__ xt, const uint16_t* __restrict__ mlp, int64_t rows,
     int C, const int64_t* __restrict__ bi, const int64_t* __restrict__ ti, uint16_t* __restrict__ bos, int64_t bsb,
     int64_t bsn, uint16_t* __restrict__ xn, const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
     float eps, uint16_t* __restrict__ ln_out, const float* __restrict__ xh_ts) {
-  const int64_t row = (int64_t)blockIdx.x * kNormRowsPerWg + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  __shared__ float red[2 * kNormRowsPerWg];
+  const int wave = threadIdx.x >> 6, slot = wave / NWR, part = wave % NWR;
+  const int64_t row = (int64_t)blockIdx.x * (kNormRowsPerWg / NWR) + slot;
+  if (NWR == 1 && row >= rows) return;
+  const bool live = row < rows;
   const int lane = threadIdx.x & 63;
-  const int chunks = C >> 3;
-  const uint4* av = reinterpret_cast<const uint4*>(xa + row * C);
-  const uint4* tv = reinterpret_cast<const uint4*>(xt + row * C);
-  const uint4* mv = reinterpret_cast<const uint4*>(mlp + row * C);
-  uint4* ov = reinterpret_cast<uint4*>(xn + row * C);
-  uint4* bv = reinterpret_cast<uint4*>(bos + bi[row] * bsb + ti[row] * bsn);
+  const int chunks = (C >> 3) / NWR;
+  const int c0 = part * chunks * 8;
+  const int64_t r = live ? row : 0;
+  const uint4* av = reinterpret_cast<const uint4*>(xa + r * C + c0);
+  const uint4* tv = reinterpret_cast<const uint4*>(xt + r * C + c0);
+  const uint4* mv = reinterpret_cast<const uint4*>(mlp + r * C + c0);
+  uint4* ov = reinterpret_cast<uint4*>(xn + r * C + c0);
+  uint4* bv = reinterpret_cast<uint4*>(bos + (live ? bi[row] * bsb + ti[row] * bsn : 0) + c0);
   uint4 ra[CH], rt[CH], rm[CH];  // every load of the lane in flight before the first use
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
     const int c = lane + 64 * j;
-    if (c < chunks) {
+    if (live && c < chunks) {
       ra[j] = av[c];
       rt[j] = tv[c];
       rm[j] = mv[c];
+    } else {
+      ra[j] = rt[j] = rm[j] = make_uint4(0u, 0u, 0u, 0u);
     }
   }
   float v[CH][8];
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
     const int c = lane + 64 * j;
-    if (c < chunks) {
-      float fa[8], ft[8], fm[8], fo[8], fb[8];
-      unpack8(ra[j], fa);
-      unpack8(rt[j], ft);
-      unpack8(rm[j], fm);
+    float fa[8], ft[8], fm[8], fo[8], fb[8];
+    unpack8(ra[j], fa);
+    unpack8(rt[j], ft);
+    unpack8(rm[j], fm);
 #pragma unroll
-      for (int e = 0; e < 8; ++e) {
-        fo[e] = ft[e] + fm[e];
-        fb[e] = round_bf16(ft[e] - fa[e]) + fm[e];
-      }
-      const uint4 o = pack8(fo);
+    for (int e = 0; e < 8; ++e) {
+      fo[e] = ft[e] + fm[e];
+      fb[e] = round_bf16(ft[e] - fa[e]) + fm[e];
+    }
+    const uint4 o = pack8(fo);
+    if (live && c < chunks) {
       ov[c] = o;
       bv[c] = pack8(fb);
-      unpack8(o, v[j]);
     }
+    unpack8(o, v[j]);
   }
-  layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, ln_out + row * C, xh_ts);
+  layernorm_row<CH, NWR>(v, lane, chunks, C, w + c0, bias + c0, eps, ln_out + r * C + c0, xh_ts, red, slot, part,
+                         live);
 }
 
 // The split-K reduce of a LayerScale projection (fc2 / w3) fused with the packed residual step and
 // the next block's LayerNorm: mlp = bf16(bf16(sum_s P[s] * acc_scale + b) * gamma), the slices summed
 // in order from slice 0 (splitk_reduce_kernel's arithmetic), then exactly packed_residual_ln_kernel
 // (x_new, the blocks_out_sum row, and LayerNorm(x_new) when w is given). One wave per row.
-template <int CH>
+template <int CH, int NWR>
 __global__ __launch_bounds__(kNormThreads) void splitk_ls_residual_ln_kernel(
     const float* __restrict__ P, int S, const uint16_t* __restrict__ fb, const uint16_t* __restrict__ fg,
     float acc_scale, const uint16_t* __restrict__ xa, const uint16_t* __restrict__ xt, int64_t rows, int C,
     const int64_t* __restrict__ bi, const int64_t* __restrict__ ti, uint16_t* __restrict__ bos, int64_t bsb,
     int64_t bsn, uint16_t* __restrict__ xn, const uint16_t* __restrict__ w, const uint16_t* __restrict__ bias,
     float eps, uint16_t* __restrict__ ln_out) {
-  const int64_t row = (int64_t)blockIdx.x * kNormRowsPerWg + (threadIdx.x >> 6);
-  if (row >= rows) return;
+  __shared__ float red[2 * kNormRowsPerWg];
+  const int wave = threadIdx.x >> 6, slot = wave / NWR, part = wave % NWR;
+  const int64_t row = (int64_t)blockIdx.x * (kNormRowsPerWg / NWR) + slot;
+  if (NWR == 1 && row >= rows) return;
+  const bool live = row < rows;
   const int lane = threadIdx.x & 63;
-  const int chunks = C >> 3;
+  const int chunks = (C >> 3) / NWR;
+  const int c0 = part * chunks * 8;
+  const int64_t r = live ? row : 0;
   const int64_t slice = rows * (int64_t)C;
-  const uint4* av = reinterpret_cast<const uint4*>(xa + row * C);
-  const uint4* tv = reinterpret_cast<const uint4*>(xt + row * C);
-  uint4* ov = reinterpret_cast<uint4*>(xn + row * C);
-  uint4* bv = reinterpret_cast<uint4*>(bos + bi[row] * bsb + ti[row] * bsn);
+  const uint4* av = reinterpret_cast<const uint4*>(xa + r * C + c0);
+  const uint4* tv = reinterpret_cast<const uint4*>(xt + r * C + c0);
+  uint4* ov = reinterpret_cast<uint4*>(xn + r * C + c0);
+  uint4* bv = reinterpret_cast<uint4*>(bos + (live ? bi[row] * bsb + ti[row] * bsn : 0) + c0);
   float v[CH][8];
 #pragma unroll
   for (int j = 0; j < CH; ++j) {
     const int c = lane + 64 * j;
-    if (c < chunks) {
-      const float* p = P + row * C + 8 * c;
+#pragma unroll
+    for (int e = 0; e < 8; ++e) v[j][e] = 0.0f;
+    if (live && c < chunks) {
+      const float* p = P + r * C + c0 + 8 * c;
       float4 a0 = *reinterpret_cast<const float4*>(p), a1 = *reinterpret_cast<const float4*>(p + 4);
       for (int sl = 1; sl < S; ++sl) {
         const float4 b0 = *reinterpret_cast<const float4*>(p + sl * slice);
@@ -254,12 +313,12 @@ __global__ __launch_bounds__(kNormThreads) void splitk_ls_residual_ln_kernel(
       const float acc[8] = {a0.x, a0.y, a0.z, a0.w, a1.x, a1.y, a1.z, a1.w};
       float fbias[8], g[8], xm[8], fa[8], ft[8], fm[8], fo[8], fbo[8];
       if (fb) {
-        unpack8(reinterpret_cast<const uint4*>(fb)[c], fbias);
+        unpack8(reinterpret_cast<const uint4*>(fb + c0)[c], fbias);
       } else {
 #pragma unroll
         for (int e = 0; e < 8; ++e) fbias[e] = 0.0f;
       }
-      unpack8(reinterpret_cast<const uint4*>(fg)[c], g);
+      unpack8(reinterpret_cast<const uint4*>(fg + c0)[c], g);
 #pragma unroll
       for (int e = 0; e < 8; ++e) xm[e] = round_bf16(__builtin_fmaf(acc[e], acc_scale, fbias[e])) * g[e];
       unpack8(pack8(xm), fm);  // the bf16 mlp row, as the unfused step reads it back
@@ -276,7 +335,8 @@ __global__ __launch_bounds__(kNormThreads) void splitk_ls_residual_ln_kernel(
       unpack8(o, v[j]);
     }
   }
-  if (w) layernorm_row<CH>(v, lane, chunks, C, w, bias, eps, ln_out + row * C);
+  if (w) layernorm_row<CH, NWR>(v, lane, chunks, C, w + c0, bias + c0, eps, ln_out + r * C + c0, nullptr, red, slot,
+                                part, live);
 }
 
 // Thread = (row, head, chunk of 8 in the left half). Rows with patch_mask == 0 are left untouched.
@@ -399,6 +459,34 @@ __global__ __launch_bounds__(256) void qkv_rope_kv_scatter_kernel(
 
 using namespace oudjat;
 
+// Calls f(CH, NWR) (integral constants) with the instance of a LayerNorm-family kernel for row width C:
+// NWR = row_parts(C) waves per row and CH 16-byte chunks per lane (the wave's part over 64 lanes).
+template <typename F>
+static void row_dispatch(int64_t C, F&& f) {
+  using I1 = std::integral_constant<int, 1>;
+  using I2 = std::integral_constant<int, 2>;
+  using I4 = std::integral_constant<int, 4>;
+  using I8 = std::integral_constant<int, 8>;
+  using I16 = std::integral_constant<int, 16>;
+  const int parts = row_parts(C);
+  if (parts == 4) {
+    if (C <= 4096) f(I2{}, I4{});
+    else f(I4{}, I4{});
+  } else if (parts == 2) {
+    f(I2{}, I2{});
+  } else if (C <= 512) {
+    f(I1{}, I1{});
+  } else if (C <= 1024) {
+    f(I2{}, I1{});
+  } else if (C <= 2048) {
+    f(I4{}, I1{});
+  } else if (C <= 4096) {
+    f(I8{}, I1{});
+  } else {
+    f(I16{}, I1{});
+  }
+}
+
 static int layernorm_launch(const uint16_t* x, int64_t rows, int64_t C, int64_t xs, const uint16_t* w,
                             const uint16_t* b, float eps, const float* xh_ts, uint16_t* out, int64_t os,
                             oudjat_stream_t stream, const char* what, const void* pf = nullptr,
@@ -415,20 +503,15 @@ static int layernorm_launch(const uint16_t* x, int64_t rows, int64_t C, int64_t 
                  OUDJAT_ERR_UNSUPPORTED_LAYOUT, "%s: 16-byte aligned rows with C %% 8 == 0 required", what);
   OUDJAT_REQUIRE(!xh_ts || C % 16 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE, "%s: NVFP4 output needs C %% 16 == 0", what);
   OUDJAT_REQUIRE(C <= 8192, OUDJAT_ERR_TOO_LARGE, "%s: C=%lld > 8192", what, (long long)C);
-  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg);
+  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg / row_parts(C));
   hipStream_t st = as_stream(stream);
   const int64_t pf_lines = pf_bytes / 128;  // whole lines; a partial last line is left to the reader
   const uint32_t* p = static_cast<const uint32_t*>(pf);
   auto go = [&](auto pf_c) {
-    constexpr bool P = decltype(pf_c)::value;
-#define OUDJAT_LN(CHV) \
-  layernorm_kernel<CHV, P><<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os, xh_ts, p, pf_lines)
-    if (C <= 512) OUDJAT_LN(1);
-    else if (C <= 1024) OUDJAT_LN(2);
-    else if (C <= 2048) OUDJAT_LN(4);
-    else if (C <= 4096) OUDJAT_LN(8);
-    else OUDJAT_LN(16);
-#undef OUDJAT_LN
+    row_dispatch(C, [&](auto ch, auto nwr) {
+      layernorm_kernel<decltype(ch)::value, decltype(nwr)::value, decltype(pf_c)::value>
+          <<<grid, kNormThreads, 0, st>>>(x, rows, (int)C, xs, w, b, eps, out, os, xh_ts, p, pf_lines);
+    });
   };
   if (pf_lines > 0) go(std::true_type{});
   else go(std::false_type{});
@@ -471,17 +554,12 @@ extern "C" int oudjat_gather_rows_ln(const uint16_t* x, int64_t stride_b, int64_
   OUDJAT_REQUIRE(!tensor_scale || C % 16 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE, "%s: NVFP4 output needs C %% 16 == 0",
                  what);
   OUDJAT_REQUIRE(C <= 8192, OUDJAT_ERR_TOO_LARGE, "%s: C=%lld > 8192", what, (long long)C);
-  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg);
+  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg / row_parts(C));
   hipStream_t st = as_stream(stream);
-#define OUDJAT_GATHER_LN(CHV)                                                                                     \
-  gather_ln_kernel<CHV><<<grid, kNormThreads, 0, st>>>(x, stride_b, stride_n, batch_idx, token_idx, rows, (int)C, w, \
-                                                       b, eps, x_out, ln_out, tensor_scale)
-  if (C <= 512) OUDJAT_GATHER_LN(1);
-  else if (C <= 1024) OUDJAT_GATHER_LN(2);
-  else if (C <= 2048) OUDJAT_GATHER_LN(4);
-  else if (C <= 4096) OUDJAT_GATHER_LN(8);
-  else OUDJAT_GATHER_LN(16);
-#undef OUDJAT_GATHER_LN
+  row_dispatch(C, [&](auto ch, auto nwr) {
+    gather_ln_kernel<decltype(ch)::value, decltype(nwr)::value><<<grid, kNormThreads, 0, st>>>(
+        x, stride_b, stride_n, batch_idx, token_idx, rows, (int)C, w, b, eps, x_out, ln_out, tensor_scale);
+  });
   return check_launch(what);
 }
 
@@ -563,18 +641,13 @@ static int packed_residual_ln_launch(const uint16_t* x_act, const uint16_t* x_at
                  OUDJAT_ERR_UNSUPPORTED_LAYOUT, "%s: 16-byte aligned rows, C %% 8 == 0", what);
   OUDJAT_REQUIRE(!xh_ts || C % 16 == 0, OUDJAT_ERR_UNSUPPORTED_SHAPE, "%s: NVFP4 output needs C %% 16 == 0", what);
   OUDJAT_REQUIRE(C <= 8192, OUDJAT_ERR_TOO_LARGE, "%s: C=%lld > 8192", what, (long long)C);
-  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg);
+  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg / row_parts(C));
   hipStream_t st = as_stream(stream);
-#define OUDJAT_PRLN(CHV)                                                                                        \
-  packed_residual_ln_kernel<CHV><<<grid, kNormThreads, 0, st>>>(x_act, x_attn, mlp, rows, (int)C, batch_idx,     \
-                                                                token_idx, bos, bos_stride_b, bos_stride_n, x_new, \
-                                                                ln_w, ln_b, eps, ln_out, xh_ts)
-  if (C <= 512) OUDJAT_PRLN(1);
-  else if (C <= 1024) OUDJAT_PRLN(2);
-  else if (C <= 2048) OUDJAT_PRLN(4);
-  else if (C <= 4096) OUDJAT_PRLN(8);
-  else OUDJAT_PRLN(16);
-#undef OUDJAT_PRLN
+  row_dispatch(C, [&](auto ch, auto nwr) {
+    packed_residual_ln_kernel<decltype(ch)::value, decltype(nwr)::value><<<grid, kNormThreads, 0, st>>>(
+        x_act, x_attn, mlp, rows, (int)C, batch_idx, token_idx, bos, bos_stride_b, bos_stride_n, x_new, ln_w, ln_b,
+        eps, ln_out, xh_ts);
+  });
   return check_launch(what);
 }
 
@@ -621,18 +694,12 @@ extern "C" int oudjat_splitk_ls_packed_residual(const float* partials, int64_t s
                  OUDJAT_ERR_UNSUPPORTED_LAYOUT, "splitk_ls_packed_residual: 16-byte aligned rows, C %% 8 == 0");
   OUDJAT_REQUIRE(C <= 8192 && slices < 65536, OUDJAT_ERR_TOO_LARGE, "splitk_ls_packed_residual: C=%lld > 8192",
                  (long long)C);
-  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg);
+  const unsigned grid = (unsigned)cdiv(rows, kNormRowsPerWg / row_parts(C));
   hipStream_t st = as_stream(stream);
-#define OUDJAT_SKRL(CHV)                                                                                        \
-  splitk_ls_residual_ln_kernel<CHV><<<grid, kNormThreads, 0, st>>>(partials, (int)slices, fc_bias, ls_gamma,      \
-                                                                   acc_scale, x_act, x_attn, rows, (int)C,        \
-                                                                   batch_idx, token_idx, bos, bos_stride_b,       \
-                                                                   bos_stride_n, x_new, ln_w, ln_b, eps, ln_out)
-  if (C <= 512) OUDJAT_SKRL(1);
-  else if (C <= 1024) OUDJAT_SKRL(2);
-  else if (C <= 2048) OUDJAT_SKRL(4);
-  else if (C <= 4096) OUDJAT_SKRL(8);
-  else OUDJAT_SKRL(16);
-#undef OUDJAT_SKRL
+  row_dispatch(C, [&](auto ch, auto nwr) {
+    splitk_ls_residual_ln_kernel<decltype(ch)::value, decltype(nwr)::value><<<grid, kNormThreads, 0, st>>>(
+        partials, (int)slices, fc_bias, ls_gamma, acc_scale, x_act, x_attn, rows, (int)C, batch_idx, token_idx, bos,
+        bos_stride_b, bos_stride_n, x_new, ln_w, ln_b, eps, ln_out);
+  });
   return check_launch("splitk_ls_packed_residual");
 }

@@ -198,9 +198,12 @@ def test_linear_without_workspace_does_not_split(dev):
     _check_gemm(dev, out, x, w, b, "unsplit")
 
 
-@pytest.mark.parametrize("rows,C", [(4176, 1024), (103, 384), (1656, 4096), (7, 8192)])
+@pytest.mark.parametrize("rows,C", [(4176, 1024), (103, 384), (1656, 4096), (7, 8192), (5, 2048), (3, 1536),
+                                    (9, 3072), (6, 1032)])
 def test_layer_norm(dev, rows, C):
-    """|got - oracle| <= ulp(oracle) + 64 u rstd |w| max|x_row| (fp32 statistics vs fp64)."""
+    """|got - oracle| <= ulp(oracle) + 64 u rstd |w| max|x_row| (fp32 statistics vs fp64). Rows wider than
+    1024 run on 2 or 4 waves each (C = 1536, 2048: two; 3072, 4096, 8192: four; 1032 does not split
+    evenly and stays on one), with row counts that leave rows past the end in the last workgroup."""
     x = (_rand((rows, C), 22).float() * 3 + 1).to(torch.bfloat16)
     w, b = _rand((C,), 23), _rand((C,), 24)
     got = K.layer_norm(x.to(dev), w.to(dev), b.to(dev), 1e-5).cpu().double()

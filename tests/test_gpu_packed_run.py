@@ -162,7 +162,8 @@ def test_packed_run_in_place(dev):
     assert_bits_equal(out_a, xb.cpu(), "x_out")
 
 
-@pytest.mark.parametrize("B,N,C,M", [(16, 261, 1024, 4176), (2, 40, 384, 30), (1, 9, 8, 3), (3, 20, 1536, 17)])
+@pytest.mark.parametrize("B,N,C,M", [(16, 261, 1024, 4176), (2, 40, 384, 30), (1, 9, 8, 3), (3, 20, 1536, 17),
+                                     (2, 30, 2048, 5), (4, 414, 4096, 1656), (2, 9, 4096, 7), (1, 9, 1032, 5)])
 def test_packed_residual_ln_equals_unfused(dev, B, N, C, M):
     """The residual step fused with the next block's LayerNorm equals packed_residual_persist followed by
     layer_norm, bit for bit (x_new, blocks_out_sum rows and the LayerNorm output)."""
