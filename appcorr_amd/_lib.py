@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be loaded before the HIP library, see module docstring
 
 LIB_PATH = Path(__file__).resolve().parent / "liboudjat_hip.so"
-ABI_VERSION = 16
+ABI_VERSION = 17
 
 OK = 0
 STATUS_NAMES = {
@@ -110,6 +110,8 @@ SIGNATURES: dict[str, list] = {
     "oudjat_sparse_query_attention_ws": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32,
                                          _p, _i64, _p, _i64, _p],
     "oudjat_sparse_query_attention_workspace_elems": [_i64, _i64, _i64, _i64, _i64],
+    "oudjat_sparse_query_attention_fp8": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32,
+                                          _p, _p, _i64, _p],
     "oudjat_sparse_query_attention_lse": [_p, _i64, _i64, _i64, _i64, _i64, _p, _i64, _i64, _i64, _i64, _i64, _f32,
                                           _p, _i64, _p, _p],
     "oudjat_patch_attention_prob_workspace_elems": [_i64, _i64, _i64, _i32],

@@ -27,6 +27,7 @@
 #include <type_traits>
 
 #include "common.hpp"
+#include "fp8.hpp"
 
 namespace oudjat {
 
@@ -96,11 +97,15 @@ __device__ __forceinline__ float prob_row_sum(const bf16x8_t (&pf)[4]) {
 // LSE: also write each query's row log-sum-exp (natural log) of the scaled scores to lse[b][h][t],
 // from an fp32 sum of the unrounded probabilities kept beside the bf16-weight sum that normalises
 // the output (the output is the same bit for bit either way).
-template <int DH, int MINW, bool DOUBLE_SET, bool LSE = false>
+// F8OUT: the output row is written instead as the e4m3fn codes of its bf16 values times *f8s, the
+// consuming FP8 linear's activation quantizer (fp8_act_code) applied in the store: out8, one byte per
+// element, row stride ors.
+template <int DH, int MINW, bool DOUBLE_SET, bool LSE = false, bool F8OUT = false>
 __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void sq_attention_kernel(
     const uint16_t* __restrict__ q, int64_t qrs, int T, const uint16_t* __restrict__ kv, int64_t kvb, int64_t kvn,
     int64_t kvkv, int64_t kvh, int N, float scale_log2, uint16_t* __restrict__ out, int64_t ors,
-    int waves_per_wg, float* __restrict__ lse) {
+    int waves_per_wg, float* __restrict__ lse, uint8_t* __restrict__ out8 = nullptr,
+    const float* __restrict__ f8s = nullptr) {
   constexpr int CPR = DH / 8;                 // 16-byte chunks per K / V row
   constexpr int KROWB = DH * 2;               // bytes per K / V row in LDS
   constexpr int KSTAGE = kKeyTile * KROWB;
@@ -338,7 +343,20 @@ __global__ __launch_bounds__((DH == 64 ? kMaxWaves64 : kMaxWaves128) * 64) void 
   // O^T[d][q]: lane l, register v of block db -> d = db*32 + 8(v/4) + 4g + v%4 (4 consecutive d per
   // group of 4 registers -> one 8-byte store), q = q0 + l32.
   const int qr = q0 + l32;
-  if (active && qr < T) {
+  if (F8OUT && active && qr < T) {
+    const float inv = 1.0f / l_i;
+    const float s8 = *f8s;
+    uint8_t* orow = out8 + ((int64_t)b * T + qr) * ors + (int64_t)h * DH;
+#pragma unroll
+    for (int d = 0; d < OB; ++d)
+#pragma unroll
+      for (int r4 = 0; r4 < 4; ++r4) {
+        uint32_t w = 0;
+#pragma unroll
+        for (int e = 0; e < 4; ++e) w |= fp8_act_code(round_bf16(o[d][4 * r4 + e] * inv), s8) << (8 * e);
+        *reinterpret_cast<uint32_t*>(orow + d * 32 + 8 * r4 + 4 * g) = w;
+      }
+  } else if (active && qr < T) {
     const float inv = 1.0f / l_i;
     uint16_t* orow = out + ((int64_t)b * T + qr) * ors + (int64_t)h * DH;
 #pragma unroll
@@ -1139,6 +1157,34 @@ extern "C" int oudjat_sparse_query_attention_lse(const uint16_t* q, int64_t qrs,
                  "sparse_query_attention: null lse");
   return sparse_query_attention_impl(q, qrs, B, T, H, Dh, kv, kvb, kvn, kvkv, kvh, N, scale, out, ors, nullptr, 0,
                                      lse, stream);
+}
+
+extern "C" int oudjat_sparse_query_attention_fp8(const uint16_t* q, int64_t qrs, int64_t B, int64_t T, int64_t H,
+                                                 int64_t Dh, const uint16_t* kv, int64_t kvb, int64_t kvn,
+                                                 int64_t kvkv, int64_t kvh, int64_t N, float scale,
+                                                 const float* act_inv_scale, uint8_t* out, int64_t ors,
+                                                 oudjat_stream_t stream) {
+  OUDJAT_REQUIRE(B >= 0 && T >= 0 && H >= 0 && N >= 0, OUDJAT_ERR_INVALID_ARGUMENT,
+                 "sparse_query_attention_fp8: negative size");
+  if (B == 0 || T == 0 || H == 0) return OUDJAT_OK;
+  OUDJAT_REQUIRE(q && kv && out && act_inv_scale, OUDJAT_ERR_INVALID_ARGUMENT,
+                 "sparse_query_attention_fp8: null pointer");
+  OUDJAT_REQUIRE(N > 0, OUDJAT_ERR_UNSUPPORTED_SHAPE, "sparse_query_attention_fp8: no keys");
+  OUDJAT_REQUIRE(Dh == 128, OUDJAT_ERR_UNSUPPORTED_SHAPE, "sparse_query_attention_fp8: Dh=%lld (128 only)",
+                 (long long)Dh);
+  OUDJAT_REQUIRE(qrs % 8 == 0 && kvb % 8 == 0 && kvn % 8 == 0 && kvkv % 8 == 0 && kvh % 8 == 0 && ors % 4 == 0 &&
+                     aligned(q, 16) && aligned(kv, 16) && aligned(out, 4) && aligned(act_inv_scale, 4),
+                 OUDJAT_ERR_UNSUPPORTED_LAYOUT, "sparse_query_attention_fp8: 16-byte aligned q and kv rows, "
+                 "4-byte aligned output rows required");
+  OUDJAT_REQUIRE(B <= 65535 && H <= 65535 && N < ((int64_t)1 << 30) && T < ((int64_t)1 << 30), OUDJAT_ERR_TOO_LARGE,
+                 "sparse_query_attention_fp8: too large");
+  const AttnShape s = attn_shape(B, T, H, Dh, N, true);
+  dim3 grid((unsigned)s.n_wg, (unsigned)H, (unsigned)B);
+  const size_t lds = 2 * 2 * (size_t)kKeyTile * Dh * 2;
+  sq_attention_kernel<128, kMinWaves, false, false, true><<<grid, s.w * 64, lds, as_stream(stream)>>>(
+      q, qrs, (int)T, kv, kvb, kvn, kvkv, kvh, (int)N, scale * 1.4426950408889634f, nullptr, ors, s.w, nullptr, out,
+      act_inv_scale);
+  return check_launch("sparse_query_attention_fp8");
 }
 
 extern "C" int64_t oudjat_sparse_query_attention_workspace_elems(int64_t B, int64_t T, int64_t H, int64_t Dh,

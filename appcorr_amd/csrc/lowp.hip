@@ -11,22 +11,13 @@
 //     file's scale_bias (out = raw * s + b, fp32, one rounding) or, for the SwiGLU pair, the fused
 //     silu(raw1 * s1 + b1) * (raw2 * s2 + b2) epilogue (token_update.py:571-669);
 //   FP8 (scales inside the GEMM): bf16(acc * (sa * sb) + b) by the GEMM's accumulator scale.
+#include "fp8.hpp"
 #include "nvfp4.hpp"
 
 namespace oudjat {
 namespace {
 
 constexpr int kLpThreads = 256;
-
-// e4m3fn code of |v| <= 448 with round-to-nearest-even (subnormals included), OCP 8-bit definition.
-__device__ __forceinline__ uint32_t e4m3_code_abs(float a) {
-  const uint32_t u = __float_as_uint(a);
-  const int e = (int)((u >> 23) & 0xff) - 127;
-  if (e < -6) return (uint32_t)__builtin_rintf(a * 512.0f);  // m * 2^-9, m in [0, 8]
-  const uint32_t r = u + 0x7ffffu + ((u >> 20) & 1u);      // RNE from 23 to 3 mantissa bits
-  const uint32_t code = ((uint32_t)((int)((r >> 23) & 0xff) - 127 + 7) << 3) | ((r >> 20) & 7u);
-  return code > 0x7eu ? 0x7eu : code;
-}
 
 __device__ __forceinline__ float e4m3_value_abs(uint32_t c) {
   const uint32_t e = (c >> 3) & 0xf, m = c & 7u;
@@ -79,9 +70,13 @@ __global__ void __launch_bounds__(kLpThreads) fp8_quantize_kernel(const uint16_t
   uint32_t code[8];
 #pragma unroll
   for (int e = 0; e < 8; ++e) {
-    const float v = mode == 0 ? f[e] * s : round_bf16((float)((double)f[e] / (double)s));
-    const uint32_t sign = (__float_as_uint(v) >> 31) << 7;
-    code[e] = sign | (v != v ? 0x7fu : e4m3_code_abs(fminf(fabsf(v), 448.0f)));
+    if (mode == 0) {
+      code[e] = fp8_act_code(f[e], s);
+    } else {
+      const float v = round_bf16((float)((double)f[e] / (double)s));
+      const uint32_t sign = (__float_as_uint(v) >> 31) << 7;
+      code[e] = sign | (v != v ? 0x7fu : e4m3_code_abs(fminf(fabsf(v), 448.0f)));
+    }
   }
   uint2 w;
   w.x = code[0] | (code[1] << 8) | (code[2] << 16) | (code[3] << 24);

@@ -226,10 +226,11 @@ class SelfAttention(nn.Module):
         return out, cache_feature
 
     def _qkv_attention(self, xn: Tensor, rope, kv: Tensor, qs: PackedQueryState, xn_is_xhat: bool = False,
-                       lse: Tensor | None = None):
+                       lse: Tensor | None = None, fp8_out: Tensor | None = None):
         """q, K/V rows and the attention output of the packed rows from their norm1 output xn -- for a
         frozen NVFP4 qkv linear, xn may already be its NVFP4 operand x_hat (xn_is_xhat: the producer wrote
-        it). lse (fp32 [B, H, T]) receives the attention's row log-sum-exp when given."""
+        it). lse (fp32 [B, H, T]) receives the attention's row log-sum-exp when given. fp8_out (the
+        frozen FP8 proj's activation inverse scale): the output is instead its e4m3fn codes (uint8)."""
         M, C = xn.shape
         H, D = self.num_heads, self.head_dim
         B = kv.shape[0]
@@ -274,6 +275,8 @@ class SelfAttention(nn.Module):
         if qkv is not None:
             K.qkv_rope_kv_scatter(qkv.view(M, 3, H, D), rope, qs.active_patch_mask, qs.active_rope_idx,
                                   qs.active_batch_idx, qs.active_token_idx, kv, q)
+        if fp8_out is not None:
+            return q, K.sparse_query_attention_fp8(q, kv, T, self.scale, fp8_out)
         attn = K.sparse_query_attention(q, kv, T, self.scale, lse=lse)
         return q, attn
 
@@ -717,10 +720,17 @@ class SelfAttentionBlock(nn.Module):
                 ts1 = _fp4_scale(self.attn.qkv)
                 xn = K.layer_norm(x_act, self.norm1.weight, self.norm1.bias, self.norm1.eps, nvfp4_scale=ts1)
                 xn_is_xhat = ts1 is not None
-            _, attn = self.attn._qkv_attention(xn, rope, kv, qs, xn_is_xhat)           # attention.py:415-523
-            g1 = self._gamma(self.ls1, x_act)
             proj = self.attn.proj
-            if LP.low_precision_state(proj) == "fp4":                                    # proj_precision "fp4"
+            # A native FP8 proj takes the attention's output as e4m3 codes written by the attention itself
+            # (its activation quantizer in the attention's store, one launch fewer).
+            fp8_codes = (LP.low_precision_state(proj) == "fp8" and proj.native and self.attn.head_dim == 128)
+            _, attn = self.attn._qkv_attention(xn, rope, kv, qs, xn_is_xhat,           # attention.py:415-523
+                                               fp8_out=proj.act_inv_f32 if fp8_codes else None)
+            g1 = self._gamma(self.ls1, x_act)
+            if fp8_codes:
+                x_attn = proj.linear_codes(attn, proj.bias, "proj", epilogue=_lib.EPI_BIAS_LS_RESID, gamma=g1,
+                                           resid=x_act)
+            elif LP.low_precision_state(proj) == "fp4":                                  # proj_precision "fp4"
                 x_attn = _fp4_linear(proj, attn, "proj", epilogue=_lib.EPI_BIAS_LS_RESID, gamma=g1, resid=x_act)
             else:
                 x_attn = _linear_route(proj, attn, "proj", epilogue=_lib.EPI_BIAS_LS_RESID,  # attention.py:532 +

@@ -188,6 +188,16 @@ class FastFP8Linear(_LowPrecisionLinear):
         """The activation's e4m3fn codes, uint8 (the operand of the native FP8 GEMM)."""
         return K.fp8_quantize(x2d, self._act_inv_f32, K.FP8_ACTIVATION)
 
+    @property
+    def act_inv_f32(self) -> torch.Tensor:
+        """The frozen activation quantizer's operand: the bf16 inverse scale as an fp32 device scalar."""
+        return self._act_inv_f32
+
+    def linear_codes(self, x8: torch.Tensor, bias: torch.Tensor | None, site: str, **kw) -> torch.Tensor:
+        """`linear` of an activation already given as its e4m3fn codes (quantize_codes' output, written by
+        the producer itself); native FP8 GEMM only."""
+        return K.linear_fp8(x8, self.weight_q, bias, acc_scale=self.acc_scale_f, site=site, **kw)
+
     def linear(self, x: torch.Tensor, bias: torch.Tensor | None, site: str, **kw) -> torch.Tensor:
         """The frozen linear's output: bf16(acc * act_scale * weight_scale + bias) with the epilogue of
         `kw` (fp8_fast_linear.py:174-196)."""

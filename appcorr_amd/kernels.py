@@ -943,6 +943,25 @@ def sparse_query_attention(q: torch.Tensor, kv_cache: torch.Tensor, T: int, scal
     return out
 
 
+def sparse_query_attention_fp8(q: torch.Tensor, kv_cache: torch.Tensor, T: int, scale: float,
+                               act_inv_scale: torch.Tensor) -> torch.Tensor:
+    """sparse_query_attention's output as the e4m3fn codes (uint8 [B*T, H*Dh]) of FastFP8Linear's
+    activation quantizer with the device scalar act_inv_scale (fp32, the bf16 inverse scale), in the
+    attention's own store: fp8_quantize(sparse_query_attention(...), act_inv_scale) bit for bit. Dh = 128."""
+    _require_cuda(q, kv_cache, act_inv_scale)
+    _require(q.dtype == kv_cache.dtype == torch.bfloat16, "attention: bf16 only")
+    B, N, two, H, Dh = kv_cache.shape
+    _require(two == 2 and kv_cache.stride(4) == 1 and kv_cache.stride(3) == Dh, "attention: kv heads must be packed")
+    _require(q.dim() == 3 and q.shape[1:] == (H, Dh) and q.shape[0] == B * T and q.stride(2) == 1
+             and q.stride(1) == Dh, "attention: q must be [B*T, H, Dh] with packed heads")
+    _require(act_inv_scale.dtype == torch.float32 and act_inv_scale.numel() == 1, "attention: fp32 scalar scale")
+    out = torch.empty((B * T, H * Dh), device=q.device, dtype=torch.uint8)
+    _launch("attention", q, "oudjat_sparse_query_attention_fp8", _ptr(q), q.stride(0), B, T, H, Dh, _ptr(kv_cache),
+            kv_cache.stride(0), kv_cache.stride(1), kv_cache.stride(2), kv_cache.stride(3), N, float(scale),
+            _ptr(act_inv_scale), _ptr(out), out.stride(0), _stream(q))
+    return out
+
+
 # ------------------------------------------------------------------------------------------------
 # Server scores of the approximate pass (attention.py:246-273)
 # ------------------------------------------------------------------------------------------------

@@ -419,6 +419,19 @@ int oudjat_sparse_query_attention_lse(const uint16_t* q, int64_t q_row_stride, i
                                       int64_t N, float scale, uint16_t* out, int64_t out_row_stride,
                                       float* lse, oudjat_stream_t stream);
 
+/* Row 10 + the FP8 route's attn.proj input (attention.py:497-532 with attn.proj a frozen FastFP8Linear,
+ * fp8_fast_linear.py:183-196; fp4_fast_linear.py:309-311 routes proj to FP8 in the NVFP4 mode):
+ * oudjat_sparse_query_attention whose output is written as the e4m3fn codes that FastFP8Linear's
+ * activation quantizer gives on it (oudjat_fp8_quantize mode 0 with act_inv_scale, the bf16 inverse
+ * activation scale as fp32, applied to the bf16 attention output), one byte per element: the operand of
+ * oudjat_linear_fp8, in one launch. Dh == 128 only (OUDJAT_ERR_UNSUPPORTED_SHAPE otherwise);
+ * out_row_stride in bytes, 4-byte aligned rows; other arguments as oudjat_sparse_query_attention. */
+int oudjat_sparse_query_attention_fp8(const uint16_t* q, int64_t q_row_stride, int64_t B, int64_t T,
+                                      int64_t H, int64_t Dh, const uint16_t* kv, int64_t kv_stride_b,
+                                      int64_t kv_stride_n, int64_t kv_stride_kv, int64_t kv_stride_h,
+                                      int64_t N, float scale, const float* act_inv_scale, uint8_t* out,
+                                      int64_t out_row_stride, oudjat_stream_t stream);
+
 /* fp32 elements of workspace oudjat_sparse_query_attention_ws uses for this shape (0: it never
  * splits the keys of this shape). */
 int64_t oudjat_sparse_query_attention_workspace_elems(int64_t B, int64_t T, int64_t H, int64_t Dh,

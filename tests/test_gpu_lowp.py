@@ -170,6 +170,22 @@ def test_fp8_codes_are_the_operand_values(dev):
         assert bool((signs | torch.isnan(vals.float())).all()), mode
 
 
+@pytest.mark.parametrize("B,T,H,N", [(4, 414, 32, 4101), (2, 50, 4, 300), (1, 7, 2, 70)])
+def test_attention_fp8_codes_equal_quantize_after(dev, B, T, H, N):
+    """The attention writing the FP8 proj's activation codes itself equals the bf16 attention followed
+    by fp8_quantize (FastFP8Linear's activation mode), byte for byte; Dh = 128 (the ViT-7B heads)."""
+    g = torch.Generator().manual_seed(B * T + N)
+    D = 128
+    q = (torch.randn(B * T, H, D, generator=g) * 2).to(torch.bfloat16).to(dev)
+    kv = (torch.randn(B, N, 2, H, D, generator=g) * 2).to(torch.bfloat16).to(dev)
+    inv = torch.tensor([float(round_bf16(np.float32(448.0) / np.float32(3.0)))], device=dev)
+    want = K.fp8_quantize(K.sparse_query_attention(q, kv, T, D ** -0.5), inv, K.FP8_ACTIVATION)
+    got = K.sparse_query_attention_fp8(q, kv, T, D ** -0.5, inv)
+    torch.cuda.synchronize()
+    assert got.dtype == torch.uint8 and got.shape == want.shape
+    assert torch.equal(got, want)
+
+
 @pytest.mark.parametrize("M,N,Kd,epi", [
     (1656, 12288, 4096, _lib.EPI_BIAS),          # the ViT-7B qkv shape (plain epilogue)
     (1656, 4096, 4096, _lib.EPI_BIAS_LS_RESID),  # proj

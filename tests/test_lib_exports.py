@@ -136,6 +136,18 @@ def test_lse_entry_points_reject_bad_arguments():
               NULL)
 
 
+def test_attention_fp8_rejects_bad_arguments():
+    # Dh = 64 has no FP8-output kernel; a null scale; a misaligned output row stride
+    _expect("OUDJAT_ERR_UNSUPPORTED_SHAPE", "oudjat_sparse_query_attention_fp8", ctypes.c_void_p(16), 64, 1, 4, 1, 64,
+            ctypes.c_void_p(16), 1024, 128, 64, 64, 8, 0.1, ctypes.c_void_p(16), ctypes.c_void_p(16), 64, NULL)
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_sparse_query_attention_fp8", ctypes.c_void_p(16), 128, 1, 4, 1,
+            128, ctypes.c_void_p(16), 2048, 256, 128, 128, 8, 0.1, NULL, ctypes.c_void_p(16), 128, NULL)
+    _expect("OUDJAT_ERR_UNSUPPORTED_LAYOUT", "oudjat_sparse_query_attention_fp8", ctypes.c_void_p(16), 128, 1, 4, 1,
+            128, ctypes.c_void_p(16), 2048, 256, 128, 128, 8, 0.1, ctypes.c_void_p(16), ctypes.c_void_p(16), 130, NULL)
+    _lib.call("oudjat_sparse_query_attention_fp8", NULL, 128, 0, 4, 1, 128, NULL, 0, 0, 0, 0, 8, 0.1, NULL, NULL,
+              128, NULL)
+
+
 def test_layernorm_prefetch_rejects_bad_regions():
     """The cache-warming region is checked before anything else (here with zero rows, so no GPU)."""
     _expect("OUDJAT_ERR_INVALID_ARGUMENT", "oudjat_layernorm_rows_prefetch", NULL, 0, 1024, 1024, NULL, NULL, 1e-5,
