@@ -1734,6 +1734,7 @@ static const GemmCfg kCfgs[] = {
     OUDJAT_GEMM_PP8_CFG(224, 256),  // 36
     OUDJAT_GEMM_PP8_CFG(192, 256),  // 37
     OUDJAT_GEMM_PP8_CFG(128, 256),  // 38
+    OUDJAT_GEMM_PP_CFG(224, 384),  // 39: ping-pong 224 x 384 (one round where 256-wide tiles need two)
 };
 static constexpr int kNumCfgs = sizeof(kCfgs) / sizeof(kCfgs[0]);
 
@@ -1806,6 +1807,11 @@ static int choose_cfg(int64_t M, int64_t N, int64_t K, bool aligned_io) {
   if (N % 256 == 0 && tiles288 > 512) return 27;
   if (N % 256 == 0 && tiles224 >= 224 && tiles224 <= 256 && tiles288 < tiles224) return 30;
   if (N % 256 == 0 && tiles288 >= 192 && tiles288 <= 256) return 27;
+  // One round of 224 x 384 ping-pong tiles where the 256-wide ones need more than one (ViT-7B qkv,
+  // 1656 x 12288 x 4096: 256 tiles, 135.1 us, against 170.4 for 432 tiles of 192 x 256 in two uneven
+  // rounds and 147.2 for hipBLASLt; 22 % fewer operand bytes per FLOP than 192 x 256).
+  const int64_t tiles384 = cdiv(M, 224) * (N / 384);
+  if (N % 384 == 0 && tiles384 >= 224 && tiles384 <= 256) return 39;
   // Two rounds of 288-, 224- or 192-row ping-pong tiles 256 wide, whichever fills them most (ViT-L
   // keep 50 %, M = 8272: fc1 4096 wide, 464 tiles of 288 x 256, 62.7 us; qkv 3072 wide, 444 tiles of
   // 224 x 256, 53.7 us, where 128 x 128 tiles took 85.0 and 73.3 us; ViT-7B qkv, 1656 x 12288 x 4096:
@@ -1904,6 +1910,9 @@ static int choose_splitk(int64_t M, int64_t N, int64_t K, int epi, int* S_out) {
 // 288 x 192 (ping-pong) tiles when the plain choice would leave more CUs idle in its single round.
 static int choose_qkv_cfg(int64_t M, int64_t N, int64_t K, int64_t Dh) {
   if (tiny_grid(M, N) && 64 % Dh == 0 && N % 64 == 0) return 33;  // ViT-S at B = 1: 10.5 -> 8.2 us
+  // One round of whole-head 224 x 384 tiles (ViT-7B: 179.6 -> 140.3 us per fused QKV in the pass).
+  const int64_t t384 = cdiv(M, 224) * (N / 384);
+  if (N % 384 == 0 && 384 % Dh == 0 && t384 >= 224 && t384 <= 256) return 39;
   int ci = choose_cfg(M, N, K, true);
   const int64_t tiles288n = cdiv(M, 288) * (N / 192);
   if (N % 192 == 0 && tiles288n >= 192 && tiles288n <= 256 &&

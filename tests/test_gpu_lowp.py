@@ -259,7 +259,7 @@ def test_swiglu_block_through_the_controller(dev, precision):
 # QKV on 192 x 256 ping-pong tiles (whole 128-wide heads), proj on 16-row-block 128 x 256 tiles, w1 / w2
 # on 224 x 256 ping-pong tiles and w3 in two K slices of 288 x 256 ping-pong tiles (split K).
 _VIT7B_TILES = {
-    (1656, 12288, 4096, 5): "oudjat::gemm_bf16_pp_kernel<192, 256, 5>",  # 5: the fused QKV kernel
+    (1656, 12288, 4096, 5): "oudjat::gemm_bf16_pp_kernel<224, 384, 5>",  # 5: the fused QKV kernel
     (1656, 4096, 4096, _lib.EPI_BIAS_LS_RESID): "oudjat::gemm_bf16_r16_kernel<128, 256, 2, 4, 1, 64, 3, false, 2>",
     (1656, 8192, 4096, _lib.EPI_BIAS_SILU_MUL): "oudjat::gemm_bf16_pp_kernel<224, 256, 4>",
     (1656, 8192, 4096, _lib.EPI_BIAS): "oudjat::gemm_bf16_pp_kernel<224, 256, 0>",
