@@ -715,8 +715,8 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     // ---- Light wave (<= 16 queries left, e.g. the 5 of T = 261 after 8 full waves): 16 queries on
     // v_mfma_f32_16x16x32_bf16, half the MFMA and softmax work of a full wave. 8 full waves and one
     // light wave would put three waves on one SIMD, which every other SIMD then waits for at each
-    // tile's barrier; so, split (light_split), the light wave's tiles are shared by kLightParts
-    // waves, one per SIMD, part p taking the tiles of stage p (t % NST == p). Each part keeps its
+    // tile's barrier; so, split (light_split), the light wave's keys are shared by kLightParts
+    // waves, one per SIMD, part p taking a quarter of every tile (below). Each part keeps its
     // own running max, sum and output; parts 1.. park them in LDS after the loop and part 0 merges
     // them (rescaled to the largest reference max, summed in part order) and stores the rows.
     // Layout: lane l, 16-lane group G = l / 16. S^T = K . Q^T per 16-key block kb (A = K rows
@@ -824,9 +824,71 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
         }
       }
     };
-    Scores16 sa, sb;
-    static_assert(kLightParts == NST, "one light part per stage");
-    pipeline(sa, sb, scores, finish, lpart >= 0 ? 1 << lpart : (1 << NST) - 1, active);
+    using AllStages = std::integral_constant<int, (1 << NST) - 1>;
+    if (lpart >= 0) {
+      // Split light wave: part p takes keys 16 p .. 16 p + 15 of every tile, so every SIMD gets the
+      // same share of the light work at every step. S^T of the slice is one 16-key block (A = K rows
+      // 16 p + l % 16): sq.s[v] = S^T[key 16 p + 4 G + v][query l % 16]. O^T += V^T . P^T on
+      // v_mfma_f32_16x16x16_bf16 per 16-dim block db: B = P^T in that same layout (keys 16 p + 4 G +
+      // {0..3} of query l % 16), A = V^T from one transpose read (dim 16 db + l % 16 of those keys).
+      static_assert(kLightParts * 16 == kKeyTile, "one 16-key slice per light part");
+      const int pofs = lpart * 16 * 128;
+      int kq[2], vq[4];
+#pragma unroll
+      for (int ks = 0; ks < 2; ++ks) kq[ks] = koff[ks] + pofs;
+#pragma unroll
+      for (int db = 0; db < 4; ++db) vq[db] = voff[db][0] + pofs;
+      struct ScoresQ {
+        f32x4_t s;
+      };
+      auto scores_q = [&](ScoresQ& sc, const unsigned char* st) __attribute__((always_inline)) {
+        const bf16x8_t k0 = as_bf16x8(*reinterpret_cast<const uint4*>(st + kq[0]));
+        const bf16x8_t k1 = as_bf16x8(*reinterpret_cast<const uint4*>(st + kq[1]));
+        const f32x4_t zero = {};
+        sc.s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k0, qf[0], zero, 0, 0, 0);
+        sc.s = __builtin_amdgcn_mfma_f32_16x16x32_bf16(k1, qf[1], sc.s, 0, 0, 0);
+      };
+      auto finish_q = [&](ScoresQ& sc, const unsigned char* st, int t, auto mask_c) __attribute__((always_inline)) {
+        f32x4_t& sv = sc.s;
+        const int key0 = (tb + t) * kKeyTile + 16 * lpart;  // first key of the slice
+        if (decltype(mask_c)::value && key0 + 16 > N) {
+          if (key0 >= N) return;  // no key in the slice: the part's running state stays as it is
+#pragma unroll
+          for (int v = 0; v < 4; ++v)
+            if (key0 + 4 * G + v >= N) sv[v] = -INFINITY;
+        }
+        const float mx = xor32_max(xor16_max(fmaxf(fmaxf(sv[0], sv[1]), fmaxf(sv[2], sv[3]))));
+        const float m_new = softmax_ref_max(m_i, mx, scale_log2);
+        const float alpha = __builtin_amdgcn_exp2f((m_i - m_new) * scale_log2);
+        const float mc = m_new * scale_log2;
+#pragma unroll
+        for (int v = 0; v < 4; ++v) sv[v] = __builtin_amdgcn_exp2f(fmaf(sv[v], scale_log2, -mc));
+        typedef __bf16 bf16x4v_t __attribute__((ext_vector_type(4)));
+        const bf16x4v_t pb = __builtin_convertvector(sv, bf16x4v_t);
+        typedef __bf16 bf16x2v_t __attribute__((ext_vector_type(2)));
+        const bf16x2v_t ones = {(__bf16)1.0f, (__bf16)1.0f};
+        float r = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb, pb, 0, 1), ones, 0.0f, false);
+        r = __builtin_amdgcn_fdot2_f32_bf16(__builtin_shufflevector(pb, pb, 2, 3), ones, r, false);
+        l_i = l_i * alpha + xor32_sum(xor16_sum(r));
+        m_i = m_new;
+        if (__builtin_amdgcn_ballot_w64(alpha != 1.0f)) {
+#pragma unroll
+          for (int d = 0; d < 4; ++d) o[d] *= alpha;
+        }
+        const i16x4_t pbits = __builtin_bit_cast(i16x4_t, pb);
+#pragma unroll
+        for (int db = 0; db < 4; ++db) {
+          const i16x4_t vt = __builtin_amdgcn_ds_read_tr16_b64_v4i16(
+              (__attribute__((address_space(3))) i16x4_t*)(st + vq[db]));
+          o[db] = __builtin_amdgcn_mfma_f32_16x16x16bf16_1k(vt, pbits, o[db], 0, 0, 0);
+        }
+      };
+      ScoresQ qa, qb;
+      pipeline(qa, qb, scores_q, finish_q, AllStages{}, active);
+    } else {
+      Scores16 sa, sb;
+      pipeline(sa, sb, scores, finish, AllStages{}, active);
+    }
 
     if (merged) {
       // Every wave has passed its last tile's reads after the first barrier, so the stages are free.
@@ -855,7 +917,8 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
         float m = mp[0];
 #pragma unroll
         for (int p = 1; p < kLightParts; ++p) m = fmaxf(m, mp[p]);
-        // Part 0 holds tile 0, so m is finite; a part without tiles has m = -inf, l = 0, o = 0.
+        // Part 0 holds key 0 of the first tile, so m is finite; a part whose slices held no key has
+        // m = -inf, l = 0, o = 0.
         float a[kLightParts];
 #pragma unroll
         for (int p = 0; p < kLightParts; ++p) a[p] = __builtin_amdgcn_exp2f((mp[p] - m) * scale_log2);
