@@ -482,6 +482,24 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     else wait_vmcnt<6>();
   };
 
+  // Query fragments, loaded before the K/V prologue so that their latency overlaps the first tiles'
+  // (the prologue's vmcnt waits then cover them as older loads). Full wave (T - q0 > 16): query
+  // q0 + lane % 32, dims 16 ks + 8 (lane / 32) .. + 7; light wave: query q0 + lane % 16, dims
+  // 32 ks + 8 (lane / 16) .. + 7, ks < 2.
+  const bool full_wave = T - q0 > 16;
+  uint4 qraw[QK_STEPS];
+  {
+    const int qr = q0 + (full_wave ? l32 : (lane & 15));
+    const int dim0 = full_wave ? 8 * g : 8 * (lane >> 4);
+    const int kstride = full_wave ? 16 : 32;
+    const uint16_t* qrow = q + ((int64_t)b * T + qr) * qrs + (int64_t)h * DH + dim0;
+#pragma unroll
+    for (int ks = 0; ks < QK_STEPS; ++ks) {
+      qraw[ks] = make_uint4(0, 0, 0, 0);
+      if (qr < T && (full_wave || ks < 2)) qraw[ks] = *reinterpret_cast<const uint4*>(qrow + ks * kstride);
+    }
+  }
+
   // The prologue of the K/V pipeline is common to both wave kinds below.
   static_assert(NST == 4, "the unrolled loops below are written for four stages");
 #pragma unroll
@@ -534,18 +552,11 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     if (t + 3 < ntiles) step(I3{}, t + 3, sb, sa, BT{});
   };
 
-  if (T - q0 > 16) {
+  if (full_wave) {
     // ---- Full wave: 32 queries on v_mfma_f32_32x32x16_bf16 (layout in the file comment). ----
     bf16x8_t qf[QK_STEPS];
-    {
-      const int qr = q0 + l32;
 #pragma unroll
-      for (int ks = 0; ks < QK_STEPS; ++ks) {
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (qr < T) v = *reinterpret_cast<const uint4*>(q + ((int64_t)b * T + qr) * qrs + (int64_t)h * DH + ks * 16 + 8 * g);
-        qf[ks] = as_bf16x8(v);
-      }
-    }
+    for (int ks = 0; ks < QK_STEPS; ++ks) qf[ks] = as_bf16x8(qraw[ks]);
     f32x16_t o[OB];
 #pragma unroll
     for (int d = 0; d < OB; ++d)
@@ -728,15 +739,8 @@ __global__ __launch_bounds__(kDmaMaxWaves * 64) void sq_attention_dma_kernel(
     // consecutive keys).
     const int l16 = lane & 15, G = lane >> 4;
     bf16x8_t qf[2];
-    {
-      const int qr = q0 + l16;
 #pragma unroll
-      for (int ks = 0; ks < 2; ++ks) {
-        uint4 v = make_uint4(0, 0, 0, 0);
-        if (qr < T) v = *reinterpret_cast<const uint4*>(q + ((int64_t)b * T + qr) * qrs + (int64_t)h * DH + ks * 32 + 8 * G);
-        qf[ks] = as_bf16x8(v);
-      }
-    }
+    for (int ks = 0; ks < 2; ++ks) qf[ks] = as_bf16x8(qraw[ks]);
     f32x4_t o[4];
 #pragma unroll
     for (int d = 0; d < 4; ++d) o[d] = f32x4_t{0.0f, 0.0f, 0.0f, 0.0f};
