@@ -17,7 +17,7 @@ from pathlib import Path
 import torch  # noqa: F401  -- must be loaded before the HIP library, see module docstring
 
 LIB_PATH = Path(__file__).resolve().parent / "liboudjat_hip.so"
-ABI_VERSION = 17
+ABI_VERSION = 18
 
 OK = 0
 STATUS_NAMES = {
@@ -91,7 +91,10 @@ SIGNATURES: dict[str, list] = {
     "oudjat_layernorm_rows_prefetch": [_p, _i64, _i64, _i64, _p, _p, _f32, _p, _i64, _p, _i64, _p],
     "oudjat_linear_bf16": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i32, _p, _p, _i64, _p, _i64, _f32, _p, _i64,
                            _p],
+    "oudjat_linear_bf16_warm": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i32, _p, _p, _i64, _p, _i64, _f32, _p,
+                                _i64, _p, _i64, _p],
     "oudjat_linear_workspace_elems": [_i64, _i64, _i64, _i32],
+    "oudjat_linear_warm_slots": [_i64, _i64, _i64, _i32],
     "oudjat_linear_splitk_partial": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _p, _p],
     "oudjat_splitk_ls_packed_residual": [_p, _i64, _p, _p, _f32, _p, _p, _i64, _i64, _p, _p, _p, _i64, _i64, _p, _p,
                                          _p, _f32, _p, _p],
@@ -101,6 +104,8 @@ SIGNATURES: dict[str, list] = {
     "oudjat_fold_residual_rows": [_p, _i64, _i64, _p, _p, _p, _i64, _p, _p],
     "oudjat_linear_qkv_rope_kv": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p, _p,
                                   _i64, _i64, _p, _f32, _p],
+    "oudjat_linear_qkv_rope_kv_warm": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p, _p,
+                                       _p, _i64, _i64, _p, _f32, _p, _i64, _p],
     "oudjat_linear_swiglu_nvfp4": [_p, _i64, _i64, _i64, _p, _i64, _i64, _p, _i64, _f32, _p, _f32, _p, _p, _p, _i64,
                                    _p],
     "oudjat_linear_qkv_rope_kv_nvfp4": [_p, _i64, _i64, _i64, _p, _i64, _p, _i64, _i64, _p, _p, _i64, _p, _p, _p,
@@ -144,7 +149,7 @@ SIGNATURES: dict[str, list] = {
                                             _i64, _i32, _p],
 }
 _RESTYPES = {"oudjat_status_string": ctypes.c_char_p, "oudjat_last_error": ctypes.c_char_p,
-             "oudjat_linear_workspace_elems": ctypes.c_int64,
+             "oudjat_linear_workspace_elems": ctypes.c_int64, "oudjat_linear_warm_slots": ctypes.c_int64,
              "oudjat_sparse_query_attention_workspace_elems": ctypes.c_int64,
              "oudjat_patch_attention_prob_workspace_elems": ctypes.c_int64}
 

@@ -1,7 +1,7 @@
 // Status plumbing, ABI version and the runtime self-test.
 #include "common.hpp"
 
-#define OUDJAT_ABI_VERSION 17
+#define OUDJAT_ABI_VERSION 18
 
 namespace oudjat {
 

@@ -46,6 +46,7 @@ namespace oudjat {
 
 static constexpr int kBK = 64;
 static constexpr int kNumXcd = 8;
+static constexpr int kNumCus = 256;  // MI355X: 8 XCDs of 32 CUs
 
 // Epilogue kind beyond the public ones: QKV projection followed by RoPE on q and k of patch rows,
 // q written packed and k, v written into the K/V cache rows (used by oudjat_linear_qkv_rope_kv).
@@ -96,7 +97,31 @@ struct EpiArgs {
   const uint16_t* b1;
   const uint16_t* b2;
   const float* xh_ts;
+  // Cache warming (direct-to-LDS 16-row and ping-pong kernels, unsplit launches): workgroups
+  // blockIdx.x >= work_tiles compute no tile; they read one dword of every 128-byte line of
+  // warm[0 .. warm_lines * 32) (the weight of a later launch) and exit. work_tiles = 0: every
+  // workgroup computes a tile.
+  const uint32_t* warm;
+  int64_t warm_lines;
+  int work_tiles;
 };
+
+// A warming workgroup's share of the lines (part of parts), eight loads in flight per lane; the
+// loaded words are consumed by an empty asm so that the loads stay.
+__device__ __forceinline__ void warm_lines(const uint32_t* __restrict__ p, int64_t lines, int part, int parts) {
+  const int64_t stride = (int64_t)parts * blockDim.x;
+  int64_t l = (int64_t)part * blockDim.x + threadIdx.x;
+  uint32_t acc = 0;
+  for (; l + 7 * stride < lines; l += 8 * stride) {
+    uint32_t v[8];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) v[u] = p[(l + u * stride) * 32];
+#pragma unroll
+    for (int u = 0; u < 8; ++u) acc ^= v[u];
+  }
+  for (; l < lines; l += stride) acc ^= p[l * 32];
+  asm volatile("" ::"v"(acc));
+}
 
 // OUDJAT_EPI_RAW_BF16 on 8 consecutive bf16 values of columns col .. col + 7 (already bf16(acc)):
 // bf16(v * raw_scale + raw_bias), or bf16(v * raw_scale) without a bias (scale_bias's arithmetic).
@@ -1088,6 +1113,11 @@ void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t 
   static_assert(SUB % KSPLIT == 0 && SUBW >= 1 && WM % 16 == 0 && WN % 16 == 0 && NST >= 2, "tile shape");
 
   extern __shared__ __align__(16) unsigned char smem[];
+  const int tiles = ea.work_tiles > 0 ? ea.work_tiles : (int)gridDim.x;
+  if ((int)blockIdx.x >= tiles) {  // a warming workgroup
+    warm_lines(ea.warm, ea.warm_lines, (int)blockIdx.x - tiles, (int)gridDim.x - tiles);
+    return;
+  }
   constexpr int kLutOff = r16_lut_offset(BM, BN, WGM, WGN, KSPLIT, BK, NST);
   if constexpr (EPI == OUDJAT_EPI_BIAS_GELU) load_gelu_table<NT>(smem + kLutOff);
   if constexpr (EPI == kEpiPartial) {  // K slice blockIdx.y of length K (lda, ldw stay the full strides)
@@ -1097,7 +1127,6 @@ void gemm_bf16_r16_kernel(const uint16_t* __restrict__ A, int M, int K, int64_t 
 
   const int tiles_n = (N + BN - 1) / BN;
   const int tiles_m = (M + BM - 1) / BM;
-  const int tiles = gridDim.x;
   const int bid = blockIdx.x;
   const int xcd = bid % kNumXcd;
   const int q = tiles / kNumXcd, r = tiles % kNumXcd;
@@ -1327,6 +1356,11 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A16, int M, int K, int64_t
   static_assert(WM % 16 == 0 && WN % 16 == 0, "tile shape");
 
   extern __shared__ __align__(16) unsigned char smem[];
+  const int tiles = ea.work_tiles > 0 ? ea.work_tiles : (int)gridDim.x;
+  if ((int)blockIdx.x >= tiles) {  // a warming workgroup
+    warm_lines(ea.warm, ea.warm_lines, (int)blockIdx.x - tiles, (int)gridDim.x - tiles);
+    return;
+  }
   constexpr int kLutOff = r16_lut_offset(BM, BN, WGM, WGN, 1, BK, NST);
   const unsigned char* A = reinterpret_cast<const unsigned char*>(A16);
   const unsigned char* W = reinterpret_cast<const unsigned char*>(W16);
@@ -1348,7 +1382,6 @@ void gemm_bf16_pp_kernel(const uint16_t* __restrict__ A16, int M, int K, int64_t
 
   const int tiles_n = (N + BN - 1) / BN;
   const int tiles_m = (M + BM - 1) / BM;
-  const int tiles = gridDim.x;
   const int bid = blockIdx.x;
   const int xcd = bid % kNumXcd;
   const int q = tiles / kNumXcd, r = tiles % kNumXcd;
@@ -1946,12 +1979,29 @@ static int choose_cfg_fp8(int64_t M, int64_t N) {
 }
 
 // Launches configuration `ci` with epilogue `epi` (arguments already validated).
+// Warming workgroups a launch of configuration `cfg` with this many tiles (unsplit) carries: one per
+// CU its tiles leave idle, for the 16-row and ping-pong kernels (one workgroup per CU).
+static int64_t warm_slots(const GemmCfg& cfg, int64_t tiles) {
+  return (cfg.pf == -2 || cfg.pf == -3) && tiles < kNumCus ? kNumCus - tiles : 0;
+}
+
+// warm / warm_bytes: a region (4-byte aligned) to read into the caches from the CUs an unsplit launch
+// of fewer tiles than CUs leaves idle (one workgroup per CU: the kernels that take it hold a CU's
+// registers or LDS), for the launch after the next that reads it; ignored by the other kernels.
 static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W, int64_t N,
-                       int64_t ldw, int epi, const EpiArgs& ea, uint16_t* C, int64_t ldc, hipStream_t stream,
-                       const char* what, int splits = 1) {
+                       int64_t ldw, int epi, const EpiArgs& ea_in, uint16_t* C, int64_t ldc, hipStream_t stream,
+                       const char* what, int splits = 1, const void* warm = nullptr, int64_t warm_bytes = 0) {
   const GemmCfg& cfg = kCfgs[ci];
   const int64_t tiles = cdiv(M, cfg.bm) * cdiv(N, cfg.bn);
   OUDJAT_REQUIRE(tiles < ((int64_t)1 << 31), OUDJAT_ERR_TOO_LARGE, "%s: too many tiles", what);
+  EpiArgs ea = ea_in;
+  int64_t grid = tiles;
+  if (warm && warm_bytes >= 128 && splits == 1 && warm_slots(cfg, tiles) > 0) {
+    ea.warm = static_cast<const uint32_t*>(warm);
+    ea.warm_lines = warm_bytes / 128;
+    ea.work_tiles = (int)tiles;
+    grid = tiles + warm_slots(cfg, tiles);
+  }
   // K stages, or (direct-to-LDS kernels) the bf16 output tile of the epilogue if that is larger.
   size_t lds = cfg.pf < 0 ? (size_t)kStages * (cfg.bm + cfg.bn) * 64 : (size_t)2 * (cfg.bm + cfg.bn) * 128;
   if (cfg.pf <= 0) lds = lds > (size_t)cfg.bm * (cfg.bn + 8) * 2 ? lds : (size_t)cfg.bm * (cfg.bn + 8) * 2;
@@ -1978,7 +2028,7 @@ static int launch_gemm(int ci, const uint16_t* A, int64_t M, int64_t K, int64_t 
   }
   const int threads = cfg.wgm * cfg.wgn * (cfg.pf <= -2 ? cfg.ks : 1) * 64;
   // A split launch (epi == kEpiPartial) runs K / splits per workgroup, slice = blockIdx.y.
-  hipLaunchKernelGGL(fn, dim3((unsigned)tiles, (unsigned)splits), dim3(threads), lds, stream, A, (int)M,
+  hipLaunchKernelGGL(fn, dim3((unsigned)grid, (unsigned)splits), dim3(threads), lds, stream, A, (int)M,
                      (int)(K / splits), lda, W, (int)N, ldw, ea, C, ldc, kGroupM);
   return check_launch(what);
 }
@@ -2022,11 +2072,15 @@ static int launch_gemm_splitk(int ci, int S, const uint16_t* A, int64_t M, int64
 
 using namespace oudjat;
 
-extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W, int64_t N,
-                                  int64_t ldw, const uint16_t* bias, int epi, const uint16_t* gamma,
-                                  const uint16_t* resid, int64_t ldr, uint16_t* C, int64_t ldc, float acc_scale,
-                                  float* workspace, int64_t workspace_elems, oudjat_stream_t stream) {
+static int linear_bf16_impl(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W, int64_t N,
+                            int64_t ldw, const uint16_t* bias, int epi, const uint16_t* gamma, const uint16_t* resid,
+                            int64_t ldr, uint16_t* C, int64_t ldc, float acc_scale, float* workspace,
+                            int64_t workspace_elems, const void* warm, int64_t warm_bytes, oudjat_stream_t stream) {
   OUDJAT_REQUIRE(M >= 0 && N >= 0 && K >= 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_bf16: negative size");
+  OUDJAT_REQUIRE(warm_bytes >= 0 && (warm_bytes == 0 || warm), OUDJAT_ERR_INVALID_ARGUMENT,
+                 "linear_bf16: bad warm region (bytes < 0, or NULL with bytes > 0)");
+  OUDJAT_REQUIRE(warm_bytes == 0 || aligned(warm, 4), OUDJAT_ERR_UNSUPPORTED_LAYOUT,
+                 "linear_bf16: the warm region must be 4-byte aligned");
   const int raw_round = (epi & OUDJAT_EPI_RAW_BF16) != 0;
   epi &= ~OUDJAT_EPI_RAW_BF16;
   OUDJAT_REQUIRE(epi >= OUDJAT_EPI_BIAS && epi <= OUDJAT_EPI_BIAS_SILU_MUL, OUDJAT_ERR_INVALID_ARGUMENT,
@@ -2072,7 +2126,24 @@ extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64
                                 "linear_bf16");
   }
   return launch_gemm(choose_cfg(M, N, K, aligned_io), A, M, K, lda, W, N, ldw, epi, ea, C, ldc, as_stream(stream),
-                     "linear_bf16");
+                     "linear_bf16", 1, warm, warm_bytes);
+}
+
+extern "C" int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W, int64_t N,
+                                  int64_t ldw, const uint16_t* bias, int epi, const uint16_t* gamma,
+                                  const uint16_t* resid, int64_t ldr, uint16_t* C, int64_t ldc, float acc_scale,
+                                  float* workspace, int64_t workspace_elems, oudjat_stream_t stream) {
+  return linear_bf16_impl(A, M, K, lda, W, N, ldw, bias, epi, gamma, resid, ldr, C, ldc, acc_scale, workspace,
+                          workspace_elems, nullptr, 0, stream);
+}
+
+extern "C" int oudjat_linear_bf16_warm(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                                       int64_t N, int64_t ldw, const uint16_t* bias, int epi, const uint16_t* gamma,
+                                       const uint16_t* resid, int64_t ldr, uint16_t* C, int64_t ldc, float acc_scale,
+                                       float* workspace, int64_t workspace_elems, const void* warm,
+                                       int64_t warm_bytes, oudjat_stream_t stream) {
+  return linear_bf16_impl(A, M, K, lda, W, N, ldw, bias, epi, gamma, resid, ldr, C, ldc, acc_scale, workspace,
+                          workspace_elems, warm, warm_bytes, stream);
 }
 
 extern "C" int oudjat_linear_swiglu_nvfp4(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
@@ -2142,13 +2213,29 @@ extern "C" int64_t oudjat_linear_workspace_elems(int64_t M, int64_t N, int64_t K
   return (int64_t)S * M * N;
 }
 
+extern "C" int64_t oudjat_linear_warm_slots(int64_t M, int64_t N, int64_t K, int epi) {
+  epi &= ~OUDJAT_EPI_RAW_BF16;
+  if (M <= 0 || N <= 0 || K <= 0 || N % 64 != 0 || K % kBK != 0 || epi < OUDJAT_EPI_BIAS ||
+      epi > OUDJAT_EPI_BIAS_SILU_MUL)
+    return 0;
+  int S = 1;
+  if (choose_splitk(M, N, K, epi, &S) >= 0 && S > 1) return 0;  // split launches take none
+  const GemmCfg& c = kCfgs[choose_cfg(M, N, K, true)];
+  return warm_slots(c, cdiv(M, c.bm) * cdiv(N, c.bn));
+}
+
 static int linear_qkv_rope_kv_impl(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
                                    int64_t ldw, const uint16_t* bias, int64_t H, int64_t Dh, const float* sin_table,
                                    const float* cos_table, int64_t table_stride, const uint8_t* patch_mask,
                                    const int64_t* rope_idx, const int64_t* batch_idx, const int64_t* token_idx,
                                    uint16_t* kv, int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
-                                   float acc_scale, int raw_round, oudjat_stream_t stream) {
+                                   float acc_scale, int raw_round, oudjat_stream_t stream, const void* warm = nullptr,
+                                   int64_t warm_bytes = 0) {
   OUDJAT_REQUIRE(M >= 0 && K >= 0 && H > 0 && Dh > 0, OUDJAT_ERR_INVALID_ARGUMENT, "linear_qkv_rope_kv: bad size");
+  OUDJAT_REQUIRE(warm_bytes >= 0 && (warm_bytes == 0 || warm), OUDJAT_ERR_INVALID_ARGUMENT,
+                 "linear_qkv_rope_kv: bad warm region (bytes < 0, or NULL with bytes > 0)");
+  OUDJAT_REQUIRE(warm_bytes == 0 || aligned(warm, 4), OUDJAT_ERR_UNSUPPORTED_LAYOUT,
+                 "linear_qkv_rope_kv: the warm region must be 4-byte aligned");
   if (M == 0) return OUDJAT_OK;
   const int64_t N = 3 * H * Dh;
   OUDJAT_REQUIRE(A && W && kv && q_out && sin_table && cos_table && patch_mask && rope_idx && batch_idx && token_idx,
@@ -2180,7 +2267,7 @@ static int linear_qkv_rope_kv_impl(const uint16_t* A, int64_t M, int64_t K, int6
   ea.qkv = QkvArgs{(int)H, (int)Dh, sin_table, cos_table, table_stride, patch_mask, rope_idx, batch_idx, token_idx,
                    kv, kv_stride_b, kv_stride_n, q_out};
   return launch_gemm(choose_qkv_cfg(M, N, K, Dh), A, M, K, lda, W, N, ldw, kEpiQkv, ea, nullptr, 0, as_stream(stream),
-                     "linear_qkv_rope_kv");
+                     "linear_qkv_rope_kv", 1, warm, warm_bytes);
 }
 
 extern "C" int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
@@ -2193,6 +2280,19 @@ extern "C" int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K
   return linear_qkv_rope_kv_impl(A, M, K, lda, W, ldw, bias, H, Dh, sin_table, cos_table, table_stride, patch_mask,
                                  rope_idx, batch_idx, token_idx, kv, kv_stride_b, kv_stride_n, q_out, acc_scale, 0,
                                  stream);
+}
+
+extern "C" int oudjat_linear_qkv_rope_kv_warm(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                                              int64_t ldw, const uint16_t* bias, int64_t H, int64_t Dh,
+                                              const float* sin_table, const float* cos_table, int64_t table_stride,
+                                              const uint8_t* patch_mask, const int64_t* rope_idx,
+                                              const int64_t* batch_idx, const int64_t* token_idx, uint16_t* kv,
+                                              int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
+                                              float acc_scale, const void* warm, int64_t warm_bytes,
+                                              oudjat_stream_t stream) {
+  return linear_qkv_rope_kv_impl(A, M, K, lda, W, ldw, bias, H, Dh, sin_table, cos_table, table_stride, patch_mask,
+                                 rope_idx, batch_idx, token_idx, kv, kv_stride_b, kv_stride_n, q_out, acc_scale, 0,
+                                 stream, warm, warm_bytes);
 }
 
 extern "C" int oudjat_linear_qkv_rope_kv_nvfp4(const uint16_t* A, int64_t M, int64_t K, int64_t lda,

@@ -52,6 +52,15 @@ def _linear_route(mod: nn.Module, x: Tensor, site: str, *, bias: Tensor | None =
     return K.linear(x, mod.weight, b, site=site, **kw)
 
 
+def _bf16_weight(mod: nn.Module | None) -> Tensor | None:
+    """The weight a bf16 linear's GEMM reads (a cache-warming target), or None when `mod` is absent or
+    runs in low precision."""
+    if mod is None or LP.low_precision_state(mod) != "bf16":
+        return None
+    w = getattr(mod, "weight", None)
+    return w if isinstance(w, Tensor) and w.dtype == torch.bfloat16 and w.is_contiguous() else None
+
+
 _IDENTITY_PLANS: Dict[tuple, "PackedQueryState"] = {}
 
 
@@ -226,11 +235,12 @@ class SelfAttention(nn.Module):
         return out, cache_feature
 
     def _qkv_attention(self, xn: Tensor, rope, kv: Tensor, qs: PackedQueryState, xn_is_xhat: bool = False,
-                       lse: Tensor | None = None, fp8_out: Tensor | None = None):
+                       lse: Tensor | None = None, fp8_out: Tensor | None = None, warm: Tensor | None = None):
         """q, K/V rows and the attention output of the packed rows from their norm1 output xn -- for a
         frozen NVFP4 qkv linear, xn may already be its NVFP4 operand x_hat (xn_is_xhat: the producer wrote
         it). lse (fp32 [B, H, T]) receives the attention's row log-sum-exp when given. fp8_out (the
-        frozen FP8 proj's activation inverse scale): the output is instead its e4m3fn codes (uint8)."""
+        frozen FP8 proj's activation inverse scale): the output is instead its e4m3fn codes (uint8). warm:
+        a later launch's weight, read into the caches by the bf16 QKV GEMM's idle CUs."""
         M, C = xn.shape
         H, D = self.num_heads, self.head_dim
         B = kv.shape[0]
@@ -268,7 +278,7 @@ class SelfAttention(nn.Module):
                     mod.observe(xn)
                 a, w, s = xn, mod.weight, 1.0
             K.linear_qkv_rope_kv(a, w, self.qkv_bias(), rope, qs.active_patch_mask, qs.active_rope_idx,
-                                 qs.active_batch_idx, qs.active_token_idx, kv, q, acc_scale=s)
+                                 qs.active_batch_idx, qs.active_token_idx, kv, q, acc_scale=s, warm=warm)
             qkv = None
         else:
             qkv = _linear_route(mod, xn, "qkv", bias=self.qkv_bias())
@@ -330,15 +340,18 @@ class SelfAttentionBlock(nn.Module):
             self._ones = torch.ones(like.shape[-1], device=like.device, dtype=torch.bfloat16)
         return self._ones
 
-    def _mlp_scaled(self, xn: Tensor, xn_is_xhat: bool = False) -> Tensor:
+    def _mlp_scaled(self, xn: Tensor, xn_is_xhat: bool = False, warm=(None, None)) -> Tensor:
         """gamma2 * MLP(xn) with GELU / SwiGLU and LayerScale fused into the GEMM epilogues; the SwiGLU
         linears in their low-precision route when the block is a converted view (dinov3/lowp.py). With
         NVFP4 linears xn may already be w1's NVFP4 operand x_hat (xn_is_xhat), and the SwiGLU kernel
-        writes w3's x_hat directly."""
+        writes w3's x_hat directly. warm: the weights (or None) that the bf16 fc1 and fc2 GEMMs read
+        into the caches from their idle CUs."""
         g2 = self._gamma(self.ls2, xn)
         if isinstance(self.mlp, Mlp):
-            h = K.linear(xn, self.mlp.fc1.weight, self.mlp.fc1.bias, epilogue=_lib.EPI_BIAS_GELU, site="fc1")
-            return K.linear(h, self.mlp.fc2.weight, self.mlp.fc2.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g2, site="fc2")
+            h = K.linear(xn, self.mlp.fc1.weight, self.mlp.fc1.bias, epilogue=_lib.EPI_BIAS_GELU, site="fc1",
+                         warm=warm[0])
+            return K.linear(h, self.mlp.fc2.weight, self.mlp.fc2.bias, epilogue=_lib.EPI_BIAS_LS, gamma=g2, site="fc2",
+                            warm=warm[1])
         w1, w2, w3 = self.mlp.w1, self.mlp.w2, self.mlp.w3
         states = {LP.low_precision_state(m) for m in (w1, w2, w3)}
         if "fp4" in states:
@@ -708,13 +721,16 @@ class SelfAttentionBlock(nn.Module):
         return plan, key, kv, bos
 
     def _correct_rows(self, x_act: Tensor, rope, kv: Tensor, qs: PackedQueryState, xn: Tensor | None = None,
-                      residual=None, xn_is_xhat: bool = False):
+                      residual=None, xn_is_xhat: bool = False, next_block: "SelfAttentionBlock | None" = None):
         """The block's arithmetic on the packed selected rows (block.py:1111-1141): returns
         (x_attn, mlp); the K/V cache rows of the selected tokens are rewritten in place. `xn`, when
         given, is norm1(x_act) already computed (by the previous block's fused residual step).
         `residual` = (blocks_out_sum, next block's norm1 or None): when the last MLP product splits K,
         its reduce runs fused with the packed residual step, and the second value returned is then
-        (x_new, norm1(x_new) or None) instead of mlp (see _mlp_scaled_residual)."""
+        (x_new, norm1(x_new) or None) instead of mlp (see _mlp_scaled_residual). `next_block` (the block
+        that runs next in a packed run, or None): the bf16 GEMMs read the weights of later launches
+        into the caches from the CUs they leave idle -- qkv fc1's, proj fc2's (else norm2's launch
+        does), fc1 the next block's qkv, fc2 the next block's proj -- a cache hint only."""
         with trace_range("correct_attn"):
             if xn is None:   # block.py:1114 (an NVFP4 qkv linear's x_hat, written by the LayerNorm itself)
                 ts1 = _fp4_scale(self.attn.qkv)
@@ -724,9 +740,17 @@ class SelfAttentionBlock(nn.Module):
             # A native FP8 proj takes the attention's output as e4m3 codes written by the attention itself
             # (its activation quantizer in the attention's store, one launch fewer).
             fp8_codes = (LP.low_precision_state(proj) == "fp8" and proj.native and self.attn.head_dim == 128)
+            fc1 = self.mlp.fc1 if isinstance(self.mlp, Mlp) else None
             _, attn = self.attn._qkv_attention(xn, rope, kv, qs, xn_is_xhat,           # attention.py:415-523
-                                               fp8_out=proj.act_inv_f32 if fp8_codes else None)
+                                               fp8_out=proj.act_inv_f32 if fp8_codes else None,
+                                               warm=_bf16_weight(fc1))
             g1 = self._gamma(self.ls1, x_act)
+            # fc2's weight is warmed by a bf16 proj's idle CUs where its launch leaves any, else by
+            # norm2's launch (_mlp_prefetch)
+            fc2_w = self._mlp_prefetch()
+            proj_warm = (fc2_w if fc2_w is not None and _bf16_weight(proj) is not None and
+                         K.linear_warm_slots(x_act.shape[0], proj.out_features, proj.in_features,
+                                             _lib.EPI_BIAS_LS_RESID) > 0 else None)
             if fp8_codes:
                 x_attn = proj.linear_codes(attn, proj.bias, "proj", epilogue=_lib.EPI_BIAS_LS_RESID, gamma=g1,
                                            resid=x_act)
@@ -734,16 +758,19 @@ class SelfAttentionBlock(nn.Module):
                 x_attn = _fp4_linear(proj, attn, "proj", epilogue=_lib.EPI_BIAS_LS_RESID, gamma=g1, resid=x_act)
             else:
                 x_attn = _linear_route(proj, attn, "proj", epilogue=_lib.EPI_BIAS_LS_RESID,  # attention.py:532 +
-                                       gamma=g1, resid=x_act)                             # block.py:1129-1134
+                                       gamma=g1, resid=x_act,                             # block.py:1129-1134
+                                       **({} if proj_warm is None else {"warm": proj_warm}))
         with trace_range("correct_ffn"):
             ts2 = None if isinstance(self.mlp, Mlp) else _fp4_scale(self.mlp.w1)
             xn2 = K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps, nvfp4_scale=ts2,  # :1141
-                               prefetch=self._mlp_prefetch())
+                               prefetch=fc2_w if proj_warm is None else None)
             if residual is not None and ts2 is None:
                 fused = self._mlp_scaled_residual(xn2, x_act, x_attn, qs, *residual)
                 if fused is not None:
                     return x_attn, fused
-            mlp = self._mlp_scaled(xn2, xn_is_xhat=ts2 is not None)
+            nb = next_block
+            warm = (None, None) if nb is None else (_bf16_weight(nb.attn.qkv), _bf16_weight(nb.attn.proj))
+            mlp = self._mlp_scaled(xn2, xn_is_xhat=ts2 is not None, warm=warm)
         return x_attn, mlp
 
     def _mlp_prefetch(self) -> Tensor | None:
@@ -870,7 +897,8 @@ def correct_blocks_packed(blocks, x: Tensor, dindice: Tensor, rope, cache_featur
         if x_p.shape[0] > 0:
             ts_next = _fp4_scale(blocks[i + 1].attn.qkv) if i + 1 < len(blocks) else None
             nxt = blocks[i + 1].norm1 if i + 1 < len(blocks) and ts_next is None else None
-            x_attn, mlp = blk._correct_rows(x_p, rope, kv, qs, xn=xn, residual=(bos, nxt), xn_is_xhat=xn_is_xhat)
+            x_attn, mlp = blk._correct_rows(x_p, rope, kv, qs, xn=xn, residual=(bos, nxt), xn_is_xhat=xn_is_xhat,
+                                            next_block=blocks[i + 1] if i + 1 < len(blocks) else None)
             if isinstance(mlp, tuple):  # the residual step ran fused with the last MLP product
                 x_p, xn = mlp
                 xn_is_xhat = False

@@ -271,6 +271,17 @@ def linear_splits_k(M: int, N: int, K: int) -> bool:
     return elems > 0
 
 
+def linear_warm_slots(M: int, N: int, K: int, epilogue: int) -> int:
+    """Warming workgroups `linear(..., warm=...)` adds for an M x N x K product with this epilogue (0:
+    its tiles fill the GPU or it splits K, and the region is not read)."""
+    key = ("warm", M, N, K, int(epilogue))
+    n = _WS_ELEMS.get(key)
+    if n is None:
+        n = int(_lib.load().oudjat_linear_warm_slots(M, N, K, int(epilogue)))
+        _WS_ELEMS[key] = n
+    return n
+
+
 def linear_ls_packed_residual(h: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, gamma: torch.Tensor,
                               x_act: torch.Tensor, x_attn: torch.Tensor, batch_idx: torch.Tensor,
                               token_idx: torch.Tensor, blocks_out_sum: torch.Tensor, ln=None, site: str = "fc2"):
@@ -705,12 +716,14 @@ def qkv_fusable(H: int, Dh: int) -> bool:
 def linear_qkv_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None, rope,
                        patch_mask: torch.Tensor, rope_idx: torch.Tensor, batch_idx: torch.Tensor,
                        token_idx: torch.Tensor, kv_cache: torch.Tensor, q_out: torch.Tensor,
-                       acc_scale: float = 1.0, raw_bf16: bool = False) -> None:
+                       acc_scale: float = 1.0, raw_bf16: bool = False, warm: torch.Tensor | None = None) -> None:
     """One kernel for attention.py:415-454: qkv = x . weight^T + bias, RoPE on q and k of patch rows,
     k and v written into kv_cache [B, N, 2, H, Dh] rows (b, t) in place, q written to q_out [M, H, Dh].
     The qkv tensor itself is never materialised. `acc_scale` multiplies the fp32 accumulator before
     its first rounding (an FP8 GEMM's per-tensor scales). raw_bf16: an NVFP4 linear (x and weight its
-    x_hat operands, acc_scale its output scale): qkv = bf16(bf16(x . weight^T) * acc_scale + bias)."""
+    x_hat operands, acc_scale its output scale): qkv = bf16(bf16(x . weight^T) * acc_scale + bias).
+    `warm`: a tensor (the weight of a later launch) read into the caches from the CUs the launch leaves
+    idle, where it leaves any (a cache hint; the results do not depend on it)."""
     sin, cos = rope
     _require_cuda(x, weight, bias, patch_mask, rope_idx, batch_idx, token_idx, kv_cache, q_out, sin, cos)
     M, Kd = x.shape
@@ -723,12 +736,19 @@ def linear_qkv_rope_kv(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor
     _require(q_out.is_contiguous() and q_out.shape == (M, H, Dh), "linear_qkv_rope_kv: q_out must be contiguous [M, H, Dh]")
     _require(sin.dtype == cos.dtype == torch.float32 and sin.stride(1) == 1 and cos.stride() == sin.stride(),
              "linear_qkv_rope_kv: fp32 RoPE tables with contiguous rows")
-    entry = "oudjat_linear_qkv_rope_kv_nvfp4" if raw_bf16 else "oudjat_linear_qkv_rope_kv"
-    _launch("qkv", x, entry, _ptr(x), M, Kd, x.stride(0), _ptr(weight), weight.stride(0),
+    args = [_ptr(x), M, Kd, x.stride(0), _ptr(weight), weight.stride(0),
             _ptr(None if bias is None else bias.contiguous()), H, Dh, _ptr(sin), _ptr(cos), sin.stride(0),
             _ptr(patch_mask), _ptr(_index(rope_idx, "rope_idx")), _ptr(_index(batch_idx, "batch_idx")),
             _ptr(_index(token_idx, "token_idx")), _ptr(kv_cache), kv_cache.stride(0), kv_cache.stride(1), _ptr(q_out),
-            float(acc_scale), _stream(x))
+            float(acc_scale)]
+    if warm is not None and not raw_bf16:
+        _require_cuda(warm)
+        _require(warm.is_contiguous(), "linear_qkv_rope_kv: warm must be contiguous")
+        _launch("qkv", x, "oudjat_linear_qkv_rope_kv_warm", *args, _ptr(warm), warm.numel() * warm.element_size(),
+                _stream(x))
+        return
+    entry = "oudjat_linear_qkv_rope_kv_nvfp4" if raw_bf16 else "oudjat_linear_qkv_rope_kv"
+    _launch("qkv", x, entry, *args, _stream(x))
 
 
 def linear_swiglu_nvfp4(xh: torch.Tensor, w2_hat: torch.Tensor, x1: torch.Tensor, s1: float,
@@ -875,11 +895,14 @@ def _gemm_workspace(x: torch.Tensor, M: int, N: int, K: int, epilogue: int) -> t
 
 def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = None, *,
            epilogue: int = _lib.EPI_BIAS, gamma: torch.Tensor | None = None, resid: torch.Tensor | None = None,
-           out: torch.Tensor | None = None, site: str = "linear", acc_scale: float = 1.0) -> torch.Tensor:
+           out: torch.Tensor | None = None, site: str = "linear", acc_scale: float = 1.0,
+           warm: torch.Tensor | None = None) -> torch.Tensor:
     """bf16 x[..., K] . weight[N, K]^T with a fused epilogue (see include/oudjat.h). `site` names the
     launch for the timing probe ("proj", "fc1", "fc2", "w1", "w2", "w3", ...). `acc_scale` multiplies
     the fp32 accumulator before the epilogue's first rounding (an FP8 GEMM's per-tensor scales); with
-    `epilogue | EPI_RAW_BF16` (an NVFP4 linear) the accumulator is rounded to bf16 before it."""
+    `epilogue | EPI_RAW_BF16` (an NVFP4 linear) the accumulator is rounded to bf16 before it. `warm`: a
+    tensor (the weight of a later launch) read into the caches from the CUs the launch leaves idle,
+    where it leaves any (a cache hint; the results do not depend on it)."""
     _require_cuda(x, weight, bias, gamma, resid, out)
     _require(x.dtype == weight.dtype == torch.bfloat16, "linear: bf16 only")
     K = x.shape[-1]
@@ -896,10 +919,16 @@ def linear(x: torch.Tensor, weight: torch.Tensor, bias: torch.Tensor | None = No
         r2 = resid.reshape(-1, N)
         _require(r2.stride(1) == 1 and r2.shape[0] == M, "linear: resid must be [M, N] with contiguous rows")
     ws = _gemm_workspace(x, M, N, K, int(epilogue))
-    _launch(site, x, "oudjat_linear_bf16", _ptr(x2), M, K, x2.stride(0), _ptr(weight), N, weight.stride(0),
-         _ptr(None if bias is None else bias.contiguous()), int(epilogue),
-         _ptr(None if gamma is None else gamma.contiguous()), _ptr(r2), 0 if r2 is None else r2.stride(0), _ptr(o2),
-         o2.stride(0), float(acc_scale), _ptr(ws), 0 if ws is None else ws.numel(), _stream(x))
+    args = [_ptr(x2), M, K, x2.stride(0), _ptr(weight), N, weight.stride(0),
+            _ptr(None if bias is None else bias.contiguous()), int(epilogue),
+            _ptr(None if gamma is None else gamma.contiguous()), _ptr(r2), 0 if r2 is None else r2.stride(0), _ptr(o2),
+            o2.stride(0), float(acc_scale), _ptr(ws), 0 if ws is None else ws.numel()]
+    if warm is not None:
+        _require_cuda(warm)
+        _require(warm.is_contiguous(), "linear: warm must be contiguous")
+        _launch(site, x, "oudjat_linear_bf16_warm", *args, _ptr(warm), warm.numel() * warm.element_size(), _stream(x))
+    else:
+        _launch(site, x, "oudjat_linear_bf16", *args, _stream(x))
     return out
 
 

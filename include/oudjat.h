@@ -310,6 +310,26 @@ int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64_t lda, con
                        int64_t ldc, float acc_scale, float* workspace, int64_t workspace_elems,
                        oudjat_stream_t stream);
 
+/* Rows 6, 11, 12, 13 -- oudjat_linear_bf16 (same output bits) that also reads one 32-bit word of
+ * every whole 128-byte line of the read-only device region [warm, warm + warm_bytes) into the caches
+ * from the CUs the launch leaves idle: when the product is not split and has fewer output tiles than
+ * the GPU has CUs, the launch carries extra workgroups that do only that, on the otherwise idle CUs
+ * (the weight of the launch after the next: the correction block's fc1 warming the next block's qkv
+ * weight, fc2 the next block's proj weight). Elsewhere it is oudjat_linear_bf16. The reference's
+ * linears have no such argument (a cache hint with no effect on results). warm_bytes >= 0; warm 4-byte
+ * aligned and non-NULL when warm_bytes > 0. */
+int oudjat_linear_bf16_warm(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                            int64_t N, int64_t ldw, const uint16_t* bias, int epilogue,
+                            const uint16_t* gamma, const uint16_t* resid, int64_t ldr, uint16_t* C,
+                            int64_t ldc, float acc_scale, float* workspace, int64_t workspace_elems,
+                            const void* warm, int64_t warm_bytes, oudjat_stream_t stream);
+
+/* The number of warming workgroups an oudjat_linear_bf16_warm call of this shape and epilogue (with
+ * 16-byte aligned operands and the workspace oudjat_linear_workspace_elems names) adds: 0 when its
+ * tiles fill the GPU or it splits K, so that a caller can warm the region some other way. No
+ * counterpart in the reference. */
+int64_t oudjat_linear_warm_slots(int64_t M, int64_t N, int64_t K, int epilogue);
+
 /* The workspace (fp32 elements) oudjat_linear_bf16 can use for an M x N x K product with this
  * epilogue; 0 when it would not split K. No counterpart in the reference (cuBLAS sizes its own). */
 int64_t oudjat_linear_workspace_elems(int64_t M, int64_t N, int64_t K, int epilogue);
@@ -354,6 +374,18 @@ int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K, int64_t l
                               const int64_t* batch_idx, const int64_t* token_idx, uint16_t* kv,
                               int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
                               float acc_scale, oudjat_stream_t stream);
+
+/* Rows 6-9 -- oudjat_linear_qkv_rope_kv (same outputs) with the warm region of
+ * oudjat_linear_bf16_warm read from its idle CUs (the correction block's qkv warming its fc1 weight,
+ * ffn_layers.py:43-49). No such argument in the reference (a cache hint with no effect on results). */
+int oudjat_linear_qkv_rope_kv_warm(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
+                                   int64_t ldw, const uint16_t* bias, int64_t H, int64_t Dh,
+                                   const float* sin_table, const float* cos_table, int64_t table_stride,
+                                   const uint8_t* patch_mask, const int64_t* rope_idx,
+                                   const int64_t* batch_idx, const int64_t* token_idx, uint16_t* kv,
+                                   int64_t kv_stride_b, int64_t kv_stride_n, uint16_t* q_out,
+                                   float acc_scale, const void* warm, int64_t warm_bytes,
+                                   oudjat_stream_t stream);
 
 /* oudjat_linear_qkv_rope_kv for an NVFP4 qkv linear (fp4_fast_linear.py:221-283, then
  * attention.py:415-454): qkv = bf16(bf16(A . W^T) * out_scale + bias) (bias NULL: bf16(bf16(A . W^T) *

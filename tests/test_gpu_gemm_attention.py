@@ -233,6 +233,58 @@ def test_layer_norm_prefetch_is_the_same_layer_norm(dev, rows, C, pf_elems, pf_d
     assert bool((region == 1).all())  # read only
 
 
+@pytest.mark.parametrize("M,N,Kd,epi,warm_elems", [(4176, 1024, 1024, _lib.EPI_BIAS_LS_RESID, 1 << 22),
+                                                    (4176, 4096, 1024, _lib.EPI_BIAS_GELU, 3 << 20),
+                                                    (4176, 1024, 4096, _lib.EPI_BIAS_LS, 1 << 20),
+                                                    (1712, 4096, 1024, _lib.EPI_BIAS, 77),
+                                                    (8272, 4096, 1024, _lib.EPI_BIAS_GELU, 1 << 22),
+                                                    (414, 1024, 1024, _lib.EPI_BIAS, 1 << 20)])
+def test_linear_warm_is_the_same_linear(dev, M, N, Kd, epi, warm_elems):
+    """Warming workgroups (added to launches with fewer tiles than CUs: the headline's proj, fc1 and
+    fc2 shapes) leave the product's bits alone; launches that fill the GPU or split K take none. The
+    region (any size, here also below one line) is only read."""
+    x = _rand((M, Kd), 50).to(dev)
+    w = _rand((N, Kd), 51, 0.02).to(dev)
+    b = _rand((N,), 52, 0.1).to(dev)
+    g = _rand((N,), 53).to(dev)
+    r = _rand((M, N), 54).to(dev)
+    region = torch.ones(warm_elems, device=dev, dtype=torch.bfloat16)
+    kw = dict(epilogue=epi, gamma=g if epi in (_lib.EPI_BIAS_LS, _lib.EPI_BIAS_LS_RESID) else None,
+              resid=r if epi == _lib.EPI_BIAS_LS_RESID else None)
+    want = K.linear(x, w, b, **kw)
+    got = K.linear(x, w, b, warm=region, **kw)
+    torch.cuda.synchronize()
+    assert_bits_equal(got, want, "linear with warming workgroups")
+    assert bool((region == 1).all())
+
+
+def test_linear_qkv_rope_kv_warm_is_the_same(dev):
+    """The fused QKV GEMM at the headline shape with a warm region: same q and K/V bits."""
+    B, T, H, D, Kd, N = 16, 261, 16, 64, 1024, 1029
+    M = B * T
+    _, sin, cos, _, _, _ = _rope_inputs(1, H, D, 0)
+    rng = np.random.default_rng(7)
+    toks = np.stack([np.concatenate([np.arange(5), np.sort(rng.choice(np.arange(5, N), T - 5, replace=False))])
+                     for _ in range(B)])
+    tok = torch.from_numpy(toks.reshape(-1).astype(np.int64)).to(dev)
+    bi = torch.arange(B).repeat_interleave(T).to(dev)
+    pm, ri = tok >= 5, (tok - 5).clamp_min(0)
+    x = _rand((M, Kd), 60).to(dev)
+    w = _rand((3 * H * D, Kd), 61, 0.02).to(dev)
+    b = _rand((3 * H * D,), 62, 0.1).to(dev)
+    kv0 = _rand((B, N, 2, H, D), 63).to(dev)
+    rope = (sin.to(dev), cos.to(dev))
+    region = torch.ones(4 << 20, device=dev, dtype=torch.bfloat16)
+    kv_a, q_a = kv0.clone(), torch.empty((M, H, D), dtype=torch.bfloat16, device=dev)
+    K.linear_qkv_rope_kv(x, w, b, rope, pm, ri, bi, tok, kv_a, q_a)
+    kv_b, q_b = kv0.clone(), torch.empty((M, H, D), dtype=torch.bfloat16, device=dev)
+    K.linear_qkv_rope_kv(x, w, b, rope, pm, ri, bi, tok, kv_b, q_b, warm=region)
+    torch.cuda.synchronize()
+    assert_bits_equal(q_b, q_a, "q packed")
+    assert_bits_equal(kv_b, kv_a, "kv cache")
+    assert bool((region == 1).all())
+
+
 def _rope_inputs(M, H, D, seed):
     cfg = OM.with_overrides(OM.CONFIGS["vitl16_512"], dim=H * D, heads=H)
     sin, cos = OM.rope_tables(cfg)

@@ -161,6 +161,22 @@ def test_layernorm_prefetch_rejects_bad_regions():
     _lib.call("oudjat_layernorm_rows_prefetch", NULL, 0, 1024, 1024, NULL, NULL, 1e-5, NULL, 1024, NULL, 0, NULL)
 
 
+def test_gemm_warm_regions_are_checked_first():
+    """The GEMMs' cache-warming region is checked before anything else (zero rows: no GPU)."""
+    lin = ("oudjat_linear_bf16_warm", NULL, 0, 1024, 1024, NULL, 1024, 1024, NULL, 0, NULL, NULL, 0, NULL, 1024, 1.0,
+           NULL, 0)
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", *lin, NULL, 4096, NULL)
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", *lin, ctypes.c_void_p(256), -128, NULL)
+    _expect("OUDJAT_ERR_UNSUPPORTED_LAYOUT", *lin, ctypes.c_void_p(258), 4096, NULL)
+    _lib.call(*lin, ctypes.c_void_p(256), 4096, NULL)
+    _lib.call(*lin, NULL, 0, NULL)
+    qkv = ("oudjat_linear_qkv_rope_kv_warm", NULL, 0, 1024, 1024, NULL, 1024, NULL, 16, 64, NULL, NULL, 64, NULL, NULL,
+           NULL, NULL, NULL, 0, 0, NULL, 1.0)
+    _expect("OUDJAT_ERR_INVALID_ARGUMENT", *qkv, NULL, 4096, NULL)
+    _expect("OUDJAT_ERR_UNSUPPORTED_LAYOUT", *qkv, ctypes.c_void_p(258), 4096, NULL)
+    _lib.call(*qkv, ctypes.c_void_p(256), 4096, NULL)
+
+
 def test_zero_sized_calls_are_noops():
     # Nothing to do -> OK without touching any pointer (and without a GPU).
     _lib.call("oudjat_gather_rows", NULL, 0, 0, 2048, NULL, NULL, 0, NULL, 2048, NULL)
