@@ -403,11 +403,13 @@ def test_sparse_query_attention(dev, B, T, N, H, D):
 @pytest.mark.parametrize("B,T,N,H,scale_up", [(16, 261, 1029, 16, 1.0), (2, 300, 777, 4, 1.0), (1, 256, 64, 3, 1.0),
                                                (2, 260, 65, 2, 1.0), (2, 261, 300, 2, 8.0), (16, 107, 1029, 16, 1.0),
                                                (16, 517, 1029, 16, 1.0), (2, 128, 1029, 4, 1.0), (2, 137, 1029, 4, 1.0),
-                                               (2, 103, 201, 6, 8.0)])
+                                               (2, 103, 201, 6, 8.0), (2, 261, 20, 2, 1.0), (1, 261, 40, 3, 8.0)])
 def test_attention_buffer_load_kernel_shapes(dev, B, T, N, H, scale_up):
     """Dh = 64 with >= 8 waves runs the kernel that loads K/V tiles straight into LDS and reads V^T
     through LDS transpose reads, with the light last wave (T % 32 in 1..16: T = 261, 260, 300, 517)
-    split over four waves: one key tile, a ragged last tile of one key, 10 waves, large logits, and
+    split over four waves by 16-key quarters of every tile (N = 20, 40: one tile whose last quarters
+    hold no key, so those parts merge with nothing): one key tile, a ragged last tile of one key,
+    10 waves, large logits, and
     the ViT-L keep-10 % / 50 % query counts (T = 107, 517); at few query waves (T = 103, 107, 128, 137)
     each full wave's key tiles are split over two waves and merged; all against the float64
     reference, and repeated launches are bit-identical."""
@@ -434,7 +436,7 @@ def _attention_call(entry, q, kv, B, T, H, N, out, *ws):
 @pytest.mark.parametrize("B,T,N,H,scale_up", [(8, 261, 1029, 12, 1.0), (1, 103, 1029, 6, 1.0), (2, 300, 777, 4, 8.0),
                                                (1, 272, 577, 2, 1.0), (3, 107, 1029, 16, 1.0), (1, 5, 1029, 1, 1.0),
                                                (2, 32, 1100, 4, 1.0), (2, 256, 1029, 4, 1.0), (1, 33, 700, 3, 1.0),
-                                               (2, 16, 900, 2, 1.0)])
+                                               (2, 16, 900, 2, 1.0), (1, 261, 600, 2, 8.0)])
 def test_attention_key_split(dev, B, T, N, H, scale_up):
     """Few (image, head) pairs with many key tiles (ViT-B at B = 8: 96 pairs of 17 tiles): the keys are
     dealt in contiguous tile ranges to several workgroups per pair, whose fp32 partials a second
