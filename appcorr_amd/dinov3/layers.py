@@ -774,9 +774,9 @@ class SelfAttentionBlock(nn.Module):
         return x_attn, mlp
 
     def _mlp_prefetch(self) -> Tensor | None:
-        """The weight that norm2's launch warms in the last-level cache: fc2's (8 MB at ViT-L), read by
-        the MLP's second GEMM after fc1 and otherwise fetched from HBM on first touch (measured at the
-        headline: fc2 48.7 -> 43.7 us per block). bf16 Mlp only; None otherwise."""
+        """fc2's weight (8 MB at ViT-L), read by the MLP's second GEMM after fc1 and otherwise fetched from
+        HBM on first touch (measured at the headline: fc2 48.7 -> 43.7 us per block warmed): warmed by a
+        bf16 proj's idle CUs in the correction, else by norm2's launch. bf16 Mlp only; None otherwise."""
         if isinstance(self.mlp, Mlp) and LP.low_precision_state(self.mlp.fc2) == "bf16":
             return self.mlp.fc2.weight
         return None
