@@ -508,6 +508,55 @@ __device__ __forceinline__ void store_tile_phase2(unsigned char* smem, const uin
     }
     return;
   }
+  if constexpr ((EPI == OUDJAT_EPI_BIAS_LS_RESID || EPI == OUDJAT_EPI_BIAS_SILU_MUL) && BN < 384) {
+    // The epilogues that read a row segment (the residual or the gate) take their chunks in batches
+    // of EB: every LDS read and global load (gamma, the row segment) of a batch is issued before
+    // the first is used, so a batch costs one memory round trip instead of one per chunk; the
+    // arithmetic is the per-chunk loop's below. (The 384-wide tiles keep that loop: their kernel has
+    // no registers to spare for the batch.)
+    constexpr int ITERS = (BM * CPR + NT - 1) / NT;
+    constexpr int EB = 4;
+#pragma unroll
+    for (int b0 = 0; b0 < ITERS; b0 += EB) {
+      uint4 o[EB], gv[EB], rv[EB];
+      bool live[EB];
+#pragma unroll
+      for (int u = 0; u < EB; ++u) {
+        const int c = threadIdx.x + (b0 + u) * NT;
+        const int rl = c / CPR, cl = (c - rl * CPR) * 8;
+        live[u] = b0 + u < ITERS && c < BM * CPR && m0 + rl < M;
+        if (live[u]) {
+          o[u] = *reinterpret_cast<const uint4*>(ct + rl * LDT + cl);
+          if constexpr (EPI == OUDJAT_EPI_BIAS_LS_RESID) gv[u] = *reinterpret_cast<const uint4*>(ea.gamma + n0 + cl);
+          rv[u] = *reinterpret_cast<const uint4*>(ea.resid + (int64_t)(m0 + rl) * ea.ldr + n0 + cl);
+        }
+      }
+#pragma unroll
+      for (int u = 0; u < EB; ++u) {
+        if (!live[u]) continue;
+        const int c = threadIdx.x + (b0 + u) * NT;
+        const int rl = c / CPR, cl = (c - rl * CPR) * 8;
+        const int row = m0 + rl, col = n0 + cl;
+        uint4 w = o[u];
+        if (ea.raw_round) w = raw_scale_bias8(w, col, ea);
+        float v[8], g[8], r[8];
+        unpack8(w, v);
+        if constexpr (EPI == OUDJAT_EPI_BIAS_LS_RESID) unpack8(gv[u], g);
+        unpack8(rv[u], r);
+#pragma unroll
+        for (int e = 0; e < 8; ++e) {
+          if constexpr (EPI == OUDJAT_EPI_BIAS_LS_RESID) v[e] = fmaf(v[e], g[e], r[e]);
+          else v[e] = round_bf16(v[e] / (1.0f + expf(-v[e]))) * r[e];
+        }
+        w.x = cvt_pk_bf16(v[0], v[1]);
+        w.y = cvt_pk_bf16(v[2], v[3]);
+        w.z = cvt_pk_bf16(v[4], v[5]);
+        w.w = cvt_pk_bf16(v[6], v[7]);
+        *reinterpret_cast<uint4*>(C + (int64_t)row * ldc + col) = w;
+      }
+    }
+    return;
+  }
   for (int c = threadIdx.x; c < BM * CPR; c += NW * 64) {
     const int rl = c / CPR, cl = (c - rl * CPR) * 8;
     const int row = m0 + rl, col = n0 + cl;
