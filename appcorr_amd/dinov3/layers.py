@@ -729,8 +729,8 @@ class SelfAttentionBlock(nn.Module):
         its reduce runs fused with the packed residual step, and the second value returned is then
         (x_new, norm1(x_new) or None) instead of mlp (see _mlp_scaled_residual). `next_block` (the block
         that runs next in a packed run, or None): the bf16 GEMMs read the weights of later launches
-        into the caches from the CUs they leave idle -- qkv fc1's, proj fc2's (else norm2's launch
-        does), fc1 the next block's qkv, fc2 the next block's proj -- a cache hint only."""
+        into the caches from the CUs they leave idle -- qkv proj's, proj fc1's, fc1 fc2's (else
+        norm2's launch does), fc2 the next block's qkv -- a cache hint only."""
         with trace_range("correct_attn"):
             if xn is None:   # block.py:1114 (an NVFP4 qkv linear's x_hat, written by the LayerNorm itself)
                 ts1 = _fp4_scale(self.attn.qkv)
@@ -743,14 +743,14 @@ class SelfAttentionBlock(nn.Module):
             fc1 = self.mlp.fc1 if isinstance(self.mlp, Mlp) else None
             _, attn = self.attn._qkv_attention(xn, rope, kv, qs, xn_is_xhat,           # attention.py:415-523
                                                fp8_out=proj.act_inv_f32 if fp8_codes else None,
-                                               warm=_bf16_weight(fc1))
+                                               warm=_bf16_weight(proj))
             g1 = self._gamma(self.ls1, x_act)
-            # fc2's weight is warmed by a bf16 proj's idle CUs where its launch leaves any, else by
-            # norm2's launch (_mlp_prefetch)
+            # proj warms fc1's weight, fc1 fc2's (norm2's launch does where fc1's leaves no CU idle)
             fc2_w = self._mlp_prefetch()
-            proj_warm = (fc2_w if fc2_w is not None and _bf16_weight(proj) is not None and
-                         K.linear_warm_slots(x_act.shape[0], proj.out_features, proj.in_features,
-                                             _lib.EPI_BIAS_LS_RESID) > 0 else None)
+            proj_warm = _bf16_weight(fc1) if _bf16_weight(proj) is not None else None
+            fc1_warms = (fc2_w is not None and
+                         K.linear_warm_slots(x_act.shape[0], fc1.out_features, fc1.in_features,
+                                             _lib.EPI_BIAS_GELU) > 0)
             if fp8_codes:
                 x_attn = proj.linear_codes(attn, proj.bias, "proj", epilogue=_lib.EPI_BIAS_LS_RESID, gamma=g1,
                                            resid=x_act)
@@ -763,20 +763,20 @@ class SelfAttentionBlock(nn.Module):
         with trace_range("correct_ffn"):
             ts2 = None if isinstance(self.mlp, Mlp) else _fp4_scale(self.mlp.w1)
             xn2 = K.layer_norm(x_attn, self.norm2.weight, self.norm2.bias, self.norm2.eps, nvfp4_scale=ts2,  # :1141
-                               prefetch=fc2_w if proj_warm is None else None)
+                               prefetch=None if fc1_warms else fc2_w)
             if residual is not None and ts2 is None:
                 fused = self._mlp_scaled_residual(xn2, x_act, x_attn, qs, *residual)
                 if fused is not None:
                     return x_attn, fused
             nb = next_block
-            warm = (None, None) if nb is None else (_bf16_weight(nb.attn.qkv), _bf16_weight(nb.attn.proj))
+            warm = (fc2_w if fc1_warms else None, None if nb is None else _bf16_weight(nb.attn.qkv))
             mlp = self._mlp_scaled(xn2, xn_is_xhat=ts2 is not None, warm=warm)
         return x_attn, mlp
 
     def _mlp_prefetch(self) -> Tensor | None:
         """fc2's weight (8 MB at ViT-L), read by the MLP's second GEMM after fc1 and otherwise fetched from
-        HBM on first touch (measured at the headline: fc2 48.7 -> 43.7 us per block warmed): warmed by a
-        bf16 proj's idle CUs in the correction, else by norm2's launch. bf16 Mlp only; None otherwise."""
+        HBM on first touch (measured at the headline: fc2 48.7 -> 43.7 us per block warmed): warmed by
+        fc1's idle CUs in the correction, else by norm2's launch. bf16 Mlp only; None otherwise."""
         if isinstance(self.mlp, Mlp) and LP.low_precision_state(self.mlp.fc2) == "bf16":
             return self.mlp.fc2.weight
         return None

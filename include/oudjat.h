@@ -314,8 +314,8 @@ int oudjat_linear_bf16(const uint16_t* A, int64_t M, int64_t K, int64_t lda, con
  * every whole 128-byte line of the read-only device region [warm, warm + warm_bytes) into the caches
  * from the CUs the launch leaves idle: when the product is not split and has fewer output tiles than
  * the GPU has CUs, the launch carries extra workgroups that do only that, on the otherwise idle CUs
- * (the weight of the launch after the next: the correction block's fc1 warming the next block's qkv
- * weight, fc2 the next block's proj weight). Elsewhere it is oudjat_linear_bf16. The reference's
+ * (the weight of a later launch: the correction block's proj warming its fc1 weight, fc1 its fc2
+ * weight, fc2 the next block's qkv weight). Elsewhere it is oudjat_linear_bf16. The reference's
  * linears have no such argument (a cache hint with no effect on results). warm_bytes >= 0; warm 4-byte
  * aligned and non-NULL when warm_bytes > 0. */
 int oudjat_linear_bf16_warm(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
@@ -376,7 +376,7 @@ int oudjat_linear_qkv_rope_kv(const uint16_t* A, int64_t M, int64_t K, int64_t l
                               float acc_scale, oudjat_stream_t stream);
 
 /* Rows 6-9 -- oudjat_linear_qkv_rope_kv (same outputs) with the warm region of
- * oudjat_linear_bf16_warm read from its idle CUs (the correction block's qkv warming its fc1 weight,
+ * oudjat_linear_bf16_warm read from its idle CUs (the correction block's qkv warming its proj weight,
  * ffn_layers.py:43-49). No such argument in the reference (a cache hint with no effect on results). */
 int oudjat_linear_qkv_rope_kv_warm(const uint16_t* A, int64_t M, int64_t K, int64_t lda, const uint16_t* W,
                                    int64_t ldw, const uint16_t* bias, int64_t H, int64_t Dh,
